@@ -1,0 +1,312 @@
+#!/usr/bin/env python3
+"""Benchmark of the quantized-decode hot path on one MI355X.
+
+Metric: achieved HBM GB/s of the INT4 matvec and the INT8-KV
+(TurboQuant) decode attention, as a fraction of the 8 TB/s HBM3E peak.
+
+Workload of the headline number: the Qwen3-4B decode
+FFN block at batch 1 -- fused gate+up 2560 -> 2 x 9728 with SiLU, then down
+9728 -> 2560, INT4 group-128 weights from N(0, 0.02), AWQ scales U[0.5, 2],
+fp16 activations N(0,1) with 1 % of channels x20.  A step is one such FFN block
+through the public ops (activation image + matvec for each projection).  The
+weights are replicated over >= 512 MB of distinct buffers and the steps
+rotate through them, so the MI355X's 256 MB Infinity Cache cannot serve them.
+
+Bytes are counted as in the reference's kernel_bandwidth_bench
+(ironmill-bench/examples/kernel_bandwidth_bench.rs:351-370): codes + f16
+scales + f16 zeros + AWQ + x + y.
+
+The JSON line also carries
+  roofline     -- the dominant kernel (fused gate+up matvec, prepared
+                  activation) timed per launch with HIP events on its stream;
+  cpu_baseline -- the C oracle's dequantize-then-compute FFN step on the host
+                  cores (weights dequantized once outside the timing);
+  details      -- batch 4/8 FFN kernels and TurboQuant attention at 32k.
+
+Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--quick]
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import math
+import os
+import sys
+import time
+
+import numpy as np
+
+REPO = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, REPO)
+
+HBM_PEAK_GBS = 8000.0
+H, F = 2560, 9728
+INT4_BYTES_PER_ELEM = 0.5 + 4.0 / 128.0  # codes + f16 scale + f16 zero per 128
+
+
+def log(msg):
+    print(f"[bench] {msg}", file=sys.stderr, flush=True)
+
+
+def gate_up_bytes(b):
+    return 2 * F * H * INT4_BYTES_PER_ELEM + 2 * H + 2 * H * b + 2 * F * b
+
+
+def down_bytes(b):
+    return F * H * INT4_BYTES_PER_ELEM + 2 * F + 2 * F * b + 2 * H * b
+
+
+def tq_bytes(b, ctx, nkv=8, nh=32, d=128):
+    return b * (nkv * ctx * (2 * d + 12) + 2 * nh * d * 2)
+
+
+def make_weights(seed):
+    from ironmill_amd import quant
+    rng = np.random.default_rng(seed)
+    awq_h = rng.uniform(0.5, 2.0, H).astype(np.float32)
+    awq_f = rng.uniform(0.5, 2.0, F).astype(np.float32)
+    wg = (rng.standard_normal((F, H)) * 0.02).astype(np.float16).astype(np.float32)
+    wu = (rng.standard_normal((F, H)) * 0.02).astype(np.float16).astype(np.float32)
+    wd = (rng.standard_normal((H, F)) * 0.02).astype(np.float16).astype(np.float32)
+    return (quant.quantize_int4(wg, awq_scales=awq_h), quant.quantize_int4(wu, awq_scales=awq_h),
+            quant.quantize_int4(wd, awq_scales=awq_f))
+
+
+def make_x(b, k, seed):
+    rng = np.random.default_rng(seed)
+    x = rng.standard_normal((b, k)).astype(np.float32)
+    idx = rng.choice(k, k // 100, replace=False)
+    x[:, idx] *= 20.0
+    return x.astype(np.float16)
+
+
+def time_loop(dev, stream, fn, steps, warmup, per_launch=False):
+    """Run fn(i) warmup + steps times; return (total_ms, [per-launch ms])."""
+    for i in range(warmup):
+        fn(i)
+    stream.sync()
+    if per_launch:
+        evs = [(dev.event(), dev.event()) for _ in range(steps)]
+        for i, (a, b) in enumerate(evs):
+            a.record(stream)
+            fn(i)
+            b.record(stream)
+        stream.sync()
+        times = [a.elapsed_ms(b) for a, b in evs]
+        return sum(times), times
+    s, e = dev.event(), dev.event()
+    s.record(stream)
+    for i in range(steps):
+        fn(i)
+    e.record(stream)
+    stream.sync()
+    return s.elapsed_ms(e), None
+
+
+def cpu_baseline(qg, qu, qd, seconds):
+    import oracle as O
+    threads = min(os.cpu_count() or 1, 16)
+    wg = O.dequant_affine_int4(qg.data, qg.scales_f32, qg.zeros_f32, F, H)
+    wu = O.dequant_affine_int4(qu.data, qu.scales_f32, qu.zeros_f32, F, H)
+    wd = O.dequant_affine_int4(qd.data, qd.scales_f32, qd.zeros_f32, H, F)
+    x = make_x(1, H, 7)
+    reps, t0 = 0, time.perf_counter()
+    while True:
+        g = O.matvec_f16w(wg, x, qg.awq, nthreads=threads)
+        u = O.matvec_f16w(wu, x, qg.awq, nthreads=threads)
+        act = (g / (1.0 + np.exp(-g)) * u).astype(np.float16)
+        O.matvec_f16w(wd, act, qd.awq, nthreads=threads)
+        reps += 1
+        if time.perf_counter() - t0 >= seconds:
+            break
+    dt = (time.perf_counter() - t0) / reps
+    gbs = (gate_up_bytes(1) + down_bytes(1)) / dt / 1e9
+    return {"value": round(gbs, 3), "unit": "GB/s (INT4 bytes model, FFN step batch 1)",
+            "cores": threads, "kind": "port",
+            "sample": f"{reps} Qwen3-4B FFN steps (gate+up+SiLU+down, batch 1) in {reps * dt:.1f} s; "
+                      f"C oracle, weights dequantized to f16 once outside the timing, "
+                      f"{1e3 * dt:.1f} ms/step"}
+
+
+def bench_attention(dev, stream, ops, batch, ctx, steps, warmup, layers):
+    """TurboQuant decode attention over `layers` distinct caches (rotated)."""
+    nkv, nh, d = 8, 32, 128
+    tq = ops.TurboQuantModel(dev, d, 8, 42)
+    rng = np.random.default_rng(ctx + batch)
+    caches = []
+    chunk = 4096
+    for _ in range(layers):
+        c = ops.TurboQuantKvCache(dev, batch, nkv, d, ctx)
+        for p0 in range(0, ctx, chunk):
+            t = min(chunk, ctx - p0)
+            kv = (rng.standard_normal((batch, t, nkv, d))).astype(np.float16)
+            kd = dev.upload(kv)
+            ops.encode_turboquant_cache_write(stream, tq, c, kd, t, p0, True)
+            ops.encode_turboquant_cache_write(stream, tq, c, kd, t, p0, False)
+            stream.sync()
+        caches.append(c)
+    q = dev.upload(rng.standard_normal((batch, nh, d)).astype(np.float16))
+    out = dev.empty((batch, nh, d), np.float16)
+    scale = 1.0 / math.sqrt(d)
+
+    def step(i):
+        ops.encode_turboquant_attention(stream, tq, caches[i % layers], q, nh, ctx, out, scale)
+
+    total, per = time_loop(dev, stream, step, steps, warmup, per_launch=True)
+    ms = total / steps
+    gbs = tq_bytes(batch, ctx) / (ms * 1e-3) / 1e9
+    return {"batch": batch, "ctx": ctx, "us": round(ms * 1e3, 2), "GB/s": round(gbs, 1),
+            "frac": round(gbs / HBM_PEAK_GBS, 4), "bytes": tq_bytes(batch, ctx)}
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=200)
+    ap.add_argument("--warmup", type=int, default=20)
+    ap.add_argument("--batch", type=int, default=1)
+    ap.add_argument("--cpu-seconds", type=float, default=12.0)
+    ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--no-details", action="store_true")
+    ap.add_argument("--kernel-only", action="store_true",
+                    help="only the prepared fused gate+up kernel loop (for rocprofv3 counter runs)")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py: this build measures one GPU; --gpus {args.gpus} is not supported "
+              "(the hot path has no multi-GPU code, see DESIGN.md for how it would shard)",
+              file=sys.stderr)
+        sys.exit(2)
+
+    from ironmill_amd import Device, ops
+    dev = Device(0)
+    stream = dev.stream()
+    info = dev.info()
+    log(f"device {info['arch']} CUs={info['compute_units']}")
+
+    B = args.batch
+    qg, qu, qd = make_weights(1234)
+    per_copy = (qg.data.nbytes + qg.scales.nbytes * 2) * 3
+    reps = max(1, math.ceil(512e6 / per_copy))
+    log(f"uploading {reps} weight replicas ({reps * per_copy / 1e6:.0f} MB)")
+    W = [(ops.AffineQuantizedWeight(dev, qg), ops.AffineQuantizedWeight(dev, qu),
+          ops.AffineQuantizedWeight(dev, qd)) for _ in range(reps)]
+    x = dev.upload(make_x(B, H, 99))
+    act = dev.empty((B, F), np.float16)
+    y = dev.empty((B, H), np.float16)
+
+    # ---- dominant kernel: fused gate+up matvec on a prepared activation ----
+    prep = ops.PreparedActivation(dev, B, H)
+    ops.encode_int4_activation(stream, x, prep, awq=W[0][0].awq_scales)
+
+    def gate_up_kernel(i):
+        g, u, _ = W[i % reps]
+        ops.encode_int4_matvec_prepared(stream, prep, g, act, u, None, epilogue="silu")
+
+    ksteps = args.steps if not args.kernel_only else max(args.steps, 500)
+    tot, per = time_loop(dev, stream, gate_up_kernel, ksteps, args.warmup, per_launch=True)
+    k_us = 1e3 * tot / ksteps
+    k_bytes = gate_up_bytes(B)
+    k_gbs = k_bytes / (k_us * 1e-6) / 1e9
+    log(f"gate+up kernel: {k_us:.2f} us  {k_gbs:.0f} GB/s ({100 * k_gbs / HBM_PEAK_GBS:.1f} %)")
+    if args.kernel_only:
+        print(json.dumps({"kernel": "int4_matvec_kernel<2,SILU,hi+lo>", "us": round(k_us, 3),
+                          "GB/s": round(k_gbs, 1), "launches": ksteps}))
+        return
+
+    # ---- the step: FFN block through the public ops ----
+    def ffn_step(i):
+        g, u, d = W[i % reps]
+        ops.encode_fused_ffn_gate_up_act_int4(stream, x, g, u, act, B)
+        ops.encode_projection(stream, act, d, y, B)
+
+    total_ms, _ = time_loop(dev, stream, ffn_step, args.steps, args.warmup)
+    ms = total_ms / args.steps
+    step_bytes = gate_up_bytes(B) + down_bytes(B)
+    value = step_bytes / (ms * 1e-3) / 1e9
+    log(f"FFN step: {ms * 1e3:.2f} us  {value:.0f} GB/s")
+
+    traffic = None
+    tpath = os.path.join(REPO, "profiles", "traffic_gate_up_b1.json")
+    if os.path.exists(tpath):
+        with open(tpath) as f:
+            traffic = json.load(f).get("hbm_bytes_per_launch")
+
+    details = {}
+    if not args.no_details:
+        # down projection kernel alone, and the FFN kernels at batch 4 / 8
+        prep_d = ops.PreparedActivation(dev, B, F)
+        ops.encode_int4_activation(stream, act, prep_d, awq=W[0][2].awq_scales)
+
+        def down_kernel(i):
+            ops.encode_int4_matvec_prepared(stream, prep_d, W[i % reps][2], y)
+
+        t, _ = time_loop(dev, stream, down_kernel, args.steps, args.warmup, per_launch=True)
+        d_us = 1e3 * t / args.steps
+        details["down_kernel_b%d" % B] = {"us": round(d_us, 2),
+                                          "GB/s": round(down_bytes(B) / (d_us * 1e-6) / 1e9, 1)}
+        for bb in (4, 8):
+            xb = dev.upload(make_x(bb, H, 5 + bb))
+            pb = ops.PreparedActivation(dev, bb, H)
+            ops.encode_int4_activation(stream, xb, pb, awq=W[0][0].awq_scales)
+            ab = dev.empty((bb, F), np.float16)
+
+            def gu(i, pb=pb, ab=ab):
+                g, u, _ = W[i % reps]
+                ops.encode_int4_matvec_prepared(stream, pb, g, ab, u, None, epilogue="silu")
+
+            t, _ = time_loop(dev, stream, gu, args.steps, args.warmup, per_launch=True)
+            us = 1e3 * t / args.steps
+            details[f"gate_up_kernel_b{bb}"] = {"us": round(us, 2),
+                                                "GB/s": round(gate_up_bytes(bb) / (us * 1e-6) / 1e9, 1)}
+            pdn = ops.PreparedActivation(dev, bb, F)
+            ops.encode_int4_activation(stream, ab, pdn, awq=W[0][2].awq_scales)
+            yb = dev.empty((bb, H), np.float16)
+
+            def dn(i, pdn=pdn, yb=yb):
+                ops.encode_int4_matvec_prepared(stream, pdn, W[i % reps][2], yb)
+
+            t, _ = time_loop(dev, stream, dn, args.steps, args.warmup, per_launch=True)
+            us = 1e3 * t / args.steps
+            details[f"down_kernel_b{bb}"] = {"us": round(us, 2),
+                                             "GB/s": round(down_bytes(bb) / (us * 1e-6) / 1e9, 1)}
+        del W
+        stream.sync()
+        for bb, layers in ((1, 8), (16, 1)):
+            r = bench_attention(dev, stream, ops, bb, 32768, max(20, args.steps // 4), 5, layers)
+            details[f"tq_attention_b{bb}_ctx32k"] = r
+            log(f"TQ attention B={bb} ctx=32k: {r['us']} us {r['GB/s']} GB/s")
+        log(json.dumps(details))
+
+    cpu = None
+    if not args.no_cpu:
+        log("CPU baseline ...")
+        cpu = cpu_baseline(qg, qu, qd, args.cpu_seconds)
+
+    line = {
+        "metric": "INT4 matvec & INT8-KV decode attn: achieved HBM GB/s (% peak); decode tok/s",
+        "value": round(value, 2),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms, 6),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f16",
+        "data": "synthetic",
+        "config": {"workload": "qwen3-4b decode FFN block, INT4 g128 + AWQ (BASELINE configs[1])",
+                   "batch": B, "gate_up": [H, 2, F], "down": [F, H], "group_size": 128,
+                   "awq": True, "weight_replicas": reps},
+        "roofline": {"bound": "hbm", "achieved": round(k_gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": round(k_gbs / HBM_PEAK_GBS, 4), "traffic": traffic,
+                     "kernel": "int4_matvec_kernel (fused gate+up, SiLU, AWQ hi/lo)",
+                     "bytes_per_launch": k_bytes, "us_per_launch": round(k_us, 3)},
+        "cpu_baseline": cpu,
+        "details": details,
+    }
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == "__main__":
+    main()

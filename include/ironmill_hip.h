@@ -1,0 +1,283 @@
+/*
+ * ironmill_hip.h -- C ABI of the MI355X (gfx950) quantized-decode backend.
+ *
+ * Two tiers, mirroring jafreck/ironmill's Metal backend boundary
+ * (paths below are under the reference's crates/):
+ *
+ *  1. Runtime tier -- the counterpart of ironmill-metal-sys
+ *     (ironmill-metal-sys/src/{device,buffer,command}.rs): device, buffers
+ *     with bounds-checked read/write, in-order streams (command queues) and
+ *     timing events.
+ *  2. Op tier -- the counterpart of the Metal op encoders in
+ *     ironmill-inference/src/metal/{projection.rs, ops/quantized.rs,
+ *     ops/fused.rs, attention.rs}: every entry point enqueues work on a
+ *     stream and returns immediately.
+ *
+ * Conventions (from ironmill-compile-ffi/src/lib.rs:13-31,69-79,446):
+ *  - int status: IMH_OK (0) or a negative IMH_E* code; the thread-local
+ *    message of the last failure is returned by imh_last_error().
+ *  - every allocating call has a matching *_free; no C++ exception crosses
+ *    the ABI.
+ *  - op arguments are plain device pointers (any allocation on the stream's
+ *    device: imh_buffer_device_ptr(), hipMalloc, a torch tensor's data_ptr)
+ *    plus sizes.  f16 data is IEEE binary16 passed as uint16_t.
+ *  - a stream must not be used from two threads at once (the analogue of a
+ *    Metal ComputeEncoder being Send but not Sync, command.rs:339); handles
+ *    may move between threads.
+ *  - the library allocates per-stream scratch memory lazily (first op that
+ *    needs it, or growth); the kernels themselves never allocate.
+ */
+#ifndef IRONMILL_HIP_H
+#define IRONMILL_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define IMH_OK 0
+#define IMH_EINVAL (-1)       /* bad argument (MetalSysError::InvalidArgument, error.rs:4-41) */
+#define IMH_EUNSUPPORTED (-2) /* valid but not implemented here (e.g. group_size != 128) */
+#define IMH_EDEVICE (-3)      /* HIP runtime failure */
+#define IMH_ENOMEM (-4)       /* device allocation failed */
+#define IMH_ERANGE (-5)       /* sequence position beyond the cache (cache.rs:494-504) */
+
+typedef struct imh_device imh_device;
+typedef struct imh_buffer imh_buffer;
+typedef struct imh_stream imh_stream;
+typedef struct imh_event imh_event;
+typedef struct imh_tq_tables imh_tq_tables;
+
+/* Thread-local message of the last failed call on this thread
+ * (ironmill-compile-ffi/src/lib.rs:69-79 mil_last_error). Never NULL. */
+const char *imh_last_error(void);
+
+/* ===================== runtime tier (ironmill-metal-sys) ===================== */
+
+typedef struct {
+    int ordinal;
+    int compute_units;
+    int wavefront_size;
+    int clock_khz;
+    size_t total_global_mem;
+    size_t lds_per_block;
+    char arch[64]; /* e.g. "gfx950:sramecc+:xnack-" */
+} imh_device_info;
+
+/* MetalDevice::system_default (device.rs:74-96) generalised to an ordinal. */
+int imh_device_count(int *count);
+int imh_device_open(int ordinal, imh_device **out);
+void imh_device_free(imh_device *dev);
+/* recommended_max_working_set / device queries (device.rs:380-395) */
+int imh_device_get_info(const imh_device *dev, imh_device_info *out);
+
+/* MetalDevice::create_buffer / create_buffer_with_data (device.rs:105-160) */
+int imh_buffer_alloc(imh_device *dev, size_t length, imh_buffer **out);
+int imh_buffer_alloc_with_data(imh_device *dev, const void *data, size_t length,
+                               imh_buffer **out);
+void imh_buffer_free(imh_buffer *buf);
+/* MetalBuffer::length / contents (buffer.rs:60-93); the pointer is a device address */
+size_t imh_buffer_length(const imh_buffer *buf);
+void *imh_buffer_device_ptr(const imh_buffer *buf);
+/* MetalBuffer::write_bytes / read_bytes (buffer.rs:95-158): synchronous,
+ * IMH_EINVAL when offset+length exceeds the buffer. */
+int imh_buffer_write(imh_buffer *buf, size_t offset, const void *src, size_t length);
+int imh_buffer_read(const imh_buffer *buf, size_t offset, void *dst, size_t length);
+
+/* CommandQueue / CommandBuffer (command.rs:16-130): one in-order HIP stream
+ * at default priority.  imh_stream_sync = commit + wait_until_completed. */
+int imh_stream_create(imh_device *dev, imh_stream **out);
+void imh_stream_free(imh_stream *stream);
+int imh_stream_sync(imh_stream *stream);
+void *imh_stream_native(imh_stream *stream); /* the hipStream_t */
+/* Zero `length` bytes at a device pointer with a fill kernel (capturable). */
+int imh_fill_zero(imh_stream *stream, void *dst, size_t length);
+
+/* gpu_start_time / gpu_end_time (command.rs:470-489) as stream events. */
+int imh_event_create(imh_device *dev, imh_event **out);
+void imh_event_free(imh_event *ev);
+int imh_event_record(imh_event *ev, imh_stream *stream);
+int imh_event_elapsed_ms(imh_event *start, imh_event *end, float *ms);
+
+/* ========================= op tier: INT4 affine weights ========================= */
+
+/* AffineQuantizedWeight (ironmill-inference/src/metal/weights.rs:129-147) in
+ * the separate-array upload layout of metal/weights.rs:1064-1103:
+ *   data   [n][k/2] bytes, element k of a row in the low nibble when k is even
+ *          (int4_pack.rs:20-34, quantized.rs:441-447);
+ *   scales [n][k/group_size] f16; zeros [n][k/group_size] f16 raw zero-points
+ *          (dequant: w = (q - z) * s, core/dequant.rs:130-140);
+ *   awq_scales [k] f16 or NULL: the activation is divided by it
+ *          (affine_batched.metal:70-79).
+ * group_size must be 128 and k a multiple of 128 (IMH_EUNSUPPORTED otherwise). */
+typedef struct {
+    const uint8_t *data;
+    const uint16_t *scales;
+    const uint16_t *zeros;
+    const uint16_t *awq_scales;
+    uint32_t n;
+    uint32_t k;
+    uint32_t group_size;
+} imh_affine_int4_weight;
+
+/* encode_projection -> encode_affine_projection (projection.rs:35-56,227-312),
+ * with the dequantize-then-compute semantics of core/dequant.rs:85-180:
+ *   y[t][r] = f16( sum_k (x[t][k] / awq[k]) * (q[r][k] - z) * s ),  f32 accumulate.
+ * x: [token_count][k] f16, y: [token_count][n] f16. */
+int imh_encode_affine_projection_int4(imh_stream *stream, const uint16_t *x,
+                                      uint32_t token_count, const imh_affine_int4_weight *w,
+                                      uint16_t *y);
+
+/* encode_batched_affine_matvec_int4 (ops/quantized.rs:198-232): gate and up in
+ * one launch; gate's awq_scales divide the activation for both
+ * (ops/quantized.rs:218-224).  gate->n must equal up->n. */
+int imh_encode_batched_affine_matvec_int4(imh_stream *stream, const uint16_t *x,
+                                          uint32_t token_count,
+                                          const imh_affine_int4_weight *gate, uint16_t *gate_out,
+                                          const imh_affine_int4_weight *up, uint16_t *up_out);
+
+/* encode_fused_ffn_gate_up_act_int4 (ops/quantized.rs:238-270,
+ * affine_fused.metal:89-107): out = f16(act(gate) * up) with gate, up in f32;
+ * act = SiLU g/(1+e^-g), or tanh-GELU with the inner term clamped to +-10. */
+int imh_encode_fused_ffn_gate_up_act_int4(imh_stream *stream, const uint16_t *x,
+                                          uint32_t token_count,
+                                          const imh_affine_int4_weight *gate,
+                                          const imh_affine_int4_weight *up, uint16_t *out,
+                                          int use_gelu);
+
+/* FusedResidualNormAffineInt4Params (ops/fused.rs:45-66) with a token count. */
+typedef struct {
+    const uint16_t *a;           /* [token_count][k] */
+    const uint16_t *b;           /* [token_count][k] */
+    const uint16_t *norm_weight; /* [k] */
+    uint16_t *residual_output;   /* [token_count][k]: f16(a + b) */
+    const imh_affine_int4_weight *weight;
+    uint16_t *output;            /* [token_count][n] */
+    uint16_t *normed_output;     /* [token_count][k]: f16((a+b) * rms_inv * gamma) */
+    uint32_t token_count;
+    float eps;
+} imh_fused_residual_norm_params;
+
+/* encode_fused_residual_norm_affine_matvec_int4 (ops/fused.rs:102-129,
+ * superblock_fused_norm.metal:37-124): r = a + b, rms_inv = 1/sqrt(mean(r^2)+eps),
+ * output = f16(rms_inv * sum_k r_k*gamma_k(/awq_k) * W[n][k]). */
+int imh_encode_fused_residual_norm_affine_matvec_int4(imh_stream *stream,
+                                                      const imh_fused_residual_norm_params *p);
+
+/* Activation operand image.  The INT4 ops above first rewrite their activation
+ * (x / awq, or (a + b) * gamma / awq with a per-row rms factor) into the order
+ * the matrix-core kernel consumes, then run the matvec.  These two entry points
+ * expose the two steps, so a producer can build the image once for several
+ * projections and a caller can time the matvec kernel alone.  No reference
+ * counterpart: the Metal kernels read x directly. */
+typedef struct {
+    const uint16_t *hi;      /* [token_count][k] f16 in kernel operand order */
+    const uint16_t *lo;      /* residual halves, or NULL when x is exactly f16 */
+    const float *row_scale;  /* [token_count] output multiplier, or NULL */
+    uint32_t token_count;
+    uint32_t k;
+} imh_int4_activation;
+
+/* Bytes of caller storage imh_encode_int4_activation needs. */
+size_t imh_int4_activation_bytes(uint32_t token_count, uint32_t k);
+/* Build the image of x [token_count][k] (divided by awq[k] when awq != NULL)
+ * in `storage` (16-byte aligned, imh_int4_activation_bytes long). */
+int imh_encode_int4_activation(imh_stream *stream, const uint16_t *x, uint32_t token_count,
+                               uint32_t k, const uint16_t *awq, void *storage,
+                               imh_int4_activation *out);
+#define IMH_EPI_STORE 0     /* out0 = f16(W0 x) [, out1 = f16(W1 x)] */
+#define IMH_EPI_SILU 2      /* out0 = f16(silu(W0 x) * (W1 x)) */
+#define IMH_EPI_GELU 3      /* out0 = f16(gelu_tanh(W0 x) * (W1 x)) */
+/* Matvec over a prepared activation: one weight (w1 == NULL, IMH_EPI_STORE) or
+ * a gate/up pair sharing the activation. */
+int imh_encode_int4_matvec_prepared(imh_stream *stream, const imh_int4_activation *act,
+                                    const imh_affine_int4_weight *w0,
+                                    const imh_affine_int4_weight *w1, int epilogue,
+                                    uint16_t *out0, uint16_t *out1);
+
+/* ====================== op tier: TurboQuant INT8 KV cache ====================== */
+
+/* MetalTurboQuantModel (metal/turboquant/mod.rs:51-79,221-287): rotation signs
+ * (seed), K codebook of 2^(n_bits-1) Lloyd-Max levels + boundaries, V codebook of
+ * 2^n_bits levels + boundaries, QJL matrix [head_dim][head_dim] (seed + 1).
+ * head_dim must be a power of two (IMH_EINVAL otherwise, mod.rs:222-226); the
+ * kernels are built for head_dim 128 and n_bits 8 (IMH_EUNSUPPORTED otherwise). */
+int imh_tq_tables_create(imh_device *dev, uint32_t head_dim, uint32_t n_bits,
+                         uint64_t rotation_seed, imh_tq_tables **out);
+/* Same from caller-provided host tables (f32): signs[head_dim],
+ * k_codebook[2^(n_bits-1)], k_bounds[2^(n_bits-1)-1], v_codebook[2^n_bits],
+ * v_bounds[2^n_bits-1], qjl[head_dim*head_dim] row-major. */
+int imh_tq_tables_create_from_host(imh_device *dev, uint32_t head_dim, uint32_t n_bits,
+                                   const float *signs, const float *k_codebook,
+                                   const float *k_bounds, const float *v_codebook,
+                                   const float *v_bounds, const float *qjl,
+                                   imh_tq_tables **out);
+void imh_tq_tables_free(imh_tq_tables *t);
+#define IMH_TQ_SIGNS 0
+#define IMH_TQ_K_CODEBOOK 1
+#define IMH_TQ_K_BOUNDS 2
+#define IMH_TQ_V_CODEBOOK 3
+#define IMH_TQ_V_BOUNDS 4
+#define IMH_TQ_QJL 5
+/* Copy one table back to the host; *count receives its length in floats. */
+int imh_tq_tables_read(const imh_tq_tables *t, int which, float *dst, size_t capacity,
+                       size_t *count);
+
+/* One layer of MetalKvCache (metal/turboquant/cache.rs:45-96) for `batch`
+ * sequences, TurboQuantCacheLayout (turboquant/cache_layout.rs:83-142) per sequence:
+ *   k_codes, v_codes: [batch][num_kv_heads][max_seq_len][head_dim] bytes
+ *     (K byte = 7-bit codebook index | QJL sign in bit 7; V byte = 8-bit index);
+ *   k_scales, v_scales, k_r_norms: [batch][num_kv_heads][max_seq_len] f32. */
+typedef struct {
+    uint8_t *k_codes;
+    uint8_t *v_codes;
+    float *k_scales;
+    float *v_scales;
+    float *k_r_norms;
+    uint32_t batch;
+    uint32_t num_kv_heads;
+    uint32_t head_dim;
+    uint32_t max_seq_len;
+} imh_tq_kv_cache;
+
+/* Byte sizes of the five arrays above (cache_layout.rs:83-142). */
+int imh_tq_cache_sizes(uint32_t batch, uint32_t num_kv_heads, uint32_t head_dim,
+                       uint32_t max_seq_len, size_t *codes_bytes, size_t *scale_bytes);
+
+/* turboquant_cache_write (turboquant.metal:52-170) as encoded at
+ * attention.rs:344-391, for K (is_k = 1) or V (is_k = 0):
+ * kv_proj [batch][token_count][num_kv_heads][head_dim] f16; token t of sequence b
+ * goes to position ((positions ? positions[b] : base_pos) + t) % max_seq_len.
+ * positions is a device int32 array [batch] or NULL. */
+int imh_encode_turboquant_cache_write(imh_stream *stream, const imh_tq_tables *t,
+                                      const imh_tq_kv_cache *cache, const uint16_t *kv_proj,
+                                      uint32_t token_count, uint32_t base_pos,
+                                      const int32_t *positions, int is_k);
+
+/* Decode attention over the cache (turboquant_attention, turboquant.metal:202-462,
+ * + the split/LSE combine of fused_sdpa_reduce, flash_decode.metal:163-215):
+ * q [batch][num_heads][head_dim] f16, GQA head h reads kv head h/(num_heads/num_kv_heads),
+ * sequence b attends to positions [0, seq_lens ? seq_lens[b] : seq_len);
+ * out [batch][num_heads][head_dim] f16.  num_splits = 0 picks the KV split
+ * count from the shape; seq_len > max_seq_len is IMH_ERANGE. */
+int imh_encode_turboquant_attention(imh_stream *stream, const imh_tq_tables *t,
+                                    const imh_tq_kv_cache *cache, const uint16_t *q,
+                                    uint32_t num_heads, uint32_t seq_len,
+                                    const int32_t *seq_lens, float attn_scale, uint16_t *out,
+                                    uint32_t num_splits);
+
+/* encode_kv_cache_and_attention (attention.rs:117-610), decode step (one token
+ * per sequence): write K and V at position seq_pos, then attend over
+ * [0, seq_pos + 1). */
+int imh_encode_kv_cache_and_attention(imh_stream *stream, const imh_tq_tables *t,
+                                      const imh_tq_kv_cache *cache, const uint16_t *k_proj,
+                                      const uint16_t *v_proj, const uint16_t *q,
+                                      uint32_t num_heads, uint32_t seq_pos, float attn_scale,
+                                      uint16_t *out);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* IRONMILL_HIP_H */

@@ -1,0 +1,187 @@
+"""ctypes binding of libironmill_hip.so (the C ABI in include/ironmill_hip.h).
+
+The shared library is the product: every op runs there.  There is no Python
+or CPU fallback -- if the library is missing, importing this module raises.
+"""
+from __future__ import annotations
+
+import ctypes as C
+import os
+
+_HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(_HERE, "lib", "libironmill_hip.so")
+
+IMH_OK = 0
+IMH_EINVAL = -1
+IMH_EUNSUPPORTED = -2
+IMH_EDEVICE = -3
+IMH_ENOMEM = -4
+IMH_ERANGE = -5
+
+ERROR_NAMES = {
+    IMH_EINVAL: "IMH_EINVAL",
+    IMH_EUNSUPPORTED: "IMH_EUNSUPPORTED",
+    IMH_EDEVICE: "IMH_EDEVICE",
+    IMH_ENOMEM: "IMH_ENOMEM",
+    IMH_ERANGE: "IMH_ERANGE",
+}
+
+IMH_TQ_SIGNS, IMH_TQ_K_CODEBOOK, IMH_TQ_K_BOUNDS, IMH_TQ_V_CODEBOOK, IMH_TQ_V_BOUNDS, IMH_TQ_QJL = range(6)
+
+
+class IronmillError(RuntimeError):
+    """A non-zero status from the C ABI, with the library's own message."""
+
+    def __init__(self, code: int, message: str):
+        self.code = code
+        super().__init__(f"{ERROR_NAMES.get(code, code)}: {message}")
+
+
+class DeviceInfo(C.Structure):
+    _fields_ = [
+        ("ordinal", C.c_int),
+        ("compute_units", C.c_int),
+        ("wavefront_size", C.c_int),
+        ("clock_khz", C.c_int),
+        ("total_global_mem", C.c_size_t),
+        ("lds_per_block", C.c_size_t),
+        ("arch", C.c_char * 64),
+    ]
+
+
+class AffineInt4Weight(C.Structure):
+    """imh_affine_int4_weight (AffineQuantizedWeight, metal/weights.rs:129-147)."""
+
+    _fields_ = [
+        ("data", C.c_void_p),
+        ("scales", C.c_void_p),
+        ("zeros", C.c_void_p),
+        ("awq_scales", C.c_void_p),
+        ("n", C.c_uint32),
+        ("k", C.c_uint32),
+        ("group_size", C.c_uint32),
+    ]
+
+
+class FusedResidualNormParams(C.Structure):
+    """imh_fused_residual_norm_params (FusedResidualNormAffineInt4Params, ops/fused.rs:45-66)."""
+
+    _fields_ = [
+        ("a", C.c_void_p),
+        ("b", C.c_void_p),
+        ("norm_weight", C.c_void_p),
+        ("residual_output", C.c_void_p),
+        ("weight", C.POINTER(AffineInt4Weight)),
+        ("output", C.c_void_p),
+        ("normed_output", C.c_void_p),
+        ("token_count", C.c_uint32),
+        ("eps", C.c_float),
+    ]
+
+
+class Int4Activation(C.Structure):
+    """imh_int4_activation: the operand image the INT4 kernels consume."""
+
+    _fields_ = [
+        ("hi", C.c_void_p),
+        ("lo", C.c_void_p),
+        ("row_scale", C.c_void_p),
+        ("token_count", C.c_uint32),
+        ("k", C.c_uint32),
+    ]
+
+
+IMH_EPI_STORE, IMH_EPI_SILU, IMH_EPI_GELU = 0, 2, 3
+
+
+class TqKvCache(C.Structure):
+    """imh_tq_kv_cache (one layer of MetalKvCache, metal/turboquant/cache.rs:45-96)."""
+
+    _fields_ = [
+        ("k_codes", C.c_void_p),
+        ("v_codes", C.c_void_p),
+        ("k_scales", C.c_void_p),
+        ("v_scales", C.c_void_p),
+        ("k_r_norms", C.c_void_p),
+        ("batch", C.c_uint32),
+        ("num_kv_heads", C.c_uint32),
+        ("head_dim", C.c_uint32),
+        ("max_seq_len", C.c_uint32),
+    ]
+
+
+P = C.c_void_p
+U32 = C.c_uint32
+SZ = C.c_size_t
+I = C.c_int
+
+# name -> (restype, argtypes); kept in the order of include/ironmill_hip.h
+SIGNATURES = {
+    "imh_last_error": (C.c_char_p, []),
+    "imh_device_count": (I, [C.POINTER(I)]),
+    "imh_device_open": (I, [I, C.POINTER(P)]),
+    "imh_device_free": (None, [P]),
+    "imh_device_get_info": (I, [P, C.POINTER(DeviceInfo)]),
+    "imh_buffer_alloc": (I, [P, SZ, C.POINTER(P)]),
+    "imh_buffer_alloc_with_data": (I, [P, P, SZ, C.POINTER(P)]),
+    "imh_buffer_free": (None, [P]),
+    "imh_buffer_length": (SZ, [P]),
+    "imh_buffer_device_ptr": (P, [P]),
+    "imh_buffer_write": (I, [P, SZ, P, SZ]),
+    "imh_buffer_read": (I, [P, SZ, P, SZ]),
+    "imh_stream_create": (I, [P, C.POINTER(P)]),
+    "imh_stream_free": (None, [P]),
+    "imh_stream_sync": (I, [P]),
+    "imh_stream_native": (P, [P]),
+    "imh_fill_zero": (I, [P, P, SZ]),
+    "imh_event_create": (I, [P, C.POINTER(P)]),
+    "imh_event_free": (None, [P]),
+    "imh_event_record": (I, [P, P]),
+    "imh_event_elapsed_ms": (I, [P, P, C.POINTER(C.c_float)]),
+    "imh_encode_affine_projection_int4": (I, [P, P, U32, C.POINTER(AffineInt4Weight), P]),
+    "imh_encode_batched_affine_matvec_int4": (I, [P, P, U32, C.POINTER(AffineInt4Weight), P,
+                                                  C.POINTER(AffineInt4Weight), P]),
+    "imh_encode_fused_ffn_gate_up_act_int4": (I, [P, P, U32, C.POINTER(AffineInt4Weight),
+                                                  C.POINTER(AffineInt4Weight), P, I]),
+    "imh_encode_fused_residual_norm_affine_matvec_int4": (I, [P, C.POINTER(FusedResidualNormParams)]),
+    "imh_int4_activation_bytes": (SZ, [U32, U32]),
+    "imh_encode_int4_activation": (I, [P, P, U32, U32, P, P, C.POINTER(Int4Activation)]),
+    "imh_encode_int4_matvec_prepared": (I, [P, C.POINTER(Int4Activation), C.POINTER(AffineInt4Weight),
+                                            C.POINTER(AffineInt4Weight), I, P, P]),
+    "imh_tq_tables_create": (I, [P, U32, U32, C.c_uint64, C.POINTER(P)]),
+    "imh_tq_tables_create_from_host": (I, [P, U32, U32, P, P, P, P, P, P, C.POINTER(P)]),
+    "imh_tq_tables_free": (None, [P]),
+    "imh_tq_tables_read": (I, [P, I, P, SZ, C.POINTER(SZ)]),
+    "imh_tq_cache_sizes": (I, [U32, U32, U32, U32, C.POINTER(SZ), C.POINTER(SZ)]),
+    "imh_encode_turboquant_cache_write": (I, [P, P, C.POINTER(TqKvCache), P, U32, U32, P, I]),
+    "imh_encode_turboquant_attention": (I, [P, P, C.POINTER(TqKvCache), P, U32, U32, P, C.c_float, P,
+                                            U32]),
+    "imh_encode_kv_cache_and_attention": (I, [P, P, C.POINTER(TqKvCache), P, P, P, U32, U32, C.c_float,
+                                              P]),
+}
+
+
+def _load():
+    if not os.path.exists(LIB_PATH):
+        raise ImportError(
+            f"libironmill_hip.so not found at {LIB_PATH}; build it with "
+            "`python ironmill_amd/build.py` (hipcc, gfx950)")
+    lib = C.CDLL(LIB_PATH)
+    for name, (res, args) in SIGNATURES.items():
+        fn = getattr(lib, name)
+        fn.restype = res
+        fn.argtypes = args
+    return lib
+
+
+lib = _load()
+
+
+def last_error() -> str:
+    msg = lib.imh_last_error()
+    return msg.decode(errors="replace") if msg else ""
+
+
+def check(rc: int) -> None:
+    if rc != IMH_OK:
+        raise IronmillError(rc, last_error())

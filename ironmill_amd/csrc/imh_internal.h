@@ -1,0 +1,71 @@
+// imh_internal.h -- shared host-side definitions of libironmill_hip.
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <cstddef>
+#include <cstdint>
+#include <string>
+
+#include "../../include/ironmill_hip.h"
+
+namespace imh {
+
+// Thread-local last-error text (ironmill-compile-ffi/src/lib.rs:69-79 pattern).
+int fail(int code, const std::string &msg);
+int hip_fail(hipError_t e, const char *what);
+void clear_error();
+
+#define IMH_HIP(call)                                  \
+    do {                                               \
+        hipError_t e_ = (call);                        \
+        if (e_ != hipSuccess) return imh::hip_fail(e_, #call); \
+    } while (0)
+
+}  // namespace imh
+
+struct imh_device {
+    int ordinal;
+    hipDeviceProp_t props;
+};
+
+struct imh_buffer {
+    imh_device *dev;
+    void *ptr;
+    size_t length;
+};
+
+// Per-stream scratch memory, grown on demand by the host code of an op.
+struct imh_stream {
+    imh_device *dev;
+    hipStream_t stream;
+    void *scratch;
+    size_t scratch_bytes;
+};
+
+struct imh_event {
+    imh_device *dev;
+    hipEvent_t ev;
+};
+
+struct imh_tq_tables {
+    imh_device *dev;
+    uint32_t head_dim;
+    uint32_t n_bits;
+    // one device allocation holding all tables, f32:
+    //   signs[d] | k_cb[2^(b-1)] | k_bd[2^(b-1)-1] | v_cb[2^b] | v_bd[2^b-1] | qjl[d*d] | qjl_t[d*d]
+    float *base;
+    float *signs, *k_codebook, *k_bounds, *v_codebook, *v_bounds, *qjl, *qjl_t;
+    size_t total_floats;
+};
+
+namespace imh {
+
+// Ensure the stream's scratch holds at least `bytes`; synchronises the stream
+// before replacing a smaller allocation.
+int stream_scratch(imh_stream *s, size_t bytes, void **out);
+
+// Make the stream's device current for the calling thread.
+int use_device(const imh_device *dev);
+
+}  // namespace imh

@@ -1,0 +1,528 @@
+// tq_kernels.hip -- TurboQuant INT8 KV cache: cache write and GQA decode attention.
+//
+// Cache write (turboquant.metal:52-170): rotate by R = D.H.D/sqrt(d), L2 norm as
+// the per-(token, head) scale, nearest-centroid index by boundary scan; for K
+// the 7-bit index is completed by the sign of the QJL projection of the
+// residual.  The f32 operation order is fixed (halving-stride tree sums over
+// the 128 lanes, fmaf QJL dot in increasing k, no contraction elsewhere) so the
+// codes are reproducible bit for bit by the CPU oracle.
+//
+// Decode attention (turboquant.metal:202-462 semantics; the structure is this
+// file's own): one workgroup per (KV split, kv head, sequence) serves all
+// query heads of the GQA group, so each KV byte is read once per group instead
+// of once per query head.  Per 16-position chunk a wave
+//   * builds the dequantized K chunk as MFMA operand B with one LDS lookup per
+//     byte (codebook entry as an f16 hi/lo pair) plus the +-1 QJL signs taken
+//     straight from bit 7, and runs v_mfma_f32_16x16x32_f16 against the rotated
+//     query (and its QJL projection) as operand A, both split hi + lo;
+//   * folds the per-position scales in, runs an online softmax per head with
+//     16-lane shuffles, and accumulates V (codebook lookup * weight) in f32.
+// Waves combine through LDS; splits are combined (log-sum-exp) and rotated
+// back by a second small kernel (fused_sdpa_reduce, flash_decode.metal:163-215).
+#include <hip/hip_runtime.h>
+#include <hip/hip_fp16.h>
+
+#include <algorithm>
+#include <cmath>
+#include <string>
+
+#include "imh_internal.h"
+
+namespace {
+
+typedef _Float16 half8_t __attribute__((ext_vector_type(8)));
+typedef float float4_t __attribute__((ext_vector_type(4)));
+
+constexpr int kD = 128;          // head_dim the kernels are built for
+constexpr int kChunk = 16;       // positions per MFMA block
+constexpr int kWaves = 4;        // waves per attention workgroup
+constexpr int kSplitQuantum = kChunk * kWaves;
+
+// ---------------------------------------------------------------------------
+// cache write: grid (num_kv_heads, token_count, batch), block kD
+// ---------------------------------------------------------------------------
+__global__ void __launch_bounds__(kD) tq_cache_write_kernel(
+    const __half *__restrict__ kv, int tokens, int nkv, int max_seq, int base_pos,
+    const int32_t *__restrict__ positions, int is_k, const float *__restrict__ signs,
+    const float *__restrict__ codebook, const float *__restrict__ bounds, int n_levels,
+    const float *__restrict__ qjl_t, uint8_t *__restrict__ cache, float *__restrict__ scales,
+    float *__restrict__ r_norms) {
+#pragma clang fp contract(off)
+    __shared__ float x[kD];
+    __shared__ float red[kD];
+    __shared__ float res[kD];
+    __shared__ float bnd[256];
+
+    const int i = threadIdx.x;
+    const int h = blockIdx.x, t = blockIdx.y, b = blockIdx.z;
+    const int nb = n_levels - 1;
+    for (int j = i; j < nb; j += kD) bnd[j] = bounds[j];
+
+    const long long start = positions ? (long long)positions[b] : (long long)base_pos;
+    long long pl = (start + t) % max_seq;
+    if (pl < 0) pl += max_seq;
+    const size_t slot = ((size_t)b * nkv + h) * (size_t)max_seq + (size_t)pl;
+    const size_t src = (((size_t)b * tokens + t) * nkv + h) * kD;
+
+    const float sg = signs[i];
+    x[i] = __half2float(kv[src + i]) * sg;
+    __syncthreads();
+    for (int step = 1; step < kD; step *= 2) {
+        if (i < kD / 2) {
+            const int j = (i / step) * (step * 2) + (i % step);
+            const float a = x[j], c = x[j + step];
+            x[j] = a + c;
+            x[j + step] = a - c;
+        }
+        __syncthreads();
+    }
+    const float rscale = 1.0f / sqrtf((float)kD);
+    const float xr = x[i] * (sg * rscale);
+
+    red[i] = xr * xr;
+    __syncthreads();
+    for (int s = kD / 2; s > 0; s >>= 1) {
+        if (i < s) red[i] = red[i] + red[i + s];
+        __syncthreads();
+    }
+    const float l2 = __fsqrt_rn(fmaxf(red[0], 1e-20f));
+    const float inv = __fdiv_rn(1.0f, fmaxf(l2, 1e-10f));
+    const float u = xr * inv;
+    int idx = 0;
+    for (int j = 0; j < nb; j++) idx = (u >= bnd[j]) ? j + 1 : idx;
+    uint32_t code = (uint32_t)idx;
+
+    if (is_k) {
+        const float r = u - codebook[idx];
+        res[i] = r;
+        __syncthreads();  // every lane has read red[0] above
+        red[i] = r * r;
+        __syncthreads();
+        for (int s = kD / 2; s > 0; s >>= 1) {
+            if (i < s) red[i] = red[i] + red[i + s];
+            __syncthreads();
+        }
+        const float rn = __fsqrt_rn(fmaxf(red[0], 1e-20f));
+        float acc = 0.0f;
+        for (int k = 0; k < kD; k++) acc = __builtin_fmaf(qjl_t[(size_t)k * kD + i], res[k], acc);
+        if (acc >= 0.0f) code |= 0x80u;
+        if (i == 0) r_norms[slot] = rn;
+    }
+    cache[slot * kD + i] = (uint8_t)code;
+    if (i == 0) scales[slot] = l2;
+}
+
+// ---------------------------------------------------------------------------
+// decode attention: grid (num_splits, num_kv_heads, batch), block 64 * kWaves
+// ---------------------------------------------------------------------------
+__device__ __forceinline__ float shfl_xor16(float v, int m) { return __shfl_xor(v, m, 16); }
+
+template <int GQA>
+__global__ void __launch_bounds__(64 * kWaves) tq_attention_kernel(
+    const __half *__restrict__ q, int nh, int nkv, int max_seq, int seq_len,
+    const int32_t *__restrict__ seq_lens, float attn_scale, const float *__restrict__ signs,
+    const float *__restrict__ kcb, const float *__restrict__ vcb, const float *__restrict__ qjl_t,
+    const uint8_t *__restrict__ kcodes, const uint8_t *__restrict__ vcodes,
+    const float *__restrict__ kscales, const float *__restrict__ vscales,
+    const float *__restrict__ krnorm, int split_len, float *__restrict__ part_o,
+    float *__restrict__ part_m, float *__restrict__ part_l) {
+    __shared__ float qs[GQA][kD];
+    __shared__ float ss[GQA][kD];
+    __shared__ uint32_t ktab[128];
+    __shared__ float vtab[256];
+    __shared__ float om[kWaves][GQA][kD];
+    __shared__ float mm[kWaves][GQA];
+    __shared__ float ll[kWaves][GQA];
+
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int wave = tid >> 6;
+    const int split = blockIdx.x, kvh = blockIdx.y, b = blockIdx.z;
+    const int S = gridDim.x;
+
+    // tables: K codebook as (f16 hi | f16 lo << 16), V codebook in f32
+    if (tid < 128) {
+        const float c = kcb[tid];
+        const _Float16 hi = (_Float16)c;
+        const _Float16 lo = (_Float16)(c - (float)hi);
+        ktab[tid] = (uint32_t)__builtin_bit_cast(uint16_t, hi) |
+                    ((uint32_t)__builtin_bit_cast(uint16_t, lo) << 16);
+    }
+    vtab[tid] = vcb[tid];
+
+    // rotate the GQA group's queries: q_rot = D.H.D/sqrt(d) q
+    for (int e = tid; e < GQA * kD; e += 64 * kWaves) {
+        const int hh = e / kD, d = e % kD;
+        qs[hh][d] = __half2float(q[((size_t)b * nh + kvh * GQA + hh) * kD + d]) * signs[d];
+    }
+    __syncthreads();
+    for (int step = 1; step < kD; step *= 2) {
+        for (int e = tid; e < GQA * kD / 2; e += 64 * kWaves) {
+            const int hh = e / (kD / 2), i = e % (kD / 2);
+            const int j = (i / step) * (step * 2) + (i % step);
+            const float a = qs[hh][j], c = qs[hh][j + step];
+            qs[hh][j] = a + c;
+            qs[hh][j + step] = a - c;
+        }
+        __syncthreads();
+    }
+    const float rscale = 1.0f / sqrtf((float)kD);
+    for (int e = tid; e < GQA * kD; e += 64 * kWaves) {
+        const int hh = e / kD, d = e % kD;
+        qs[hh][d] = qs[hh][d] * (signs[d] * rscale);
+    }
+    __syncthreads();
+    // QJL projection of the rotated query: s_q[d] = sum_k S[d][k] q_rot[k]
+    for (int e = tid; e < GQA * kD; e += 64 * kWaves) {
+        const int hh = e / kD, d = e % kD;
+        float acc = 0.0f;
+        for (int k = 0; k < kD; k++) acc = __builtin_fmaf(qjl_t[(size_t)k * kD + d], qs[hh][k], acc);
+        ss[hh][d] = acc;
+    }
+    __syncthreads();
+
+    // operand A (rows = heads of the group, hi and lo halves), k-slot order
+    // within each 4-byte word: bytes {0, 2, 1, 3}
+    const int am = lane & 15;
+    const int kg = lane >> 4;
+    half8_t aq_hi[4], aq_lo[4], as_hi[4], as_lo[4];
+    constexpr int slot_byte[8] = {0, 2, 1, 3, 4, 6, 5, 7};
+#pragma unroll
+    for (int j = 0; j < 4; j++) {
+#pragma unroll
+        for (int i = 0; i < 8; i++) {
+            float vq = 0.0f, vs = 0.0f;
+            if (am < GQA) {
+                const int d = kg * 32 + j * 8 + slot_byte[i];
+                vq = qs[am][d];
+                vs = ss[am][d];
+            }
+            const _Float16 qh = (_Float16)vq, sh = (_Float16)vs;
+            aq_hi[j][i] = qh;
+            aq_lo[j][i] = (_Float16)(vq - (float)qh);
+            as_hi[j][i] = sh;
+            as_lo[j][i] = (_Float16)(vs - (float)sh);
+        }
+    }
+
+    int L = seq_lens ? seq_lens[b] : seq_len;
+    L = L < 0 ? 0 : (L > max_seq ? max_seq : L);
+    const int p_begin = split * split_len;
+    const int p_end = min(p_begin + split_len, L);
+    const size_t head_base = ((size_t)b * nkv + kvh) * (size_t)max_seq;
+    const float qjl_factor = sqrtf(2.0f / 3.14159265f) / (float)kD;
+
+    float m_run[GQA], l_run[GQA];
+    float o[GQA][16];
+#pragma unroll
+    for (int hh = 0; hh < GQA; hh++) {
+        m_run[hh] = -INFINITY;
+        l_run[hh] = 0.0f;
+#pragma unroll
+        for (int e = 0; e < 16; e++) o[hh][e] = 0.0f;
+    }
+
+    const int n_l = lane & 15;
+    const int vgrp = lane & 7;    // which 16-dim slice of V this lane accumulates
+    const int vpos = lane >> 3;   // which of 8 positions per round
+
+    for (int p0 = p_begin + wave * kChunk; p0 < p_end; p0 += kChunk * kWaves) {
+        // ---- scores: S[h][n] for 16 positions via MFMA ----
+        const int pk = min(p0 + n_l, p_end - 1);
+        const uint4 *kp = reinterpret_cast<const uint4 *>(kcodes + (head_base + pk) * kD + kg * 32);
+        const uint4 k0 = kp[0], k1 = kp[1];
+        const uint32_t kw[8] = {k0.x, k0.y, k0.z, k0.w, k1.x, k1.y, k1.z, k1.w};
+        float4_t d1 = {0, 0, 0, 0}, d2 = {0, 0, 0, 0};
+#pragma unroll
+        for (int j = 0; j < 4; j++) {
+            uint32_t bh[4], bl[4], bs[4];
+#pragma unroll
+            for (int hw = 0; hw < 2; hw++) {
+                const uint32_t w = kw[2 * j + hw];
+                const uint32_t t0 = ktab[w & 0x7F];
+                const uint32_t t1 = ktab[(w >> 8) & 0x7F];
+                const uint32_t t2 = ktab[(w >> 16) & 0x7F];
+                const uint32_t t3 = ktab[(w >> 24) & 0x7F];
+                bh[2 * hw] = __builtin_amdgcn_perm(t2, t0, 0x05040100u);
+                bl[2 * hw] = __builtin_amdgcn_perm(t2, t0, 0x07060302u);
+                bh[2 * hw + 1] = __builtin_amdgcn_perm(t3, t1, 0x05040100u);
+                bl[2 * hw + 1] = __builtin_amdgcn_perm(t3, t1, 0x07060302u);
+                const uint32_t nw = ~w;
+                bs[2 * hw] = ((nw << 8) & 0x80008000u) | 0x3C003C00u;
+                bs[2 * hw + 1] = (nw & 0x80008000u) | 0x3C003C00u;
+            }
+            const half8_t Bh = __builtin_bit_cast(half8_t, make_uint4(bh[0], bh[1], bh[2], bh[3]));
+            const half8_t Bl = __builtin_bit_cast(half8_t, make_uint4(bl[0], bl[1], bl[2], bl[3]));
+            const half8_t Bs = __builtin_bit_cast(half8_t, make_uint4(bs[0], bs[1], bs[2], bs[3]));
+            d1 = __builtin_amdgcn_mfma_f32_16x16x32_f16(aq_hi[j], Bh, d1, 0, 0, 0);
+            d1 = __builtin_amdgcn_mfma_f32_16x16x32_f16(aq_lo[j], Bh, d1, 0, 0, 0);
+            d1 = __builtin_amdgcn_mfma_f32_16x16x32_f16(aq_hi[j], Bl, d1, 0, 0, 0);
+            d2 = __builtin_amdgcn_mfma_f32_16x16x32_f16(as_hi[j], Bs, d2, 0, 0, 0);
+            d2 = __builtin_amdgcn_mfma_f32_16x16x32_f16(as_lo[j], Bs, d2, 0, 0, 0);
+        }
+        // lanes 0..15 hold D[h][n] for h = 0..3 (rows), position p0 + n
+        const bool valid = (p0 + n_l) < p_end;
+        const float ksc = kscales[head_base + pk];
+        const float qw = krnorm[head_base + pk] * qjl_factor * ksc;
+        const float vsc = vscales[head_base + pk];
+        float wgt[GQA];
+        float corr[GQA];
+        bool rescale = false;
+#pragma unroll
+        for (int hh = 0; hh < GQA; hh++) {
+            float sc = valid ? attn_scale * (d1[hh] * ksc + d2[hh] * qw) : -INFINITY;
+            float cm = sc;
+            cm = fmaxf(cm, shfl_xor16(cm, 8));
+            cm = fmaxf(cm, shfl_xor16(cm, 4));
+            cm = fmaxf(cm, shfl_xor16(cm, 2));
+            cm = fmaxf(cm, shfl_xor16(cm, 1));
+            cm = __shfl(cm, 0);
+            const float nm = fmaxf(m_run[hh], cm);
+            corr[hh] = __expf(m_run[hh] - nm);
+            const float w = __expf(sc - nm);
+            float ws = w;
+            ws += shfl_xor16(ws, 8);
+            ws += shfl_xor16(ws, 4);
+            ws += shfl_xor16(ws, 2);
+            ws += shfl_xor16(ws, 1);
+            ws = __shfl(ws, 0);
+            l_run[hh] = l_run[hh] * corr[hh] + ws;
+            m_run[hh] = nm;
+            wgt[hh] = w * vsc;
+            rescale |= corr[hh] != 1.0f;
+        }
+        if (rescale) {
+#pragma unroll
+            for (int hh = 0; hh < GQA; hh++)
+#pragma unroll
+                for (int e = 0; e < 16; e++) o[hh][e] *= corr[hh];
+        }
+        // ---- o += w * V over the chunk: lane covers 16 dims of one position per round ----
+#pragma unroll
+        for (int r = 0; r < 2; r++) {
+            const int pi = r * 8 + vpos;
+            float wv[GQA];
+#pragma unroll
+            for (int hh = 0; hh < GQA; hh++) wv[hh] = __shfl(wgt[hh], pi);
+            const int pv = min(p0 + pi, p_end - 1);
+            const uint4 vv = *reinterpret_cast<const uint4 *>(vcodes + (head_base + pv) * kD + vgrp * 16);
+            const uint32_t vw[4] = {vv.x, vv.y, vv.z, vv.w};
+#pragma unroll
+            for (int e = 0; e < 16; e++) {
+                const float v = vtab[(vw[e >> 2] >> (8 * (e & 3))) & 0xFF];
+#pragma unroll
+                for (int hh = 0; hh < GQA; hh++) o[hh][e] = __builtin_fmaf(wv[hh], v, o[hh][e]);
+            }
+        }
+    }
+
+    // reduce the 8 position lanes that share a V slice
+#pragma unroll
+    for (int hh = 0; hh < GQA; hh++)
+#pragma unroll
+        for (int e = 0; e < 16; e++) {
+            float v = o[hh][e];
+            v += __shfl_xor(v, 8);
+            v += __shfl_xor(v, 16);
+            v += __shfl_xor(v, 32);
+            o[hh][e] = v;
+        }
+    if (lane < 8) {
+#pragma unroll
+        for (int hh = 0; hh < GQA; hh++)
+#pragma unroll
+            for (int e = 0; e < 16; e++) om[wave][hh][lane * 16 + e] = o[hh][e];
+    }
+    if (lane == 0) {
+#pragma unroll
+        for (int hh = 0; hh < GQA; hh++) {
+            mm[wave][hh] = m_run[hh];
+            ll[wave][hh] = l_run[hh];
+        }
+    }
+    __syncthreads();
+    for (int e = tid; e < GQA * kD; e += 64 * kWaves) {
+        const int hh = e / kD, d = e % kD;
+        float M = -INFINITY;
+        for (int w = 0; w < kWaves; w++) M = fmaxf(M, mm[w][hh]);
+        float ov = 0.0f, lv = 0.0f;
+        if (M != -INFINITY) {
+            for (int w = 0; w < kWaves; w++) {
+                if (mm[w][hh] == -INFINITY) continue;
+                const float f = __expf(mm[w][hh] - M);
+                ov += om[w][hh][d] * f;
+                lv += ll[w][hh] * f;
+            }
+        }
+        const size_t pidx = ((size_t)b * nh + kvh * GQA + hh) * S + split;
+        part_o[pidx * kD + d] = ov;
+        if (d == 0) {
+            part_m[pidx] = M;
+            part_l[pidx] = lv;
+        }
+    }
+}
+
+// combine splits, normalise, rotate back: grid (num_heads, batch), block kD
+__global__ void __launch_bounds__(kD) tq_attention_reduce_kernel(
+    const float *__restrict__ part_o, const float *__restrict__ part_m,
+    const float *__restrict__ part_l, const float *__restrict__ signs, int nh, int S,
+    __half *__restrict__ out) {
+    __shared__ float x[kD];
+    const int d = threadIdx.x;
+    const int h = blockIdx.x, b = blockIdx.y;
+    const size_t base = ((size_t)b * nh + h) * S;
+    float M = -INFINITY;
+    for (int s = 0; s < S; s++) M = fmaxf(M, part_m[base + s]);
+    float ov = 0.0f, lv = 0.0f;
+    if (M != -INFINITY) {
+        for (int s = 0; s < S; s++) {
+            const float m = part_m[base + s];
+            if (m == -INFINITY) continue;
+            const float f = __expf(m - M);
+            ov += part_o[(base + s) * kD + d] * f;
+            lv += part_l[base + s] * f;
+        }
+    }
+    const float sg = signs[d];
+    x[d] = (ov / fmaxf(lv, 1e-10f)) * sg;
+    __syncthreads();
+    for (int step = 1; step < kD; step *= 2) {
+        if (d < kD / 2) {
+            const int j = (d / step) * (step * 2) + (d % step);
+            const float a = x[j], c = x[j + step];
+            x[j] = a + c;
+            x[j + step] = a - c;
+        }
+        __syncthreads();
+    }
+    const float rscale = 1.0f / sqrtf((float)kD);
+    out[((size_t)b * nh + h) * kD + d] = __float2half(x[d] * (sg * rscale));
+}
+
+int check_cache(const imh_tq_tables *t, const imh_tq_kv_cache *c, const char *who) {
+    if (!t || !c) return imh::fail(IMH_EINVAL, std::string(who) + ": NULL tables or cache");
+    if (!c->k_codes || !c->v_codes || !c->k_scales || !c->v_scales || !c->k_r_norms)
+        return imh::fail(IMH_EINVAL, std::string(who) + ": a cache array is NULL");
+    if (c->head_dim != t->head_dim)
+        return imh::fail(IMH_EINVAL, std::string(who) + ": cache head_dim differs from the tables'");
+    if (c->head_dim != kD)
+        return imh::fail(IMH_EUNSUPPORTED, std::string(who) + ": kernels are built for head_dim 128");
+    if (c->batch == 0 || c->num_kv_heads == 0 || c->max_seq_len == 0)
+        return imh::fail(IMH_EINVAL, std::string(who) + ": empty cache shape");
+    if ((reinterpret_cast<uintptr_t>(c->k_codes) | reinterpret_cast<uintptr_t>(c->v_codes)) & 15)
+        return imh::fail(IMH_EINVAL, std::string(who) + ": code arrays must be 16-byte aligned");
+    return IMH_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+int imh_encode_turboquant_cache_write(imh_stream *stream, const imh_tq_tables *t,
+                                      const imh_tq_kv_cache *cache, const uint16_t *kv_proj,
+                                      uint32_t token_count, uint32_t base_pos,
+                                      const int32_t *positions, int is_k) {
+    const char *who = "imh_encode_turboquant_cache_write";
+    if (!stream || !kv_proj) return imh::fail(IMH_EINVAL, std::string(who) + ": NULL argument");
+    int rc = check_cache(t, cache, who);
+    if (rc) return rc;
+    if (token_count == 0) return IMH_OK;
+    rc = imh::use_device(stream->dev);
+    if (rc) return rc;
+    const int nlev = is_k ? (1 << (t->n_bits - 1)) : (1 << t->n_bits);
+    dim3 grid(cache->num_kv_heads, token_count, cache->batch);
+    hipLaunchKernelGGL(tq_cache_write_kernel, grid, dim3(kD), 0, stream->stream,
+                       reinterpret_cast<const __half *>(kv_proj), (int)token_count,
+                       (int)cache->num_kv_heads, (int)cache->max_seq_len, (int)base_pos, positions,
+                       is_k ? 1 : 0, t->signs, is_k ? t->k_codebook : t->v_codebook,
+                       is_k ? t->k_bounds : t->v_bounds, nlev, t->qjl_t,
+                       is_k ? cache->k_codes : cache->v_codes, is_k ? cache->k_scales : cache->v_scales,
+                       cache->k_r_norms);
+    IMH_HIP(hipGetLastError());
+    return IMH_OK;
+}
+
+int imh_encode_turboquant_attention(imh_stream *stream, const imh_tq_tables *t,
+                                    const imh_tq_kv_cache *cache, const uint16_t *q,
+                                    uint32_t num_heads, uint32_t seq_len, const int32_t *seq_lens,
+                                    float attn_scale, uint16_t *out, uint32_t num_splits) {
+    const char *who = "imh_encode_turboquant_attention";
+    if (!stream || !q || !out) return imh::fail(IMH_EINVAL, std::string(who) + ": NULL argument");
+    int rc = check_cache(t, cache, who);
+    if (rc) return rc;
+    const uint32_t nkv = cache->num_kv_heads;
+    if (num_heads == 0 || num_heads % nkv != 0)
+        return imh::fail(IMH_EINVAL, std::string(who) + ": num_heads must be a multiple of num_kv_heads");
+    const uint32_t gqa = num_heads / nkv;
+    if (gqa != 1 && gqa != 2 && gqa != 4)
+        return imh::fail(IMH_EUNSUPPORTED, std::string(who) + ": GQA group of " + std::to_string(gqa) +
+                                               " heads not built (1, 2, 4)");
+    if (seq_len > cache->max_seq_len)
+        return imh::fail(IMH_ERANGE, std::string(who) + ": seq_len " + std::to_string(seq_len) +
+                                         " exceeds max_seq_len " + std::to_string(cache->max_seq_len));
+    rc = imh::use_device(stream->dev);
+    if (rc) return rc;
+
+    // KV split: aim for ~1024 workgroups (4 per CU) with >= 64 positions each.
+    const uint32_t L = seq_len;
+    const uint32_t B = cache->batch;
+    uint32_t want = num_splits;
+    if (want == 0) {
+        const uint32_t groups = B * nkv;
+        want = (1024 + groups - 1) / groups;
+    }
+    const uint32_t max_splits = std::max<uint32_t>(1, (L + kSplitQuantum - 1) / kSplitQuantum);
+    want = std::max<uint32_t>(1, std::min(want, max_splits));
+    uint32_t split_len = (L + want - 1) / want;
+    split_len = std::max<uint32_t>(kSplitQuantum,
+                                   (split_len + kSplitQuantum - 1) / kSplitQuantum * kSplitQuantum);
+    const uint32_t S = std::max<uint32_t>(1, (L + split_len - 1) / split_len);
+
+    const size_t nparts = (size_t)B * num_heads * S;
+    const size_t need = nparts * kD * 4 + nparts * 8 + 512;
+    void *scr = nullptr;
+    rc = imh::stream_scratch(stream, need, &scr);
+    if (rc) return rc;
+    float *po = static_cast<float *>(scr);
+    float *pm = po + nparts * kD;
+    float *pl = pm + nparts;
+
+    dim3 grid(S, nkv, B);
+    const __half *qh = reinterpret_cast<const __half *>(q);
+#define IMH_TQ_LAUNCH(G)                                                                            \
+    hipLaunchKernelGGL(tq_attention_kernel<G>, grid, dim3(64 * kWaves), 0, stream->stream, qh,      \
+                       (int)num_heads, (int)nkv, (int)cache->max_seq_len, (int)seq_len, seq_lens,   \
+                       attn_scale, t->signs, t->k_codebook, t->v_codebook, t->qjl_t, cache->k_codes, \
+                       cache->v_codes, cache->k_scales, cache->v_scales, cache->k_r_norms,          \
+                       (int)split_len, po, pm, pl)
+    if (gqa == 4) IMH_TQ_LAUNCH(4);
+    else if (gqa == 2) IMH_TQ_LAUNCH(2);
+    else IMH_TQ_LAUNCH(1);
+#undef IMH_TQ_LAUNCH
+    IMH_HIP(hipGetLastError());
+    hipLaunchKernelGGL(tq_attention_reduce_kernel, dim3(num_heads, B), dim3(kD), 0, stream->stream, po,
+                       pm, pl, t->signs, (int)num_heads, (int)S, reinterpret_cast<__half *>(out));
+    IMH_HIP(hipGetLastError());
+    return IMH_OK;
+}
+
+int imh_encode_kv_cache_and_attention(imh_stream *stream, const imh_tq_tables *t,
+                                      const imh_tq_kv_cache *cache, const uint16_t *k_proj,
+                                      const uint16_t *v_proj, const uint16_t *q, uint32_t num_heads,
+                                      uint32_t seq_pos, float attn_scale, uint16_t *out) {
+    const char *who = "imh_encode_kv_cache_and_attention";
+    int rc = check_cache(t, cache, who);
+    if (rc) return rc;
+    if ((uint64_t)seq_pos + 1 > cache->max_seq_len)
+        return imh::fail(IMH_ERANGE, std::string(who) + ": position " + std::to_string(seq_pos) +
+                                         " is beyond max_seq_len " + std::to_string(cache->max_seq_len));
+    rc = imh_encode_turboquant_cache_write(stream, t, cache, k_proj, 1, seq_pos, nullptr, 1);
+    if (rc) return rc;
+    rc = imh_encode_turboquant_cache_write(stream, t, cache, v_proj, 1, seq_pos, nullptr, 0);
+    if (rc) return rc;
+    return imh_encode_turboquant_attention(stream, t, cache, q, num_heads, seq_pos + 1, nullptr, attn_scale,
+                                           out, 0);
+}
+
+}  // extern "C"

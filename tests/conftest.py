@@ -1,0 +1,51 @@
+"""Shared test setup: the `gpu` marker, repo on sys.path, device fixtures."""
+import os
+import sys
+
+import numpy as np
+import pytest
+
+REPO = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+if REPO not in sys.path:
+    sys.path.insert(0, REPO)
+
+
+def pytest_configure(config):
+    config.addinivalue_line("markers", "gpu: needs an MI355X (runs through the C ABI)")
+
+
+@pytest.fixture(scope="session")
+def dev():
+    from ironmill_amd import Device
+    d = Device(0)
+    yield d
+
+
+@pytest.fixture(scope="session")
+def stream(dev):
+    s = dev.stream()
+    yield s
+    s.sync()
+
+
+def rel_l2(got, ref):
+    got = np.asarray(got, np.float64)
+    ref = np.asarray(ref, np.float64)
+    den = np.linalg.norm(ref)
+    return float(np.linalg.norm(got - ref) / (den if den > 0 else 1.0))
+
+
+# fp32 accumulate, fp16 out
+REL_L2_TOL = 1e-3
+MAX_ABS_TOL = 2e-2
+
+
+def assert_close(got, ref, rel=REL_L2_TOL, max_abs=MAX_ABS_TOL, what=""):
+    got = np.asarray(got, np.float64)
+    ref = np.asarray(ref, np.float64)
+    assert got.shape == ref.shape, (what, got.shape, ref.shape)
+    assert np.all(np.isfinite(got)), f"{what}: non-finite output"
+    r = rel_l2(got, ref)
+    m = float(np.max(np.abs(got - ref))) if got.size else 0.0
+    assert r <= rel and m <= max_abs, f"{what}: rel_l2={r:.3e} (tol {rel}) max_abs={m:.3e} (tol {max_abs})"
+    return r, m

@@ -1,0 +1,184 @@
+"""GPU parity of the INT4 affine ops against the CPU oracle, through the C ABI.
+
+The expected values come from the oracle's own chain -- quantize_tensor_int4
+(quantized.rs:408-465) -> dequant_affine with f32 params (core/dequant.rs:85-180)
+-> f32-accumulate dot -- on the same seeded inputs; the GPU gets its weights
+from the library's host quantizer, so a mismatch in either shows up here.
+Tolerance: rel-L2 <= 1e-3 and max-abs <= 2e-2 on
+the f16 outputs.
+"""
+import numpy as np
+import pytest
+
+import oracle as O
+from conftest import assert_close
+from ironmill_amd import IronmillError, ops, quant
+
+pytestmark = pytest.mark.gpu
+
+
+def make_weight(n, k, seed, awq=False):
+    rng = np.random.default_rng(seed)
+    w = (rng.standard_normal((n, k)) * 0.02).astype(np.float16).astype(np.float32)
+    s = rng.uniform(0.5, 2.0, k).astype(np.float32) if awq else None
+    return w, s
+
+
+def make_x(batch, k, seed, outliers=True):
+    rng = np.random.default_rng(seed + 1000)
+    x = rng.standard_normal((batch, k)).astype(np.float32)
+    if outliers:  # 1 % of channels x20
+        idx = rng.choice(k, max(1, k // 100), replace=False)
+        x[:, idx] *= 20.0
+    return x.astype(np.float16)
+
+
+def oracle_dense(w, s):
+    """Oracle quantize + CPU dequant -> dense f16 W and the f16 AWQ vector."""
+    wq = w if s is None else (w * s[None, :]).astype(np.float32)
+    packed, sc, zp = O.quantize_tensor_int4(wq, 128)
+    n, k = w.shape
+    wdq = O.dequant_affine_int4(packed, sc, zp, n, k, 128)
+    awq16 = None if s is None else s.astype(np.float16)
+    return wdq, awq16
+
+
+def upload_weight(dev, w, s):
+    return ops.AffineQuantizedWeight(dev, quant.quantize_int4(w, awq_scales=s))
+
+
+@pytest.mark.parametrize("n,k,batch,awq", [
+    (1024, 1024, 1, False),
+    (1024, 1024, 4, True),
+    (1000, 256, 3, False),    # ragged N (not a multiple of 16)
+    (64, 128, 17, True),      # one group, batch beyond one 16-row MFMA tile
+    (2560, 9728, 1, True),    # Qwen3-4B down projection
+    (2560, 9728, 8, True),
+    (4096, 2560, 1, False),   # Qwen3-4B Q projection
+])
+def test_projection_matches_oracle(dev, stream, n, k, batch, awq):
+    w, s = make_weight(n, k, seed=n + k + batch, awq=awq)
+    x16 = make_x(batch, k, seed=n * 7 + k)
+    wt = upload_weight(dev, w, s)
+    xd = dev.upload(x16)
+    yd = dev.empty((batch, n), np.float16)
+    ops.encode_projection(stream, xd, wt, yd, batch)
+    stream.sync()
+    got = yd.read()
+    wdq, awq16 = oracle_dense(w, s)
+    ref = O.matvec_f16w(wdq, x16, awq16, nthreads=8)
+    assert_close(got, ref, what=f"projection n={n} k={k} B={batch} awq={awq}")
+
+
+@pytest.mark.parametrize("batch", [1, 4, 8])
+@pytest.mark.parametrize("act", ["silu", "gelu"])
+def test_fused_gate_up_qwen_shape(dev, stream, batch, act):
+    n, k = 9728, 2560
+    wg, s = make_weight(n, k, seed=11, awq=True)
+    wu, _ = make_weight(n, k, seed=12, awq=False)
+    x16 = make_x(batch, k, seed=13 + batch)
+    q_up = quant.quantize_int4(wu, awq_scales=s)  # gate's AWQ divides x for both (ops/quantized.rs:218-224)
+    gate = upload_weight(dev, wg, s)
+    up = ops.AffineQuantizedWeight(dev, q_up)
+    xd = dev.upload(x16)
+    out = dev.empty((batch, n), np.float16)
+    ops.encode_fused_ffn_gate_up_act_int4(stream, xd, gate, up, out, batch, use_gelu=(act == "gelu"))
+    stream.sync()
+    wdq_g, awq16 = oracle_dense(wg, s)
+    wdq_u, _ = oracle_dense(wu, s)
+    ref = O.gate_up_act(wdq_g, wdq_u, x16, awq16, act=act)
+    assert_close(out.read(), ref, what=f"fused gate+up {act} B={batch}")
+
+
+@pytest.mark.parametrize("batch,awq", [(1, True), (8, False)])
+def test_batched_gate_up(dev, stream, batch, awq):
+    n, k = 9728, 2560
+    wg, s = make_weight(n, k, seed=21, awq=awq)
+    wu, _ = make_weight(n, k, seed=22)
+    x16 = make_x(batch, k, seed=23)
+    gate = upload_weight(dev, wg, s)
+    up = ops.AffineQuantizedWeight(dev, quant.quantize_int4(wu, awq_scales=s))
+    xd = dev.upload(x16)
+    go, uo = dev.empty((batch, n), np.float16), dev.empty((batch, n), np.float16)
+    ops.encode_batched_affine_matvec_int4(stream, xd, gate, go, up, uo, batch)
+    stream.sync()
+    wdq_g, awq16 = oracle_dense(wg, s)
+    wdq_u, _ = oracle_dense(wu, s)
+    assert_close(go.read(), O.matvec_f16w(wdq_g, x16, awq16, nthreads=8), what="gate")
+    assert_close(uo.read(), O.matvec_f16w(wdq_u, x16, awq16, nthreads=8), what="up")
+
+
+@pytest.mark.parametrize("batch,awq", [(1, False), (1, True), (3, True)])
+def test_fused_residual_norm_projection(dev, stream, batch, awq):
+    n, k, eps = 4096, 2560, 1e-6
+    w, s = make_weight(n, k, seed=31, awq=awq)
+    rng = np.random.default_rng(32)
+    a = rng.standard_normal((batch, k)).astype(np.float16)
+    b = (rng.standard_normal((batch, k)) * 0.5).astype(np.float16)
+    gamma = rng.uniform(0.5, 1.5, k).astype(np.float16)
+    wt = upload_weight(dev, w, s)
+    ad, bd, gd = dev.upload(a), dev.upload(b), dev.upload(gamma)
+    y = dev.empty((batch, n), np.float16)
+    res = dev.empty((batch, k), np.float16)
+    nrm = dev.empty((batch, k), np.float16)
+    ops.encode_fused_residual_norm_affine_matvec_int4(stream, ad, bd, gd, res, wt, y, nrm, eps, batch)
+    stream.sync()
+    wdq, awq16 = oracle_dense(w, s)
+    y_ref, res_ref, nrm_ref = O.fused_residual_norm_matvec(a, b, gamma, wdq, eps, awq16)
+    assert_close(y.read(), y_ref, what="resnorm y")
+    # f16(a + b) is one f32 add and one RNE rounding on both sides: bit-exact
+    assert np.array_equal(res.read().view(np.uint16), res_ref.view(np.uint16))
+    assert_close(nrm.read(), nrm_ref.astype(np.float32), rel=1e-3, max_abs=2e-3, what="normed")
+
+
+def test_codes_equal_to_zero_point_give_exact_zero(dev, stream):
+    """Closed form: q == z everywhere -> (q - z) * s == 0, so y == 0 exactly."""
+    n, k = 256, 1024
+    q = quant.QuantizedInt4(
+        data=np.full((n, k // 2), 0x77, np.uint8),
+        scales=np.full((n, k // 128), 0.01, np.float16), zeros=np.full((n, k // 128), 7.0, np.float16),
+        scales_f32=None, zeros_f32=None, awq=None, n=n, k=k)
+    wt = ops.AffineQuantizedWeight(dev, q)
+    x16 = make_x(4, k, seed=5)
+    xd, yd = dev.upload(x16), dev.empty((4, n), np.float16)
+    ops.encode_projection(stream, xd, wt, yd, 4)
+    stream.sync()
+    assert np.array_equal(yd.read().view(np.uint16), np.zeros((4, n), np.uint16))
+
+
+def test_single_nibble_picks_one_column(dev, stream):
+    """Closed form: one code differs from z by d at (r, c) -> y[r] = x[c] * d * s."""
+    n, k = 32, 256
+    codes = np.full((n, k), 8, np.uint8)
+    codes[5, 77] = 11   # +3 steps
+    codes[20, 200] = 2  # -6 steps
+    data = (codes[:, 1::2] << 4 | codes[:, 0::2]).astype(np.uint8)
+    q = quant.QuantizedInt4(data=data, scales=np.full((n, 2), 0.25, np.float16),
+                            zeros=np.full((n, 2), 8.0, np.float16), scales_f32=None, zeros_f32=None,
+                            awq=None, n=n, k=k)
+    wt = ops.AffineQuantizedWeight(dev, q)
+    x16 = make_x(1, k, seed=9, outliers=False)
+    xd, yd = dev.upload(x16), dev.empty((1, n), np.float16)
+    ops.encode_projection(stream, xd, wt, yd, 1)
+    stream.sync()
+    exp = np.zeros(n, np.float32)
+    exp[5] = np.float32(x16[0, 77]) * 3 * 0.25
+    exp[20] = np.float32(x16[0, 200]) * -6 * 0.25
+    assert np.array_equal(yd.read()[0], exp.astype(np.float16))
+
+
+def test_error_paths(dev, stream):
+    w, _ = make_weight(64, 256, seed=1)
+    wt = upload_weight(dev, w, None)
+    bad = ops.AffineQuantizedWeight.from_pointers(wt.data, wt.scales, wt.zeros, None, 64, 256, 64)
+    xd, yd = dev.upload(make_x(1, 256, 2)), dev.empty((1, 64), np.float16)
+    with pytest.raises(IronmillError, match="group_size"):
+        ops.encode_projection(stream, xd, bad, yd, 1)
+    bad_k = ops.AffineQuantizedWeight.from_pointers(wt.data, wt.scales, wt.zeros, None, 64, 200, 128)
+    with pytest.raises(IronmillError, match="multiple of 128"):
+        ops.encode_projection(stream, xd, bad_k, yd, 1)
+    other = ops.AffineQuantizedWeight.from_pointers(wt.data, wt.scales, wt.zeros, None, 32, 256, 128)
+    with pytest.raises(IronmillError, match="shapes differ"):
+        ops.encode_fused_ffn_gate_up_act_int4(stream, xd, wt, other, yd, 1)
+    ops.encode_projection(stream, xd, wt, yd, 0)  # zero tokens: no-op
+    stream.sync()

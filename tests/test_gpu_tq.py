@@ -1,0 +1,185 @@
+"""GPU parity of the TurboQuant INT8 KV cache ops against the CPU oracle.
+
+* tables made by the library == the oracle's restatement of
+  MetalTurboQuantModel::new (mod.rs:221-287), bit for bit;
+* cache-write codes, scales and residual norms == oracle, bit for bit
+  (turboquant.metal:52-170 in the fixed f32 order both sides implement);
+* decode attention == oracle's f64 dequantize-then-compute attention within
+  rel-L2 <= 1e-3 and max-abs <= 2e-2, for single/split KV ranges, ragged and
+  empty sequences, GQA 1/2/4, and the 32k-context configuration.
+"""
+import math
+
+import numpy as np
+import pytest
+
+import oracle as O
+from conftest import assert_close
+from ironmill_amd import IronmillError, ops
+
+pytestmark = pytest.mark.gpu
+
+D = 128
+
+
+@pytest.fixture(scope="module")
+def tq(dev):
+    return ops.TurboQuantModel(dev, D, 8, 42)
+
+
+@pytest.fixture(scope="module")
+def tables():
+    return O.TQTables(D, 8, 42)
+
+
+def kv_data(batch, tokens, nkv, seed):
+    """K/V fp16 N(0,1) with 4 seeded outlier channels per head scaled x10."""
+    rng = np.random.default_rng(seed)
+    x = rng.standard_normal((batch, tokens, nkv, D)).astype(np.float32)
+    for h in range(nkv):
+        ch = rng.choice(D, 4, replace=False)
+        x[:, :, h, ch] *= 10.0
+    return x.astype(np.float16)
+
+
+def test_tables_match_oracle(tq, tables):
+    t = tq.tables()
+    for name in ("signs", "k_codebook", "k_bounds", "v_codebook", "v_bounds"):
+        ref = getattr(tables, name)
+        assert np.array_equal(t[name].view(np.uint32), ref.view(np.uint32)), name
+    assert np.array_equal(t["qjl"].view(np.uint32), tables.qjl.view(np.uint32))
+
+
+@pytest.mark.parametrize("is_k", [True, False])
+def test_cache_write_bit_exact(dev, stream, tq, tables, is_k):
+    batch, tokens, nkv, max_seq = 3, 5, 8, 64
+    kv = kv_data(batch, tokens, nkv, seed=7 + is_k)
+    positions = np.array([0, 17, 62], np.int32)  # the last one wraps around (% max_seq)
+    cache = ops.TurboQuantKvCache(dev, batch, nkv, D, max_seq)
+    cache.zero(stream)
+    kd, pd = dev.upload(kv), dev.upload(positions)
+    ops.encode_turboquant_cache_write(stream, tq, cache, kd, tokens, 0, is_k, positions=pd)
+    stream.sync()
+    codes_ref, sc_ref, rn_ref = O.tq_cache_write(kv, tables, is_k, max_seq, positions=positions)
+    codes = (cache.k_codes if is_k else cache.v_codes).read()
+    scales = (cache.k_scales if is_k else cache.v_scales).read()
+    assert np.array_equal(codes, codes_ref)
+    assert np.array_equal(scales.view(np.uint32), sc_ref.view(np.uint32))
+    if is_k:
+        assert np.array_equal(cache.k_r_norms.read().view(np.uint32), rn_ref.view(np.uint32))
+
+
+def fill_cache(dev, stream, tq, batch, nkv, max_seq, ctx, seed):
+    cache = ops.TurboQuantKvCache(dev, batch, nkv, D, max_seq)
+    cache.zero(stream)
+    k = kv_data(batch, ctx, nkv, seed)
+    v = kv_data(batch, ctx, nkv, seed + 1)
+    kd, vd = dev.upload(k), dev.upload(v)
+    ops.encode_turboquant_cache_write(stream, tq, cache, kd, ctx, 0, True)
+    ops.encode_turboquant_cache_write(stream, tq, cache, vd, ctx, 0, False)
+    stream.sync()
+    return cache
+
+
+def read_cache(cache):
+    return (cache.k_codes.read(), cache.v_codes.read(), cache.k_scales.read(), cache.v_scales.read(),
+            cache.k_r_norms.read())
+
+
+def run_attention(dev, stream, tq, cache, q16, nh, seq_len, seq_lens=None, num_splits=0):
+    qd = dev.upload(q16)
+    out = dev.empty(q16.shape, np.float16)
+    sl = dev.upload(np.asarray(seq_lens, np.int32)) if seq_lens is not None else None
+    ops.encode_turboquant_attention(stream, tq, cache, qd, nh, seq_len, out, 1.0 / math.sqrt(D),
+                                    seq_lens=sl, num_splits=num_splits)
+    stream.sync()
+    return out.read()
+
+
+@pytest.mark.parametrize("nh,nkv", [(32, 8), (16, 8), (8, 8)])
+@pytest.mark.parametrize("num_splits", [0, 1, 7])
+def test_attention_matches_oracle(dev, stream, tq, tables, nh, nkv, num_splits):
+    batch, ctx, max_seq = 2, 300, 512
+    cache = fill_cache(dev, stream, tq, batch, nkv, max_seq, ctx, seed=100 + nh)
+    q16 = np.random.default_rng(5).standard_normal((batch, nh, D)).astype(np.float16)
+    got = run_attention(dev, stream, tq, cache, q16, nh, ctx, num_splits=num_splits)
+    kc, vc, ks, vs, kr = read_cache(cache)
+    ref = O.tq_attention(q16, tables, kc, vc, ks, vs, kr, ctx, 1.0 / math.sqrt(D), nthreads=8)
+    assert_close(got, ref, what=f"attention nh={nh} nkv={nkv} splits={num_splits}")
+
+
+def test_split_and_single_pass_agree(dev, stream, tq):
+    cache = fill_cache(dev, stream, tq, 1, 8, 4096, 4000, seed=3)
+    q16 = np.random.default_rng(6).standard_normal((1, 32, D)).astype(np.float16)
+    a = run_attention(dev, stream, tq, cache, q16, 32, 4000, num_splits=1).astype(np.float32)
+    b = run_attention(dev, stream, tq, cache, q16, 32, 4000, num_splits=40).astype(np.float32)
+    assert_close(a, b, rel=2e-3, max_abs=2e-3, what="split vs single")
+
+
+def test_ragged_and_empty_sequences(dev, stream, tq, tables):
+    batch, nkv, nh, max_seq = 4, 8, 32, 512
+    cache = fill_cache(dev, stream, tq, batch, nkv, max_seq, 400, seed=9)
+    lens = np.array([400, 1, 0, 77], np.int32)
+    q16 = np.random.default_rng(8).standard_normal((batch, nh, D)).astype(np.float16)
+    got = run_attention(dev, stream, tq, cache, q16, nh, 400, seq_lens=lens)
+    kc, vc, ks, vs, kr = read_cache(cache)
+    ref = O.tq_attention(q16, tables, kc, vc, ks, vs, kr, 400, 1.0 / math.sqrt(D), seq_lens=lens,
+                         nthreads=8)
+    assert_close(got, ref, what="ragged")
+    assert np.array_equal(got[2].view(np.uint16), np.zeros((nh, D), np.uint16))  # empty -> 0
+
+
+def test_single_position_returns_rotated_value(dev, stream, tq, tables):
+    """seq_len 1: softmax weight is 1, so out = R (vcb[c] * v_scale) exactly (closed form)."""
+    cache = fill_cache(dev, stream, tq, 1, 8, 64, 1, seed=11)
+    q16 = np.random.default_rng(1).standard_normal((1, 32, D)).astype(np.float16)
+    got = run_attention(dev, stream, tq, cache, q16, 32, 1)
+    vc, vs = cache.v_codes.read(), cache.v_scales.read()
+    for h in range(32):
+        kvh = h // 4
+        v = tables.v_codebook[vc[0, kvh, 0]].astype(np.float64) * vs[0, kvh, 0]
+        ref = O.hadamard_rotate(v.astype(np.float32), tables.signs)
+        assert_close(got[0, h], ref, rel=1e-3, max_abs=4e-3, what=f"head {h}")
+
+
+@pytest.mark.parametrize("batch,ctx", [(1, 32768), (16, 2048)])
+def test_attention_full_size(dev, stream, tq, tables, batch, ctx):
+    nkv, nh = 8, 32
+    cache = fill_cache(dev, stream, tq, batch, nkv, ctx, ctx, seed=ctx + batch)
+    q16 = np.random.default_rng(12).standard_normal((batch, nh, D)).astype(np.float16)
+    got = run_attention(dev, stream, tq, cache, q16, nh, ctx)
+    kc, vc, ks, vs, kr = read_cache(cache)
+    ref = O.tq_attention(q16, tables, kc, vc, ks, vs, kr, ctx, 1.0 / math.sqrt(D), nthreads=8)
+    assert_close(got, ref, what=f"full size B={batch} ctx={ctx}")
+
+
+def test_decode_step_write_then_attend(dev, stream, tq, tables):
+    batch, nkv, nh, max_seq, pos = 2, 8, 32, 256, 150
+    cache = fill_cache(dev, stream, tq, batch, nkv, max_seq, pos, seed=21)
+    k1, v1 = kv_data(batch, 1, nkv, 22), kv_data(batch, 1, nkv, 23)
+    q16 = np.random.default_rng(24).standard_normal((batch, nh, D)).astype(np.float16)
+    out = dev.empty((batch, nh, D), np.float16)
+    ops.encode_kv_cache_and_attention(stream, tq, cache, dev.upload(k1), dev.upload(v1),
+                                      dev.upload(q16), nh, pos, out)
+    stream.sync()
+    kc, vc, ks, vs, kr = read_cache(cache)
+    kc1, ks1, kr1 = O.tq_cache_write(k1, tables, True, 1)
+    assert np.array_equal(kc[:, :, pos], kc1[:, :, 0]) and np.array_equal(ks[:, :, pos], ks1[:, :, 0])
+    ref = O.tq_attention(q16, tables, kc, vc, ks, vs, kr, pos + 1, 1.0 / math.sqrt(D), nthreads=8)
+    assert_close(out.read(), ref, what="decode step")
+
+
+def test_attention_error_paths(dev, stream, tq):
+    cache = ops.TurboQuantKvCache(dev, 1, 8, D, 64)
+    q = dev.empty((1, 32, D), np.float16)
+    out = dev.empty((1, 32, D), np.float16)
+    with pytest.raises(IronmillError, match="exceeds max_seq_len"):
+        ops.encode_turboquant_attention(stream, tq, cache, q, 32, 65, out)
+    with pytest.raises(IronmillError, match="multiple of num_kv_heads"):
+        ops.encode_turboquant_attention(stream, tq, cache, q, 30, 10, out)
+    with pytest.raises(IronmillError, match="beyond max_seq_len"):
+        ops.encode_kv_cache_and_attention(stream, tq, cache, q, q, q, 32, 64, out)
+    with pytest.raises(IronmillError, match="power of two"):
+        ops.TurboQuantModel(dev, 96, 8, 42)
+    with pytest.raises(IronmillError, match="built for head_dim 128"):
+        ops.TurboQuantModel(dev, 64, 8, 42)
