@@ -36,11 +36,15 @@ struct imh_buffer {
 };
 
 // Per-stream scratch memory, grown on demand by the host code of an op.
+// Slot 0: activation operand images; slot 1: split partials (matvec, attention);
+// slot 2: arrival counters, zero-filled when allocated and left at zero by
+// every kernel that uses them.
+constexpr int kScratchSlots = 3;
 struct imh_stream {
     imh_device *dev;
     hipStream_t stream;
-    void *scratch;
-    size_t scratch_bytes;
+    void *scratch[kScratchSlots];
+    size_t scratch_bytes[kScratchSlots];
 };
 
 struct imh_event {
@@ -61,9 +65,9 @@ struct imh_tq_tables {
 
 namespace imh {
 
-// Ensure the stream's scratch holds at least `bytes`; synchronises the stream
-// before replacing a smaller allocation.
-int stream_scratch(imh_stream *s, size_t bytes, void **out);
+// Ensure scratch slot `slot` of the stream holds at least `bytes`; synchronises
+// the stream before replacing a smaller allocation.  Slot 2 is zero-filled.
+int stream_scratch(imh_stream *s, int slot, size_t bytes, void **out);
 
 // Make the stream's device current for the calling thread.
 int use_device(const imh_device *dev);

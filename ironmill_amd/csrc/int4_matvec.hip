@@ -41,8 +41,7 @@ typedef float float4_t __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
 
 constexpr int kGS = 128;       // group size the kernels are built for
-constexpr int kMaxGroups = 12; // groups one wave may own (its weights stay in registers)
-constexpr int kMaxWaves = 8;
+constexpr int kMaxGroups = 10; // groups one item may own (its weights stay in registers)
 
 enum Epi : int { EPI_STORE = IMH_EPI_STORE, EPI_SILU = IMH_EPI_SILU, EPI_GELU = IMH_EPI_GELU };
 
@@ -169,121 +168,160 @@ __global__ void __launch_bounds__(256) int4_prep_resnorm(
 // ---------------------------------------------------------------------------
 // main matvec kernel
 // ---------------------------------------------------------------------------
-// grid (ceil(N/16), ceil(B/16)), block 64 * NMAT * parts.
-// Wave w handles matrix w / parts and the group range of part w % parts.
+// grid (tiles * S, ceil(B/16)), block 64: one wave per item.  Item = 16 weight
+// rows of each of the NMAT matrices x the K range of split `s` (kc groups).
+//   1. every weight load of the item is issued (NMAT * kc 16-byte loads/lane);
+//   2. the wave copies its activation slice (<= 16 batch rows x kc*128, hi and
+//      lo planes) into LDS, so all activation misses overlap in one round trip;
+//   3. per group: operand B from the nibbles, operand A from LDS, MFMAs, and
+//      the group's f32 partial is scaled by s into the running accumulator;
+//   4. with S > 1 the item stores its partial; the last item of a tile to
+//      arrive (atomic counter) sums the S partials in split order -- the same
+//      order on every run -- applies the epilogue and re-arms the counter.
 template <int NMAT, int EPI, bool HAS_LO>
-__global__ void __launch_bounds__(512) int4_matvec_kernel(MatPtrs mp, const _Float16 *__restrict__ xa_hi,
-                                                           const _Float16 *__restrict__ xa_lo,
-                                                           const float *__restrict__ rms_inv, int N,
-                                                           int K, int B, int parts) {
-    __shared__ float4_t red[kMaxWaves][64];
+__global__ void __launch_bounds__(64) int4_matvec_kernel(
+    MatPtrs mp, const _Float16 *__restrict__ xa_hi, const _Float16 *__restrict__ xa_lo,
+    const float *__restrict__ rms_inv, int N, int K, int B, int S, int kc,
+    float *__restrict__ partial, unsigned *__restrict__ counters) {
+    extern __shared__ __attribute__((aligned(16))) _Float16 xs[];
 
-    const int lane = threadIdx.x & 63;
-    const int wave = threadIdx.x >> 6;
-    const int mat = wave / parts;
-    const int part = wave - mat * parts;
+    const int lane = threadIdx.x;
     const int G = K / kGS;
-    const int g0 = (part * G) / parts;
-    const int g1 = ((part + 1) * G) / parts;
-    const int ng = g1 - g0;
-
-    const int n_l = lane & 15;   // weight row within the tile (B operand column)
-    const int kq = lane >> 4;    // which 16-byte quarter of a group this lane reads
-    const int row = blockIdx.x * 16 + n_l;
-    const int row_c = row < N ? row : N - 1;
+    const int item = blockIdx.x;
+    const int tile = item / S;
+    const int split = item - tile * S;
+    const int g0 = split * kc;
+    const int ng = min(g0 + kc, G) - g0;
     const int m0 = blockIdx.y * 16;
-    const int mb = m0 + n_l;     // batch row this lane supplies to operand A
-    const bool a_on = mb < B;
+    const int bc = min(16, B - m0);
+    const int RS = kc * kGS + 8;          // LDS row stride in halfs (16-byte pad)
 
-    const uint8_t *wrow = mp.data[mat] + (size_t)row_c * (K / 2) + kq * 16;
-    const __half *srow = mp.scales[mat] + (size_t)row_c * G;
-    const __half *zrow = mp.zeros[mat] + (size_t)row_c * G;
+    const int n_l = lane & 15;            // weight row within the tile (B operand column)
+    const int kq = lane >> 4;             // 16-byte quarter of a group this lane reads
+    const int row = tile * 16 + n_l;
+    const int row_c = row < N ? row : N - 1;
 
-    // Issue every weight load of this wave's K slice up front.
-    u32x4_t wq[kMaxGroups];
-    _Float16 sc[kMaxGroups], zr[kMaxGroups];
+    // 1. weights, scales, zeros of the whole item
+    u32x4_t wq[NMAT][kMaxGroups];
+    _Float16 sc[NMAT][kMaxGroups], zr[NMAT][kMaxGroups];
 #pragma unroll
-    for (int i = 0; i < kMaxGroups; i++) {
-        if (i < ng) {
-            const int g = g0 + i;
-            wq[i] = __builtin_nontemporal_load(reinterpret_cast<const u32x4_t *>(wrow + (size_t)g * 64));
-            sc[i] = reinterpret_cast<const _Float16 *>(srow)[g];
-            zr[i] = reinterpret_cast<const _Float16 *>(zrow)[g];
-        }
-    }
-
-    const _Float16 *xh_row = xa_hi + (size_t)(a_on ? mb : 0) * K + kq * 32;
-    const _Float16 *xl_row = HAS_LO ? xa_lo + (size_t)(a_on ? mb : 0) * K + kq * 32 : nullptr;
-
-    half8_t ah[4], al[4], ah_n[4], al_n[4];
-    auto load_a = [&](int g, half8_t *hi, half8_t *lo) {
+    for (int mt = 0; mt < NMAT; mt++) {
+        const uint8_t *wrow = mp.data[mt] + (size_t)row_c * (K / 2) + kq * 16;
+        const _Float16 *srow = reinterpret_cast<const _Float16 *>(mp.scales[mt]) + (size_t)row_c * G;
+        const _Float16 *zrow = reinterpret_cast<const _Float16 *>(mp.zeros[mt]) + (size_t)row_c * G;
 #pragma unroll
-        for (int j = 0; j < 4; j++) {
-            if (a_on) {
-                hi[j] = *reinterpret_cast<const half8_t *>(xh_row + (size_t)g * kGS + j * 8);
-                if (HAS_LO) lo[j] = *reinterpret_cast<const half8_t *>(xl_row + (size_t)g * kGS + j * 8);
-            } else {
-                hi[j] = (half8_t){0, 0, 0, 0, 0, 0, 0, 0};
-                if (HAS_LO) lo[j] = (half8_t){0, 0, 0, 0, 0, 0, 0, 0};
-            }
-        }
-    };
-    if (ng > 0) load_a(g0, ah, al);
-
-    float4_t acc = {0.0f, 0.0f, 0.0f, 0.0f};
-#pragma unroll
-    for (int i = 0; i < kMaxGroups; i++) {
-        if (i < ng) {
-            if (i + 1 < ng) load_a(g0 + i + 1, ah_n, al_n);
-            const float s = (float)sc[i];
-            const _Float16 nb = (_Float16)(-(1024.0f + (float)zr[i]));
-            const half2_t bias = {nb, nb};
-            const uint32_t wv[4] = {wq[i][0], wq[i][1], wq[i][2], wq[i][3]};
-            float4_t accg = {0.0f, 0.0f, 0.0f, 0.0f};
-#pragma unroll
-            for (int j = 0; j < 4; j++) {
-                const uint32_t w = wv[j];
-                half8_t bq;
-#pragma unroll
-                for (int p = 0; p < 4; p++) {
-                    const uint32_t bits = ((w >> (4 * p)) & 0x000F000Fu) | 0x64006400u;
-                    const half2_t d = as_h2(bits) + bias;   // (q_p - z, q_{p+4} - z), exact
-                    bq[2 * p] = d[0];
-                    bq[2 * p + 1] = d[1];
-                }
-                accg = __builtin_amdgcn_mfma_f32_16x16x32_f16(ah[j], bq, accg, 0, 0, 0);
-                if (HAS_LO) accg = __builtin_amdgcn_mfma_f32_16x16x32_f16(al[j], bq, accg, 0, 0, 0);
-            }
-#pragma unroll
-            for (int r = 0; r < 4; r++) acc[r] = __builtin_fmaf(accg[r], s, acc[r]);
-            if (i + 1 < ng) {
-#pragma unroll
-                for (int j = 0; j < 4; j++) {
-                    ah[j] = ah_n[j];
-                    if (HAS_LO) al[j] = al_n[j];
-                }
+        for (int i = 0; i < kMaxGroups; i++) {
+            if (i < ng) {
+                const int g = g0 + i;
+                wq[mt][i] = *reinterpret_cast<const u32x4_t *>(wrow + (size_t)g * 64);
+                sc[mt][i] = srow[g];
+                zr[mt][i] = zrow[g];
             }
         }
     }
 
-    red[wave][lane] = acc;
+    // 2. activation slice -> LDS (hi plane, then lo plane)
+    {
+        const int per_row = ng * 16;      // 8-half chunks per batch row
+        const int chunks = bc * per_row;
+        for (int c = lane; c < chunks; c += 64) {
+            const int r = c / per_row;
+            const int cc = c - r * per_row;
+            const size_t src = (size_t)(m0 + r) * K + (size_t)g0 * kGS + (size_t)cc * 8;
+            *reinterpret_cast<u32x4_t *>(xs + r * RS + cc * 8) =
+                *reinterpret_cast<const u32x4_t *>(xa_hi + src);
+            if (HAS_LO)
+                *reinterpret_cast<u32x4_t *>(xs + (bc + r) * RS + cc * 8) =
+                    *reinterpret_cast<const u32x4_t *>(xa_lo + src);
+        }
+    }
     __syncthreads();
 
-    // Epilogue.  Lane l holds D[m = 4*(l>>4) + r][n = l & 15].
-    const int mrow = 4 * (lane >> 4);
-    if (EPI == EPI_SILU || EPI == EPI_GELU) {
-        if (wave != 0) return;
-        float4_t gsum = {0, 0, 0, 0}, usum = {0, 0, 0, 0};
-        for (int p = 0; p < parts; p++) {
-            gsum += red[p][lane];
-            usum += red[parts + p][lane];
-        }
-        if (row >= N) return;
+    // 3. MFMA over the item's groups
+    const bool a_on = n_l < bc;
+    const _Float16 *xh = xs + n_l * RS + kq * 32;
+    const _Float16 *xl = xs + (bc + n_l) * RS + kq * 32;
+    float4_t acc[NMAT];
 #pragma unroll
-        for (int r = 0; r < 4; r++) {
-            const int m = m0 + mrow + r;
-            if (m >= B) break;
-            const float g = gsum[r], u = usum[r];
+    for (int mt = 0; mt < NMAT; mt++) acc[mt] = (float4_t){0.0f, 0.0f, 0.0f, 0.0f};
+    const half8_t zero8 = {0, 0, 0, 0, 0, 0, 0, 0};
+#pragma unroll
+    for (int i = 0; i < kMaxGroups; i++) {
+        if (i < ng) {
+            half8_t ah[4], al[4];
+#pragma unroll
+            for (int j = 0; j < 4; j++) {
+                ah[j] = a_on ? *reinterpret_cast<const half8_t *>(xh + i * kGS + j * 8) : zero8;
+                if (HAS_LO) al[j] = a_on ? *reinterpret_cast<const half8_t *>(xl + i * kGS + j * 8) : zero8;
+            }
+#pragma unroll
+            for (int mt = 0; mt < NMAT; mt++) {
+                const _Float16 nb = (_Float16)(-(1024.0f + (float)zr[mt][i]));
+                const half2_t bias = {nb, nb};
+                float4_t accg = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+                for (int j = 0; j < 4; j++) {
+                    const uint32_t w = wq[mt][i][j];
+                    half8_t bq;
+#pragma unroll
+                    for (int p = 0; p < 4; p++) {
+                        const uint32_t bits = ((w >> (4 * p)) & 0x000F000Fu) | 0x64006400u;
+                        const half2_t d = as_h2(bits) + bias;   // (q_p - z, q_{p+4} - z), exact
+                        bq[2 * p] = d[0];
+                        bq[2 * p + 1] = d[1];
+                    }
+                    accg = __builtin_amdgcn_mfma_f32_16x16x32_f16(ah[j], bq, accg, 0, 0, 0);
+                    if (HAS_LO) accg = __builtin_amdgcn_mfma_f32_16x16x32_f16(al[j], bq, accg, 0, 0, 0);
+                }
+                const float s = (float)sc[mt][i];
+#pragma unroll
+                for (int r = 0; r < 4; r++) acc[mt][r] = __builtin_fmaf(accg[r], s, acc[mt][r]);
+            }
+        }
+    }
+
+    // 4. split reduction.  Lane l holds D[m = 4*(l>>4) + r][n = l & 15].
+    const int mrow = m0 + 4 * (lane >> 4);
+    const size_t NT = (size_t)NMAT * N;
+    if (S > 1) {
+#pragma unroll
+        for (int mt = 0; mt < NMAT; mt++)
+#pragma unroll
+            for (int r = 0; r < 4; r++) {
+                const int m = mrow + r;
+                if (m < B && row < N) partial[((size_t)split * B + m) * NT + (size_t)mt * N + row] = acc[mt][r];
+            }
+        __threadfence();
+        unsigned prev = 0;
+        unsigned *ctr = counters + (size_t)tile * gridDim.y + blockIdx.y;
+        if (lane == 0) prev = atomicAdd(ctr, 1u);
+        prev = __shfl(prev, 0);
+        if (prev != (unsigned)(S - 1)) return;
+        __threadfence();
+#pragma unroll
+        for (int mt = 0; mt < NMAT; mt++)
+#pragma unroll
+            for (int r = 0; r < 4; r++) {
+                const int m = mrow + r;
+                float v = 0.0f;
+                if (m < B && row < N) {
+                    const float *src = partial + (size_t)m * NT + (size_t)mt * N + row;
+                    for (int sp = 0; sp < S; sp++) v += __builtin_nontemporal_load(src + (size_t)sp * B * NT);
+                }
+                acc[mt][r] = v;
+            }
+        if (lane == 0) *ctr = 0u;
+    }
+
+    // 5. epilogue
+    if (row >= N) return;
+#pragma unroll
+    for (int r = 0; r < 4; r++) {
+        const int m = mrow + r;
+        if (m >= B) break;
+        const float scale = rms_inv ? rms_inv[m] : 1.0f;
+        if (EPI == EPI_SILU || EPI == EPI_GELU) {
+            const float g = acc[0][r], u = acc[NMAT - 1][r];
             float act;
             if (EPI == EPI_SILU) {
                 act = g / (1.0f + __expf(-g));
@@ -292,22 +330,11 @@ __global__ void __launch_bounds__(512) int4_matvec_kernel(MatPtrs mp, const _Flo
                 inner = fminf(fmaxf(inner, -10.0f), 10.0f);
                 act = 0.5f * g * (1.0f + tanhf(inner));
             }
-            const float sc = rms_inv ? rms_inv[m] : 1.0f;
-            mp.out[0][(size_t)m * N + row] = __float2half(act * u * sc);
-        }
-    } else {
-        if (wave >= NMAT) return;
-        float4_t sum = {0, 0, 0, 0};
-        for (int p = 0; p < parts; p++) sum += red[wave * parts + p][lane];
-        if (row >= N) return;
-        __half *out = mp.out[wave];
+            mp.out[0][(size_t)m * N + row] = __float2half(act * u * scale);
+        } else {
 #pragma unroll
-        for (int r = 0; r < 4; r++) {
-            const int m = m0 + mrow + r;
-            if (m >= B) break;
-            float v = sum[r];
-            if (rms_inv) v *= rms_inv[m];
-            out[(size_t)m * N + row] = __float2half(v);
+            for (int mt = 0; mt < NMAT; mt++)
+                mp.out[mt][(size_t)m * N + row] = __float2half(acc[mt][r] * scale);
         }
     }
 }
@@ -336,14 +363,16 @@ bool misaligned16(const void *p) { return (reinterpret_cast<uintptr_t>(p) & 15) 
 
 size_t act_bytes(uint32_t B, uint32_t K) { return (size_t)B * K * 4 + (size_t)B * 4 + 256; }
 
-int pick_parts(int tiles, int nmat, int G) {
-    // Enough groups per wave to keep the whole slice in registers (<= kMaxGroups),
-    // and enough waves overall (~2k) to cover the 1024 SIMDs of an MI355X twice.
-    int need = (G + kMaxGroups - 1) / kMaxGroups;
-    int want = (2048 + tiles * nmat - 1) / (tiles * nmat);
-    int parts = std::max(need, std::min(want, G));
-    int cap = kMaxWaves / nmat;
-    return std::min(parts, cap);
+// Split of K across items: the activation slice of one item stays within
+// ~12 KB of LDS and in kMaxGroups groups of registers, and there are enough
+// items (>= ~1100) to spread over the 256 CUs in even rounds.
+int pick_kc(int tiles, int G, int B, bool lo) {
+    const int rows = std::min(B, 16);
+    const int bytes_per_group = rows * kGS * 2 * (lo ? 2 : 1);
+    int kc = std::max(1, std::min(kMaxGroups, (12 * 1024) / bytes_per_group));
+    const int want_splits = (1100 + tiles - 1) / tiles;
+    if (want_splits > 1) kc = std::min(kc, std::max(2, (G + want_splits - 1) / want_splits));
+    return std::max(1, std::min(kc, G));
 }
 
 int prep_plain(imh_stream *s, const uint16_t *x, uint32_t B, uint32_t K, const uint16_t *awq,
@@ -368,13 +397,28 @@ int prep_plain(imh_stream *s, const uint16_t *x, uint32_t B, uint32_t K, const u
 template <int NMAT, int EPI, bool HAS_LO>
 int launch_main(imh_stream *s, const MatPtrs &mp, const imh_int4_activation *act, int N) {
     const int K = (int)act->k, B = (int)act->token_count;
+    const int G = K / kGS;
     const int tiles = (N + 15) / 16;
-    const int parts = pick_parts(tiles, NMAT, K / kGS);
-    dim3 grid(tiles, (B + 15) / 16);
-    dim3 block(64 * NMAT * parts);
-    hipLaunchKernelGGL((int4_matvec_kernel<NMAT, EPI, HAS_LO>), grid, block, 0, s->stream, mp,
+    const int kc = pick_kc(tiles, G, B, HAS_LO);
+    const int S = (G + kc - 1) / kc;
+    const int chunks = (B + 15) / 16;
+    float *partial = nullptr;
+    unsigned *counters = nullptr;
+    if (S > 1) {
+        void *p = nullptr;
+        int rc = imh::stream_scratch(s, 1, (size_t)S * B * NMAT * N * sizeof(float), &p);
+        if (rc) return rc;
+        partial = static_cast<float *>(p);
+        rc = imh::stream_scratch(s, 2, (size_t)tiles * chunks * sizeof(unsigned), &p);
+        if (rc) return rc;
+        counters = static_cast<unsigned *>(p);
+    }
+    const size_t lds = (size_t)(HAS_LO ? 2 : 1) * std::min(B, 16) * (kc * kGS + 8) * sizeof(_Float16);
+    dim3 grid(tiles * S, chunks);
+    hipLaunchKernelGGL((int4_matvec_kernel<NMAT, EPI, HAS_LO>), grid, dim3(64), lds, s->stream, mp,
                        reinterpret_cast<const _Float16 *>(act->hi),
-                       reinterpret_cast<const _Float16 *>(act->lo), act->row_scale, N, K, B, parts);
+                       reinterpret_cast<const _Float16 *>(act->lo), act->row_scale, N, K, B, S, kc,
+                       partial, counters);
     IMH_HIP(hipGetLastError());
     return IMH_OK;
 }
@@ -434,7 +478,7 @@ int plain_op(imh_stream *s, const uint16_t *x, uint32_t B, const imh_affine_int4
     rc = imh::use_device(s->dev);
     if (rc) return rc;
     void *scr = nullptr;
-    rc = imh::stream_scratch(s, act_bytes(B, w0->k), &scr);
+    rc = imh::stream_scratch(s, 0, act_bytes(B, w0->k), &scr);
     if (rc) return rc;
     imh_int4_activation act;
     rc = prep_plain(s, x, B, w0->k, w0->awq_scales, scr, &act);
@@ -512,7 +556,7 @@ int imh_encode_fused_residual_norm_affine_matvec_int4(imh_stream *stream,
     if (rc) return rc;
     const uint32_t B = p->token_count, K = p->weight->k;
     void *scr = nullptr;
-    rc = imh::stream_scratch(stream, act_bytes(B, K), &scr);
+    rc = imh::stream_scratch(stream, 0, act_bytes(B, K), &scr);
     if (rc) return rc;
     _Float16 *hi = static_cast<_Float16 *>(scr);
     _Float16 *lo = hi + (size_t)B * K;

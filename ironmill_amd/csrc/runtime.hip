@@ -32,21 +32,26 @@ int use_device(const imh_device *dev) {
     return IMH_OK;
 }
 
-int stream_scratch(imh_stream *s, size_t bytes, void **out) {
-    if (s->scratch_bytes < bytes) {
+int stream_scratch(imh_stream *s, int slot, size_t bytes, void **out) {
+    if (slot < 0 || slot >= kScratchSlots) return fail(IMH_EINVAL, "stream_scratch: bad slot");
+    if (s->scratch_bytes[slot] < bytes) {
         int rc = use_device(s->dev);
         if (rc) return rc;
-        if (s->scratch) {
+        if (s->scratch[slot]) {
             IMH_HIP(hipStreamSynchronize(s->stream));
-            IMH_HIP(hipFree(s->scratch));
-            s->scratch = nullptr;
-            s->scratch_bytes = 0;
+            IMH_HIP(hipFree(s->scratch[slot]));
+            s->scratch[slot] = nullptr;
+            s->scratch_bytes[slot] = 0;
         }
         size_t want = bytes < (1u << 20) ? (1u << 20) : bytes;
-        IMH_HIP(hipMalloc(&s->scratch, want));
-        s->scratch_bytes = want;
+        IMH_HIP(hipMalloc(&s->scratch[slot], want));
+        s->scratch_bytes[slot] = want;
+        if (slot == 2) {
+            IMH_HIP(hipMemset(s->scratch[slot], 0, want));
+            IMH_HIP(hipDeviceSynchronize());
+        }
     }
-    *out = s->scratch;
+    *out = s->scratch[slot];
     return IMH_OK;
 }
 
@@ -199,7 +204,7 @@ int imh_stream_create(imh_device *dev, imh_stream **out) {
     if (rc) return rc;
     hipStream_t s;
     IMH_HIP(hipStreamCreateWithFlags(&s, hipStreamNonBlocking));
-    imh_stream *st = new (std::nothrow) imh_stream{dev, s, nullptr, 0};
+    imh_stream *st = new (std::nothrow) imh_stream{dev, s, {nullptr, nullptr, nullptr}, {0, 0, 0}};
     if (!st) {
         (void)hipStreamDestroy(s);
         return imh::fail(IMH_ENOMEM, "imh_stream_create: host allocation failed");
@@ -212,7 +217,8 @@ void imh_stream_free(imh_stream *stream) {
     if (!stream) return;
     imh::use_device(stream->dev);
     (void)hipStreamSynchronize(stream->stream);
-    if (stream->scratch) (void)hipFree(stream->scratch);
+    for (int i = 0; i < kScratchSlots; i++)
+        if (stream->scratch[i]) (void)hipFree(stream->scratch[i]);
     (void)hipStreamDestroy(stream->stream);
     delete stream;
 }

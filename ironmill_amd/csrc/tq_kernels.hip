@@ -38,6 +38,21 @@ constexpr int kChunk = 16;       // positions per MFMA block
 constexpr int kWaves = 4;        // waves per attention workgroup
 constexpr int kSplitQuantum = kChunk * kWaves;
 
+// IEEE round-to-nearest f32 square root: the hardware v_sqrt_f32 result
+// (within 1 ulp) corrected with two fma residuals.  Inputs here are finite
+// and >= 1e-20, so no denormal rescaling is needed.
+__device__ __forceinline__ float sqrt_rn(float x) {
+    float s = __builtin_amdgcn_sqrtf(x);
+    const int si = __builtin_bit_cast(int, s);
+    const float dn = __builtin_bit_cast(float, si - 1);
+    const float up = __builtin_bit_cast(float, si + 1);
+    const float r_dn = __builtin_fmaf(-dn, s, x);
+    const float r_up = __builtin_fmaf(-up, s, x);
+    s = (r_dn <= 0.0f) ? dn : s;
+    s = (r_up > 0.0f) ? up : s;
+    return s;
+}
+
 // ---------------------------------------------------------------------------
 // cache write: grid (num_kv_heads, token_count, batch), block kD
 // ---------------------------------------------------------------------------
@@ -85,7 +100,7 @@ __global__ void __launch_bounds__(kD) tq_cache_write_kernel(
         if (i < s) red[i] = red[i] + red[i + s];
         __syncthreads();
     }
-    const float l2 = __fsqrt_rn(fmaxf(red[0], 1e-20f));
+    const float l2 = sqrt_rn(fmaxf(red[0], 1e-20f));
     const float inv = __fdiv_rn(1.0f, fmaxf(l2, 1e-10f));
     const float u = xr * inv;
     int idx = 0;
@@ -102,7 +117,7 @@ __global__ void __launch_bounds__(kD) tq_cache_write_kernel(
             if (i < s) red[i] = red[i] + red[i + s];
             __syncthreads();
         }
-        const float rn = __fsqrt_rn(fmaxf(red[0], 1e-20f));
+        const float rn = sqrt_rn(fmaxf(red[0], 1e-20f));
         float acc = 0.0f;
         for (int k = 0; k < kD; k++) acc = __builtin_fmaf(qjl_t[(size_t)k * kD + i], res[k], acc);
         if (acc >= 0.0f) code |= 0x80u;
@@ -482,7 +497,7 @@ int imh_encode_turboquant_attention(imh_stream *stream, const imh_tq_tables *t,
     const size_t nparts = (size_t)B * num_heads * S;
     const size_t need = nparts * kD * 4 + nparts * 8 + 512;
     void *scr = nullptr;
-    rc = imh::stream_scratch(stream, need, &scr);
+    rc = imh::stream_scratch(stream, 1, need, &scr);
     if (rc) return rc;
     float *po = static_cast<float *>(scr);
     float *pm = po + nparts * kD;
