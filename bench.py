@@ -18,7 +18,8 @@ scales + f16 zeros + AWQ + x + y.
 
 The JSON line also carries
   roofline     -- the dominant kernel (fused gate+up matvec, prepared
-                  activation) timed per launch with HIP events on its stream;
+                  activation): K launches recorded into a HIP graph, replayed
+                  between two HIP events on its stream, time / K;
   cpu_baseline -- the C oracle's dequantize-then-compute FFN step on the host
                   cores (weights dequantized once outside the timing);
   details      -- batch 4/8 FFN kernels and TurboQuant attention at 32k.
@@ -80,27 +81,27 @@ def make_x(b, k, seed):
     return x.astype(np.float16)
 
 
-def time_loop(dev, stream, fn, steps, warmup, per_launch=False):
-    """Run fn(i) warmup + steps times; return (total_ms, [per-launch ms])."""
-    for i in range(warmup):
-        fn(i)
+def time_loop(dev, stream, fn, steps, warmup):
+    """GPU time of `steps` calls fn(0..steps-1), back to back.
+
+    The calls are recorded into a HIP graph (imh_stream_begin/end_capture) and
+    replayed, so the device runs them without host launch gaps; a warmup graph
+    of `warmup` calls runs first.  HIP events on the same stream bracket the
+    timed replay.  Returns total ms.
+    """
+    fn(0)  # any scratch memory an op needs exists before capture
     stream.sync()
-    if per_launch:
-        evs = [(dev.event(), dev.event()) for _ in range(steps)]
-        for i, (a, b) in enumerate(evs):
-            a.record(stream)
-            fn(i)
-            b.record(stream)
-        stream.sync()
-        times = [a.elapsed_ms(b) for a, b in evs]
-        return sum(times), times
+    if warmup > 0:
+        wg = stream.capture(lambda: [fn(i) for i in range(warmup)])
+        wg.launch()
+    g = stream.capture(lambda: [fn(i) for i in range(steps)])
+    stream.sync()
     s, e = dev.event(), dev.event()
     s.record(stream)
-    for i in range(steps):
-        fn(i)
+    g.launch()
     e.record(stream)
     stream.sync()
-    return s.elapsed_ms(e), None
+    return s.elapsed_ms(e)
 
 
 def cpu_baseline(qg, qu, qd, seconds):
@@ -152,7 +153,7 @@ def bench_attention(dev, stream, ops, batch, ctx, steps, warmup, layers):
     def step(i):
         ops.encode_turboquant_attention(stream, tq, caches[i % layers], q, nh, ctx, out, scale)
 
-    total, per = time_loop(dev, stream, step, steps, warmup, per_launch=True)
+    total = time_loop(dev, stream, step, steps, warmup)
     ms = total / steps
     gbs = tq_bytes(batch, ctx) / (ms * 1e-3) / 1e9
     return {"batch": batch, "ctx": ctx, "us": round(ms * 1e3, 2), "GB/s": round(gbs, 1),
@@ -168,6 +169,9 @@ def main():
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-details", action="store_true")
+    ap.add_argument("--replicas", type=int, default=0,
+                    help="weight copies rotated through (default: enough for >= 512 MB, beyond the "
+                         "256 MB Infinity Cache; 1 measures a cache-resident matrix)")
     ap.add_argument("--kernel-only", action="store_true",
                     help="only the prepared fused gate+up kernel loop (for rocprofv3 counter runs)")
     args = ap.parse_args()
@@ -186,7 +190,7 @@ def main():
     B = args.batch
     qg, qu, qd = make_weights(1234)
     per_copy = (qg.data.nbytes + qg.scales.nbytes * 2) * 3
-    reps = max(1, math.ceil(512e6 / per_copy))
+    reps = args.replicas or max(1, math.ceil(512e6 / per_copy))
     log(f"uploading {reps} weight replicas ({reps * per_copy / 1e6:.0f} MB)")
     W = [(ops.AffineQuantizedWeight(dev, qg), ops.AffineQuantizedWeight(dev, qu),
           ops.AffineQuantizedWeight(dev, qd)) for _ in range(reps)]
@@ -203,7 +207,7 @@ def main():
         ops.encode_int4_matvec_prepared(stream, prep, g, act, u, None, epilogue="silu")
 
     ksteps = args.steps if not args.kernel_only else max(args.steps, 500)
-    tot, per = time_loop(dev, stream, gate_up_kernel, ksteps, args.warmup, per_launch=True)
+    tot = time_loop(dev, stream, gate_up_kernel, ksteps, args.warmup)
     k_us = 1e3 * tot / ksteps
     k_bytes = gate_up_bytes(B)
     k_gbs = k_bytes / (k_us * 1e-6) / 1e9
@@ -219,7 +223,7 @@ def main():
         ops.encode_fused_ffn_gate_up_act_int4(stream, x, g, u, act, B)
         ops.encode_projection(stream, act, d, y, B)
 
-    total_ms, _ = time_loop(dev, stream, ffn_step, args.steps, args.warmup)
+    total_ms = time_loop(dev, stream, ffn_step, args.steps, args.warmup)
     ms = total_ms / args.steps
     step_bytes = gate_up_bytes(B) + down_bytes(B)
     value = step_bytes / (ms * 1e-3) / 1e9
@@ -240,7 +244,7 @@ def main():
         def down_kernel(i):
             ops.encode_int4_matvec_prepared(stream, prep_d, W[i % reps][2], y)
 
-        t, _ = time_loop(dev, stream, down_kernel, args.steps, args.warmup, per_launch=True)
+        t = time_loop(dev, stream, down_kernel, args.steps, args.warmup)
         d_us = 1e3 * t / args.steps
         details["down_kernel_b%d" % B] = {"us": round(d_us, 2),
                                           "GB/s": round(down_bytes(B) / (d_us * 1e-6) / 1e9, 1)}
@@ -254,7 +258,7 @@ def main():
                 g, u, _ = W[i % reps]
                 ops.encode_int4_matvec_prepared(stream, pb, g, ab, u, None, epilogue="silu")
 
-            t, _ = time_loop(dev, stream, gu, args.steps, args.warmup, per_launch=True)
+            t = time_loop(dev, stream, gu, args.steps, args.warmup)
             us = 1e3 * t / args.steps
             details[f"gate_up_kernel_b{bb}"] = {"us": round(us, 2),
                                                 "GB/s": round(gate_up_bytes(bb) / (us * 1e-6) / 1e9, 1)}
@@ -265,7 +269,7 @@ def main():
             def dn(i, pdn=pdn, yb=yb):
                 ops.encode_int4_matvec_prepared(stream, pdn, W[i % reps][2], yb)
 
-            t, _ = time_loop(dev, stream, dn, args.steps, args.warmup, per_launch=True)
+            t = time_loop(dev, stream, dn, args.steps, args.warmup)
             us = 1e3 * t / args.steps
             details[f"down_kernel_b{bb}"] = {"us": round(us, 2),
                                              "GB/s": round(down_bytes(bb) / (us * 1e-6) / 1e9, 1)}

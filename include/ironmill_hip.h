@@ -95,6 +95,18 @@ void *imh_stream_native(imh_stream *stream); /* the hipStream_t */
 /* Zero `length` bytes at a device pointer with a fill kernel (capturable). */
 int imh_fill_zero(imh_stream *stream, void *dst, size_t length);
 
+/* Recorded command sequence: ops encoded on a stream between begin and end
+ * capture are recorded (not run) into a HIP graph, which can then be replayed
+ * with one launch -- the counterpart of encoding a whole decode step into one
+ * Metal command buffer and committing it (pipeline.rs:336-343,1205-1213).
+ * Scratch memory an op needs must already exist (run it once before capture);
+ * capture fails with IMH_EINVAL otherwise. */
+typedef struct imh_graph imh_graph;
+int imh_stream_begin_capture(imh_stream *stream);
+int imh_stream_end_capture(imh_stream *stream, imh_graph **out);
+int imh_graph_launch(imh_graph *graph, imh_stream *stream);
+void imh_graph_free(imh_graph *graph);
+
 /* gpu_start_time / gpu_end_time (command.rs:470-489) as stream events. */
 int imh_event_create(imh_device *dev, imh_event **out);
 void imh_event_free(imh_event *ev);

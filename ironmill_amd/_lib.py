@@ -9,7 +9,8 @@ import ctypes as C
 import os
 
 _HERE = os.path.dirname(os.path.abspath(__file__))
-LIB_PATH = os.path.join(_HERE, "lib", "libironmill_hip.so")
+# IRONMILL_HIP_LIB selects another build of the same library (e.g. a debug build)
+LIB_PATH = os.environ.get("IRONMILL_HIP_LIB") or os.path.join(_HERE, "lib", "libironmill_hip.so")
 
 IMH_OK = 0
 IMH_EINVAL = -1
@@ -134,6 +135,10 @@ SIGNATURES = {
     "imh_stream_sync": (I, [P]),
     "imh_stream_native": (P, [P]),
     "imh_fill_zero": (I, [P, P, SZ]),
+    "imh_stream_begin_capture": (I, [P]),
+    "imh_stream_end_capture": (I, [P, C.POINTER(P)]),
+    "imh_graph_launch": (I, [P, P]),
+    "imh_graph_free": (None, [P]),
     "imh_event_create": (I, [P, C.POINTER(P)]),
     "imh_event_free": (None, [P]),
     "imh_event_record": (I, [P, P]),

@@ -45,6 +45,13 @@ struct imh_stream {
     hipStream_t stream;
     void *scratch[kScratchSlots];
     size_t scratch_bytes[kScratchSlots];
+    bool capturing;
+};
+
+struct imh_graph {
+    imh_device *dev;
+    hipGraph_t graph;
+    hipGraphExec_t exec;
 };
 
 struct imh_event {

@@ -9,22 +9,25 @@
 //
 // MI355X design:
 //  * the contraction runs on the matrix cores: v_mfma_f32_16x16x32_f16 with
-//    the activation as operand A (16 batch rows, unused rows zero) and the
-//    weights as operand B (16 weight rows).  (q - z) is formed exactly in f16
-//    from the nibbles with the 0x6400 exponent trick and one packed f16 add, so
-//    every product is exact and the accumulation is f32.
+//    the activation as operand A (16 batch rows; rows past the batch read
+//    row 0 and their results are dropped) and the weights as operand B (16
+//    weight rows).  (q - z) is formed exactly in f16: nibbles are split into
+//    bytes, v_perm_b32 places each beside a 0x64 exponent byte (1024 + q), and
+//    one packed f16 add of -(1024 + z) gives (q - z) -- every product is exact,
+//    the accumulation is f32.
 //  * an activation that is not exactly f16 (x/awq, normed values) is split
 //    into hi + lo f16 halves and fed through two MFMAs: ~22-bit operands.
-//  * one 16-byte load per lane covers a whole 128-element group of one row
-//    (the 4 lane groups of a wave read the 64 bytes of the group), and every
-//    group a wave owns is loaded before the first MFMA, so each wave keeps its
-//    whole K slice of weights in flight.
-//  * a workgroup owns one 16-row tile; its waves split K (and gate/up) and
-//    reduce through LDS in a fixed order, so results are deterministic and no
-//    cross-workgroup synchronisation is needed.
-//  * the activation is first rewritten by a small prep kernel into the MFMA
-//    operand order (k-slot i of an 8-chunk holds element {0,4,1,5,2,6,3,7}[i]),
-//    which matches the nibble pairs (q_i, q_{i+4}) the B operand is built from.
+//  * one workgroup owns one 16-row tile (of each matrix of a gate/up pair);
+//    its waves split K, each holding all of its slice's weights in registers
+//    (one 16-byte load per lane per 128-element group, issued up front), and
+//    reduce through LDS in a fixed order: deterministic, no cross-workgroup
+//    synchronisation.
+//  * the activation image is staged into LDS by the whole workgroup, with its
+//    loads issued before the weight loads and an LDS-only barrier, so the
+//    weights stay in flight while the first groups compute.
+//  * a small prep kernel writes the activation in MFMA operand order: slot i
+//    of each 8-element chunk holds element {0,2,4,6,1,3,5,7}[i], the order in
+//    which the nibble unpack produces weights.
 #include <hip/hip_runtime.h>
 #include <hip/hip_fp16.h>
 
@@ -41,7 +44,11 @@ typedef float float4_t __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
 
 constexpr int kGS = 128;       // group size the kernels are built for
-constexpr int kMaxGroups = 10; // groups one item may own (its weights stay in registers)
+constexpr int kMaxGroups = 10;   // groups one wave holds per stage (weights stay in registers)
+constexpr int kMaxWaves = 16;    // waves per workgroup
+constexpr int kXChunks = 2;      // activation chunks per thread loaded ahead of the weights
+constexpr int kSZChunks = 2;     // scale/zero pairs per thread loaded ahead of the weights
+constexpr int kLdsBudget = 64 * 1024;
 
 enum Epi : int { EPI_STORE = IMH_EPI_STORE, EPI_SILU = IMH_EPI_SILU, EPI_GELU = IMH_EPI_GELU };
 
@@ -85,7 +92,7 @@ __global__ void __launch_bounds__(256) int4_prep_plain(const __half *__restrict_
 #pragma unroll
         for (int i = 0; i < 8; i++) v[i] = (float)xh[i];
     }
-    constexpr int perm[8] = {0, 4, 1, 5, 2, 6, 3, 7};
+    constexpr int perm[8] = {0, 2, 4, 6, 1, 3, 5, 7};
     half8_t hi, lo;
 #pragma unroll
     for (int i = 0; i < 8; i++) {
@@ -128,7 +135,7 @@ __global__ void __launch_bounds__(256) int4_prep_resnorm(
     }
     const float rms_inv = 1.0f / __builtin_sqrtf(red[0] / (float)K + eps);
     if (threadIdx.x == 0) rms_out[m] = rms_inv;
-    constexpr int perm[8] = {0, 4, 1, 5, 2, 6, 3, 7};
+    constexpr int perm[8] = {0, 2, 4, 6, 1, 3, 5, 7};
     for (int c = threadIdx.x; c * 8 < K; c += blockDim.x) {
         const size_t off = row + (size_t)c * 8;
         uint4 av = *reinterpret_cast<const uint4 *>(a + off);
@@ -168,160 +175,186 @@ __global__ void __launch_bounds__(256) int4_prep_resnorm(
 // ---------------------------------------------------------------------------
 // main matvec kernel
 // ---------------------------------------------------------------------------
-// grid (tiles * S, ceil(B/16)), block 64: one wave per item.  Item = 16 weight
-// rows of each of the NMAT matrices x the K range of split `s` (kc groups).
-//   1. every weight load of the item is issued (NMAT * kc 16-byte loads/lane);
-//   2. the wave copies its activation slice (<= 16 batch rows x kc*128, hi and
-//      lo planes) into LDS, so all activation misses overlap in one round trip;
-//   3. per group: operand B from the nibbles, operand A from LDS, MFMAs, and
-//      the group's f32 partial is scaled by s into the running accumulator;
-//   4. with S > 1 the item stores its partial; the last item of a tile to
-//      arrive (atomic counter) sums the S partials in split order -- the same
-//      order on every run -- applies the epilogue and re-arms the counter.
+// grid (ceil(N/16), ceil(B/16)), block 64 * NMAT * parts.  Wave w works on
+// matrix w / parts and, in every K stage, on part w % parts of the stage's
+// groups.  A stage is the range of groups whose activation image fits the
+// LDS budget (normally all of K: one stage).
 template <int NMAT, int EPI, bool HAS_LO>
-__global__ void __launch_bounds__(64) int4_matvec_kernel(
+__global__ void __launch_bounds__(1024) int4_matvec_kernel(
     MatPtrs mp, const _Float16 *__restrict__ xa_hi, const _Float16 *__restrict__ xa_lo,
-    const float *__restrict__ rms_inv, int N, int K, int B, int S, int kc,
-    float *__restrict__ partial, unsigned *__restrict__ counters) {
-    extern __shared__ __attribute__((aligned(16))) _Float16 xs[];
+    const float *__restrict__ rms_inv, int N, int K, int B, int parts, int SG) {
+    // dynamic LDS: [NMAT][16][G + 1] u32 (scale | zero << 16), then the activation planes
+    extern __shared__ __attribute__((aligned(16))) uint32_t lds_dyn[];
+    __shared__ float4_t red[kMaxWaves][64];
 
-    const int lane = threadIdx.x;
+    const int tid = threadIdx.x;
+    const int nthr = blockDim.x;
+    const int lane = tid & 63;
+    const int wave = tid >> 6;
+    const int mat = wave / parts;
+    const int part = wave - mat * parts;
     const int G = K / kGS;
-    const int item = blockIdx.x;
-    const int tile = item / S;
-    const int split = item - tile * S;
-    const int g0 = split * kc;
-    const int ng = min(g0 + kc, G) - g0;
     const int m0 = blockIdx.y * 16;
     const int bc = min(16, B - m0);
-    const int RS = kc * kGS + 8;          // LDS row stride in halfs (16-byte pad)
+    const int RSX = SG * kGS + 8;        // LDS row stride in halfs (16-byte pad)
 
-    const int n_l = lane & 15;            // weight row within the tile (B operand column)
-    const int kq = lane >> 4;             // 16-byte quarter of a group this lane reads
-    const int row = tile * 16 + n_l;
+    const int n_l = lane & 15;           // weight row within the tile (B operand column)
+    const int kq = lane >> 4;            // 16-byte quarter of a group this lane reads
+    const int row = blockIdx.x * 16 + n_l;
     const int row_c = row < N ? row : N - 1;
+    const int arow = n_l < bc ? n_l : 0; // rows past the batch reuse row 0; dropped below
 
-    // 1. weights, scales, zeros of the whole item
-    u32x4_t wq[NMAT][kMaxGroups];
-    _Float16 sc[NMAT][kMaxGroups], zr[NMAT][kMaxGroups];
+    const uint8_t *wrow = mp.data[mat] + (size_t)row_c * (K / 2) + kq * 16;
+    const uint32_t c64 = 0x64646464u;
+
+    // scales and zeros of the tile: 16 consecutive rows, one contiguous block
+    // per array, staged once into LDS by the whole workgroup
+    const int SZR = G + 1;                                   // LDS row stride (u32)
+    uint32_t *szs = lds_dyn;
+    _Float16 *xs = reinterpret_cast<_Float16 *>(lds_dyn + ((NMAT * 16 * SZR + 3) & ~3));
+    const int row0 = blockIdx.x * 16;
+    const int sz_total = NMAT * 16 * G;
+    uint32_t szv[kSZChunks];
 #pragma unroll
-    for (int mt = 0; mt < NMAT; mt++) {
-        const uint8_t *wrow = mp.data[mt] + (size_t)row_c * (K / 2) + kq * 16;
-        const _Float16 *srow = reinterpret_cast<const _Float16 *>(mp.scales[mt]) + (size_t)row_c * G;
-        const _Float16 *zrow = reinterpret_cast<const _Float16 *>(mp.zeros[mt]) + (size_t)row_c * G;
+    for (int i = 0; i < kSZChunks; i++) {
+        const int e = min(i * nthr + tid, sz_total - 1);
+        const int mt = e / (16 * G);
+        const int rg = e - mt * 16 * G;
+        const int rr = rg / G;
+        const size_t src = (size_t)min(row0 + rr, N - 1) * G + (rg - rr * G);
+        szv[i] = (uint32_t)reinterpret_cast<const uint16_t *>(mp.scales[mt])[src] |
+                 ((uint32_t)reinterpret_cast<const uint16_t *>(mp.zeros[mt])[src] << 16);
+    }
+
+    float4_t acc = {0.0f, 0.0f, 0.0f, 0.0f};
+    for (int gs0 = 0; gs0 < G; gs0 += SG) {
+        const int SGs = min(SG, G - gs0);
+        // (a) activation loads of this stage first
+        const int cpr = SGs * 16;                  // 8-half chunks per batch row
+        const int total = bc * cpr;
+        u32x4_t xv[kXChunks], lv[kXChunks];
+#pragma unroll
+        for (int i = 0; i < kXChunks; i++) {
+            const int c = min(i * nthr + tid, total - 1);
+            const int r = c / cpr;
+            const size_t src = (size_t)(m0 + r) * K + (size_t)gs0 * kGS + (size_t)(c - r * cpr) * 8;
+            xv[i] = *reinterpret_cast<const u32x4_t *>(xa_hi + src);
+            if (HAS_LO) lv[i] = *reinterpret_cast<const u32x4_t *>(xa_lo + src);
+        }
+        // (b) this wave's weights for the stage: unconditional, clamped loads
+        const int wg0 = gs0 + (part * SGs) / parts;
+        const int ng = gs0 + ((part + 1) * SGs) / parts - wg0;
+        u32x4_t wq[kMaxGroups];
+#pragma unroll
+        for (int i = 0; i < kMaxGroups; i++) {
+            const int g = min(max(wg0 + min(i, ng - 1), 0), G - 1);
+            wq[i] = *reinterpret_cast<const u32x4_t *>(wrow + (size_t)g * 64);
+        }
+        if (gs0 == 0) {  // scales/zeros -> LDS (read after the barrier below)
+#pragma unroll
+            for (int i = 0; i < kSZChunks; i++) {
+                const int e = i * nthr + tid;
+                if (e < sz_total) {
+                    const int mt = e / (16 * G);
+                    const int rg = e - mt * 16 * G;
+                    const int rr = rg / G;
+                    szs[(mt * 16 + rr) * SZR + (rg - rr * G)] = szv[i];
+                }
+            }
+            for (int e = kSZChunks * nthr + tid; e < sz_total; e += nthr) {
+                const int mt = e / (16 * G);
+                const int rg = e - mt * 16 * G;
+                const int rr = rg / G;
+                const size_t src = (size_t)min(row0 + rr, N - 1) * G + (rg - rr * G);
+                szs[(mt * 16 + rr) * SZR + (rg - rr * G)] =
+                    (uint32_t)reinterpret_cast<const uint16_t *>(mp.scales[mt])[src] |
+                    ((uint32_t)reinterpret_cast<const uint16_t *>(mp.zeros[mt])[src] << 16);
+            }
+        }
+        // (c) activation -> LDS (after the previous stage is done with it)
+        if (gs0 > 0) {
+            __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
+            __builtin_amdgcn_s_barrier();
+            __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+        }
+#pragma unroll
+        for (int i = 0; i < kXChunks; i++) {
+            const int c = i * nthr + tid;
+            if (c < total) {
+                const int r = c / cpr;
+                const int off = r * RSX + (c - r * cpr) * 8;
+                *reinterpret_cast<u32x4_t *>(xs + off) = xv[i];
+                if (HAS_LO) *reinterpret_cast<u32x4_t *>(xs + bc * RSX + off) = lv[i];
+            }
+        }
+        for (int c = kXChunks * nthr + tid; c < total; c += nthr) {  // activation beyond one pass
+            const int r = c / cpr;
+            const size_t src = (size_t)(m0 + r) * K + (size_t)gs0 * kGS + (size_t)(c - r * cpr) * 8;
+            const int off = r * RSX + (c - r * cpr) * 8;
+            *reinterpret_cast<u32x4_t *>(xs + off) = *reinterpret_cast<const u32x4_t *>(xa_hi + src);
+            if (HAS_LO)
+                *reinterpret_cast<u32x4_t *>(xs + bc * RSX + off) = *reinterpret_cast<const u32x4_t *>(xa_lo + src);
+        }
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
+        __builtin_amdgcn_s_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+
+        // (d) MFMA over the wave's groups
+        const _Float16 *xh = xs + arow * RSX + (wg0 - gs0) * kGS + kq * 32;
+        const _Float16 *xl = xh + bc * RSX;
 #pragma unroll
         for (int i = 0; i < kMaxGroups; i++) {
             if (i < ng) {
-                const int g = g0 + i;
-                wq[mt][i] = *reinterpret_cast<const u32x4_t *>(wrow + (size_t)g * 64);
-                sc[mt][i] = srow[g];
-                zr[mt][i] = zrow[g];
-            }
-        }
-    }
-
-    // 2. activation slice -> LDS (hi plane, then lo plane)
-    {
-        const int per_row = ng * 16;      // 8-half chunks per batch row
-        const int chunks = bc * per_row;
-        for (int c = lane; c < chunks; c += 64) {
-            const int r = c / per_row;
-            const int cc = c - r * per_row;
-            const size_t src = (size_t)(m0 + r) * K + (size_t)g0 * kGS + (size_t)cc * 8;
-            *reinterpret_cast<u32x4_t *>(xs + r * RS + cc * 8) =
-                *reinterpret_cast<const u32x4_t *>(xa_hi + src);
-            if (HAS_LO)
-                *reinterpret_cast<u32x4_t *>(xs + (bc + r) * RS + cc * 8) =
-                    *reinterpret_cast<const u32x4_t *>(xa_lo + src);
-        }
-    }
-    __syncthreads();
-
-    // 3. MFMA over the item's groups
-    const bool a_on = n_l < bc;
-    const _Float16 *xh = xs + n_l * RS + kq * 32;
-    const _Float16 *xl = xs + (bc + n_l) * RS + kq * 32;
-    float4_t acc[NMAT];
-#pragma unroll
-    for (int mt = 0; mt < NMAT; mt++) acc[mt] = (float4_t){0.0f, 0.0f, 0.0f, 0.0f};
-    const half8_t zero8 = {0, 0, 0, 0, 0, 0, 0, 0};
-#pragma unroll
-    for (int i = 0; i < kMaxGroups; i++) {
-        if (i < ng) {
-            half8_t ah[4], al[4];
-#pragma unroll
-            for (int j = 0; j < 4; j++) {
-                ah[j] = a_on ? *reinterpret_cast<const half8_t *>(xh + i * kGS + j * 8) : zero8;
-                if (HAS_LO) al[j] = a_on ? *reinterpret_cast<const half8_t *>(xl + i * kGS + j * 8) : zero8;
-            }
-#pragma unroll
-            for (int mt = 0; mt < NMAT; mt++) {
-                const _Float16 nb = (_Float16)(-(1024.0f + (float)zr[mt][i]));
+                const uint32_t sz = szs[(mat * 16 + n_l) * SZR + wg0 + i];
+                const float zf = (float)__builtin_bit_cast(_Float16, (uint16_t)(sz >> 16));
+                const _Float16 nb = (_Float16)(-(1024.0f + zf));
                 const half2_t bias = {nb, nb};
                 float4_t accg = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
                 for (int j = 0; j < 4; j++) {
-                    const uint32_t w = wq[mt][i][j];
-                    half8_t bq;
-#pragma unroll
-                    for (int p = 0; p < 4; p++) {
-                        const uint32_t bits = ((w >> (4 * p)) & 0x000F000Fu) | 0x64006400u;
-                        const half2_t d = as_h2(bits) + bias;   // (q_p - z, q_{p+4} - z), exact
-                        bq[2 * p] = d[0];
-                        bq[2 * p + 1] = d[1];
+                    const half8_t ah = *reinterpret_cast<const half8_t *>(xh + i * kGS + j * 8);
+                    const uint32_t w = wq[i][j];
+                    const uint32_t lo = w & 0x0F0F0F0Fu;          // q0 q2 q4 q6
+                    const uint32_t hi = (w >> 4) & 0x0F0F0F0Fu;   // q1 q3 q5 q7
+                    const half2_t p0 = as_h2(__builtin_amdgcn_perm(lo, c64, 0x00050004u)) + bias;
+                    const half2_t p1 = as_h2(__builtin_amdgcn_perm(lo, c64, 0x00070006u)) + bias;
+                    const half2_t p2 = as_h2(__builtin_amdgcn_perm(hi, c64, 0x00050004u)) + bias;
+                    const half2_t p3 = as_h2(__builtin_amdgcn_perm(hi, c64, 0x00070006u)) + bias;
+                    const half8_t bq = __builtin_bit_cast(
+                        half8_t, (u32x4_t){as_u32(p0), as_u32(p1), as_u32(p2), as_u32(p3)});
+                    accg = __builtin_amdgcn_mfma_f32_16x16x32_f16(ah, bq, accg, 0, 0, 0);
+                    if (HAS_LO) {
+                        const half8_t al = *reinterpret_cast<const half8_t *>(xl + i * kGS + j * 8);
+                        accg = __builtin_amdgcn_mfma_f32_16x16x32_f16(al, bq, accg, 0, 0, 0);
                     }
-                    accg = __builtin_amdgcn_mfma_f32_16x16x32_f16(ah[j], bq, accg, 0, 0, 0);
-                    if (HAS_LO) accg = __builtin_amdgcn_mfma_f32_16x16x32_f16(al[j], bq, accg, 0, 0, 0);
                 }
-                const float s = (float)sc[mt][i];
+                const float s = (float)__builtin_bit_cast(_Float16, (uint16_t)(sz & 0xFFFFu));
 #pragma unroll
-                for (int r = 0; r < 4; r++) acc[mt][r] = __builtin_fmaf(accg[r], s, acc[mt][r]);
+                for (int r = 0; r < 4; r++) acc[r] = __builtin_fmaf(accg[r], s, acc[r]);
             }
         }
     }
 
-    // 4. split reduction.  Lane l holds D[m = 4*(l>>4) + r][n = l & 15].
-    const int mrow = m0 + 4 * (lane >> 4);
-    const size_t NT = (size_t)NMAT * N;
-    if (S > 1) {
+    // reduce the parts of each matrix in part order.  Lane l holds
+    // D[m = 4*(l>>4) + r][n = l & 15].
+    red[wave][lane] = acc;
+    __syncthreads();
+    if (wave != 0) return;
+    float4_t sum[NMAT];
 #pragma unroll
-        for (int mt = 0; mt < NMAT; mt++)
-#pragma unroll
-            for (int r = 0; r < 4; r++) {
-                const int m = mrow + r;
-                if (m < B && row < N) partial[((size_t)split * B + m) * NT + (size_t)mt * N + row] = acc[mt][r];
-            }
-        __threadfence();
-        unsigned prev = 0;
-        unsigned *ctr = counters + (size_t)tile * gridDim.y + blockIdx.y;
-        if (lane == 0) prev = atomicAdd(ctr, 1u);
-        prev = __shfl(prev, 0);
-        if (prev != (unsigned)(S - 1)) return;
-        __threadfence();
-#pragma unroll
-        for (int mt = 0; mt < NMAT; mt++)
-#pragma unroll
-            for (int r = 0; r < 4; r++) {
-                const int m = mrow + r;
-                float v = 0.0f;
-                if (m < B && row < N) {
-                    const float *src = partial + (size_t)m * NT + (size_t)mt * N + row;
-                    for (int sp = 0; sp < S; sp++) v += __builtin_nontemporal_load(src + (size_t)sp * B * NT);
-                }
-                acc[mt][r] = v;
-            }
-        if (lane == 0) *ctr = 0u;
+    for (int mt = 0; mt < NMAT; mt++) {
+        sum[mt] = red[mt * parts][lane];
+        for (int p = 1; p < parts; p++) sum[mt] += red[mt * parts + p][lane];
     }
-
-    // 5. epilogue
     if (row >= N) return;
+    const int mrow = m0 + 4 * (lane >> 4);
 #pragma unroll
     for (int r = 0; r < 4; r++) {
         const int m = mrow + r;
         if (m >= B) break;
         const float scale = rms_inv ? rms_inv[m] : 1.0f;
         if (EPI == EPI_SILU || EPI == EPI_GELU) {
-            const float g = acc[0][r], u = acc[NMAT - 1][r];
+            const float g = sum[0][r], u = sum[NMAT - 1][r];
             float act;
             if (EPI == EPI_SILU) {
                 act = g / (1.0f + __expf(-g));
@@ -334,7 +367,7 @@ __global__ void __launch_bounds__(64) int4_matvec_kernel(
         } else {
 #pragma unroll
             for (int mt = 0; mt < NMAT; mt++)
-                mp.out[mt][(size_t)m * N + row] = __float2half(acc[mt][r] * scale);
+                mp.out[mt][(size_t)m * N + row] = __float2half(sum[mt][r] * scale);
         }
     }
 }
@@ -363,16 +396,22 @@ bool misaligned16(const void *p) { return (reinterpret_cast<uintptr_t>(p) & 15) 
 
 size_t act_bytes(uint32_t B, uint32_t K) { return (size_t)B * K * 4 + (size_t)B * 4 + 256; }
 
-// Split of K across items: the activation slice of one item stays within
-// ~12 KB of LDS and in kMaxGroups groups of registers, and there are enough
-// items (>= ~1100) to spread over the 256 CUs in even rounds.
-int pick_kc(int tiles, int G, int B, bool lo) {
+// Waves per tile: each wave holds at most kMaxGroups groups per stage, and
+// the grid carries ~4 waves per SIMD (1024 SIMDs on an MI355X).
+int pick_parts(int tiles, int nmat, int G) {
+    const int need = (G + kMaxGroups - 1) / kMaxGroups;
+    const int want = (4096 + tiles * nmat - 1) / (tiles * nmat);
+    const int cap = std::min(kMaxWaves / nmat, G);
+    return std::max(1, std::min(cap, std::max(need, want)));
+}
+
+// Groups per K stage: as many as the LDS budget holds for the batch rows.
+int pick_stage(int G, int B, bool lo, int parts) {
     const int rows = std::min(B, 16);
-    const int bytes_per_group = rows * kGS * 2 * (lo ? 2 : 1);
-    int kc = std::max(1, std::min(kMaxGroups, (12 * 1024) / bytes_per_group));
-    const int want_splits = (1100 + tiles - 1) / tiles;
-    if (want_splits > 1) kc = std::min(kc, std::max(2, (G + want_splits - 1) / want_splits));
-    return std::max(1, std::min(kc, G));
+    const int per_group = rows * kGS * 2 * (lo ? 2 : 1);
+    int SG = std::max(1, (kLdsBudget - 64) / per_group);
+    SG = std::min(SG, parts * kMaxGroups);
+    return std::min(SG, G);
 }
 
 int prep_plain(imh_stream *s, const uint16_t *x, uint32_t B, uint32_t K, const uint16_t *awq,
@@ -399,26 +438,15 @@ int launch_main(imh_stream *s, const MatPtrs &mp, const imh_int4_activation *act
     const int K = (int)act->k, B = (int)act->token_count;
     const int G = K / kGS;
     const int tiles = (N + 15) / 16;
-    const int kc = pick_kc(tiles, G, B, HAS_LO);
-    const int S = (G + kc - 1) / kc;
-    const int chunks = (B + 15) / 16;
-    float *partial = nullptr;
-    unsigned *counters = nullptr;
-    if (S > 1) {
-        void *p = nullptr;
-        int rc = imh::stream_scratch(s, 1, (size_t)S * B * NMAT * N * sizeof(float), &p);
-        if (rc) return rc;
-        partial = static_cast<float *>(p);
-        rc = imh::stream_scratch(s, 2, (size_t)tiles * chunks * sizeof(unsigned), &p);
-        if (rc) return rc;
-        counters = static_cast<unsigned *>(p);
-    }
-    const size_t lds = (size_t)(HAS_LO ? 2 : 1) * std::min(B, 16) * (kc * kGS + 8) * sizeof(_Float16);
-    dim3 grid(tiles * S, chunks);
-    hipLaunchKernelGGL((int4_matvec_kernel<NMAT, EPI, HAS_LO>), grid, dim3(64), lds, s->stream, mp,
-                       reinterpret_cast<const _Float16 *>(act->hi),
-                       reinterpret_cast<const _Float16 *>(act->lo), act->row_scale, N, K, B, S, kc,
-                       partial, counters);
+    const int parts = pick_parts(tiles, NMAT, G);
+    const int SG = pick_stage(G, B, HAS_LO, parts);
+    const size_t sz_words = ((size_t)NMAT * 16 * (G + 1) + 3) & ~(size_t)3;
+    const size_t lds = sz_words * sizeof(uint32_t) +
+                       (size_t)(HAS_LO ? 2 : 1) * std::min(B, 16) * (SG * kGS + 8) * sizeof(_Float16);
+    dim3 grid(tiles, (B + 15) / 16);
+    hipLaunchKernelGGL((int4_matvec_kernel<NMAT, EPI, HAS_LO>), grid, dim3(64 * NMAT * parts), lds, s->stream,
+                       mp, reinterpret_cast<const _Float16 *>(act->hi),
+                       reinterpret_cast<const _Float16 *>(act->lo), act->row_scale, N, K, B, parts, SG);
     IMH_HIP(hipGetLastError());
     return IMH_OK;
 }

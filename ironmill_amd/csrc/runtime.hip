@@ -35,6 +35,9 @@ int use_device(const imh_device *dev) {
 int stream_scratch(imh_stream *s, int slot, size_t bytes, void **out) {
     if (slot < 0 || slot >= kScratchSlots) return fail(IMH_EINVAL, "stream_scratch: bad slot");
     if (s->scratch_bytes[slot] < bytes) {
+        if (s->capturing)
+            return fail(IMH_EINVAL, "scratch memory must grow during stream capture: run the op once "
+                                    "with the same shapes before capturing it");
         int rc = use_device(s->dev);
         if (rc) return rc;
         if (s->scratch[slot]) {
@@ -204,7 +207,7 @@ int imh_stream_create(imh_device *dev, imh_stream **out) {
     if (rc) return rc;
     hipStream_t s;
     IMH_HIP(hipStreamCreateWithFlags(&s, hipStreamNonBlocking));
-    imh_stream *st = new (std::nothrow) imh_stream{dev, s, {nullptr, nullptr, nullptr}, {0, 0, 0}};
+    imh_stream *st = new (std::nothrow) imh_stream{dev, s, {nullptr, nullptr, nullptr}, {0, 0, 0}, false};
     if (!st) {
         (void)hipStreamDestroy(s);
         return imh::fail(IMH_ENOMEM, "imh_stream_create: host allocation failed");
@@ -243,6 +246,52 @@ int imh_fill_zero(imh_stream *stream, void *dst, size_t length) {
                        static_cast<uint8_t *>(dst), length);
     IMH_HIP(hipGetLastError());
     return IMH_OK;
+}
+
+int imh_stream_begin_capture(imh_stream *stream) {
+    if (!stream) return imh::fail(IMH_EINVAL, "imh_stream_begin_capture: NULL stream");
+    if (stream->capturing) return imh::fail(IMH_EINVAL, "imh_stream_begin_capture: already capturing");
+    int rc = imh::use_device(stream->dev);
+    if (rc) return rc;
+    IMH_HIP(hipStreamBeginCapture(stream->stream, hipStreamCaptureModeThreadLocal));
+    stream->capturing = true;
+    return IMH_OK;
+}
+
+int imh_stream_end_capture(imh_stream *stream, imh_graph **out) {
+    if (!stream || !out) return imh::fail(IMH_EINVAL, "imh_stream_end_capture: NULL argument");
+    *out = nullptr;
+    if (!stream->capturing) return imh::fail(IMH_EINVAL, "imh_stream_end_capture: stream is not capturing");
+    stream->capturing = false;
+    hipGraph_t g = nullptr;
+    IMH_HIP(hipStreamEndCapture(stream->stream, &g));
+    hipGraphExec_t ex = nullptr;
+    hipError_t e = hipGraphInstantiate(&ex, g, nullptr, nullptr, 0);
+    if (e != hipSuccess) {
+        (void)hipGraphDestroy(g);
+        return imh::hip_fail(e, "hipGraphInstantiate");
+    }
+    imh_graph *gr = new (std::nothrow) imh_graph{stream->dev, g, ex};
+    if (!gr) {
+        (void)hipGraphExecDestroy(ex);
+        (void)hipGraphDestroy(g);
+        return imh::fail(IMH_ENOMEM, "imh_stream_end_capture: host allocation failed");
+    }
+    *out = gr;
+    return IMH_OK;
+}
+
+int imh_graph_launch(imh_graph *graph, imh_stream *stream) {
+    if (!graph || !stream) return imh::fail(IMH_EINVAL, "imh_graph_launch: NULL argument");
+    IMH_HIP(hipGraphLaunch(graph->exec, stream->stream));
+    return IMH_OK;
+}
+
+void imh_graph_free(imh_graph *graph) {
+    if (!graph) return;
+    (void)hipGraphExecDestroy(graph->exec);
+    (void)hipGraphDestroy(graph->graph);
+    delete graph;
 }
 
 int imh_event_create(imh_device *dev, imh_event **out) {

@@ -22,7 +22,8 @@ def _round_half_away(x: np.ndarray) -> np.ndarray:
     """Rust f32::round (ties away from zero), exactly, in f32."""
     t = np.trunc(x)
     frac = np.abs(x - t)  # exact for f32
-    return (t + np.where(frac >= np.float32(0.5), np.sign(x), np.float32(0))).astype(np.float32)
+    # np.where keeps the sign of a truncated -0.0 (Rust: (-0.25f32).round() == -0.0)
+    return np.where(frac >= np.float32(0.5), t + np.sign(x), t).astype(np.float32)
 
 
 def quantize_groups(g: np.ndarray, qmax: float = 15.0):

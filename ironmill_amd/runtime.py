@@ -136,9 +136,43 @@ class Stream:
     def zero(self, buf: Buffer):
         check(lib.imh_fill_zero(self._h, buf.ptr, buf.nbytes))
 
+    def capture(self, fn) -> "Graph":
+        """Record the ops fn() encodes on this stream into a replayable graph."""
+        check(lib.imh_stream_begin_capture(self._h))
+        try:
+            fn()
+        except BaseException:
+            g = C.c_void_p()
+            lib.imh_stream_end_capture(self._h, C.byref(g))
+            if g:
+                lib.imh_graph_free(g)
+            raise
+        g = C.c_void_p()
+        check(lib.imh_stream_end_capture(self._h, C.byref(g)))
+        return Graph(g, self)
+
     def close(self):
         if getattr(self, "_h", None):
             lib.imh_stream_free(self._h)
+            self._h = None
+
+    def __del__(self):
+        self.close()
+
+
+class Graph:
+    """A captured op sequence (imh_graph): replay with launch()."""
+
+    def __init__(self, handle, stream: Stream):
+        self._h = handle
+        self._stream = stream
+
+    def launch(self, stream: Stream | None = None):
+        check(lib.imh_graph_launch(self._h, (stream or self._stream).handle))
+
+    def close(self):
+        if getattr(self, "_h", None):
+            lib.imh_graph_free(self._h)
             self._h = None
 
     def __del__(self):
