@@ -44,9 +44,8 @@ typedef float float4_t __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
 
 constexpr int kGS = 128;       // group size the kernels are built for
-constexpr int kMaxGroups = 10;   // groups one wave holds per stage (weights stay in registers)
+constexpr int kMaxGroups = 8;    // groups one wave holds per stage (weights stay in registers)
 constexpr int kMaxWaves = 16;    // waves per workgroup
-constexpr int kXChunks = 2;      // activation chunks per thread loaded ahead of the weights
 constexpr int kSZChunks = 2;     // scale/zero pairs per thread loaded ahead of the weights
 constexpr int kLdsBudget = 64 * 1024;
 
@@ -177,15 +176,19 @@ __global__ void __launch_bounds__(256) int4_prep_resnorm(
 // ---------------------------------------------------------------------------
 // grid (ceil(N/16), ceil(B/16)), block 64 * NMAT * parts.  Wave w works on
 // matrix w / parts and, in every K stage, on part w % parts of the stage's
-// groups.  A stage is the range of groups whose activation image fits the
-// LDS budget (normally all of K: one stage).
-template <int NMAT, int EPI, bool HAS_LO>
-__global__ void __launch_bounds__(1024) int4_matvec_kernel(
+// groups (at most NG of them).  A stage is the range of groups whose
+// activation image fits the LDS budget (normally all of K: one stage).
+// XC activation chunks per thread are loaded ahead of the weights (the rest,
+// if any, after them).
+template <int NMAT, int EPI, bool HAS_LO, int NG, int XC>
+__global__ void __launch_bounds__(1024) __attribute__((amdgpu_waves_per_eu((NG < 5 || (NG == 5 && XC == 1)) ? 6 : 5)))
+int4_matvec_kernel(
     MatPtrs mp, const _Float16 *__restrict__ xa_hi, const _Float16 *__restrict__ xa_lo,
     const float *__restrict__ rms_inv, int N, int K, int B, int parts, int SG) {
-    // dynamic LDS: [NMAT][16][G + 1] u32 (scale | zero << 16), then the activation planes
+    // dynamic LDS: [NMAT][16][G + 1] u32 (scale | zero << 16), the activation
+    // planes ([min(B,16)][SG*128 + 8] f16, hi then lo), then [waves][64] float4
+    // partial sums
     extern __shared__ __attribute__((aligned(16))) uint32_t lds_dyn[];
-    __shared__ float4_t red[kMaxWaves][64];
 
     const int tid = threadIdx.x;
     const int nthr = blockDim.x;
@@ -212,6 +215,7 @@ __global__ void __launch_bounds__(1024) int4_matvec_kernel(
     const int SZR = G + 1;                                   // LDS row stride (u32)
     uint32_t *szs = lds_dyn;
     _Float16 *xs = reinterpret_cast<_Float16 *>(lds_dyn + ((NMAT * 16 * SZR + 3) & ~3));
+    float4_t *red = reinterpret_cast<float4_t *>(xs + (HAS_LO ? 2 : 1) * min(B, 16) * RSX);
     const int row0 = blockIdx.x * 16;
     const int sz_total = NMAT * 16 * G;
     uint32_t szv[kSZChunks];
@@ -232,9 +236,9 @@ __global__ void __launch_bounds__(1024) int4_matvec_kernel(
         // (a) activation loads of this stage first
         const int cpr = SGs * 16;                  // 8-half chunks per batch row
         const int total = bc * cpr;
-        u32x4_t xv[kXChunks], lv[kXChunks];
+        u32x4_t xv[XC], lv[XC];
 #pragma unroll
-        for (int i = 0; i < kXChunks; i++) {
+        for (int i = 0; i < XC; i++) {
             const int c = min(i * nthr + tid, total - 1);
             const int r = c / cpr;
             const size_t src = (size_t)(m0 + r) * K + (size_t)gs0 * kGS + (size_t)(c - r * cpr) * 8;
@@ -244,9 +248,9 @@ __global__ void __launch_bounds__(1024) int4_matvec_kernel(
         // (b) this wave's weights for the stage: unconditional, clamped loads
         const int wg0 = gs0 + (part * SGs) / parts;
         const int ng = gs0 + ((part + 1) * SGs) / parts - wg0;
-        u32x4_t wq[kMaxGroups];
+        u32x4_t wq[NG];
 #pragma unroll
-        for (int i = 0; i < kMaxGroups; i++) {
+        for (int i = 0; i < NG; i++) {
             const int g = min(max(wg0 + min(i, ng - 1), 0), G - 1);
             wq[i] = *reinterpret_cast<const u32x4_t *>(wrow + (size_t)g * 64);
         }
@@ -278,7 +282,7 @@ __global__ void __launch_bounds__(1024) int4_matvec_kernel(
             __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
         }
 #pragma unroll
-        for (int i = 0; i < kXChunks; i++) {
+        for (int i = 0; i < XC; i++) {
             const int c = i * nthr + tid;
             if (c < total) {
                 const int r = c / cpr;
@@ -287,7 +291,7 @@ __global__ void __launch_bounds__(1024) int4_matvec_kernel(
                 if (HAS_LO) *reinterpret_cast<u32x4_t *>(xs + bc * RSX + off) = lv[i];
             }
         }
-        for (int c = kXChunks * nthr + tid; c < total; c += nthr) {  // activation beyond one pass
+        for (int c = XC * nthr + tid; c < total; c += nthr) {  // activation beyond one pass
             const int r = c / cpr;
             const size_t src = (size_t)(m0 + r) * K + (size_t)gs0 * kGS + (size_t)(c - r * cpr) * 8;
             const int off = r * RSX + (c - r * cpr) * 8;
@@ -303,7 +307,7 @@ __global__ void __launch_bounds__(1024) int4_matvec_kernel(
         const _Float16 *xh = xs + arow * RSX + (wg0 - gs0) * kGS + kq * 32;
         const _Float16 *xl = xh + bc * RSX;
 #pragma unroll
-        for (int i = 0; i < kMaxGroups; i++) {
+        for (int i = 0; i < NG; i++) {
             if (i < ng) {
                 const uint32_t sz = szs[(mat * 16 + n_l) * SZR + wg0 + i];
                 const float zf = (float)__builtin_bit_cast(_Float16, (uint16_t)(sz >> 16));
@@ -337,14 +341,14 @@ __global__ void __launch_bounds__(1024) int4_matvec_kernel(
 
     // reduce the parts of each matrix in part order.  Lane l holds
     // D[m = 4*(l>>4) + r][n = l & 15].
-    red[wave][lane] = acc;
+    red[wave * 64 + lane] = acc;
     __syncthreads();
     if (wave != 0) return;
     float4_t sum[NMAT];
 #pragma unroll
     for (int mt = 0; mt < NMAT; mt++) {
-        sum[mt] = red[mt * parts][lane];
-        for (int p = 1; p < parts; p++) sum[mt] += red[mt * parts + p][lane];
+        sum[mt] = red[mt * parts * 64 + lane];
+        for (int p = 1; p < parts; p++) sum[mt] += red[(mt * parts + p) * 64 + lane];
     }
     if (row >= N) return;
     const int mrow = m0 + 4 * (lane >> 4);
@@ -396,13 +400,18 @@ bool misaligned16(const void *p) { return (reinterpret_cast<uintptr_t>(p) & 15) 
 
 size_t act_bytes(uint32_t B, uint32_t K) { return (size_t)B * K * 4 + (size_t)B * 4 + 256; }
 
-// Waves per tile: each wave holds at most kMaxGroups groups per stage, and
-// the grid carries ~4 waves per SIMD (1024 SIMDs on an MI355X).
-int pick_parts(int tiles, int nmat, int G) {
+// Waves per tile.  Each wave holds at most kMaxGroups groups per stage, and
+// the whole grid should be resident at once -- one round of workgroups, so
+// every weight load is in flight together.  The kernels run 6 waves per SIMD
+// (24 per CU); within that, ~6 waves per SIMD in total is enough to cover
+// HBM latency.
+int pick_parts(int tiles, int nmat, int G, int cus) {
     const int need = (G + kMaxGroups - 1) / kMaxGroups;
-    const int want = (4096 + tiles * nmat - 1) / (tiles * nmat);
+    const int per_cu = (tiles + cus - 1) / cus;              // workgroups each CU must hold
+    const int resident = 24 / per_cu / nmat;
+    const int total = 6 * 4 * cus / std::max(1, tiles * nmat);
     const int cap = std::min(kMaxWaves / nmat, G);
-    return std::max(1, std::min(cap, std::max(need, want)));
+    return std::max(1, std::min(cap, std::max(need, std::min(resident, total))));
 }
 
 // Groups per K stage: as many as the LDS budget holds for the batch rows.
@@ -438,15 +447,35 @@ int launch_main(imh_stream *s, const MatPtrs &mp, const imh_int4_activation *act
     const int K = (int)act->k, B = (int)act->token_count;
     const int G = K / kGS;
     const int tiles = (N + 15) / 16;
-    const int parts = pick_parts(tiles, NMAT, G);
+    const int btiles = (B + 15) / 16;
+    const int parts = pick_parts(tiles * btiles, NMAT, G, s->dev->props.multiProcessorCount);
     const int SG = pick_stage(G, B, HAS_LO, parts);
+    const int ng = (SG + parts - 1) / parts;  // most groups a wave takes in one stage
+    const int waves = NMAT * parts;
     const size_t sz_words = ((size_t)NMAT * 16 * (G + 1) + 3) & ~(size_t)3;
     const size_t lds = sz_words * sizeof(uint32_t) +
-                       (size_t)(HAS_LO ? 2 : 1) * std::min(B, 16) * (SG * kGS + 8) * sizeof(_Float16);
-    dim3 grid(tiles, (B + 15) / 16);
-    hipLaunchKernelGGL((int4_matvec_kernel<NMAT, EPI, HAS_LO>), grid, dim3(64 * NMAT * parts), lds, s->stream,
-                       mp, reinterpret_cast<const _Float16 *>(act->hi),
-                       reinterpret_cast<const _Float16 *>(act->lo), act->row_scale, N, K, B, parts, SG);
+                       (size_t)(HAS_LO ? 2 : 1) * std::min(B, 16) * (SG * kGS + 8) * sizeof(_Float16) +
+                       (size_t)waves * 64 * sizeof(float4_t);
+    dim3 grid(tiles, btiles), block(64 * waves);
+    const _Float16 *hi = reinterpret_cast<const _Float16 *>(act->hi);
+    const _Float16 *lo = reinterpret_cast<const _Float16 *>(act->lo);
+    const bool one_chunk = std::min(B, 16) * SG * 16 <= 64 * waves;  // activation chunks per thread
+#define IMH_NG(NGV)                                                                                        \
+    do {                                                                                                   \
+        if (one_chunk)                                                                                     \
+            hipLaunchKernelGGL((int4_matvec_kernel<NMAT, EPI, HAS_LO, NGV, 1>), grid, block, lds, s->stream, \
+                               mp, hi, lo, act->row_scale, N, K, B, parts, SG);                           \
+        else                                                                                               \
+            hipLaunchKernelGGL((int4_matvec_kernel<NMAT, EPI, HAS_LO, NGV, 2>), grid, block, lds, s->stream, \
+                               mp, hi, lo, act->row_scale, N, K, B, parts, SG);                           \
+    } while (0)
+    if (ng <= 2) IMH_NG(2);
+    else if (ng <= 3) IMH_NG(3);
+    else if (ng <= 4) IMH_NG(4);
+    else if (ng <= 5) IMH_NG(5);
+    else if (ng <= 6) IMH_NG(6);
+    else IMH_NG(8);
+#undef IMH_NG
     IMH_HIP(hipGetLastError());
     return IMH_OK;
 }
