@@ -180,6 +180,12 @@ __global__ void __launch_bounds__(256) int4_prep_resnorm(
 // activation image fits the LDS budget (normally all of K: one stage).
 // XC activation chunks per thread are loaded ahead of the weights (the rest,
 // if any, after them).
+//
+// Issue order matters: vector-memory loads of a wave complete in order, so
+// the small loads the LDS staging needs (scales/zeros, activation) are issued
+// first and the weight loads right after them, before anything waits.  The
+// first stage is peeled so that no loop-carried wait sits ahead of the first
+// weight loads.
 template <int NMAT, int EPI, bool HAS_LO, int NG, int XC>
 __global__ void __launch_bounds__(1024) __attribute__((amdgpu_waves_per_eu((NG < 5 || (NG == 5 && XC == 1)) ? 6 : 5)))
 int4_matvec_kernel(
@@ -203,37 +209,52 @@ int4_matvec_kernel(
 
     const int n_l = lane & 15;           // weight row within the tile (B operand column)
     const int kq = lane >> 4;            // 16-byte quarter of a group this lane reads
-    const int row = blockIdx.x * 16 + n_l;
+    const int row0 = blockIdx.x * 16;
+    const int row = row0 + n_l;
     const int row_c = row < N ? row : N - 1;
     const int arow = n_l < bc ? n_l : 0; // rows past the batch reuse row 0; dropped below
 
-    const uint8_t *wrow = mp.data[mat] + (size_t)row_c * (K / 2) + kq * 16;
+    // matrix pointers by select: a dynamic index into the kernel-argument
+    // struct would turn into dependent memory loads
+    const uint8_t *wdata = (NMAT == 2 && mat) ? mp.data[1] : mp.data[0];
+    const uint8_t *wrow = wdata + (size_t)row_c * (K / 2) + kq * 16;
     const uint32_t c64 = 0x64646464u;
 
-    // scales and zeros of the tile: 16 consecutive rows, one contiguous block
-    // per array, staged once into LDS by the whole workgroup
     const int SZR = G + 1;                                   // LDS row stride (u32)
     uint32_t *szs = lds_dyn;
     _Float16 *xs = reinterpret_cast<_Float16 *>(lds_dyn + ((NMAT * 16 * SZR + 3) & ~3));
     float4_t *red = reinterpret_cast<float4_t *>(xs + (HAS_LO ? 2 : 1) * min(B, 16) * RSX);
-    const int row0 = blockIdx.x * 16;
-    const int sz_total = NMAT * 16 * G;
-    uint32_t szv[kSZChunks];
+
+    // scales and zeros of the tile: per matrix one contiguous run of 16 * G
+    // halfs starting at row0 * G (elements past the last row clamp to it;
+    // their rows are never stored)
+    const int per_mat = 16 * G;
+    const int sz_total = NMAT * per_mat;
+    const size_t sz_last = (size_t)N * G - 1;
+    // element e of the tile's scales/zeros: source offset, arrays, LDS slot
+    auto sz_elem = [&](int e, const uint16_t *&sp, const uint16_t *&zp, int &dst) {
+        const bool second = NMAT == 2 && e >= per_mat;
+        const int el = second ? e - per_mat : e;
+        sp = reinterpret_cast<const uint16_t *>(second ? mp.scales[1] : mp.scales[0]);
+        zp = reinterpret_cast<const uint16_t *>(second ? mp.zeros[1] : mp.zeros[0]);
+        const int rr = el / G;
+        dst = ((second ? 16 : 0) + rr) * SZR + (el - rr * G);
+        return min((size_t)row0 * G + el, sz_last);
+    };
+    uint32_t sv[kSZChunks], zv[kSZChunks];
+    int sd[kSZChunks];
 #pragma unroll
     for (int i = 0; i < kSZChunks; i++) {
-        const int e = min(i * nthr + tid, sz_total - 1);
-        const int mt = e / (16 * G);
-        const int rg = e - mt * 16 * G;
-        const int rr = rg / G;
-        const size_t src = (size_t)min(row0 + rr, N - 1) * G + (rg - rr * G);
-        szv[i] = (uint32_t)reinterpret_cast<const uint16_t *>(mp.scales[mt])[src] |
-                 ((uint32_t)reinterpret_cast<const uint16_t *>(mp.zeros[mt])[src] << 16);
+        const uint16_t *sp, *zp;
+        const size_t src = sz_elem(min(i * nthr + tid, sz_total - 1), sp, zp, sd[i]);
+        sv[i] = sp[src];
+        zv[i] = zp[src];
     }
 
     float4_t acc = {0.0f, 0.0f, 0.0f, 0.0f};
-    for (int gs0 = 0; gs0 < G; gs0 += SG) {
+    auto stage = [&](const int gs0, const bool first) __attribute__((always_inline)) {
         const int SGs = min(SG, G - gs0);
-        // (a) activation loads of this stage first
+        // (a) activation loads of this stage
         const int cpr = SGs * 16;                  // 8-half chunks per batch row
         const int total = bc * cpr;
         u32x4_t xv[XC], lv[XC];
@@ -254,44 +275,35 @@ int4_matvec_kernel(
             const int g = min(max(wg0 + min(i, ng - 1), 0), G - 1);
             wq[i] = *reinterpret_cast<const u32x4_t *>(wrow + (size_t)g * 64);
         }
-        if (gs0 == 0) {  // scales/zeros -> LDS (read after the barrier below)
+        // (c) scales/zeros -> LDS (first stage only; read after the barrier below)
+        // Writes are unconditional: threads past the end rewrite the last
+        // element with its own value, so the compiler has no branch to sink
+        // the loads into (behind a wait for the weights).
+        if (first) {
 #pragma unroll
-            for (int i = 0; i < kSZChunks; i++) {
-                const int e = i * nthr + tid;
-                if (e < sz_total) {
-                    const int mt = e / (16 * G);
-                    const int rg = e - mt * 16 * G;
-                    const int rr = rg / G;
-                    szs[(mt * 16 + rr) * SZR + (rg - rr * G)] = szv[i];
-                }
-            }
+            for (int i = 0; i < kSZChunks; i++) szs[sd[i]] = sv[i] | (zv[i] << 16);
             for (int e = kSZChunks * nthr + tid; e < sz_total; e += nthr) {
-                const int mt = e / (16 * G);
-                const int rg = e - mt * 16 * G;
-                const int rr = rg / G;
-                const size_t src = (size_t)min(row0 + rr, N - 1) * G + (rg - rr * G);
-                szs[(mt * 16 + rr) * SZR + (rg - rr * G)] =
-                    (uint32_t)reinterpret_cast<const uint16_t *>(mp.scales[mt])[src] |
-                    ((uint32_t)reinterpret_cast<const uint16_t *>(mp.zeros[mt])[src] << 16);
+                const uint16_t *sp, *zp;
+                int dst;
+                const size_t src = sz_elem(e, sp, zp, dst);
+                szs[dst] = (uint32_t)sp[src] | ((uint32_t)zp[src] << 16);
             }
-        }
-        // (c) activation -> LDS (after the previous stage is done with it)
-        if (gs0 > 0) {
+        } else {
+            // the previous stage is done with the activation planes
             __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
             __builtin_amdgcn_s_barrier();
             __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
         }
+        // (d) activation -> LDS
 #pragma unroll
         for (int i = 0; i < XC; i++) {
-            const int c = i * nthr + tid;
-            if (c < total) {
-                const int r = c / cpr;
-                const int off = r * RSX + (c - r * cpr) * 8;
-                *reinterpret_cast<u32x4_t *>(xs + off) = xv[i];
-                if (HAS_LO) *reinterpret_cast<u32x4_t *>(xs + bc * RSX + off) = lv[i];
-            }
+            const int c = min(i * nthr + tid, total - 1);
+            const int r = c / cpr;
+            const int off = r * RSX + (c - r * cpr) * 8;
+            *reinterpret_cast<u32x4_t *>(xs + off) = xv[i];
+            if (HAS_LO) *reinterpret_cast<u32x4_t *>(xs + bc * RSX + off) = lv[i];
         }
-        for (int c = XC * nthr + tid; c < total; c += nthr) {  // activation beyond one pass
+        for (int c = XC * nthr + tid; c < total; c += nthr) {  // activation beyond XC chunks
             const int r = c / cpr;
             const size_t src = (size_t)(m0 + r) * K + (size_t)gs0 * kGS + (size_t)(c - r * cpr) * 8;
             const int off = r * RSX + (c - r * cpr) * 8;
@@ -299,11 +311,12 @@ int4_matvec_kernel(
             if (HAS_LO)
                 *reinterpret_cast<u32x4_t *>(xs + bc * RSX + off) = *reinterpret_cast<const u32x4_t *>(xa_lo + src);
         }
+        // LDS-only barrier: the weight loads stay in flight across it
         __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
         __builtin_amdgcn_s_barrier();
         __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
 
-        // (d) MFMA over the wave's groups
+        // (e) MFMA over the wave's groups
         const _Float16 *xh = xs + arow * RSX + (wg0 - gs0) * kGS + kq * 32;
         const _Float16 *xl = xh + bc * RSX;
 #pragma unroll
@@ -337,7 +350,9 @@ int4_matvec_kernel(
                 for (int r = 0; r < 4; r++) acc[r] = __builtin_fmaf(accg[r], s, acc[r]);
             }
         }
-    }
+    };
+    stage(0, true);
+    for (int gs0 = SG; gs0 < G; gs0 += SG) stage(gs0, false);
 
     // reduce the parts of each matrix in part order.  Lane l holds
     // D[m = 4*(l>>4) + r][n = l & 15].
