@@ -185,9 +185,10 @@ int imh_encode_fused_residual_norm_affine_matvec_int4(imh_stream *stream,
  * projections and a caller can time the matvec kernel alone.  No reference
  * counterpart: the Metal kernels read x directly. */
 typedef struct {
-    const uint16_t *hi;      /* [token_count][k] f16 in kernel operand order */
-    const uint16_t *lo;      /* residual halves, or NULL when x is exactly f16 */
-    const float *row_scale;  /* [token_count] output multiplier, or NULL */
+    const uint16_t *hi;        /* [token_count][k] f16 operand values, kernel order */
+    const uint16_t *lo;        /* [token_count][k] f16 residuals of the same values */
+    const float *group_sums;   /* [token_count][2][k/128] per-group operand sums (hi, lo) */
+    const float *row_scale;    /* [token_count] output multiplier, or NULL */
     uint32_t token_count;
     uint32_t k;
 } imh_int4_activation;

@@ -86,6 +86,7 @@ class Int4Activation(C.Structure):
     _fields_ = [
         ("hi", C.c_void_p),
         ("lo", C.c_void_p),
+        ("group_sums", C.c_void_p),
         ("row_scale", C.c_void_p),
         ("token_count", C.c_uint32),
         ("k", C.c_uint32),
