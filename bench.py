@@ -8,8 +8,7 @@ Workload of the headline number: the Qwen3-4B decode
 FFN block at batch 1 -- fused gate+up 2560 -> 2 x 9728 with SiLU, then down
 9728 -> 2560, INT4 group-128 weights from N(0, 0.02), AWQ scales U[0.5, 2],
 fp16 activations N(0,1) with 1 % of channels x20.  A step is one such FFN block
-through the public ops (activation image + matvec for each projection).  The
-weights are replicated over >= 512 MB of distinct buffers and the steps
+through the public ops (one kernel launch each).  The weights are replicated over >= 512 MB of distinct buffers and the steps
 rotate through them, so the MI355X's 256 MB Infinity Cache cannot serve them.
 
 Bytes are counted as in the reference's kernel_bandwidth_bench
@@ -17,9 +16,9 @@ Bytes are counted as in the reference's kernel_bandwidth_bench
 scales + f16 zeros + AWQ + x + y.
 
 The JSON line also carries
-  roofline     -- the dominant kernel (fused gate+up matvec, prepared
-                  activation): K launches recorded into a HIP graph, replayed
-                  between two HIP events on its stream, time / K;
+  roofline     -- the dominant kernel (fused gate+up matvec with SiLU): K
+                  launches recorded into a HIP graph, replayed between two HIP
+                  events on its stream, time / K;
   cpu_baseline -- the C oracle's dequantize-then-compute FFN step on the host
                   cores (weights dequantized once outside the timing);
   details      -- batch 4/8 FFN kernels and TurboQuant attention at 32k.
@@ -198,13 +197,10 @@ def main():
     act = dev.empty((B, F), np.float16)
     y = dev.empty((B, H), np.float16)
 
-    # ---- dominant kernel: fused gate+up matvec on a prepared activation ----
-    prep = ops.PreparedActivation(dev, B, H)
-    ops.encode_int4_activation(stream, x, prep, awq=W[0][0].awq_scales)
-
+    # ---- dominant kernel: fused gate+up matvec (one launch per op) ----
     def gate_up_kernel(i):
         g, u, _ = W[i % reps]
-        ops.encode_int4_matvec_prepared(stream, prep, g, act, u, None, epilogue="silu")
+        ops.encode_fused_ffn_gate_up_act_int4(stream, x, g, u, act, B)
 
     ksteps = args.steps if not args.kernel_only else max(args.steps, 500)
     tot = time_loop(dev, stream, gate_up_kernel, ksteps, args.warmup)
@@ -213,7 +209,7 @@ def main():
     k_gbs = k_bytes / (k_us * 1e-6) / 1e9
     log(f"gate+up kernel: {k_us:.2f} us  {k_gbs:.0f} GB/s ({100 * k_gbs / HBM_PEAK_GBS:.1f} %)")
     if args.kernel_only:
-        print(json.dumps({"kernel": "int4_matvec_kernel<2,SILU,hi+lo>", "us": round(k_us, 3),
+        print(json.dumps({"kernel": "int4_matvec_kernel<2,SILU>", "us": round(k_us, 3),
                           "GB/s": round(k_gbs, 1), "launches": ksteps}))
         return
 
@@ -238,11 +234,8 @@ def main():
     details = {}
     if not args.no_details:
         # down projection kernel alone, and the FFN kernels at batch 4 / 8
-        prep_d = ops.PreparedActivation(dev, B, F)
-        ops.encode_int4_activation(stream, act, prep_d, awq=W[0][2].awq_scales)
-
         def down_kernel(i):
-            ops.encode_int4_matvec_prepared(stream, prep_d, W[i % reps][2], y)
+            ops.encode_projection(stream, act, W[i % reps][2], y, B)
 
         t = time_loop(dev, stream, down_kernel, args.steps, args.warmup)
         d_us = 1e3 * t / args.steps
@@ -250,24 +243,21 @@ def main():
                                           "GB/s": round(down_bytes(B) / (d_us * 1e-6) / 1e9, 1)}
         for bb in (4, 8):
             xb = dev.upload(make_x(bb, H, 5 + bb))
-            pb = ops.PreparedActivation(dev, bb, H)
-            ops.encode_int4_activation(stream, xb, pb, awq=W[0][0].awq_scales)
             ab = dev.empty((bb, F), np.float16)
 
-            def gu(i, pb=pb, ab=ab):
+            def gu(i, xb=xb, ab=ab, bb=bb):
                 g, u, _ = W[i % reps]
-                ops.encode_int4_matvec_prepared(stream, pb, g, ab, u, None, epilogue="silu")
+                ops.encode_fused_ffn_gate_up_act_int4(stream, xb, g, u, ab, bb)
 
             t = time_loop(dev, stream, gu, args.steps, args.warmup)
             us = 1e3 * t / args.steps
             details[f"gate_up_kernel_b{bb}"] = {"us": round(us, 2),
                                                 "GB/s": round(gate_up_bytes(bb) / (us * 1e-6) / 1e9, 1)}
-            pdn = ops.PreparedActivation(dev, bb, F)
-            ops.encode_int4_activation(stream, ab, pdn, awq=W[0][2].awq_scales)
+            ops.encode_fused_ffn_gate_up_act_int4(stream, xb, W[0][0], W[0][1], ab, bb)
             yb = dev.empty((bb, H), np.float16)
 
-            def dn(i, pdn=pdn, yb=yb):
-                ops.encode_int4_matvec_prepared(stream, pdn, W[i % reps][2], yb)
+            def dn(i, ab=ab, yb=yb, bb=bb):
+                ops.encode_projection(stream, ab, W[i % reps][2], yb, bb)
 
             t = time_loop(dev, stream, dn, args.steps, args.warmup)
             us = 1e3 * t / args.steps
@@ -304,7 +294,7 @@ def main():
                    "awq": True, "weight_replicas": reps},
         "roofline": {"bound": "hbm", "achieved": round(k_gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(k_gbs / HBM_PEAK_GBS, 4), "traffic": traffic,
-                     "kernel": "int4_matvec_kernel (fused gate+up, SiLU, AWQ hi/lo)",
+                     "kernel": "int4_matvec_kernel (fused gate+up, SiLU, AWQ)",
                      "bytes_per_launch": k_bytes, "us_per_launch": round(k_us, 3)},
         "cpu_baseline": cpu,
         "details": details,

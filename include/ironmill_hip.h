@@ -178,38 +178,6 @@ typedef struct {
 int imh_encode_fused_residual_norm_affine_matvec_int4(imh_stream *stream,
                                                       const imh_fused_residual_norm_params *p);
 
-/* Activation operand image.  The INT4 ops above first rewrite their activation
- * (x / awq, or (a + b) * gamma / awq with a per-row rms factor) into the order
- * the matrix-core kernel consumes, then run the matvec.  These two entry points
- * expose the two steps, so a producer can build the image once for several
- * projections and a caller can time the matvec kernel alone.  No reference
- * counterpart: the Metal kernels read x directly. */
-typedef struct {
-    const uint16_t *hi;        /* [token_count][k] f16 operand values, kernel order */
-    const uint16_t *lo;        /* [token_count][k] f16 residuals of the same values */
-    const float *group_sums;   /* [token_count][2][k/128] per-group operand sums (hi, lo) */
-    const float *row_scale;    /* [token_count] output multiplier, or NULL */
-    uint32_t token_count;
-    uint32_t k;
-} imh_int4_activation;
-
-/* Bytes of caller storage imh_encode_int4_activation needs. */
-size_t imh_int4_activation_bytes(uint32_t token_count, uint32_t k);
-/* Build the image of x [token_count][k] (divided by awq[k] when awq != NULL)
- * in `storage` (16-byte aligned, imh_int4_activation_bytes long). */
-int imh_encode_int4_activation(imh_stream *stream, const uint16_t *x, uint32_t token_count,
-                               uint32_t k, const uint16_t *awq, void *storage,
-                               imh_int4_activation *out);
-#define IMH_EPI_STORE 0     /* out0 = f16(W0 x) [, out1 = f16(W1 x)] */
-#define IMH_EPI_SILU 2      /* out0 = f16(silu(W0 x) * (W1 x)) */
-#define IMH_EPI_GELU 3      /* out0 = f16(gelu_tanh(W0 x) * (W1 x)) */
-/* Matvec over a prepared activation: one weight (w1 == NULL, IMH_EPI_STORE) or
- * a gate/up pair sharing the activation. */
-int imh_encode_int4_matvec_prepared(imh_stream *stream, const imh_int4_activation *act,
-                                    const imh_affine_int4_weight *w0,
-                                    const imh_affine_int4_weight *w1, int epilogue,
-                                    uint16_t *out0, uint16_t *out1);
-
 /* ====================== op tier: TurboQuant INT8 KV cache ====================== */
 
 /* MetalTurboQuantModel (metal/turboquant/mod.rs:51-79,221-287): rotation signs

@@ -80,22 +80,6 @@ class FusedResidualNormParams(C.Structure):
     ]
 
 
-class Int4Activation(C.Structure):
-    """imh_int4_activation: the operand image the INT4 kernels consume."""
-
-    _fields_ = [
-        ("hi", C.c_void_p),
-        ("lo", C.c_void_p),
-        ("group_sums", C.c_void_p),
-        ("row_scale", C.c_void_p),
-        ("token_count", C.c_uint32),
-        ("k", C.c_uint32),
-    ]
-
-
-IMH_EPI_STORE, IMH_EPI_SILU, IMH_EPI_GELU = 0, 2, 3
-
-
 class TqKvCache(C.Structure):
     """imh_tq_kv_cache (one layer of MetalKvCache, metal/turboquant/cache.rs:45-96)."""
 
@@ -150,10 +134,6 @@ SIGNATURES = {
     "imh_encode_fused_ffn_gate_up_act_int4": (I, [P, P, U32, C.POINTER(AffineInt4Weight),
                                                   C.POINTER(AffineInt4Weight), P, I]),
     "imh_encode_fused_residual_norm_affine_matvec_int4": (I, [P, C.POINTER(FusedResidualNormParams)]),
-    "imh_int4_activation_bytes": (SZ, [U32, U32]),
-    "imh_encode_int4_activation": (I, [P, P, U32, U32, P, P, C.POINTER(Int4Activation)]),
-    "imh_encode_int4_matvec_prepared": (I, [P, C.POINTER(Int4Activation), C.POINTER(AffineInt4Weight),
-                                            C.POINTER(AffineInt4Weight), I, P, P]),
     "imh_tq_tables_create": (I, [P, U32, U32, C.c_uint64, C.POINTER(P)]),
     "imh_tq_tables_create_from_host": (I, [P, U32, U32, P, P, P, P, P, P, C.POINTER(P)]),
     "imh_tq_tables_free": (None, [P]),

@@ -14,8 +14,7 @@ import math
 import numpy as np
 
 from . import _lib
-from ._lib import (IMH_EPI_GELU, IMH_EPI_SILU, IMH_EPI_STORE, AffineInt4Weight,
-                   FusedResidualNormParams, Int4Activation, TqKvCache, check, lib)
+from ._lib import AffineInt4Weight, FusedResidualNormParams, TqKvCache, check, lib
 from .quant import QuantizedInt4
 from .runtime import Buffer, Device, Stream
 
@@ -85,29 +84,6 @@ def encode_fused_residual_norm_affine_matvec_int4(stream: Stream, a, b, norm_wei
                                 C.pointer(weight.c), _ptr(output), _ptr(normed_output), token_count,
                                 eps)
     check(lib.imh_encode_fused_residual_norm_affine_matvec_int4(stream.handle, C.byref(p)))
-
-
-class PreparedActivation:
-    """Operand image of an activation (imh_encode_int4_activation) in its own storage."""
-
-    def __init__(self, dev: Device, token_count: int, k: int):
-        self.storage = dev.buffer(max(1, lib.imh_int4_activation_bytes(token_count, k)))
-        self.c = Int4Activation()
-        self.token_count, self.k = token_count, k
-
-
-def encode_int4_activation(stream: Stream, x, act: PreparedActivation, awq=None):
-    check(lib.imh_encode_int4_activation(stream.handle, _ptr(x), act.token_count, act.k, _ptr(awq),
-                                         act.storage.ptr, C.byref(act.c)))
-
-
-def encode_int4_matvec_prepared(stream: Stream, act: PreparedActivation, w0: AffineQuantizedWeight,
-                                out0, w1: AffineQuantizedWeight | None = None, out1=None,
-                                epilogue: str = "store"):
-    epi = {"store": IMH_EPI_STORE, "silu": IMH_EPI_SILU, "gelu": IMH_EPI_GELU}[epilogue]
-    check(lib.imh_encode_int4_matvec_prepared(stream.handle, C.byref(act.c), C.byref(w0.c),
-                                              C.byref(w1.c) if w1 is not None else None, epi,
-                                              _ptr(out0), _ptr(out1)))
 
 
 # ------------------------------------------------------------------ TurboQuant
@@ -219,7 +195,6 @@ def encode_kv_cache_and_attention(stream: Stream, tq: TurboQuantModel, cache: Tu
 __all__ = [
     "AffineQuantizedWeight", "encode_projection", "encode_batched_affine_matvec_int4",
     "encode_fused_ffn_gate_up_act_int4", "encode_fused_residual_norm_affine_matvec_int4",
-    "PreparedActivation", "encode_int4_activation", "encode_int4_matvec_prepared",
     "TurboQuantModel", "TurboQuantKvCache", "encode_turboquant_cache_write",
     "encode_turboquant_attention", "encode_kv_cache_and_attention", "_lib",
 ]

@@ -102,7 +102,6 @@ def test_error_paths_without_gpu():
     assert L.imh_device_open(0, None) == _lib.IMH_EINVAL
     assert L.imh_encode_affine_projection_int4(None, None, 1, None, None) == _lib.IMH_EINVAL
     assert b"NULL" in L.imh_last_error()
-    assert L.imh_int4_activation_bytes(4, 2560) >= 4 * 2560 * 4
     n = C.c_int(-1)
     L.imh_device_count(C.byref(n))  # no GPU here: an error code or 0, never a crash
     assert n.value >= 0
