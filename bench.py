@@ -173,7 +173,19 @@ def main():
                          "256 MB Infinity Cache; 1 measures a cache-resident matrix)")
     ap.add_argument("--kernel-only", action="store_true",
                     help="only the prepared fused gate+up kernel loop (for rocprofv3 counter runs)")
+    ap.add_argument("--calibrate-copy", action="store_true",
+                    help="only 5 device-to-device copies of 256 MiB (calibrates rocprofv3 "
+                         "FETCH_SIZE / WRITE_SIZE against a known byte count), then exit")
     args = ap.parse_args()
+    if args.calibrate_copy:
+        import torch
+        a = torch.ones(64 << 20, dtype=torch.int32, device="cuda")
+        b = torch.empty_like(a)
+        for _ in range(5):
+            b.copy_(a)
+        torch.cuda.synchronize()
+        log(f"copy calibration: 5 copies of {a.numel() * 4} bytes")
+        return
     if args.gpus != 1:
         print(f"bench.py: this build measures one GPU; --gpus {args.gpus} is not supported "
               "(the hot path has no multi-GPU code, see DESIGN.md for how it would shard)",
