@@ -128,21 +128,72 @@ __global__ void __launch_bounds__(kD) tq_cache_write_kernel(
 }
 
 // ---------------------------------------------------------------------------
-// decode attention: grid (num_splits, num_kv_heads, batch), block 64 * kWaves
+// decode attention
 // ---------------------------------------------------------------------------
+// Query prep: grid (num_kv_heads, batch), block kD.  For every query head of
+// the GQA group: q_rot = D.H.D/sqrt(d) q (butterfly in LDS) and its QJL
+// projection s_q[d] = sum_k S[d][k] q_rot[k] (fmaf in increasing k, S^T read
+// coalesced).  Written once per group to qprep [batch][nh][2][kD] f32, so the
+// split workgroups of the attention kernel only load it.
+template <int GQA>
+__global__ void __launch_bounds__(kD) tq_query_prep_kernel(const __half *__restrict__ q, int nh,
+                                                           const float *__restrict__ signs,
+                                                           const float *__restrict__ qjl_t,
+                                                           float *__restrict__ qprep) {
+    __shared__ float qs[GQA][kD];
+    const int d = threadIdx.x;
+    const int kvh = blockIdx.x, b = blockIdx.y;
+    const float sg = signs[d];
+#pragma unroll
+    for (int hh = 0; hh < GQA; hh++) qs[hh][d] = __half2float(q[((size_t)b * nh + kvh * GQA + hh) * kD + d]) * sg;
+    __syncthreads();
+    for (int step = 1; step < kD; step *= 2) {
+        if (d < kD / 2) {
+            const int j = (d / step) * (step * 2) + (d % step);
+#pragma unroll
+            for (int hh = 0; hh < GQA; hh++) {
+                const float a = qs[hh][j], c = qs[hh][j + step];
+                qs[hh][j] = a + c;
+                qs[hh][j + step] = a - c;
+            }
+        }
+        __syncthreads();
+    }
+    const float rscale = 1.0f / sqrtf((float)kD);
+#pragma unroll
+    for (int hh = 0; hh < GQA; hh++) qs[hh][d] = qs[hh][d] * (sg * rscale);
+    __syncthreads();
+    float acc[GQA];
+#pragma unroll
+    for (int hh = 0; hh < GQA; hh++) acc[hh] = 0.0f;
+    for (int k = 0; k < kD; k++) {
+        const float s = qjl_t[(size_t)k * kD + d];
+#pragma unroll
+        for (int hh = 0; hh < GQA; hh++) acc[hh] = __builtin_fmaf(s, qs[hh][k], acc[hh]);
+    }
+#pragma unroll
+    for (int hh = 0; hh < GQA; hh++) {
+        float *dst = qprep + ((size_t)b * nh + kvh * GQA + hh) * 2 * kD;
+        dst[d] = qs[hh][d];
+        dst[kD + d] = acc[hh];
+    }
+}
+
+// Attention: grid (num_splits, num_kv_heads, batch), block 64 * kWaves.  Each
+// wave walks its split in 16-position chunks; the codes and per-position
+// scales of the next chunk are loaded before the current one is computed.
 __device__ __forceinline__ float shfl_xor16(float v, int m) { return __shfl_xor(v, m, 16); }
 
 template <int GQA>
 __global__ void __launch_bounds__(64 * kWaves) tq_attention_kernel(
-    const __half *__restrict__ q, int nh, int nkv, int max_seq, int seq_len,
-    const int32_t *__restrict__ seq_lens, float attn_scale, const float *__restrict__ signs,
-    const float *__restrict__ kcb, const float *__restrict__ vcb, const float *__restrict__ qjl_t,
+    const float *__restrict__ qprep, int nh, int nkv, int max_seq, int seq_len,
+    const int32_t *__restrict__ seq_lens, float attn_scale,
+    const float *__restrict__ kcb, const float *__restrict__ vcb,
     const uint8_t *__restrict__ kcodes, const uint8_t *__restrict__ vcodes,
     const float *__restrict__ kscales, const float *__restrict__ vscales,
     const float *__restrict__ krnorm, int split_len, float *__restrict__ part_o,
     float *__restrict__ part_m, float *__restrict__ part_l) {
-    __shared__ float qs[GQA][kD];
-    __shared__ float ss[GQA][kD];
+    __shared__ float qs[GQA][2][kD];
     __shared__ uint32_t ktab[128];
     __shared__ float vtab[256];
     __shared__ float om[kWaves][GQA][kD];
@@ -155,7 +206,39 @@ __global__ void __launch_bounds__(64 * kWaves) tq_attention_kernel(
     const int split = blockIdx.x, kvh = blockIdx.y, b = blockIdx.z;
     const int S = gridDim.x;
 
-    // tables: K codebook as (f16 hi | f16 lo << 16), V codebook in f32
+    int L = seq_lens ? seq_lens[b] : seq_len;
+    L = L < 0 ? 0 : (L > max_seq ? max_seq : L);
+    const int p_begin = split * split_len;
+    const int p_end = min(p_begin + split_len, L);
+    const size_t head_base = ((size_t)b * nkv + kvh) * (size_t)max_seq;
+    const int n_l = lane & 15;
+    const int kg = lane >> 4;
+    const int vgrp = lane & 7;    // which 16-dim slice of V this lane accumulates
+    const int vpos = lane >> 3;   // which of 8 positions per round
+
+    // chunk inputs, loaded one chunk ahead
+    struct ChunkIn {
+        uint4 k0, k1, v0, v1;
+        float ksc, krn, vsc;
+    };
+    auto load_chunk = [&](int p0, ChunkIn &c) __attribute__((always_inline)) {
+        const int last = p_end - 1;
+        const int pk = min(p0 + n_l, last);
+        const uint4 *kp = reinterpret_cast<const uint4 *>(kcodes + (head_base + pk) * kD + kg * 32);
+        c.k0 = kp[0];
+        c.k1 = kp[1];
+        c.v0 = *reinterpret_cast<const uint4 *>(vcodes + (head_base + min(p0 + vpos, last)) * kD + vgrp * 16);
+        c.v1 = *reinterpret_cast<const uint4 *>(vcodes + (head_base + min(p0 + 8 + vpos, last)) * kD + vgrp * 16);
+        c.ksc = kscales[head_base + pk];
+        c.krn = krnorm[head_base + pk];
+        c.vsc = vscales[head_base + pk];
+    };
+    ChunkIn cur;
+    const int p_first = p_begin + wave * kChunk;
+    if (p_first < p_end) load_chunk(p_first, cur);
+
+    // tables: K codebook as (f16 hi | f16 lo << 16), V codebook in f32; the
+    // group's prepared queries
     if (tid < 128) {
         const float c = kcb[tid];
         const _Float16 hi = (_Float16)c;
@@ -164,42 +247,13 @@ __global__ void __launch_bounds__(64 * kWaves) tq_attention_kernel(
                     ((uint32_t)__builtin_bit_cast(uint16_t, lo) << 16);
     }
     vtab[tid] = vcb[tid];
-
-    // rotate the GQA group's queries: q_rot = D.H.D/sqrt(d) q
-    for (int e = tid; e < GQA * kD; e += 64 * kWaves) {
-        const int hh = e / kD, d = e % kD;
-        qs[hh][d] = __half2float(q[((size_t)b * nh + kvh * GQA + hh) * kD + d]) * signs[d];
-    }
-    __syncthreads();
-    for (int step = 1; step < kD; step *= 2) {
-        for (int e = tid; e < GQA * kD / 2; e += 64 * kWaves) {
-            const int hh = e / (kD / 2), i = e % (kD / 2);
-            const int j = (i / step) * (step * 2) + (i % step);
-            const float a = qs[hh][j], c = qs[hh][j + step];
-            qs[hh][j] = a + c;
-            qs[hh][j + step] = a - c;
-        }
-        __syncthreads();
-    }
-    const float rscale = 1.0f / sqrtf((float)kD);
-    for (int e = tid; e < GQA * kD; e += 64 * kWaves) {
-        const int hh = e / kD, d = e % kD;
-        qs[hh][d] = qs[hh][d] * (signs[d] * rscale);
-    }
-    __syncthreads();
-    // QJL projection of the rotated query: s_q[d] = sum_k S[d][k] q_rot[k]
-    for (int e = tid; e < GQA * kD; e += 64 * kWaves) {
-        const int hh = e / kD, d = e % kD;
-        float acc = 0.0f;
-        for (int k = 0; k < kD; k++) acc = __builtin_fmaf(qjl_t[(size_t)k * kD + d], qs[hh][k], acc);
-        ss[hh][d] = acc;
-    }
+    const float *qg = qprep + ((size_t)b * nh + kvh * GQA) * 2 * kD;
+    for (int e = tid; e < GQA * 2 * kD; e += 64 * kWaves) (&qs[0][0][0])[e] = qg[e];
     __syncthreads();
 
     // operand A (rows = heads of the group, hi and lo halves), k-slot order
     // within each 4-byte word: bytes {0, 2, 1, 3}
     const int am = lane & 15;
-    const int kg = lane >> 4;
     half8_t aq_hi[4], aq_lo[4], as_hi[4], as_lo[4];
     constexpr int slot_byte[8] = {0, 2, 1, 3, 4, 6, 5, 7};
 #pragma unroll
@@ -209,8 +263,8 @@ __global__ void __launch_bounds__(64 * kWaves) tq_attention_kernel(
             float vq = 0.0f, vs = 0.0f;
             if (am < GQA) {
                 const int d = kg * 32 + j * 8 + slot_byte[i];
-                vq = qs[am][d];
-                vs = ss[am][d];
+                vq = qs[am][0][d];
+                vs = qs[am][1][d];
             }
             const _Float16 qh = (_Float16)vq, sh = (_Float16)vs;
             aq_hi[j][i] = qh;
@@ -220,13 +274,7 @@ __global__ void __launch_bounds__(64 * kWaves) tq_attention_kernel(
         }
     }
 
-    int L = seq_lens ? seq_lens[b] : seq_len;
-    L = L < 0 ? 0 : (L > max_seq ? max_seq : L);
-    const int p_begin = split * split_len;
-    const int p_end = min(p_begin + split_len, L);
-    const size_t head_base = ((size_t)b * nkv + kvh) * (size_t)max_seq;
     const float qjl_factor = sqrtf(2.0f / 3.14159265f) / (float)kD;
-
     float m_run[GQA], l_run[GQA];
     float o[GQA][16];
 #pragma unroll
@@ -237,16 +285,11 @@ __global__ void __launch_bounds__(64 * kWaves) tq_attention_kernel(
         for (int e = 0; e < 16; e++) o[hh][e] = 0.0f;
     }
 
-    const int n_l = lane & 15;
-    const int vgrp = lane & 7;    // which 16-dim slice of V this lane accumulates
-    const int vpos = lane >> 3;   // which of 8 positions per round
-
-    for (int p0 = p_begin + wave * kChunk; p0 < p_end; p0 += kChunk * kWaves) {
+    for (int p0 = p_first; p0 < p_end; p0 += kChunk * kWaves) {
+        const ChunkIn c = cur;
+        if (p0 + kChunk * kWaves < p_end) load_chunk(p0 + kChunk * kWaves, cur);
         // ---- scores: S[h][n] for 16 positions via MFMA ----
-        const int pk = min(p0 + n_l, p_end - 1);
-        const uint4 *kp = reinterpret_cast<const uint4 *>(kcodes + (head_base + pk) * kD + kg * 32);
-        const uint4 k0 = kp[0], k1 = kp[1];
-        const uint32_t kw[8] = {k0.x, k0.y, k0.z, k0.w, k1.x, k1.y, k1.z, k1.w};
+        const uint32_t kw[8] = {c.k0.x, c.k0.y, c.k0.z, c.k0.w, c.k1.x, c.k1.y, c.k1.z, c.k1.w};
         float4_t d1 = {0, 0, 0, 0}, d2 = {0, 0, 0, 0};
 #pragma unroll
         for (int j = 0; j < 4; j++) {
@@ -277,15 +320,13 @@ __global__ void __launch_bounds__(64 * kWaves) tq_attention_kernel(
         }
         // lanes 0..15 hold D[h][n] for h = 0..3 (rows), position p0 + n
         const bool valid = (p0 + n_l) < p_end;
-        const float ksc = kscales[head_base + pk];
-        const float qw = krnorm[head_base + pk] * qjl_factor * ksc;
-        const float vsc = vscales[head_base + pk];
+        const float qw = c.krn * qjl_factor * c.ksc;
         float wgt[GQA];
         float corr[GQA];
         bool rescale = false;
 #pragma unroll
         for (int hh = 0; hh < GQA; hh++) {
-            float sc = valid ? attn_scale * (d1[hh] * ksc + d2[hh] * qw) : -INFINITY;
+            float sc = valid ? attn_scale * (d1[hh] * c.ksc + d2[hh] * qw) : -INFINITY;
             float cm = sc;
             cm = fmaxf(cm, shfl_xor16(cm, 8));
             cm = fmaxf(cm, shfl_xor16(cm, 4));
@@ -303,7 +344,7 @@ __global__ void __launch_bounds__(64 * kWaves) tq_attention_kernel(
             ws = __shfl(ws, 0);
             l_run[hh] = l_run[hh] * corr[hh] + ws;
             m_run[hh] = nm;
-            wgt[hh] = w * vsc;
+            wgt[hh] = w * c.vsc;
             rescale |= corr[hh] != 1.0f;
         }
         if (rescale) {
@@ -319,8 +360,7 @@ __global__ void __launch_bounds__(64 * kWaves) tq_attention_kernel(
             float wv[GQA];
 #pragma unroll
             for (int hh = 0; hh < GQA; hh++) wv[hh] = __shfl(wgt[hh], pi);
-            const int pv = min(p0 + pi, p_end - 1);
-            const uint4 vv = *reinterpret_cast<const uint4 *>(vcodes + (head_base + pv) * kD + vgrp * 16);
+            const uint4 vv = r ? c.v1 : c.v0;
             const uint32_t vw[4] = {vv.x, vv.y, vv.z, vv.w};
 #pragma unroll
             for (int e = 0; e < 16; e++) {
@@ -479,13 +519,15 @@ int imh_encode_turboquant_attention(imh_stream *stream, const imh_tq_tables *t,
     rc = imh::use_device(stream->dev);
     if (rc) return rc;
 
-    // KV split: aim for ~1024 workgroups (4 per CU) with >= 64 positions each.
+    // KV split: aim for ~512 workgroups (2 per CU, 8 waves) with >= 64
+    // positions each; a wave keeps one chunk in flight ahead of the one it
+    // computes.
     const uint32_t L = seq_len;
     const uint32_t B = cache->batch;
     uint32_t want = num_splits;
     if (want == 0) {
         const uint32_t groups = B * nkv;
-        want = (1024 + groups - 1) / groups;
+        want = (512 + groups - 1) / groups;
     }
     const uint32_t max_splits = std::max<uint32_t>(1, (L + kSplitQuantum - 1) / kSplitQuantum);
     want = std::max<uint32_t>(1, std::min(want, max_splits));
@@ -494,23 +536,30 @@ int imh_encode_turboquant_attention(imh_stream *stream, const imh_tq_tables *t,
                                    (split_len + kSplitQuantum - 1) / kSplitQuantum * kSplitQuantum);
     const uint32_t S = std::max<uint32_t>(1, (L + split_len - 1) / split_len);
 
+    // scratch: prepared queries [B][nh][2][kD], then the split partials
+    const size_t nq = (size_t)B * num_heads * 2 * kD;
     const size_t nparts = (size_t)B * num_heads * S;
-    const size_t need = nparts * kD * 4 + nparts * 8 + 512;
+    const size_t need = nq * 4 + nparts * kD * 4 + nparts * 8 + 512;
     void *scr = nullptr;
     rc = imh::stream_scratch(stream, 1, need, &scr);
     if (rc) return rc;
-    float *po = static_cast<float *>(scr);
+    float *qprep = static_cast<float *>(scr);
+    float *po = qprep + nq;
     float *pm = po + nparts * kD;
     float *pl = pm + nparts;
 
-    dim3 grid(S, nkv, B);
     const __half *qh = reinterpret_cast<const __half *>(q);
-#define IMH_TQ_LAUNCH(G)                                                                            \
-    hipLaunchKernelGGL(tq_attention_kernel<G>, grid, dim3(64 * kWaves), 0, stream->stream, qh,      \
-                       (int)num_heads, (int)nkv, (int)cache->max_seq_len, (int)seq_len, seq_lens,   \
-                       attn_scale, t->signs, t->k_codebook, t->v_codebook, t->qjl_t, cache->k_codes, \
-                       cache->v_codes, cache->k_scales, cache->v_scales, cache->k_r_norms,          \
-                       (int)split_len, po, pm, pl)
+    dim3 grid(S, nkv, B);
+#define IMH_TQ_LAUNCH(G)                                                                              \
+    do {                                                                                              \
+        hipLaunchKernelGGL(tq_query_prep_kernel<G>, dim3(nkv, B), dim3(kD), 0, stream->stream, qh,    \
+                           (int)num_heads, t->signs, t->qjl_t, qprep);                                \
+        hipLaunchKernelGGL(tq_attention_kernel<G>, grid, dim3(64 * kWaves), 0, stream->stream, qprep, \
+                           (int)num_heads, (int)nkv, (int)cache->max_seq_len, (int)seq_len, seq_lens, \
+                           attn_scale, t->k_codebook, t->v_codebook, cache->k_codes, cache->v_codes,  \
+                           cache->k_scales, cache->v_scales, cache->k_r_norms, (int)split_len, po, pm, \
+                           pl);                                                                       \
+    } while (0)
     if (gqa == 4) IMH_TQ_LAUNCH(4);
     else if (gqa == 2) IMH_TQ_LAUNCH(2);
     else IMH_TQ_LAUNCH(1);
