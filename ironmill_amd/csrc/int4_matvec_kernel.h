@@ -52,6 +52,8 @@
 
 #include <algorithm>
 
+#include "dpp_reduce.h"
+
 namespace imh_int4 {
 
 typedef _Float16 half8_t __attribute__((ext_vector_type(8)));
@@ -127,16 +129,7 @@ __device__ __forceinline__ void chunk_operands(const float v[8], half8_t &hi, ha
     }
 }
 
-// Sum over each DPP row (16 consecutive lanes), the total in every lane of the
-// row: quad butterflies (quad_perm [1,0,3,2], [2,3,0,1]) then row rotations
-// by 4 and 8.  Lane 0 of a row always adds in the same order.
-__device__ __forceinline__ float row16_sum(float v) {
-    v += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), 0xB1, 0xF, 0xF, false));
-    v += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), 0x4E, 0xF, 0xF, false));
-    v += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), 0x124, 0xF, 0xF, false));
-    v += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), 0x128, 0xF, 0xF, false));
-    return v;
-}
+using imh_dpp::row16_sum;
 
 // v / w to within ~2 ulp (hardware reciprocal, then a multiply); the operand
 // keeps ~22 bits, so the difference from a correctly rounded quotient is far

@@ -26,6 +26,7 @@
 #include <cmath>
 #include <string>
 
+#include "dpp_reduce.h"
 #include "imh_internal.h"
 
 namespace {
@@ -143,6 +144,10 @@ __global__ void __launch_bounds__(kD) tq_query_prep_kernel(const __half *__restr
     __shared__ float qs[GQA][kD];
     const int d = threadIdx.x;
     const int kvh = blockIdx.x, b = blockIdx.y;
+    // column d of S^T, all loads in flight before anything waits
+    float sv[kD];
+#pragma unroll
+    for (int k = 0; k < kD; k++) sv[k] = qjl_t[(size_t)k * kD + d];
     const float sg = signs[d];
 #pragma unroll
     for (int hh = 0; hh < GQA; hh++) qs[hh][d] = __half2float(q[((size_t)b * nh + kvh * GQA + hh) * kD + d]) * sg;
@@ -166,10 +171,10 @@ __global__ void __launch_bounds__(kD) tq_query_prep_kernel(const __half *__restr
     float acc[GQA];
 #pragma unroll
     for (int hh = 0; hh < GQA; hh++) acc[hh] = 0.0f;
-    for (int k = 0; k < kD; k++) {
-        const float s = qjl_t[(size_t)k * kD + d];
 #pragma unroll
-        for (int hh = 0; hh < GQA; hh++) acc[hh] = __builtin_fmaf(s, qs[hh][k], acc[hh]);
+    for (int k = 0; k < kD; k++) {
+#pragma unroll
+        for (int hh = 0; hh < GQA; hh++) acc[hh] = __builtin_fmaf(sv[k], qs[hh][k], acc[hh]);
     }
 #pragma unroll
     for (int hh = 0; hh < GQA; hh++) {
@@ -182,8 +187,6 @@ __global__ void __launch_bounds__(kD) tq_query_prep_kernel(const __half *__restr
 // Attention: grid (num_splits, num_kv_heads, batch), block 64 * kWaves.  Each
 // wave walks its split in 16-position chunks; the codes and per-position
 // scales of the next chunk are loaded before the current one is computed.
-__device__ __forceinline__ float shfl_xor16(float v, int m) { return __shfl_xor(v, m, 16); }
-
 template <int GQA>
 __global__ void __launch_bounds__(64 * kWaves) tq_attention_kernel(
     const float *__restrict__ qprep, int nh, int nkv, int max_seq, int seq_len,
@@ -326,22 +329,13 @@ __global__ void __launch_bounds__(64 * kWaves) tq_attention_kernel(
         bool rescale = false;
 #pragma unroll
         for (int hh = 0; hh < GQA; hh++) {
-            float sc = valid ? attn_scale * (d1[hh] * c.ksc + d2[hh] * qw) : -INFINITY;
-            float cm = sc;
-            cm = fmaxf(cm, shfl_xor16(cm, 8));
-            cm = fmaxf(cm, shfl_xor16(cm, 4));
-            cm = fmaxf(cm, shfl_xor16(cm, 2));
-            cm = fmaxf(cm, shfl_xor16(cm, 1));
-            cm = __shfl(cm, 0);
+            // positions of the chunk are lanes 0..15 (one DPP row)
+            const float sc = valid ? attn_scale * (d1[hh] * c.ksc + d2[hh] * qw) : -INFINITY;
+            const float cm = imh_dpp::first_lane(imh_dpp::row16_max(sc));
             const float nm = fmaxf(m_run[hh], cm);
             corr[hh] = __expf(m_run[hh] - nm);
             const float w = __expf(sc - nm);
-            float ws = w;
-            ws += shfl_xor16(ws, 8);
-            ws += shfl_xor16(ws, 4);
-            ws += shfl_xor16(ws, 2);
-            ws += shfl_xor16(ws, 1);
-            ws = __shfl(ws, 0);
+            const float ws = imh_dpp::first_lane(imh_dpp::row16_sum(w));
             l_run[hh] = l_run[hh] * corr[hh] + ws;
             m_run[hh] = nm;
             wgt[hh] = w * c.vsc;
@@ -424,21 +418,49 @@ __global__ void __launch_bounds__(kD) tq_attention_reduce_kernel(
     const float *__restrict__ part_l, const float *__restrict__ signs, int nh, int S,
     __half *__restrict__ out) {
     __shared__ float x[kD];
+    __shared__ float fs[kD];
+    __shared__ float red[kD];
     const int d = threadIdx.x;
     const int h = blockIdx.x, b = blockIdx.y;
     const size_t base = ((size_t)b * nh + h) * S;
-    float M = -INFINITY;
-    for (int s = 0; s < S; s++) M = fmaxf(M, part_m[base + s]);
-    float ov = 0.0f, lv = 0.0f;
-    if (M != -INFINITY) {
-        for (int s = 0; s < S; s++) {
-            const float m = part_m[base + s];
-            if (m == -INFINITY) continue;
-            const float f = __expf(m - M);
-            ov += part_o[(base + s) * kD + d] * f;
-            lv += part_l[base + s] * f;
-        }
+    // M = max over splits (threads stride the splits, then a tree in LDS)
+    float mloc = -INFINITY;
+    for (int s = d; s < S; s += kD) mloc = fmaxf(mloc, part_m[base + s]);
+    red[d] = mloc;
+    __syncthreads();
+    for (int w = kD / 2; w > 0; w >>= 1) {
+        if (d < w) red[d] = fmaxf(red[d], red[d + w]);
+        __syncthreads();
     }
+    const float M = red[0];
+    __syncthreads();
+    // splits in tiles of kD: thread s of a tile forms its weight exp(m_s - M),
+    // then every thread d sums its output dim over the tile in split order
+    float ov = 0.0f, lloc = 0.0f;
+    for (int s0 = 0; s0 < S; s0 += kD) {
+        const int s = s0 + d;
+        float f = 0.0f;
+        if (s < S) {
+            const float m = part_m[base + s];
+            if (m != -INFINITY) {
+                f = __expf(m - M);
+                lloc += part_l[base + s] * f;
+            }
+        }
+        fs[d] = f;
+        __syncthreads();
+        const int n = min(kD, S - s0);
+#pragma unroll 8
+        for (int i = 0; i < n; i++) ov = __builtin_fmaf(part_o[(base + s0 + i) * kD + d], fs[i], ov);
+        __syncthreads();
+    }
+    red[d] = lloc;
+    __syncthreads();
+    for (int w = kD / 2; w > 0; w >>= 1) {
+        if (d < w) red[d] += red[d + w];
+        __syncthreads();
+    }
+    const float lv = red[0];
     const float sg = signs[d];
     x[d] = (ov / fmaxf(lv, 1e-10f)) * sg;
     __syncthreads();
