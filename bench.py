@@ -21,7 +21,9 @@ The JSON line also carries
                   events on its stream, time / K;
   cpu_baseline -- the C oracle's dequantize-then-compute FFN step on the host
                   cores (weights dequantized once outside the timing);
-  details      -- batch 4/8 FFN kernels and TurboQuant attention at 32k.
+  details      -- batch 4/8 FFN kernels, the prefill INT4 GEMM (M = 512 / 2048,
+                  TFLOP/s against the 2.5 PFLOP/s dense f16 MFMA peak) and
+                  TurboQuant attention at 32k.
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--quick]
 """
@@ -40,6 +42,7 @@ REPO = os.path.dirname(os.path.abspath(__file__))
 sys.path.insert(0, REPO)
 
 HBM_PEAK_GBS = 8000.0
+MFMA_F16_PEAK_TFS = 2500.0  # MI355X dense f16/bf16 matrix peak
 H, F = 2560, 9728
 INT4_BYTES_PER_ELEM = 0.5 + 4.0 / 128.0  # codes + f16 scale + f16 zero per 128
 
@@ -275,6 +278,22 @@ def main():
             us = 1e3 * t / args.steps
             details[f"down_kernel_b{bb}"] = {"us": round(us, 2),
                                              "GB/s": round(down_bytes(bb) / (us * 1e-6) / 1e9, 1)}
+        # prefill INT4 GEMM: M tokens through the projection op
+        for mm in (512, 2048):
+            for (kk, nn, wi) in ((H, F, 0), (F, H, 2)):
+                xm = dev.upload(make_x(mm, kk, 11 + mm))
+                ym = dev.empty((mm, nn), np.float16)
+
+                def gm(i, xm=xm, ym=ym, mm=mm, wi=wi):
+                    ops.encode_projection(stream, xm, W[i % reps][wi], ym, mm)
+
+                t = time_loop(dev, stream, gm, max(20, args.steps // 4), 3)
+                us = 1e3 * t / max(20, args.steps // 4)
+                tfs = 2.0 * mm * nn * kk / (us * 1e-6) / 1e12
+                details[f"gemm_m{mm}_k{kk}_n{nn}"] = {"us": round(us, 2), "TFLOP/s": round(tfs, 1),
+                                                      "frac": round(tfs / MFMA_F16_PEAK_TFS, 4)}
+                log(f"prefill GEMM M={mm} K={kk} N={nn}: {us:.1f} us {tfs:.0f} TFLOP/s "
+                    f"({100 * tfs / MFMA_F16_PEAK_TFS:.1f} % of dense f16 MFMA)")
         del W
         stream.sync()
         for bb, layers in ((1, 8), (16, 1)):

@@ -36,9 +36,9 @@ struct imh_buffer {
 };
 
 // Per-stream scratch memory, grown on demand by the host code of an op.
-// Slot 0: activation operand images; slot 1: split partials (matvec, attention);
-// slot 2: arrival counters, zero-filled when allocated and left at zero by
-// every kernel that uses them.
+// Slot 0: INT4 activation operand images; slot 1: attention queries and split
+// partials, the gate output of a prefill gate/up op; slot 2: GEMM split-K
+// partials.
 constexpr int kScratchSlots = 3;
 struct imh_stream {
     imh_device *dev;
@@ -73,7 +73,7 @@ struct imh_tq_tables {
 namespace imh {
 
 // Ensure scratch slot `slot` of the stream holds at least `bytes`; synchronises
-// the stream before replacing a smaller allocation.  Slot 2 is zero-filled.
+// the stream before replacing a smaller allocation.
 int stream_scratch(imh_stream *s, int slot, size_t bytes, void **out);
 
 // Make the stream's device current for the calling thread.

@@ -9,6 +9,7 @@
 #include <string>
 
 #include "imh_internal.h"
+#include "int4_gemm.h"
 #include "int4_matvec_kernel.h"
 
 namespace {
@@ -251,6 +252,32 @@ int launch_image(int nmat, int epi, const Launch &L, const MatPtrs &mp, const Ac
     return IMH_OK;
 }
 
+// Prefill-sized token counts: the residual-norm rows first when asked, then
+// the GEMM (one matrix, or a gate/up pair with its epilogue).  Scratch slot 2
+// holds the GEMM's split-K partials.
+int run_gemm(imh_stream *s, const ActIn &in, int M, const imh_affine_int4_weight *w0,
+             const imh_affine_int4_weight *w1, int epi, uint16_t *out0, uint16_t *out1) {
+    const int N = (int)w0->n, K = (int)w0->k;
+    const int nmat = w1 ? 2 : 1;
+    const int cus = s->dev->props.multiProcessorCount;
+    void *ws = nullptr;
+    const size_t ws_bytes = gemm_workspace_bytes(M, N, K, nmat, cus);
+    int rc = IMH_OK;
+    if (ws_bytes) {
+        rc = imh::stream_scratch(s, 2, ws_bytes, &ws);
+        if (rc) return rc;
+    }
+    const __half *x = in.a;
+    if (in.b) {   // residual + RMSNorm rows, then the projection of the normed rows
+        rc = encode_resnorm_rows(s, in.a, in.b, in.gamma, in.eps, in.residual_out, in.normed_out, M, K);
+        if (rc) return rc;
+        x = in.normed_out;
+    }
+    const int ge = epi == EPI_SILU ? 2 : epi == EPI_GELU ? 3 : 0;
+    return encode_gemm(s, x, M, w0, w1, ge, reinterpret_cast<__half *>(out0), reinterpret_cast<__half *>(out1),
+                       ws);
+}
+
 // Validates the weights and runs the op: x (plain) or the residual-norm
 // inputs (in.b != NULL) -> out0 [, out1].
 int run_op(imh_stream *s, ActIn in, uint32_t B, const imh_affine_int4_weight *w0,
@@ -284,6 +311,7 @@ int run_op(imh_stream *s, ActIn in, uint32_t B, const imh_affine_int4_weight *w0
     const bool rn = in.b != nullptr;
     const int nmat = w1 ? 2 : 1;
     const int N = (int)w0->n, K = (int)w0->k;
+    if ((int)B >= kGemmMinTokens) return run_gemm(s, in, (int)B, w0, w1, epi, out0, out1);
     Plan p;
     rc = plan_launch(s, nmat, rn, N, K, (int)B, who, p);
     if (rc) return rc;

@@ -49,10 +49,6 @@ int stream_scratch(imh_stream *s, int slot, size_t bytes, void **out) {
         size_t want = bytes < (1u << 20) ? (1u << 20) : bytes;
         IMH_HIP(hipMalloc(&s->scratch[slot], want));
         s->scratch_bytes[slot] = want;
-        if (slot == 2) {
-            IMH_HIP(hipMemset(s->scratch[slot], 0, want));
-            IMH_HIP(hipDeviceSynchronize());
-        }
     }
     *out = s->scratch[slot];
     return IMH_OK;
