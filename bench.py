@@ -63,6 +63,10 @@ def tq_bytes(b, ctx, nkv=8, nh=32, d=128):
     return b * (nkv * ctx * (2 * d + 12) + 2 * nh * d * 2)
 
 
+def fp16_kv_bytes(b, ctx, nkv=8, nh=32, d=128):
+    return b * (nkv * ctx * 2 * d * 2 + 2 * nh * d * 2)
+
+
 def make_weights(seed):
     from ironmill_amd import quant
     rng = np.random.default_rng(seed)
@@ -160,6 +164,34 @@ def bench_attention(dev, stream, ops, batch, ctx, steps, warmup, layers):
     gbs = tq_bytes(batch, ctx) / (ms * 1e-3) / 1e9
     return {"batch": batch, "ctx": ctx, "us": round(ms * 1e3, 2), "GB/s": round(gbs, 1),
             "frac": round(gbs / HBM_PEAK_GBS, 4), "bytes": tq_bytes(batch, ctx)}
+
+
+def bench_fp16_attention(dev, stream, ops, batch, ctx, steps, warmup, layers):
+    """FP16-KV decode attention (fused_sdpa / FlashDecoding) over `layers` distinct caches."""
+    nkv, nh, d = 8, 32, 128
+    rng = np.random.default_rng(ctx + batch + 1)
+    caches = []
+    chunk = 4096
+    for _ in range(layers):
+        c = ops.Fp16KvCache(dev, batch, nkv, d, ctx)
+        for p0 in range(0, ctx, chunk):
+            t = min(chunk, ctx - p0)
+            kd = dev.upload(rng.standard_normal((batch, t, nkv, d)).astype(np.float16))
+            ops.encode_kv_scatter(stream, c, kd, t, p0, True)
+            ops.encode_kv_scatter(stream, c, kd, t, p0, False)
+            stream.sync()
+        caches.append(c)
+    q = dev.upload(rng.standard_normal((batch, nh, d)).astype(np.float16))
+    out = dev.empty((batch, nh, d), np.float16)
+
+    def step(i):
+        ops.encode_fp16_attention(stream, caches[i % layers], q, nh, ctx, out, attn_scale=1.0 / math.sqrt(d))
+
+    ms = time_loop(dev, stream, step, steps, warmup) / steps
+    nbytes = fp16_kv_bytes(batch, ctx)
+    gbs = nbytes / (ms * 1e-3) / 1e9
+    return {"batch": batch, "ctx": ctx, "us": round(ms * 1e3, 2), "GB/s": round(gbs, 1),
+            "frac": round(gbs / HBM_PEAK_GBS, 4), "bytes": nbytes}
 
 
 def main():
@@ -300,6 +332,10 @@ def main():
             r = bench_attention(dev, stream, ops, bb, 32768, max(20, args.steps // 4), 5, layers)
             details[f"tq_attention_b{bb}_ctx32k"] = r
             log(f"TQ attention B={bb} ctx=32k: {r['us']} us {r['GB/s']} GB/s")
+        for bb, layers in ((1, 8), (16, 1)):
+            r = bench_fp16_attention(dev, stream, ops, bb, 32768, max(20, args.steps // 4), 5, layers)
+            details[f"fp16_attention_b{bb}_ctx32k"] = r
+            log(f"FP16-KV attention B={bb} ctx=32k: {r['us']} us {r['GB/s']} GB/s")
         log(json.dumps(details))
 
     cpu = None

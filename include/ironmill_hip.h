@@ -258,6 +258,54 @@ int imh_encode_kv_cache_and_attention(imh_stream *stream, const imh_tq_tables *t
                                       uint32_t num_heads, uint32_t seq_pos, float attn_scale,
                                       uint16_t *out);
 
+/* One layer of the FP16 KV cache (fp16_kv_cache.layer_caches, attention.rs:492-496)
+ * for `batch` sequences: k, v [batch][num_kv_heads][max_seq_len][head_dim] f16,
+ * 16-byte aligned.  The kernels are built for head_dim 128 (IMH_EUNSUPPORTED
+ * otherwise). */
+typedef struct {
+    uint16_t *k;
+    uint16_t *v;
+    uint32_t batch;
+    uint32_t num_kv_heads;
+    uint32_t head_dim;
+    uint32_t max_seq_len;
+} imh_fp16_kv_cache;
+
+/* encode_kv_scatter (ops/kv.rs:35-58, kv_scatter.metal:20-45) for the K
+ * (is_k = 1) or V (is_k = 0) array: proj [batch][token_count][num_kv_heads][head_dim]
+ * f16; token t of sequence b goes to position
+ * ((positions ? positions[b] : base_pos) + t) % max_seq_len (the ring-buffer
+ * wrap of kv_scatter.metal:36-39).  positions is a device int32 array [batch]
+ * or NULL. */
+int imh_encode_kv_scatter(imh_stream *stream, const imh_fp16_kv_cache *cache, const uint16_t *proj,
+                          uint32_t token_count, uint32_t base_pos, const int32_t *positions,
+                          int is_k);
+
+/* FP16-KV attention: fused_sdpa (fused_sdpa.metal:52-251, encode_fused_sdpa,
+ * attention_ops.rs:274-306) and its FlashDecoding split + reduce
+ * (flash_decode.metal:25-215, encode_flash_decode, attention_ops.rs:346-417).
+ * q [batch][token_count][num_heads][head_dim] f16; GQA head h reads kv head
+ * h/(num_heads/num_kv_heads); token t of sequence b attends to positions
+ * [0, L_b - token_count + t + 1) with L_b = seq_lens ? seq_lens[b] : seq_len
+ * (the causal limit of fused_sdpa.metal:166-173); out has q's layout.  A row
+ * with no position gives 0.  num_splits = 0 picks the KV split count from the
+ * shape.  seq_len > max_seq_len is IMH_ERANGE; token_count > seq_len (without
+ * seq_lens) is IMH_EINVAL.  The kernel is built for decode (token_count 1);
+ * larger token counts are computed correctly, without prefill tiling. */
+int imh_encode_fp16_attention(imh_stream *stream, const imh_fp16_kv_cache *cache, const uint16_t *q,
+                              uint32_t num_heads, uint32_t token_count, uint32_t seq_len,
+                              const int32_t *seq_lens, float attn_scale, uint16_t *out,
+                              uint32_t num_splits);
+
+/* The FP16 branch of encode_kv_cache_and_attention (attention.rs:491-607):
+ * scatter K and V at seq_pos, then attend over [0, seq_pos + token_count)
+ * causally. */
+int imh_encode_fp16_kv_cache_and_attention(imh_stream *stream, const imh_fp16_kv_cache *cache,
+                                           const uint16_t *k_proj, const uint16_t *v_proj,
+                                           const uint16_t *q, uint32_t num_heads,
+                                           uint32_t token_count, uint32_t seq_pos,
+                                           float attn_scale, uint16_t *out);
+
 #ifdef __cplusplus
 }
 #endif

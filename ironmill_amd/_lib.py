@@ -96,6 +96,19 @@ class TqKvCache(C.Structure):
     ]
 
 
+class Fp16KvCache(C.Structure):
+    """imh_fp16_kv_cache (one layer of the FP16 KV cache, attention.rs:492-496)."""
+
+    _fields_ = [
+        ("k", C.c_void_p),
+        ("v", C.c_void_p),
+        ("batch", C.c_uint32),
+        ("num_kv_heads", C.c_uint32),
+        ("head_dim", C.c_uint32),
+        ("max_seq_len", C.c_uint32),
+    ]
+
+
 P = C.c_void_p
 U32 = C.c_uint32
 SZ = C.c_size_t
@@ -144,6 +157,10 @@ SIGNATURES = {
                                             U32]),
     "imh_encode_kv_cache_and_attention": (I, [P, P, C.POINTER(TqKvCache), P, P, P, U32, U32, C.c_float,
                                               P]),
+    "imh_encode_kv_scatter": (I, [P, C.POINTER(Fp16KvCache), P, U32, U32, P, I]),
+    "imh_encode_fp16_attention": (I, [P, C.POINTER(Fp16KvCache), P, U32, U32, U32, P, C.c_float, P, U32]),
+    "imh_encode_fp16_kv_cache_and_attention": (I, [P, C.POINTER(Fp16KvCache), P, P, P, U32, U32, U32,
+                                                   C.c_float, P]),
 }
 
 

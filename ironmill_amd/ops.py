@@ -192,9 +192,59 @@ def encode_kv_cache_and_attention(stream: Stream, tq: TurboQuantModel, cache: Tu
                                                 seq_pos, attn_scale, _ptr(out)))
 
 
+class Fp16KvCache:
+    """One layer of the FP16 KV cache (attention.rs:492-496) for `batch` sequences:
+    k, v [batch, num_kv_heads, max_seq_len, head_dim] f16."""
+
+    def __init__(self, dev: Device, batch: int, num_kv_heads: int, head_dim: int, max_seq_len: int):
+        self.batch, self.num_kv_heads, self.head_dim, self.max_seq_len = (
+            batch, num_kv_heads, head_dim, max_seq_len)
+        shp = (batch, num_kv_heads, max_seq_len, head_dim)
+        self.k = dev.empty(shp, np.float16)
+        self.v = dev.empty(shp, np.float16)
+        self._c = _lib.Fp16KvCache(self.k.ptr, self.v.ptr, batch, num_kv_heads, head_dim, max_seq_len)
+
+    @property
+    def c(self):
+        return self._c
+
+    def zero(self, stream: Stream):
+        stream.zero(self.k)
+        stream.zero(self.v)
+
+
+def encode_kv_scatter(stream: Stream, cache: Fp16KvCache, proj, token_count: int, base_pos: int,
+                      is_k: bool, positions=None):
+    """encode_kv_scatter (ops/kv.rs:35-58) into the K or V array."""
+    check(lib.imh_encode_kv_scatter(stream.handle, C.byref(cache.c), _ptr(proj), token_count, base_pos,
+                                    _ptr(positions), int(bool(is_k))))
+
+
+def encode_fp16_attention(stream: Stream, cache: Fp16KvCache, q, num_heads: int, seq_len: int, out,
+                          token_count: int = 1, attn_scale: float | None = None, seq_lens=None,
+                          num_splits: int = 0):
+    """fused_sdpa / FlashDecoding split + reduce (attention_ops.rs:274-417)."""
+    if attn_scale is None:
+        attn_scale = 1.0 / math.sqrt(cache.head_dim)
+    check(lib.imh_encode_fp16_attention(stream.handle, C.byref(cache.c), _ptr(q), num_heads, token_count,
+                                        seq_len, _ptr(seq_lens), attn_scale, _ptr(out), num_splits))
+
+
+def encode_fp16_kv_cache_and_attention(stream: Stream, cache: Fp16KvCache, k_proj, v_proj, q,
+                                       num_heads: int, seq_pos: int, out, token_count: int = 1,
+                                       attn_scale: float | None = None):
+    """The FP16 branch of encode_kv_cache_and_attention (attention.rs:491-607)."""
+    if attn_scale is None:
+        attn_scale = 1.0 / math.sqrt(cache.head_dim)
+    check(lib.imh_encode_fp16_kv_cache_and_attention(stream.handle, C.byref(cache.c), _ptr(k_proj),
+                                                     _ptr(v_proj), _ptr(q), num_heads, token_count,
+                                                     seq_pos, attn_scale, _ptr(out)))
+
+
 __all__ = [
     "AffineQuantizedWeight", "encode_projection", "encode_batched_affine_matvec_int4",
     "encode_fused_ffn_gate_up_act_int4", "encode_fused_residual_norm_affine_matvec_int4",
     "TurboQuantModel", "TurboQuantKvCache", "encode_turboquant_cache_write",
-    "encode_turboquant_attention", "encode_kv_cache_and_attention", "_lib",
+    "encode_turboquant_attention", "encode_kv_cache_and_attention", "Fp16KvCache", "encode_kv_scatter",
+    "encode_fp16_attention", "encode_fp16_kv_cache_and_attention", "_lib",
 ]

@@ -156,6 +156,18 @@ void orc_tq_attention(const uint16_t *q, int batch, int nh, int nkv, int d,
                       const float *k_scales, const float *v_scales,
                       const float *k_r_norms, float *out, int nthreads);
 
+/* FP16-KV attention (metal/inference.rs:222-280 cpu_attention, the semantics
+ * of fused_sdpa.metal:52-251 and flash_decode.metal:25-215) in f64: q
+ * [batch][T][nh][d]; token t of sequence b attends to p < seq_len(b) - T + t + 1;
+ * softmax(attn_scale * q . k) . v; caches [batch][nkv][max_seq][d] f16; out f32
+ * [batch][T][nh][d].  Pinned by closed forms (one position -> its V; identical
+ * keys -> mean of V; a dominant score selects its V; the causal rows of a
+ * prefill equal decode steps at growing lengths) and equality with a float64
+ * numpy softmax on small cases. */
+void orc_fp16_attention(const uint16_t *q, int batch, int token_count, int nh, int nkv, int d,
+                        int max_seq, int seq_len, const int32_t *seq_lens, float attn_scale,
+                        const uint16_t *k_cache, const uint16_t *v_cache, float *out, int nthreads);
+
 #ifdef __cplusplus
 }
 #endif

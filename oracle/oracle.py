@@ -67,6 +67,8 @@ def _declare(L):
         "orc_tq_quantize_vector": (None, [P, C.c_int, C.c_int, P, P, P, C.c_int, P, P, P, P]),
         "orc_tq_cache_write": (None, [P, C.c_int, C.c_int, C.c_int, C.c_int, C.c_int, C.c_int, P,
                                       C.c_int, P, P, P, C.c_int, P, P, P, P]),
+        "orc_fp16_attention": (None, [P, C.c_int, C.c_int, C.c_int, C.c_int, C.c_int, C.c_int,
+                                      C.c_int, P, C.c_float, P, P, P, C.c_int]),
         "orc_tq_attention": (None, [P, C.c_int, C.c_int, C.c_int, C.c_int, C.c_int, C.c_int, P,
                                     C.c_float, P, P, P, P, P, P, P, P, P, P, C.c_int]),
     }
@@ -314,3 +316,21 @@ def tq_attention(q16, tables: TQTables, k_cache, v_cache, k_scales, v_scales, k_
                            _p(_c(k_scales, np.float32)), _p(_c(v_scales, np.float32)),
                            _p(_c(k_r_norms, np.float32)), _p(out), nthreads)
     return out
+
+
+def fp16_attention(q16, k_cache16, v_cache16, seq_len, attn_scale, seq_lens=None, nthreads=1):
+    """q16: [B, nh, d] (one token) or [B, T, nh, d]; caches [B, nkv, max_seq, d]
+    f16 -> f32 of q's shape.  Token t attends to p < seq_len - T + t + 1."""
+    q = _c(q16, np.float16).view(np.uint16)
+    squeeze = q.ndim == 3
+    if squeeze:
+        q = q[:, None]
+    k = _c(k_cache16, np.float16).view(np.uint16)
+    v = _c(v_cache16, np.float16).view(np.uint16)
+    b, t, nh, d = q.shape
+    nkv, max_seq = k.shape[1], k.shape[2]
+    out = np.zeros((b, t, nh, d), np.float32)
+    sl = None if seq_lens is None else _c(seq_lens, np.int32)
+    lib().orc_fp16_attention(_p(_c(q, np.uint16)), b, t, nh, nkv, d, max_seq, seq_len, _p(sl), attn_scale,
+                             _p(k), _p(v), _p(out), nthreads)
+    return out[:, 0] if squeeze else out

@@ -350,3 +350,57 @@ void orc_tq_attention(const uint16_t *q, int batch, int nh, int nkv, int d, int 
     }
     (void)nthreads;
 }
+
+/* FP16-KV attention (metal/inference.rs:222-280 cpu_attention, the semantics
+ * of fused_sdpa.metal:52-251 / flash_decode.metal:25-215), in f64.  q is
+ * [batch][T][nh][d] for T = token_count query tokens per sequence; token t of
+ * sequence b attends causally to p < seq_len(b) - T + t + 1 (inference.rs:241,
+ * fused_sdpa.metal:166-173); kv head = h / (nh/nkv); score_p = attn_scale *
+ * q . k_p; o = sum_p w_p v_p / sum_p w_p.  Caches are [batch][nkv][max_seq][d]
+ * f16; out is f32 [batch][T][nh][d]; a row with no position gives 0. */
+void orc_fp16_attention(const uint16_t *q, int batch, int token_count, int nh, int nkv, int d,
+                        int max_seq, int seq_len, const int32_t *seq_lens, float attn_scale,
+                        const uint16_t *k_cache, const uint16_t *v_cache, float *out, int nthreads) {
+    int group = nh / nkv;
+    int T = token_count;
+    long total = (long)batch * T * nh;
+#ifdef _OPENMP
+    int nt = nthreads > 0 ? nthreads : 1;
+#pragma omp parallel for num_threads(nt) schedule(dynamic)
+#endif
+    for (long row = 0; row < total; row++) {
+        int b = (int)(row / ((long)T * nh));
+        int t = (int)((row / nh) % T);
+        int h = (int)(row % nh);
+        int kvh = h / group;
+        int L = seq_lens ? seq_lens[b] : seq_len;
+        if (L > max_seq) L = max_seq;
+        L = L - T + t + 1;
+        if (L < 0) L = 0;
+        double qv[1024], o[1024];
+        for (int i = 0; i < d; i++) {
+            qv[i] = orc_f16_to_f32(q[(size_t)row * d + i]);
+            o[i] = 0.0;
+        }
+        size_t base = ((size_t)b * nkv + kvh) * (size_t)max_seq;
+        double *sc = (double *)malloc(sizeof(double) * (L > 0 ? L : 1));
+        double mx = -INFINITY;
+        for (int p = 0; p < L; p++) {
+            const uint16_t *kp = k_cache + (base + p) * (size_t)d;
+            double acc = 0.0;
+            for (int i = 0; i < d; i++) acc += qv[i] * (double)orc_f16_to_f32(kp[i]);
+            sc[p] = (double)attn_scale * acc;
+            if (sc[p] > mx) mx = sc[p];
+        }
+        double den = 0.0;
+        for (int p = 0; p < L; p++) {
+            double wgt = exp(sc[p] - mx);
+            den += wgt;
+            const uint16_t *vp = v_cache + (base + p) * (size_t)d;
+            for (int i = 0; i < d; i++) o[i] += wgt * (double)orc_f16_to_f32(vp[i]);
+        }
+        free(sc);
+        for (int i = 0; i < d; i++) out[(size_t)row * d + i] = L > 0 ? (float)(o[i] / den) : 0.0f;
+    }
+    (void)nthreads;
+}

@@ -425,3 +425,75 @@ def test_tq_attention_matches_float_attention_on_dequantized_cache(tabs):
     w = np.exp(s - s.max())
     exact = (w / w.sum()) @ vf
     assert np.linalg.norm(out[0, 0] - exact) / np.linalg.norm(exact) < 0.1
+
+
+# ---- FP16-KV attention (cpu_attention, metal/inference.rs:222-280) ----
+
+def _fp16_cache(rng, batch, nkv, max_seq, scale=1.0):
+    k = (rng.standard_normal((batch, nkv, max_seq, 128)) * scale).astype(np.float16)
+    v = rng.standard_normal((batch, nkv, max_seq, 128)).astype(np.float16)
+    return k, v
+
+
+def test_fp16_attention_single_position_returns_value():
+    rng = np.random.default_rng(31)
+    k, v = _fp16_cache(rng, 2, 2, 8)
+    q = rng.standard_normal((2, 4, 128)).astype(np.float16)
+    out = O.fp16_attention(q, k, v, 1, 0.3)
+    for h in range(4):
+        assert np.array_equal(out[:, h], v[:, h // 2, 0].astype(np.float32))
+
+
+def test_fp16_attention_identical_keys_average_values():
+    rng = np.random.default_rng(32)
+    k, v = _fp16_cache(rng, 1, 1, 64)
+    k[:] = k[:, :, :1]
+    q = rng.standard_normal((1, 1, 128)).astype(np.float16)
+    out = O.fp16_attention(q, k, v, 50, 1 / math.sqrt(128))
+    assert np.allclose(out[0, 0], v[0, 0, :50].astype(np.float64).mean(0), atol=1e-6)
+
+
+def test_fp16_attention_dominant_score_selects_value():
+    rng = np.random.default_rng(33)
+    k, v = _fp16_cache(rng, 1, 1, 64, scale=0.01)
+    kvec = rng.standard_normal(128)
+    k[0, 0, 17] = (kvec / np.linalg.norm(kvec) * 4).astype(np.float16)
+    q = (k[0, 0, 17].astype(np.float32) * 8).astype(np.float16)[None, None, :]
+    out = O.fp16_attention(q, k, v, 40, 1.0)
+    assert np.allclose(out[0, 0], v[0, 0, 17].astype(np.float32), atol=1e-6)
+
+
+def test_fp16_attention_matches_scipy_softmax():
+    """Small case against scipy.special.softmax (a library routine, not this oracle's loop)."""
+    from scipy.special import softmax
+    rng = np.random.default_rng(34)
+    k, v = _fp16_cache(rng, 2, 2, 48)
+    q = rng.standard_normal((2, 8, 128)).astype(np.float16)
+    lens = np.array([48, 5], np.int32)
+    out = O.fp16_attention(q, k, v, 0, 0.125, seq_lens=lens)
+    for b in range(2):
+        for h in range(8):
+            kk = k[b, h // 4, :lens[b]].astype(np.float64)
+            w = softmax(0.125 * (kk @ q[b, h].astype(np.float64)))
+            assert np.allclose(out[b, h], w @ v[b, h // 4, :lens[b]].astype(np.float64), atol=1e-6)
+
+
+def test_fp16_attention_prefill_rows_are_decode_steps():
+    """Causal prefill: token t of T equals a decode step at length seq_len - T + t + 1."""
+    rng = np.random.default_rng(35)
+    k, v = _fp16_cache(rng, 1, 2, 40)
+    T, L = 5, 30
+    q = rng.standard_normal((1, T, 4, 128)).astype(np.float16)
+    pre = O.fp16_attention(q, k, v, L, 0.09)
+    for t in range(T):
+        dec = O.fp16_attention(q[:, t], k, v, L - T + t + 1, 0.09)
+        assert np.array_equal(pre[:, t], dec)
+
+
+def test_fp16_attention_empty_rows_are_zero():
+    rng = np.random.default_rng(36)
+    k, v = _fp16_cache(rng, 2, 1, 8)
+    q = rng.standard_normal((2, 3, 2, 128)).astype(np.float16)
+    out = O.fp16_attention(q, k, v, 0, 0.1, seq_lens=np.array([0, 2], np.int32))
+    assert np.all(out[0] == 0)
+    assert np.all(out[1, 0] == 0) and np.any(out[1, 1] != 0)  # limit 2 - 3 + t + 1 = t
