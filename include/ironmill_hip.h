@@ -85,6 +85,10 @@ void *imh_buffer_device_ptr(const imh_buffer *buf);
  * IMH_EINVAL when offset+length exceeds the buffer. */
 int imh_buffer_write(imh_buffer *buf, size_t offset, const void *src, size_t length);
 int imh_buffer_read(const imh_buffer *buf, size_t offset, void *dst, size_t length);
+/* Synchronous copy of device memory the library handed out by pointer (a
+ * decoder's KV cache) to the host (MetalBuffer::read_bytes, buffer.rs:130-158,
+ * for memory without a buffer handle). */
+int imh_copy_to_host(imh_device *dev, void *dst, const void *src, size_t length);
 
 /* CommandQueue / CommandBuffer (command.rs:16-130): one in-order HIP stream
  * at default priority.  imh_stream_sync = commit + wait_until_completed. */
@@ -240,9 +244,11 @@ int imh_encode_turboquant_cache_write(imh_stream *stream, const imh_tq_tables *t
 /* Decode attention over the cache (turboquant_attention, turboquant.metal:202-462,
  * + the split/LSE combine of fused_sdpa_reduce, flash_decode.metal:163-215):
  * q [batch][num_heads][head_dim] f16, GQA head h reads kv head h/(num_heads/num_kv_heads),
- * sequence b attends to positions [0, seq_lens ? seq_lens[b] : seq_len);
- * out [batch][num_heads][head_dim] f16.  num_splits = 0 picks the KV split
- * count from the shape; seq_len > max_seq_len is IMH_ERANGE. */
+ * sequence b attends to positions [0, seq_lens ? min(seq_lens[b], bound) : seq_len)
+ * where, with seq_lens (a device int32 array [batch]), seq_len is the bound
+ * (0 = max_seq_len) the KV splits span; out [batch][num_heads][head_dim] f16.
+ * num_splits = 0 picks the KV split count from the shape; seq_len > max_seq_len
+ * is IMH_ERANGE. */
 int imh_encode_turboquant_attention(imh_stream *stream, const imh_tq_tables *t,
                                     const imh_tq_kv_cache *cache, const uint16_t *q,
                                     uint32_t num_heads, uint32_t seq_len,
@@ -257,6 +263,71 @@ int imh_encode_kv_cache_and_attention(imh_stream *stream, const imh_tq_tables *t
                                       const uint16_t *v_proj, const uint16_t *q,
                                       uint32_t num_heads, uint32_t seq_pos, float attn_scale,
                                       uint16_t *out);
+
+/* ========================= op tier: decode-step glue ========================= */
+
+/* rms_norm (normalization.metal:19-57, encode_rms_norm): per row of
+ * hidden_size, out = f16(x * rms_inv * w), rms_inv = 1/sqrt(mean(x^2) + eps),
+ * f32 arithmetic.  input/output [token_count][hidden_size] f16, weight [hidden_size]. */
+int imh_encode_rms_norm(imh_stream *stream, const uint16_t *input, const uint16_t *weight,
+                        uint16_t *output, uint32_t hidden_size, uint32_t token_count, float eps);
+
+/* fused_residual_rms_norm (fused_residual_norm.metal:33-75,
+ * encode_fused_residual_rms_norm): x = f32(a) + f32(b); residual_output = f16(x);
+ * normed_output = f16(x * rms_inv * w) with x unrounded. */
+int imh_encode_fused_residual_rms_norm(imh_stream *stream, const uint16_t *a, const uint16_t *b,
+                                       const uint16_t *weight, uint16_t *normed_output,
+                                       uint16_t *residual_output, uint32_t hidden_size,
+                                       uint32_t token_count, float eps);
+
+/* residual_add (encode_residual_add, attention.rs:693-700): out = f16(f32(a) + f32(b))
+ * over n elements. */
+int imh_encode_residual_add(imh_stream *stream, const uint16_t *a, const uint16_t *b, uint16_t *out,
+                            size_t n);
+
+/* fused_embedding_norm (fused_embedding_norm.metal:29-73, pipeline.rs:476-489):
+ * x = embedding[id] * embed_scale (0 for id >= vocab_size); raw_output = f16(x);
+ * normed_output = f16(x * rms_inv * norm_weight).  token_ids is a device uint32
+ * array [token_count]; embedding [vocab_size][hidden_size] f16. */
+int imh_encode_fused_embedding_norm(imh_stream *stream, const uint32_t *token_ids,
+                                    const uint16_t *embedding, const uint16_t *norm_weight,
+                                    uint16_t *normed_output, uint16_t *raw_output,
+                                    uint32_t hidden_size, uint32_t token_count, uint32_t vocab_size,
+                                    float eps, float embed_scale);
+
+/* precompute_rope_cache (ironmill-core/src/rope.rs:22-50), on the host: cos/sin
+ * [max_pos][head_dim/2] f16, angle = pos / theta^(2i/rotary_dim) in f64, rounded
+ * once to f16; entries i >= rotary_dim/2 are (1, 0).  rotary_dim 0 = head_dim. */
+int imh_rope_cache_fill(uint32_t head_dim, uint32_t max_pos, double theta, uint32_t rotary_dim,
+                        uint16_t *cos_out, uint16_t *sin_out);
+
+/* QK RMSNorm + RoPE in place (encode_qk_norm_and_rope, attention.rs:26-92).
+ * With q_norm and k_norm: fused_qk_norm_rope (fused_qk_norm_rope.metal:43-124),
+ * RMSNorm over each head then rotation of pairs (d, d + rotary_dim/2),
+ * d < rotary_dim/2.  Without (both NULL): rope (rope.metal), pairs
+ * (d, d + head_dim/2).  q [batch][token_count][num_heads][head_dim],
+ * k [batch][token_count][num_kv_heads][head_dim] f16; token t of sequence b sits
+ * at position (positions ? positions[b] : seq_offset) + t, clamped to the table
+ * (positions: device int32 [batch] or NULL). */
+typedef struct {
+    uint16_t *q;
+    uint16_t *k;
+    const uint16_t *q_norm;    /* [head_dim] or NULL */
+    const uint16_t *k_norm;    /* [head_dim] or NULL */
+    const uint16_t *cos_cache; /* [max_pos][head_dim/2] */
+    const uint16_t *sin_cache;
+    uint32_t num_heads;
+    uint32_t num_kv_heads;
+    uint32_t head_dim;
+    uint32_t rotary_dim;       /* 0 = head_dim */
+    uint32_t max_pos;
+    uint32_t seq_offset;
+    const int32_t *positions;
+    uint32_t batch;
+    uint32_t token_count;
+    float eps;
+} imh_qk_norm_rope_params;
+int imh_encode_qk_norm_rope(imh_stream *stream, const imh_qk_norm_rope_params *p);
 
 /* One layer of the FP16 KV cache (fp16_kv_cache.layer_caches, attention.rs:492-496)
  * for `batch` sequences: k, v [batch][num_kv_heads][max_seq_len][head_dim] f16,
@@ -286,8 +357,9 @@ int imh_encode_kv_scatter(imh_stream *stream, const imh_fp16_kv_cache *cache, co
  * (flash_decode.metal:25-215, encode_flash_decode, attention_ops.rs:346-417).
  * q [batch][token_count][num_heads][head_dim] f16; GQA head h reads kv head
  * h/(num_heads/num_kv_heads); token t of sequence b attends to positions
- * [0, L_b - token_count + t + 1) with L_b = seq_lens ? seq_lens[b] : seq_len
- * (the causal limit of fused_sdpa.metal:166-173); out has q's layout.  A row
+ * [0, L_b - token_count + t + 1) with L_b = seq_lens ? min(seq_lens[b], bound) :
+ * seq_len (the causal limit of fused_sdpa.metal:166-173), the bound being
+ * seq_len, 0 = max_seq_len, when seq_lens is given; out has q's layout.  A row
  * with no position gives 0.  num_splits = 0 picks the KV split count from the
  * shape.  seq_len > max_seq_len is IMH_ERANGE; token_count > seq_len (without
  * seq_lens) is IMH_EINVAL.  The kernel is built for decode (token_count 1);
@@ -305,6 +377,78 @@ int imh_encode_fp16_kv_cache_and_attention(imh_stream *stream, const imh_fp16_kv
                                            const uint16_t *q, uint32_t num_heads,
                                            uint32_t token_count, uint32_t seq_pos,
                                            float attn_scale, uint16_t *out);
+
+/* ===================== decode step (InferenceEngine::decode_step) ===================== */
+
+/* One decode step of a standard pre-norm transformer (MetalInference::decode_step,
+ * metal/engine.rs:178-180 -> run_pipeline_inner, metal/pipeline.rs:228-1313) with
+ * INT4-affine projections (LM head included), QK RMSNorm + RoPE, and a TurboQuant
+ * INT8 or FP16 KV cache, for `batch` sequences of one token each.  The decoder
+ * owns the activations, the RoPE tables (rope_theta, rotary_dim; 0 = head_dim),
+ * the KV caches of every layer and the per-sequence positions, all in device
+ * memory; weights stay caller-owned.  A step reads token_ids (device uint32
+ * [batch]), writes logits (device f16 [batch][vocab_size]) and advances every
+ * position by one on the device, so a captured step replays as the next token
+ * (the caller keeps positions below max_seq_len across replays; the kernels
+ * clamp rather than overrun).  attn_scale 0 = 1/sqrt(head_dim); embed_scale
+ * 0 = 1. */
+#define IMH_KV_TURBOQUANT 0
+#define IMH_KV_FP16 1
+typedef struct imh_decoder imh_decoder;
+typedef struct {
+    uint32_t hidden_size;
+    uint32_t intermediate_size;
+    uint32_t num_layers;
+    uint32_t num_heads;
+    uint32_t num_kv_heads;
+    uint32_t head_dim;
+    uint32_t vocab_size;
+    uint32_t max_seq_len;
+    uint32_t batch;
+    uint32_t rotary_dim;
+    float rms_eps;
+    float attn_scale;
+    float embed_scale;
+    int use_gelu;
+    int kv_cache;       /* IMH_KV_TURBOQUANT or IMH_KV_FP16 */
+    double rope_theta;
+    uint64_t tq_seed;   /* TurboQuant rotation seed (QJL uses seed + 1) */
+} imh_decoder_config;
+
+/* The weights of one layer (LayerWeights of metal/weights.rs) as the schedule
+ * reads them; q_norm/k_norm both NULL selects plain RoPE. */
+typedef struct {
+    const uint16_t *input_norm;      /* [hidden] */
+    const uint16_t *post_attn_norm;  /* [hidden] */
+    const uint16_t *q_norm;          /* [head_dim] or NULL */
+    const uint16_t *k_norm;          /* [head_dim] or NULL */
+    imh_affine_int4_weight q_proj;   /* [num_heads*head_dim][hidden] */
+    imh_affine_int4_weight k_proj;   /* [num_kv_heads*head_dim][hidden] */
+    imh_affine_int4_weight v_proj;
+    imh_affine_int4_weight o_proj;   /* [hidden][num_heads*head_dim] */
+    imh_affine_int4_weight gate_proj;/* [intermediate][hidden] */
+    imh_affine_int4_weight up_proj;
+    imh_affine_int4_weight down_proj;/* [hidden][intermediate] */
+} imh_decoder_layer_weights;
+
+int imh_decoder_create(imh_device *dev, const imh_decoder_config *cfg, imh_decoder **out);
+void imh_decoder_free(imh_decoder *d);
+int imh_decoder_set_layer(imh_decoder *d, uint32_t layer, const imh_decoder_layer_weights *w);
+/* embedding [vocab][hidden] f16, final_norm [hidden], lm_head [vocab][hidden] INT4 */
+int imh_decoder_set_model(imh_decoder *d, const uint16_t *embedding, const uint16_t *final_norm,
+                          const imh_affine_int4_weight *lm_head);
+/* Set every sequence's next write position (host int32 [batch], NULL = 0); synchronises. */
+int imh_decoder_reset(imh_decoder *d, imh_stream *stream, const int32_t *positions);
+/* Encode one step (pipeline.rs:424-1172 for token_count 1).  IMH_ERANGE when a
+ * position has reached max_seq_len (cache.rs:494-504). */
+int imh_decoder_step(imh_decoder *d, imh_stream *stream, const uint32_t *token_ids, uint16_t *logits);
+/* Host mirror of the positions after the encoded steps (host int32 [batch]). */
+int imh_decoder_positions(const imh_decoder *d, int32_t *out);
+/* The KV cache of one layer (a view; the decoder owns the memory). */
+int imh_decoder_kv_cache(const imh_decoder *d, uint32_t layer, imh_tq_kv_cache *tq_out,
+                         imh_fp16_kv_cache *fp16_out);
+/* The TurboQuant tables the decoder created (NULL for an FP16 cache). */
+int imh_decoder_tq_tables(const imh_decoder *d, imh_tq_tables **out);
 
 #ifdef __cplusplus
 }

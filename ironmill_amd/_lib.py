@@ -109,6 +109,74 @@ class Fp16KvCache(C.Structure):
     ]
 
 
+class QkNormRopeParams(C.Structure):
+    """imh_qk_norm_rope_params (QkNormAndRopeParams, metal/attention.rs:12-24)."""
+
+    _fields_ = [
+        ("q", C.c_void_p),
+        ("k", C.c_void_p),
+        ("q_norm", C.c_void_p),
+        ("k_norm", C.c_void_p),
+        ("cos_cache", C.c_void_p),
+        ("sin_cache", C.c_void_p),
+        ("num_heads", C.c_uint32),
+        ("num_kv_heads", C.c_uint32),
+        ("head_dim", C.c_uint32),
+        ("rotary_dim", C.c_uint32),
+        ("max_pos", C.c_uint32),
+        ("seq_offset", C.c_uint32),
+        ("positions", C.c_void_p),
+        ("batch", C.c_uint32),
+        ("token_count", C.c_uint32),
+        ("eps", C.c_float),
+    ]
+
+
+class DecoderConfig(C.Structure):
+    """imh_decoder_config."""
+
+    _fields_ = [
+        ("hidden_size", C.c_uint32),
+        ("intermediate_size", C.c_uint32),
+        ("num_layers", C.c_uint32),
+        ("num_heads", C.c_uint32),
+        ("num_kv_heads", C.c_uint32),
+        ("head_dim", C.c_uint32),
+        ("vocab_size", C.c_uint32),
+        ("max_seq_len", C.c_uint32),
+        ("batch", C.c_uint32),
+        ("rotary_dim", C.c_uint32),
+        ("rms_eps", C.c_float),
+        ("attn_scale", C.c_float),
+        ("embed_scale", C.c_float),
+        ("use_gelu", C.c_int),
+        ("kv_cache", C.c_int),
+        ("rope_theta", C.c_double),
+        ("tq_seed", C.c_uint64),
+    ]
+
+
+class DecoderLayerWeights(C.Structure):
+    """imh_decoder_layer_weights."""
+
+    _fields_ = [
+        ("input_norm", C.c_void_p),
+        ("post_attn_norm", C.c_void_p),
+        ("q_norm", C.c_void_p),
+        ("k_norm", C.c_void_p),
+        ("q_proj", AffineInt4Weight),
+        ("k_proj", AffineInt4Weight),
+        ("v_proj", AffineInt4Weight),
+        ("o_proj", AffineInt4Weight),
+        ("gate_proj", AffineInt4Weight),
+        ("up_proj", AffineInt4Weight),
+        ("down_proj", AffineInt4Weight),
+    ]
+
+
+IMH_KV_TURBOQUANT = 0
+IMH_KV_FP16 = 1
+
 P = C.c_void_p
 U32 = C.c_uint32
 SZ = C.c_size_t
@@ -128,6 +196,7 @@ SIGNATURES = {
     "imh_buffer_device_ptr": (P, [P]),
     "imh_buffer_write": (I, [P, SZ, P, SZ]),
     "imh_buffer_read": (I, [P, SZ, P, SZ]),
+    "imh_copy_to_host": (I, [P, P, P, SZ]),
     "imh_stream_create": (I, [P, C.POINTER(P)]),
     "imh_stream_free": (None, [P]),
     "imh_stream_sync": (I, [P]),
@@ -157,10 +226,25 @@ SIGNATURES = {
                                             U32]),
     "imh_encode_kv_cache_and_attention": (I, [P, P, C.POINTER(TqKvCache), P, P, P, U32, U32, C.c_float,
                                               P]),
+    "imh_encode_rms_norm": (I, [P, P, P, P, U32, U32, C.c_float]),
+    "imh_encode_fused_residual_rms_norm": (I, [P, P, P, P, P, P, U32, U32, C.c_float]),
+    "imh_encode_residual_add": (I, [P, P, P, P, SZ]),
+    "imh_encode_fused_embedding_norm": (I, [P, P, P, P, P, P, U32, U32, U32, C.c_float, C.c_float]),
+    "imh_rope_cache_fill": (I, [U32, U32, C.c_double, U32, P, P]),
+    "imh_encode_qk_norm_rope": (I, [P, C.POINTER(QkNormRopeParams)]),
     "imh_encode_kv_scatter": (I, [P, C.POINTER(Fp16KvCache), P, U32, U32, P, I]),
     "imh_encode_fp16_attention": (I, [P, C.POINTER(Fp16KvCache), P, U32, U32, U32, P, C.c_float, P, U32]),
     "imh_encode_fp16_kv_cache_and_attention": (I, [P, C.POINTER(Fp16KvCache), P, P, P, U32, U32, U32,
                                                    C.c_float, P]),
+    "imh_decoder_create": (I, [P, C.POINTER(DecoderConfig), C.POINTER(P)]),
+    "imh_decoder_free": (None, [P]),
+    "imh_decoder_set_layer": (I, [P, U32, C.POINTER(DecoderLayerWeights)]),
+    "imh_decoder_set_model": (I, [P, P, P, C.POINTER(AffineInt4Weight)]),
+    "imh_decoder_reset": (I, [P, P, P]),
+    "imh_decoder_step": (I, [P, P, P, P]),
+    "imh_decoder_positions": (I, [P, P]),
+    "imh_decoder_kv_cache": (I, [P, U32, C.POINTER(TqKvCache), C.POINTER(Fp16KvCache)]),
+    "imh_decoder_tq_tables": (I, [P, C.POINTER(P)]),
 }
 
 

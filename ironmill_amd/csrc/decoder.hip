@@ -1,0 +1,400 @@
+// decoder.hip -- one decode step of a standard pre-norm transformer over the
+// library's ops: the per-layer schedule of run_pipeline_inner
+// (metal/pipeline.rs:228-1313, layer loop :533-1135) for INT4-affine weights
+// and a TurboQuant INT8 or FP16 KV cache, for `batch` sequences at once.
+//
+// All per-step state lives in device memory: positions[b] (the cache row the
+// step writes) and seq_lens[b] = positions[b] + 1 are read by the kernels and
+// advanced by the step's last kernel.  A step therefore has no host-side
+// arguments that change between tokens, so a caller can capture one step into
+// a HIP graph and replay it once per token (the graph replaces the
+// reference's per-token command-buffer encode).
+//
+// Schedule per layer l (B rows = one token per sequence):
+//   [l == 0] embedding + input RMSNorm          -> hidden, norm_out
+//   Q (unless the previous layer's end fused it), K, V projections of norm_out
+//   QK RMSNorm + RoPE at positions[b]           -> q, k in place
+//   cache write K, V at positions[b]; attention over [0, seq_lens[b]) -> attn_out
+//   O projection                                -> ffn_down
+//   residual + post-attention RMSNorm           -> norm_out, residual
+//   gate/up + SiLU/GELU, down projection        -> act, ffn_down
+//   [l < L-1] residual + next input RMSNorm + next Q projection (one launch)
+//   [l = L-1] residual add                      -> hidden
+// final RMSNorm, LM head -> logits; positions += 1.
+#include <hip/hip_runtime.h>
+
+#include <cmath>
+#include <cstring>
+#include <string>
+#include <vector>
+
+#include "imh_internal.h"
+
+struct imh_decoder {
+    imh_device *dev;
+    imh_decoder_config cfg;
+    std::vector<imh_decoder_layer_weights> layers;
+    std::vector<bool> layer_set;
+    const uint16_t *embedding = nullptr;
+    const uint16_t *final_norm = nullptr;
+    imh_affine_int4_weight lm_head{};
+    bool model_set = false;
+
+    void *arena = nullptr;  // activations, positions, RoPE tables
+    uint16_t *hidden, *residual, *norm_out, *q, *k, *v, *attn_out, *ffn_down, *act;
+    int32_t *positions, *seq_lens;
+    uint16_t *rope_cos, *rope_sin;
+
+    void *kv_arena = nullptr;
+    imh_tq_tables *tq = nullptr;
+    std::vector<imh_tq_kv_cache> tq_caches;
+    std::vector<imh_fp16_kv_cache> fp16_caches;
+
+    std::vector<int32_t> host_positions;  // mirror of positions for range checks
+};
+
+namespace {
+
+__global__ void decoder_advance_kernel(int32_t *positions, int32_t *seq_lens, int batch, int max_seq) {
+    const int b = blockIdx.x * blockDim.x + threadIdx.x;
+    if (b >= batch) return;
+    const int p = positions[b] + 1;
+    positions[b] = p;
+    seq_lens[b] = p + 1 > max_seq ? max_seq : p + 1;
+}
+
+size_t align256(size_t x) { return (x + 255) & ~size_t(255); }
+
+int check_weight(const imh_affine_int4_weight &w, uint32_t n, uint32_t k, const char *name) {
+    if (!w.data || !w.scales || !w.zeros)
+        return imh::fail(IMH_EINVAL, std::string("imh_decoder: ") + name + ": NULL weight array");
+    if (w.n != n || w.k != k)
+        return imh::fail(IMH_EINVAL, std::string("imh_decoder: ") + name + " is " + std::to_string(w.n) + "x" +
+                                         std::to_string(w.k) + ", expected " + std::to_string(n) + "x" +
+                                         std::to_string(k));
+    return IMH_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+int imh_decoder_create(imh_device *dev, const imh_decoder_config *cfg, imh_decoder **out) {
+    const char *who = "imh_decoder_create";
+    if (!dev || !cfg || !out) return imh::fail(IMH_EINVAL, std::string(who) + ": NULL argument");
+    *out = nullptr;
+    const imh_decoder_config &c = *cfg;
+    if (!c.hidden_size || !c.intermediate_size || !c.num_layers || !c.num_heads || !c.num_kv_heads ||
+        !c.head_dim || !c.vocab_size || !c.max_seq_len || !c.batch)
+        return imh::fail(IMH_EINVAL, std::string(who) + ": zero dimension in the config");
+    if (c.num_heads % c.num_kv_heads)
+        return imh::fail(IMH_EINVAL, std::string(who) + ": num_heads must be a multiple of num_kv_heads");
+    if (c.kv_cache != IMH_KV_TURBOQUANT && c.kv_cache != IMH_KV_FP16)
+        return imh::fail(IMH_EINVAL, std::string(who) + ": unknown kv_cache kind");
+    if (c.batch > 65535) return imh::fail(IMH_EINVAL, std::string(who) + ": batch above 65535");
+    int rc = imh::use_device(dev);
+    if (rc) return rc;
+
+    imh_decoder *d = new imh_decoder();
+    d->dev = dev;
+    d->cfg = c;
+    if (d->cfg.attn_scale == 0.0f) d->cfg.attn_scale = 1.0f / std::sqrt((float)c.head_dim);
+    if (d->cfg.embed_scale == 0.0f) d->cfg.embed_scale = 1.0f;
+    d->layers.resize(c.num_layers);
+    d->layer_set.assign(c.num_layers, false);
+    d->host_positions.assign(c.batch, 0);
+
+    const size_t B = c.batch, H = c.hidden_size, F = c.intermediate_size;
+    const size_t qd = (size_t)c.num_heads * c.head_dim, kvd = (size_t)c.num_kv_heads * c.head_dim;
+    const size_t half_dim = c.head_dim / 2;
+    size_t off = 0;
+    auto take = [&](size_t bytes) {
+        const size_t o = off;
+        off += align256(bytes);
+        return o;
+    };
+    const size_t o_hidden = take(B * H * 2), o_res = take(B * H * 2), o_norm = take(B * H * 2);
+    const size_t o_q = take(B * qd * 2), o_k = take(B * kvd * 2), o_v = take(B * kvd * 2);
+    const size_t o_attn = take(B * qd * 2), o_down = take(B * H * 2), o_act = take(B * F * 2);
+    const size_t o_pos = take(B * 4), o_sl = take(B * 4);
+    const size_t o_cos = take((size_t)c.max_seq_len * half_dim * 2), o_sin = take((size_t)c.max_seq_len * half_dim * 2);
+    hipError_t e = hipMalloc(&d->arena, off);
+    if (e != hipSuccess) {
+        delete d;
+        return imh::fail(IMH_ENOMEM, std::string(who) + ": activation arena of " + std::to_string(off) + " bytes");
+    }
+    char *base = static_cast<char *>(d->arena);
+    d->hidden = reinterpret_cast<uint16_t *>(base + o_hidden);
+    d->residual = reinterpret_cast<uint16_t *>(base + o_res);
+    d->norm_out = reinterpret_cast<uint16_t *>(base + o_norm);
+    d->q = reinterpret_cast<uint16_t *>(base + o_q);
+    d->k = reinterpret_cast<uint16_t *>(base + o_k);
+    d->v = reinterpret_cast<uint16_t *>(base + o_v);
+    d->attn_out = reinterpret_cast<uint16_t *>(base + o_attn);
+    d->ffn_down = reinterpret_cast<uint16_t *>(base + o_down);
+    d->act = reinterpret_cast<uint16_t *>(base + o_act);
+    d->positions = reinterpret_cast<int32_t *>(base + o_pos);
+    d->seq_lens = reinterpret_cast<int32_t *>(base + o_sl);
+    d->rope_cos = reinterpret_cast<uint16_t *>(base + o_cos);
+    d->rope_sin = reinterpret_cast<uint16_t *>(base + o_sin);
+
+    auto cleanup = [&](int code) {
+        imh_decoder_free(d);
+        return code;
+    };
+    // RoPE tables (rope.rs:22-50), built on the host once
+    {
+        std::vector<uint16_t> cs((size_t)c.max_seq_len * half_dim), sn(cs.size());
+        rc = imh_rope_cache_fill(c.head_dim, c.max_seq_len, c.rope_theta, c.rotary_dim, cs.data(), sn.data());
+        if (rc) return cleanup(rc);
+        e = hipMemcpy(d->rope_cos, cs.data(), cs.size() * 2, hipMemcpyHostToDevice);
+        if (e == hipSuccess) e = hipMemcpy(d->rope_sin, sn.data(), sn.size() * 2, hipMemcpyHostToDevice);
+        if (e != hipSuccess) return cleanup(imh::hip_fail(e, "imh_decoder_create: RoPE upload"));
+    }
+    e = hipMemset(d->arena, 0, o_cos);
+    if (e != hipSuccess) return cleanup(imh::hip_fail(e, "imh_decoder_create: clear"));
+    {
+        std::vector<int32_t> sl(B, 1);
+        e = hipMemcpy(d->seq_lens, sl.data(), B * 4, hipMemcpyHostToDevice);
+        if (e != hipSuccess) return cleanup(imh::hip_fail(e, "imh_decoder_create: seq_lens"));
+    }
+
+    // KV caches: one allocation for every layer, zeroed
+    const size_t rows = B * c.num_kv_heads * (size_t)c.max_seq_len;
+    size_t per_layer = 0;
+    if (c.kv_cache == IMH_KV_TURBOQUANT) {
+        rc = imh_tq_tables_create(dev, c.head_dim, 8, c.tq_seed, &d->tq);
+        if (rc) return cleanup(rc);
+        per_layer = 2 * align256(rows * c.head_dim) + 3 * align256(rows * 4);
+    } else {
+        per_layer = 2 * align256(rows * c.head_dim * 2);
+    }
+    const size_t kv_bytes = per_layer * c.num_layers;
+    e = hipMalloc(&d->kv_arena, kv_bytes);
+    if (e != hipSuccess)
+        return cleanup(imh::fail(IMH_ENOMEM, std::string(who) + ": KV cache of " + std::to_string(kv_bytes) + " bytes"));
+    e = hipMemset(d->kv_arena, 0, kv_bytes);
+    if (e != hipSuccess) return cleanup(imh::hip_fail(e, "imh_decoder_create: KV clear"));
+    char *kv = static_cast<char *>(d->kv_arena);
+    for (uint32_t l = 0; l < c.num_layers; l++) {
+        char *p = kv + per_layer * l;
+        if (c.kv_cache == IMH_KV_TURBOQUANT) {
+            imh_tq_kv_cache t{};
+            t.k_codes = reinterpret_cast<uint8_t *>(p);
+            p += align256(rows * c.head_dim);
+            t.v_codes = reinterpret_cast<uint8_t *>(p);
+            p += align256(rows * c.head_dim);
+            t.k_scales = reinterpret_cast<float *>(p);
+            p += align256(rows * 4);
+            t.v_scales = reinterpret_cast<float *>(p);
+            p += align256(rows * 4);
+            t.k_r_norms = reinterpret_cast<float *>(p);
+            t.batch = c.batch;
+            t.num_kv_heads = c.num_kv_heads;
+            t.head_dim = c.head_dim;
+            t.max_seq_len = c.max_seq_len;
+            d->tq_caches.push_back(t);
+        } else {
+            imh_fp16_kv_cache f{};
+            f.k = reinterpret_cast<uint16_t *>(p);
+            f.v = reinterpret_cast<uint16_t *>(p + align256(rows * c.head_dim * 2));
+            f.batch = c.batch;
+            f.num_kv_heads = c.num_kv_heads;
+            f.head_dim = c.head_dim;
+            f.max_seq_len = c.max_seq_len;
+            d->fp16_caches.push_back(f);
+        }
+    }
+    *out = d;
+    return IMH_OK;
+}
+
+void imh_decoder_free(imh_decoder *d) {
+    if (!d) return;
+    imh::use_device(d->dev);
+    if (d->arena) (void)hipFree(d->arena);
+    if (d->kv_arena) (void)hipFree(d->kv_arena);
+    if (d->tq) imh_tq_tables_free(d->tq);
+    delete d;
+}
+
+int imh_decoder_set_layer(imh_decoder *d, uint32_t layer, const imh_decoder_layer_weights *w) {
+    if (!d || !w) return imh::fail(IMH_EINVAL, "imh_decoder_set_layer: NULL argument");
+    const imh_decoder_config &c = d->cfg;
+    if (layer >= c.num_layers) return imh::fail(IMH_EINVAL, "imh_decoder_set_layer: layer out of range");
+    if (!w->input_norm || !w->post_attn_norm)
+        return imh::fail(IMH_EINVAL, "imh_decoder_set_layer: NULL norm weight");
+    if (!w->q_norm != !w->k_norm)
+        return imh::fail(IMH_EINVAL, "imh_decoder_set_layer: give both QK-norm weights or none");
+    const uint32_t H = c.hidden_size, F = c.intermediate_size;
+    const uint32_t qd = c.num_heads * c.head_dim, kvd = c.num_kv_heads * c.head_dim;
+    int rc = check_weight(w->q_proj, qd, H, "q_proj");
+    if (!rc) rc = check_weight(w->k_proj, kvd, H, "k_proj");
+    if (!rc) rc = check_weight(w->v_proj, kvd, H, "v_proj");
+    if (!rc) rc = check_weight(w->o_proj, H, qd, "o_proj");
+    if (!rc) rc = check_weight(w->gate_proj, F, H, "gate_proj");
+    if (!rc) rc = check_weight(w->up_proj, F, H, "up_proj");
+    if (!rc) rc = check_weight(w->down_proj, H, F, "down_proj");
+    if (rc) return rc;
+    d->layers[layer] = *w;
+    d->layer_set[layer] = true;
+    return IMH_OK;
+}
+
+int imh_decoder_set_model(imh_decoder *d, const uint16_t *embedding, const uint16_t *final_norm,
+                          const imh_affine_int4_weight *lm_head) {
+    if (!d || !embedding || !final_norm || !lm_head) return imh::fail(IMH_EINVAL, "imh_decoder_set_model: NULL argument");
+    int rc = check_weight(*lm_head, d->cfg.vocab_size, d->cfg.hidden_size, "lm_head");
+    if (rc) return rc;
+    d->embedding = embedding;
+    d->final_norm = final_norm;
+    d->lm_head = *lm_head;
+    d->model_set = true;
+    return IMH_OK;
+}
+
+int imh_decoder_reset(imh_decoder *d, imh_stream *stream, const int32_t *positions) {
+    if (!d || !stream) return imh::fail(IMH_EINVAL, "imh_decoder_reset: NULL argument");
+    if (stream->capturing) return imh::fail(IMH_EINVAL, "imh_decoder_reset: not allowed while capturing");
+    const uint32_t B = d->cfg.batch;
+    std::vector<int32_t> pos(B, 0), sl(B);
+    for (uint32_t b = 0; b < B; b++) {
+        if (positions) pos[b] = positions[b];
+        if (pos[b] < 0 || (uint32_t)pos[b] >= d->cfg.max_seq_len)
+            return imh::fail(IMH_ERANGE, "imh_decoder_reset: position " + std::to_string(pos[b]) +
+                                             " outside the cache of " + std::to_string(d->cfg.max_seq_len));
+        sl[b] = pos[b] + 1;
+    }
+    int rc = imh::use_device(d->dev);
+    if (rc) return rc;
+    IMH_HIP(hipMemcpyAsync(d->positions, pos.data(), B * 4, hipMemcpyHostToDevice, stream->stream));
+    IMH_HIP(hipMemcpyAsync(d->seq_lens, sl.data(), B * 4, hipMemcpyHostToDevice, stream->stream));
+    IMH_HIP(hipStreamSynchronize(stream->stream));
+    d->host_positions = pos;
+    return IMH_OK;
+}
+
+int imh_decoder_step(imh_decoder *d, imh_stream *s, const uint32_t *token_ids, uint16_t *logits) {
+    const char *who = "imh_decoder_step";
+    if (!d || !s || !token_ids || !logits) return imh::fail(IMH_EINVAL, std::string(who) + ": NULL argument");
+    if (!d->model_set) return imh::fail(IMH_EINVAL, std::string(who) + ": model weights not set");
+    for (uint32_t l = 0; l < d->cfg.num_layers; l++)
+        if (!d->layer_set[l])
+            return imh::fail(IMH_EINVAL, std::string(who) + ": layer " + std::to_string(l) + " weights not set");
+    for (int32_t p : d->host_positions)
+        if ((uint32_t)p >= d->cfg.max_seq_len)
+            return imh::fail(IMH_ERANGE, std::string(who) + ": sequence position " + std::to_string(p) +
+                                             " beyond max_seq_len (cache.rs:494-504)");
+    const imh_decoder_config &c = d->cfg;
+    const uint32_t B = c.batch, H = c.hidden_size;
+    int rc = imh::use_device(d->dev);
+    if (rc) return rc;
+#define IMH_TRY(call)            \
+    do {                         \
+        int rc_ = (call);        \
+        if (rc_) return rc_;     \
+    } while (0)
+
+    IMH_TRY(imh_encode_fused_embedding_norm(s, token_ids, d->embedding, d->layers[0].input_norm, d->norm_out,
+                                            d->hidden, H, B, c.vocab_size, c.rms_eps, c.embed_scale));
+    bool q_done = false;
+    for (uint32_t l = 0; l < c.num_layers; l++) {
+        const imh_decoder_layer_weights &w = d->layers[l];
+        if (!q_done) IMH_TRY(imh_encode_affine_projection_int4(s, d->norm_out, B, &w.q_proj, d->q));
+        // K and V read the same activation: one launch when they share the AWQ scales
+        if (w.k_proj.awq_scales == w.v_proj.awq_scales)
+            IMH_TRY(imh_encode_batched_affine_matvec_int4(s, d->norm_out, B, &w.k_proj, d->k, &w.v_proj, d->v));
+        else {
+            IMH_TRY(imh_encode_affine_projection_int4(s, d->norm_out, B, &w.k_proj, d->k));
+            IMH_TRY(imh_encode_affine_projection_int4(s, d->norm_out, B, &w.v_proj, d->v));
+        }
+        imh_qk_norm_rope_params qp{};
+        qp.q = d->q;
+        qp.k = d->k;
+        qp.q_norm = w.q_norm;
+        qp.k_norm = w.k_norm;
+        qp.cos_cache = d->rope_cos;
+        qp.sin_cache = d->rope_sin;
+        qp.num_heads = c.num_heads;
+        qp.num_kv_heads = c.num_kv_heads;
+        qp.head_dim = c.head_dim;
+        qp.rotary_dim = c.rotary_dim;
+        qp.max_pos = c.max_seq_len;
+        qp.positions = d->positions;
+        qp.batch = B;
+        qp.token_count = 1;
+        qp.eps = c.rms_eps;
+        IMH_TRY(imh_encode_qk_norm_rope(s, &qp));
+        if (c.kv_cache == IMH_KV_TURBOQUANT) {
+            const imh_tq_kv_cache *kc = &d->tq_caches[l];
+            IMH_TRY(imh_encode_turboquant_cache_write(s, d->tq, kc, d->k, 1, 0, d->positions, 1));
+            IMH_TRY(imh_encode_turboquant_cache_write(s, d->tq, kc, d->v, 1, 0, d->positions, 0));
+            IMH_TRY(imh_encode_turboquant_attention(s, d->tq, kc, d->q, c.num_heads, 0, d->seq_lens, c.attn_scale,
+                                                    d->attn_out, 0));
+        } else {
+            const imh_fp16_kv_cache *kc = &d->fp16_caches[l];
+            IMH_TRY(imh_encode_kv_scatter(s, kc, d->k, 1, 0, d->positions, 1));
+            IMH_TRY(imh_encode_kv_scatter(s, kc, d->v, 1, 0, d->positions, 0));
+            IMH_TRY(imh_encode_fp16_attention(s, kc, d->q, c.num_heads, 1, 0, d->seq_lens, c.attn_scale, d->attn_out,
+                                              0));
+        }
+        IMH_TRY(imh_encode_affine_projection_int4(s, d->attn_out, B, &w.o_proj, d->ffn_down));
+        IMH_TRY(imh_encode_fused_residual_rms_norm(s, d->hidden, d->ffn_down, w.post_attn_norm, d->norm_out,
+                                                   d->residual, H, B, c.rms_eps));
+        IMH_TRY(imh_encode_fused_ffn_gate_up_act_int4(s, d->norm_out, B, &w.gate_proj, &w.up_proj, d->act,
+                                                      c.use_gelu));
+        IMH_TRY(imh_encode_affine_projection_int4(s, d->act, B, &w.down_proj, d->ffn_down));
+        if (l + 1 < c.num_layers) {
+            const imh_decoder_layer_weights &nw = d->layers[l + 1];
+            imh_fused_residual_norm_params fp{};
+            fp.a = d->residual;
+            fp.b = d->ffn_down;
+            fp.norm_weight = nw.input_norm;
+            fp.residual_output = d->hidden;
+            fp.weight = &nw.q_proj;
+            fp.output = d->q;
+            fp.normed_output = d->norm_out;
+            fp.token_count = B;
+            fp.eps = c.rms_eps;
+            IMH_TRY(imh_encode_fused_residual_norm_affine_matvec_int4(s, &fp));
+            q_done = true;
+        } else {
+            IMH_TRY(imh_encode_residual_add(s, d->residual, d->ffn_down, d->hidden, (size_t)B * H));
+        }
+    }
+    IMH_TRY(imh_encode_rms_norm(s, d->hidden, d->final_norm, d->norm_out, H, B, c.rms_eps));
+    IMH_TRY(imh_encode_affine_projection_int4(s, d->norm_out, B, &d->lm_head, logits));
+#undef IMH_TRY
+    hipLaunchKernelGGL(decoder_advance_kernel, dim3((B + 63) / 64), dim3(64), 0, s->stream, d->positions, d->seq_lens,
+                       (int)B, (int)c.max_seq_len);
+    IMH_HIP(hipGetLastError());
+    for (auto &p : d->host_positions) p++;
+    return IMH_OK;
+}
+
+int imh_decoder_positions(const imh_decoder *d, int32_t *out) {
+    if (!d || !out) return imh::fail(IMH_EINVAL, "imh_decoder_positions: NULL argument");
+    std::memcpy(out, d->host_positions.data(), d->host_positions.size() * 4);
+    return IMH_OK;
+}
+
+int imh_decoder_kv_cache(const imh_decoder *d, uint32_t layer, imh_tq_kv_cache *tq_out, imh_fp16_kv_cache *fp16_out) {
+    if (!d) return imh::fail(IMH_EINVAL, "imh_decoder_kv_cache: NULL decoder");
+    if (layer >= d->cfg.num_layers) return imh::fail(IMH_EINVAL, "imh_decoder_kv_cache: layer out of range");
+    if (d->cfg.kv_cache == IMH_KV_TURBOQUANT) {
+        if (!tq_out) return imh::fail(IMH_EINVAL, "imh_decoder_kv_cache: TurboQuant cache needs tq_out");
+        *tq_out = d->tq_caches[layer];
+    } else {
+        if (!fp16_out) return imh::fail(IMH_EINVAL, "imh_decoder_kv_cache: FP16 cache needs fp16_out");
+        *fp16_out = d->fp16_caches[layer];
+    }
+    return IMH_OK;
+}
+
+int imh_decoder_tq_tables(const imh_decoder *d, imh_tq_tables **out) {
+    if (!d || !out) return imh::fail(IMH_EINVAL, "imh_decoder_tq_tables: NULL argument");
+    *out = d->tq;
+    return IMH_OK;
+}
+
+}  // extern "C"

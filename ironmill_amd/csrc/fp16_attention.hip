@@ -77,7 +77,8 @@ __global__ void __launch_bounds__(64 * kWaves) fp16_attention_kernel(
     const int S = gridDim.x;
     const int t0 = qb * TB;
 
-    int L = seq_lens ? seq_lens[b] : seq_len;
+    // with seq_lens, seq_len is the bound every length is clamped to
+    int L = seq_lens ? min(seq_lens[b], seq_len) : seq_len;
     L = L > max_seq ? max_seq : L;
     // causal limit of row r: positions < L - T + t + 1
     int lim[R];
@@ -357,8 +358,9 @@ int imh_encode_fp16_attention(imh_stream *stream, const imh_fp16_kv_cache *cache
     if (rc) return rc;
 
     // KV split: ~512 workgroups, each split a multiple of one pass of the
-    // workgroup's waves (64 positions); with seq_lens the bound is max_seq_len
-    const uint32_t L = seq_lens ? cache->max_seq_len : seq_len;
+    // workgroup's waves (64 positions); with per-sequence lengths the splits
+    // span the bound (0 = max_seq_len)
+    const uint32_t L = seq_lens && seq_len == 0 ? cache->max_seq_len : seq_len;
     uint32_t want = num_splits;
     if (want == 0) want = (512 + B * nkv * qblocks - 1) / (B * nkv * qblocks);
     const uint32_t max_splits = std::max<uint32_t>(1, (L + kSplitQuantum - 1) / kSplitQuantum);
@@ -380,7 +382,7 @@ int imh_encode_fp16_attention(imh_stream *stream, const imh_fp16_kv_cache *cache
     const __half *vc = reinterpret_cast<const __half *>(cache->v);
 #define IMH_FP16_ATTN(G, TBV)                                                                                      \
     hipLaunchKernelGGL((fp16_attention_kernel<G, TBV>), grid, dim3(64 * kWaves), 0, stream->stream, qh,             \
-                       (int)token_count, (int)num_heads, (int)nkv, (int)cache->max_seq_len, (int)seq_len, seq_lens, \
+                       (int)token_count, (int)num_heads, (int)nkv, (int)cache->max_seq_len, (int)L, seq_lens,        \
                        attn_scale, kc, vc, (int)split_len, po, pm, pl)
     if (gqa == 4) IMH_FP16_ATTN(4, 1);
     else if (gqa == 2 && tb == 1) IMH_FP16_ATTN(2, 1);

@@ -196,6 +196,15 @@ int imh_buffer_read(const imh_buffer *buf, size_t offset, void *dst, size_t leng
     return IMH_OK;
 }
 
+int imh_copy_to_host(imh_device *dev, void *dst, const void *src, size_t length) {
+    if (!dev || ((!dst || !src) && length)) return imh::fail(IMH_EINVAL, "imh_copy_to_host: NULL argument");
+    if (!length) return IMH_OK;
+    int rc = imh::use_device(dev);
+    if (rc) return rc;
+    IMH_HIP(hipMemcpy(dst, src, length, hipMemcpyDeviceToHost));
+    return IMH_OK;
+}
+
 int imh_stream_create(imh_device *dev, imh_stream **out) {
     if (!dev || !out) return imh::fail(IMH_EINVAL, "imh_stream_create: NULL argument");
     *out = nullptr;

@@ -209,7 +209,8 @@ __global__ void __launch_bounds__(64 * kWaves) tq_attention_kernel(
     const int split = blockIdx.x, kvh = blockIdx.y, b = blockIdx.z;
     const int S = gridDim.x;
 
-    int L = seq_lens ? seq_lens[b] : seq_len;
+    // with seq_lens, seq_len is the bound every length is clamped to
+    int L = seq_lens ? min(seq_lens[b], seq_len) : seq_len;
     L = L < 0 ? 0 : (L > max_seq ? max_seq : L);
     const int p_begin = split * split_len;
     const int p_end = min(p_begin + split_len, L);
@@ -544,7 +545,8 @@ int imh_encode_turboquant_attention(imh_stream *stream, const imh_tq_tables *t,
     // KV split: aim for ~512 workgroups (2 per CU, 8 waves) with >= 64
     // positions each; a wave keeps one chunk in flight ahead of the one it
     // computes.
-    const uint32_t L = seq_len;
+    // with per-sequence lengths the splits span the bound (0 = max_seq_len)
+    const uint32_t L = seq_lens && seq_len == 0 ? cache->max_seq_len : seq_len;
     const uint32_t B = cache->batch;
     uint32_t want = num_splits;
     if (want == 0) {
@@ -577,7 +579,7 @@ int imh_encode_turboquant_attention(imh_stream *stream, const imh_tq_tables *t,
         hipLaunchKernelGGL(tq_query_prep_kernel<G>, dim3(nkv, B), dim3(kD), 0, stream->stream, qh,    \
                            (int)num_heads, t->signs, t->qjl_t, qprep);                                \
         hipLaunchKernelGGL(tq_attention_kernel<G>, grid, dim3(64 * kWaves), 0, stream->stream, qprep, \
-                           (int)num_heads, (int)nkv, (int)cache->max_seq_len, (int)seq_len, seq_lens, \
+                           (int)num_heads, (int)nkv, (int)cache->max_seq_len, (int)L, seq_lens, \
                            attn_scale, t->k_codebook, t->v_codebook, cache->k_codes, cache->v_codes,  \
                            cache->k_scales, cache->v_scales, cache->k_r_norms, (int)split_len, po, pm, \
                            pl);                                                                       \

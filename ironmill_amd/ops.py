@@ -14,7 +14,8 @@ import math
 import numpy as np
 
 from . import _lib
-from ._lib import AffineInt4Weight, FusedResidualNormParams, TqKvCache, check, lib
+from ._lib import (AffineInt4Weight, DecoderConfig, DecoderLayerWeights, FusedResidualNormParams, QkNormRopeParams,
+                   TqKvCache, check, lib)
 from .quant import QuantizedInt4
 from .runtime import Buffer, Device, Stream
 
@@ -241,10 +242,143 @@ def encode_fp16_kv_cache_and_attention(stream: Stream, cache: Fp16KvCache, k_pro
                                                      seq_pos, attn_scale, _ptr(out)))
 
 
+# ------------------------------------------------------------ decode-step glue
+
+
+def read_device(dev: Device, ptr: int, shape, dtype) -> np.ndarray:
+    """Copy device memory handed out by pointer (e.g. a decoder's KV cache) to the host."""
+    out = np.empty(shape, dtype)
+    check(lib.imh_copy_to_host(dev.handle, out.ctypes.data_as(C.c_void_p), ptr, out.nbytes))
+    return out
+
+
+def encode_rms_norm(stream: Stream, x, weight, out, hidden_size: int, token_count: int, eps: float):
+    """rms_norm (normalization.metal:19-57)."""
+    check(lib.imh_encode_rms_norm(stream.handle, _ptr(x), _ptr(weight), _ptr(out), hidden_size, token_count, eps))
+
+
+def encode_fused_residual_rms_norm(stream: Stream, a, b, weight, normed_output, residual_output,
+                                   hidden_size: int, token_count: int, eps: float):
+    """fused_residual_rms_norm (fused_residual_norm.metal:33-75)."""
+    check(lib.imh_encode_fused_residual_rms_norm(stream.handle, _ptr(a), _ptr(b), _ptr(weight), _ptr(normed_output),
+                                                 _ptr(residual_output), hidden_size, token_count, eps))
+
+
+def encode_residual_add(stream: Stream, a, b, out, n: int):
+    check(lib.imh_encode_residual_add(stream.handle, _ptr(a), _ptr(b), _ptr(out), n))
+
+
+def encode_fused_embedding_norm(stream: Stream, token_ids, embedding, norm_weight, normed_output, raw_output,
+                                hidden_size: int, token_count: int, vocab_size: int, eps: float,
+                                embed_scale: float = 1.0):
+    """fused_embedding_norm (fused_embedding_norm.metal:29-73)."""
+    check(lib.imh_encode_fused_embedding_norm(stream.handle, _ptr(token_ids), _ptr(embedding), _ptr(norm_weight),
+                                              _ptr(normed_output), _ptr(raw_output), hidden_size, token_count,
+                                              vocab_size, eps, embed_scale))
+
+
+def rope_cache(head_dim: int, max_pos: int, theta: float, rotary_dim: int = 0):
+    """precompute_rope_cache (ironmill-core/src/rope.rs:22-50) -> (cos, sin) f16 [max_pos, head_dim/2]."""
+    cos = np.empty((max_pos, head_dim // 2), np.float16)
+    sin = np.empty_like(cos)
+    check(lib.imh_rope_cache_fill(head_dim, max_pos, theta, rotary_dim, cos.ctypes.data_as(C.c_void_p),
+                                  sin.ctypes.data_as(C.c_void_p)))
+    return cos, sin
+
+
+def encode_qk_norm_rope(stream: Stream, q, k, cos_cache, sin_cache, num_heads: int, num_kv_heads: int,
+                        head_dim: int, max_pos: int, q_norm=None, k_norm=None, rotary_dim: int = 0,
+                        seq_offset: int = 0, positions=None, batch: int = 1, token_count: int = 1,
+                        eps: float = 1e-6):
+    """encode_qk_norm_and_rope (metal/attention.rs:26-92), in place on q and k."""
+    p = QkNormRopeParams(_ptr(q), _ptr(k), _ptr(q_norm), _ptr(k_norm), _ptr(cos_cache), _ptr(sin_cache), num_heads,
+                         num_kv_heads, head_dim, rotary_dim, max_pos, seq_offset, _ptr(positions), batch,
+                         token_count, eps)
+    check(lib.imh_encode_qk_norm_rope(stream.handle, C.byref(p)))
+
+
+class Decoder:
+    """One decode step of a pre-norm transformer over INT4 weights and a TurboQuant
+    or FP16 KV cache (MetalInference::decode_step, metal/engine.rs:178-180 ->
+    run_pipeline_inner, metal/pipeline.rs:228-1313), for `batch` sequences."""
+
+    def __init__(self, dev: Device, *, hidden_size, intermediate_size, num_layers, num_heads, num_kv_heads,
+                 head_dim, vocab_size, max_seq_len, batch=1, rotary_dim=0, rms_eps=1e-6, rope_theta=1e6,
+                 attn_scale=0.0, embed_scale=0.0, use_gelu=False, kv_cache="turboquant", tq_seed=42):
+        self.dev = dev
+        kind = {"turboquant": _lib.IMH_KV_TURBOQUANT, "fp16": _lib.IMH_KV_FP16}[kv_cache]
+        self.kv_kind = kv_cache
+        self.cfg = DecoderConfig(hidden_size, intermediate_size, num_layers, num_heads, num_kv_heads, head_dim,
+                                 vocab_size, max_seq_len, batch, rotary_dim, rms_eps, attn_scale, embed_scale,
+                                 int(bool(use_gelu)), kind, rope_theta, tq_seed)
+        h = C.c_void_p()
+        check(lib.imh_decoder_create(dev.handle, C.byref(self.cfg), C.byref(h)))
+        self._h = h
+        self._keep = {}
+
+    @property
+    def handle(self):
+        return self._h
+
+    def set_layer(self, layer: int, *, input_norm, post_attn_norm, q_proj, k_proj, v_proj, o_proj, gate_proj,
+                  up_proj, down_proj, q_norm=None, k_norm=None):
+        w = DecoderLayerWeights(_ptr(input_norm), _ptr(post_attn_norm), _ptr(q_norm), _ptr(k_norm), q_proj.c,
+                                k_proj.c, v_proj.c, o_proj.c, gate_proj.c, up_proj.c, down_proj.c)
+        check(lib.imh_decoder_set_layer(self._h, layer, C.byref(w)))
+        self._keep[layer] = (input_norm, post_attn_norm, q_norm, k_norm, q_proj, k_proj, v_proj, o_proj,
+                             gate_proj, up_proj, down_proj)
+
+    def set_model(self, embedding, final_norm, lm_head: AffineQuantizedWeight):
+        check(lib.imh_decoder_set_model(self._h, _ptr(embedding), _ptr(final_norm), C.byref(lm_head.c)))
+        self._keep["model"] = (embedding, final_norm, lm_head)
+
+    def reset(self, stream: Stream, positions=None):
+        if positions is not None:
+            pos = np.ascontiguousarray(positions, np.int32)
+            check(lib.imh_decoder_reset(self._h, stream.handle, pos.ctypes.data_as(C.c_void_p)))
+        else:
+            check(lib.imh_decoder_reset(self._h, stream.handle, None))
+
+    def step(self, stream: Stream, token_ids, logits):
+        check(lib.imh_decoder_step(self._h, stream.handle, _ptr(token_ids), _ptr(logits)))
+
+    def positions(self) -> np.ndarray:
+        out = np.empty(self.cfg.batch, np.int32)
+        check(lib.imh_decoder_positions(self._h, out.ctypes.data_as(C.c_void_p)))
+        return out
+
+    def kv_cache(self, layer: int) -> dict:
+        """Host copies of one layer's cache arrays."""
+        c = self.cfg
+        shp = (c.batch, c.num_kv_heads, c.max_seq_len)
+        if self.kv_kind == "turboquant":
+            t = TqKvCache()
+            check(lib.imh_decoder_kv_cache(self._h, layer, C.byref(t), None))
+            return {"k_codes": read_device(self.dev, t.k_codes, shp + (c.head_dim,), np.uint8),
+                    "v_codes": read_device(self.dev, t.v_codes, shp + (c.head_dim,), np.uint8),
+                    "k_scales": read_device(self.dev, t.k_scales, shp, np.float32),
+                    "v_scales": read_device(self.dev, t.v_scales, shp, np.float32),
+                    "k_r_norms": read_device(self.dev, t.k_r_norms, shp, np.float32)}
+        f = _lib.Fp16KvCache()
+        check(lib.imh_decoder_kv_cache(self._h, layer, None, C.byref(f)))
+        return {"k": read_device(self.dev, f.k, shp + (c.head_dim,), np.float16),
+                "v": read_device(self.dev, f.v, shp + (c.head_dim,), np.float16)}
+
+    def close(self):
+        if getattr(self, "_h", None):
+            lib.imh_decoder_free(self._h)
+            self._h = None
+
+    def __del__(self):
+        self.close()
+
+
 __all__ = [
     "AffineQuantizedWeight", "encode_projection", "encode_batched_affine_matvec_int4",
     "encode_fused_ffn_gate_up_act_int4", "encode_fused_residual_norm_affine_matvec_int4",
     "TurboQuantModel", "TurboQuantKvCache", "encode_turboquant_cache_write",
     "encode_turboquant_attention", "encode_kv_cache_and_attention", "Fp16KvCache", "encode_kv_scatter",
-    "encode_fp16_attention", "encode_fp16_kv_cache_and_attention", "_lib",
+    "encode_fp16_attention", "encode_fp16_kv_cache_and_attention", "read_device", "encode_rms_norm",
+    "encode_fused_residual_rms_norm", "encode_residual_add", "encode_fused_embedding_norm", "rope_cache",
+    "encode_qk_norm_rope", "Decoder", "_lib",
 ]

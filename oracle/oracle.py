@@ -334,3 +334,201 @@ def fp16_attention(q16, k_cache16, v_cache16, seq_len, attn_scale, seq_lens=None
     lib().orc_fp16_attention(_p(_c(q, np.uint16)), b, t, nh, nkv, d, max_seq, seq_len, _p(sl), attn_scale,
                              _p(k), _p(v), _p(out), nthreads)
     return out[:, 0] if squeeze else out
+
+
+# ------------------------------------------------------------ decode-step glue
+# numpy restatements in f64 arithmetic with f16 storage at the points where the
+# kernels store f16.
+
+def _f64(x16):
+    return np.asarray(x16, np.float16).astype(np.float64)
+
+
+def rms_norm(x16, w16, eps):
+    """rms_norm (normalization.metal:19-57): f16(x * 1/sqrt(mean(x^2)+eps) * w) per row."""
+    x = _f64(x16)
+    inv = 1.0 / np.sqrt((x * x).mean(axis=-1, keepdims=True) + eps)
+    return (x * inv * _f64(w16)).astype(np.float16)
+
+
+def fused_residual_rms_norm(a16, b16, w16, eps):
+    """fused_residual_rms_norm (fused_residual_norm.metal:33-75) -> (normed, residual)."""
+    x = _f64(a16) + _f64(b16)
+    inv = 1.0 / np.sqrt((x * x).mean(axis=-1, keepdims=True) + eps)
+    return (x * inv * _f64(w16)).astype(np.float16), x.astype(np.float16)
+
+
+def residual_add(a16, b16):
+    return (_f64(a16) + _f64(b16)).astype(np.float16)
+
+
+def fused_embedding_norm(ids, table16, w16, eps, embed_scale=1.0):
+    """fused_embedding_norm (fused_embedding_norm.metal:29-73) -> (normed, raw); ids >= vocab give 0."""
+    ids = np.asarray(ids, np.int64)
+    vocab = table16.shape[0]
+    valid = (ids >= 0) & (ids < vocab)
+    x = np.where(valid[:, None], _f64(table16[np.where(valid, ids, 0)]) * np.float64(np.float32(embed_scale)), 0.0)
+    inv = 1.0 / np.sqrt((x * x).mean(axis=-1, keepdims=True) + eps)
+    return (x * inv * _f64(w16)).astype(np.float16), x.astype(np.float16)
+
+
+def rope_cache(head_dim, max_pos, theta, rotary_dim=None):
+    """precompute_rope_cache (ironmill-core/src/rope.rs:22-50): f16 cos/sin [max_pos, head_dim/2],
+    f64 angles rounded once to f16 (numpy's double -> half cast rounds to nearest even)."""
+    half = head_dim // 2
+    rd = rotary_dim or head_dim
+    i = np.arange(half, dtype=np.float64)
+    freq = 1.0 / np.power(np.float64(theta), 2.0 * i / rd)
+    ang = np.arange(max_pos, dtype=np.float64)[:, None] * freq[None, :]
+    cos, sin = np.cos(ang), np.sin(ang)
+    cos[:, rd // 2:] = 1.0
+    sin[:, rd // 2:] = 0.0
+    return cos.astype(np.float16), sin.astype(np.float16)
+
+
+def qk_norm_rope(x16, norm_w16, cos16, sin16, pos, eps, rotary_dim=None):
+    """One tensor of encode_qk_norm_and_rope (attention.rs:26-92) for rows x16 [..., heads, hd]
+    at integer positions pos (broadcast over heads).  With norm_w16: fused_qk_norm_rope
+    (fused_qk_norm_rope.metal:43-124), pairs (d, d + rotary/2); without: rope.metal, pairs
+    (d, d + hd/2)."""
+    x = _f64(x16)
+    hd = x.shape[-1]
+    pos = np.asarray(pos, np.int64)
+    c = _f64(cos16)[pos][..., None, :]   # [..., 1, hd/2]
+    s = _f64(sin16)[pos][..., None, :]
+    out = x.copy()
+    if norm_w16 is not None:
+        rd = rotary_dim or hd
+        hr = rd // 2
+        inv = 1.0 / np.sqrt((x * x).mean(axis=-1, keepdims=True) + eps)
+        y = x * inv * _f64(norm_w16)
+        lo, hi = y[..., :hr], y[..., hr:rd]
+        out[..., :hr] = lo * c[..., :hr] - hi * s[..., :hr]
+        out[..., hr:rd] = lo * s[..., :hr] + hi * c[..., :hr]
+        out[..., rd:] = y[..., rd:]
+    else:
+        h = hd // 2
+        lo, hi = x[..., :h], x[..., h:]
+        out[..., :h] = lo * c - hi * s
+        out[..., h:] = lo * s + hi * c
+    return out.astype(np.float16)
+
+
+class DecoderReference:
+    """The decode step of run_pipeline_inner (metal/pipeline.rs:424-1172, token_count 1) restated
+    on the CPU over the dequantize-then-compute ops: every projection uses the f16 dense weight
+    of dequant_affine (core/dequant.rs:85-180) with an f32 accumulator; activations are stored
+    as f16 at the same points as the GPU buffers (norm_out, q/k/v, attn_out, ffn_down, residual,
+    hidden); attention runs on the cache as written (FP16 rows, or TurboQuant codes from
+    tq_cache_write).
+
+    layers: list of dicts with input_norm, post_attn_norm, q_norm, k_norm (f16 arrays or None)
+    and q_proj, k_proj, v_proj, o_proj, gate_proj, up_proj, down_proj (objects with data,
+    scales_f32, zeros_f32, awq, n, k)."""
+
+    def __init__(self, cfg: dict, layers, embedding16, final_norm16, lm_head, kv_cache="turboquant",
+                 tq_seed=42):
+        self.cfg = dict(cfg)
+        c = self.cfg
+        self.B = c["batch"]
+        self.nh, self.nkv, self.hd = c["num_heads"], c["num_kv_heads"], c["head_dim"]
+        self.eps = c.get("rms_eps", 1e-6)
+        self.scale = c.get("attn_scale") or 1.0 / np.sqrt(self.hd)
+        self.max_seq = c["max_seq_len"]
+        self.cos, self.sin = rope_cache(self.hd, self.max_seq, c.get("rope_theta", 1e6), c.get("rotary_dim") or None)
+        self.kv = kv_cache
+        self.emb = np.asarray(embedding16, np.float16)
+        self.final_norm = final_norm16
+        self.layers = []
+        for L in layers:
+            d = dict(L)
+            for name in ("q_proj", "k_proj", "v_proj", "o_proj", "gate_proj", "up_proj", "down_proj"):
+                w = L[name]
+                d[name] = (dequant_affine_int4(w.data, w.scales_f32, w.zeros_f32, w.n, w.k), w.awq)
+            self.layers.append(d)
+        self.lm = (dequant_affine_int4(lm_head.data, lm_head.scales_f32, lm_head.zeros_f32, lm_head.n, lm_head.k),
+                   lm_head.awq)
+        shp = (self.B, self.nkv, self.max_seq)
+        if kv_cache == "turboquant":
+            self.tables = TQTables(self.hd, 8, tq_seed)
+            self.caches = [dict(k_codes=np.zeros(shp + (self.hd,), np.uint8),
+                                v_codes=np.zeros(shp + (self.hd,), np.uint8),
+                                k_scales=np.zeros(shp, np.float32), v_scales=np.zeros(shp, np.float32),
+                                k_r_norms=np.zeros(shp, np.float32)) for _ in layers]
+        else:
+            self.caches = [dict(k=np.zeros(shp + (self.hd,), np.float16), v=np.zeros(shp + (self.hd,), np.float16))
+                           for _ in layers]
+        self.positions = np.zeros(self.B, np.int32)
+
+    @staticmethod
+    def _proj(w, x16):
+        dense, awq = w
+        return matvec_f16w(dense, x16, awq, nthreads=8).astype(np.float16)
+
+    def _write_cache(self, l, k16, v16):
+        cache, pos = self.caches[l], self.positions
+        if self.kv == "turboquant":
+            for x, is_k, cn, sn in ((k16, True, "k_codes", "k_scales"), (v16, False, "v_codes", "v_scales")):
+                codes, sc, rn = tq_cache_write(x[:, None], self.tables, is_k, self.max_seq, positions=pos)
+                for b in range(self.B):
+                    p = pos[b] % self.max_seq
+                    cache[cn][b, :, p] = codes[b, :, p]
+                    cache[sn][b, :, p] = sc[b, :, p]
+                    if is_k:
+                        cache["k_r_norms"][b, :, p] = rn[b, :, p]
+        else:
+            for b in range(self.B):
+                p = pos[b] % self.max_seq
+                cache["k"][b, :, p] = k16[b]
+                cache["v"][b, :, p] = v16[b]
+
+    def _attend(self, l, q16):
+        cache = self.caches[l]
+        lens = np.minimum(self.positions + 1, self.max_seq).astype(np.int32)
+        if self.kv == "turboquant":
+            out = tq_attention(q16, self.tables, cache["k_codes"], cache["v_codes"], cache["k_scales"],
+                               cache["v_scales"], cache["k_r_norms"], 0, self.scale, seq_lens=lens, nthreads=8)
+        else:
+            out = fp16_attention(q16, cache["k"], cache["v"], 0, self.scale, seq_lens=lens, nthreads=8)
+        return out.astype(np.float16)
+
+    def step(self, token_ids, cache_hook=None):
+        """One token per sequence -> f32 logits [B, vocab]; advances the positions.
+        cache_hook(layer, cache, positions), if given, runs after each layer's cache write
+        (a test may substitute the rows the GPU wrote there)."""
+        B, nh, nkv, hd, eps = self.B, self.nh, self.nkv, self.hd, self.eps
+        L0 = self.layers[0]
+        normed, hidden = fused_embedding_norm(token_ids, self.emb, L0["input_norm"], eps,
+                                              self.cfg.get("embed_scale") or 1.0)
+        q = None
+        for l, L in enumerate(self.layers):
+            if q is None:
+                q = self._proj(L["q_proj"], normed)
+            k = self._proj(L["k_proj"], normed)
+            v = self._proj(L["v_proj"], normed)
+            pos = self.positions
+            rd = self.cfg.get("rotary_dim") or None
+            q = qk_norm_rope(q.reshape(B, nh, hd), L.get("q_norm"), self.cos, self.sin, pos, eps, rd)
+            k = qk_norm_rope(k.reshape(B, nkv, hd), L.get("k_norm"), self.cos, self.sin, pos, eps, rd)
+            self._write_cache(l, k, v.reshape(B, nkv, hd))
+            if cache_hook is not None:
+                cache_hook(l, self.caches[l], self.positions)
+            attn = self._attend(l, q)
+            o = self._proj(L["o_proj"], attn.reshape(B, nh * hd))
+            normed, residual = fused_residual_rms_norm(hidden, o, L["post_attn_norm"], eps)
+            (gd, gawq), (ud, _) = L["gate_proj"], L["up_proj"]
+            act = gate_up_act(gd, ud, normed, gawq,
+                              act="gelu" if self.cfg.get("use_gelu") else "silu").astype(np.float16)
+            down = self._proj(L["down_proj"], act)
+            if l + 1 < len(self.layers):
+                nL = self.layers[l + 1]
+                qd, qawq = nL["q_proj"]
+                y, hidden, normed = fused_residual_norm_matvec(residual, down, nL["input_norm"], qd, eps, qawq)
+                q = y.astype(np.float16)
+            else:
+                hidden = residual_add(residual, down)
+                q = None
+        normed = rms_norm(hidden, self.final_norm, eps)
+        logits = matvec_f16w(self.lm[0], normed, self.lm[1], nthreads=8)
+        self.positions = self.positions + 1
+        return logits

@@ -1,0 +1,290 @@
+"""GPU parity of the decode-step glue and of the whole decode step.
+
+Glue (against the numpy oracle, which stores f16 where the kernels do):
+* residual add, the residual output of the fused residual norm and the raw
+  output of the embedding lookup: bit for bit (one f32 add or copy, one rounding);
+* RMSNorm outputs and QK-norm + RoPE: within one f16 step of the oracle's f64
+  value rounded to f16 (the kernels sum squares in f32 in another order and may
+  contract a multiply-add).
+
+Decode step (imh_decoder_step, the schedule of pipeline.rs:424-1172) against
+oracle.DecoderReference, the same schedule over the CPU dequantize-then-compute
+ops, for an FP16 and a TurboQuant KV cache, four tokens for two sequences at
+different positions.  Every stored activation is f16 on both sides, so each op
+adds at most the op-level differences the per-op tests bound; over two layers
+the logits stay within rel-L2 <= 1e-3 of the reference.
+With the TurboQuant cache a one-step difference in a K/V projection can move a
+vector across a codebook boundary (free-running, the logits drift to ~5e-3), so
+that test hands the oracle the code rows the GPU wrote at each step (the cache
+write itself is bit-exact on equal inputs in the op tests), bounds the share of
+code bytes that differed by the oracle's own sensitivity to one-step input
+changes, and holds the logits to the same 1e-3.
+"""
+import numpy as np
+import pytest
+
+import oracle as O
+from conftest import assert_close, rel_l2
+from ironmill_amd import IronmillError, ops, quant
+
+pytestmark = pytest.mark.gpu
+
+
+def assert_ulps(got16, ref16, n=1, what=""):
+    got = np.asarray(got16, np.float16).astype(np.float64)
+    ref = np.asarray(ref16, np.float16)
+    err = np.abs(got - ref.astype(np.float64))
+    bound = n * np.spacing(np.abs(ref)).astype(np.float64)
+    worst = float(np.max(err / np.maximum(bound, 1e-30))) if err.size else 0.0
+    assert np.all(err <= bound), f"{what}: worst error {worst:.2f} x {n} f16 step(s)"
+
+
+@pytest.mark.parametrize("hidden,rows", [(2560, 1), (2560, 5), (1000, 3)])  # 1000: scalar path
+def test_rms_norm(dev, stream, hidden, rows):
+    rng = np.random.default_rng(hidden + rows)
+    x = (rng.standard_normal((rows, hidden)) * 3).astype(np.float16)
+    w = rng.uniform(0.5, 1.5, hidden).astype(np.float16)
+    out = dev.empty((rows, hidden), np.float16)
+    ops.encode_rms_norm(stream, dev.upload(x), dev.upload(w), out, hidden, rows, 1e-6)
+    stream.sync()
+    assert_ulps(out.read(), O.rms_norm(x, w, 1e-6), what="rms_norm")
+
+
+@pytest.mark.parametrize("hidden,rows", [(2560, 1), (2560, 8), (1000, 2)])
+def test_fused_residual_rms_norm(dev, stream, hidden, rows):
+    rng = np.random.default_rng(7 * hidden + rows)
+    a = rng.standard_normal((rows, hidden)).astype(np.float16)
+    b = (rng.standard_normal((rows, hidden)) * 0.3).astype(np.float16)
+    w = rng.uniform(0.5, 1.5, hidden).astype(np.float16)
+    normed, res = dev.empty((rows, hidden), np.float16), dev.empty((rows, hidden), np.float16)
+    ops.encode_fused_residual_rms_norm(stream, dev.upload(a), dev.upload(b), dev.upload(w), normed, res, hidden,
+                                       rows, 1e-6)
+    stream.sync()
+    n_ref, r_ref = O.fused_residual_rms_norm(a, b, w, 1e-6)
+    assert np.array_equal(res.read().view(np.uint16), r_ref.view(np.uint16))
+    assert_ulps(normed.read(), n_ref, what="fused residual norm")
+
+
+def test_residual_add(dev, stream):
+    rng = np.random.default_rng(3)
+    a = rng.standard_normal(10000).astype(np.float16)
+    b = rng.standard_normal(10000).astype(np.float16)
+    out = dev.empty((10000,), np.float16)
+    ops.encode_residual_add(stream, dev.upload(a), dev.upload(b), out, 10000)
+    stream.sync()
+    assert np.array_equal(out.read().view(np.uint16), O.residual_add(a, b).view(np.uint16))
+
+
+def test_embedding_norm(dev, stream):
+    rng = np.random.default_rng(4)
+    vocab, hidden = 3000, 2560
+    table = rng.standard_normal((vocab, hidden)).astype(np.float16)
+    w = rng.uniform(0.5, 1.5, hidden).astype(np.float16)
+    ids = np.array([5, 2999, 3000, 0, 123456], np.uint32)   # 3000, 123456: out of range -> 0
+    normed, raw = dev.empty((5, hidden), np.float16), dev.empty((5, hidden), np.float16)
+    ops.encode_fused_embedding_norm(stream, dev.upload(ids), dev.upload(table), dev.upload(w), normed, raw, hidden,
+                                    5, vocab, 1e-6)
+    stream.sync()
+    n_ref, r_ref = O.fused_embedding_norm(ids.astype(np.int64), table, w, 1e-6)
+    assert np.array_equal(raw.read().view(np.uint16), r_ref.view(np.uint16))
+    assert_ulps(normed.read(), n_ref, what="embedding norm")
+    assert not raw.read()[2].view(np.uint16).any() and not normed.read()[4].view(np.uint16).any()
+
+
+@pytest.mark.parametrize("norm,rotary", [(True, 0), (True, 32), (False, 0)])
+@pytest.mark.parametrize("use_positions", [True, False])
+def test_qk_norm_rope(dev, stream, norm, rotary, use_positions):
+    rng = np.random.default_rng(10 + rotary + norm + 2 * use_positions)
+    batch, tokens, nh, nkv, hd, max_pos = 3, 2, 32, 8, 128, 512
+    q = (rng.standard_normal((batch, tokens, nh, hd)) * 2).astype(np.float16)
+    k = (rng.standard_normal((batch, tokens, nkv, hd)) * 2).astype(np.float16)
+    qn = rng.uniform(0.5, 1.5, hd).astype(np.float16) if norm else None
+    kn = rng.uniform(0.5, 1.5, hd).astype(np.float16) if norm else None
+    cos, sin = ops.rope_cache(hd, max_pos, 1e6, rotary)
+    positions = np.array([0, 17, 509], np.int32)
+    seq_offset = 100
+    qd, kd = dev.upload(q), dev.upload(k)
+    ops.encode_qk_norm_rope(stream, qd, kd, dev.upload(cos), dev.upload(sin), nh, nkv, hd, max_pos,
+                            q_norm=dev.upload(qn) if norm else None, k_norm=dev.upload(kn) if norm else None,
+                            rotary_dim=rotary, seq_offset=seq_offset,
+                            positions=dev.upload(positions) if use_positions else None, batch=batch,
+                            token_count=tokens, eps=1e-6)
+    stream.sync()
+    base = positions if use_positions else np.full(batch, seq_offset)
+    pos = base[:, None] + np.arange(tokens)[None, :]          # [batch, tokens]
+    q_ref = O.qk_norm_rope(q, qn, cos, sin, pos, 1e-6, rotary or None)
+    k_ref = O.qk_norm_rope(k, kn, cos, sin, pos, 1e-6, rotary or None)
+    assert_ulps(qd.read(), q_ref, what="q")
+    assert_ulps(kd.read(), k_ref, what="k")
+
+
+def test_qk_norm_rope_errors(dev, stream):
+    q = dev.empty((1, 32, 128), np.float16)
+    cos, sin = ops.rope_cache(128, 16, 1e6)
+    c, s = dev.upload(cos), dev.upload(sin)
+    with pytest.raises(IronmillError, match="beyond the RoPE table"):
+        ops.encode_qk_norm_rope(stream, q, q, c, s, 32, 0, 128, 16, seq_offset=16)
+    with pytest.raises(IronmillError, match="both norm weights"):
+        ops.encode_qk_norm_rope(stream, q, q, c, s, 32, 0, 128, 16, q_norm=c)
+
+
+# ------------------------------------------------------------------ decoder
+
+CFG = dict(hidden_size=256, intermediate_size=512, num_layers=2, num_heads=4, num_kv_heads=1, head_dim=128,
+           vocab_size=512, max_seq_len=64, batch=2, rms_eps=1e-6, rope_theta=1e6)
+
+
+def make_model(dev, seed, cfg=CFG, qk_norm=True):
+    rng = np.random.default_rng(seed)
+    H, F, V = cfg["hidden_size"], cfg["intermediate_size"], cfg["vocab_size"]
+    qd, kvd = cfg["num_heads"] * cfg["head_dim"], cfg["num_kv_heads"] * cfg["head_dim"]
+
+    def q4(n, k, awq):
+        w = (rng.standard_normal((n, k)) * 0.05).astype(np.float32)
+        return quant.quantize_int4(w, awq_scales=awq)
+
+    def norm(n):
+        return rng.uniform(0.8, 1.2, n).astype(np.float16)
+
+    host_layers, dev_layers = [], []
+    for l in range(cfg["num_layers"]):
+        s_in = rng.uniform(0.5, 2.0, H).astype(np.float32)
+        s_kv = s_in if l == 0 else rng.uniform(0.5, 2.0, H).astype(np.float32)
+        s_f = rng.uniform(0.5, 2.0, F).astype(np.float32)
+        hl = dict(input_norm=norm(H), post_attn_norm=norm(H),
+                  q_norm=norm(cfg["head_dim"]) if qk_norm else None,
+                  k_norm=norm(cfg["head_dim"]) if qk_norm else None,
+                  q_proj=q4(qd, H, s_in), k_proj=q4(kvd, H, s_kv), v_proj=q4(kvd, H, s_kv),
+                  o_proj=q4(H, qd, None), gate_proj=q4(F, H, s_in), up_proj=q4(F, H, s_in),
+                  down_proj=q4(H, F, s_f))
+        host_layers.append(hl)
+        dl = {k: (dev.upload(v) if isinstance(v, np.ndarray) else None) for k, v in hl.items()
+              if k.endswith("norm")}
+        for name in ("q_proj", "k_proj", "o_proj", "gate_proj", "up_proj", "down_proj"):
+            dl[name] = ops.AffineQuantizedWeight(dev, hl[name])
+        if l == 0:  # share K's AWQ buffer so the decoder takes the one-launch K/V path
+            v = hl["v_proj"]
+            kw = dl["k_proj"]
+            dl["v_proj"] = ops.AffineQuantizedWeight.from_pointers(dev.upload(v.data), dev.upload(v.scales),
+                                                                   dev.upload(v.zeros), kw.awq_scales, v.n, v.k)
+            dl["_keep"] = dl["v_proj"]
+        else:
+            dl["v_proj"] = ops.AffineQuantizedWeight(dev, hl["v_proj"])
+        dev_layers.append(dl)
+    emb = rng.standard_normal((V, H)).astype(np.float16)
+    fnorm = norm(H)
+    lm = q4(V, H, None)
+    return host_layers, dev_layers, emb, fnorm, lm
+
+
+def build_decoder(dev, model, kv_cache, cfg=CFG):
+    host_layers, dev_layers, emb, fnorm, lm = model
+    d = ops.Decoder(dev, kv_cache=kv_cache, **cfg)
+    for l, dl in enumerate(dev_layers):
+        d.set_layer(l, **{k: v for k, v in dl.items() if not k.startswith("_")})
+    d._keep_lm = ops.AffineQuantizedWeight(dev, lm)
+    d.set_model(dev.upload(emb), dev.upload(fnorm), d._keep_lm)
+    return d
+
+
+@pytest.mark.parametrize("kv_cache", ["fp16", "turboquant"])
+def test_decoder_matches_reference(dev, stream, kv_cache):
+    model = make_model(dev, 77)
+    d = build_decoder(dev, model, kv_cache)
+    host_layers, _, emb, fnorm, lm = model
+    ref = O.DecoderReference(CFG, host_layers, emb, fnorm, lm, kv_cache=kv_cache)
+    start = np.array([0, 9], np.int32)
+    d.reset(stream, start)
+    ref.positions = start.copy()
+    rng = np.random.default_rng(5)
+    logits = dev.empty((CFG["batch"], CFG["vocab_size"]), np.float16)
+    flips = {}   # layer -> [K bytes differing, V bytes differing, bytes compared, far K/V differences]
+
+    def force_rows(l, cache, pos):
+        # TurboQuant: take the code rows the GPU wrote at this step (the cache write is
+        # bit-exact on equal inputs; here the inputs differ by rounding, which can move
+        # a vector across a codebook boundary) and record how the bytes differed
+        got = d.kv_cache(l)
+        f = flips.setdefault(l, [0, 0, 0, 0])
+        for b in range(CFG["batch"]):
+            p = pos[b]
+            rk, gk = cache["k_codes"][b, :, p].astype(int), got["k_codes"][b, :, p].astype(int)
+            rv, gv = cache["v_codes"][b, :, p].astype(int), got["v_codes"][b, :, p].astype(int)
+            f[0] += int(np.count_nonzero(rk != gk))
+            f[1] += int(np.count_nonzero(rv != gv))
+            f[2] += rk.size
+            # K: 7-bit index (neighbouring entry at most) | QJL sign in bit 7; V: 8-bit index
+            f[3] += int(np.count_nonzero(np.abs((rk & 0x7F) - (gk & 0x7F)) > 1))
+            f[3] += int(np.count_nonzero(np.abs(rv - gv) > 1))
+            for name in got:
+                cache[name][b, :, p] = got[name][b, :, p]
+
+    for step in range(4):
+        tok = rng.integers(0, CFG["vocab_size"], CFG["batch"]).astype(np.uint32)
+        d.step(stream, dev.upload(tok), logits)
+        stream.sync()
+        want = ref.step(tok.astype(np.int64), cache_hook=force_rows if kv_cache == "turboquant" else None)
+        r = rel_l2(logits.read(), want)
+        assert r <= 1e-3, f"{kv_cache} step {step}: logits rel-L2 {r:.3e}"
+    assert np.array_equal(d.positions(), start + 4)
+    if kv_cache == "turboquant":
+        # one-f16-step input differences change ~4 % of K bytes (mostly QJL signs) and
+        # ~0.5 % of V bytes in the oracle itself (test_tq_write_sensitivity_to_one_step)
+        msg = f"per layer [K differ, V differ, bytes, far]: {flips}"
+        assert all(f[0] <= 0.08 * f[2] and f[1] <= 0.02 * f[2] for f in flips.values()), msg
+    else:
+        # the cache rows the steps wrote are the K/V projections: compare layer 1 with the oracle's
+        got = d.kv_cache(1)
+        for b in range(CFG["batch"]):
+            rows = slice(start[b], start[b] + 4)
+            assert_close(got["k"][b, :, rows], ref.caches[1]["k"][b, :, rows].astype(np.float32), rel=5e-3,
+                         what="layer-1 K rows")
+            assert not got["k"][b, :, start[b] + 4:].view(np.uint16).any()
+
+
+def test_decoder_graph_replay_matches_eager(dev, stream):
+    """A captured step replays as the next token: positions advance on the device."""
+    model = make_model(dev, 78, qk_norm=False)
+    eager = build_decoder(dev, model, "turboquant")
+    graphed = build_decoder(dev, model, "turboquant")
+    tok = dev.upload(np.array([7, 300], np.uint32))
+    la = dev.empty((CFG["batch"], CFG["vocab_size"]), np.float16)
+    lb = dev.empty((CFG["batch"], CFG["vocab_size"]), np.float16)
+    graphed.reset(stream)
+    graphed.step(stream, tok, lb)       # sizes the stream's scratch before the capture
+    graphed.reset(stream)
+    graph = stream.capture(lambda: graphed.step(stream, tok, lb))
+    eager.reset(stream)
+    for step in range(3):
+        eager.step(stream, tok, la)
+        graph.launch(stream)
+        stream.sync()
+        assert np.array_equal(la.read().view(np.uint16), lb.read().view(np.uint16)), f"step {step}"
+    ka, kb = eager.kv_cache(0), graphed.kv_cache(0)
+    assert np.array_equal(ka["k_codes"], kb["k_codes"]) and np.array_equal(ka["v_scales"], kb["v_scales"])
+    assert ka["k_scales"][:, :, :3].all() and not ka["k_scales"][:, :, 3:].any()
+
+
+def test_decoder_errors(dev, stream):
+    cfg = dict(CFG, num_layers=1)
+    d = ops.Decoder(dev, kv_cache="fp16", **cfg)
+    tok = dev.upload(np.zeros(2, np.uint32))
+    logits = dev.empty((2, cfg["vocab_size"]), np.float16)
+    with pytest.raises(IronmillError, match="not set"):
+        d.step(stream, tok, logits)
+    model = make_model(dev, 79, cfg)
+    dl = {k: v for k, v in model[1][0].items() if not k.startswith("_")}
+    bad = dict(dl, o_proj=dl["q_proj"])
+    with pytest.raises(IronmillError, match="o_proj"):
+        d.set_layer(0, **bad)
+    with pytest.raises(IronmillError, match="outside the cache"):
+        d.reset(stream, np.array([0, 64], np.int32))
+    d.set_layer(0, **dl)
+    lm = ops.AffineQuantizedWeight(dev, model[4])
+    d.set_model(dev.upload(model[2]), dev.upload(model[3]), lm)
+    d.reset(stream, np.array([63, 0], np.int32))
+    d.step(stream, tok, logits)
+    with pytest.raises(IronmillError, match="beyond max_seq_len"):
+        d.step(stream, tok, logits)
+    with pytest.raises(IronmillError, match="multiple of num_kv_heads"):
+        ops.Decoder(dev, **dict(CFG, num_heads=3, num_kv_heads=2))

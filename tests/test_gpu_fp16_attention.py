@@ -104,12 +104,13 @@ def test_split_and_single_pass_agree(dev, stream):
     assert_close(a, b, rel=2e-3, max_abs=2e-3, what="split vs single")
 
 
-def test_ragged_and_empty_sequences(dev, stream):
+@pytest.mark.parametrize("bound", [400, 0])  # 0: the splits span max_seq_len
+def test_ragged_and_empty_sequences(dev, stream, bound):
     batch, nkv, nh, max_seq = 4, 8, 32, 512
     cache = fill_cache(dev, stream, batch, nkv, max_seq, 400, seed=9)
     lens = np.array([400, 1, 0, 77], np.int32)
     q16 = np.random.default_rng(8).standard_normal((batch, nh, D)).astype(np.float16)
-    got = run_attention(dev, stream, cache, q16, nh, 400, seq_lens=lens)
+    got = run_attention(dev, stream, cache, q16, nh, bound, seq_lens=lens)
     ref = O.fp16_attention(q16, cache.k.read(), cache.v.read(), 400, SCALE, seq_lens=lens, nthreads=8)
     assert_close(got, ref, what="ragged")
     assert np.array_equal(got[2].view(np.uint16), np.zeros((nh, D), np.uint16))  # empty -> 0

@@ -105,3 +105,14 @@ def test_error_paths_without_gpu():
     n = C.c_int(-1)
     L.imh_device_count(C.byref(n))  # no GPU here: an error code or 0, never a crash
     assert n.value >= 0
+
+
+def test_rope_cache_is_bit_exact_with_oracle():
+    """imh_rope_cache_fill runs on the host: every f16 entry equals the oracle's."""
+    import oracle as O
+    from ironmill_amd import ops
+    for hd, mp, theta, rd in ((128, 4096, 1e6, 0), (128, 300, 1e4, 32), (64, 100, 5e5, 0)):
+        c, s = ops.rope_cache(hd, mp, theta, rd)
+        c2, s2 = O.rope_cache(hd, mp, theta, rd or None)
+        assert np.array_equal(c.view(np.uint16), c2.view(np.uint16))
+        assert np.array_equal(s.view(np.uint16), s2.view(np.uint16))

@@ -497,3 +497,107 @@ def test_fp16_attention_empty_rows_are_zero():
     out = O.fp16_attention(q, k, v, 0, 0.1, seq_lens=np.array([0, 2], np.int32))
     assert np.all(out[0] == 0)
     assert np.all(out[1, 0] == 0) and np.any(out[1, 1] != 0)  # limit 2 - 3 + t + 1 = t
+
+
+# ---- decode-step glue (normalization.metal, fused_qk_norm_rope.metal, rope.rs) ----
+
+def test_rms_norm_matches_torch():
+    """Against torch.nn.functional.rms_norm (a library routine) in float64."""
+    import torch
+    rng = np.random.default_rng(41)
+    x = rng.standard_normal((5, 640)).astype(np.float16)
+    w = rng.uniform(0.5, 1.5, 640).astype(np.float16)
+    ref = torch.nn.functional.rms_norm(torch.from_numpy(x.astype(np.float64)), (640,),
+                                       torch.from_numpy(w.astype(np.float64)), eps=1e-6).numpy()
+    assert np.array_equal(O.rms_norm(x, w, 1e-6), ref.astype(np.float16))
+
+
+def test_rms_norm_constant_row_closed_form():
+    x = np.full((1, 256), 3.0, np.float16)
+    w = np.full(256, 2.0, np.float16)
+    assert np.all(O.rms_norm(x, w, 0.0) == np.float16(2.0))   # x / |x| * w
+
+
+def test_fused_residual_rms_norm_is_add_then_norm():
+    """residual = f16(a + b); normed = torch rms_norm of the unrounded f64 sum."""
+    import torch
+    rng = np.random.default_rng(42)
+    a, b = rng.standard_normal((3, 384)).astype(np.float16), rng.standard_normal((3, 384)).astype(np.float16)
+    w = rng.uniform(0.5, 1.5, 384).astype(np.float16)
+    normed, res = O.fused_residual_rms_norm(a, b, w, 1e-6)
+    x = a.astype(np.float64) + b.astype(np.float64)
+    assert np.array_equal(res, x.astype(np.float16))
+    ref = torch.nn.functional.rms_norm(torch.from_numpy(x), (384,), torch.from_numpy(w.astype(np.float64)),
+                                       eps=1e-6).numpy()
+    assert np.array_equal(normed, ref.astype(np.float16))
+
+
+def test_embedding_norm_rows_and_invalid_ids():
+    rng = np.random.default_rng(43)
+    table = rng.standard_normal((10, 256)).astype(np.float16)
+    w = rng.uniform(0.5, 1.5, 256).astype(np.float16)
+    normed, raw = O.fused_embedding_norm(np.array([3, 10, 0, 2**31 - 1]), table, w, 1e-6)
+    assert np.array_equal(raw[0], table[3]) and np.array_equal(raw[2], table[0])
+    assert not raw[1].any() and not raw[3].any() and not normed[1].any()   # id >= vocab -> 0
+    assert np.array_equal(normed[0], O.rms_norm(table[3:4], w, 1e-6)[0])
+
+
+def test_rope_cache_reference_vectors():
+    """rope.rs tests full_rotation_basic / partial_rotation_fills_identity, plus pos 1 values."""
+    cos, sin = O.rope_cache(4, 2, 10000.0)
+    assert cos.shape == (2, 2) and cos[0, 0] == 1.0 and sin[0, 0] == 0.0
+    assert cos[1, 0] == np.float16(np.cos(1.0)) and sin[1, 1] == np.float16(np.sin(1.0 / 100.0))
+    cos, sin = O.rope_cache(8, 1, 10000.0, 4)
+    assert cos.shape == (1, 4) and cos[0, 2] == 1.0 and cos[0, 3] == 1.0 and sin[0, 2] == 0 and sin[0, 3] == 0
+
+
+def test_rope_matches_complex_rotation():
+    """Half-split RoPE is multiplication of (x_d + i x_{d+h}) by e^{i theta} (an independent form)."""
+    rng = np.random.default_rng(44)
+    x = rng.standard_normal((3, 2, 128)).astype(np.float16)
+    cos, sin = O.rope_cache(128, 50, 1e6)
+    pos = np.array([0, 17, 49])
+    out = O.qk_norm_rope(x, None, cos, sin, pos, 1e-6)
+    z = (x[..., :64].astype(np.float64) + 1j * x[..., 64:].astype(np.float64))
+    rot = z * (cos[pos].astype(np.float64) + 1j * sin[pos].astype(np.float64))[:, None, :]
+    ref = np.concatenate([rot.real, rot.imag], axis=-1).astype(np.float16)
+    assert np.array_equal(out, ref)
+    assert np.array_equal(out[0], x[0])                    # position 0: identity
+
+
+def test_qk_norm_rope_partial_rotary_and_norm():
+    rng = np.random.default_rng(45)
+    x = rng.standard_normal((2, 3, 128)).astype(np.float16)
+    w = rng.uniform(0.5, 1.5, 128).astype(np.float16)
+    cos, sin = O.rope_cache(128, 10, 1e4, 32)
+    out = O.qk_norm_rope(x, w, cos, sin, np.array([0, 5]), 1e-6, rotary_dim=32)
+    normed = O.rms_norm(x, w, 1e-6)
+    assert np.array_equal(out[0], normed[0])               # position 0 rotates nothing
+    assert np.array_equal(out[1][..., 32:], normed[1][..., 32:])   # beyond rotary_dim: normalised only
+    # rotation keeps each (d, d+16) pair's length
+    y = x[1].astype(np.float64) / np.sqrt((x[1].astype(np.float64) ** 2).mean(-1, keepdims=True) + 1e-6) * w
+    r_in = np.hypot(y[..., :16], y[..., 16:32])
+    r_out = np.hypot(out[1][..., :16].astype(np.float64), out[1][..., 16:32].astype(np.float64))
+    assert np.allclose(r_in, r_out, rtol=2e-3)
+
+
+def test_tq_write_sensitivity_to_one_step(tabs):
+    """How far the cache write moves when inputs move by one f16 step (the size of the
+    differences between two correct f16 pipelines): a few % of K bytes, mostly the QJL
+    sign of the small quantization residual, and well under 2 % of V bytes.  Rare far
+    index jumps come from the Lloyd-Max tables' coinciding tail boundaries."""
+    rng = np.random.default_rng(0)
+    n = 400
+    x = rng.standard_normal((n, 128)).astype(np.float16)
+    step = rng.choice([-1, 0, 0, 0, 1], size=x.shape)
+    xp = np.where(step > 0, np.nextafter(x, np.float16(np.inf)),
+                  np.where(step < 0, np.nextafter(x, np.float16(-np.inf)), x)).astype(np.float16)
+    k1, _, _ = O.tq_cache_write(x[None, :, None, :], tabs, True, n)
+    k2, _, _ = O.tq_cache_write(xp[None, :, None, :], tabs, True, n)
+    v1, _, _ = O.tq_cache_write(x[None, :, None, :], tabs, False, n)
+    v2, _, _ = O.tq_cache_write(xp[None, :, None, :], tabs, False, n)
+    k_diff = np.mean(k1 != k2)
+    sign_diff = np.mean((k1 >> 7) != (k2 >> 7))
+    v_diff = np.mean(v1 != v2)
+    assert 0.01 < k_diff < 0.08 and sign_diff > 0.8 * k_diff
+    assert 0.0005 < v_diff < 0.02
