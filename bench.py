@@ -194,6 +194,111 @@ def bench_fp16_attention(dev, stream, ops, batch, ctx, steps, warmup, layers):
             "frac": round(gbs / HBM_PEAK_GBS, 4), "bytes": nbytes}
 
 
+# Qwen3-4B shape of the decode-step measurement (cfg 5)
+Q3 = dict(hidden_size=2560, intermediate_size=9728, num_layers=36, num_heads=32, num_kv_heads=8, head_dim=128,
+          vocab_size=151936, rms_eps=1e-6, rope_theta=1e6)
+
+
+def decode_step_bytes(b, ctx, cfg=Q3):
+    """HBM bytes of one decode step: every INT4 weight (codes + f16 scale/zero per 128) and the
+    whole TurboQuant cache each sequence attends over (268 B per position and kv head)."""
+    H, F, L = cfg["hidden_size"], cfg["intermediate_size"], cfg["num_layers"]
+    qd, kvd = cfg["num_heads"] * cfg["head_dim"], cfg["num_kv_heads"] * cfg["head_dim"]
+    per_layer = qd * H + 2 * kvd * H + H * qd + 2 * F * H + H * F
+    weights = (L * per_layer + cfg["vocab_size"] * H) * INT4_BYTES_PER_ELEM
+    kv = b * L * cfg["num_kv_heads"] * ctx * (2 * cfg["head_dim"] + 12)
+    return weights + kv
+
+
+def random_int4(dev, ops, rng, n, k, awq=True):
+    """Synthetic INT4 weight in the upload layout: random codes, f16 scales in [1e-3, 3e-3],
+    integer zero-points 0..15, AWQ scales in [0.5, 2]."""
+    data = rng.integers(0, 256, size=(n, k // 2), dtype=np.uint8)
+    sc = rng.uniform(1e-3, 3e-3, (n, k // 128)).astype(np.float16)
+    zp = rng.integers(0, 16, size=(n, k // 128)).astype(np.float16)
+    a = dev.upload(rng.uniform(0.5, 2.0, k).astype(np.float16)) if awq else None
+    return ops.AffineQuantizedWeight.from_pointers(dev.upload(data), dev.upload(sc), dev.upload(zp), a, n, k)
+
+
+def bench_decode(dev, stream, ops, batch, ctx, steps, warmup, kv_cache="turboquant", graph=True):
+    """Decode step of a Qwen3-4B-shaped model (36 layers, random INT4 weights incl. the LM head,
+    QK-norm, TurboQuant KV cache filled to `ctx` positions): one step captured as a HIP graph and
+    replayed once per token, timed with HIP events over `steps` replays."""
+    cfg = dict(Q3, batch=batch, max_seq_len=ctx + steps + warmup + 8)
+    rng = np.random.default_rng(2024)
+    H, F, L = cfg["hidden_size"], cfg["intermediate_size"], cfg["num_layers"]
+    qd, kvd, hd = cfg["num_heads"] * cfg["head_dim"], cfg["num_kv_heads"] * cfg["head_dim"], cfg["head_dim"]
+    d = ops.Decoder(dev, kv_cache=kv_cache, **cfg)
+    keep = []
+
+    def norm(n):
+        return dev.upload(rng.uniform(0.8, 1.2, n).astype(np.float16))
+
+    for l in range(L):
+        w = dict(input_norm=norm(H), post_attn_norm=norm(H), q_norm=norm(hd), k_norm=norm(hd),
+                 q_proj=random_int4(dev, ops, rng, qd, H), k_proj=random_int4(dev, ops, rng, kvd, H),
+                 o_proj=random_int4(dev, ops, rng, H, qd, awq=False),
+                 gate_proj=random_int4(dev, ops, rng, F, H), down_proj=random_int4(dev, ops, rng, H, F))
+        w["up_proj"] = ops.AffineQuantizedWeight.from_pointers(
+            *[dev.upload(a) for a in (rng.integers(0, 256, size=(F, H // 2), dtype=np.uint8),
+                                      rng.uniform(1e-3, 3e-3, (F, H // 128)).astype(np.float16),
+                                      rng.integers(0, 16, size=(F, H // 128)).astype(np.float16))],
+            w["gate_proj"].awq_scales, F, H)
+        w["v_proj"] = ops.AffineQuantizedWeight.from_pointers(
+            *[dev.upload(a) for a in (rng.integers(0, 256, size=(kvd, H // 2), dtype=np.uint8),
+                                      rng.uniform(1e-3, 3e-3, (kvd, H // 128)).astype(np.float16),
+                                      rng.integers(0, 16, size=(kvd, H // 128)).astype(np.float16))],
+            w["k_proj"].awq_scales, kvd, H)
+        d.set_layer(l, **w)
+        keep.append(w)
+    emb = dev.upload((rng.standard_normal((cfg["vocab_size"], H)) * 0.05).astype(np.float16))
+    lm = random_int4(dev, ops, rng, cfg["vocab_size"], H, awq=False)
+    d.set_model(emb, norm(H), lm)
+    # the cache of every layer filled to ctx positions from random K/V projections
+    kv = dev.upload(rng.standard_normal((batch, ctx, cfg["num_kv_heads"], hd)).astype(np.float16))
+    kv2 = dev.upload(rng.standard_normal((batch, ctx, cfg["num_kv_heads"], hd)).astype(np.float16))
+    for l in range(L):
+        d.write_kv(stream, l, kv, kv2, ctx, 0)
+    stream.sync()
+    del kv, kv2
+    tok = dev.upload(rng.integers(0, cfg["vocab_size"], batch).astype(np.uint32))
+    logits = dev.empty((batch, cfg["vocab_size"]), np.float16)
+    start = np.full(batch, ctx, np.int32)
+    d.reset(stream, start)
+    d.step(stream, tok, logits)           # sizes the stream's scratch memory
+    stream.sync()
+    d.reset(stream, start)
+    s, e = dev.event(), dev.event()
+    ms = float("nan")
+    if graph:
+        g = stream.capture(lambda: d.step(stream, tok, logits))
+        for _ in range(warmup):
+            g.launch(stream)
+        stream.sync()
+        s.record(stream)
+        for _ in range(steps):
+            g.launch(stream)
+        e.record(stream)
+        stream.sync()
+        ms = s.elapsed_ms(e) / steps
+    # eager encode of the same step (host launches, no graph), for the launch-overhead picture
+    d.reset(stream, start)
+    s.record(stream)
+    for _ in range(5):
+        d.step(stream, tok, logits)
+    e.record(stream)
+    stream.sync()
+    ms_eager = s.elapsed_ms(e) / 5
+    nbytes = decode_step_bytes(batch, ctx)
+    out = {"batch": batch, "ctx": ctx, "kv_cache": kv_cache, "ms_per_step": round(ms, 4),
+           "tok_per_s": round(batch / (ms * 1e-3), 1), "GB/s": round(nbytes / (ms * 1e-3) / 1e9, 1),
+           "frac": round(nbytes / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4), "bytes": int(nbytes),
+           "ms_per_step_eager": round(ms_eager, 4)}
+    d.close()
+    del keep
+    return out
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -206,6 +311,11 @@ def main():
     ap.add_argument("--replicas", type=int, default=0,
                     help="weight copies rotated through (default: enough for >= 512 MB, beyond the "
                          "256 MB Infinity Cache; 1 measures a cache-resident matrix)")
+    ap.add_argument("--decode-only", action="store_true",
+                    help="only the Qwen3-4B decode-step lines (B=1 and 8, ctx 8k), for profiling")
+    ap.add_argument("--decode-batches", type=int, nargs="+", default=[1, 8])
+    ap.add_argument("--decode-eager", action="store_true",
+                    help="with --decode-only: time 5 eager steps only (no graph capture; for kernel traces)")
     ap.add_argument("--kernel-only", action="store_true",
                     help="only the prepared fused gate+up kernel loop (for rocprofv3 counter runs)")
     ap.add_argument("--calibrate-copy", action="store_true",
@@ -232,6 +342,14 @@ def main():
     stream = dev.stream()
     info = dev.info()
     log(f"device {info['arch']} CUs={info['compute_units']}")
+
+    if args.decode_only:
+        for bb in args.decode_batches:
+            r = bench_decode(dev, stream, ops, bb, 8192, max(20, args.steps // 10), 3, graph=not args.decode_eager)
+            log(f"decode step B={bb} ctx=8k: {r['ms_per_step']} ms ({r['tok_per_s']} tok/s, "
+                f"{r['GB/s']} GB/s); eager encode {r['ms_per_step_eager']} ms")
+            print(json.dumps({f"decode_step_b{bb}_ctx8k": r}), flush=True)
+        return
 
     B = args.batch
     qg, qu, qd = make_weights(1234)
@@ -336,6 +454,11 @@ def main():
             r = bench_fp16_attention(dev, stream, ops, bb, 32768, max(20, args.steps // 4), 5, layers)
             details[f"fp16_attention_b{bb}_ctx32k"] = r
             log(f"FP16-KV attention B={bb} ctx=32k: {r['us']} us {r['GB/s']} GB/s")
+        for bb in (1, 8):
+            r = bench_decode(dev, stream, ops, bb, 8192, max(20, args.steps // 10), 3)
+            details[f"decode_step_b{bb}_ctx8k"] = r
+            log(f"decode step B={bb} ctx=8k: {r['ms_per_step']} ms ({r['tok_per_s']} tok/s, "
+                f"{r['GB/s']} GB/s)")
         log(json.dumps(details))
 
     cpu = None

@@ -242,6 +242,7 @@ SIGNATURES = {
     "imh_decoder_set_model": (I, [P, P, P, C.POINTER(AffineInt4Weight)]),
     "imh_decoder_reset": (I, [P, P, P]),
     "imh_decoder_step": (I, [P, P, P, P]),
+    "imh_decoder_write_kv": (I, [P, P, U32, P, P, U32, U32]),
     "imh_decoder_positions": (I, [P, P]),
     "imh_decoder_kv_cache": (I, [P, U32, C.POINTER(TqKvCache), C.POINTER(Fp16KvCache)]),
     "imh_decoder_tq_tables": (I, [P, C.POINTER(P)]),

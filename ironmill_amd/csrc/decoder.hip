@@ -372,6 +372,24 @@ int imh_decoder_step(imh_decoder *d, imh_stream *s, const uint32_t *token_ids, u
     return IMH_OK;
 }
 
+int imh_decoder_write_kv(imh_decoder *d, imh_stream *s, uint32_t layer, const uint16_t *k_proj,
+                         const uint16_t *v_proj, uint32_t token_count, uint32_t base_pos) {
+    if (!d || !s || !k_proj || !v_proj) return imh::fail(IMH_EINVAL, "imh_decoder_write_kv: NULL argument");
+    if (layer >= d->cfg.num_layers) return imh::fail(IMH_EINVAL, "imh_decoder_write_kv: layer out of range");
+    if ((uint64_t)base_pos + token_count > d->cfg.max_seq_len)
+        return imh::fail(IMH_ERANGE, "imh_decoder_write_kv: base_pos + token_count beyond max_seq_len");
+    if (d->cfg.kv_cache == IMH_KV_TURBOQUANT) {
+        int rc = imh_encode_turboquant_cache_write(s, d->tq, &d->tq_caches[layer], k_proj, token_count, base_pos,
+                                                   nullptr, 1);
+        if (rc) return rc;
+        return imh_encode_turboquant_cache_write(s, d->tq, &d->tq_caches[layer], v_proj, token_count, base_pos,
+                                                 nullptr, 0);
+    }
+    int rc = imh_encode_kv_scatter(s, &d->fp16_caches[layer], k_proj, token_count, base_pos, nullptr, 1);
+    if (rc) return rc;
+    return imh_encode_kv_scatter(s, &d->fp16_caches[layer], v_proj, token_count, base_pos, nullptr, 0);
+}
+
 int imh_decoder_positions(const imh_decoder *d, int32_t *out) {
     if (!d || !out) return imh::fail(IMH_EINVAL, "imh_decoder_positions: NULL argument");
     std::memcpy(out, d->host_positions.data(), d->host_positions.size() * 4);

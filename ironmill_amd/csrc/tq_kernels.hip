@@ -14,9 +14,12 @@
 //   * builds the dequantized K chunk as MFMA operand B with one LDS lookup per
 //     byte (codebook entry as an f16 hi/lo pair) plus the +-1 QJL signs taken
 //     straight from bit 7, and runs v_mfma_f32_16x16x32_f16 against the rotated
-//     query (and its QJL projection) as operand A, both split hi + lo;
-//   * folds the per-position scales in, runs an online softmax per head with
-//     16-lane shuffles, and accumulates V (codebook lookup * weight) in f32.
+//     query (hi, lo) and its QJL projection (hi, lo) packed as rows of operand A;
+//   * folds the per-position scales in and runs the online softmax of all the
+//     group's heads at once with DPP row reductions;
+//   * accumulates P.V on v_mfma_f32_16x16x16_f16 (positions as the contraction
+//     index) from V codes transposed in registers and looked up in an f16
+//     codebook, with the weights (times the V scale) as f16.
 // Waves combine through LDS; splits are combined (log-sum-exp) and rotated
 // back by a second small kernel (fused_sdpa_reduce, flash_decode.metal:163-215).
 #include <hip/hip_runtime.h>
@@ -33,6 +36,7 @@ namespace {
 
 typedef _Float16 half8_t __attribute__((ext_vector_type(8)));
 typedef float float4_t __attribute__((ext_vector_type(4)));
+typedef _Float16 half4_t __attribute__((ext_vector_type(4)));
 
 constexpr int kD = 128;          // head_dim the kernels are built for
 constexpr int kChunk = 16;       // positions per MFMA block
@@ -187,6 +191,19 @@ __global__ void __launch_bounds__(kD) tq_query_prep_kernel(const __half *__restr
 // Attention: grid (num_splits, num_kv_heads, batch), block 64 * kWaves.  Each
 // wave walks its split in 16-position chunks; the codes and per-position
 // scales of the next chunk are loaded before the current one is computed.
+//
+// Register layout.  Head hh of the group owns rows 4hh..4hh+3 of the 16-row
+// MFMA operands, so in every 16x16 result lane group g = lane >> 4 holds head
+// g: the scores of one head are one DPP row (softmax reductions serve all
+// heads at once) and the running max, sum and rescale are per lane.  P.V runs
+// on v_mfma_f32_16x16x16_f16 with the positions as the contraction index:
+// result column c of block j is dim 8c + j, so lane (c, g) loads V codes of
+// positions 4g..4g+3 at dims 8c..8c+7 (four 8-byte row loads, coalesced
+// across the 16 lanes of a row) and its B operand for block j is the four
+// codebook values of byte j -- a register transpose, no LDS staging.  The
+// weights w * v_scale go through a 128-byte per-wave LDS buffer into row 4hh
+// of operand A as f16.  Built with -amdgpu-mfma-vgpr-form so the accumulators
+// stay in VGPRs (no AGPR round trip around the softmax rescale).
 template <int GQA>
 __global__ void __launch_bounds__(64 * kWaves) tq_attention_kernel(
     const float *__restrict__ qprep, int nh, int nkv, int max_seq, int seq_len,
@@ -197,8 +214,9 @@ __global__ void __launch_bounds__(64 * kWaves) tq_attention_kernel(
     const float *__restrict__ krnorm, int split_len, float *__restrict__ part_o,
     float *__restrict__ part_m, float *__restrict__ part_l) {
     __shared__ float qs[GQA][2][kD];
-    __shared__ uint32_t ktab[128];
-    __shared__ float vtab[256];
+    __shared__ uint32_t ktab[256];   // entry c & 0x7F, indexed by the whole code byte
+    __shared__ _Float16 vtab[256];
+    __shared__ _Float16 wbuf[kWaves][4][16];
     __shared__ float om[kWaves][GQA][kD];
     __shared__ float mm[kWaves][GQA];
     __shared__ float ll[kWaves][GQA];
@@ -215,179 +233,170 @@ __global__ void __launch_bounds__(64 * kWaves) tq_attention_kernel(
     const int p_begin = split * split_len;
     const int p_end = min(p_begin + split_len, L);
     const size_t head_base = ((size_t)b * nkv + kvh) * (size_t)max_seq;
-    const int n_l = lane & 15;
-    const int kg = lane >> 4;
-    const int vgrp = lane & 7;    // which 16-dim slice of V this lane accumulates
-    const int vpos = lane >> 3;   // which of 8 positions per round
+    const int n_l = lane & 15;   // score layout: position; P.V layout: column c
+    const int kg = lane >> 4;    // lane group: K dims block / head / V position quad
 
-    // chunk inputs, loaded one chunk ahead
+    // Loads go through buffer resources bounded at p_end: rows at or past the
+    // split's end read as zeros (their weights are zero), so no clamping, and
+    // each lane's offsets advance by one add per chunk.
+    constexpr uint32_t kRsrcWord3 = 0x00020000u;
+    const int rows = p_end > 0 ? p_end : 0;
+    const __amdgpu_buffer_rsrc_t kc_r = __builtin_amdgcn_make_buffer_rsrc(
+        (void *)(kcodes + head_base * kD), 0, rows * kD, kRsrcWord3);
+    const __amdgpu_buffer_rsrc_t vc_r = __builtin_amdgcn_make_buffer_rsrc(
+        (void *)(vcodes + head_base * kD), 0, rows * kD, kRsrcWord3);
+    const __amdgpu_buffer_rsrc_t ks_r = __builtin_amdgcn_make_buffer_rsrc(
+        (void *)(kscales + head_base), 0, rows * 4, kRsrcWord3);
+    const __amdgpu_buffer_rsrc_t kr_r = __builtin_amdgcn_make_buffer_rsrc(
+        (void *)(krnorm + head_base), 0, rows * 4, kRsrcWord3);
+    const __amdgpu_buffer_rsrc_t vs_r = __builtin_amdgcn_make_buffer_rsrc(
+        (void *)(vscales + head_base), 0, rows * 4, kRsrcWord3);
     struct ChunkIn {
-        uint4 k0, k1, v0, v1;
+        uint4 k0, k1;
+        uint2 v[4];
         float ksc, krn, vsc;
     };
     auto load_chunk = [&](int p0, ChunkIn &c) __attribute__((always_inline)) {
-        const int last = p_end - 1;
-        const int pk = min(p0 + n_l, last);
-        const uint4 *kp = reinterpret_cast<const uint4 *>(kcodes + (head_base + pk) * kD + kg * 32);
-        c.k0 = kp[0];
-        c.k1 = kp[1];
-        c.v0 = *reinterpret_cast<const uint4 *>(vcodes + (head_base + min(p0 + vpos, last)) * kD + vgrp * 16);
-        c.v1 = *reinterpret_cast<const uint4 *>(vcodes + (head_base + min(p0 + 8 + vpos, last)) * kD + vgrp * 16);
-        c.ksc = kscales[head_base + pk];
-        c.krn = krnorm[head_base + pk];
-        c.vsc = vscales[head_base + pk];
+        const int koff = (p0 + n_l) * kD + kg * 32;
+        c.k0 = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(kc_r, koff, 0, 0));
+        c.k1 = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(kc_r, koff + 16, 0, 0));
+        const int voff = (p0 + 4 * kg) * kD + n_l * 8;
+#pragma unroll
+        for (int i = 0; i < 4; i++)
+            c.v[i] = __builtin_bit_cast(uint2, __builtin_amdgcn_raw_buffer_load_b64(vc_r, voff + i * kD, 0, 0));
+        const int soff = (p0 + n_l) * 4;
+        c.ksc = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(ks_r, soff, 0, 0));
+        c.krn = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(kr_r, soff, 0, 0));
+        c.vsc = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(vs_r, soff, 0, 0));
     };
     ChunkIn cur;
     const int p_first = p_begin + wave * kChunk;
     if (p_first < p_end) load_chunk(p_first, cur);
 
-    // tables: K codebook as (f16 hi | f16 lo << 16), V codebook in f32; the
+    // tables: K codebook as (f16 hi | f16 lo << 16), V codebook in f16; the
     // group's prepared queries
-    if (tid < 128) {
-        const float c = kcb[tid];
+    {
+        const float c = kcb[tid & 0x7F];
         const _Float16 hi = (_Float16)c;
         const _Float16 lo = (_Float16)(c - (float)hi);
-        ktab[tid] = (uint32_t)__builtin_bit_cast(uint16_t, hi) |
-                    ((uint32_t)__builtin_bit_cast(uint16_t, lo) << 16);
+        ktab[tid] = (uint32_t)__builtin_bit_cast(uint16_t, hi) | ((uint32_t)__builtin_bit_cast(uint16_t, lo) << 16);
     }
-    vtab[tid] = vcb[tid];
+    vtab[tid] = (_Float16)vcb[tid];
     const float *qg = qprep + ((size_t)b * nh + kvh * GQA) * 2 * kD;
     for (int e = tid; e < GQA * 2 * kD; e += 64 * kWaves) (&qs[0][0][0])[e] = qg[e];
     __syncthreads();
 
-    // operand A (rows = heads of the group, hi and lo halves), k-slot order
-    // within each 4-byte word: bytes {0, 2, 1, 3}
+    // score operands A, k-slot order within each 4-byte word: bytes {0, 2, 1, 3}.
+    // Rows 4h..4h+3 carry head h: aqk = {q_hi, q_lo, 0, 0} (against K hi),
+    // aqh = {q_hi, 0, 0, 0} (against K lo), aqs = {0, 0, s_hi, s_lo} (against
+    // the QJL signs), so one accumulator holds, in lane group h's four
+    // registers, q_hi.K + q_hi.K_lo, q_lo.K_hi, s_hi.sgn, s_lo.sgn.
     const int am = lane & 15;
-    half8_t aq_hi[4], aq_lo[4], as_hi[4], as_lo[4];
+    const int ah = am >> 2, ar = am & 3;
+    const bool arow = ah < GQA;
+    half8_t aqk[4], aqh[4], aqs[4];
     constexpr int slot_byte[8] = {0, 2, 1, 3, 4, 6, 5, 7};
 #pragma unroll
     for (int j = 0; j < 4; j++) {
 #pragma unroll
         for (int i = 0; i < 8; i++) {
             float vq = 0.0f, vs = 0.0f;
-            if (am < GQA) {
+            if (arow) {
                 const int d = kg * 32 + j * 8 + slot_byte[i];
-                vq = qs[am][0][d];
-                vs = qs[am][1][d];
+                vq = qs[ah][0][d];
+                vs = qs[ah][1][d];
             }
             const _Float16 qh = (_Float16)vq, sh = (_Float16)vs;
-            aq_hi[j][i] = qh;
-            aq_lo[j][i] = (_Float16)(vq - (float)qh);
-            as_hi[j][i] = sh;
-            as_lo[j][i] = (_Float16)(vs - (float)sh);
+            const _Float16 ql = (_Float16)(vq - (float)qh), sl = (_Float16)(vs - (float)sh);
+            const _Float16 z = (_Float16)0.0f;
+            aqk[j][i] = ar == 0 ? qh : (ar == 1 ? ql : z);
+            aqh[j][i] = ar == 0 ? qh : z;
+            aqs[j][i] = ar == 2 ? sh : (ar == 3 ? sl : z);
         }
     }
 
     const float qjl_factor = sqrtf(2.0f / 3.14159265f) / (float)kD;
-    float m_run[GQA], l_run[GQA];
-    float o[GQA][16];
+    float m_run = -INFINITY, l_run = 0.0f;   // of head kg (rows of one DPP row)
+    float4_t acc[8];
 #pragma unroll
-    for (int hh = 0; hh < GQA; hh++) {
-        m_run[hh] = -INFINITY;
-        l_run[hh] = 0.0f;
-#pragma unroll
-        for (int e = 0; e < 16; e++) o[hh][e] = 0.0f;
-    }
+    for (int j = 0; j < 8; j++) acc[j] = float4_t{0, 0, 0, 0};
 
     for (int p0 = p_first; p0 < p_end; p0 += kChunk * kWaves) {
         const ChunkIn c = cur;
         if (p0 + kChunk * kWaves < p_end) load_chunk(p0 + kChunk * kWaves, cur);
-        // ---- scores: S[h][n] for 16 positions via MFMA ----
+        // ---- scores S[h][n] for 16 positions via MFMA ----
         const uint32_t kw[8] = {c.k0.x, c.k0.y, c.k0.z, c.k0.w, c.k1.x, c.k1.y, c.k1.z, c.k1.w};
-        float4_t d1 = {0, 0, 0, 0}, d2 = {0, 0, 0, 0};
+        float4_t d1 = {0, 0, 0, 0};
 #pragma unroll
         for (int j = 0; j < 4; j++) {
             uint32_t bh[4], bl[4], bs[4];
 #pragma unroll
             for (int hw = 0; hw < 2; hw++) {
                 const uint32_t w = kw[2 * j + hw];
-                const uint32_t t0 = ktab[w & 0x7F];
-                const uint32_t t1 = ktab[(w >> 8) & 0x7F];
-                const uint32_t t2 = ktab[(w >> 16) & 0x7F];
-                const uint32_t t3 = ktab[(w >> 24) & 0x7F];
+                const uint32_t t0 = ktab[w & 0xFF];
+                const uint32_t t1 = ktab[(w >> 8) & 0xFF];
+                const uint32_t t2 = ktab[(w >> 16) & 0xFF];
+                const uint32_t t3 = ktab[w >> 24];
                 bh[2 * hw] = __builtin_amdgcn_perm(t2, t0, 0x05040100u);
                 bl[2 * hw] = __builtin_amdgcn_perm(t2, t0, 0x07060302u);
                 bh[2 * hw + 1] = __builtin_amdgcn_perm(t3, t1, 0x05040100u);
                 bl[2 * hw + 1] = __builtin_amdgcn_perm(t3, t1, 0x07060302u);
-                const uint32_t nw = ~w;
-                bs[2 * hw] = ((nw << 8) & 0x80008000u) | 0x3C003C00u;
-                bs[2 * hw + 1] = (nw & 0x80008000u) | 0x3C003C00u;
+                // +1 (0x3C00) where bit 7 of the code is set, -1 (0xBC00) where not
+                bs[2 * hw] = ((w << 8) & 0x80008000u) ^ 0xBC00BC00u;
+                bs[2 * hw + 1] = (w & 0x80008000u) ^ 0xBC00BC00u;
             }
             const half8_t Bh = __builtin_bit_cast(half8_t, make_uint4(bh[0], bh[1], bh[2], bh[3]));
             const half8_t Bl = __builtin_bit_cast(half8_t, make_uint4(bl[0], bl[1], bl[2], bl[3]));
             const half8_t Bs = __builtin_bit_cast(half8_t, make_uint4(bs[0], bs[1], bs[2], bs[3]));
-            d1 = __builtin_amdgcn_mfma_f32_16x16x32_f16(aq_hi[j], Bh, d1, 0, 0, 0);
-            d1 = __builtin_amdgcn_mfma_f32_16x16x32_f16(aq_lo[j], Bh, d1, 0, 0, 0);
-            d1 = __builtin_amdgcn_mfma_f32_16x16x32_f16(aq_hi[j], Bl, d1, 0, 0, 0);
-            d2 = __builtin_amdgcn_mfma_f32_16x16x32_f16(as_hi[j], Bs, d2, 0, 0, 0);
-            d2 = __builtin_amdgcn_mfma_f32_16x16x32_f16(as_lo[j], Bs, d2, 0, 0, 0);
+            d1 = __builtin_amdgcn_mfma_f32_16x16x32_f16(aqk[j], Bh, d1, 0, 0, 0);
+            d1 = __builtin_amdgcn_mfma_f32_16x16x32_f16(aqh[j], Bl, d1, 0, 0, 0);
+            d1 = __builtin_amdgcn_mfma_f32_16x16x32_f16(aqs[j], Bs, d1, 0, 0, 0);
         }
-        // lanes 0..15 hold D[h][n] for h = 0..3 (rows), position p0 + n
+        // lane (n, g): d1[0..3] = the four partial products of head g at position p0 + n
         const bool valid = (p0 + n_l) < p_end;
         const float qw = c.krn * qjl_factor * c.ksc;
-        float wgt[GQA];
-        float corr[GQA];
-        bool rescale = false;
+        const float sc = valid ? attn_scale * ((d1[0] + d1[1]) * c.ksc + (d1[2] + d1[3]) * qw) : -INFINITY;
+        const float cm = imh_dpp::row16_max(sc);
+        const float nm = fmaxf(m_run, cm);
+        const bool live = nm != -INFINITY;   // a head with no position yet keeps weight 0
+        const float corr = live ? __expf(m_run - nm) : 1.0f;
+        const float w = live ? __expf(sc - nm) : 0.0f;
+        l_run = l_run * corr + imh_dpp::row16_sum(w);
+        m_run = nm;
+        if (__builtin_amdgcn_ballot_w64(corr != 1.0f)) {   // some head's max grew
 #pragma unroll
-        for (int hh = 0; hh < GQA; hh++) {
-            // positions of the chunk are lanes 0..15 (one DPP row)
-            const float sc = valid ? attn_scale * (d1[hh] * c.ksc + d2[hh] * qw) : -INFINITY;
-            const float cm = imh_dpp::first_lane(imh_dpp::row16_max(sc));
-            const float nm = fmaxf(m_run[hh], cm);
-            corr[hh] = __expf(m_run[hh] - nm);
-            const float w = __expf(sc - nm);
-            const float ws = imh_dpp::first_lane(imh_dpp::row16_sum(w));
-            l_run[hh] = l_run[hh] * corr[hh] + ws;
-            m_run[hh] = nm;
-            wgt[hh] = w * c.vsc;
-            rescale |= corr[hh] != 1.0f;
+            for (int j = 0; j < 8; j++) acc[j][0] *= corr;
         }
-        if (rescale) {
+        // weights * v_scale as f16 hi + lo, transposed through LDS into operand A
+        wbuf[wave][kg][n_l] = (_Float16)(w * c.vsc);
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+        half4_t wa = {0, 0, 0, 0};
+        if (arow && ar == 0) wa = *reinterpret_cast<const half4_t *>(&wbuf[wave][ah][4 * kg]);
+        // ---- o += W . V: operand B of block j = codebook values of byte j of
+        // the four position rows ----
 #pragma unroll
-            for (int hh = 0; hh < GQA; hh++)
+        for (int j = 0; j < 8; j++) {
+            half4_t bv;
 #pragma unroll
-                for (int e = 0; e < 16; e++) o[hh][e] *= corr[hh];
-        }
-        // ---- o += w * V over the chunk: lane covers 16 dims of one position per round ----
-#pragma unroll
-        for (int r = 0; r < 2; r++) {
-            const int pi = r * 8 + vpos;
-            float wv[GQA];
-#pragma unroll
-            for (int hh = 0; hh < GQA; hh++) wv[hh] = __shfl(wgt[hh], pi);
-            const uint4 vv = r ? c.v1 : c.v0;
-            const uint32_t vw[4] = {vv.x, vv.y, vv.z, vv.w};
-#pragma unroll
-            for (int e = 0; e < 16; e++) {
-                const float v = vtab[(vw[e >> 2] >> (8 * (e & 3))) & 0xFF];
-#pragma unroll
-                for (int hh = 0; hh < GQA; hh++) o[hh][e] = __builtin_fmaf(wv[hh], v, o[hh][e]);
+            for (int i = 0; i < 4; i++) {
+                const uint32_t word = j < 4 ? c.v[i].x : c.v[i].y;
+                bv[i] = vtab[(word >> (8 * (j & 3))) & 0xFF];
             }
+            acc[j] = __builtin_amdgcn_mfma_f32_16x16x16f16(wa, bv, acc[j], 0, 0, 0);
         }
+        __builtin_amdgcn_wave_barrier();   // wbuf is rewritten next chunk
     }
 
-    // reduce the 8 position lanes that share a V slice
-#pragma unroll
-    for (int hh = 0; hh < GQA; hh++)
-#pragma unroll
-        for (int e = 0; e < 16; e++) {
-            float v = o[hh][e];
-            v += __shfl_xor(v, 8);
-            v += __shfl_xor(v, 16);
-            v += __shfl_xor(v, 32);
-            o[hh][e] = v;
-        }
-    if (lane < 8) {
-#pragma unroll
-        for (int hh = 0; hh < GQA; hh++)
-#pragma unroll
-            for (int e = 0; e < 16; e++) om[wave][hh][lane * 16 + e] = o[hh][e];
-    }
-    if (lane == 0) {
-#pragma unroll
-        for (int hh = 0; hh < GQA; hh++) {
-            mm[wave][hh] = m_run[hh];
-            ll[wave][hh] = l_run[hh];
+    // lane (c, g): acc[j][0] = o[head g][dim 8c + j]
+    if (kg < GQA) {
+        float4 *dst = reinterpret_cast<float4 *>(&om[wave][kg][n_l * 8]);
+        dst[0] = make_float4(acc[0][0], acc[1][0], acc[2][0], acc[3][0]);
+        dst[1] = make_float4(acc[4][0], acc[5][0], acc[6][0], acc[7][0]);
+        if (n_l == 0) {
+            mm[wave][kg] = m_run;
+            ll[wave][kg] = l_run;
         }
     }
     __syncthreads();

@@ -342,6 +342,11 @@ class Decoder:
     def step(self, stream: Stream, token_ids, logits):
         check(lib.imh_decoder_step(self._h, stream.handle, _ptr(token_ids), _ptr(logits)))
 
+    def write_kv(self, stream: Stream, layer: int, k_proj, v_proj, token_count: int, base_pos: int = 0):
+        """Write K/V projections [batch, token_count, nkv, head_dim] of one layer into its cache."""
+        check(lib.imh_decoder_write_kv(self._h, stream.handle, layer, _ptr(k_proj), _ptr(v_proj), token_count,
+                                       base_pos))
+
     def positions(self) -> np.ndarray:
         out = np.empty(self.cfg.batch, np.int32)
         check(lib.imh_decoder_positions(self._h, out.ctypes.data_as(C.c_void_p)))
