@@ -36,10 +36,12 @@ struct imh_buffer {
 };
 
 // Per-stream scratch memory, grown on demand by the host code of an op.
-// Slot 0: INT4 activation operand images; slot 1: attention queries and split
-// partials, the gate output of a prefill gate/up op; slot 2: GEMM split-K
-// partials.
-constexpr int kScratchSlots = 3;
+// Slot 0: INT4 activation operand images; slot 1: attention split partials,
+// the gate output of a prefill gate/up op; slot 2: GEMM split-K partials;
+// slot 3: arrival counters of split reductions (zeroed when allocated, left at
+// zero by every kernel that uses them).
+constexpr int kScratchSlots = 4;
+constexpr int kCounterSlot = 3;
 struct imh_stream {
     imh_device *dev;
     hipStream_t stream;

@@ -49,6 +49,8 @@ int stream_scratch(imh_stream *s, int slot, size_t bytes, void **out) {
         size_t want = bytes < (1u << 20) ? (1u << 20) : bytes;
         IMH_HIP(hipMalloc(&s->scratch[slot], want));
         s->scratch_bytes[slot] = want;
+        // arrival counters start at zero; kernels leave them at zero
+        if (slot == kCounterSlot) IMH_HIP(hipMemset(s->scratch[slot], 0, want));
     }
     *out = s->scratch[slot];
     return IMH_OK;
@@ -212,7 +214,7 @@ int imh_stream_create(imh_device *dev, imh_stream **out) {
     if (rc) return rc;
     hipStream_t s;
     IMH_HIP(hipStreamCreateWithFlags(&s, hipStreamNonBlocking));
-    imh_stream *st = new (std::nothrow) imh_stream{dev, s, {nullptr, nullptr, nullptr}, {0, 0, 0}, false};
+    imh_stream *st = new (std::nothrow) imh_stream{dev, s, {}, {}, false};
     if (!st) {
         (void)hipStreamDestroy(s);
         return imh::fail(IMH_ENOMEM, "imh_stream_create: host allocation failed");

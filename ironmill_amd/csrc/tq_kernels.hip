@@ -42,6 +42,8 @@ constexpr int kD = 128;          // head_dim the kernels are built for
 constexpr int kChunk = 16;       // positions per MFMA block
 constexpr int kWaves = 4;        // waves per attention workgroup
 constexpr int kSplitQuantum = kChunk * kWaves;
+constexpr int kMaxSplits = 512;     // the combining workgroup stages every split's (max, sum) in LDS
+constexpr int kAutoSplitLen = 256;  // shortest split the automatic split count makes
 
 // IEEE round-to-nearest f32 square root: the hardware v_sqrt_f32 result
 // (within 1 ulp) corrected with two fma residuals.  Inputs here are finite
@@ -135,59 +137,6 @@ __global__ void __launch_bounds__(kD) tq_cache_write_kernel(
 // ---------------------------------------------------------------------------
 // decode attention
 // ---------------------------------------------------------------------------
-// Query prep: grid (num_kv_heads, batch), block kD.  For every query head of
-// the GQA group: q_rot = D.H.D/sqrt(d) q (butterfly in LDS) and its QJL
-// projection s_q[d] = sum_k S[d][k] q_rot[k] (fmaf in increasing k, S^T read
-// coalesced).  Written once per group to qprep [batch][nh][2][kD] f32, so the
-// split workgroups of the attention kernel only load it.
-template <int GQA>
-__global__ void __launch_bounds__(kD) tq_query_prep_kernel(const __half *__restrict__ q, int nh,
-                                                           const float *__restrict__ signs,
-                                                           const float *__restrict__ qjl_t,
-                                                           float *__restrict__ qprep) {
-    __shared__ float qs[GQA][kD];
-    const int d = threadIdx.x;
-    const int kvh = blockIdx.x, b = blockIdx.y;
-    // column d of S^T, all loads in flight before anything waits
-    float sv[kD];
-#pragma unroll
-    for (int k = 0; k < kD; k++) sv[k] = qjl_t[(size_t)k * kD + d];
-    const float sg = signs[d];
-#pragma unroll
-    for (int hh = 0; hh < GQA; hh++) qs[hh][d] = __half2float(q[((size_t)b * nh + kvh * GQA + hh) * kD + d]) * sg;
-    __syncthreads();
-    for (int step = 1; step < kD; step *= 2) {
-        if (d < kD / 2) {
-            const int j = (d / step) * (step * 2) + (d % step);
-#pragma unroll
-            for (int hh = 0; hh < GQA; hh++) {
-                const float a = qs[hh][j], c = qs[hh][j + step];
-                qs[hh][j] = a + c;
-                qs[hh][j + step] = a - c;
-            }
-        }
-        __syncthreads();
-    }
-    const float rscale = 1.0f / sqrtf((float)kD);
-#pragma unroll
-    for (int hh = 0; hh < GQA; hh++) qs[hh][d] = qs[hh][d] * (sg * rscale);
-    __syncthreads();
-    float acc[GQA];
-#pragma unroll
-    for (int hh = 0; hh < GQA; hh++) acc[hh] = 0.0f;
-#pragma unroll
-    for (int k = 0; k < kD; k++) {
-#pragma unroll
-        for (int hh = 0; hh < GQA; hh++) acc[hh] = __builtin_fmaf(sv[k], qs[hh][k], acc[hh]);
-    }
-#pragma unroll
-    for (int hh = 0; hh < GQA; hh++) {
-        float *dst = qprep + ((size_t)b * nh + kvh * GQA + hh) * 2 * kD;
-        dst[d] = qs[hh][d];
-        dst[kD + d] = acc[hh];
-    }
-}
-
 // Attention: grid (num_splits, num_kv_heads, batch), block 64 * kWaves.  Each
 // wave walks its split in 16-position chunks; the codes and per-position
 // scales of the next chunk are loaded before the current one is computed.
@@ -206,13 +155,14 @@ __global__ void __launch_bounds__(kD) tq_query_prep_kernel(const __half *__restr
 // stay in VGPRs (no AGPR round trip around the softmax rescale).
 template <int GQA>
 __global__ void __launch_bounds__(64 * kWaves) tq_attention_kernel(
-    const float *__restrict__ qprep, int nh, int nkv, int max_seq, int seq_len,
-    const int32_t *__restrict__ seq_lens, float attn_scale,
-    const float *__restrict__ kcb, const float *__restrict__ vcb,
+    const __half *__restrict__ q, int nh, int nkv, int max_seq, int seq_len,
+    const int32_t *__restrict__ seq_lens, float attn_scale, const float *__restrict__ signs,
+    const float *__restrict__ qjl_t, const float *__restrict__ kcb, const float *__restrict__ vcb,
     const uint8_t *__restrict__ kcodes, const uint8_t *__restrict__ vcodes,
     const float *__restrict__ kscales, const float *__restrict__ vscales,
     const float *__restrict__ krnorm, int split_len, float *__restrict__ part_o,
-    float *__restrict__ part_m, float *__restrict__ part_l) {
+    float *__restrict__ part_m, float *__restrict__ part_l, int *__restrict__ counters,
+    __half *__restrict__ out) {
     __shared__ float qs[GQA][2][kD];
     __shared__ uint32_t ktab[256];   // entry c & 0x7F, indexed by the whole code byte
     __shared__ _Float16 vtab[256];
@@ -220,6 +170,10 @@ __global__ void __launch_bounds__(64 * kWaves) tq_attention_kernel(
     __shared__ float om[kWaves][GQA][kD];
     __shared__ float mm[kWaves][GQA];
     __shared__ float ll[kWaves][GQA];
+    __shared__ int is_last;
+    __shared__ float tail_f[GQA][kMaxSplits];   // exp(m_s - M) per head and split
+    __shared__ float tail_l[GQA];
+    __shared__ float tail_o[8][kD];              // split-subset sums, [part * GQA + head]
 
     const int tid = threadIdx.x;
     const int lane = tid & 63;
@@ -282,8 +236,43 @@ __global__ void __launch_bounds__(64 * kWaves) tq_attention_kernel(
         ktab[tid] = (uint32_t)__builtin_bit_cast(uint16_t, hi) | ((uint32_t)__builtin_bit_cast(uint16_t, lo) << 16);
     }
     vtab[tid] = (_Float16)vcb[tid];
-    const float *qg = qprep + ((size_t)b * nh + kvh * GQA) * 2 * kD;
-    for (int e = tid; e < GQA * 2 * kD; e += 64 * kWaves) (&qs[0][0][0])[e] = qg[e];
+    // query prep, per workgroup while the first chunk is in flight: q_rot =
+    // D.H.D/sqrt(d) q (butterfly in LDS) into qs[h][0], and its QJL projection
+    // s_q[d] = sum_k S[d][k] q_rot[k] (fmaf in increasing k, S^T read
+    // coalesced from L2) into qs[h][1]
+    const float rscale = 1.0f / sqrtf((float)kD);
+    for (int e = tid; e < GQA * kD; e += 64 * kWaves) {
+        const int hh = e / kD, d = e % kD;
+        qs[hh][0][d] = __half2float(q[((size_t)b * nh + kvh * GQA + hh) * kD + d]) * signs[d];
+    }
+    __syncthreads();
+    for (int step = 1; step < kD; step *= 2) {
+        if (tid < GQA * kD / 2) {
+            const int hh = tid / (kD / 2), i = tid % (kD / 2);
+            const int j = (i / step) * (step * 2) + (i % step);
+            const float x0 = qs[hh][0][j], x1 = qs[hh][0][j + step];
+            qs[hh][0][j] = x0 + x1;
+            qs[hh][0][j + step] = x0 - x1;
+        }
+        __syncthreads();
+    }
+    for (int e = tid; e < GQA * kD; e += 64 * kWaves) {
+        const int hh = e / kD, d = e % kD;
+        qs[hh][0][d] = qs[hh][0][d] * (signs[d] * rscale);
+    }
+    __syncthreads();
+    {
+        const int d = tid % kD, h0 = tid / kD;   // heads h0 and h0 + 2
+        float a0 = 0.0f, a1 = 0.0f;
+#pragma unroll 16
+        for (int k = 0; k < kD; k++) {
+            const float sv = qjl_t[(size_t)k * kD + d];
+            if (h0 < GQA) a0 = __builtin_fmaf(sv, qs[h0][0][k], a0);
+            if (h0 + 2 < GQA) a1 = __builtin_fmaf(sv, qs[h0 + 2][0][k], a1);
+        }
+        if (h0 < GQA) qs[h0][1][d] = a0;
+        if (h0 + 2 < GQA) qs[h0 + 2][1][d] = a1;
+    }
     __syncthreads();
 
     // score operands A, k-slot order within each 4-byte word: bytes {0, 2, 1, 3}.
@@ -400,6 +389,8 @@ __global__ void __launch_bounds__(64 * kWaves) tq_attention_kernel(
         }
     }
     __syncthreads();
+    // combine the waves; with one split normalise here, else publish the
+    // split's partial (o unnormalised, running max, sum)
     for (int e = tid; e < GQA * kD; e += 64 * kWaves) {
         const int hh = e / kD, d = e % kD;
         float M = -INFINITY;
@@ -413,78 +404,98 @@ __global__ void __launch_bounds__(64 * kWaves) tq_attention_kernel(
                 lv += ll[w][hh] * f;
             }
         }
-        const size_t pidx = ((size_t)b * nh + kvh * GQA + hh) * S + split;
-        part_o[pidx * kD + d] = ov;
-        if (d == 0) {
-            part_m[pidx] = M;
-            part_l[pidx] = lv;
-        }
-    }
-}
-
-// combine splits, normalise, rotate back: grid (num_heads, batch), block kD
-__global__ void __launch_bounds__(kD) tq_attention_reduce_kernel(
-    const float *__restrict__ part_o, const float *__restrict__ part_m,
-    const float *__restrict__ part_l, const float *__restrict__ signs, int nh, int S,
-    __half *__restrict__ out) {
-    __shared__ float x[kD];
-    __shared__ float fs[kD];
-    __shared__ float red[kD];
-    const int d = threadIdx.x;
-    const int h = blockIdx.x, b = blockIdx.y;
-    const size_t base = ((size_t)b * nh + h) * S;
-    // M = max over splits (threads stride the splits, then a tree in LDS)
-    float mloc = -INFINITY;
-    for (int s = d; s < S; s += kD) mloc = fmaxf(mloc, part_m[base + s]);
-    red[d] = mloc;
-    __syncthreads();
-    for (int w = kD / 2; w > 0; w >>= 1) {
-        if (d < w) red[d] = fmaxf(red[d], red[d + w]);
-        __syncthreads();
-    }
-    const float M = red[0];
-    __syncthreads();
-    // splits in tiles of kD: thread s of a tile forms its weight exp(m_s - M),
-    // then every thread d sums its output dim over the tile in split order
-    float ov = 0.0f, lloc = 0.0f;
-    for (int s0 = 0; s0 < S; s0 += kD) {
-        const int s = s0 + d;
-        float f = 0.0f;
-        if (s < S) {
-            const float m = part_m[base + s];
-            if (m != -INFINITY) {
-                f = __expf(m - M);
-                lloc += part_l[base + s] * f;
+        if (S == 1) {
+            qs[hh][0][d] = (ov / fmaxf(lv, 1e-10f)) * signs[d];
+        } else {
+            // agent-scope stores write through to memory, so the workgroup that
+            // combines the splits sees them from any XCD without flushing L2
+            const size_t pidx = ((size_t)b * nh + kvh * GQA + hh) * S + split;
+            __hip_atomic_store(&part_o[pidx * kD + d], ov, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            if (d == 0) {
+                __hip_atomic_store(&part_m[pidx], M, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                __hip_atomic_store(&part_l[pidx], lv, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
             }
         }
-        fs[d] = f;
-        __syncthreads();
-        const int n = min(kD, S - s0);
-#pragma unroll 8
-        for (int i = 0; i < n; i++) ov = __builtin_fmaf(part_o[(base + s0 + i) * kD + d], fs[i], ov);
-        __syncthreads();
     }
-    red[d] = lloc;
-    __syncthreads();
-    for (int w = kD / 2; w > 0; w >>= 1) {
-        if (d < w) red[d] += red[d + w];
+    if (S > 1) {
+        // the last of the group's S workgroups to arrive combines every split
+        // (log-sum-exp, fused_sdpa_reduce semantics); nobody waits, so the
+        // grid needs no co-residency.  Each thread's partial stores complete
+        // before the arrival is counted; the counter is left at zero.
+        __builtin_amdgcn_s_waitcnt(0);
         __syncthreads();
+        if (tid == 0)
+            is_last = __hip_atomic_fetch_add(&counters[b * nkv + kvh], 1, __ATOMIC_RELAXED,
+                                             __HIP_MEMORY_SCOPE_AGENT) == S - 1;
+        __syncthreads();
+        if (!is_last) return;
+        // one invalidation of this XCD's caches, then ordinary (batched) loads
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
+        const size_t gbase = ((size_t)b * nh + kvh * GQA) * S;   // head hh at gbase + hh * S
+        for (int i = tid; i < GQA * S; i += 64 * kWaves) tail_f[i / S][i % S] = part_m[gbase + i];
+        __syncthreads();
+        // per head: M = max over splits, f_s = exp(m_s - M), l = sum f_s l_s
+        // (one wave per head, lanes stride the splits, then a DPP/shuffle sum)
+        if (wave < GQA) {
+            float mx = -INFINITY;
+            for (int sp = lane; sp < S; sp += 64) mx = fmaxf(mx, tail_f[wave][sp]);
+            mx = fmaxf(mx, __shfl_xor(mx, 32));
+            mx = fmaxf(mx, __shfl_xor(mx, 16));
+            mx = imh_dpp::row16_max(mx);
+            float lsum = 0.0f;
+            for (int sp = lane; sp < S; sp += 64) {
+                const float m = tail_f[wave][sp];
+                const float f = (mx == -INFINITY || m == -INFINITY) ? 0.0f : __expf(m - mx);
+                tail_f[wave][sp] = f;
+                lsum += f * part_l[gbase + (size_t)wave * S + sp];
+            }
+            lsum = imh_dpp::row16_sum(lsum);
+            lsum += __shfl_xor(lsum, 16);
+            lsum += __shfl_xor(lsum, 32);
+            if (lane == 0) tail_l[wave] = lsum;
+        }
+        __syncthreads();
+        // o[h][4q..4q+3] = sum_s f_s o_s: 256 threads = GQA heads x 32 dim quads x
+        // (8 / GQA) split subsets, float4 loads, 16 in flight per thread
+        constexpr int kParts = 8 / GQA;
+        const int quad = tid & 31, hh = (tid >> 5) % GQA, part = (tid >> 5) / GQA;
+        const float4 *po4 = reinterpret_cast<const float4 *>(part_o + (gbase + (size_t)hh * S) * kD) + quad;
+        float4 acc4 = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+#pragma unroll 16
+        for (int sp = part; sp < S; sp += kParts) {
+            const float4 v = po4[(size_t)sp * (kD / 4)];
+            const float f = tail_f[hh][sp];
+            acc4.x = __builtin_fmaf(v.x, f, acc4.x);
+            acc4.y = __builtin_fmaf(v.y, f, acc4.y);
+            acc4.z = __builtin_fmaf(v.z, f, acc4.z);
+            acc4.w = __builtin_fmaf(v.w, f, acc4.w);
+        }
+        reinterpret_cast<float4 *>(&tail_o[part * GQA + hh][0])[quad] = acc4;
+        __syncthreads();
+        for (int e = tid; e < GQA * kD; e += 64 * kWaves) {
+            const int h2 = e / kD, d = e % kD;
+            float ov = 0.0f;
+            for (int pp = 0; pp < kParts; pp++) ov += tail_o[pp * GQA + h2][d];
+            qs[h2][0][d] = (ov / fmaxf(tail_l[h2], 1e-10f)) * signs[d];
+        }
+        if (tid == 0) __hip_atomic_store(&counters[b * nkv + kvh], 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
-    const float lv = red[0];
-    const float sg = signs[d];
-    x[d] = (ov / fmaxf(lv, 1e-10f)) * sg;
     __syncthreads();
+    // rotate back: o = D.H.D/sqrt(d) o_rot
     for (int step = 1; step < kD; step *= 2) {
-        if (d < kD / 2) {
-            const int j = (d / step) * (step * 2) + (d % step);
-            const float a = x[j], c = x[j + step];
-            x[j] = a + c;
-            x[j + step] = a - c;
+        if (tid < GQA * kD / 2) {
+            const int hh = tid / (kD / 2), i = tid % (kD / 2);
+            const int j = (i / step) * (step * 2) + (i % step);
+            const float x0 = qs[hh][0][j], x1 = qs[hh][0][j + step];
+            qs[hh][0][j] = x0 + x1;
+            qs[hh][0][j + step] = x0 - x1;
         }
         __syncthreads();
     }
-    const float rscale = 1.0f / sqrtf((float)kD);
-    out[((size_t)b * nh + h) * kD + d] = __float2half(x[d] * (sg * rscale));
+    for (int e = tid; e < GQA * kD; e += 64 * kWaves) {
+        const int hh = e / kD, d = e % kD;
+        out[((size_t)b * nh + kvh * GQA + hh) * kD + d] = __float2half(qs[hh][0][d] * (signs[d] * rscale));
+    }
 }
 
 int check_cache(const imh_tq_tables *t, const imh_tq_kv_cache *c, const char *who) {
@@ -551,55 +562,52 @@ int imh_encode_turboquant_attention(imh_stream *stream, const imh_tq_tables *t,
     rc = imh::use_device(stream->dev);
     if (rc) return rc;
 
-    // KV split: aim for ~512 workgroups (2 per CU, 8 waves) with >= 64
-    // positions each; a wave keeps one chunk in flight ahead of the one it
-    // computes.
-    // with per-sequence lengths the splits span the bound (0 = max_seq_len)
+    // KV split: by default ~512 workgroups, but no split shorter than 256
+    // positions (the combining workgroup's work grows with the split count;
+    // measured best at ctx 8k and 32k, batch 1 to 16).  Explicit num_splits
+    // may go down to 64 positions per split.  With per-sequence lengths the
+    // splits span the bound (0 = max_seq_len).
     const uint32_t L = seq_lens && seq_len == 0 ? cache->max_seq_len : seq_len;
     const uint32_t B = cache->batch;
     uint32_t want = num_splits;
     if (want == 0) {
         const uint32_t groups = B * nkv;
-        want = (512 + groups - 1) / groups;
+        want = std::min<uint32_t>((512 + groups - 1) / groups, std::max<uint32_t>(1, L / kAutoSplitLen));
     }
     const uint32_t max_splits = std::max<uint32_t>(1, (L + kSplitQuantum - 1) / kSplitQuantum);
-    want = std::max<uint32_t>(1, std::min(want, max_splits));
+    want = std::max<uint32_t>(1, std::min(want, std::min<uint32_t>(max_splits, kMaxSplits)));
     uint32_t split_len = (L + want - 1) / want;
     split_len = std::max<uint32_t>(kSplitQuantum,
                                    (split_len + kSplitQuantum - 1) / kSplitQuantum * kSplitQuantum);
-    const uint32_t S = std::max<uint32_t>(1, (L + split_len - 1) / split_len);
+    const uint32_t S = std::max<uint32_t>(1, (L + split_len - 1) / split_len);   // <= kMaxSplits
 
-    // scratch: prepared queries [B][nh][2][kD], then the split partials
-    const size_t nq = (size_t)B * num_heads * 2 * kD;
+    // scratch: split partials and the groups' arrival counters (none for one split)
     const size_t nparts = (size_t)B * num_heads * S;
-    const size_t need = nq * 4 + nparts * kD * 4 + nparts * 8 + 512;
-    void *scr = nullptr;
-    rc = imh::stream_scratch(stream, 1, need, &scr);
-    if (rc) return rc;
-    float *qprep = static_cast<float *>(scr);
-    float *po = qprep + nq;
-    float *pm = po + nparts * kD;
-    float *pl = pm + nparts;
-
+    float *po = nullptr, *pm = nullptr, *pl = nullptr;
+    int *ctr = nullptr;
+    if (S > 1) {
+        void *scr = nullptr, *cs = nullptr;
+        rc = imh::stream_scratch(stream, 1, nparts * kD * 4 + nparts * 8 + 512, &scr);
+        if (rc) return rc;
+        rc = imh::stream_scratch(stream, kCounterSlot, (size_t)B * nkv * 4, &cs);
+        if (rc) return rc;
+        po = static_cast<float *>(scr);
+        pm = po + nparts * kD;
+        pl = pm + nparts;
+        ctr = static_cast<int *>(cs);
+    }
     const __half *qh = reinterpret_cast<const __half *>(q);
     dim3 grid(S, nkv, B);
-#define IMH_TQ_LAUNCH(G)                                                                              \
-    do {                                                                                              \
-        hipLaunchKernelGGL(tq_query_prep_kernel<G>, dim3(nkv, B), dim3(kD), 0, stream->stream, qh,    \
-                           (int)num_heads, t->signs, t->qjl_t, qprep);                                \
-        hipLaunchKernelGGL(tq_attention_kernel<G>, grid, dim3(64 * kWaves), 0, stream->stream, qprep, \
-                           (int)num_heads, (int)nkv, (int)cache->max_seq_len, (int)L, seq_lens, \
-                           attn_scale, t->k_codebook, t->v_codebook, cache->k_codes, cache->v_codes,  \
-                           cache->k_scales, cache->v_scales, cache->k_r_norms, (int)split_len, po, pm, \
-                           pl);                                                                       \
-    } while (0)
+#define IMH_TQ_LAUNCH(G)                                                                                     \
+    hipLaunchKernelGGL(tq_attention_kernel<G>, grid, dim3(64 * kWaves), 0, stream->stream, qh, (int)num_heads, \
+                       (int)nkv, (int)cache->max_seq_len, (int)L, seq_lens, attn_scale, t->signs, t->qjl_t,     \
+                       t->k_codebook, t->v_codebook, cache->k_codes, cache->v_codes, cache->k_scales,           \
+                       cache->v_scales, cache->k_r_norms, (int)split_len, po, pm, pl, ctr,                      \
+                       reinterpret_cast<__half *>(out))
     if (gqa == 4) IMH_TQ_LAUNCH(4);
     else if (gqa == 2) IMH_TQ_LAUNCH(2);
     else IMH_TQ_LAUNCH(1);
 #undef IMH_TQ_LAUNCH
-    IMH_HIP(hipGetLastError());
-    hipLaunchKernelGGL(tq_attention_reduce_kernel, dim3(num_heads, B), dim3(kD), 0, stream->stream, po,
-                       pm, pl, t->signs, (int)num_heads, (int)S, reinterpret_cast<__half *>(out));
     IMH_HIP(hipGetLastError());
     return IMH_OK;
 }
