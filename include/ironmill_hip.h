@@ -241,6 +241,13 @@ int imh_encode_turboquant_cache_write(imh_stream *stream, const imh_tq_tables *t
                                       uint32_t token_count, uint32_t base_pos,
                                       const int32_t *positions, int is_k);
 
+/* Both writes of encode_kv_cache_and_attention (attention.rs:344-391) in one
+ * launch: K from k_proj, V from v_proj, same layout and positions as above. */
+int imh_encode_turboquant_cache_write_kv(imh_stream *stream, const imh_tq_tables *t,
+                                         const imh_tq_kv_cache *cache, const uint16_t *k_proj,
+                                         const uint16_t *v_proj, uint32_t token_count,
+                                         uint32_t base_pos, const int32_t *positions);
+
 /* Decode attention over the cache (turboquant_attention, turboquant.metal:202-462,
  * + the split/LSE combine of fused_sdpa_reduce, flash_decode.metal:163-215):
  * q [batch][num_heads][head_dim] f16, GQA head h reads kv head h/(num_heads/num_kv_heads),
@@ -442,6 +449,12 @@ int imh_decoder_reset(imh_decoder *d, imh_stream *stream, const int32_t *positio
 /* Encode one step (pipeline.rs:424-1172 for token_count 1).  IMH_ERANGE when a
  * position has reached max_seq_len (cache.rs:494-504). */
 int imh_decoder_step(imh_decoder *d, imh_stream *stream, const uint32_t *token_ids, uint16_t *logits);
+/* Write token_count K/V projections ([batch][token_count][num_kv_heads][head_dim]
+ * f16) of one layer into its cache at positions base_pos.. (the cache-write half
+ * of encode_kv_cache_and_attention, attention.rs:344-391 / :497-525, as a
+ * prefill would run it). */
+int imh_decoder_write_kv(imh_decoder *d, imh_stream *stream, uint32_t layer, const uint16_t *k_proj,
+                         const uint16_t *v_proj, uint32_t token_count, uint32_t base_pos);
 /* Host mirror of the positions after the encoded steps (host int32 [batch]). */
 int imh_decoder_positions(const imh_decoder *d, int32_t *out);
 /* The KV cache of one layer (a view; the decoder owns the memory). */

@@ -222,6 +222,7 @@ SIGNATURES = {
     "imh_tq_tables_read": (I, [P, I, P, SZ, C.POINTER(SZ)]),
     "imh_tq_cache_sizes": (I, [U32, U32, U32, U32, C.POINTER(SZ), C.POINTER(SZ)]),
     "imh_encode_turboquant_cache_write": (I, [P, P, C.POINTER(TqKvCache), P, U32, U32, P, I]),
+    "imh_encode_turboquant_cache_write_kv": (I, [P, P, C.POINTER(TqKvCache), P, P, U32, U32, P]),
     "imh_encode_turboquant_attention": (I, [P, P, C.POINTER(TqKvCache), P, U32, U32, P, C.c_float, P,
                                             U32]),
     "imh_encode_kv_cache_and_attention": (I, [P, P, C.POINTER(TqKvCache), P, P, P, U32, U32, C.c_float,

@@ -327,8 +327,7 @@ int imh_decoder_step(imh_decoder *d, imh_stream *s, const uint32_t *token_ids, u
         IMH_TRY(imh_encode_qk_norm_rope(s, &qp));
         if (c.kv_cache == IMH_KV_TURBOQUANT) {
             const imh_tq_kv_cache *kc = &d->tq_caches[l];
-            IMH_TRY(imh_encode_turboquant_cache_write(s, d->tq, kc, d->k, 1, 0, d->positions, 1));
-            IMH_TRY(imh_encode_turboquant_cache_write(s, d->tq, kc, d->v, 1, 0, d->positions, 0));
+            IMH_TRY(imh_encode_turboquant_cache_write_kv(s, d->tq, kc, d->k, d->v, 1, 0, d->positions));
             IMH_TRY(imh_encode_turboquant_attention(s, d->tq, kc, d->q, c.num_heads, 0, d->seq_lens, c.attn_scale,
                                                     d->attn_out, 0));
         } else {
@@ -379,11 +378,8 @@ int imh_decoder_write_kv(imh_decoder *d, imh_stream *s, uint32_t layer, const ui
     if ((uint64_t)base_pos + token_count > d->cfg.max_seq_len)
         return imh::fail(IMH_ERANGE, "imh_decoder_write_kv: base_pos + token_count beyond max_seq_len");
     if (d->cfg.kv_cache == IMH_KV_TURBOQUANT) {
-        int rc = imh_encode_turboquant_cache_write(s, d->tq, &d->tq_caches[layer], k_proj, token_count, base_pos,
-                                                   nullptr, 1);
-        if (rc) return rc;
-        return imh_encode_turboquant_cache_write(s, d->tq, &d->tq_caches[layer], v_proj, token_count, base_pos,
-                                                 nullptr, 0);
+        return imh_encode_turboquant_cache_write_kv(s, d->tq, &d->tq_caches[layer], k_proj, v_proj, token_count,
+                                                    base_pos, nullptr);
     }
     int rc = imh_encode_kv_scatter(s, &d->fp16_caches[layer], k_proj, token_count, base_pos, nullptr, 1);
     if (rc) return rc;

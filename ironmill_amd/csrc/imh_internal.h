@@ -70,6 +70,15 @@ struct imh_tq_tables {
     float *base;
     float *signs, *k_codebook, *k_bounds, *v_codebook, *v_bounds, *qjl, *qjl_t;
     size_t total_floats;
+    // Exact fast form of the reference's index rule idx = 1 + max{j : u >= bd[j]}
+    // (0 if none), for any boundary order: the boundaries sorted by value (NaN
+    // dropped) with the running maximum of j + 1; idx = prefix max at
+    // upper_bound(u), 0 at position 0.  One device allocation:
+    //   k_sorted[k_search] f32 | k_prefmax[k_search] i32 | v_sorted | v_prefmax
+    void *search_base;
+    const float *k_sorted, *v_sorted;
+    const int32_t *k_prefmax, *v_prefmax;
+    int k_search, v_search;
 };
 
 namespace imh {

@@ -61,77 +61,142 @@ __device__ __forceinline__ float sqrt_rn(float x) {
 }
 
 // ---------------------------------------------------------------------------
-// cache write: grid (num_kv_heads, token_count, batch), block kD
+// cache write: one wave per (tensor, kv head, token, sequence); lane l holds
+// elements l and l + 64.  The Walsh-Hadamard butterfly (strides 1..32 across
+// lanes by xor shuffles, 64 inside the lane) and the halving-stride tree sums
+// (64 inside the lane, 32..1 by down shuffles) keep the f32 order of a
+// 128-element LDS tree bit for bit, with no workgroup barrier.
 // ---------------------------------------------------------------------------
-__global__ void __launch_bounds__(kD) tq_cache_write_kernel(
-    const __half *__restrict__ kv, int tokens, int nkv, int max_seq, int base_pos,
-    const int32_t *__restrict__ positions, int is_k, const float *__restrict__ signs,
-    const float *__restrict__ codebook, const float *__restrict__ bounds, int n_levels,
-    const float *__restrict__ qjl_t, uint8_t *__restrict__ cache, float *__restrict__ scales,
-    float *__restrict__ r_norms) {
+struct TqWriteArgs {
+    const __half *kv[2];   // [0] K, [1] V projections [batch][tokens][nkv][kD]
+    uint8_t *codes[2];
+    float *scales[2];
+    float *r_norms;        // K only
+    const float *codebook[2];
+    const float *sorted[2];      // boundaries sorted by value (NaN dropped)
+    const int32_t *prefmax[2];   // running max of (original index + 1)
+    int n_search[2];
+};
+
+constexpr int kWriteMaxWaves = 16;
+
+// grid (tokens, batch), block 64 * W with W = min(16, nkv * count): every K
+// and V vector of one token, one wave each (looping when there are more than
+// 16); vector v is tensor first + v / nkv, kv head v % nkv.  The QJL matrix is
+// staged into LDS once per workgroup by all threads (64 KB, one round trip).
+__global__ void __launch_bounds__(64 * kWriteMaxWaves) tq_cache_write_kernel(
+    const TqWriteArgs a, int first, int count, int tokens, int nkv, int max_seq, int base_pos,
+    const int32_t *__restrict__ positions, const float *__restrict__ signs, const float *__restrict__ qjl_t) {
 #pragma clang fp contract(off)
-    __shared__ float x[kD];
-    __shared__ float red[kD];
-    __shared__ float res[kD];
-    __shared__ float bnd[256];
+    __shared__ float sqt[kD * kD];   // S^T, row k = column k of S
+    __shared__ float bnd[2][256];    // sorted boundaries
+    __shared__ int32_t bpm[2][256];  // prefix max of index + 1
+    __shared__ float res[kWriteMaxWaves][kD];
 
-    const int i = threadIdx.x;
-    const int h = blockIdx.x, t = blockIdx.y, b = blockIdx.z;
-    const int nb = n_levels - 1;
-    for (int j = i; j < nb; j += kD) bnd[j] = bounds[j];
-
+    const int tid = threadIdx.x;
+    const int lane = tid & 63, wave = tid >> 6;
+    const int W = blockDim.x >> 6;
+    const int t = blockIdx.x, b = blockIdx.y;
+    const bool has_k = first == 0;
+    // this wave's first vector, the signs and the position are loaded before
+    // the table staging so that every load of the workgroup is in flight at once
+    auto src_of = [&](int v) {
+        return a.kv[first + v / nkv] + (((size_t)b * tokens + t) * nkv + v % nkv) * kD;
+    };
+    const int v0 = wave;
+    __half pre0 = __float2half(0.0f), pre1 = __float2half(0.0f);
+    if (v0 < nkv * count) {
+        pre0 = src_of(v0)[lane];
+        pre1 = src_of(v0)[lane + 64];
+    }
+    const float sg0 = signs[lane], sg1 = signs[lane + 64];
     const long long start = positions ? (long long)positions[b] : (long long)base_pos;
+    if (has_k) {
+        const float4 *src4 = reinterpret_cast<const float4 *>(qjl_t);
+        float4 *dst4 = reinterpret_cast<float4 *>(sqt);
+        for (int e = tid; e < kD * kD / 4; e += blockDim.x) dst4[e] = src4[e];
+    }
+    for (int w = first; w < first + count; w++)
+        for (int j = tid; j < a.n_search[w]; j += blockDim.x) {
+            bnd[w][j] = a.sorted[w][j];
+            bpm[w][j] = a.prefmax[w][j];
+        }
+    __syncthreads();
+
     long long pl = (start + t) % max_seq;
     if (pl < 0) pl += max_seq;
-    const size_t slot = ((size_t)b * nkv + h) * (size_t)max_seq + (size_t)pl;
-    const size_t src = (((size_t)b * tokens + t) * nkv + h) * kD;
-
-    const float sg = signs[i];
-    x[i] = __half2float(kv[src + i]) * sg;
-    __syncthreads();
-    for (int step = 1; step < kD; step *= 2) {
-        if (i < kD / 2) {
-            const int j = (i / step) * (step * 2) + (i % step);
-            const float a = x[j], c = x[j + step];
-            x[j] = a + c;
-            x[j + step] = a - c;
-        }
-        __syncthreads();
-    }
     const float rscale = 1.0f / sqrtf((float)kD);
-    const float xr = x[i] * (sg * rscale);
+    auto tree_sum = [&](float sq0, float sq1) {
+        float v = sq0 + sq1;
+        for (int sh = 32; sh > 0; sh >>= 1) v = v + __shfl_down(v, sh);
+        return __shfl(v, 0);
+    };
 
-    red[i] = xr * xr;
-    __syncthreads();
-    for (int s = kD / 2; s > 0; s >>= 1) {
-        if (i < s) red[i] = red[i] + red[i + s];
-        __syncthreads();
-    }
-    const float l2 = sqrt_rn(fmaxf(red[0], 1e-20f));
-    const float inv = __fdiv_rn(1.0f, fmaxf(l2, 1e-10f));
-    const float u = xr * inv;
-    int idx = 0;
-    for (int j = 0; j < nb; j++) idx = (u >= bnd[j]) ? j + 1 : idx;
-    uint32_t code = (uint32_t)idx;
-
-    if (is_k) {
-        const float r = u - codebook[idx];
-        res[i] = r;
-        __syncthreads();  // every lane has read red[0] above
-        red[i] = r * r;
-        __syncthreads();
-        for (int s = kD / 2; s > 0; s >>= 1) {
-            if (i < s) red[i] = red[i] + red[i + s];
-            __syncthreads();
+    for (int v = wave; v < nkv * count; v += W) {
+        const int which = first + v / nkv, h = v % nkv;
+        const int nb = a.n_search[which];
+        const size_t slot = ((size_t)b * nkv + h) * (size_t)max_seq + (size_t)pl;
+        const __half *src = src_of(v);
+        const __half e0 = v == v0 ? pre0 : src[lane];
+        const __half e1 = v == v0 ? pre1 : src[lane + 64];
+        float x0 = __half2float(e0) * sg0;
+        float x1 = __half2float(e1) * sg1;
+        for (int step = 1; step < 64; step *= 2) {
+            const float p0 = __shfl_xor(x0, step), p1 = __shfl_xor(x1, step);
+            const bool upper = (lane & step) != 0;   // element j + step of the pair: a - c
+            x0 = upper ? p0 - x0 : x0 + p0;
+            x1 = upper ? p1 - x1 : x1 + p1;
         }
-        const float rn = sqrt_rn(fmaxf(red[0], 1e-20f));
-        float acc = 0.0f;
-        for (int k = 0; k < kD; k++) acc = __builtin_fmaf(qjl_t[(size_t)k * kD + i], res[k], acc);
-        if (acc >= 0.0f) code |= 0x80u;
-        if (i == 0) r_norms[slot] = rn;
+        {
+            const float lo = x0, hi = x1;   // stride 64: elements lane and lane + 64
+            x0 = lo + hi;
+            x1 = lo - hi;
+        }
+        const float xr0 = x0 * (sg0 * rscale), xr1 = x1 * (sg1 * rscale);
+        const float l2 = sqrt_rn(fmaxf(tree_sum(xr0 * xr0, xr1 * xr1), 1e-20f));
+        const float inv = __fdiv_rn(1.0f, fmaxf(l2, 1e-10f));
+        const float u0 = xr0 * inv, u1 = xr1 * inv;
+        const float *bd = bnd[which];
+        const int32_t *pm = bpm[which];
+        // 1 + the last j with u >= boundary[j] in the table's own order (0 if
+        // none): the boundaries that u passes are a prefix of the sorted ones,
+        // so the answer is the prefix max there (turboquant.metal:118-124)
+        auto find = [&](float u) {
+            int lo = 0, hi = nb;
+            while (lo < hi) {
+                const int mid = (lo + hi) >> 1;
+                if (u >= bd[mid]) lo = mid + 1;
+                else hi = mid;
+            }
+            return lo == 0 ? 0 : pm[lo - 1];
+        };
+        uint32_t code0 = (uint32_t)find(u0), code1 = (uint32_t)find(u1);
+
+        if (which == 0) {
+            const float *cb = a.codebook[0];
+            const float r0 = u0 - cb[code0], r1 = u1 - cb[code1];
+            const float rn = sqrt_rn(fmaxf(tree_sum(r0 * r0, r1 * r1), 1e-20f));
+            res[wave][lane] = r0;
+            res[wave][lane + 64] = r1;
+            __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+            __builtin_amdgcn_wave_barrier();
+            __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+            float acc0 = 0.0f, acc1 = 0.0f;
+#pragma unroll 16
+            for (int k = 0; k < kD; k++) {
+                const float rk = res[wave][k];
+                acc0 = __builtin_fmaf(sqt[k * kD + lane], rk, acc0);
+                acc1 = __builtin_fmaf(sqt[k * kD + lane + 64], rk, acc1);
+            }
+            if (acc0 >= 0.0f) code0 |= 0x80u;
+            if (acc1 >= 0.0f) code1 |= 0x80u;
+            if (lane == 0) a.r_norms[slot] = rn;
+            __builtin_amdgcn_wave_barrier();   // res[wave] is rewritten by the next vector
+        }
+        a.codes[which][slot * kD + lane] = (uint8_t)code0;
+        a.codes[which][slot * kD + lane + 64] = (uint8_t)code1;
+        if (lane == 0) a.scales[which][slot] = l2;
     }
-    cache[slot * kD + i] = (uint8_t)code;
-    if (i == 0) scales[slot] = l2;
 }
 
 // ---------------------------------------------------------------------------
@@ -517,28 +582,59 @@ int check_cache(const imh_tq_tables *t, const imh_tq_kv_cache *c, const char *wh
 
 extern "C" {
 
+static int launch_cache_write(imh_stream *stream, const imh_tq_tables *t, const imh_tq_kv_cache *cache,
+                              const uint16_t *k_proj, const uint16_t *v_proj, uint32_t token_count,
+                              uint32_t base_pos, const int32_t *positions, const char *who) {
+    int rc = check_cache(t, cache, who);
+    if (rc) return rc;
+    if (token_count == 0) return IMH_OK;
+    rc = imh::use_device(stream->dev);
+    if (rc) return rc;
+    TqWriteArgs a{};
+    a.kv[0] = reinterpret_cast<const __half *>(k_proj);
+    a.kv[1] = reinterpret_cast<const __half *>(v_proj);
+    a.codes[0] = cache->k_codes;
+    a.codes[1] = cache->v_codes;
+    a.scales[0] = cache->k_scales;
+    a.scales[1] = cache->v_scales;
+    a.r_norms = cache->k_r_norms;
+    a.codebook[0] = t->k_codebook;
+    a.codebook[1] = t->v_codebook;
+    a.sorted[0] = t->k_sorted;
+    a.sorted[1] = t->v_sorted;
+    a.prefmax[0] = t->k_prefmax;
+    a.prefmax[1] = t->v_prefmax;
+    a.n_search[0] = t->k_search;
+    a.n_search[1] = t->v_search;
+    const int first = k_proj ? 0 : 1;
+    const int count = (k_proj ? 1 : 0) + (v_proj ? 1 : 0);
+    const int waves = (int)std::min<uint32_t>(kWriteMaxWaves, cache->num_kv_heads * count);
+    if (cache->batch > 65535) return imh::fail(IMH_EINVAL, std::string(who) + ": batch above 65535");
+    dim3 grid(token_count, cache->batch);
+    hipLaunchKernelGGL(tq_cache_write_kernel, grid, dim3(64 * waves), 0, stream->stream, a, first, count,
+                       (int)token_count, (int)cache->num_kv_heads, (int)cache->max_seq_len, (int)base_pos,
+                       positions, t->signs, t->qjl_t);
+    IMH_HIP(hipGetLastError());
+    return IMH_OK;
+}
+
 int imh_encode_turboquant_cache_write(imh_stream *stream, const imh_tq_tables *t,
                                       const imh_tq_kv_cache *cache, const uint16_t *kv_proj,
                                       uint32_t token_count, uint32_t base_pos,
                                       const int32_t *positions, int is_k) {
     const char *who = "imh_encode_turboquant_cache_write";
     if (!stream || !kv_proj) return imh::fail(IMH_EINVAL, std::string(who) + ": NULL argument");
-    int rc = check_cache(t, cache, who);
-    if (rc) return rc;
-    if (token_count == 0) return IMH_OK;
-    rc = imh::use_device(stream->dev);
-    if (rc) return rc;
-    const int nlev = is_k ? (1 << (t->n_bits - 1)) : (1 << t->n_bits);
-    dim3 grid(cache->num_kv_heads, token_count, cache->batch);
-    hipLaunchKernelGGL(tq_cache_write_kernel, grid, dim3(kD), 0, stream->stream,
-                       reinterpret_cast<const __half *>(kv_proj), (int)token_count,
-                       (int)cache->num_kv_heads, (int)cache->max_seq_len, (int)base_pos, positions,
-                       is_k ? 1 : 0, t->signs, is_k ? t->k_codebook : t->v_codebook,
-                       is_k ? t->k_bounds : t->v_bounds, nlev, t->qjl_t,
-                       is_k ? cache->k_codes : cache->v_codes, is_k ? cache->k_scales : cache->v_scales,
-                       cache->k_r_norms);
-    IMH_HIP(hipGetLastError());
-    return IMH_OK;
+    return launch_cache_write(stream, t, cache, is_k ? kv_proj : nullptr, is_k ? nullptr : kv_proj, token_count,
+                              base_pos, positions, who);
+}
+
+int imh_encode_turboquant_cache_write_kv(imh_stream *stream, const imh_tq_tables *t,
+                                         const imh_tq_kv_cache *cache, const uint16_t *k_proj,
+                                         const uint16_t *v_proj, uint32_t token_count, uint32_t base_pos,
+                                         const int32_t *positions) {
+    const char *who = "imh_encode_turboquant_cache_write_kv";
+    if (!stream || !k_proj || !v_proj) return imh::fail(IMH_EINVAL, std::string(who) + ": NULL argument");
+    return launch_cache_write(stream, t, cache, k_proj, v_proj, token_count, base_pos, positions, who);
 }
 
 int imh_encode_turboquant_attention(imh_stream *stream, const imh_tq_tables *t,
@@ -622,9 +718,7 @@ int imh_encode_kv_cache_and_attention(imh_stream *stream, const imh_tq_tables *t
     if ((uint64_t)seq_pos + 1 > cache->max_seq_len)
         return imh::fail(IMH_ERANGE, std::string(who) + ": position " + std::to_string(seq_pos) +
                                          " is beyond max_seq_len " + std::to_string(cache->max_seq_len));
-    rc = imh_encode_turboquant_cache_write(stream, t, cache, k_proj, 1, seq_pos, nullptr, 1);
-    if (rc) return rc;
-    rc = imh_encode_turboquant_cache_write(stream, t, cache, v_proj, 1, seq_pos, nullptr, 0);
+    rc = imh_encode_turboquant_cache_write_kv(stream, t, cache, k_proj, v_proj, 1, seq_pos, nullptr);
     if (rc) return rc;
     return imh_encode_turboquant_attention(stream, t, cache, q, num_heads, seq_pos + 1, nullptr, attn_scale,
                                            out, 0);

@@ -11,6 +11,7 @@
 // tables are still moving when the 200-iteration cap stops them.
 #include <hip/hip_runtime.h>
 
+#include <algorithm>
 #include <cmath>
 #include <cstring>
 #include <new>
@@ -208,6 +209,49 @@ int upload(imh_device *dev, uint32_t d, uint32_t bits, const float *signs, const
     t->v_bounds = t->v_codebook + nv;
     t->qjl = t->v_bounds + (nv - 1);
     t->qjl_t = t->qjl + dd;
+    // search tables for the index rule (see imh_tq_tables)
+    auto build = [](const float *bd, size_t n, std::vector<float> &sv, std::vector<int32_t> &pm) {
+        std::vector<std::pair<float, int32_t>> e;
+        for (size_t j = 0; j < n; j++)
+            if (!std::isnan(bd[j])) e.emplace_back(bd[j], (int32_t)(j + 1));
+        std::stable_sort(e.begin(), e.end(), [](const auto &x, const auto &y) { return x.first < y.first; });
+        int32_t run = 0;
+        for (const auto &p : e) {
+            run = std::max(run, p.second);
+            sv.push_back(p.first);
+            pm.push_back(run);
+        }
+    };
+    std::vector<float> ks, vs;
+    std::vector<int32_t> kp, vp;
+    build(kbd, nk - 1, ks, kp);
+    build(vbd, nv - 1, vs, vp);
+    const size_t sbytes = 4 * (2 * ks.size() + 2 * vs.size()) + 16;
+    std::vector<uint8_t> sh(sbytes, 0);
+    size_t so = 0;
+    auto put_bytes = [&](const void *src, size_t bytes) {
+        std::memcpy(sh.data() + so, src, bytes);
+        so += bytes;
+    };
+    put_bytes(ks.data(), 4 * ks.size());
+    put_bytes(kp.data(), 4 * kp.size());
+    put_bytes(vs.data(), 4 * vs.size());
+    put_bytes(vp.data(), 4 * vp.size());
+    e = hipMalloc(&t->search_base, sbytes);
+    if (e == hipSuccess) e = hipMemcpy(t->search_base, sh.data(), sbytes, hipMemcpyHostToDevice);
+    if (e != hipSuccess) {
+        if (t->search_base) (void)hipFree(t->search_base);
+        (void)hipFree(base);
+        delete t;
+        return imh::hip_fail(e, "imh_tq_tables: search tables");
+    }
+    uint8_t *sb = static_cast<uint8_t *>(t->search_base);
+    t->k_search = (int)ks.size();
+    t->v_search = (int)vs.size();
+    t->k_sorted = reinterpret_cast<const float *>(sb);
+    t->k_prefmax = reinterpret_cast<const int32_t *>(sb + 4 * ks.size());
+    t->v_sorted = reinterpret_cast<const float *>(sb + 8 * ks.size());
+    t->v_prefmax = reinterpret_cast<const int32_t *>(sb + 8 * ks.size() + 4 * vs.size());
     *out = t;
     return IMH_OK;
 }
@@ -275,6 +319,7 @@ void imh_tq_tables_free(imh_tq_tables *t) {
     if (!t) return;
     imh::use_device(t->dev);
     (void)hipFree(t->base);
+    if (t->search_base) (void)hipFree(t->search_base);
     delete t;
 }
 

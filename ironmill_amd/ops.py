@@ -171,6 +171,13 @@ def encode_turboquant_cache_write(stream: Stream, tq: TurboQuantModel, cache: Tu
                                                 _ptr(positions), int(bool(is_k))))
 
 
+def encode_turboquant_cache_write_kv(stream: Stream, tq: TurboQuantModel, cache: TurboQuantKvCache,
+                                    k_proj, v_proj, token_count: int, base_pos: int, positions=None):
+    """Both cache writes of attention.rs:344-391 in one launch."""
+    check(lib.imh_encode_turboquant_cache_write_kv(stream.handle, tq.handle, C.byref(cache.c), _ptr(k_proj),
+                                                   _ptr(v_proj), token_count, base_pos, _ptr(positions)))
+
+
 def encode_turboquant_attention(stream: Stream, tq: TurboQuantModel, cache: TurboQuantKvCache, q,
                                 num_heads: int, seq_len: int, out, attn_scale: float | None = None,
                                 seq_lens=None, num_splits: int = 0):
@@ -381,7 +388,7 @@ class Decoder:
 __all__ = [
     "AffineQuantizedWeight", "encode_projection", "encode_batched_affine_matvec_int4",
     "encode_fused_ffn_gate_up_act_int4", "encode_fused_residual_norm_affine_matvec_int4",
-    "TurboQuantModel", "TurboQuantKvCache", "encode_turboquant_cache_write",
+    "TurboQuantModel", "TurboQuantKvCache", "encode_turboquant_cache_write", "encode_turboquant_cache_write_kv",
     "encode_turboquant_attention", "encode_kv_cache_and_attention", "Fp16KvCache", "encode_kv_scatter",
     "encode_fp16_attention", "encode_fp16_kv_cache_and_attention", "read_device", "encode_rms_norm",
     "encode_fused_residual_rms_norm", "encode_residual_add", "encode_fused_embedding_norm", "rope_cache",

@@ -69,6 +69,45 @@ def test_cache_write_bit_exact(dev, stream, tq, tables, is_k):
         assert np.array_equal(cache.k_r_norms.read().view(np.uint32), rn_ref.view(np.uint32))
 
 
+def test_cache_write_kv_one_launch_bit_exact(dev, stream, tq, tables):
+    """K and V written by the one-launch entry point == the oracle's writes, bit for bit."""
+    batch, tokens, nkv, max_seq = 2, 7, 8, 32
+    k, v = kv_data(batch, tokens, nkv, seed=31), kv_data(batch, tokens, nkv, seed=32)
+    positions = np.array([3, 29], np.int32)   # the second wraps around
+    cache = ops.TurboQuantKvCache(dev, batch, nkv, D, max_seq)
+    cache.zero(stream)
+    ops.encode_turboquant_cache_write_kv(stream, tq, cache, dev.upload(k), dev.upload(v), tokens, 0,
+                                         positions=dev.upload(positions))
+    stream.sync()
+    kc, ks, kr = O.tq_cache_write(k, tables, True, max_seq, positions=positions)
+    vc, vs, _ = O.tq_cache_write(v, tables, False, max_seq, positions=positions)
+    assert np.array_equal(cache.k_codes.read(), kc) and np.array_equal(cache.v_codes.read(), vc)
+    assert np.array_equal(cache.k_scales.read().view(np.uint32), ks.view(np.uint32))
+    assert np.array_equal(cache.v_scales.read().view(np.uint32), vs.view(np.uint32))
+    assert np.array_equal(cache.k_r_norms.read().view(np.uint32), kr.view(np.uint32))
+
+
+def test_cache_write_unsorted_boundaries_scan(dev, stream):
+    """Caller tables whose boundaries are not sorted take the linear scan, which keeps the
+    reference's "last boundary <= u" rule (turboquant.metal:118-124) bit for bit."""
+    tabs = O.TQTables(D, 8, 7)
+    rng = np.random.default_rng(3)
+    for bd in (tabs.k_bounds, tabs.v_bounds):
+        i = rng.choice(bd.size - 8, 4, replace=False) + 4
+        bd[i], bd[i + 3] = bd[i + 3].copy(), bd[i].copy()   # local disorder
+    host = dict(signs=tabs.signs, k_codebook=tabs.k_codebook, k_bounds=tabs.k_bounds,
+                v_codebook=tabs.v_codebook, v_bounds=tabs.v_bounds, qjl=tabs.qjl)
+    tq2 = ops.TurboQuantModel(dev, D, 8, host_tables=host)
+    kv = kv_data(1, 40, 8, seed=5)
+    cache = ops.TurboQuantKvCache(dev, 1, 8, D, 64)
+    cache.zero(stream)
+    ops.encode_turboquant_cache_write_kv(stream, tq2, cache, dev.upload(kv), dev.upload(kv), 40, 0)
+    stream.sync()
+    kc, _, _ = O.tq_cache_write(kv, tabs, True, 64)
+    vc, _, _ = O.tq_cache_write(kv, tabs, False, 64)
+    assert np.array_equal(cache.k_codes.read(), kc) and np.array_equal(cache.v_codes.read(), vc)
+
+
 def fill_cache(dev, stream, tq, batch, nkv, max_seq, ctx, seed):
     cache = ops.TurboQuantKvCache(dev, batch, nkv, D, max_seq)
     cache.zero(stream)

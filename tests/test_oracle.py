@@ -601,3 +601,23 @@ def test_tq_write_sensitivity_to_one_step(tabs):
     v_diff = np.mean(v1 != v2)
     assert 0.01 < k_diff < 0.08 and sign_diff > 0.8 * k_diff
     assert 0.0005 < v_diff < 0.02
+
+
+def test_tq_index_rule_prefix_max_equals_scan(tabs):
+    """The reference index rule idx = 1 + max{j : u >= bound[j]} (turboquant.metal:118-124)
+    equals the running max of (j + 1) over the boundaries sorted by value, read at
+    upper_bound(u).  The real tables are not monotonic (Lloyd-Max tails), so this is the
+    form the kernel can binary-search exactly; checked against the literal scan."""
+    rng = np.random.default_rng(9)
+    for bd in (tabs.k_bounds, tabs.v_bounds):
+        assert np.any(np.diff(bd) < 0)   # the tables really are unsorted
+        order = np.argsort(bd, kind="stable")
+        sv, pm = bd[order], np.maximum.accumulate(order + 1)
+        u = np.concatenate([rng.standard_normal(2000).astype(np.float32) * 0.1, bd,
+                            np.nextafter(bd, np.float32(-1)), np.nextafter(bd, np.float32(1)),
+                            np.array([np.nan, -np.inf, np.inf, 0.0, -0.0], np.float32)])
+        scan = np.array([(np.nonzero(x >= bd)[0].max() + 1) if np.any(x >= bd) else 0 for x in u])
+        pos = np.searchsorted(sv, u, side="right")
+        pos[np.isnan(u)] = 0
+        fast = np.where(pos == 0, 0, pm[np.maximum(pos - 1, 0)])
+        assert np.array_equal(scan, fast)
