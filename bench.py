@@ -110,6 +110,21 @@ def time_loop(dev, stream, fn, steps, warmup):
     return s.elapsed_ms(e)
 
 
+def eager_loop(dev, stream, fn, steps, warmup):
+    """As time_loop but with host launches (rocprofv3 counter collection sees only
+    non-graph dispatches).  Returns total ms."""
+    for i in range(warmup):
+        fn(i)
+    stream.sync()
+    s, e = dev.event(), dev.event()
+    s.record(stream)
+    for i in range(steps):
+        fn(i)
+    e.record(stream)
+    stream.sync()
+    return s.elapsed_ms(e)
+
+
 def cpu_baseline(qg, qu, qd, seconds):
     import oracle as O
     threads = min(os.cpu_count() or 1, 16)
@@ -135,7 +150,7 @@ def cpu_baseline(qg, qu, qd, seconds):
                       f"{1e3 * dt:.1f} ms/step"}
 
 
-def bench_attention(dev, stream, ops, batch, ctx, steps, warmup, layers):
+def bench_attention(dev, stream, ops, batch, ctx, steps, warmup, layers, eager=False):
     """TurboQuant decode attention over `layers` distinct caches (rotated)."""
     nkv, nh, d = 8, 32, 128
     tq = ops.TurboQuantModel(dev, d, 8, 42)
@@ -159,14 +174,14 @@ def bench_attention(dev, stream, ops, batch, ctx, steps, warmup, layers):
     def step(i):
         ops.encode_turboquant_attention(stream, tq, caches[i % layers], q, nh, ctx, out, scale)
 
-    total = time_loop(dev, stream, step, steps, warmup)
+    total = (eager_loop if eager else time_loop)(dev, stream, step, steps, warmup)
     ms = total / steps
     gbs = tq_bytes(batch, ctx) / (ms * 1e-3) / 1e9
     return {"batch": batch, "ctx": ctx, "us": round(ms * 1e3, 2), "GB/s": round(gbs, 1),
             "frac": round(gbs / HBM_PEAK_GBS, 4), "bytes": tq_bytes(batch, ctx)}
 
 
-def bench_fp16_attention(dev, stream, ops, batch, ctx, steps, warmup, layers):
+def bench_fp16_attention(dev, stream, ops, batch, ctx, steps, warmup, layers, eager=False):
     """FP16-KV decode attention (fused_sdpa / FlashDecoding) over `layers` distinct caches."""
     nkv, nh, d = 8, 32, 128
     rng = np.random.default_rng(ctx + batch + 1)
@@ -187,7 +202,7 @@ def bench_fp16_attention(dev, stream, ops, batch, ctx, steps, warmup, layers):
     def step(i):
         ops.encode_fp16_attention(stream, caches[i % layers], q, nh, ctx, out, attn_scale=1.0 / math.sqrt(d))
 
-    ms = time_loop(dev, stream, step, steps, warmup) / steps
+    ms = (eager_loop if eager else time_loop)(dev, stream, step, steps, warmup) / steps
     nbytes = fp16_kv_bytes(batch, ctx)
     gbs = nbytes / (ms * 1e-3) / 1e9
     return {"batch": batch, "ctx": ctx, "us": round(ms * 1e3, 2), "GB/s": round(gbs, 1),
@@ -313,6 +328,10 @@ def main():
                          "256 MB Infinity Cache; 1 measures a cache-resident matrix)")
     ap.add_argument("--decode-only", action="store_true",
                     help="only the Qwen3-4B decode-step lines (B=1 and 8, ctx 8k), for profiling")
+    ap.add_argument("--attention-only", choices=["tq", "fp16"],
+                    help="only the decode attention at ctx 32k and --batch (for rocprofv3 runs)")
+    ap.add_argument("--eager", action="store_true",
+                    help="with --attention-only: host launches instead of a graph (counter runs)")
     ap.add_argument("--decode-batches", type=int, nargs="+", default=[1, 8])
     ap.add_argument("--decode-eager", action="store_true",
                     help="with --decode-only: time 5 eager steps only (no graph capture; for kernel traces)")
@@ -343,6 +362,13 @@ def main():
     info = dev.info()
     log(f"device {info['arch']} CUs={info['compute_units']}")
 
+    if args.attention_only:
+        fn = bench_attention if args.attention_only == "tq" else bench_fp16_attention
+        layers = max(1, min(8, 16 // args.batch))
+        r = fn(dev, stream, ops, args.batch, 32768, args.steps, args.warmup, layers, eager=args.eager)
+        log(f"{args.attention_only} attention B={args.batch} ctx=32k: {r['us']} us {r['GB/s']} GB/s")
+        print(json.dumps({f"{args.attention_only}_attention_b{args.batch}_ctx32k": r}), flush=True)
+        return
     if args.decode_only:
         for bb in args.decode_batches:
             r = bench_decode(dev, stream, ops, bb, 8192, max(20, args.steps // 10), 3, graph=not args.decode_eager)
