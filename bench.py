@@ -227,11 +227,15 @@ def decode_step_bytes(b, ctx, cfg=Q3):
 
 def random_int4(dev, ops, rng, n, k, awq=True):
     """Synthetic INT4 weight in the upload layout: random codes, f16 scales in [1e-3, 3e-3],
-    integer zero-points 0..15, AWQ scales in [0.5, 2]."""
+    integer zero-points 0..15, AWQ scales in [0.5, 2] (awq True: new ones; a device buffer: that
+    one, shared with another weight of the same input; False: none)."""
     data = rng.integers(0, 256, size=(n, k // 2), dtype=np.uint8)
     sc = rng.uniform(1e-3, 3e-3, (n, k // 128)).astype(np.float16)
     zp = rng.integers(0, 16, size=(n, k // 128)).astype(np.float16)
-    a = dev.upload(rng.uniform(0.5, 2.0, k).astype(np.float16)) if awq else None
+    if awq is True:
+        a = dev.upload(rng.uniform(0.5, 2.0, k).astype(np.float16))
+    else:
+        a = None if awq is False else awq
     return ops.AffineQuantizedWeight.from_pointers(dev.upload(data), dev.upload(sc), dev.upload(zp), a, n, k)
 
 
@@ -250,20 +254,15 @@ def bench_decode(dev, stream, ops, batch, ctx, steps, warmup, kv_cache="turboqua
         return dev.upload(rng.uniform(0.8, 1.2, n).astype(np.float16))
 
     for l in range(L):
+        # Q/K/V and gate/up read one activation each, so each set shares its AWQ scales
+        q = random_int4(dev, ops, rng, qd, H)
+        g = random_int4(dev, ops, rng, F, H)
         w = dict(input_norm=norm(H), post_attn_norm=norm(H), q_norm=norm(hd), k_norm=norm(hd),
-                 q_proj=random_int4(dev, ops, rng, qd, H), k_proj=random_int4(dev, ops, rng, kvd, H),
+                 q_proj=q, k_proj=random_int4(dev, ops, rng, kvd, H, awq=q.awq_scales),
+                 v_proj=random_int4(dev, ops, rng, kvd, H, awq=q.awq_scales),
                  o_proj=random_int4(dev, ops, rng, H, qd, awq=False),
-                 gate_proj=random_int4(dev, ops, rng, F, H), down_proj=random_int4(dev, ops, rng, H, F))
-        w["up_proj"] = ops.AffineQuantizedWeight.from_pointers(
-            *[dev.upload(a) for a in (rng.integers(0, 256, size=(F, H // 2), dtype=np.uint8),
-                                      rng.uniform(1e-3, 3e-3, (F, H // 128)).astype(np.float16),
-                                      rng.integers(0, 16, size=(F, H // 128)).astype(np.float16))],
-            w["gate_proj"].awq_scales, F, H)
-        w["v_proj"] = ops.AffineQuantizedWeight.from_pointers(
-            *[dev.upload(a) for a in (rng.integers(0, 256, size=(kvd, H // 2), dtype=np.uint8),
-                                      rng.uniform(1e-3, 3e-3, (kvd, H // 128)).astype(np.float16),
-                                      rng.integers(0, 16, size=(kvd, H // 128)).astype(np.float16))],
-            w["k_proj"].awq_scales, kvd, H)
+                 gate_proj=g, up_proj=random_int4(dev, ops, rng, F, H, awq=g.awq_scales),
+                 down_proj=random_int4(dev, ops, rng, H, F))
         d.set_layer(l, **w)
         keep.append(w)
     emb = dev.upload((rng.standard_normal((cfg["vocab_size"], H)) * 0.05).astype(np.float16))

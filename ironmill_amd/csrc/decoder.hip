@@ -297,16 +297,30 @@ int imh_decoder_step(imh_decoder *d, imh_stream *s, const uint32_t *token_ids, u
 
     IMH_TRY(imh_encode_fused_embedding_norm(s, token_ids, d->embedding, d->layers[0].input_norm, d->norm_out,
                                             d->hidden, H, B, c.vocab_size, c.rms_eps, c.embed_scale));
-    bool q_done = false;
+    // Q, K and V read the same activation: when they share the AWQ scales
+    // (or have none) they run as the row segments of one launch, which at a
+    // layer's end also does the residual add and the input norm
+    auto shared_awq = [](const imh_decoder_layer_weights &w) {
+        return w.q_proj.awq_scales == w.k_proj.awq_scales && w.k_proj.awq_scales == w.v_proj.awq_scales;
+    };
+    uint16_t *qkv_out[3] = {d->q, d->k, d->v};
+    bool q_done = false, kv_done = false;
     for (uint32_t l = 0; l < c.num_layers; l++) {
         const imh_decoder_layer_weights &w = d->layers[l];
-        if (!q_done) IMH_TRY(imh_encode_affine_projection_int4(s, d->norm_out, B, &w.q_proj, d->q));
-        // K and V read the same activation: one launch when they share the AWQ scales
-        if (w.k_proj.awq_scales == w.v_proj.awq_scales)
-            IMH_TRY(imh_encode_batched_affine_matvec_int4(s, d->norm_out, B, &w.k_proj, d->k, &w.v_proj, d->v));
-        else {
-            IMH_TRY(imh_encode_affine_projection_int4(s, d->norm_out, B, &w.k_proj, d->k));
-            IMH_TRY(imh_encode_affine_projection_int4(s, d->norm_out, B, &w.v_proj, d->v));
+        const imh_affine_int4_weight *qkv[3] = {&w.q_proj, &w.k_proj, &w.v_proj};
+        if (!q_done && shared_awq(w)) {
+            IMH_TRY(imh::encode_segmented_matvec_int4(s, d->norm_out, nullptr, B, 3, qkv, qkv_out));
+            kv_done = true;
+        } else if (!q_done) {
+            IMH_TRY(imh_encode_affine_projection_int4(s, d->norm_out, B, &w.q_proj, d->q));
+        }
+        if (!kv_done) {
+            if (w.k_proj.awq_scales == w.v_proj.awq_scales)
+                IMH_TRY(imh::encode_segmented_matvec_int4(s, d->norm_out, nullptr, B, 2, qkv + 1, qkv_out + 1));
+            else {
+                IMH_TRY(imh_encode_affine_projection_int4(s, d->norm_out, B, &w.k_proj, d->k));
+                IMH_TRY(imh_encode_affine_projection_int4(s, d->norm_out, B, &w.v_proj, d->v));
+            }
         }
         imh_qk_norm_rope_params qp{};
         qp.q = d->q;
@@ -355,7 +369,13 @@ int imh_decoder_step(imh_decoder *d, imh_stream *s, const uint32_t *token_ids, u
             fp.normed_output = d->norm_out;
             fp.token_count = B;
             fp.eps = c.rms_eps;
-            IMH_TRY(imh_encode_fused_residual_norm_affine_matvec_int4(s, &fp));
+            kv_done = shared_awq(nw);
+            if (kv_done) {
+                const imh_affine_int4_weight *nqkv[3] = {&nw.q_proj, &nw.k_proj, &nw.v_proj};
+                IMH_TRY(imh::encode_segmented_matvec_int4(s, nullptr, &fp, B, 3, nqkv, qkv_out));
+            } else {
+                IMH_TRY(imh_encode_fused_residual_norm_affine_matvec_int4(s, &fp));
+            }
             q_done = true;
         } else {
             IMH_TRY(imh_encode_residual_add(s, d->residual, d->ffn_down, d->hidden, (size_t)B * H));

@@ -90,4 +90,15 @@ int stream_scratch(imh_stream *s, int slot, size_t bytes, void **out);
 // Make the stream's device current for the calling thread.
 int use_device(const imh_device *dev);
 
+// Projections of one activation by up to three INT4 weights that share k and
+// the AWQ scales (a layer's Q, K and V), as the row segments of one matvec
+// launch: out[i] = act . w[i]^T.  The activation is x, or, when rn is given,
+// the fused residual + RMSNorm of rn->a + rn->b (whose residual and normed
+// rows are written as by imh_encode_fused_residual_norm_affine_matvec_int4;
+// rn->weight and rn->output are not read).  Every segment but the last has a
+// multiple of 16 rows.  Prefill-sized batches run one op per weight.
+int encode_segmented_matvec_int4(imh_stream *s, const uint16_t *x, const imh_fused_residual_norm_params *rn,
+                                 uint32_t B, int nseg, const imh_affine_int4_weight *const *w,
+                                 uint16_t *const *out);
+
 }  // namespace imh

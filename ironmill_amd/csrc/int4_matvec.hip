@@ -278,6 +278,41 @@ int run_gemm(imh_stream *s, const ActIn &in, int M, const imh_affine_int4_weight
                        ws);
 }
 
+// Plans and launches the matvec kernel for mp (N rows in total, segments
+// included): RAW when the workgroups can build the operand image themselves,
+// else the prep kernel writes it into stream scratch slot 0 first.
+int run_matvec(imh_stream *s, ActIn in, uint32_t B, int nmat, int epi, int N, int K, const MatPtrs &mp,
+               const char *who) {
+    const bool rn = in.b != nullptr;
+    Plan p;
+    int rc = plan_launch(s, nmat, rn, N, K, (int)B, who, p);
+    if (rc) return rc;
+    if (p.raw) {
+        launch_raw(nmat, epi, rn, p.L, mp, in);
+        IMH_HIP(hipGetLastError());
+        return IMH_OK;
+    }
+    // IMAGE: the prep kernel writes the image into stream scratch first
+    void *scr = nullptr;
+    rc = imh::stream_scratch(s, 0, image_bytes(B, K), &scr);
+    if (rc) return rc;
+    float *rms;
+    image_layout(scr, B, K, in, &rms);
+    _Float16 *hi = const_cast<_Float16 *>(in.hi);
+    _Float16 *lo = const_cast<_Float16 *>(in.lo);
+    float *gs = const_cast<float *>(in.gsum);
+    if (rn) {
+        hipLaunchKernelGGL(int4_prep_resnorm, dim3(B), dim3(256), 0, s->stream, in.a, in.b, in.gamma, in.awq,
+                           in.eps, in.residual_out, in.normed_out, hi, lo, gs, rms, K);
+        in.row_scale = rms;
+    } else {
+        dim3 grid((K / 8 + 255) / 256, B);
+        hipLaunchKernelGGL(int4_prep_plain, grid, dim3(256), 0, s->stream, in.a, in.awq, hi, lo, gs, K);
+    }
+    IMH_HIP(hipGetLastError());
+    return launch_image(nmat, epi, p.L, mp, in);
+}
+
 // Validates the weights and runs the op: x (plain) or the residual-norm
 // inputs (in.b != NULL) -> out0 [, out1].
 int run_op(imh_stream *s, ActIn in, uint32_t B, const imh_affine_int4_weight *w0,
@@ -308,37 +343,8 @@ int run_op(imh_stream *s, ActIn in, uint32_t B, const imh_affine_int4_weight *w0
     }
     mp.out[0] = reinterpret_cast<__half *>(out0);
     mp.out[1] = reinterpret_cast<__half *>(out1);
-    const bool rn = in.b != nullptr;
-    const int nmat = w1 ? 2 : 1;
-    const int N = (int)w0->n, K = (int)w0->k;
     if ((int)B >= kGemmMinTokens) return run_gemm(s, in, (int)B, w0, w1, epi, out0, out1);
-    Plan p;
-    rc = plan_launch(s, nmat, rn, N, K, (int)B, who, p);
-    if (rc) return rc;
-    if (p.raw) {
-        launch_raw(nmat, epi, rn, p.L, mp, in);
-        IMH_HIP(hipGetLastError());
-        return IMH_OK;
-    }
-    // IMAGE: the prep kernel writes the image into stream scratch first
-    void *scr = nullptr;
-    rc = imh::stream_scratch(s, 0, image_bytes(B, K), &scr);
-    if (rc) return rc;
-    float *rms;
-    image_layout(scr, B, K, in, &rms);
-    _Float16 *hi = const_cast<_Float16 *>(in.hi);
-    _Float16 *lo = const_cast<_Float16 *>(in.lo);
-    float *gs = const_cast<float *>(in.gsum);
-    if (rn) {
-        hipLaunchKernelGGL(int4_prep_resnorm, dim3(B), dim3(256), 0, s->stream, in.a, in.b, in.gamma, in.awq,
-                           in.eps, in.residual_out, in.normed_out, hi, lo, gs, rms, K);
-        in.row_scale = rms;
-    } else {
-        dim3 grid((K / 8 + 255) / 256, B);
-        hipLaunchKernelGGL(int4_prep_plain, grid, dim3(256), 0, s->stream, in.a, in.awq, hi, lo, gs, K);
-    }
-    IMH_HIP(hipGetLastError());
-    return launch_image(nmat, epi, p.L, mp, in);
+    return run_matvec(s, in, B, w1 ? 2 : 1, epi, (int)w0->n, (int)w0->k, mp, who);
 }
 
 // x is divided by the first weight's awq_scales; a gate/up pair shares that
@@ -351,6 +357,64 @@ ActIn plain_in(const uint16_t *x, const imh_affine_int4_weight *w) {
 }
 
 }  // namespace
+
+namespace imh {
+
+int encode_segmented_matvec_int4(imh_stream *s, const uint16_t *x, const imh_fused_residual_norm_params *rn,
+                                 uint32_t B, int nseg, const imh_affine_int4_weight *const *w,
+                                 uint16_t *const *out) {
+    const char *who = "encode_segmented_matvec_int4";
+    if (!s || (!x && !rn) || !w || !out || nseg < 1 || nseg > 3)
+        return fail(IMH_EINVAL, std::string(who) + ": bad argument");
+    int N = 0;
+    for (int i = 0; i < nseg; i++) {
+        int rc = check_weight(w[i], who);
+        if (rc) return rc;
+        if (!out[i]) return fail(IMH_EINVAL, std::string(who) + ": NULL output");
+        if (w[i]->k != w[0]->k || w[i]->awq_scales != w[0]->awq_scales)
+            return fail(IMH_EINVAL, std::string(who) + ": segments must share k and the AWQ scales");
+        if (i + 1 < nseg && w[i]->n % 16)
+            return fail(IMH_EINVAL, std::string(who) + ": segment rows must be a multiple of 16");
+        N += (int)w[i]->n;
+    }
+    ActIn in = plain_in(x, w[0]);
+    if (rn) {
+        if (!rn->a || !rn->b || !rn->norm_weight || !rn->residual_output || !rn->normed_output)
+            return fail(IMH_EINVAL, std::string(who) + ": NULL argument");
+        in.a = reinterpret_cast<const __half *>(rn->a);
+        in.b = reinterpret_cast<const __half *>(rn->b);
+        in.gamma = reinterpret_cast<const __half *>(rn->norm_weight);
+        in.residual_out = reinterpret_cast<__half *>(rn->residual_output);
+        in.normed_out = reinterpret_cast<__half *>(rn->normed_output);
+        in.eps = rn->eps;
+    }
+    if ((int)B >= kGemmMinTokens || nseg == 1) {   // one op per weight, the later ones on the normed rows
+        int rc = run_op(s, in, B, w[0], nullptr, EPI_STORE, out[0], nullptr, who);
+        const uint16_t *xn = rn ? rn->normed_output : x;
+        for (int i = 1; i < nseg && !rc; i++)
+            rc = run_op(s, plain_in(xn, w[0]), B, w[i], nullptr, EPI_STORE, out[i], nullptr, who);
+        return rc;
+    }
+    if (misaligned16(in.a) || misaligned16(in.b) || misaligned16(in.gamma) || misaligned16(in.awq) ||
+        misaligned16(in.residual_out) || misaligned16(in.normed_out))
+        return fail(IMH_EINVAL, std::string(who) + ": activation vectors must be 16-byte aligned");
+    if (B == 0) return IMH_OK;
+    int rc = use_device(s->dev);
+    if (rc) return rc;
+    MatPtrs mp = {};
+    int row = 0;
+    for (int i = 0; i < nseg; i++) {
+        mp.data[i] = w[i]->data;
+        mp.scales[i] = reinterpret_cast<const __half *>(w[i]->scales);
+        mp.zeros[i] = reinterpret_cast<const __half *>(w[i]->zeros);
+        mp.out[i] = reinterpret_cast<__half *>(out[i]);
+        if (i) mp.seg[i - 1] = row;
+        row += (int)w[i]->n;
+    }
+    return run_matvec(s, in, B, 1, EPI_STORE, N, (int)w[0]->k, mp, who);
+}
+
+}  // namespace imh
 
 extern "C" {
 

@@ -72,11 +72,17 @@ constexpr float kTwo24 = 16777216.0f;               // 2^24
 enum Epi : int { EPI_STORE, EPI_SILU, EPI_GELU };
 enum Src : int { SRC_IMAGE, SRC_RAW, SRC_RAW_RN };
 
+// Weights and outputs.  NMAT 2: entries 0 and 1 are the pair.  NMAT 1: entry
+// 0, or up to three row segments of one launch: the tiles from row seg[0] on
+// (seg[1] on) belong to entry 1 (entry 2), rows counted from the segment's
+// first row; seg[i] == 0 means no such segment.  Segment starts are multiples
+// of 16, so a tile never spans two segments.
 struct MatPtrs {
-    const uint8_t *data[2];
-    const __half *scales[2];
-    const __half *zeros[2];
-    __half *out[2];
+    const uint8_t *data[3];
+    const __half *scales[3];
+    const __half *zeros[3];
+    __half *out[3];
+    int seg[2];
 };
 
 // Activation source.  IMAGE: hi/lo [B][K] f16 operand values, gsum [B][2][G]
@@ -162,7 +168,7 @@ constexpr int waves_per_simd(int NG, int MT, int XC, int SRC) {
 
 template <int NMAT, int EPI, int MT, int NG, int XC, int SRC>
 __global__ void __launch_bounds__(1024) __attribute__((amdgpu_waves_per_eu(waves_per_simd(NG, MT, XC, SRC))))
-int4_matvec_kernel(MatPtrs mp, ActIn in, int N, int K, int B, int parts, int SG) {
+int4_matvec_kernel(MatPtrs mp, ActIn in, int Nall, int K, int B, int parts, int SG) {
     constexpr bool RAW = SRC != SRC_IMAGE;
     constexpr bool RN = SRC == SRC_RAW_RN;
     // dynamic LDS: [NMAT][G][16] u32 (scale | zero << 16); [G][MT][16] f32
@@ -184,15 +190,33 @@ int4_matvec_kernel(MatPtrs mp, ActIn in, int N, int K, int B, int parts, int SG)
     const int bc = min(16, B - m0);
     const int RSX = SG * kGS + 8;        // LDS row stride in halfs (16-byte pad)
 
+    // matrix pointers by select: a dynamic index into the kernel-argument
+    // struct would turn into dependent memory loads
+    int row0 = blockIdx.x * 16;
+    int N = Nall;
+    const uint8_t *d0 = mp.data[0], *d1 = mp.data[1];
+    const __half *sc0 = mp.scales[0], *sc1 = mp.scales[1];
+    const __half *zr0 = mp.zeros[0], *zr1 = mp.zeros[1];
+    __half *o0 = mp.out[0], *o1 = mp.out[1];
+    if (NMAT == 1 && mp.seg[0] > 0 && row0 < mp.seg[0]) {
+        N = mp.seg[0];                                        // first segment: its own row count
+    } else if (NMAT == 1 && mp.seg[0] > 0) {                  // uniform over the workgroup
+        const bool third = mp.seg[1] > 0 && row0 >= mp.seg[1];
+        const int base = third ? mp.seg[1] : mp.seg[0];
+        N = (third || mp.seg[1] == 0 ? Nall : mp.seg[1]) - base;
+        row0 -= base;
+        d0 = third ? mp.data[2] : mp.data[1];
+        sc0 = third ? mp.scales[2] : mp.scales[1];
+        zr0 = third ? mp.zeros[2] : mp.zeros[1];
+        o0 = third ? mp.out[2] : mp.out[1];
+    }
+
     const int n_l = lane & 15;           // weight row within the tile (B column) and A row
     const int kq = lane >> 4;            // 16-byte quarter of a group this lane reads
-    const int row0 = blockIdx.x * 16;
     const int row = row0 + n_l;
     const int row_c = row < N ? row : N - 1;
 
-    // matrix pointers by select: a dynamic index into the kernel-argument
-    // struct would turn into dependent memory loads
-    const uint8_t *wdata = (NMAT == 2 && mat) ? mp.data[1] : mp.data[0];
+    const uint8_t *wdata = (NMAT == 2 && mat) ? d1 : d0;
     const uint8_t *wrow = wdata + (size_t)row_c * (K / 2) + kq * 16;
 
     uint32_t *szs = lds_dyn;
@@ -211,8 +235,8 @@ int4_matvec_kernel(MatPtrs mp, ActIn in, int N, int K, int B, int parts, int SG)
     auto sz_elem = [&](int e, const uint16_t *&sp, const uint16_t *&zp, int &dst) {
         const bool second = NMAT == 2 && e >= per_mat;
         const int el = second ? e - per_mat : e;
-        sp = reinterpret_cast<const uint16_t *>(second ? mp.scales[1] : mp.scales[0]);
-        zp = reinterpret_cast<const uint16_t *>(second ? mp.zeros[1] : mp.zeros[0]);
+        sp = reinterpret_cast<const uint16_t *>(second ? sc1 : sc0);
+        zp = reinterpret_cast<const uint16_t *>(second ? zr1 : zr0);
         const int rr = el / G;
         dst = ((second ? G : 0) + (el - rr * G)) * 16 + rr;
         return min((size_t)row0 * G + el, sz_last);
@@ -498,11 +522,11 @@ int4_matvec_kernel(MatPtrs mp, ActIn in, int N, int K, int B, int parts, int SG)
                 inner = fminf(fmaxf(inner, -10.0f), 10.0f);
                 act = 0.5f * g * (1.0f + tanhf(inner));
             }
-            mp.out[0][(size_t)m * N + row] = __float2half(act * u * scale);
+            o0[(size_t)m * N + row] = __float2half(act * u * scale);
         } else {
 #pragma unroll
             for (int mt = 0; mt < NMAT; mt++)
-                mp.out[mt][(size_t)m * N + row] = __float2half(sum[mt][r] * scale);
+                (mt ? o1 : o0)[(size_t)m * N + row] = __float2half(sum[mt][r] * scale);
         }
     }
 }

@@ -130,7 +130,7 @@ def test_qk_norm_rope_errors(dev, stream):
 
 # ------------------------------------------------------------------ decoder
 
-CFG = dict(hidden_size=256, intermediate_size=512, num_layers=2, num_heads=4, num_kv_heads=1, head_dim=128,
+CFG = dict(hidden_size=256, intermediate_size=512, num_layers=3, num_heads=4, num_kv_heads=1, head_dim=128,
            vocab_size=512, max_seq_len=64, batch=2, rms_eps=1e-6, rope_theta=1e6)
 
 
@@ -149,7 +149,7 @@ def make_model(dev, seed, cfg=CFG, qk_norm=True):
     host_layers, dev_layers = [], []
     for l in range(cfg["num_layers"]):
         s_in = rng.uniform(0.5, 2.0, H).astype(np.float32)
-        s_kv = s_in if l == 0 else rng.uniform(0.5, 2.0, H).astype(np.float32)
+        s_kv = rng.uniform(0.5, 2.0, H).astype(np.float32) if l == 1 else s_in
         s_f = rng.uniform(0.5, 2.0, F).astype(np.float32)
         hl = dict(input_norm=norm(H), post_attn_norm=norm(H),
                   q_norm=norm(cfg["head_dim"]) if qk_norm else None,
@@ -160,16 +160,23 @@ def make_model(dev, seed, cfg=CFG, qk_norm=True):
         host_layers.append(hl)
         dl = {k: (dev.upload(v) if isinstance(v, np.ndarray) else None) for k, v in hl.items()
               if k.endswith("norm")}
-        for name in ("q_proj", "k_proj", "o_proj", "gate_proj", "up_proj", "down_proj"):
+        for name in ("q_proj", "o_proj", "gate_proj", "up_proj", "down_proj"):
             dl[name] = ops.AffineQuantizedWeight(dev, hl[name])
-        if l == 0:  # share K's AWQ buffer so the decoder takes the one-launch K/V path
-            v = hl["v_proj"]
-            kw = dl["k_proj"]
-            dl["v_proj"] = ops.AffineQuantizedWeight.from_pointers(dev.upload(v.data), dev.upload(v.scales),
-                                                                   dev.upload(v.zeros), kw.awq_scales, v.n, v.k)
-            dl["_keep"] = dl["v_proj"]
+
+        def shared(name, owner):
+            w = hl[name]
+            return ops.AffineQuantizedWeight.from_pointers(dev.upload(w.data), dev.upload(w.scales),
+                                                           dev.upload(w.zeros), owner.awq_scales, w.n, w.k)
+
+        # layers 0 and 2: Q, K and V share one AWQ buffer (one segmented launch
+        # for the three; at layer 2 fused with the residual norm); layer 1: K
+        # and V share theirs, Q has its own (Q apart, K and V in one launch)
+        if l == 1:
+            dl["k_proj"] = ops.AffineQuantizedWeight(dev, hl["k_proj"])
         else:
-            dl["v_proj"] = ops.AffineQuantizedWeight(dev, hl["v_proj"])
+            dl["k_proj"] = shared("k_proj", dl["q_proj"])
+        dl["v_proj"] = shared("v_proj", dl["k_proj"])
+        dl["_keep"] = (dl["k_proj"], dl["v_proj"])
         dev_layers.append(dl)
     emb = rng.standard_normal((V, H)).astype(np.float16)
     fnorm = norm(H)
