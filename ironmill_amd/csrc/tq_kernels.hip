@@ -45,6 +45,18 @@ constexpr int kSplitQuantum = kChunk * kWaves;
 constexpr int kMaxSplits = 512;     // the combining workgroup stages every split's (max, sum) in LDS
 constexpr int kAutoSplitLen = 256;  // shortest split the automatic split count makes
 
+// Strides 1..32 of the unnormalised fast Walsh-Hadamard transform of a
+// 64-element vector held one element per lane: at stride s the pair (j, j + s)
+// becomes (x_j + x_{j+s}, x_j - x_{j+s}), strides in increasing order.
+__device__ __forceinline__ float hadamard64(float x, int lane) {
+#pragma unroll
+    for (int step = 1; step < 64; step *= 2) {
+        const float p = __shfl_xor(x, step);
+        x = (lane & step) ? p - x : x + p;   // element j + step of the pair: x_j - x_{j+step}
+    }
+    return x;
+}
+
 // IEEE round-to-nearest f32 square root: the hardware v_sqrt_f32 result
 // (within 1 ulp) corrected with two fma residuals.  Inputs here are finite
 // and >= 1e-20, so no denormal rescaling is needed.
@@ -141,12 +153,8 @@ __global__ void __launch_bounds__(64 * kWriteMaxWaves) tq_cache_write_kernel(
         const __half e1 = v == v0 ? pre1 : src[lane + 64];
         float x0 = __half2float(e0) * sg0;
         float x1 = __half2float(e1) * sg1;
-        for (int step = 1; step < 64; step *= 2) {
-            const float p0 = __shfl_xor(x0, step), p1 = __shfl_xor(x1, step);
-            const bool upper = (lane & step) != 0;   // element j + step of the pair: a - c
-            x0 = upper ? p0 - x0 : x0 + p0;
-            x1 = upper ? p1 - x1 : x1 + p1;
-        }
+        x0 = hadamard64(x0, lane);
+        x1 = hadamard64(x1, lane);
         {
             const float lo = x0, hi = x1;   // stride 64: elements lane and lane + 64
             x0 = lo + hi;
@@ -219,7 +227,7 @@ __global__ void __launch_bounds__(64 * kWriteMaxWaves) tq_cache_write_kernel(
 // of operand A as f16.  Built with -amdgpu-mfma-vgpr-form so the accumulators
 // stay in VGPRs (no AGPR round trip around the softmax rescale).
 template <int GQA>
-__global__ void __launch_bounds__(64 * kWaves) tq_attention_kernel(
+__global__ void __launch_bounds__(64 * kWaves) __attribute__((amdgpu_waves_per_eu(3))) tq_attention_kernel(
     const __half *__restrict__ q, int nh, int nkv, int max_seq, int seq_len,
     const int32_t *__restrict__ seq_lens, float attn_scale, const float *__restrict__ signs,
     const float *__restrict__ qjl_t, const float *__restrict__ kcb, const float *__restrict__ vcb,
@@ -301,42 +309,63 @@ __global__ void __launch_bounds__(64 * kWaves) tq_attention_kernel(
         ktab[tid] = (uint32_t)__builtin_bit_cast(uint16_t, hi) | ((uint32_t)__builtin_bit_cast(uint16_t, lo) << 16);
     }
     vtab[tid] = (_Float16)vcb[tid];
-    // query prep, per workgroup while the first chunk is in flight: q_rot =
-    // D.H.D/sqrt(d) q (butterfly in LDS) into qs[h][0], and its QJL projection
-    // s_q[d] = sum_k S[d][k] q_rot[k] (fmaf in increasing k, S^T read
-    // coalesced from L2) into qs[h][1]
+    // query prep, per workgroup while the first chunk is in flight.  S^T
+    // (128 x 128 f32, L2-resident) is read as float4s: thread (kr, dq) =
+    // (tid >> 5, tid & 31) takes rows 16 kr .. 16 kr + 15 at columns 4 dq ..
+    // 4 dq + 3, every load issued before the first is used
+    static_assert(kWaves == 4 && GQA <= kWaves, "query prep maps 256 threads and one wave per head");
     const float rscale = 1.0f / sqrtf((float)kD);
-    for (int e = tid; e < GQA * kD; e += 64 * kWaves) {
-        const int hh = e / kD, d = e % kD;
-        qs[hh][0][d] = __half2float(q[((size_t)b * nh + kvh * GQA + hh) * kD + d]) * signs[d];
-    }
-    __syncthreads();
-    for (int step = 1; step < kD; step *= 2) {
-        if (tid < GQA * kD / 2) {
-            const int hh = tid / (kD / 2), i = tid % (kD / 2);
-            const int j = (i / step) * (step * 2) + (i % step);
-            const float x0 = qs[hh][0][j], x1 = qs[hh][0][j + step];
-            qs[hh][0][j] = x0 + x1;
-            qs[hh][0][j + step] = x0 - x1;
-        }
-        __syncthreads();
-    }
-    for (int e = tid; e < GQA * kD; e += 64 * kWaves) {
-        const int hh = e / kD, d = e % kD;
-        qs[hh][0][d] = qs[hh][0][d] * (signs[d] * rscale);
-    }
-    __syncthreads();
+    const int kr = tid >> 5, dq = tid & 31;
+    float4 st[16];
     {
-        const int d = tid % kD, h0 = tid / kD;   // heads h0 and h0 + 2
-        float a0 = 0.0f, a1 = 0.0f;
-#pragma unroll 16
-        for (int k = 0; k < kD; k++) {
-            const float sv = qjl_t[(size_t)k * kD + d];
-            if (h0 < GQA) a0 = __builtin_fmaf(sv, qs[h0][0][k], a0);
-            if (h0 + 2 < GQA) a1 = __builtin_fmaf(sv, qs[h0 + 2][0][k], a1);
+        const float4 *s4 = reinterpret_cast<const float4 *>(qjl_t) + (size_t)kr * 16 * (kD / 4) + dq;
+#pragma unroll
+        for (int i = 0; i < 16; i++) st[i] = s4[(size_t)i * (kD / 4)];
+    }
+    // q_rot = D.H.D/sqrt(d) q: wave hh rotates head hh in registers (lane
+    // holds elements lane and lane + 64; butterfly strides 1..32 by xor
+    // shuffles, stride 64 in the lane) into qs[hh][0]
+    if (wave < GQA) {
+        const __half *qh = q + ((size_t)b * nh + kvh * GQA + wave) * kD;
+        const float sg0 = signs[lane], sg1 = signs[lane + 64];
+        float x0 = __half2float(qh[lane]) * sg0, x1 = __half2float(qh[lane + 64]) * sg1;
+        x0 = hadamard64(x0, lane);
+        x1 = hadamard64(x1, lane);
+        qs[wave][0][lane] = (x0 + x1) * (sg0 * rscale);
+        qs[wave][0][lane + 64] = (x0 - x1) * (sg1 * rscale);
+    }
+    __syncthreads();
+    // its QJL projection s_q[d] = sum_k S[d][k] q_rot[k] into qs[hh][1]:
+    // 16-row partial sums, the two of a wave added by a shuffle, the four
+    // waves' through LDS (om is free until the loop ends)
+    {
+        float4 pr[GQA];
+#pragma unroll
+        for (int hh = 0; hh < GQA; hh++) pr[hh] = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+#pragma unroll
+        for (int i = 0; i < 16; i++) {
+#pragma unroll
+            for (int hh = 0; hh < GQA; hh++) {
+                const float qv = qs[hh][0][kr * 16 + i];
+                pr[hh].x = __builtin_fmaf(st[i].x, qv, pr[hh].x);
+                pr[hh].y = __builtin_fmaf(st[i].y, qv, pr[hh].y);
+                pr[hh].z = __builtin_fmaf(st[i].z, qv, pr[hh].z);
+                pr[hh].w = __builtin_fmaf(st[i].w, qv, pr[hh].w);
+            }
         }
-        if (h0 < GQA) qs[h0][1][d] = a0;
-        if (h0 + 2 < GQA) qs[h0 + 2][1][d] = a1;
+#pragma unroll
+        for (int hh = 0; hh < GQA; hh++) {
+            pr[hh].x += __shfl_xor(pr[hh].x, 32);
+            pr[hh].y += __shfl_xor(pr[hh].y, 32);
+            pr[hh].z += __shfl_xor(pr[hh].z, 32);
+            pr[hh].w += __shfl_xor(pr[hh].w, 32);
+            if (lane < 32) reinterpret_cast<float4 *>(&om[wave][hh][0])[dq] = pr[hh];
+        }
+    }
+    __syncthreads();
+    for (int e = tid; e < GQA * kD; e += 64 * kWaves) {
+        const int hh = e / kD, d = e % kD;
+        qs[hh][1][d] = (om[0][hh][d] + om[1][hh][d]) + (om[2][hh][d] + om[3][hh][d]);
     }
     __syncthreads();
 
@@ -546,20 +575,15 @@ __global__ void __launch_bounds__(64 * kWaves) tq_attention_kernel(
         if (tid == 0) __hip_atomic_store(&counters[b * nkv + kvh], 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
     __syncthreads();
-    // rotate back: o = D.H.D/sqrt(d) o_rot
-    for (int step = 1; step < kD; step *= 2) {
-        if (tid < GQA * kD / 2) {
-            const int hh = tid / (kD / 2), i = tid % (kD / 2);
-            const int j = (i / step) * (step * 2) + (i % step);
-            const float x0 = qs[hh][0][j], x1 = qs[hh][0][j + step];
-            qs[hh][0][j] = x0 + x1;
-            qs[hh][0][j + step] = x0 - x1;
-        }
-        __syncthreads();
-    }
-    for (int e = tid; e < GQA * kD; e += 64 * kWaves) {
-        const int hh = e / kD, d = e % kD;
-        out[((size_t)b * nh + kvh * GQA + hh) * kD + d] = __float2half(qs[hh][0][d] * (signs[d] * rscale));
+    // rotate back: o = D.H.D/sqrt(d) o_rot, wave hh on head hh in registers
+    if (wave < GQA) {
+        const float sg0 = signs[lane], sg1 = signs[lane + 64];
+        float x0 = qs[wave][0][lane], x1 = qs[wave][0][lane + 64];
+        x0 = hadamard64(x0, lane);
+        x1 = hadamard64(x1, lane);
+        __half *o = out + ((size_t)b * nh + kvh * GQA + wave) * kD;
+        o[lane] = __float2half((x0 + x1) * (sg0 * rscale));
+        o[lane + 64] = __float2half((x0 - x1) * (sg1 * rscale));
     }
 }
 
