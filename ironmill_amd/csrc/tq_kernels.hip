@@ -296,9 +296,12 @@ __global__ void __launch_bounds__(64 * kWaves) __attribute__((amdgpu_waves_per_e
         c.krn = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(kr_r, soff, 0, 0));
         c.vsc = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(vs_r, soff, 0, 0));
     };
+    // wave w takes chunks p_begin + 16 w + 64 i of the split, one chunk in
+    // flight; loads past the split's end read zeros and fetch nothing, so
+    // they are issued unconditionally
     ChunkIn cur;
     const int p_first = p_begin + wave * kChunk;
-    if (p_first < p_end) load_chunk(p_first, cur);
+    load_chunk(p_first, cur);
 
     // tables: K codebook as (f16 hi | f16 lo << 16), V codebook in f16; the
     // group's prepared queries
@@ -404,9 +407,7 @@ __global__ void __launch_bounds__(64 * kWaves) __attribute__((amdgpu_waves_per_e
 #pragma unroll
     for (int j = 0; j < 8; j++) acc[j] = float4_t{0, 0, 0, 0};
 
-    for (int p0 = p_first; p0 < p_end; p0 += kChunk * kWaves) {
-        const ChunkIn c = cur;
-        if (p0 + kChunk * kWaves < p_end) load_chunk(p0 + kChunk * kWaves, cur);
+    auto process = [&](const ChunkIn &c, const int p0) __attribute__((always_inline)) {
         // ---- scores S[h][n] for 16 positions via MFMA ----
         const uint32_t kw[8] = {c.k0.x, c.k0.y, c.k0.z, c.k0.w, c.k1.x, c.k1.y, c.k1.z, c.k1.w};
         float4_t d1 = {0, 0, 0, 0};
@@ -470,6 +471,11 @@ __global__ void __launch_bounds__(64 * kWaves) __attribute__((amdgpu_waves_per_e
             acc[j] = __builtin_amdgcn_mfma_f32_16x16x16f16(wa, bv, acc[j], 0, 0, 0);
         }
         __builtin_amdgcn_wave_barrier();   // wbuf is rewritten next chunk
+    };
+    for (int p0 = p_first; p0 < p_end; p0 += kChunk * kWaves) {
+        const ChunkIn c = cur;
+        load_chunk(p0 + kChunk * kWaves, cur);
+        process(c, p0);
     }
 
     // lane (c, g): acc[j][0] = o[head g][dim 8c + j]
@@ -523,25 +529,48 @@ __global__ void __launch_bounds__(64 * kWaves) __attribute__((amdgpu_waves_per_e
                                              __HIP_MEMORY_SCOPE_AGENT) == S - 1;
         __syncthreads();
         if (!is_last) return;
-        // one invalidation of this XCD's caches, then ordinary (batched) loads
+        // one invalidation of this XCD's caches, then ordinary loads, issued
+        // together: each thread's first batch of partial outputs (o[h][4q..4q+3]
+        // of its split subset: 256 threads = GQA heads x 32 dim quads x 8 / GQA
+        // subsets) and, per head (one wave), the split maxima and sums
         __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
         const size_t gbase = ((size_t)b * nh + kvh * GQA) * S;   // head hh at gbase + hh * S
-        for (int i = tid; i < GQA * S; i += 64 * kWaves) tail_f[i / S][i % S] = part_m[gbase + i];
-        __syncthreads();
+        constexpr int kParts = 8 / GQA;
+        constexpr int kBatch = 16;
+        const int quad = tid & 31, hh = (tid >> 5) % GQA, part = (tid >> 5) / GQA;
+        const float4 *po4 = reinterpret_cast<const float4 *>(part_o + (gbase + (size_t)hh * S) * kD) + quad;
+        float4 ov[kBatch];
+#pragma unroll
+        for (int i = 0; i < kBatch; i++) {
+            const int sp = part + i * kParts;
+            ov[i] = sp < S ? po4[(size_t)sp * (kD / 4)] : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+        }
         // per head: M = max over splits, f_s = exp(m_s - M), l = sum f_s l_s
-        // (one wave per head, lanes stride the splits, then a DPP/shuffle sum)
+        // (lanes stride the splits, then DPP/shuffle reductions)
         if (wave < GQA) {
+            constexpr int kPer = kMaxSplits / 64;
+            float mv[kPer], lv[kPer];
+            const float *pm = part_m + gbase + (size_t)wave * S;
+            const float *pl = part_l + gbase + (size_t)wave * S;
+#pragma unroll
+            for (int i = 0; i < kPer; i++) {
+                const int sp = lane + 64 * i;
+                mv[i] = sp < S ? pm[sp] : -INFINITY;
+                lv[i] = sp < S ? pl[sp] : 0.0f;
+            }
             float mx = -INFINITY;
-            for (int sp = lane; sp < S; sp += 64) mx = fmaxf(mx, tail_f[wave][sp]);
+#pragma unroll
+            for (int i = 0; i < kPer; i++) mx = fmaxf(mx, mv[i]);
             mx = fmaxf(mx, __shfl_xor(mx, 32));
             mx = fmaxf(mx, __shfl_xor(mx, 16));
             mx = imh_dpp::row16_max(mx);
             float lsum = 0.0f;
-            for (int sp = lane; sp < S; sp += 64) {
-                const float m = tail_f[wave][sp];
-                const float f = (mx == -INFINITY || m == -INFINITY) ? 0.0f : __expf(m - mx);
-                tail_f[wave][sp] = f;
-                lsum += f * part_l[gbase + (size_t)wave * S + sp];
+#pragma unroll
+            for (int i = 0; i < kPer; i++) {
+                const int sp = lane + 64 * i;
+                const float f = (mx == -INFINITY || mv[i] == -INFINITY) ? 0.0f : __expf(mv[i] - mx);
+                if (sp < S) tail_f[wave][sp] = f;
+                lsum = __builtin_fmaf(f, lv[i], lsum);
             }
             lsum = imh_dpp::row16_sum(lsum);
             lsum += __shfl_xor(lsum, 16);
@@ -549,14 +578,19 @@ __global__ void __launch_bounds__(64 * kWaves) __attribute__((amdgpu_waves_per_e
             if (lane == 0) tail_l[wave] = lsum;
         }
         __syncthreads();
-        // o[h][4q..4q+3] = sum_s f_s o_s: 256 threads = GQA heads x 32 dim quads x
-        // (8 / GQA) split subsets, float4 loads, 16 in flight per thread
-        constexpr int kParts = 8 / GQA;
-        const int quad = tid & 31, hh = (tid >> 5) % GQA, part = (tid >> 5) / GQA;
-        const float4 *po4 = reinterpret_cast<const float4 *>(part_o + (gbase + (size_t)hh * S) * kD) + quad;
         float4 acc4 = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+#pragma unroll
+        for (int i = 0; i < kBatch; i++) {
+            const int sp = part + i * kParts;
+            const float f = sp < S ? tail_f[hh][sp] : 0.0f;
+            acc4.x = __builtin_fmaf(ov[i].x, f, acc4.x);
+            acc4.y = __builtin_fmaf(ov[i].y, f, acc4.y);
+            acc4.z = __builtin_fmaf(ov[i].z, f, acc4.z);
+            acc4.w = __builtin_fmaf(ov[i].w, f, acc4.w);
+        }
+        // more splits than one batch: the rest, 16 loads in flight per thread
 #pragma unroll 16
-        for (int sp = part; sp < S; sp += kParts) {
+        for (int sp = part + kBatch * kParts; sp < S; sp += kParts) {
             const float4 v = po4[(size_t)sp * (kD / 4)];
             const float f = tail_f[hh][sp];
             acc4.x = __builtin_fmaf(v.x, f, acc4.x);
