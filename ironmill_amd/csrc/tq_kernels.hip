@@ -299,39 +299,42 @@ __global__ void __launch_bounds__(64 * kWaves) __attribute__((amdgpu_waves_per_e
     // wave w takes chunks p_begin + 16 w + 64 i of the split, one chunk in
     // flight; loads past the split's end read zeros and fetch nothing, so
     // they are issued unconditionally
-    ChunkIn cur;
-    const int p_first = p_begin + wave * kChunk;
-    load_chunk(p_first, cur);
-
-    // tables: K codebook as (f16 hi | f16 lo << 16), V codebook in f16; the
-    // group's prepared queries
-    {
-        const float c = kcb[tid & 0x7F];
-        const _Float16 hi = (_Float16)c;
-        const _Float16 lo = (_Float16)(c - (float)hi);
-        ktab[tid] = (uint32_t)__builtin_bit_cast(uint16_t, hi) | ((uint32_t)__builtin_bit_cast(uint16_t, lo) << 16);
-    }
-    vtab[tid] = (_Float16)vcb[tid];
-    // query prep, per workgroup while the first chunk is in flight.  S^T
-    // (128 x 128 f32, L2-resident) is read as float4s: thread (kr, dq) =
-    // (tid >> 5, tid & 31) takes rows 16 kr .. 16 kr + 15 at columns 4 dq ..
-    // 4 dq + 3, every load issued before the first is used
+    // Prologue loads go first: a wave's loads return in issue order, so the
+    // query, tables and S^T issued ahead of the first chunk are not held
+    // behind it.  S^T (128 x 128 f32, L2-resident) is read as float4s: thread
+    // (kr, dq) = (tid >> 5, tid & 31) takes rows 16 kr .. 16 kr + 15 at
+    // columns 4 dq .. 4 dq + 3.
     static_assert(kWaves == 4 && GQA <= kWaves, "query prep maps 256 threads and one wave per head");
     const float rscale = 1.0f / sqrtf((float)kD);
     const int kr = tid >> 5, dq = tid & 31;
+    const int qhead = kvh * GQA + (wave < GQA ? wave : 0);
+    const __half *qh = q + ((size_t)b * nh + qhead) * kD;
+    const __half q0 = qh[lane], q1 = qh[lane + 64];
+    const float sg0 = signs[lane], sg1 = signs[lane + 64];
+    const float kc = kcb[tid & 0x7F], vc = vcb[tid];
     float4 st[16];
     {
         const float4 *s4 = reinterpret_cast<const float4 *>(qjl_t) + (size_t)kr * 16 * (kD / 4) + dq;
 #pragma unroll
         for (int i = 0; i < 16; i++) st[i] = s4[(size_t)i * (kD / 4)];
     }
+    ChunkIn cur;
+    const int p_first = p_begin + wave * kChunk;
+    load_chunk(p_first, cur);
+    __builtin_amdgcn_sched_barrier(0);   // every load above issues before the first wait
+
+    // tables: K codebook as (f16 hi | f16 lo << 16), V codebook in f16
+    {
+        const _Float16 hi = (_Float16)kc;
+        const _Float16 lo = (_Float16)(kc - (float)hi);
+        ktab[tid] = (uint32_t)__builtin_bit_cast(uint16_t, hi) | ((uint32_t)__builtin_bit_cast(uint16_t, lo) << 16);
+    }
+    vtab[tid] = (_Float16)vc;
     // q_rot = D.H.D/sqrt(d) q: wave hh rotates head hh in registers (lane
     // holds elements lane and lane + 64; butterfly strides 1..32 by xor
     // shuffles, stride 64 in the lane) into qs[hh][0]
     if (wave < GQA) {
-        const __half *qh = q + ((size_t)b * nh + kvh * GQA + wave) * kD;
-        const float sg0 = signs[lane], sg1 = signs[lane + 64];
-        float x0 = __half2float(qh[lane]) * sg0, x1 = __half2float(qh[lane + 64]) * sg1;
+        float x0 = __half2float(q0) * sg0, x1 = __half2float(q1) * sg1;
         x0 = hadamard64(x0, lane);
         x1 = hadamard64(x1, lane);
         qs[wave][0][lane] = (x0 + x1) * (sg0 * rscale);
