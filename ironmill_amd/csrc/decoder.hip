@@ -352,10 +352,17 @@ int imh_decoder_step(imh_decoder *d, imh_stream *s, const uint32_t *token_ids, u
                                               0));
         }
         IMH_TRY(imh_encode_affine_projection_int4(s, d->attn_out, B, &w.o_proj, d->ffn_down));
-        IMH_TRY(imh_encode_fused_residual_rms_norm(s, d->hidden, d->ffn_down, w.post_attn_norm, d->norm_out,
-                                                   d->residual, H, B, c.rms_eps));
-        IMH_TRY(imh_encode_fused_ffn_gate_up_act_int4(s, d->norm_out, B, &w.gate_proj, &w.up_proj, d->act,
-                                                      c.use_gelu));
+        {   // post-attention residual + norm, then gate + up + activation: one launch
+            imh_fused_residual_norm_params rp{};
+            rp.a = d->hidden;
+            rp.b = d->ffn_down;
+            rp.norm_weight = w.post_attn_norm;
+            rp.residual_output = d->residual;
+            rp.normed_output = d->norm_out;
+            rp.token_count = B;
+            rp.eps = c.rms_eps;
+            IMH_TRY(imh::encode_resnorm_gate_up_act_int4(s, &rp, B, &w.gate_proj, &w.up_proj, d->act, c.use_gelu));
+        }
         IMH_TRY(imh_encode_affine_projection_int4(s, d->act, B, &w.down_proj, d->ffn_down));
         if (l + 1 < c.num_layers) {
             const imh_decoder_layer_weights &nw = d->layers[l + 1];

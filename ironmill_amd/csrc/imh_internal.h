@@ -95,10 +95,20 @@ int use_device(const imh_device *dev);
 // launch: out[i] = act . w[i]^T.  The activation is x, or, when rn is given,
 // the fused residual + RMSNorm of rn->a + rn->b (whose residual and normed
 // rows are written as by imh_encode_fused_residual_norm_affine_matvec_int4;
-// rn->weight and rn->output are not read).  Every segment but the last has a
-// multiple of 16 rows.  Prefill-sized batches run one op per weight.
+// rn->weight and rn->output are not read): w[0] projects it as that op does,
+// the other weights project the f16 normed rows.  Every segment but the last
+// has a multiple of 16 rows.  Prefill-sized batches run one op per weight.
 int encode_segmented_matvec_int4(imh_stream *s, const uint16_t *x, const imh_fused_residual_norm_params *rn,
                                  uint32_t B, int nseg, const imh_affine_int4_weight *const *w,
                                  uint16_t *const *out);
+
+// The fused residual + RMSNorm of rn->a + rn->b (residual and normed rows
+// written as by imh_encode_fused_residual_norm_affine_matvec_int4; rn->weight
+// and rn->output are not read) feeding the fused gate + up + SiLU/GELU of
+// imh_encode_fused_ffn_gate_up_act_int4 with the f16 normed rows as its
+// input (as after a separate norm), in one launch below 32 tokens.
+int encode_resnorm_gate_up_act_int4(imh_stream *s, const imh_fused_residual_norm_params *rn, uint32_t B,
+                                    const imh_affine_int4_weight *gate, const imh_affine_int4_weight *up,
+                                    uint16_t *out, int use_gelu);
 
 }  // namespace imh

@@ -66,12 +66,15 @@ __global__ void __launch_bounds__(256) int4_prep_plain(const __half *__restrict_
 }
 
 // Residual + RMSNorm mode.  grid (B), block 256: r = a + b, rms_inv, writes
-// residual_out / normed_out and the operand image of r * gamma / awq.
+// residual_out / normed_out and the operand image of r * gamma / awq (the
+// matvec then scales by rms_inv); `rounded` 1: of normed_out / awq instead;
+// 2: both, the rounded one as the second image (hi2 / lo2 / gsum2).
 __global__ void __launch_bounds__(256) int4_prep_resnorm(
     const __half *__restrict__ a, const __half *__restrict__ b, const __half *__restrict__ gamma,
     const __half *__restrict__ awq, float eps, __half *__restrict__ residual_out,
     __half *__restrict__ normed_out, _Float16 *__restrict__ xa_hi, _Float16 *__restrict__ xa_lo,
-    float *__restrict__ gsum, float *__restrict__ rms_out, int K) {
+    float *__restrict__ gsum, float *__restrict__ rms_out, int K, int rounded, _Float16 *__restrict__ xa_hi2,
+    _Float16 *__restrict__ xa_lo2, float *__restrict__ gsum2) {
     const int m = blockIdx.x;
     const int G = K / kGS;
     const size_t row = (size_t)m * K;
@@ -110,18 +113,22 @@ __global__ void __launch_bounds__(256) int4_prep_resnorm(
         const _Float16 *ah = reinterpret_cast<const _Float16 *>(&av);
         const _Float16 *bh = reinterpret_cast<const _Float16 *>(&bv);
         const _Float16 *gh = reinterpret_cast<const _Float16 *>(&gv);
-        float v[8];
+        float v[8], v2[8];
         half8_t res, nrm;
         for (int i = 0; i < 8; i++) {
             float r = (float)ah[i] + (float)bh[i];
             res[i] = (_Float16)r;
             nrm[i] = (_Float16)(r * rms_inv * (float)gh[i]);
-            v[i] = r * (float)gh[i];
+            v[i] = rounded == 1 ? (float)nrm[i] : r * (float)gh[i];
+            v2[i] = (float)nrm[i];
         }
         if (awq) {
             uint4 wv = *reinterpret_cast<const uint4 *>(awq + (size_t)c * 8);
             const _Float16 *wh = reinterpret_cast<const _Float16 *>(&wv);
-            for (int i = 0; i < 8; i++) v[i] = div_awq(v[i], (float)wh[i]);
+            for (int i = 0; i < 8; i++) {
+                v[i] = div_awq(v[i], (float)wh[i]);
+                v2[i] = div_awq(v2[i], (float)wh[i]);
+            }
         }
         half8_t hi, lo;
         float sh, sl;
@@ -133,6 +140,14 @@ __global__ void __launch_bounds__(256) int4_prep_resnorm(
             *reinterpret_cast<half8_t *>(xa_lo + off) = lo;
         }
         store_group_sums(sh, sl, live, gsum + (size_t)m * 2 * G, G, c / 16);
+        if (rounded == 2) {   // uniform: the second (rounded) image
+            chunk_operands(v2, hi, lo, sh, sl);
+            if (live) {
+                *reinterpret_cast<half8_t *>(xa_hi2 + off) = hi;
+                *reinterpret_cast<half8_t *>(xa_lo2 + off) = lo;
+            }
+            store_group_sums(sh, sl, live, gsum2 + (size_t)m * 2 * G, G, c / 16);
+        }
     }
 }
 
@@ -293,18 +308,31 @@ int run_matvec(imh_stream *s, ActIn in, uint32_t B, int nmat, int epi, int N, in
         return IMH_OK;
     }
     // IMAGE: the prep kernel writes the image into stream scratch first
+    // (two images for a mixed rounding: the unrounded one for the first
+    // segment, the rounded one for the rest)
+    const bool two = rn && in.round_mode == 2;
     void *scr = nullptr;
-    rc = imh::stream_scratch(s, 0, image_bytes(B, K), &scr);
+    rc = imh::stream_scratch(s, 0, image_bytes(B, K) * (two ? 2 : 1), &scr);
     if (rc) return rc;
-    float *rms;
+    float *rms, *rms2;
+    ActIn in2 = in;
+    if (two) image_layout(static_cast<uint8_t *>(scr) + image_bytes(B, K), B, K, in2, &rms2);
     image_layout(scr, B, K, in, &rms);
     _Float16 *hi = const_cast<_Float16 *>(in.hi);
     _Float16 *lo = const_cast<_Float16 *>(in.lo);
     float *gs = const_cast<float *>(in.gsum);
     if (rn) {
+        const int rounded = in.round_mode;
         hipLaunchKernelGGL(int4_prep_resnorm, dim3(B), dim3(256), 0, s->stream, in.a, in.b, in.gamma, in.awq,
-                           in.eps, in.residual_out, in.normed_out, hi, lo, gs, rms, K);
-        in.row_scale = rms;
+                           in.eps, in.residual_out, in.normed_out, hi, lo, gs, rms, K, rounded,
+                           const_cast<_Float16 *>(in2.hi), const_cast<_Float16 *>(in2.lo),
+                           const_cast<float *>(in2.gsum));
+        in.row_scale = rounded == 1 ? nullptr : rms;
+        if (two) {
+            in.hi2 = in2.hi;
+            in.lo2 = in2.lo;
+            in.gsum2 = in2.gsum;
+        }
     } else {
         dim3 grid((K / 8 + 255) / 256, B);
         hipLaunchKernelGGL(int4_prep_plain, grid, dim3(256), 0, s->stream, in.a, in.awq, hi, lo, gs, K);
@@ -388,6 +416,13 @@ int encode_segmented_matvec_int4(imh_stream *s, const uint16_t *x, const imh_fus
         in.normed_out = reinterpret_cast<__half *>(rn->normed_output);
         in.eps = rn->eps;
     }
+    if (rn && nseg > 1 && (int)B < kGemmMinTokens) {
+        // the first segment projects r * gamma * rms_inv unrounded (the fused
+        // residual-norm projection); the others read the f16 normed rows, as
+        // they would after a separate norm (RAW: each workgroup builds the
+        // operand its segment reads; IMAGE: the prep kernel writes both)
+        in.round_mode = 2;
+    }
     if ((int)B >= kGemmMinTokens || nseg == 1) {   // one op per weight, the later ones on the normed rows
         int rc = run_op(s, in, B, w[0], nullptr, EPI_STORE, out[0], nullptr, who);
         const uint16_t *xn = rn ? rn->normed_output : x;
@@ -412,6 +447,24 @@ int encode_segmented_matvec_int4(imh_stream *s, const uint16_t *x, const imh_fus
         row += (int)w[i]->n;
     }
     return run_matvec(s, in, B, 1, EPI_STORE, N, (int)w[0]->k, mp, who);
+}
+
+int encode_resnorm_gate_up_act_int4(imh_stream *s, const imh_fused_residual_norm_params *rn, uint32_t B,
+                                    const imh_affine_int4_weight *gate, const imh_affine_int4_weight *up,
+                                    uint16_t *out, int use_gelu) {
+    const char *who = "encode_resnorm_gate_up_act_int4";
+    if (!s || !rn || !rn->a || !rn->b || !rn->norm_weight || !rn->residual_output || !rn->normed_output || !gate ||
+        !up || !out)
+        return fail(IMH_EINVAL, std::string(who) + ": NULL argument");
+    ActIn in = plain_in(nullptr, gate);
+    in.a = reinterpret_cast<const __half *>(rn->a);
+    in.b = reinterpret_cast<const __half *>(rn->b);
+    in.gamma = reinterpret_cast<const __half *>(rn->norm_weight);
+    in.residual_out = reinterpret_cast<__half *>(rn->residual_output);
+    in.normed_out = reinterpret_cast<__half *>(rn->normed_output);
+    in.eps = rn->eps;
+    in.round_mode = 1;   // gate and up read the f16 normed rows
+    return run_op(s, in, B, gate, up, use_gelu ? EPI_GELU : EPI_SILU, out, nullptr, who);
 }
 
 }  // namespace imh

@@ -88,8 +88,9 @@ struct MatPtrs {
 // Activation source.  IMAGE: hi/lo [B][K] f16 operand values, gsum [B][2][G]
 // f32 group sums (prescaled), row_scale [B] or NULL.  RAW: a = x [B][K] and
 // awq [K] or NULL.  RAW_RN: r = a + b, operand r * gamma / awq, output scaled
-// by rms_inv = 1 / sqrt(mean(r^2) + eps); the workgroups of tile column 0 also
-// write residual_out = f16(r) and normed_out = f16(r * rms_inv * gamma).
+// by rms_inv = 1 / sqrt(mean(r^2) + eps) (round_mode below); the workgroups
+// of tile column 0 also write residual_out = f16(r) and normed_out =
+// f16(r * rms_inv * gamma).
 struct ActIn {
     const _Float16 *hi;
     const _Float16 *lo;
@@ -102,6 +103,15 @@ struct ActIn {
     __half *residual_out;
     __half *normed_out;
     float eps;
+    // residual-norm operand: 0 -- r * gamma / awq with rms_inv applied to the
+    // output (the fused residual-norm projection); 1 -- the f16-rounded
+    // normed row f16(r * rms_inv * gamma) / awq, as a separate RMSNorm feeding
+    // the projection would give; 2 -- 0 for the first row segment, 1 for the
+    // rest (IMAGE: the second image hi2 / lo2 / gsum2, with no row scale)
+    int round_mode;
+    const _Float16 *hi2;
+    const _Float16 *lo2;
+    const float *gsum2;
 };
 
 // Split v into f16 hi + lo with hi + lo == v to ~22 bits.
@@ -198,10 +208,12 @@ int4_matvec_kernel(MatPtrs mp, ActIn in, int Nall, int K, int B, int parts, int 
     const __half *sc0 = mp.scales[0], *sc1 = mp.scales[1];
     const __half *zr0 = mp.zeros[0], *zr1 = mp.zeros[1];
     __half *o0 = mp.out[0], *o1 = mp.out[1];
+    int seg_idx = 0;
     if (NMAT == 1 && mp.seg[0] > 0 && row0 < mp.seg[0]) {
         N = mp.seg[0];                                        // first segment: its own row count
     } else if (NMAT == 1 && mp.seg[0] > 0) {                  // uniform over the workgroup
         const bool third = mp.seg[1] > 0 && row0 >= mp.seg[1];
+        seg_idx = third ? 2 : 1;
         const int base = third ? mp.seg[1] : mp.seg[0];
         N = (third || mp.seg[1] == 0 ? Nall : mp.seg[1]) - base;
         row0 -= base;
@@ -217,6 +229,13 @@ int4_matvec_kernel(MatPtrs mp, ActIn in, int Nall, int K, int B, int parts, int 
     const int row_c = row < N ? row : N - 1;
 
     const uint8_t *wdata = (NMAT == 2 && mat) ? d1 : d0;
+    // RAW_RN with a rounded operand: the row's rms is reduced before the image is built
+    const bool rnd = RN && (in.round_mode == 1 || (in.round_mode == 2 && seg_idx > 0));
+    // IMAGE with a rounded second image for the later segments
+    const bool img2 = !RAW && in.round_mode == 2 && seg_idx > 0;
+    const _Float16 *ihi = img2 ? in.hi2 : in.hi;
+    const _Float16 *ilo = img2 ? in.lo2 : in.lo;
+    const float *igs = img2 ? in.gsum2 : in.gsum;
     const uint8_t *wrow = wdata + (size_t)row_c * (K / 2) + kq * 16;
 
     uint32_t *szs = lds_dyn;
@@ -266,7 +285,7 @@ int4_matvec_kernel(MatPtrs mp, ActIn in, int Nall, int K, int B, int parts, int 
     float xsum[RAW ? 1 : kSXChunks];
     if (!RAW) {
 #pragma unroll
-        for (int i = 0; i < kSXChunks; i++) xsum[i] = in.gsum[sx_src(min(i * nthr + tid, sx_total - 1))];
+        for (int i = 0; i < kSXChunks; i++) xsum[i] = igs[sx_src(min(i * nthr + tid, sx_total - 1))];
     }
 
     // A rows of this lane in each tile: plane n_l >> 3, batch row 8t + (n_l & 7)
@@ -290,8 +309,8 @@ int4_matvec_kernel(MatPtrs mp, ActIn in, int Nall, int K, int B, int parts, int 
         const size_t e = (size_t)gs0 * kGS + (size_t)col * 8;   // column within the row
         const size_t src = (size_t)(m0 + r) * K + e;
         if (!RAW) {
-            ch.a = *reinterpret_cast<const u32x4_t *>(in.hi + src);
-            ch.b = *reinterpret_cast<const u32x4_t *>(in.lo + src);
+            ch.a = *reinterpret_cast<const u32x4_t *>(ihi + src);
+            ch.b = *reinterpret_cast<const u32x4_t *>(ilo + src);
             return;
         }
         ch.a = *reinterpret_cast<const u32x4_t *>(in.a + src);
@@ -318,11 +337,17 @@ int4_matvec_kernel(MatPtrs mp, ActIn in, int Nall, int K, int B, int parts, int 
         if (RN) {
             const _Float16 *bh = reinterpret_cast<const _Float16 *>(&ch.b);
             const _Float16 *gh = reinterpret_cast<const _Float16 *>(&ch.g);
+            float ri = 1.0f;
+            if (rnd) {   // rms_inv of row r from the per-group sums already in LDS
+                float ss = 0.0f;
+                for (int g = 0; g < G; g++) ss += rsq[g * 16 + r];
+                ri = 1.0f / __builtin_sqrtf(ss / (float)K + in.eps);
+            }
 #pragma unroll
             for (int i = 0; i < 8; i++) {
                 const float rr = (float)ah[i] + (float)bh[i];
                 sq = __builtin_fmaf(rr, rr, sq);
-                v[i] = rr * (float)gh[i];
+                v[i] = rnd ? (float)(_Float16)(rr * ri * (float)gh[i]) : rr * (float)gh[i];
             }
         } else {
 #pragma unroll
@@ -340,14 +365,28 @@ int4_matvec_kernel(MatPtrs mp, ActIn in, int Nall, int K, int B, int parts, int 
         *reinterpret_cast<half8_t *>(xs + bc * RSX + off) = lo;
         sh = row16_sum(sh);
         sl = row16_sum(sl);
-        if (RN) sq = row16_sum(sq);
+        if (RN && !rnd) sq = row16_sum(sq);
         if (live && (tid & 15) == 0) {
             const int g = gs0 + col / 16;
             float *sx = sxs + (g * MT + (r >> 3)) * 16 + (r & 7);
             sx[0] = sh * kTwoM24;
             sx[8] = sl * kTwoM24;
-            if (RN) rsq[g * 16 + r] = sq;
+            if (RN && !rnd) rsq[g * 16 + r] = sq;
         }
+    };
+    // rounded RAW_RN operand: the per-group sums of r^2 first (as chunk_store
+    // would store them), then a barrier, so every chunk sees its row's rms
+    auto chunk_sq = [&](int r, int col, int gs0, const Chunk &ch, bool live) __attribute__((always_inline)) {
+        const _Float16 *ah = reinterpret_cast<const _Float16 *>(&ch.a);
+        const _Float16 *bh = reinterpret_cast<const _Float16 *>(&ch.b);
+        float sq = 0.0f;
+#pragma unroll
+        for (int i = 0; i < 8; i++) {
+            const float rr = (float)ah[i] + (float)bh[i];
+            sq = __builtin_fmaf(rr, rr, sq);
+        }
+        sq = row16_sum(sq);
+        if (live && (tid & 15) == 0) rsq[(gs0 + col / 16) * 16 + r] = sq;
     };
 
     auto stage = [&](const int gs0, const bool first) __attribute__((always_inline)) {
@@ -387,7 +426,7 @@ int4_matvec_kernel(MatPtrs mp, ActIn in, int Nall, int K, int B, int parts, int 
             if (!RAW) {
 #pragma unroll
                 for (int i = 0; i < kSXChunks; i++) sxs[min(i * nthr + tid, sx_total - 1)] = xsum[i];
-                for (int e = kSXChunks * nthr + tid; e < sx_total; e += nthr) sxs[e] = in.gsum[sx_src(e)];
+                for (int e = kSXChunks * nthr + tid; e < sx_total; e += nthr) sxs[e] = igs[sx_src(e)];
             }
         } else {
             // the previous stage is done with the activation planes
@@ -396,6 +435,17 @@ int4_matvec_kernel(MatPtrs mp, ActIn in, int Nall, int K, int B, int parts, int 
             __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
         }
         // (d) operand image -> LDS (clamped duplicates write identical values)
+        if (RN && rnd) {
+#pragma unroll
+            for (int i = 0; i < XC; i++) {
+                const int c = min(i * nthr + tid, total - 1);
+                const int r = c / cpr;
+                chunk_sq(r, c - r * cpr, gs0, ch[i], i * nthr + tid < total);
+            }
+            __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
+            __builtin_amdgcn_s_barrier();
+            __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+        }
 #pragma unroll
         for (int i = 0; i < XC; i++) {
             const int c = min(i * nthr + tid, total - 1);
@@ -510,10 +560,11 @@ int4_matvec_kernel(MatPtrs mp, ActIn in, int Nall, int K, int B, int parts, int 
         const int m = m0 + mrow + r;
         if (m >= B) break;
         float scale = 1.0f;
-        if (RN) scale = rmsv[mrow + r];
-        else if (!RAW && in.row_scale) scale = in.row_scale[m];
+        if (RN) scale = rnd ? 1.0f : rmsv[mrow + r];
+        else if (!RAW && in.row_scale && !img2) scale = in.row_scale[m];
         if (EPI == EPI_SILU || EPI == EPI_GELU) {
-            const float g = sum[0][r], u = sum[NMAT - 1][r];
+            // the row scale (rms_inv) belongs to both projections, ahead of the activation
+            const float g = sum[0][r] * scale, u = sum[NMAT - 1][r] * scale;
             float act;
             if (EPI == EPI_SILU) {
                 act = g / (1.0f + __expf(-g));
@@ -522,7 +573,7 @@ int4_matvec_kernel(MatPtrs mp, ActIn in, int Nall, int K, int B, int parts, int 
                 inner = fminf(fmaxf(inner, -10.0f), 10.0f);
                 act = 0.5f * g * (1.0f + tanhf(inner));
             }
-            o0[(size_t)m * N + row] = __float2half(act * u * scale);
+            o0[(size_t)m * N + row] = __float2half(act * u);
         } else {
 #pragma unroll
             for (int mt = 0; mt < NMAT; mt++)
@@ -565,7 +616,8 @@ void launch_ng(const Launch &L, const MatPtrs &mp, const ActIn &in) {
 }
 
 // RAW-source launches (instantiated in int4_matvec_raw.hip): nmat/epi as in
-// the kernel, rn selects SRC_RAW_RN (nmat 1, EPI_STORE only); L.mt must be 1.
+// the kernel, rn selects SRC_RAW_RN (nmat 1 with EPI_STORE, or nmat 2 with
+// EPI_SILU / EPI_GELU); L.mt must be 1.
 void launch_raw(int nmat, int epi, bool rn, const Launch &L, const MatPtrs &mp, const ActIn &in);
 // IMAGE-source launches with two MFMA tiles (int4_matvec_mt2.hip).
 void launch_image_mt2(int nmat, int epi, const Launch &L, const MatPtrs &mp, const ActIn &in);

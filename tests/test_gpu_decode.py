@@ -249,6 +249,39 @@ def test_decoder_matches_reference(dev, stream, kv_cache):
             assert not got["k"][b, :, start[b] + 4:].view(np.uint16).any()
 
 
+@pytest.mark.parametrize("batch", [2, 8])
+def test_decoder_wide_matches_reference(dev, stream, batch):
+    """Hidden 2560: at batch 2 the projections build their operand in the
+    workgroup; at batch 8 the fused residual-norm projections (Q/K/V and
+    gate/up) take the operand-image path (prep kernel + image matvec).
+
+    Tolerance 3e-3 on the logits: each op is within 1e-3 of the oracle on its
+    own (test_gpu_int4.py), but two layers at K = 2560 compound the oracle's
+    f16 rounding of the dequantized weights (the kernels keep (q - z) * s
+    exact): measured 1.2e-3 to 1.5e-3 at both batch sizes with two layers, so
+    an error of the image path alone would show as a gap between the two."""
+    B = batch
+    # three layers: the end of layer 1 runs the segmented Q/K/V launch fused
+    # with the residual norm (layer 2 shares the AWQ scales across Q, K, V)
+    cfg = dict(CFG, hidden_size=2560, intermediate_size=1024, num_layers=3, batch=B, vocab_size=256)
+    model = make_model(dev, 81, cfg)
+    d = build_decoder(dev, model, "fp16", cfg)
+    host_layers, _, emb, fnorm, lm = model
+    ref = O.DecoderReference(cfg, host_layers, emb, fnorm, lm, kv_cache="fp16")
+    start = np.arange(B, dtype=np.int32) * 3
+    d.reset(stream, start)
+    ref.positions = start.copy()
+    rng = np.random.default_rng(6)
+    logits = dev.empty((B, cfg["vocab_size"]), np.float16)
+    for step in range(2):
+        tok = rng.integers(0, cfg["vocab_size"], B).astype(np.uint32)
+        d.step(stream, dev.upload(tok), logits)
+        stream.sync()
+        want = ref.step(tok.astype(np.int64))
+        r = rel_l2(logits.read(), want)
+        assert r <= 3e-3, f"batch {B} step {step}: logits rel-L2 {r:.3e}"
+
+
 def test_decoder_graph_replay_matches_eager(dev, stream):
     """A captured step replays as the next token: positions advance on the device."""
     model = make_model(dev, 78, qk_norm=False)
