@@ -338,13 +338,23 @@ int imh_decoder_step(imh_decoder *d, imh_stream *s, const uint32_t *token_ids, u
         qp.batch = B;
         qp.token_count = 1;
         qp.eps = c.rms_eps;
-        IMH_TRY(imh_encode_qk_norm_rope(s, &qp));
-        if (c.kv_cache == IMH_KV_TURBOQUANT) {
+        // TurboQuant with QK-norms at head_dim = rotary_dim = 128: the norm and
+        // rotation run inside the cache write (K) and the attention prologue (Q)
+        const bool fold = c.kv_cache == IMH_KV_TURBOQUANT && w.q_norm && w.k_norm && c.head_dim == 128 &&
+                          (c.rotary_dim == 0 || c.rotary_dim == 128);
+        if (fold) {
+            const imh_tq_kv_cache *kc = &d->tq_caches[l];
+            IMH_TRY(imh::encode_tq_write_kv_rope(s, d->tq, kc, d->k, d->v, 1, d->positions, &qp));
+            IMH_TRY(imh::encode_tq_attention_rope(s, d->tq, kc, d->q, c.num_heads, 0, d->seq_lens, c.attn_scale,
+                                                  d->attn_out, 0, &qp));
+        } else if (c.kv_cache == IMH_KV_TURBOQUANT) {
+            IMH_TRY(imh_encode_qk_norm_rope(s, &qp));
             const imh_tq_kv_cache *kc = &d->tq_caches[l];
             IMH_TRY(imh_encode_turboquant_cache_write_kv(s, d->tq, kc, d->k, d->v, 1, 0, d->positions));
             IMH_TRY(imh_encode_turboquant_attention(s, d->tq, kc, d->q, c.num_heads, 0, d->seq_lens, c.attn_scale,
                                                     d->attn_out, 0));
         } else {
+            IMH_TRY(imh_encode_qk_norm_rope(s, &qp));
             const imh_fp16_kv_cache *kc = &d->fp16_caches[l];
             IMH_TRY(imh_encode_kv_scatter(s, kc, d->k, 1, 0, d->positions, 1));
             IMH_TRY(imh_encode_kv_scatter(s, kc, d->v, 1, 0, d->positions, 0));

@@ -16,6 +16,7 @@
 #include <string>
 
 #include "dpp_reduce.h"
+#include "qk_norm_rope.h"
 #include "imh_internal.h"
 
 namespace {
@@ -172,6 +173,13 @@ __global__ void __launch_bounds__(64) qk_norm_rope_kernel(__half *__restrict__ q
     const int half_dim = hd / 2;
     const __half *cs = cos_t + (size_t)pos * half_dim;
     const __half *sn = sin_t + (size_t)pos * half_dim;
+    if (nw && hd == imh_qk::kHd && rotary == imh_qk::kHd) {   // one head in registers (qk_norm_rope.h)
+        float x0 = h2f(p, tid), x1 = h2f(p, tid + 64);
+        imh_qk::norm_rope_128(x0, x1, tid, nw, cs, sn, eps);
+        p[tid] = __float2half(x0);
+        p[tid + 64] = __float2half(x1);
+        return;
+    }
 
     float ss = 0.0f;
     for (int d = tid; d < hd; d += 64) {

@@ -31,6 +31,7 @@
 
 #include "dpp_reduce.h"
 #include "imh_internal.h"
+#include "qk_norm_rope.h"
 
 namespace {
 
@@ -88,6 +89,13 @@ struct TqWriteArgs {
     const float *sorted[2];      // boundaries sorted by value (NaN dropped)
     const int32_t *prefmax[2];   // running max of (original index + 1)
     int n_search[2];
+    // optional QK-norm + RoPE of K ahead of the quantization (head_dim 128 =
+    // rotary_dim): norm weight [128], cos / sin tables [max_pos][64]
+    const __half *k_norm;
+    const __half *rope_cos;
+    const __half *rope_sin;
+    int rope_max_pos;
+    float eps;
 };
 
 constexpr int kWriteMaxWaves = 16;
@@ -149,10 +157,15 @@ __global__ void __launch_bounds__(64 * kWriteMaxWaves) tq_cache_write_kernel(
         const int nb = a.n_search[which];
         const size_t slot = ((size_t)b * nkv + h) * (size_t)max_seq + (size_t)pl;
         const __half *src = src_of(v);
-        const __half e0 = v == v0 ? pre0 : src[lane];
-        const __half e1 = v == v0 ? pre1 : src[lane + 64];
-        float x0 = __half2float(e0) * sg0;
-        float x1 = __half2float(e1) * sg1;
+        float f0 = __half2float(v == v0 ? pre0 : src[lane]);
+        float f1 = __half2float(v == v0 ? pre1 : src[lane + 64]);
+        if (which == 0 && a.k_norm) {   // uniform: K through the QK-norm + RoPE first
+            const long rp = imh_qk::clamp_pos(start + t, a.rope_max_pos);
+            imh_qk::norm_rope_128(f0, f1, lane, a.k_norm, a.rope_cos + rp * (kD / 2), a.rope_sin + rp * (kD / 2),
+                                  a.eps);
+        }
+        float x0 = f0 * sg0;
+        float x1 = f1 * sg1;
         x0 = hadamard64(x0, lane);
         x1 = hadamard64(x1, lane);
         {
@@ -226,6 +239,19 @@ __global__ void __launch_bounds__(64 * kWriteMaxWaves) tq_cache_write_kernel(
 // weights w * v_scale go through a 128-byte per-wave LDS buffer into row 4hh
 // of operand A as f16.  Built with -amdgpu-mfma-vgpr-form so the accumulators
 // stay in VGPRs (no AGPR round trip around the softmax rescale).
+// Optional QK-norm + RoPE of the query ahead of the rotation (head_dim 128 =
+// rotary_dim): norm weight [128], cos / sin tables [max_pos][64], the query's
+// position positions[b].  norm == NULL: the query is used as given (the other
+// pointers still address readable memory: max_pos 1, 64 table entries).
+struct QkRope {
+    const __half *norm;
+    const __half *cos;
+    const __half *sin;
+    const int32_t *positions;
+    int max_pos;
+    float eps;
+};
+
 template <int GQA>
 __global__ void __launch_bounds__(64 * kWaves) __attribute__((amdgpu_waves_per_eu(3))) tq_attention_kernel(
     const __half *__restrict__ q, int nh, int nkv, int max_seq, int seq_len,
@@ -235,7 +261,7 @@ __global__ void __launch_bounds__(64 * kWaves) __attribute__((amdgpu_waves_per_e
     const float *__restrict__ kscales, const float *__restrict__ vscales,
     const float *__restrict__ krnorm, int split_len, float *__restrict__ part_o,
     float *__restrict__ part_m, float *__restrict__ part_l, int *__restrict__ counters,
-    __half *__restrict__ out) {
+    __half *__restrict__ out, const QkRope qr) {
     __shared__ float qs[GQA][2][kD];
     __shared__ uint32_t ktab[256];   // entry c & 0x7F, indexed by the whole code byte
     __shared__ _Float16 vtab[256];
@@ -311,6 +337,12 @@ __global__ void __launch_bounds__(64 * kWaves) __attribute__((amdgpu_waves_per_e
     const __half *qh = q + ((size_t)b * nh + qhead) * kD;
     const __half q0 = qh[lane], q1 = qh[lane + 64];
     const float sg0 = signs[lane], sg1 = signs[lane + 64];
+    // QK-norm + RoPE operands, loaded unconditionally (a branch here would
+    // make the compiler wait for them before the loads below issue)
+    const __half *qnw = qr.norm ? qr.norm : qh;
+    const long rp = imh_qk::clamp_pos(qr.positions[b], qr.max_pos);
+    const __half qw0 = qnw[lane], qw1 = qnw[lane + 64];
+    const __half qc = qr.cos[rp * (kD / 2) + lane], qsn = qr.sin[rp * (kD / 2) + lane];
     const float kc = kcb[tid & 0x7F], vc = vcb[tid];
     float4 st[16];
     {
@@ -334,7 +366,11 @@ __global__ void __launch_bounds__(64 * kWaves) __attribute__((amdgpu_waves_per_e
     // holds elements lane and lane + 64; butterfly strides 1..32 by xor
     // shuffles, stride 64 in the lane) into qs[hh][0]
     if (wave < GQA) {
-        float x0 = __half2float(q0) * sg0, x1 = __half2float(q1) * sg1;
+        float f0 = __half2float(q0), f1 = __half2float(q1);
+        if (qr.norm)
+            imh_qk::norm_rope_128(f0, f1, __half2float(qw0), __half2float(qw1), __half2float(qc), __half2float(qsn),
+                                  qr.eps);
+        float x0 = f0 * sg0, x1 = f1 * sg1;
         x0 = hadamard64(x0, lane);
         x1 = hadamard64(x1, lane);
         qs[wave][0][lane] = (x0 + x1) * (sg0 * rscale);
@@ -645,7 +681,8 @@ extern "C" {
 
 static int launch_cache_write(imh_stream *stream, const imh_tq_tables *t, const imh_tq_kv_cache *cache,
                               const uint16_t *k_proj, const uint16_t *v_proj, uint32_t token_count,
-                              uint32_t base_pos, const int32_t *positions, const char *who) {
+                              uint32_t base_pos, const int32_t *positions, const char *who,
+                              const imh_qk_norm_rope_params *qk = nullptr) {
     int rc = check_cache(t, cache, who);
     if (rc) return rc;
     if (token_count == 0) return IMH_OK;
@@ -661,6 +698,13 @@ static int launch_cache_write(imh_stream *stream, const imh_tq_tables *t, const 
     a.r_norms = cache->k_r_norms;
     a.codebook[0] = t->k_codebook;
     a.codebook[1] = t->v_codebook;
+    if (qk) {   // K through the QK-norm + RoPE first
+        a.k_norm = reinterpret_cast<const __half *>(qk->k_norm);
+        a.rope_cos = reinterpret_cast<const __half *>(qk->cos_cache);
+        a.rope_sin = reinterpret_cast<const __half *>(qk->sin_cache);
+        a.rope_max_pos = (int)qk->max_pos;
+        a.eps = qk->eps;
+    }
     a.sorted[0] = t->k_sorted;
     a.sorted[1] = t->v_sorted;
     a.prefmax[0] = t->k_prefmax;
@@ -698,11 +742,10 @@ int imh_encode_turboquant_cache_write_kv(imh_stream *stream, const imh_tq_tables
     return launch_cache_write(stream, t, cache, k_proj, v_proj, token_count, base_pos, positions, who);
 }
 
-int imh_encode_turboquant_attention(imh_stream *stream, const imh_tq_tables *t,
-                                    const imh_tq_kv_cache *cache, const uint16_t *q,
-                                    uint32_t num_heads, uint32_t seq_len, const int32_t *seq_lens,
-                                    float attn_scale, uint16_t *out, uint32_t num_splits) {
-    const char *who = "imh_encode_turboquant_attention";
+static int run_attention(imh_stream *stream, const imh_tq_tables *t, const imh_tq_kv_cache *cache,
+                         const uint16_t *q, uint32_t num_heads, uint32_t seq_len, const int32_t *seq_lens,
+                         float attn_scale, uint16_t *out, uint32_t num_splits, const char *who,
+                         const imh_qk_norm_rope_params *qk) {
     if (!stream || !q || !out) return imh::fail(IMH_EINVAL, std::string(who) + ": NULL argument");
     int rc = check_cache(t, cache, who);
     if (rc) return rc;
@@ -760,13 +803,34 @@ int imh_encode_turboquant_attention(imh_stream *stream, const imh_tq_tables *t,
                        (int)nkv, (int)cache->max_seq_len, (int)L, seq_lens, attn_scale, t->signs, t->qjl_t,     \
                        t->k_codebook, t->v_codebook, cache->k_codes, cache->v_codes, cache->k_scales,           \
                        cache->v_scales, cache->k_r_norms, (int)split_len, po, pm, pl, ctr,                      \
-                       reinterpret_cast<__half *>(out))
+                       reinterpret_cast<__half *>(out), qr)
+    // without the QK-norm the kernel still reads (and discards) one position
+    // and 64 table entries: point them at the codebook
+    QkRope qr{nullptr, reinterpret_cast<const __half *>(t->v_codebook),
+              reinterpret_cast<const __half *>(t->v_codebook), reinterpret_cast<const int32_t *>(t->v_codebook), 1,
+              0.0f};
+    if (qk) {   // the query through the QK-norm + RoPE first
+        qr.norm = reinterpret_cast<const __half *>(qk->q_norm);
+        qr.cos = reinterpret_cast<const __half *>(qk->cos_cache);
+        qr.sin = reinterpret_cast<const __half *>(qk->sin_cache);
+        qr.positions = qk->positions;
+        qr.max_pos = (int)qk->max_pos;
+        qr.eps = qk->eps;
+    }
     if (gqa == 4) IMH_TQ_LAUNCH(4);
     else if (gqa == 2) IMH_TQ_LAUNCH(2);
     else IMH_TQ_LAUNCH(1);
 #undef IMH_TQ_LAUNCH
     IMH_HIP(hipGetLastError());
     return IMH_OK;
+}
+
+int imh_encode_turboquant_attention(imh_stream *stream, const imh_tq_tables *t,
+                                    const imh_tq_kv_cache *cache, const uint16_t *q,
+                                    uint32_t num_heads, uint32_t seq_len, const int32_t *seq_lens,
+                                    float attn_scale, uint16_t *out, uint32_t num_splits) {
+    return run_attention(stream, t, cache, q, num_heads, seq_len, seq_lens, attn_scale, out, num_splits,
+                         "imh_encode_turboquant_attention", nullptr);
 }
 
 int imh_encode_kv_cache_and_attention(imh_stream *stream, const imh_tq_tables *t,
@@ -786,3 +850,38 @@ int imh_encode_kv_cache_and_attention(imh_stream *stream, const imh_tq_tables *t
 }
 
 }  // extern "C"
+
+namespace imh {
+
+// QK-norm + RoPE folded into the cache write (K) and the attention prologue
+// (Q); qk must have head_dim = rotary_dim = 128, both norms and positions.
+static int check_qk(const imh_qk_norm_rope_params *qk, const char *who) {
+    if (!qk || !qk->q_norm || !qk->k_norm || !qk->cos_cache || !qk->sin_cache || !qk->positions)
+        return fail(IMH_EINVAL, std::string(who) + ": QK-norm + RoPE needs both norms, the tables and positions");
+    if (qk->head_dim != (uint32_t)kD || (qk->rotary_dim != 0 && qk->rotary_dim != (uint32_t)kD) || qk->max_pos == 0)
+        return fail(IMH_EUNSUPPORTED, std::string(who) + ": folded QK-norm + RoPE is built for head_dim = "
+                                                          "rotary_dim = 128");
+    return IMH_OK;
+}
+
+int encode_tq_write_kv_rope(imh_stream *stream, const imh_tq_tables *t, const imh_tq_kv_cache *cache,
+                            const uint16_t *k_proj, const uint16_t *v_proj, uint32_t token_count,
+                            const int32_t *positions, const imh_qk_norm_rope_params *qk) {
+    const char *who = "encode_tq_write_kv_rope";
+    if (!stream || !k_proj || !v_proj || !positions) return fail(IMH_EINVAL, std::string(who) + ": NULL argument");
+    int rc = check_qk(qk, who);
+    if (rc) return rc;
+    return launch_cache_write(stream, t, cache, k_proj, v_proj, token_count, 0, positions, who, qk);
+}
+
+int encode_tq_attention_rope(imh_stream *stream, const imh_tq_tables *t, const imh_tq_kv_cache *cache,
+                             const uint16_t *q, uint32_t num_heads, uint32_t seq_len, const int32_t *seq_lens,
+                             float attn_scale, uint16_t *out, uint32_t num_splits,
+                             const imh_qk_norm_rope_params *qk) {
+    const char *who = "encode_tq_attention_rope";
+    int rc = check_qk(qk, who);
+    if (rc) return rc;
+    return run_attention(stream, t, cache, q, num_heads, seq_len, seq_lens, attn_scale, out, num_splits, who, qk);
+}
+
+}  // namespace imh
