@@ -471,12 +471,16 @@ def main():
                     f"({100 * tfs / MFMA_F16_PEAK_TFS:.1f} % of dense f16 MFMA)")
         del W
         stream.sync()
+        # sustained rates: a warmup graph long enough for the clocks to settle
+        # (measured: the first ~50 ms of back-to-back launches after the weight
+        # benchmarks run up to 10 % slower than the steady state)
+        att_warm = max(200, args.warmup)
         for bb, layers in ((1, 8), (16, 1)):
-            r = bench_attention(dev, stream, ops, bb, 32768, max(20, args.steps // 4), 5, layers)
+            r = bench_attention(dev, stream, ops, bb, 32768, max(20, args.steps // 4), att_warm, layers)
             details[f"tq_attention_b{bb}_ctx32k"] = r
             log(f"TQ attention B={bb} ctx=32k: {r['us']} us {r['GB/s']} GB/s")
         for bb, layers in ((1, 8), (16, 1)):
-            r = bench_fp16_attention(dev, stream, ops, bb, 32768, max(20, args.steps // 4), 5, layers)
+            r = bench_fp16_attention(dev, stream, ops, bb, 32768, max(20, args.steps // 4), att_warm, layers)
             details[f"fp16_attention_b{bb}_ctx32k"] = r
             log(f"FP16-KV attention B={bb} ctx=32k: {r['us']} us {r['GB/s']} GB/s")
         for bb in (1, 8):
