@@ -495,6 +495,21 @@ int imh_encode_fused_ffn_gate_up_act_int4(imh_stream *stream, const uint16_t *x,
                   nullptr, who);
 }
 
+int imh_encode_ffn_block_int4(imh_stream *stream, const uint16_t *x, uint32_t token_count,
+                              const imh_affine_int4_weight *gate, const imh_affine_int4_weight *up,
+                              const imh_affine_int4_weight *down, uint16_t *act_out, uint16_t *y, int use_gelu) {
+    const char *who = "imh_encode_ffn_block_int4";
+    if (!stream || !x || !act_out || !y || !gate || !up || !down)
+        return imh::fail(IMH_EINVAL, std::string(who) + ": NULL argument");
+    int rc = check_weight(down, who);
+    if (rc) return rc;
+    if (down->k != gate->n)
+        return imh::fail(IMH_EINVAL, std::string(who) + ": down.k must equal the intermediate size (gate.n)");
+    rc = run_op(stream, plain_in(x, gate), token_count, gate, up, use_gelu ? EPI_GELU : EPI_SILU, act_out, nullptr,
+                who);
+    return rc ? rc : run_op(stream, plain_in(act_out, down), token_count, down, nullptr, EPI_STORE, y, nullptr, who);
+}
+
 int imh_encode_fused_residual_norm_affine_matvec_int4(imh_stream *stream,
                                                       const imh_fused_residual_norm_params *p) {
     const char *who = "imh_encode_fused_residual_norm_affine_matvec_int4";

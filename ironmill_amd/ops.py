@@ -77,6 +77,13 @@ def encode_fused_ffn_gate_up_act_int4(stream: Stream, x, gate: AffineQuantizedWe
                                                     int(bool(use_gelu))))
 
 
+def encode_ffn_block_int4(stream: Stream, x, gate: AffineQuantizedWeight, up: AffineQuantizedWeight,
+                          down: AffineQuantizedWeight, act_out, y, token_count: int = 1, use_gelu: bool = False):
+    """encode_ffn_block (metal/ffn.rs:13-144): act_out = act(x.Wg) * (x.Wu), y = act_out . Wd^T."""
+    check(lib.imh_encode_ffn_block_int4(stream.handle, _ptr(x), token_count, C.byref(gate.c), C.byref(up.c),
+                                        C.byref(down.c), _ptr(act_out), _ptr(y), int(bool(use_gelu))))
+
+
 def encode_fused_residual_norm_affine_matvec_int4(stream: Stream, a, b, norm_weight, residual_output,
                                                   weight: AffineQuantizedWeight, output,
                                                   normed_output, eps: float, token_count: int = 1):

@@ -104,6 +104,87 @@ def test_fused_gate_up_qwen_shape(dev, stream, batch, act):
     assert_close(out.read(), ref, what=f"fused gate+up {act} B={batch}", ulps=2)
 
 
+def _ffn_case(dev, n, k, batch, seed):
+    wg, s = make_weight(n, k, seed=seed, awq=True)
+    wu, _ = make_weight(n, k, seed=seed + 1)
+    wd, sd = make_weight(k, n, seed=seed + 2, awq=True)
+    x16 = make_x(batch, k, seed=seed + 3 + batch)
+    gate = upload_weight(dev, wg, s)
+    up = ops.AffineQuantizedWeight(dev, quant.quantize_int4(wu, awq_scales=s))
+    down = upload_weight(dev, wd, sd)
+    return (wg, wu, wd, s, sd, x16), (gate, up, down)
+
+
+@pytest.mark.parametrize("n,k,batch,act", [
+    (9728, 2560, 1, "silu"),   # Qwen3-4B FFN
+    (9728, 2560, 1, "gelu"),
+    (512, 256, 2, "silu"),
+    (9728, 2560, 4, "silu"),
+    (10240, 2560, 1, "silu"),  # Qwen3.5-4B intermediate size
+    (512, 256, 40, "silu"),    # prefill-sized: the GEMM ops
+])
+def test_ffn_block_matches_oracle(dev, stream, n, k, batch, act):
+    """encode_ffn_block: act against the oracle's gate_up_act; y against the
+    oracle's down projection of the act the GPU wrote (so act's own rounding is
+    not counted twice); the same act as the fused gate+up op, bit for bit, and
+    y within tolerance of the two-op path."""
+    (wg, wu, wd, s, sd, x16), (gate, up, down) = _ffn_case(dev, n, k, batch, seed=21)
+    xd = dev.upload(x16)
+    act_d = dev.empty((batch, n), np.float16)
+    y = dev.empty((batch, k), np.float16)
+    gelu = act == "gelu"
+    ops.encode_ffn_block_int4(stream, xd, gate, up, down, act_d, y, batch, use_gelu=gelu)
+    stream.sync()
+    got_act, got_y = act_d.read(), y.read()
+    wdq_g, awq16 = oracle_dense(wg, s)
+    wdq_u, _ = oracle_dense(wu, s)
+    assert_close(got_act, O.gate_up_act(wdq_g, wdq_u, x16, awq16, act=act), what="ffn act", ulps=2)
+    wdq_d, awqd = oracle_dense(wd, sd)
+    assert_close(got_y, O.matvec_f16w(wdq_d, got_act, awqd, nthreads=8), what="ffn y", ulps=2)
+    # the two ops on the same inputs
+    act2 = dev.empty((batch, n), np.float16)
+    y2 = dev.empty((batch, k), np.float16)
+    ops.encode_fused_ffn_gate_up_act_int4(stream, xd, gate, up, act2, batch, use_gelu=gelu)
+    ops.encode_projection(stream, act2, down, y2, batch)
+    stream.sync()
+    assert np.array_equal(act2.read().view(np.uint16), got_act.view(np.uint16)), "act differs from the fused op"
+    assert_close(got_y, y2.read().astype(np.float32), what="ffn y vs two ops", ulps=2)
+
+
+def test_ffn_block_repeated_launches(dev, stream):
+    """Back-to-back FFN blocks of different shapes on one stream, then a graph
+    replaying one (with eager work between the replays), give the eager result
+    every time."""
+    big = _ffn_case(dev, 9728, 2560, 1, seed=31)
+    small = _ffn_case(dev, 512, 256, 2, seed=41)
+    outs = {}
+    for name, ((*_, x16), (gate, up, down)), b in (("big", big, 1), ("small", small, 2)):
+        xd = dev.upload(x16)
+        a = dev.empty((b, gate.n), np.float16)
+        y = dev.empty((b, gate.k), np.float16)
+        outs[name] = (xd, gate, up, down, a, y, b)
+    ref = {}
+    for it in range(3):
+        for name in ("big", "small", "big"):
+            xd, gate, up, down, a, y, b = outs[name]
+            ops.encode_ffn_block_int4(stream, xd, gate, up, down, a, y, b)
+            stream.sync()
+            got = y.read().view(np.uint16).copy()
+            if name not in ref:
+                ref[name] = got
+            assert np.array_equal(got, ref[name]), f"launch {it} {name}"
+    xd, gate, up, down, a, y, b = outs["big"]
+    graph = stream.capture(lambda: [ops.encode_ffn_block_int4(stream, xd, gate, up, down, a, y, b)
+                                    for _ in range(4)])
+    for rep in range(3):
+        y.write(np.zeros((b, gate.k), np.float16))
+        graph.launch(stream)
+        stream.sync()
+        assert np.array_equal(y.read().view(np.uint16), ref["big"]), f"graph replay {rep}"
+        ops.encode_ffn_block_int4(stream, *outs["small"][:6], 2)   # eager work between replays
+        stream.sync()
+
+
 @pytest.mark.parametrize("batch,awq", [(1, True), (8, False)])
 def test_batched_gate_up(dev, stream, batch, awq):
     n, k = 9728, 2560
