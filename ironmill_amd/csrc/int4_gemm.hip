@@ -86,10 +86,13 @@ __device__ __forceinline__ float gate_act(float g, float u, int epi) {
 // (64-wide K stages).  With AWQ, x / awq is split into f16 hi + lo planes
 // (~22-bit operands, two MFMAs per step, 32-wide K stages so two workgroups
 // still fit a CU's LDS): rounding x / awq to f16 alone moves outputs by
-// several fp16 steps where terms cancel.
+// several fp16 steps where terms cancel.  The planes are built once, in slot
+// order, by int4_gemm_prep_kernel (x = the hi plane, xlo = the lo plane):
+// built per workgroup they were redone by every column tile and made the
+// kernel VALU-bound.
 template <bool AWQ, int NMAT>
 __global__ void __launch_bounds__(kThreads, 2) int4_gemm_kernel(
-    const __half *__restrict__ x, const __half *__restrict__ awq, GemmMats mats, int epi,
+    const __half *__restrict__ x, const __half *__restrict__ xlo, GemmMats mats, int epi,
     float *__restrict__ part, int M, int N, int K, int stages_per_split) {
     constexpr int kTN = kBN / NMAT;          // output columns per matrix
     constexpr int BK = AWQ ? 32 : 64;        // K per stage
@@ -125,11 +128,16 @@ __global__ void __launch_bounds__(kThreads, 2) int4_gemm_kernel(
     const __half *zeros = b_mat ? mats.zeros[1] : mats.zeros[0];
     const uint8_t *b_src = b_data + (size_t)b_n * (K / 2) + b_half * (BK / 4);
 
-    u32x4_t a_reg[ACH], a_w[ACH];
-    uint32_t b_reg[BDW];
-    uint32_t b_sz;
+    // one stage's global loads, held in registers until stored to LDS
+    struct StageRegs {
+        u32x4_t a[ACH], w[ACH];
+        uint32_t b[BDW];
+        uint32_t sz;
+    };
 
-    auto load_stage = [&](int st) __attribute__((always_inline)) {
+    auto load_stage = [&](int st, StageRegs &rg) __attribute__((always_inline)) {
+        u32x4_t *a_reg = rg.a, *a_w = rg.w;
+        uint32_t *b_reg = rg.b;
         const int k0 = st * BK;
 #pragma unroll
         for (int i = 0; i < ACH; i++) {
@@ -137,7 +145,7 @@ __global__ void __launch_bounds__(kThreads, 2) int4_gemm_kernel(
             const int r = c / (BK / 8), kc = c % (BK / 8);
             const int m = min(m0 + r, M - 1);
             a_reg[i] = *reinterpret_cast<const u32x4_t *>(x + (size_t)m * K + k0 + kc * 8);
-            if (AWQ) a_w[i] = *reinterpret_cast<const u32x4_t *>(awq + k0 + kc * 8);
+            if (AWQ) a_w[i] = *reinterpret_cast<const u32x4_t *>(xlo + (size_t)m * K + k0 + kc * 8);
         }
         const uint32_t *bp = reinterpret_cast<const uint32_t *>(b_src + (size_t)k0 / 2);
         if (BDW == 4) {
@@ -150,8 +158,8 @@ __global__ void __launch_bounds__(kThreads, 2) int4_gemm_kernel(
             b_reg[BDW - 1] = v.y;
         }
         const size_t gi = (size_t)b_n * G + k0 / kGS;
-        b_sz = (uint32_t)reinterpret_cast<const uint16_t *>(scales)[gi] |
-               ((uint32_t)reinterpret_cast<const uint16_t *>(zeros)[gi] << 16);
+        rg.sz = (uint32_t)reinterpret_cast<const uint16_t *>(scales)[gi] |
+                ((uint32_t)reinterpret_cast<const uint16_t *>(zeros)[gi] << 16);
     };
 
     // (e0 e1)(e2 e3)(e4 e5)(e6 e7) -> (e0 e2)(e4 e6)(e1 e3)(e5 e7)
@@ -160,25 +168,18 @@ __global__ void __launch_bounds__(kThreads, 2) int4_gemm_kernel(
                          __builtin_amdgcn_perm(v[1], v[0], 0x07060302u), __builtin_amdgcn_perm(v[3], v[2], 0x07060302u)};
     };
 
-    auto store_stage = [&](int buf) __attribute__((always_inline)) {
+    auto store_stage = [&](int buf, const StageRegs &rg) __attribute__((always_inline)) {
+        const u32x4_t *a_reg = rg.a, *a_w = rg.w;
+        const uint32_t *b_reg = rg.b;
+        const uint32_t b_sz = rg.sz;
         // activation: x, or x / awq as hi + lo; slots {0,2,4,6,1,3,5,7} within each chunk
 #pragma unroll
         for (int i = 0; i < ACH; i++) {
             const int c = i * kThreads + tid;
             const int r = c / (BK / 8), kc = c % (BK / 8);
-            if (AWQ) {
-                const _Float16 *xh = reinterpret_cast<const _Float16 *>(&a_reg[i]);
-                const _Float16 *wh = reinterpret_cast<const _Float16 *>(&a_w[i]);
-                half8_t hi, lo;
-#pragma unroll
-                for (int j = 0; j < 8; j++) {
-                    const float v = (float)xh[j] * __builtin_amdgcn_rcpf((float)wh[j]);
-                    hi[j] = (_Float16)v;
-                    lo[j] = (_Float16)(v - (float)hi[j]);
-                }
-                *reinterpret_cast<u32x4_t *>(&As[buf][0][r * ROW + kc * 8]) = slot_order(__builtin_bit_cast(u32x4_t, hi));
-                *reinterpret_cast<u32x4_t *>(&As[buf][NPL - 1][r * ROW + kc * 8]) =
-                    slot_order(__builtin_bit_cast(u32x4_t, lo));
+            if (AWQ) {   // planes already in slot order
+                *reinterpret_cast<u32x4_t *>(&As[buf][0][r * ROW + kc * 8]) = a_reg[i];
+                *reinterpret_cast<u32x4_t *>(&As[buf][NPL - 1][r * ROW + kc * 8]) = a_w[i];
             } else {
                 *reinterpret_cast<u32x4_t *>(&As[buf][0][r * ROW + kc * 8]) = slot_order(a_reg[i]);
             }
@@ -216,15 +217,8 @@ __global__ void __launch_bounds__(kThreads, 2) int4_gemm_kernel(
         }
 
     const int fr = lane & 15, fk = (lane >> 4) * 8;
-    if (s_begin < s_end) {
-        load_stage(s_begin);
-        store_stage(0);
-        __syncthreads();
-    }
-    for (int st = s_begin; st < s_end; st++) {
-        const int buf = (st - s_begin) & 1;
-        const bool more = st + 1 < s_end;
-        if (more) load_stage(st + 1);
+    // the MFMAs of stage st from LDS buffer buf, and the group-end fold
+    auto compute_stage = [&](int st, int buf) __attribute__((always_inline)) {
 #pragma unroll
         for (int ks = 0; ks < BK; ks += 32) {
             half8_t bf[4];
@@ -256,7 +250,19 @@ __global__ void __launch_bounds__(kThreads, 2) int4_gemm_kernel(
                 }
             }
         }
-        if (more) store_stage(buf ^ 1);
+    };
+    StageRegs rg;
+    if (s_begin < s_end) {
+        load_stage(s_begin, rg);
+        store_stage(0, rg);
+        __syncthreads();
+    }
+    for (int st = s_begin; st < s_end; st++) {
+        const int buf = (st - s_begin) & 1;
+        const bool more = st + 1 < s_end;
+        if (more) load_stage(st + 1, rg);
+        compute_stage(st, buf);
+        if (more) store_stage(buf ^ 1, rg);
         __syncthreads();
     }
 
@@ -319,6 +325,35 @@ __global__ void __launch_bounds__(kThreads, 2) int4_gemm_kernel(
                 if (m < M) o[(size_t)m * N + n] = __float2half(acc[i][j][r]);
             }
         }
+}
+
+// The AWQ activation planes: hi = f16(x / awq), lo = f16(x / awq - hi), each
+// 8-element chunk in slot order {0, 2, 4, 6, 1, 3, 5, 7}.  grid (M,
+// ceil(K/8 / 256)), block 256: one chunk per thread.
+__global__ void __launch_bounds__(256) int4_gemm_prep_kernel(const __half *__restrict__ x,
+                                                             const __half *__restrict__ awq,
+                                                             __half *__restrict__ hi_out,
+                                                             __half *__restrict__ lo_out, int K) {
+    const int c = blockIdx.y * blockDim.x + threadIdx.x;
+    if (c * 8 >= K) return;
+    const size_t off = (size_t)blockIdx.x * K + (size_t)c * 8;
+    const u32x4_t xv = *reinterpret_cast<const u32x4_t *>(x + off);
+    const u32x4_t wv = *reinterpret_cast<const u32x4_t *>(awq + (size_t)c * 8);
+    const _Float16 *xh = reinterpret_cast<const _Float16 *>(&xv);
+    const _Float16 *wh = reinterpret_cast<const _Float16 *>(&wv);
+    half8_t hi, lo;
+#pragma unroll
+    for (int j = 0; j < 8; j++) {
+        const float v = (float)xh[j] * __builtin_amdgcn_rcpf((float)wh[j]);
+        hi[j] = (_Float16)v;
+        lo[j] = (_Float16)(v - (float)hi[j]);
+    }
+    auto slot_order = [](u32x4_t v) {
+        return (u32x4_t){__builtin_amdgcn_perm(v[1], v[0], 0x05040100u), __builtin_amdgcn_perm(v[3], v[2], 0x05040100u),
+                         __builtin_amdgcn_perm(v[1], v[0], 0x07060302u), __builtin_amdgcn_perm(v[3], v[2], 0x07060302u)};
+    };
+    *reinterpret_cast<u32x4_t *>(hi_out + off) = slot_order(__builtin_bit_cast(u32x4_t, hi));
+    *reinterpret_cast<u32x4_t *>(lo_out + off) = slot_order(__builtin_bit_cast(u32x4_t, lo));
 }
 
 // Sum the split partials in split order, then store (or, for a gate/up pair,
@@ -434,11 +469,24 @@ int encode_gemm(imh_stream *s, const __half *x, int M, const imh_affine_int4_wei
     }
     mats.out[0] = y0;
     mats.out[1] = y1;
-    // both matrices of a pair divide x by the first one's awq scales
+    // both matrices of a pair divide x by the first one's awq scales; the
+    // hi / lo planes of x / awq are built once, into stream scratch slot 0
     const __half *awq = reinterpret_cast<const __half *>(w0->awq_scales);
+    const __half *xa = x, *xlo = nullptr;
+    if (awq) {
+        void *planes = nullptr;
+        int rc = imh::stream_scratch(s, 0, (size_t)M * K * 2 * sizeof(__half), &planes);
+        if (rc) return rc;
+        __half *hi = static_cast<__half *>(planes), *lo = hi + (size_t)M * K;
+        hipLaunchKernelGGL(int4_gemm_prep_kernel, dim3(M, (K / 8 + 255) / 256), dim3(256), 0, s->stream, x, awq, hi,
+                           lo, K);
+        IMH_HIP(hipGetLastError());
+        xa = hi;
+        xlo = lo;
+    }
     const int ge = epi == 2 ? GE_SILU : epi == 3 ? GE_GELU : GE_STORE;
-#define IMH_GEMM(A, NM)                                                                                       \
-    hipLaunchKernelGGL((int4_gemm_kernel<A, NM>), grid, dim3(kThreads), 0, s->stream, x, awq, mats, ge, part, M, \
+#define IMH_GEMM(A, NM)                                                                                        \
+    hipLaunchKernelGGL((int4_gemm_kernel<A, NM>), grid, dim3(kThreads), 0, s->stream, xa, xlo, mats, ge, part, M, \
                        N, K, per)
     if (awq) {
         if (nmat == 2) IMH_GEMM(true, 2);
