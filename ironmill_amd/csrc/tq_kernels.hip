@@ -17,11 +17,13 @@
 //     query (hi, lo) and its QJL projection (hi, lo) packed as rows of operand A;
 //   * folds the per-position scales in and runs the online softmax of all the
 //     group's heads at once with DPP row reductions;
-//   * accumulates P.V on v_mfma_f32_16x16x16_f16 (positions as the contraction
-//     index) from V codes transposed in registers and looked up in an f16
-//     codebook, with the weights (times the V scale) as f16.
-// Waves combine through LDS; splits are combined (log-sum-exp) and rotated
-// back by a second small kernel (fused_sdpa_reduce, flash_decode.metal:163-215).
+//   * accumulates P.V on v_mfma_f32_16x16x32_f16 (positions as the contraction
+//     index, each position twice: against the f16 hi and lo halves of its
+//     codebook value) from V codes transposed in registers, with the weights
+//     (times the V scale) as f16.
+// Waves combine through LDS; the last workgroup of a group to finish combines
+// the splits (log-sum-exp, fused_sdpa_reduce, flash_decode.metal:163-215) and
+// rotates the result back.
 #include <hip/hip_runtime.h>
 #include <hip/hip_fp16.h>
 
@@ -231,13 +233,13 @@ __global__ void __launch_bounds__(64 * kWriteMaxWaves) tq_cache_write_kernel(
 // MFMA operands, so in every 16x16 result lane group g = lane >> 4 holds head
 // g: the scores of one head are one DPP row (softmax reductions serve all
 // heads at once) and the running max, sum and rescale are per lane.  P.V runs
-// on v_mfma_f32_16x16x16_f16 with the positions as the contraction index:
+// on v_mfma_f32_16x16x32_f16 with the positions as the contraction index:
 // result column c of block j is dim 8c + j, so lane (c, g) loads V codes of
 // positions 4g..4g+3 at dims 8c..8c+7 (four 8-byte row loads, coalesced
-// across the 16 lanes of a row) and its B operand for block j is the four
-// codebook values of byte j -- a register transpose, no LDS staging.  The
-// weights w * v_scale go through a 128-byte per-wave LDS buffer into row 4hh
-// of operand A as f16.  Built with -amdgpu-mfma-vgpr-form so the accumulators
+// across the 16 lanes of a row) and its B operand for block j is the
+// codebook values (f16 hi, lo) of byte j of the four rows -- a register
+// transpose, no LDS staging.  The weights w * v_scale go through a 128-byte
+// per-wave LDS buffer into row 4hh of operand A as f16, each weight twice.  Built with -amdgpu-mfma-vgpr-form so the accumulators
 // stay in VGPRs (no AGPR round trip around the softmax rescale).
 // Optional QK-norm + RoPE of the query ahead of the rotation (head_dim 128 =
 // rotary_dim): norm weight [128], cos / sin tables [max_pos][64], the query's
@@ -264,7 +266,7 @@ __global__ void __launch_bounds__(64 * kWaves) __attribute__((amdgpu_waves_per_e
     __half *__restrict__ out, const QkRope qr) {
     __shared__ float qs[GQA][2][kD];
     __shared__ uint32_t ktab[256];   // entry c & 0x7F, indexed by the whole code byte
-    __shared__ _Float16 vtab[256];
+    __shared__ uint32_t vtab[256];   // V entry c, same packing as ktab
     __shared__ _Float16 wbuf[kWaves][4][16];
     __shared__ float om[kWaves][GQA][kD];
     __shared__ float mm[kWaves][GQA];
@@ -355,13 +357,18 @@ __global__ void __launch_bounds__(64 * kWaves) __attribute__((amdgpu_waves_per_e
     load_chunk(p_first, cur);
     __builtin_amdgcn_sched_barrier(0);   // every load above issues before the first wait
 
-    // tables: K codebook as (f16 hi | f16 lo << 16), V codebook in f16
+    // tables: K and V codebooks as (f16 hi | f16 lo << 16).  An f16 V entry
+    // alone would bias every output by its rounding error, a bias that does
+    // not average out over positions while the output itself shrinks as
+    // 1/sqrt(positions) (rel-L2 1.9e-3 at 30k positions of random V).
     {
         const _Float16 hi = (_Float16)kc;
         const _Float16 lo = (_Float16)(kc - (float)hi);
         ktab[tid] = (uint32_t)__builtin_bit_cast(uint16_t, hi) | ((uint32_t)__builtin_bit_cast(uint16_t, lo) << 16);
+        const _Float16 vh = (_Float16)vc;
+        const _Float16 vl = (_Float16)(vc - (float)vh);
+        vtab[tid] = (uint32_t)__builtin_bit_cast(uint16_t, vh) | ((uint32_t)__builtin_bit_cast(uint16_t, vl) << 16);
     }
-    vtab[tid] = (_Float16)vc;
     // q_rot = D.H.D/sqrt(d) q: wave hh rotates head hh in registers (lane
     // holds elements lane and lane + 64; butterfly strides 1..32 by xor
     // shuffles, stride 64 in the lane) into qs[hh][0]
@@ -495,19 +502,21 @@ __global__ void __launch_bounds__(64 * kWaves) __attribute__((amdgpu_waves_per_e
         __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
         __builtin_amdgcn_wave_barrier();
         __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-        half4_t wa = {0, 0, 0, 0};
-        if (arow && ar == 0) wa = *reinterpret_cast<const half4_t *>(&wbuf[wave][ah][4 * kg]);
-        // ---- o += W . V: operand B of block j = codebook values of byte j of
-        // the four position rows ----
+        half4_t w4 = {0, 0, 0, 0};
+        if (arow && ar == 0) w4 = *reinterpret_cast<const half4_t *>(&wbuf[wave][ah][4 * kg]);
+        const half8_t wa = {w4[0], w4[0], w4[1], w4[1], w4[2], w4[2], w4[3], w4[3]};
+        // ---- o += W . V: operand B of block j = codebook values (hi, lo) of
+        // byte j of the four position rows ----
 #pragma unroll
         for (int j = 0; j < 8; j++) {
-            half4_t bv;
+            uint32_t e[4];
 #pragma unroll
             for (int i = 0; i < 4; i++) {
                 const uint32_t word = j < 4 ? c.v[i].x : c.v[i].y;
-                bv[i] = vtab[(word >> (8 * (j & 3))) & 0xFF];
+                e[i] = vtab[(word >> (8 * (j & 3))) & 0xFF];
             }
-            acc[j] = __builtin_amdgcn_mfma_f32_16x16x16f16(wa, bv, acc[j], 0, 0, 0);
+            const half8_t bv = __builtin_bit_cast(half8_t, make_uint4(e[0], e[1], e[2], e[3]));
+            acc[j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(wa, bv, acc[j], 0, 0, 0);
         }
         __builtin_amdgcn_wave_barrier();   // wbuf is rewritten next chunk
     };

@@ -32,11 +32,11 @@ def tables():
     return O.TQTables(D, 8, 42)
 
 
-def kv_data(batch, tokens, nkv, seed):
+def kv_data(batch, tokens, nkv, seed, outliers=True):
     """K/V fp16 N(0,1) with 4 seeded outlier channels per head scaled x10."""
     rng = np.random.default_rng(seed)
     x = rng.standard_normal((batch, tokens, nkv, D)).astype(np.float32)
-    for h in range(nkv):
+    for h in range(nkv if outliers else 0):
         ch = rng.choice(D, 4, replace=False)
         x[:, :, h, ch] *= 10.0
     return x.astype(np.float16)
@@ -108,11 +108,11 @@ def test_cache_write_unsorted_boundaries_scan(dev, stream):
     assert np.array_equal(cache.k_codes.read(), kc) and np.array_equal(cache.v_codes.read(), vc)
 
 
-def fill_cache(dev, stream, tq, batch, nkv, max_seq, ctx, seed):
+def fill_cache(dev, stream, tq, batch, nkv, max_seq, ctx, seed, outliers=True):
     cache = ops.TurboQuantKvCache(dev, batch, nkv, D, max_seq)
     cache.zero(stream)
-    k = kv_data(batch, ctx, nkv, seed)
-    v = kv_data(batch, ctx, nkv, seed + 1)
+    k = kv_data(batch, ctx, nkv, seed, outliers)
+    v = kv_data(batch, ctx, nkv, seed + 1, outliers)
     kd, vd = dev.upload(k), dev.upload(v)
     ops.encode_turboquant_cache_write(stream, tq, cache, kd, ctx, 0, True)
     ops.encode_turboquant_cache_write(stream, tq, cache, vd, ctx, 0, False)
@@ -193,6 +193,20 @@ def test_attention_full_size(dev, stream, tq, tables, batch, ctx):
     kc, vc, ks, vs, kr = read_cache(cache)
     ref = O.tq_attention(q16, tables, kc, vc, ks, vs, kr, ctx, 1.0 / math.sqrt(D), nthreads=8)
     assert_close(got, ref, what=f"full size B={batch} ctx={ctx}")
+
+
+def test_attention_long_context_plain_normal(dev, stream, tq, tables):
+    """Plain N(0,1) K/V at 30000 positions: the weights are nearly uniform, so the output
+    shrinks as 1/sqrt(positions) while a rounding bias of the V codebook does not.  With the
+    codebook in f16 alone this case gives rel-L2 1.9e-3 (computed on the CPU with the rounded
+    codebook); the hi + lo codebook keeps it near the f16 weight rounding (~2e-4)."""
+    nkv, nh, ctx = 8, 32, 30000
+    cache = fill_cache(dev, stream, tq, 1, nkv, ctx, ctx, seed=77, outliers=False)
+    q16 = np.random.default_rng(13).standard_normal((1, nh, D)).astype(np.float16)
+    got = run_attention(dev, stream, tq, cache, q16, nh, ctx)
+    kc, vc, ks, vs, kr = read_cache(cache)
+    ref = O.tq_attention(q16, tables, kc, vc, ks, vs, kr, ctx, 1.0 / math.sqrt(D), nthreads=8)
+    assert_close(got, ref, rel=5e-4, what="plain N(0,1) K/V, 30000 positions")
 
 
 def test_decode_step_write_then_attend(dev, stream, tq, tables):

@@ -427,6 +427,24 @@ def test_tq_attention_matches_float_attention_on_dequantized_cache(tabs):
     assert np.linalg.norm(out[0, 0] - exact) / np.linalg.norm(exact) < 0.1
 
 
+def test_tq_attention_long_context_exposes_f16_codebook_bias(tabs):
+    """Planted mistake: the V codebook rounded to f16 (an f16-only operand table) moves the
+    output of plain N(0,1) K/V at 30000 positions by rel-L2 > 1e-3 -- the bias does not
+    average out while the output shrinks as 1/sqrt(positions).  The GPU test of the same
+    shape asserts 5e-4, so it fails for a kernel with that table."""
+    import copy
+    rng = np.random.default_rng(77)
+    ctx = 30000
+    kv = rng.standard_normal((2, 1, ctx, 1, 128)).astype(np.float16)
+    caches = _write(tabs, kv, ctx)
+    q = rng.standard_normal((1, 4, 128)).astype(np.float16)
+    out = O.tq_attention(q, tabs, *caches, ctx, 1 / math.sqrt(128), nthreads=4)
+    bad = copy.copy(tabs)
+    bad.v_codebook = tabs.v_codebook.astype(np.float16).astype(np.float32)
+    out_bad = O.tq_attention(q, bad, *caches, ctx, 1 / math.sqrt(128), nthreads=4)
+    assert np.linalg.norm(out_bad - out) / np.linalg.norm(out) > 1e-3
+
+
 # ---- FP16-KV attention (cpu_attention, metal/inference.rs:222-280) ----
 
 def _fp16_cache(rng, batch, nkv, max_seq, scale=1.0):
