@@ -12,13 +12,16 @@
 //
 // Schedule per layer l (B rows = one token per sequence):
 //   [l == 0] embedding + input RMSNorm          -> hidden, norm_out
-//   Q (unless the previous layer's end fused it), K, V projections of norm_out
-//   QK RMSNorm + RoPE at positions[b]           -> q, k in place
-//   cache write K, V at positions[b]; attention over [0, seq_lens[b]) -> attn_out
+//   Q | K | V projections of norm_out as the row segments of one launch
+//     (for l > 0 fused into the previous layer's end, see below)
+//   TurboQuant: cache write of K, V at positions[b] and attention over
+//     [0, seq_lens[b]) in one launch, the QK RMSNorm + RoPE of K and Q inside
+//     it; FP16 cache: QK RMSNorm + RoPE, K / V scatter, attention -> attn_out
 //   O projection                                -> ffn_down
-//   residual + post-attention RMSNorm           -> norm_out, residual
-//   gate/up + SiLU/GELU, down projection        -> act, ffn_down
-//   [l < L-1] residual + next input RMSNorm + next Q projection (one launch)
+//   residual + post-attention RMSNorm + gate/up + SiLU/GELU (one launch)
+//                                               -> residual, act
+//   down projection                             -> ffn_down
+//   [l < L-1] residual + next input RMSNorm + next Q | K | V (one launch)
 //   [l = L-1] residual add                      -> hidden
 // final RMSNorm, LM head -> logits; positions += 1.
 #include <hip/hip_runtime.h>
@@ -338,21 +341,15 @@ int imh_decoder_step(imh_decoder *d, imh_stream *s, const uint32_t *token_ids, u
         qp.batch = B;
         qp.token_count = 1;
         qp.eps = c.rms_eps;
-        // TurboQuant with QK-norms at head_dim = rotary_dim = 128: the norm and
-        // rotation run inside the cache write (K) and the attention prologue (Q)
+        // TurboQuant: the token's cache write runs inside the attention launch;
+        // with QK-norms at head_dim = rotary_dim = 128 so do the norm and
+        // rotation of K (in the writing workgroup) and Q (in the prologue)
         const bool fold = c.kv_cache == IMH_KV_TURBOQUANT && w.q_norm && w.k_norm && c.head_dim == 128 &&
                           (c.rotary_dim == 0 || c.rotary_dim == 128);
-        if (fold) {
-            const imh_tq_kv_cache *kc = &d->tq_caches[l];
-            IMH_TRY(imh::encode_tq_write_kv_rope(s, d->tq, kc, d->k, d->v, 1, d->positions, &qp));
-            IMH_TRY(imh::encode_tq_attention_rope(s, d->tq, kc, d->q, c.num_heads, 0, d->seq_lens, c.attn_scale,
-                                                  d->attn_out, 0, &qp));
-        } else if (c.kv_cache == IMH_KV_TURBOQUANT) {
-            IMH_TRY(imh_encode_qk_norm_rope(s, &qp));
-            const imh_tq_kv_cache *kc = &d->tq_caches[l];
-            IMH_TRY(imh_encode_turboquant_cache_write_kv(s, d->tq, kc, d->k, d->v, 1, 0, d->positions));
-            IMH_TRY(imh_encode_turboquant_attention(s, d->tq, kc, d->q, c.num_heads, 0, d->seq_lens, c.attn_scale,
-                                                    d->attn_out, 0));
+        if (c.kv_cache == IMH_KV_TURBOQUANT) {
+            if (!fold) IMH_TRY(imh_encode_qk_norm_rope(s, &qp));
+            IMH_TRY(imh::encode_tq_write_attend(s, d->tq, &d->tq_caches[l], d->q, d->k, d->v, c.num_heads,
+                                                d->seq_lens, c.attn_scale, d->attn_out, fold ? &qp : nullptr));
         } else {
             IMH_TRY(imh_encode_qk_norm_rope(s, &qp));
             const imh_fp16_kv_cache *kc = &d->fp16_caches[l];

@@ -111,20 +111,14 @@ int encode_resnorm_gate_up_act_int4(imh_stream *s, const imh_fused_residual_norm
                                     const imh_affine_int4_weight *gate, const imh_affine_int4_weight *up,
                                     uint16_t *out, int use_gelu);
 
-// TurboQuant cache write of one decode token's K and V (positions[b] per
-// sequence) with K first through the QK-norm + RoPE of qk (k_norm, tables,
-// max_pos, eps), as imh_encode_qk_norm_rope followed by
-// imh_encode_turboquant_cache_write_kv would give (tq_kernels.hip).  Built
-// for head_dim = rotary_dim = 128.
-int encode_tq_write_kv_rope(imh_stream *stream, const imh_tq_tables *t, const imh_tq_kv_cache *cache,
-                            const uint16_t *k_proj, const uint16_t *v_proj, uint32_t token_count,
-                            const int32_t *positions, const imh_qk_norm_rope_params *qk);
-
-// imh_encode_turboquant_attention with the query first through the QK-norm +
-// RoPE of qk (q_norm, tables, positions[b], max_pos, eps).
-int encode_tq_attention_rope(imh_stream *stream, const imh_tq_tables *t, const imh_tq_kv_cache *cache,
-                             const uint16_t *q, uint32_t num_heads, uint32_t seq_len, const int32_t *seq_lens,
-                             float attn_scale, uint16_t *out, uint32_t num_splits,
-                             const imh_qk_norm_rope_params *qk);
+// The step's token written to the TurboQuant cache at row seq_lens[b] - 1
+// and attended over [0, seq_lens[b]) in one launch (the write runs in one
+// extra workgroup per (kv head, sequence) beside the attention splits).  With
+// qk (head_dim = rotary_dim = 128, both norms, positions[b] = seq_lens[b] - 1)
+// Q and K go through the QK-norm + RoPE inside the launch.
+int encode_tq_write_attend(imh_stream *stream, const imh_tq_tables *t, const imh_tq_kv_cache *cache,
+                           const uint16_t *q, const uint16_t *k_proj, const uint16_t *v_proj, uint32_t num_heads,
+                           const int32_t *seq_lens, float attn_scale, uint16_t *out,
+                           const imh_qk_norm_rope_params *qk);
 
 }  // namespace imh

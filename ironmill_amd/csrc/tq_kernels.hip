@@ -91,14 +91,68 @@ struct TqWriteArgs {
     const float *sorted[2];      // boundaries sorted by value (NaN dropped)
     const int32_t *prefmax[2];   // running max of (original index + 1)
     int n_search[2];
-    // optional QK-norm + RoPE of K ahead of the quantization (head_dim 128 =
-    // rotary_dim): norm weight [128], cos / sin tables [max_pos][64]
-    const __half *k_norm;
-    const __half *rope_cos;
-    const __half *rope_sin;
-    int rope_max_pos;
-    float eps;
 };
+
+// Sum of a 128-element vector held as (element lane, element lane + 64): the
+// pair first, then halving strides 32..1 by down shuffles -- the f32 order of
+// a 128-element halving tree.  Every lane gets the sum.
+__device__ __forceinline__ float tree_sum128(float a, float b) {
+#pragma clang fp contract(off)
+    float v = a + b;
+    for (int sh = 32; sh > 0; sh >>= 1) v = v + __shfl_down(v, sh);
+    return __shfl(v, 0);
+}
+
+// One vector's TurboQuant codes (turboquant.metal:52-170), held by one wave as
+// f0 = element lane, f1 = element lane + 64: rotation, L2 norm as the scale,
+// centroid index by the table's own boundary rule; with kcb (K) also the
+// residual u - kcb[code] and its norm.  The QJL sign bit is the caller's.
+struct TqCodes {
+    uint32_t c0, c1;   // codes of elements lane, lane + 64
+    float l2;          // scale
+    float r0, r1, rn;  // K: residual elements and norm
+};
+__device__ __forceinline__ TqCodes tq_quantize_vec(float f0, float f1, int lane, float sg0, float sg1,
+                                                   const float *bd, const int32_t *pm, int nb,
+                                                   const float *kcb) {
+#pragma clang fp contract(off)
+    const float rscale = 1.0f / sqrtf((float)kD);
+    float x0 = f0 * sg0;
+    float x1 = f1 * sg1;
+    x0 = hadamard64(x0, lane);
+    x1 = hadamard64(x1, lane);
+    {
+        const float lo = x0, hi = x1;   // stride 64: elements lane and lane + 64
+        x0 = lo + hi;
+        x1 = lo - hi;
+    }
+    const float xr0 = x0 * (sg0 * rscale), xr1 = x1 * (sg1 * rscale);
+    TqCodes r;
+    r.l2 = sqrt_rn(fmaxf(tree_sum128(xr0 * xr0, xr1 * xr1), 1e-20f));
+    const float inv = __fdiv_rn(1.0f, fmaxf(r.l2, 1e-10f));
+    const float u0 = xr0 * inv, u1 = xr1 * inv;
+    // 1 + the last j with u >= boundary[j] in the table's own order (0 if
+    // none): the boundaries that u passes are a prefix of the sorted ones,
+    // so the answer is the prefix max there (turboquant.metal:118-124)
+    auto find = [&](float u) {
+        int lo = 0, hi = nb;
+        while (lo < hi) {
+            const int mid = (lo + hi) >> 1;
+            if (u >= bd[mid]) lo = mid + 1;
+            else hi = mid;
+        }
+        return lo == 0 ? 0 : pm[lo - 1];
+    };
+    r.c0 = (uint32_t)find(u0);
+    r.c1 = (uint32_t)find(u1);
+    r.r0 = r.r1 = r.rn = 0.0f;
+    if (kcb) {
+        r.r0 = u0 - kcb[r.c0];
+        r.r1 = u1 - kcb[r.c1];
+        r.rn = sqrt_rn(fmaxf(tree_sum128(r.r0 * r.r0, r.r1 * r.r1), 1e-20f));
+    }
+    return r;
+}
 
 constexpr int kWriteMaxWaves = 16;
 
@@ -147,60 +201,21 @@ __global__ void __launch_bounds__(64 * kWriteMaxWaves) tq_cache_write_kernel(
 
     long long pl = (start + t) % max_seq;
     if (pl < 0) pl += max_seq;
-    const float rscale = 1.0f / sqrtf((float)kD);
-    auto tree_sum = [&](float sq0, float sq1) {
-        float v = sq0 + sq1;
-        for (int sh = 32; sh > 0; sh >>= 1) v = v + __shfl_down(v, sh);
-        return __shfl(v, 0);
-    };
 
     for (int v = wave; v < nkv * count; v += W) {
         const int which = first + v / nkv, h = v % nkv;
-        const int nb = a.n_search[which];
         const size_t slot = ((size_t)b * nkv + h) * (size_t)max_seq + (size_t)pl;
         const __half *src = src_of(v);
         float f0 = __half2float(v == v0 ? pre0 : src[lane]);
         float f1 = __half2float(v == v0 ? pre1 : src[lane + 64]);
-        if (which == 0 && a.k_norm) {   // uniform: K through the QK-norm + RoPE first
-            const long rp = imh_qk::clamp_pos(start + t, a.rope_max_pos);
-            imh_qk::norm_rope_128(f0, f1, lane, a.k_norm, a.rope_cos + rp * (kD / 2), a.rope_sin + rp * (kD / 2),
-                                  a.eps);
-        }
-        float x0 = f0 * sg0;
-        float x1 = f1 * sg1;
-        x0 = hadamard64(x0, lane);
-        x1 = hadamard64(x1, lane);
-        {
-            const float lo = x0, hi = x1;   // stride 64: elements lane and lane + 64
-            x0 = lo + hi;
-            x1 = lo - hi;
-        }
-        const float xr0 = x0 * (sg0 * rscale), xr1 = x1 * (sg1 * rscale);
-        const float l2 = sqrt_rn(fmaxf(tree_sum(xr0 * xr0, xr1 * xr1), 1e-20f));
-        const float inv = __fdiv_rn(1.0f, fmaxf(l2, 1e-10f));
-        const float u0 = xr0 * inv, u1 = xr1 * inv;
-        const float *bd = bnd[which];
-        const int32_t *pm = bpm[which];
-        // 1 + the last j with u >= boundary[j] in the table's own order (0 if
-        // none): the boundaries that u passes are a prefix of the sorted ones,
-        // so the answer is the prefix max there (turboquant.metal:118-124)
-        auto find = [&](float u) {
-            int lo = 0, hi = nb;
-            while (lo < hi) {
-                const int mid = (lo + hi) >> 1;
-                if (u >= bd[mid]) lo = mid + 1;
-                else hi = mid;
-            }
-            return lo == 0 ? 0 : pm[lo - 1];
-        };
-        uint32_t code0 = (uint32_t)find(u0), code1 = (uint32_t)find(u1);
+        const TqCodes qc = tq_quantize_vec(f0, f1, lane, sg0, sg1, bnd[which], bpm[which], a.n_search[which],
+                                           which == 0 ? a.codebook[0] : nullptr);
+        uint32_t code0 = qc.c0, code1 = qc.c1;
+        const float l2 = qc.l2;
 
         if (which == 0) {
-            const float *cb = a.codebook[0];
-            const float r0 = u0 - cb[code0], r1 = u1 - cb[code1];
-            const float rn = sqrt_rn(fmaxf(tree_sum(r0 * r0, r1 * r1), 1e-20f));
-            res[wave][lane] = r0;
-            res[wave][lane + 64] = r1;
+            res[wave][lane] = qc.r0;
+            res[wave][lane + 64] = qc.r1;
             __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
             __builtin_amdgcn_wave_barrier();
             __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
@@ -213,7 +228,7 @@ __global__ void __launch_bounds__(64 * kWriteMaxWaves) tq_cache_write_kernel(
             }
             if (acc0 >= 0.0f) code0 |= 0x80u;
             if (acc1 >= 0.0f) code1 |= 0x80u;
-            if (lane == 0) a.r_norms[slot] = rn;
+            if (lane == 0) a.r_norms[slot] = qc.rn;
             __builtin_amdgcn_wave_barrier();   // res[wave] is rewritten by the next vector
         }
         a.codes[which][slot * kD + lane] = (uint8_t)code0;
@@ -254,7 +269,33 @@ struct QkRope {
     float eps;
 };
 
-template <int GQA>
+// Optional cache write of the step's token in the same launch (k_new == NULL:
+// attention only).  The grid then has one more workgroup per (kv head,
+// sequence), the last in x: it quantizes the token's K (after the QK-norm +
+// RoPE when k_norm is set, with qr's tables) and V as the cache write does,
+// stores the codes at row L - 1 (L = the sequence's length with the token),
+// and publishes that one position as its split's partial; the other splits
+// cover [0, L - 1).  Its work overlaps theirs, and the last-arriving combine
+// merges it like any split.
+struct TqFuse {
+    const __half *k_new, *v_new;   // [batch][nkv][kD]
+    uint8_t *kcodes, *vcodes;      // the cache, writable
+    float *kscales, *vscales, *krnorm;
+    const float *sorted[2];        // search tables of the cache write
+    const int32_t *prefmax[2];
+    int n_search[2];
+    const __half *k_norm;
+    const float *qjl_t;   // S^T again: a separate argument, so its addresses are
+                          // not shared with (and held live from) the prologue's
+};
+
+// f16 hi + lo pair of a codebook table entry as f32
+__device__ __forceinline__ float tab_f32(uint32_t e) {
+    return (float)__builtin_bit_cast(_Float16, (uint16_t)(e & 0xFFFFu)) +
+           (float)__builtin_bit_cast(_Float16, (uint16_t)(e >> 16));
+}
+
+template <int GQA, bool FUSED>
 __global__ void __launch_bounds__(64 * kWaves) __attribute__((amdgpu_waves_per_eu(3))) tq_attention_kernel(
     const __half *__restrict__ q, int nh, int nkv, int max_seq, int seq_len,
     const int32_t *__restrict__ seq_lens, float attn_scale, const float *__restrict__ signs,
@@ -263,8 +304,10 @@ __global__ void __launch_bounds__(64 * kWaves) __attribute__((amdgpu_waves_per_e
     const float *__restrict__ kscales, const float *__restrict__ vscales,
     const float *__restrict__ krnorm, int split_len, float *__restrict__ part_o,
     float *__restrict__ part_m, float *__restrict__ part_l, int *__restrict__ counters,
-    __half *__restrict__ out, const QkRope qr) {
+    __half *__restrict__ out, const QkRope qr, const TqFuse fz) {
     __shared__ float qs[GQA][2][kD];
+    __shared__ float wtab[2][256];     // token writer: sorted boundaries
+    __shared__ int32_t wpm[2][256];    // token writer: prefix maxima
     __shared__ uint32_t ktab[256];   // entry c & 0x7F, indexed by the whole code byte
     __shared__ uint32_t vtab[256];   // V entry c, same packing as ktab
     __shared__ _Float16 wbuf[kWaves][4][16];
@@ -281,10 +324,13 @@ __global__ void __launch_bounds__(64 * kWaves) __attribute__((amdgpu_waves_per_e
     const int wave = tid >> 6;
     const int split = blockIdx.x, kvh = blockIdx.y, b = blockIdx.z;
     const int S = gridDim.x;
+    const bool writer = FUSED && split == S - 1;   // the step's token (uniform per workgroup)
 
     // with seq_lens, seq_len is the bound every length is clamped to
     int L = seq_lens ? min(seq_lens[b], seq_len) : seq_len;
     L = L < 0 ? 0 : (L > max_seq ? max_seq : L);
+    const int L_tok = L;               // with the fused write: the token is row L_tok - 1
+    if (FUSED) L = L > 0 ? L - 1 : 0;
     const int p_begin = split * split_len;
     const int p_end = min(p_begin + split_len, L);
     const size_t head_base = ((size_t)b * nkv + kvh) * (size_t)max_seq;
@@ -418,122 +464,228 @@ __global__ void __launch_bounds__(64 * kWaves) __attribute__((amdgpu_waves_per_e
     }
     __syncthreads();
 
-    // score operands A, k-slot order within each 4-byte word: bytes {0, 2, 1, 3}.
-    // Rows 4h..4h+3 carry head h: aqk = {q_hi, q_lo, 0, 0} (against K hi),
-    // aqh = {q_hi, 0, 0, 0} (against K lo), aqs = {0, 0, s_hi, s_lo} (against
-    // the QJL signs), so one accumulator holds, in lane group h's four
-    // registers, q_hi.K + q_hi.K_lo, q_lo.K_hi, s_hi.sgn, s_lo.sgn.
-    const int am = lane & 15;
-    const int ah = am >> 2, ar = am & 3;
-    const bool arow = ah < GQA;
-    half8_t aqk[4], aqh[4], aqs[4];
-    constexpr int slot_byte[8] = {0, 2, 1, 3, 4, 6, 5, 7};
-#pragma unroll
-    for (int j = 0; j < 4; j++) {
-#pragma unroll
-        for (int i = 0; i < 8; i++) {
-            float vq = 0.0f, vs = 0.0f;
-            if (arow) {
-                const int d = kg * 32 + j * 8 + slot_byte[i];
-                vq = qs[ah][0][d];
-                vs = qs[ah][1][d];
-            }
-            const _Float16 qh = (_Float16)vq, sh = (_Float16)vs;
-            const _Float16 ql = (_Float16)(vq - (float)qh), sl = (_Float16)(vs - (float)sh);
-            const _Float16 z = (_Float16)0.0f;
-            aqk[j][i] = ar == 0 ? qh : (ar == 1 ? ql : z);
-            aqh[j][i] = ar == 0 ? qh : z;
-            aqs[j][i] = ar == 2 ? sh : (ar == 3 ? sl : z);
-        }
-    }
-
     const float qjl_factor = sqrtf(2.0f / 3.14159265f) / (float)kD;
-    float m_run = -INFINITY, l_run = 0.0f;   // of head kg (rows of one DPP row)
-    float4_t acc[8];
+    if constexpr (!FUSED) (void)fz;
+    if (FUSED && writer) {
+        // ---- the step's token: cache write and its one-position partial ----
+        // the lane id again, from mbcnt: values derived from `lane` in the
+        // prologue (shuffle addresses) would otherwise be shared with this
+        // path and held across the loop's registers
+        const int wl = (int)__builtin_amdgcn_mbcnt_hi(~0u, __builtin_amdgcn_mbcnt_lo(~0u, 0u));
+        const bool has = L_tok > 0;
+        const int row = L_tok - 1;
+        // thread (kr, dq)'s S^T block again (L2 hits; holding the prologue's
+        // copy across the branch would cost the loop registers)
+        float4 sw[16];
+        {
+            const float4 *s4 = reinterpret_cast<const float4 *>(fz.qjl_t) + (size_t)kr * 16 * (kD / 4) + dq;
 #pragma unroll
-    for (int j = 0; j < 8; j++) acc[j] = float4_t{0, 0, 0, 0};
-
-    auto process = [&](const ChunkIn &c, const int p0) __attribute__((always_inline)) {
-        // ---- scores S[h][n] for 16 positions via MFMA ----
-        const uint32_t kw[8] = {c.k0.x, c.k0.y, c.k0.z, c.k0.w, c.k1.x, c.k1.y, c.k1.z, c.k1.w};
-        float4_t d1 = {0, 0, 0, 0};
+            for (int i = 0; i < 16; i++) sw[i] = s4[(size_t)i * (kD / 4)];
+        }
+        for (int w = 0; w < 2; w++)
+            for (int j = tid; j < fz.n_search[w]; j += 64 * kWaves) {
+                wtab[w][j] = fz.sorted[w][j];
+                wpm[w][j] = fz.prefmax[w][j];
+            }
+        float f0 = 0.0f, f1 = 0.0f;
+        if (wave < 2 && has) {   // wave 0: K, wave 1: V
+            const __half *src = (wave == 0 ? fz.k_new : fz.v_new) + ((size_t)b * nkv + kvh) * kD;
+            f0 = __half2float(src[wl]);
+            f1 = __half2float(src[wl + 64]);
+            if (wave == 0 && fz.k_norm) {
+                const long rpk = imh_qk::clamp_pos(row, qr.max_pos);
+                imh_qk::norm_rope_128(f0, f1, wl, fz.k_norm, qr.cos + rpk * (kD / 2), qr.sin + rpk * (kD / 2),
+                                      qr.eps);
+            }
+        }
+        __syncthreads();   // search tables staged
+        TqCodes tc{};
+        if (wave < 2 && has) {
+            tc = tq_quantize_vec(f0, f1, wl, sg0, sg1, wtab[wave], wpm[wave], fz.n_search[wave],
+                                 wave == 0 ? kcb : nullptr);
+            if (wave == 0) {
+                tail_o[0][wl] = tc.r0;
+                tail_o[0][wl + 64] = tc.r1;
+            }
+        }
+        __syncthreads();
+        // QJL signs of the K residual: s[d] = sum_k S[d][k] r[k] as one fmaf
+        // chain per d in increasing k, the cache write's order (bit-exact sign
+        // bits).  Thread (kr, dq) holds S^T rows 16 kr .. 16 kr + 15 at columns
+        // 4 dq .. 4 dq + 3 in sw[]; row block kr continues the chains of block
+        // kr - 1 through LDS.
+        for (int blk = 0; blk < 8; blk++) {
+            if (kr == blk) {
+                float4 a4 = blk == 0 ? make_float4(0.0f, 0.0f, 0.0f, 0.0f)
+                                     : reinterpret_cast<const float4 *>(tail_o[1])[dq];
 #pragma unroll
+                for (int i = 0; i < 16; i++) {
+                    const float rk = tail_o[0][16 * blk + i];
+                    a4.x = __builtin_fmaf(sw[i].x, rk, a4.x);
+                    a4.y = __builtin_fmaf(sw[i].y, rk, a4.y);
+                    a4.z = __builtin_fmaf(sw[i].z, rk, a4.z);
+                    a4.w = __builtin_fmaf(sw[i].w, rk, a4.w);
+                }
+                reinterpret_cast<float4 *>(tail_o[1])[dq] = a4;
+            }
+            __syncthreads();
+        }
+        const size_t slot = head_base + (size_t)(has ? row : 0);
+        if (wave == 0 && has) {
+            const uint32_t c0 = tc.c0 | (tail_o[1][wl] >= 0.0f ? 0x80u : 0u);
+            const uint32_t c1 = tc.c1 | (tail_o[1][wl + 64] >= 0.0f ? 0x80u : 0u);
+            fz.kcodes[slot * kD + wl] = (uint8_t)c0;
+            fz.kcodes[slot * kD + wl + 64] = (uint8_t)c1;
+            if (wl == 0) {
+                fz.kscales[slot] = tc.l2;
+                fz.krnorm[slot] = tc.rn;
+            }
+            // each head's score against the dequantized K, the loop's terms
+            const float k0 = tab_f32(ktab[c0]), k1 = tab_f32(ktab[c1]);
+            const float g0 = (c0 & 0x80u) ? 1.0f : -1.0f, g1 = (c1 & 0x80u) ? 1.0f : -1.0f;
+            const float qw = tc.rn * qjl_factor * tc.l2;
+#pragma unroll
+            for (int hh = 0; hh < GQA; hh++) {
+                const float t1 = imh_qk::wave_sum64(__builtin_fmaf(qs[hh][0][wl + 64], k1, qs[hh][0][wl] * k0));
+                const float t2 = imh_qk::wave_sum64(__builtin_fmaf(qs[hh][1][wl + 64], g1, qs[hh][1][wl] * g0));
+                if (wl == 0) {
+                    mm[0][hh] = attn_scale * (t1 * tc.l2 + t2 * qw);
+                    ll[0][hh] = 1.0f;
+                }
+            }
+        } else if (wave == 1 && has) {
+            fz.vcodes[slot * kD + wl] = (uint8_t)tc.c0;
+            fz.vcodes[slot * kD + wl + 64] = (uint8_t)tc.c1;
+            if (wl == 0) fz.vscales[slot] = tc.l2;
+            // weight 1 at its own maximum: the partial output is the value
+            const float v0 = tab_f32(vtab[tc.c0]) * tc.l2, v1 = tab_f32(vtab[tc.c1]) * tc.l2;
+#pragma unroll
+            for (int hh = 0; hh < GQA; hh++) {
+                om[0][hh][wl] = v0;
+                om[0][hh][wl + 64] = v1;
+            }
+        }
+        if ((wave != 0 || !has) && wl < GQA) {
+            mm[wave][wl] = -INFINITY;
+            ll[wave][wl] = 0.0f;
+        }
+    } else {
+        // score operands A, k-slot order within each 4-byte word: bytes {0, 2, 1, 3}.
+        // Rows 4h..4h+3 carry head h: aqk = {q_hi, q_lo, 0, 0} (against K hi),
+        // aqh = {q_hi, 0, 0, 0} (against K lo), aqs = {0, 0, s_hi, s_lo} (against
+        // the QJL signs), so one accumulator holds, in lane group h's four
+        // registers, q_hi.K + q_hi.K_lo, q_lo.K_hi, s_hi.sgn, s_lo.sgn.
+        const int am = lane & 15;
+        const int ah = am >> 2, ar = am & 3;
+        const bool arow = ah < GQA;
+        half8_t aqk[4], aqh[4], aqs[4];
+        constexpr int slot_byte[8] = {0, 2, 1, 3, 4, 6, 5, 7};
+    #pragma unroll
         for (int j = 0; j < 4; j++) {
-            uint32_t bh[4], bl[4], bs[4];
-#pragma unroll
-            for (int hw = 0; hw < 2; hw++) {
-                const uint32_t w = kw[2 * j + hw];
-                const uint32_t t0 = ktab[w & 0xFF];
-                const uint32_t t1 = ktab[(w >> 8) & 0xFF];
-                const uint32_t t2 = ktab[(w >> 16) & 0xFF];
-                const uint32_t t3 = ktab[w >> 24];
-                bh[2 * hw] = __builtin_amdgcn_perm(t2, t0, 0x05040100u);
-                bl[2 * hw] = __builtin_amdgcn_perm(t2, t0, 0x07060302u);
-                bh[2 * hw + 1] = __builtin_amdgcn_perm(t3, t1, 0x05040100u);
-                bl[2 * hw + 1] = __builtin_amdgcn_perm(t3, t1, 0x07060302u);
-                // +1 (0x3C00) where bit 7 of the code is set, -1 (0xBC00) where not
-                bs[2 * hw] = ((w << 8) & 0x80008000u) ^ 0xBC00BC00u;
-                bs[2 * hw + 1] = (w & 0x80008000u) ^ 0xBC00BC00u;
+    #pragma unroll
+            for (int i = 0; i < 8; i++) {
+                float vq = 0.0f, vs = 0.0f;
+                if (arow) {
+                    const int d = kg * 32 + j * 8 + slot_byte[i];
+                    vq = qs[ah][0][d];
+                    vs = qs[ah][1][d];
+                }
+                const _Float16 qh = (_Float16)vq, sh = (_Float16)vs;
+                const _Float16 ql = (_Float16)(vq - (float)qh), sl = (_Float16)(vs - (float)sh);
+                const _Float16 z = (_Float16)0.0f;
+                aqk[j][i] = ar == 0 ? qh : (ar == 1 ? ql : z);
+                aqh[j][i] = ar == 0 ? qh : z;
+                aqs[j][i] = ar == 2 ? sh : (ar == 3 ? sl : z);
             }
-            const half8_t Bh = __builtin_bit_cast(half8_t, make_uint4(bh[0], bh[1], bh[2], bh[3]));
-            const half8_t Bl = __builtin_bit_cast(half8_t, make_uint4(bl[0], bl[1], bl[2], bl[3]));
-            const half8_t Bs = __builtin_bit_cast(half8_t, make_uint4(bs[0], bs[1], bs[2], bs[3]));
-            d1 = __builtin_amdgcn_mfma_f32_16x16x32_f16(aqk[j], Bh, d1, 0, 0, 0);
-            d1 = __builtin_amdgcn_mfma_f32_16x16x32_f16(aqh[j], Bl, d1, 0, 0, 0);
-            d1 = __builtin_amdgcn_mfma_f32_16x16x32_f16(aqs[j], Bs, d1, 0, 0, 0);
         }
-        // lane (n, g): d1[0..3] = the four partial products of head g at position p0 + n
-        const bool valid = (p0 + n_l) < p_end;
-        const float qw = c.krn * qjl_factor * c.ksc;
-        const float sc = valid ? attn_scale * ((d1[0] + d1[1]) * c.ksc + (d1[2] + d1[3]) * qw) : -INFINITY;
-        const float cm = imh_dpp::row16_max(sc);
-        const float nm = fmaxf(m_run, cm);
-        const bool live = nm != -INFINITY;   // a head with no position yet keeps weight 0
-        const float corr = live ? __expf(m_run - nm) : 1.0f;
-        const float w = live ? __expf(sc - nm) : 0.0f;
-        l_run = l_run * corr + imh_dpp::row16_sum(w);
-        m_run = nm;
-        if (__builtin_amdgcn_ballot_w64(corr != 1.0f)) {   // some head's max grew
-#pragma unroll
-            for (int j = 0; j < 8; j++) acc[j][0] *= corr;
-        }
-        // weights * v_scale as f16 hi + lo, transposed through LDS into operand A
-        wbuf[wave][kg][n_l] = (_Float16)(w * c.vsc);
-        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-        __builtin_amdgcn_wave_barrier();
-        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-        half4_t w4 = {0, 0, 0, 0};
-        if (arow && ar == 0) w4 = *reinterpret_cast<const half4_t *>(&wbuf[wave][ah][4 * kg]);
-        const half8_t wa = {w4[0], w4[0], w4[1], w4[1], w4[2], w4[2], w4[3], w4[3]};
-        // ---- o += W . V: operand B of block j = codebook values (hi, lo) of
-        // byte j of the four position rows ----
-#pragma unroll
-        for (int j = 0; j < 8; j++) {
-            uint32_t e[4];
-#pragma unroll
-            for (int i = 0; i < 4; i++) {
-                const uint32_t word = j < 4 ? c.v[i].x : c.v[i].y;
-                e[i] = vtab[(word >> (8 * (j & 3))) & 0xFF];
-            }
-            const half8_t bv = __builtin_bit_cast(half8_t, make_uint4(e[0], e[1], e[2], e[3]));
-            acc[j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(wa, bv, acc[j], 0, 0, 0);
-        }
-        __builtin_amdgcn_wave_barrier();   // wbuf is rewritten next chunk
-    };
-    for (int p0 = p_first; p0 < p_end; p0 += kChunk * kWaves) {
-        const ChunkIn c = cur;
-        load_chunk(p0 + kChunk * kWaves, cur);
-        process(c, p0);
-    }
 
-    // lane (c, g): acc[j][0] = o[head g][dim 8c + j]
-    if (kg < GQA) {
-        float4 *dst = reinterpret_cast<float4 *>(&om[wave][kg][n_l * 8]);
-        dst[0] = make_float4(acc[0][0], acc[1][0], acc[2][0], acc[3][0]);
-        dst[1] = make_float4(acc[4][0], acc[5][0], acc[6][0], acc[7][0]);
-        if (n_l == 0) {
-            mm[wave][kg] = m_run;
-            ll[wave][kg] = l_run;
+        float m_run = -INFINITY, l_run = 0.0f;   // of head kg (rows of one DPP row)
+        float4_t acc[8];
+    #pragma unroll
+        for (int j = 0; j < 8; j++) acc[j] = float4_t{0, 0, 0, 0};
+
+        auto process = [&](const ChunkIn &c, const int p0) __attribute__((always_inline)) {
+            // ---- scores S[h][n] for 16 positions via MFMA ----
+            const uint32_t kw[8] = {c.k0.x, c.k0.y, c.k0.z, c.k0.w, c.k1.x, c.k1.y, c.k1.z, c.k1.w};
+            float4_t d1 = {0, 0, 0, 0};
+    #pragma unroll
+            for (int j = 0; j < 4; j++) {
+                uint32_t bh[4], bl[4], bs[4];
+    #pragma unroll
+                for (int hw = 0; hw < 2; hw++) {
+                    const uint32_t w = kw[2 * j + hw];
+                    const uint32_t t0 = ktab[w & 0xFF];
+                    const uint32_t t1 = ktab[(w >> 8) & 0xFF];
+                    const uint32_t t2 = ktab[(w >> 16) & 0xFF];
+                    const uint32_t t3 = ktab[w >> 24];
+                    bh[2 * hw] = __builtin_amdgcn_perm(t2, t0, 0x05040100u);
+                    bl[2 * hw] = __builtin_amdgcn_perm(t2, t0, 0x07060302u);
+                    bh[2 * hw + 1] = __builtin_amdgcn_perm(t3, t1, 0x05040100u);
+                    bl[2 * hw + 1] = __builtin_amdgcn_perm(t3, t1, 0x07060302u);
+                    // +1 (0x3C00) where bit 7 of the code is set, -1 (0xBC00) where not
+                    bs[2 * hw] = ((w << 8) & 0x80008000u) ^ 0xBC00BC00u;
+                    bs[2 * hw + 1] = (w & 0x80008000u) ^ 0xBC00BC00u;
+                }
+                const half8_t Bh = __builtin_bit_cast(half8_t, make_uint4(bh[0], bh[1], bh[2], bh[3]));
+                const half8_t Bl = __builtin_bit_cast(half8_t, make_uint4(bl[0], bl[1], bl[2], bl[3]));
+                const half8_t Bs = __builtin_bit_cast(half8_t, make_uint4(bs[0], bs[1], bs[2], bs[3]));
+                d1 = __builtin_amdgcn_mfma_f32_16x16x32_f16(aqk[j], Bh, d1, 0, 0, 0);
+                d1 = __builtin_amdgcn_mfma_f32_16x16x32_f16(aqh[j], Bl, d1, 0, 0, 0);
+                d1 = __builtin_amdgcn_mfma_f32_16x16x32_f16(aqs[j], Bs, d1, 0, 0, 0);
+            }
+            // lane (n, g): d1[0..3] = the four partial products of head g at position p0 + n
+            const bool valid = (p0 + n_l) < p_end;
+            const float qw = c.krn * qjl_factor * c.ksc;
+            const float sc = valid ? attn_scale * ((d1[0] + d1[1]) * c.ksc + (d1[2] + d1[3]) * qw) : -INFINITY;
+            const float cm = imh_dpp::row16_max(sc);
+            const float nm = fmaxf(m_run, cm);
+            const bool live = nm != -INFINITY;   // a head with no position yet keeps weight 0
+            const float corr = live ? __expf(m_run - nm) : 1.0f;
+            const float w = live ? __expf(sc - nm) : 0.0f;
+            l_run = l_run * corr + imh_dpp::row16_sum(w);
+            m_run = nm;
+            if (__builtin_amdgcn_ballot_w64(corr != 1.0f)) {   // some head's max grew
+    #pragma unroll
+                for (int j = 0; j < 8; j++) acc[j][0] *= corr;
+            }
+            // weights * v_scale as f16 hi + lo, transposed through LDS into operand A
+            wbuf[wave][kg][n_l] = (_Float16)(w * c.vsc);
+            __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+            __builtin_amdgcn_wave_barrier();
+            __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+            half4_t w4 = {0, 0, 0, 0};
+            if (arow && ar == 0) w4 = *reinterpret_cast<const half4_t *>(&wbuf[wave][ah][4 * kg]);
+            const half8_t wa = {w4[0], w4[0], w4[1], w4[1], w4[2], w4[2], w4[3], w4[3]};
+            // ---- o += W . V: operand B of block j = codebook values (hi, lo) of
+            // byte j of the four position rows ----
+    #pragma unroll
+            for (int j = 0; j < 8; j++) {
+                uint32_t e[4];
+    #pragma unroll
+                for (int i = 0; i < 4; i++) {
+                    const uint32_t word = j < 4 ? c.v[i].x : c.v[i].y;
+                    e[i] = vtab[(word >> (8 * (j & 3))) & 0xFF];
+                }
+                const half8_t bv = __builtin_bit_cast(half8_t, make_uint4(e[0], e[1], e[2], e[3]));
+                acc[j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(wa, bv, acc[j], 0, 0, 0);
+            }
+            __builtin_amdgcn_wave_barrier();   // wbuf is rewritten next chunk
+        };
+        for (int p0 = p_first; p0 < p_end; p0 += kChunk * kWaves) {
+            const ChunkIn c = cur;
+            load_chunk(p0 + kChunk * kWaves, cur);
+            process(c, p0);
+        }
+
+        // lane (c, g): acc[j][0] = o[head g][dim 8c + j]
+        if (kg < GQA) {
+            float4 *dst = reinterpret_cast<float4 *>(&om[wave][kg][n_l * 8]);
+            dst[0] = make_float4(acc[0][0], acc[1][0], acc[2][0], acc[3][0]);
+            dst[1] = make_float4(acc[4][0], acc[5][0], acc[6][0], acc[7][0]);
+            if (n_l == 0) {
+                mm[wave][kg] = m_run;
+                ll[wave][kg] = l_run;
+            }
         }
     }
     __syncthreads();
@@ -658,14 +810,17 @@ __global__ void __launch_bounds__(64 * kWaves) __attribute__((amdgpu_waves_per_e
     }
     __syncthreads();
     // rotate back: o = D.H.D/sqrt(d) o_rot, wave hh on head hh in registers
+    // (lane id from mbcnt, so the prologue's shuffle addresses are not held
+    // to here across the loop)
     if (wave < GQA) {
-        const float sg0 = signs[lane], sg1 = signs[lane + 64];
-        float x0 = qs[wave][0][lane], x1 = qs[wave][0][lane + 64];
-        x0 = hadamard64(x0, lane);
-        x1 = hadamard64(x1, lane);
+        const int ol = (int)__builtin_amdgcn_mbcnt_hi(~0u, __builtin_amdgcn_mbcnt_lo(~0u, 0u));
+        const float sg0 = signs[ol], sg1 = signs[ol + 64];
+        float x0 = qs[wave][0][ol], x1 = qs[wave][0][ol + 64];
+        x0 = hadamard64(x0, ol);
+        x1 = hadamard64(x1, ol);
         __half *o = out + ((size_t)b * nh + kvh * GQA + wave) * kD;
-        o[lane] = __float2half((x0 + x1) * (sg0 * rscale));
-        o[lane + 64] = __float2half((x0 - x1) * (sg1 * rscale));
+        o[ol] = __float2half((x0 + x1) * (sg0 * rscale));
+        o[ol + 64] = __float2half((x0 - x1) * (sg1 * rscale));
     }
 }
 
@@ -690,8 +845,7 @@ extern "C" {
 
 static int launch_cache_write(imh_stream *stream, const imh_tq_tables *t, const imh_tq_kv_cache *cache,
                               const uint16_t *k_proj, const uint16_t *v_proj, uint32_t token_count,
-                              uint32_t base_pos, const int32_t *positions, const char *who,
-                              const imh_qk_norm_rope_params *qk = nullptr) {
+                              uint32_t base_pos, const int32_t *positions, const char *who) {
     int rc = check_cache(t, cache, who);
     if (rc) return rc;
     if (token_count == 0) return IMH_OK;
@@ -707,13 +861,6 @@ static int launch_cache_write(imh_stream *stream, const imh_tq_tables *t, const 
     a.r_norms = cache->k_r_norms;
     a.codebook[0] = t->k_codebook;
     a.codebook[1] = t->v_codebook;
-    if (qk) {   // K through the QK-norm + RoPE first
-        a.k_norm = reinterpret_cast<const __half *>(qk->k_norm);
-        a.rope_cos = reinterpret_cast<const __half *>(qk->cos_cache);
-        a.rope_sin = reinterpret_cast<const __half *>(qk->sin_cache);
-        a.rope_max_pos = (int)qk->max_pos;
-        a.eps = qk->eps;
-    }
     a.sorted[0] = t->k_sorted;
     a.sorted[1] = t->v_sorted;
     a.prefmax[0] = t->k_prefmax;
@@ -754,8 +901,10 @@ int imh_encode_turboquant_cache_write_kv(imh_stream *stream, const imh_tq_tables
 static int run_attention(imh_stream *stream, const imh_tq_tables *t, const imh_tq_kv_cache *cache,
                          const uint16_t *q, uint32_t num_heads, uint32_t seq_len, const int32_t *seq_lens,
                          float attn_scale, uint16_t *out, uint32_t num_splits, const char *who,
-                         const imh_qk_norm_rope_params *qk) {
+                         const imh_qk_norm_rope_params *qk, const uint16_t *k_new = nullptr,
+                         const uint16_t *v_new = nullptr) {
     if (!stream || !q || !out) return imh::fail(IMH_EINVAL, std::string(who) + ": NULL argument");
+    const bool fused = k_new != nullptr;   // the token's cache write in the same launch
     int rc = check_cache(t, cache, who);
     if (rc) return rc;
     const uint32_t nkv = cache->num_kv_heads;
@@ -784,11 +933,12 @@ static int run_attention(imh_stream *stream, const imh_tq_tables *t, const imh_t
         want = std::min<uint32_t>((512 + groups - 1) / groups, std::max<uint32_t>(1, L / kAutoSplitLen));
     }
     const uint32_t max_splits = std::max<uint32_t>(1, (L + kSplitQuantum - 1) / kSplitQuantum);
-    want = std::max<uint32_t>(1, std::min(want, std::min<uint32_t>(max_splits, kMaxSplits)));
+    want = std::max<uint32_t>(1, std::min(want, std::min<uint32_t>(max_splits, kMaxSplits - (fused ? 1 : 0))));
     uint32_t split_len = (L + want - 1) / want;
     split_len = std::max<uint32_t>(kSplitQuantum,
                                    (split_len + kSplitQuantum - 1) / kSplitQuantum * kSplitQuantum);
-    const uint32_t S = std::max<uint32_t>(1, (L + split_len - 1) / split_len);   // <= kMaxSplits
+    // <= kMaxSplits, with the token writer's split
+    const uint32_t S = std::max<uint32_t>(1, (L + split_len - 1) / split_len) + (fused ? 1 : 0);
 
     // scratch: split partials and the groups' arrival counters (none for one split)
     const size_t nparts = (size_t)B * num_heads * S;
@@ -807,12 +957,12 @@ static int run_attention(imh_stream *stream, const imh_tq_tables *t, const imh_t
     }
     const __half *qh = reinterpret_cast<const __half *>(q);
     dim3 grid(S, nkv, B);
-#define IMH_TQ_LAUNCH(G)                                                                                     \
-    hipLaunchKernelGGL(tq_attention_kernel<G>, grid, dim3(64 * kWaves), 0, stream->stream, qh, (int)num_heads, \
+#define IMH_TQ_LAUNCH(G, F)                                                                                  \
+    hipLaunchKernelGGL((tq_attention_kernel<G, F>), grid, dim3(64 * kWaves), 0, stream->stream, qh, (int)num_heads, \
                        (int)nkv, (int)cache->max_seq_len, (int)L, seq_lens, attn_scale, t->signs, t->qjl_t,     \
                        t->k_codebook, t->v_codebook, cache->k_codes, cache->v_codes, cache->k_scales,           \
                        cache->v_scales, cache->k_r_norms, (int)split_len, po, pm, pl, ctr,                      \
-                       reinterpret_cast<__half *>(out), qr)
+                       reinterpret_cast<__half *>(out), qr, fz)
     // without the QK-norm the kernel still reads (and discards) one position
     // and 64 table entries: point them at the codebook
     QkRope qr{nullptr, reinterpret_cast<const __half *>(t->v_codebook),
@@ -826,9 +976,33 @@ static int run_attention(imh_stream *stream, const imh_tq_tables *t, const imh_t
         qr.max_pos = (int)qk->max_pos;
         qr.eps = qk->eps;
     }
-    if (gqa == 4) IMH_TQ_LAUNCH(4);
-    else if (gqa == 2) IMH_TQ_LAUNCH(2);
-    else IMH_TQ_LAUNCH(1);
+    TqFuse fz{};
+    if (fused) {
+        fz.k_new = reinterpret_cast<const __half *>(k_new);
+        fz.v_new = reinterpret_cast<const __half *>(v_new);
+        fz.kcodes = cache->k_codes;
+        fz.vcodes = cache->v_codes;
+        fz.kscales = cache->k_scales;
+        fz.vscales = cache->v_scales;
+        fz.krnorm = cache->k_r_norms;
+        fz.sorted[0] = t->k_sorted;
+        fz.sorted[1] = t->v_sorted;
+        fz.prefmax[0] = t->k_prefmax;
+        fz.prefmax[1] = t->v_prefmax;
+        fz.n_search[0] = t->k_search;
+        fz.n_search[1] = t->v_search;
+        fz.k_norm = qk ? reinterpret_cast<const __half *>(qk->k_norm) : nullptr;
+        fz.qjl_t = t->qjl_t;
+    }
+    if (fused) {   // the writer workgroups only in this instantiation
+        if (gqa == 4) IMH_TQ_LAUNCH(4, true);
+        else if (gqa == 2) IMH_TQ_LAUNCH(2, true);
+        else IMH_TQ_LAUNCH(1, true);
+    } else {
+        if (gqa == 4) IMH_TQ_LAUNCH(4, false);
+        else if (gqa == 2) IMH_TQ_LAUNCH(2, false);
+        else IMH_TQ_LAUNCH(1, false);
+    }
 #undef IMH_TQ_LAUNCH
     IMH_HIP(hipGetLastError());
     return IMH_OK;
@@ -852,10 +1026,12 @@ int imh_encode_kv_cache_and_attention(imh_stream *stream, const imh_tq_tables *t
     if ((uint64_t)seq_pos + 1 > cache->max_seq_len)
         return imh::fail(IMH_ERANGE, std::string(who) + ": position " + std::to_string(seq_pos) +
                                          " is beyond max_seq_len " + std::to_string(cache->max_seq_len));
-    rc = imh_encode_turboquant_cache_write_kv(stream, t, cache, k_proj, v_proj, 1, seq_pos, nullptr);
-    if (rc) return rc;
-    return imh_encode_turboquant_attention(stream, t, cache, q, num_heads, seq_pos + 1, nullptr, attn_scale,
-                                           out, 0);
+    if (!k_proj || !v_proj) return imh::fail(IMH_EINVAL, std::string(who) + ": NULL argument");
+    // one launch: the token's K / V are quantized and stored at row seq_pos by
+    // one extra workgroup per (kv head, sequence) while the others attend
+    // over [0, seq_pos); that workgroup's partial is the token's position
+    return run_attention(stream, t, cache, q, num_heads, seq_pos + 1, nullptr, attn_scale, out, 0, who, nullptr,
+                         k_proj, v_proj);
 }
 
 }  // extern "C"
@@ -873,24 +1049,17 @@ static int check_qk(const imh_qk_norm_rope_params *qk, const char *who) {
     return IMH_OK;
 }
 
-int encode_tq_write_kv_rope(imh_stream *stream, const imh_tq_tables *t, const imh_tq_kv_cache *cache,
-                            const uint16_t *k_proj, const uint16_t *v_proj, uint32_t token_count,
-                            const int32_t *positions, const imh_qk_norm_rope_params *qk) {
-    const char *who = "encode_tq_write_kv_rope";
-    if (!stream || !k_proj || !v_proj || !positions) return fail(IMH_EINVAL, std::string(who) + ": NULL argument");
-    int rc = check_qk(qk, who);
-    if (rc) return rc;
-    return launch_cache_write(stream, t, cache, k_proj, v_proj, token_count, 0, positions, who, qk);
-}
-
-int encode_tq_attention_rope(imh_stream *stream, const imh_tq_tables *t, const imh_tq_kv_cache *cache,
-                             const uint16_t *q, uint32_t num_heads, uint32_t seq_len, const int32_t *seq_lens,
-                             float attn_scale, uint16_t *out, uint32_t num_splits,
-                             const imh_qk_norm_rope_params *qk) {
-    const char *who = "encode_tq_attention_rope";
-    int rc = check_qk(qk, who);
-    if (rc) return rc;
-    return run_attention(stream, t, cache, q, num_heads, seq_len, seq_lens, attn_scale, out, num_splits, who, qk);
+int encode_tq_write_attend(imh_stream *stream, const imh_tq_tables *t, const imh_tq_kv_cache *cache,
+                           const uint16_t *q, const uint16_t *k_proj, const uint16_t *v_proj, uint32_t num_heads,
+                           const int32_t *seq_lens, float attn_scale, uint16_t *out,
+                           const imh_qk_norm_rope_params *qk) {
+    const char *who = "encode_tq_write_attend";
+    if (!k_proj || !v_proj || !seq_lens) return fail(IMH_EINVAL, std::string(who) + ": NULL argument");
+    if (qk) {
+        int rc = check_qk(qk, who);
+        if (rc) return rc;
+    }
+    return run_attention(stream, t, cache, q, num_heads, 0, seq_lens, attn_scale, out, 0, who, qk, k_proj, v_proj);
 }
 
 }  // namespace imh

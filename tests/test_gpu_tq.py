@@ -209,9 +209,22 @@ def test_attention_long_context_plain_normal(dev, stream, tq, tables):
     assert_close(got, ref, rel=5e-4, what="plain N(0,1) K/V, 30000 positions")
 
 
-def test_decode_step_write_then_attend(dev, stream, tq, tables):
-    batch, nkv, nh, max_seq, pos = 2, 8, 32, 256, 150
-    cache = fill_cache(dev, stream, tq, batch, nkv, max_seq, pos, seed=21)
+@pytest.mark.parametrize("batch,nh,pos,max_seq", [(2, 32, 150, 256), (1, 8, 0, 64), (3, 16, 4095, 8192),
+                                                  (1, 32, 8191, 8192)])
+def test_decode_step_write_then_attend(dev, stream, tq, tables, batch, nh, pos, max_seq):
+    """encode_kv_cache_and_attention: the token's K / V are written in the attention launch
+    (one extra workgroup per kv head and sequence) -- codes, scales and residual norms at row
+    pos bit-exact with the oracle's write, every other row untouched, and the output equal to
+    the oracle's attention over [0, pos] of the written cache.  Covers the first position (no
+    other split has work), many splits, GQA 1 / 2 / 4 and the cache's last row."""
+    nkv = 8
+    if pos:
+        cache = fill_cache(dev, stream, tq, batch, nkv, max_seq, pos, seed=21 + pos)
+    else:
+        cache = ops.TurboQuantKvCache(dev, batch, nkv, D, max_seq)
+        cache.zero(stream)
+        stream.sync()
+    before = read_cache(cache)
     k1, v1 = kv_data(batch, 1, nkv, 22), kv_data(batch, 1, nkv, 23)
     q16 = np.random.default_rng(24).standard_normal((batch, nh, D)).astype(np.float16)
     out = dev.empty((batch, nh, D), np.float16)
@@ -220,9 +233,17 @@ def test_decode_step_write_then_attend(dev, stream, tq, tables):
     stream.sync()
     kc, vc, ks, vs, kr = read_cache(cache)
     kc1, ks1, kr1 = O.tq_cache_write(k1, tables, True, 1)
-    assert np.array_equal(kc[:, :, pos], kc1[:, :, 0]) and np.array_equal(ks[:, :, pos], ks1[:, :, 0])
+    vc1, vs1, _ = O.tq_cache_write(v1, tables, False, 1)
+    assert np.array_equal(kc[:, :, pos], kc1[:, :, 0]) and np.array_equal(vc[:, :, pos], vc1[:, :, 0])
+    for got, ref in ((ks, ks1), (kr, kr1), (vs, vs1)):
+        assert np.array_equal(got[:, :, pos].view(np.uint32), ref[:, :, 0].view(np.uint32))
+    other = np.arange(max_seq) != pos
+    for got, old in zip((kc, vc, ks, vs, kr), before):
+        assert np.array_equal(got[:, :, other], old[:, :, other])
     ref = O.tq_attention(q16, tables, kc, vc, ks, vs, kr, pos + 1, 1.0 / math.sqrt(D), nthreads=8)
-    assert_close(out.read(), ref, what="decode step")
+    # the token's position is combined in f32 (no f16 weight), the rest as in the plain
+    # attention (~3e-4)
+    assert_close(out.read(), ref, rel=5e-4, what=f"decode step B={batch} nh={nh} pos={pos}")
 
 
 def test_attention_error_paths(dev, stream, tq):
