@@ -273,8 +273,9 @@ int imh_encode_turboquant_attention(imh_stream *stream, const imh_tq_tables *t,
                                     uint32_t num_splits);
 
 /* encode_kv_cache_and_attention (attention.rs:117-610), decode step (one token
- * per sequence): write K and V at position seq_pos, then attend over
- * [0, seq_pos + 1). */
+ * per sequence): write K and V at position seq_pos and attend over
+ * [0, seq_pos + 1), in one launch (the codes written equal
+ * imh_encode_turboquant_cache_write_kv's bit for bit). */
 int imh_encode_kv_cache_and_attention(imh_stream *stream, const imh_tq_tables *t,
                                       const imh_tq_kv_cache *cache, const uint16_t *k_proj,
                                       const uint16_t *v_proj, const uint16_t *q,
