@@ -322,8 +322,20 @@ __global__ void __launch_bounds__(64 * kWaves) __attribute__((amdgpu_waves_per_e
     const int tid = threadIdx.x;
     const int lane = tid & 63;
     const int wave = tid >> 6;
-    const int split = blockIdx.x, kvh = blockIdx.y, b = blockIdx.z;
     const int S = gridDim.x;
+    // With the token writers (FUSED): the grid in dispatch order is every
+    // group's S - 1 splits first, then the groups' writers, so the streaming
+    // workgroups spread evenly over the CUs (two per CU at ~512) and the
+    // short-lived writers take spare slots.
+    int split = blockIdx.x, kvh = blockIdx.y, b = blockIdx.z;
+    if (FUSED) {
+        const int i = (blockIdx.z * gridDim.y + blockIdx.y) * S + blockIdx.x;
+        const int sa = S - 1, streaming = sa * (int)(gridDim.y * gridDim.z);
+        const int g = i < streaming ? i / sa : i - streaming;
+        split = i < streaming ? i - g * sa : sa;
+        kvh = g % (int)gridDim.y;
+        b = g / (int)gridDim.y;
+    }
     const bool writer = FUSED && split == S - 1;   // the step's token (uniform per workgroup)
 
     // with seq_lens, seq_len is the bound every length is clamped to
