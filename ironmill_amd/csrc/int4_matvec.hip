@@ -223,11 +223,14 @@ int plan_launch(imh_stream *s, int nmat, bool rn, int N, int K, int B, const cha
     const size_t red_bytes = (size_t)MT * waves * 64 * sizeof(float4_t);
     const size_t per_group = (size_t)2 * rows * kGS * sizeof(_Float16);
     const size_t pad = (size_t)2 * rows * 8 * sizeof(_Float16);
-    // raw when all of K fits one stage at two chunks per thread; else image
+    // RAW when the workgroup's share of building the operand is small: all of
+    // K in one stage at two chunks per thread, or (plain source, any number
+    // of stages) up to 96 row-groups -- ~12K elements, measured the break-even
+    // against the prep launch at batch 2-8 (K 2560-9728).  Else IMAGE.
     size_t fixed = 0;
     int SG = 0;
     for (int raw = 1; raw >= 0; raw--) {
-        p.raw = raw && MT == 1 && rows * G * 16 <= 2 * nthr;
+        p.raw = raw && MT == 1 && (rows * G * 16 <= 2 * nthr || (!rn && rows * G <= 96));
         if (raw && !p.raw) continue;
         // LDS: scales/zeros, group sums (+ RN sums and rms), then
         // max(activation planes, partial sums)
@@ -237,7 +240,9 @@ int plan_launch(imh_stream *s, int nmat, bool rn, int N, int K, int B, const cha
                                                    " too large for the LDS staging of this kernel");
         SG = (int)((kLdsBudget - fixed - pad) / per_group);
         SG = std::min(std::min(SG, parts * kMaxGroups), G);
-        if (!p.raw || SG == G) break;
+        // several RAW stages only under the row-group rule (RAW_RN needs the
+        // whole row in one stage)
+        if (!p.raw || SG == G || (!rn && rows * G <= 96)) break;
     }
     Launch &L = p.L;
     L.grid = dim3(tiles, btiles);

@@ -452,7 +452,7 @@ int4_matvec_kernel(MatPtrs mp, ActIn in, int Nall, int K, int B, int parts, int 
             const int r = c / cpr;
             chunk_store(r, c - r * cpr, gs0, ch[i], i * nthr + tid < total);
         }
-        if (!RAW) {
+        if (!RN) {
             for (int c = XC * nthr + tid; c < total; c += nthr) {  // chunks beyond XC per thread
                 const int r = c / cpr;
                 Chunk cx;
