@@ -272,6 +272,19 @@ int imh_encode_turboquant_attention(imh_stream *stream, const imh_tq_tables *t,
                                     const int32_t *seq_lens, float attn_scale, uint16_t *out,
                                     uint32_t num_splits);
 
+/* Causal attention of token_count query tokens per sequence (the prefill form
+ * of turboquant_attention, turboquant.metal:202-462 with token_idx = tgid.y,
+ * seq_len = base + token_idx + 1): q and out [batch][token_count][num_heads]
+ * [head_dim] f16; token t of sequence b attends to positions
+ * [0, L_b - token_count + t + 1) with L_b as in imh_encode_turboquant_attention
+ * (the length including the new tokens, whose K / V the cache already holds).
+ * batch x token_count <= 65535. */
+int imh_encode_turboquant_attention_tokens(imh_stream *stream, const imh_tq_tables *t,
+                                           const imh_tq_kv_cache *cache, const uint16_t *q,
+                                           uint32_t num_heads, uint32_t token_count, uint32_t seq_len,
+                                           const int32_t *seq_lens, float attn_scale, uint16_t *out,
+                                           uint32_t num_splits);
+
 /* encode_kv_cache_and_attention (attention.rs:117-610), decode step (one token
  * per sequence): write K and V at position seq_pos and attend over
  * [0, seq_pos + 1), in one launch (the codes written equal

@@ -297,7 +297,7 @@ __device__ __forceinline__ float tab_f32(uint32_t e) {
 
 template <int GQA, bool FUSED>
 __global__ void __launch_bounds__(64 * kWaves) __attribute__((amdgpu_waves_per_eu(3))) tq_attention_kernel(
-    const __half *__restrict__ q, int nh, int nkv, int max_seq, int seq_len,
+    const __half *__restrict__ q, int nh, int nkv, int max_seq, int seq_len, int T,
     const int32_t *__restrict__ seq_lens, float attn_scale, const float *__restrict__ signs,
     const float *__restrict__ qjl_t, const float *__restrict__ kcb, const float *__restrict__ vcb,
     const uint8_t *__restrict__ kcodes, const uint8_t *__restrict__ vcodes,
@@ -327,20 +327,25 @@ __global__ void __launch_bounds__(64 * kWaves) __attribute__((amdgpu_waves_per_e
     // group's S - 1 splits first, then the groups' writers, so the streaming
     // workgroups spread evenly over the CUs (two per CU at ~512) and the
     // short-lived writers take spare slots.
-    int split = blockIdx.x, kvh = blockIdx.y, b = blockIdx.z;
+    // z = b * T + t: query token t of sequence b (T tokens per sequence)
+    int split = blockIdx.x, kvh = blockIdx.y, z = blockIdx.z;
     if (FUSED) {
         const int i = (blockIdx.z * gridDim.y + blockIdx.y) * S + blockIdx.x;
         const int sa = S - 1, streaming = sa * (int)(gridDim.y * gridDim.z);
         const int g = i < streaming ? i / sa : i - streaming;
         split = i < streaming ? i - g * sa : sa;
         kvh = g % (int)gridDim.y;
-        b = g / (int)gridDim.y;
+        z = g / (int)gridDim.y;
     }
+    const int b = z / T, tq = z - b * T;
     const bool writer = FUSED && split == S - 1;   // the step's token (uniform per workgroup)
 
     // with seq_lens, seq_len is the bound every length is clamped to
     int L = seq_lens ? min(seq_lens[b], seq_len) : seq_len;
     L = L < 0 ? 0 : (L > max_seq ? max_seq : L);
+    // causal (turboquant.metal:268): token t of T sees positions < L - T + t + 1
+    L -= T - 1 - tq;
+    L = L < 0 ? 0 : L;
     const int L_tok = L;               // with the fused write: the token is row L_tok - 1
     if (FUSED) L = L > 0 ? L - 1 : 0;
     const int p_begin = split * split_len;
@@ -394,7 +399,7 @@ __global__ void __launch_bounds__(64 * kWaves) __attribute__((amdgpu_waves_per_e
     const float rscale = 1.0f / sqrtf((float)kD);
     const int kr = tid >> 5, dq = tid & 31;
     const int qhead = kvh * GQA + (wave < GQA ? wave : 0);
-    const __half *qh = q + ((size_t)b * nh + qhead) * kD;
+    const __half *qh = q + ((size_t)z * nh + qhead) * kD;
     const __half q0 = qh[lane], q1 = qh[lane + 64];
     const float sg0 = signs[lane], sg1 = signs[lane + 64];
     // QK-norm + RoPE operands, loaded unconditionally (a branch here would
@@ -721,7 +726,7 @@ __global__ void __launch_bounds__(64 * kWaves) __attribute__((amdgpu_waves_per_e
         } else {
             // agent-scope stores write through to memory, so the workgroup that
             // combines the splits sees them from any XCD without flushing L2
-            const size_t pidx = ((size_t)b * nh + kvh * GQA + hh) * S + split;
+            const size_t pidx = ((size_t)z * nh + kvh * GQA + hh) * S + split;
             __hip_atomic_store(&part_o[pidx * kD + d], ov, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
             if (d == 0) {
                 __hip_atomic_store(&part_m[pidx], M, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
@@ -737,7 +742,7 @@ __global__ void __launch_bounds__(64 * kWaves) __attribute__((amdgpu_waves_per_e
         __builtin_amdgcn_s_waitcnt(0);
         __syncthreads();
         if (tid == 0)
-            is_last = __hip_atomic_fetch_add(&counters[b * nkv + kvh], 1, __ATOMIC_RELAXED,
+            is_last = __hip_atomic_fetch_add(&counters[z * nkv + kvh], 1, __ATOMIC_RELAXED,
                                              __HIP_MEMORY_SCOPE_AGENT) == S - 1;
         __syncthreads();
         if (!is_last) return;
@@ -746,7 +751,7 @@ __global__ void __launch_bounds__(64 * kWaves) __attribute__((amdgpu_waves_per_e
         // of its split subset: 256 threads = GQA heads x 32 dim quads x 8 / GQA
         // subsets) and, per head (one wave), the split maxima and sums
         __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
-        const size_t gbase = ((size_t)b * nh + kvh * GQA) * S;   // head hh at gbase + hh * S
+        const size_t gbase = ((size_t)z * nh + kvh * GQA) * S;   // head hh at gbase + hh * S
         constexpr int kParts = 8 / GQA;
         constexpr int kBatch = 16;
         const int quad = tid & 31, hh = (tid >> 5) % GQA, part = (tid >> 5) / GQA;
@@ -818,7 +823,7 @@ __global__ void __launch_bounds__(64 * kWaves) __attribute__((amdgpu_waves_per_e
             for (int pp = 0; pp < kParts; pp++) ov += tail_o[pp * GQA + h2][d];
             qs[h2][0][d] = (ov / fmaxf(tail_l[h2], 1e-10f)) * signs[d];
         }
-        if (tid == 0) __hip_atomic_store(&counters[b * nkv + kvh], 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        if (tid == 0) __hip_atomic_store(&counters[z * nkv + kvh], 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
     __syncthreads();
     // rotate back: o = D.H.D/sqrt(d) o_rot, wave hh on head hh in registers
@@ -830,7 +835,7 @@ __global__ void __launch_bounds__(64 * kWaves) __attribute__((amdgpu_waves_per_e
         float x0 = qs[wave][0][ol], x1 = qs[wave][0][ol + 64];
         x0 = hadamard64(x0, ol);
         x1 = hadamard64(x1, ol);
-        __half *o = out + ((size_t)b * nh + kvh * GQA + wave) * kD;
+        __half *o = out + ((size_t)z * nh + kvh * GQA + wave) * kD;
         o[ol] = __float2half((x0 + x1) * (sg0 * rscale));
         o[ol + 64] = __float2half((x0 - x1) * (sg1 * rscale));
     }
@@ -914,7 +919,7 @@ static int run_attention(imh_stream *stream, const imh_tq_tables *t, const imh_t
                          const uint16_t *q, uint32_t num_heads, uint32_t seq_len, const int32_t *seq_lens,
                          float attn_scale, uint16_t *out, uint32_t num_splits, const char *who,
                          const imh_qk_norm_rope_params *qk, const uint16_t *k_new = nullptr,
-                         const uint16_t *v_new = nullptr) {
+                         const uint16_t *v_new = nullptr, uint32_t token_count = 1) {
     if (!stream || !q || !out) return imh::fail(IMH_EINVAL, std::string(who) + ": NULL argument");
     const bool fused = k_new != nullptr;   // the token's cache write in the same launch
     int rc = check_cache(t, cache, who);
@@ -938,7 +943,12 @@ static int run_attention(imh_stream *stream, const imh_tq_tables *t, const imh_t
     // may go down to 64 positions per split.  With per-sequence lengths the
     // splits span the bound (0 = max_seq_len).
     const uint32_t L = seq_lens && seq_len == 0 ? cache->max_seq_len : seq_len;
-    const uint32_t B = cache->batch;
+    if (token_count == 0 || (token_count > 1 && (fused || qk)))
+        return imh::fail(IMH_EINVAL, std::string(who) + ": token_count must be 1 with the cache write or "
+                                                         "QK-norm, and at least 1");
+    // query rows: token t of sequence b is row b * token_count + t
+    const uint32_t B = cache->batch * token_count;
+    if (B > 65535) return imh::fail(IMH_EINVAL, std::string(who) + ": batch x token_count above 65535");
     uint32_t want = num_splits;
     if (want == 0) {
         const uint32_t groups = B * nkv;
@@ -971,7 +981,8 @@ static int run_attention(imh_stream *stream, const imh_tq_tables *t, const imh_t
     dim3 grid(S, nkv, B);
 #define IMH_TQ_LAUNCH(G, F)                                                                                  \
     hipLaunchKernelGGL((tq_attention_kernel<G, F>), grid, dim3(64 * kWaves), 0, stream->stream, qh, (int)num_heads, \
-                       (int)nkv, (int)cache->max_seq_len, (int)L, seq_lens, attn_scale, t->signs, t->qjl_t,     \
+                       (int)nkv, (int)cache->max_seq_len, (int)L, (int)token_count, seq_lens, attn_scale,       \
+                       t->signs, t->qjl_t,                                                                      \
                        t->k_codebook, t->v_codebook, cache->k_codes, cache->v_codes, cache->k_scales,           \
                        cache->v_scales, cache->k_r_norms, (int)split_len, po, pm, pl, ctr,                      \
                        reinterpret_cast<__half *>(out), qr, fz)
@@ -1026,6 +1037,14 @@ int imh_encode_turboquant_attention(imh_stream *stream, const imh_tq_tables *t,
                                     float attn_scale, uint16_t *out, uint32_t num_splits) {
     return run_attention(stream, t, cache, q, num_heads, seq_len, seq_lens, attn_scale, out, num_splits,
                          "imh_encode_turboquant_attention", nullptr);
+}
+
+int imh_encode_turboquant_attention_tokens(imh_stream *stream, const imh_tq_tables *t,
+                                           const imh_tq_kv_cache *cache, const uint16_t *q, uint32_t num_heads,
+                                           uint32_t token_count, uint32_t seq_len, const int32_t *seq_lens,
+                                           float attn_scale, uint16_t *out, uint32_t num_splits) {
+    return run_attention(stream, t, cache, q, num_heads, seq_len, seq_lens, attn_scale, out, num_splits,
+                         "imh_encode_turboquant_attention_tokens", nullptr, nullptr, nullptr, token_count);
 }
 
 int imh_encode_kv_cache_and_attention(imh_stream *stream, const imh_tq_tables *t,

@@ -187,10 +187,17 @@ def encode_turboquant_cache_write_kv(stream: Stream, tq: TurboQuantModel, cache:
 
 def encode_turboquant_attention(stream: Stream, tq: TurboQuantModel, cache: TurboQuantKvCache, q,
                                 num_heads: int, seq_len: int, out, attn_scale: float | None = None,
-                                seq_lens=None, num_splits: int = 0):
-    """turboquant_attention + fused_sdpa_reduce (attention.rs:394-489)."""
+                                seq_lens=None, num_splits: int = 0, token_count: int = 1):
+    """turboquant_attention + fused_sdpa_reduce (attention.rs:394-489).  token_count > 1:
+    q / out [batch][token_count][heads][d], token t attends causally to positions
+    < seq_len - token_count + t + 1 (turboquant.metal:268, token_idx = tgid.y)."""
     if attn_scale is None:
         attn_scale = 1.0 / math.sqrt(cache.head_dim)  # mil-rs/src/weights.rs:210-217
+    if token_count != 1:
+        check(lib.imh_encode_turboquant_attention_tokens(stream.handle, tq.handle, C.byref(cache.c), _ptr(q),
+                                                         num_heads, token_count, seq_len, _ptr(seq_lens),
+                                                         attn_scale, _ptr(out), num_splits))
+        return
     check(lib.imh_encode_turboquant_attention(stream.handle, tq.handle, C.byref(cache.c), _ptr(q),
                                               num_heads, seq_len, _ptr(seq_lens), attn_scale,
                                               _ptr(out), num_splits))

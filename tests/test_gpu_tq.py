@@ -246,6 +246,32 @@ def test_decode_step_write_then_attend(dev, stream, tq, tables, batch, nh, pos, 
     assert_close(out.read(), ref, rel=5e-4, what=f"decode step B={batch} nh={nh} pos={pos}")
 
 
+@pytest.mark.parametrize("nh,tokens,ragged", [(32, 5, False), (16, 3, True), (8, 7, False)])
+def test_attention_multi_token_causal(dev, stream, tq, tables, nh, tokens, ragged):
+    """Prefill form (turboquant.metal:268): token t of sequence b attends to positions
+    < L_b - T + t + 1; each token equals the one-token oracle at that length.  Ragged:
+    per-sequence lengths, one shorter than T (its early tokens see nothing -> 0)."""
+    nkv, batch, max_seq = 8, 2, 1024
+    cache = fill_cache(dev, stream, tq, batch, nkv, max_seq, 700, seed=61 + tokens)
+    q16 = np.random.default_rng(62).standard_normal((batch, tokens, nh, D)).astype(np.float16)
+    out = dev.empty((batch, tokens, nh, D), np.float16)
+    lens = np.array([700, tokens - 2 if ragged else 433], np.int32)
+    ops.encode_turboquant_attention(stream, tq, cache, dev.upload(q16), nh, 0, out, 1.0 / math.sqrt(D),
+                                    seq_lens=dev.upload(lens), token_count=tokens)
+    stream.sync()
+    got = out.read()
+    kc, vc, ks, vs, kr = read_cache(cache)
+    for t in range(tokens):
+        lt = np.maximum(lens - tokens + t + 1, 0).astype(np.int32)
+        ref = O.tq_attention(q16[:, t], tables, kc, vc, ks, vs, kr, max_seq, 1.0 / math.sqrt(D),
+                             seq_lens=lt, nthreads=8)
+        for bb in range(batch):
+            if lt[bb] == 0:
+                assert not got[bb, t].astype(np.float32).any()
+            else:
+                assert_close(got[bb, t], ref[bb], rel=5e-4, what=f"token {t} of seq {bb} (len {lt[bb]})")
+
+
 def test_attention_error_paths(dev, stream, tq):
     cache = ops.TurboQuantKvCache(dev, 1, 8, D, 64)
     q = dev.empty((1, 32, D), np.float16)
