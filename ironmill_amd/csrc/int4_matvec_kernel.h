@@ -337,12 +337,7 @@ int4_matvec_kernel(MatPtrs mp, ActIn in, int Nall, int K, int B, int parts, int 
         if (RN) {
             const _Float16 *bh = reinterpret_cast<const _Float16 *>(&ch.b);
             const _Float16 *gh = reinterpret_cast<const _Float16 *>(&ch.g);
-            float ri = 1.0f;
-            if (rnd) {   // rms_inv of row r from the per-group sums already in LDS
-                float ss = 0.0f;
-                for (int g = 0; g < G; g++) ss += rsq[g * 16 + r];
-                ri = 1.0f / __builtin_sqrtf(ss / (float)K + in.eps);
-            }
+            const float ri = rnd ? rmsv[r] : 1.0f;   // rms_inv of row r (row_rms, before)
 #pragma unroll
             for (int i = 0; i < 8; i++) {
                 const float rr = (float)ah[i] + (float)bh[i];
@@ -374,8 +369,22 @@ int4_matvec_kernel(MatPtrs mp, ActIn in, int Nall, int K, int B, int parts, int 
             if (RN && !rnd) rsq[g * 16 + r] = sq;
         }
     };
+    // rms_inv of every batch row from the per-group sums of r^2 in LDS, by
+    // wave 0: lane (r, j) = (lane >> 3, lane & 7) adds groups j, j + 8, ...
+    // of row r, then an xor tree over j (rows <= 8 when RN)
+    auto row_rms = [&]() __attribute__((always_inline)) {
+        const int r = lane >> 3, j = lane & 7;
+        float ss = 0.0f;
+        if (r < bc)
+            for (int g = j; g < G; g += 8) ss += rsq[g * 16 + r];
+        ss += __shfl_xor(ss, 1);
+        ss += __shfl_xor(ss, 2);
+        ss += __shfl_xor(ss, 4);
+        if (r < bc && j == 0) rmsv[r] = 1.0f / __builtin_sqrtf(ss / (float)K + in.eps);
+    };
     // rounded RAW_RN operand: the per-group sums of r^2 first (as chunk_store
-    // would store them), then a barrier, so every chunk sees its row's rms
+    // would store them), then a barrier and row_rms, so every chunk sees its
+    // row's rms
     auto chunk_sq = [&](int r, int col, int gs0, const Chunk &ch, bool live) __attribute__((always_inline)) {
         const _Float16 *ah = reinterpret_cast<const _Float16 *>(&ch.a);
         const _Float16 *bh = reinterpret_cast<const _Float16 *>(&ch.b);
@@ -445,6 +454,10 @@ int4_matvec_kernel(MatPtrs mp, ActIn in, int Nall, int K, int B, int parts, int 
             __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
             __builtin_amdgcn_s_barrier();
             __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+            if (wave == 0) row_rms();
+            __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
+            __builtin_amdgcn_s_barrier();
+            __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
         }
 #pragma unroll
         for (int i = 0; i < XC; i++) {
@@ -507,11 +520,7 @@ int4_matvec_kernel(MatPtrs mp, ActIn in, int Nall, int K, int B, int parts, int 
     __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
     __builtin_amdgcn_s_barrier();
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
-    if (RN && tid < bc) {  // rms_inv of batch row m0 + tid: groups summed in order
-        float s = 0.0f;
-        for (int g = 0; g < G; g++) s += rsq[g * 16 + tid];
-        rmsv[tid] = 1.0f / __builtin_sqrtf(s / (float)K + in.eps);
-    }
+    if (RN && !rnd && wave == 0) row_rms();   // (rounded: computed before the operand)
 #pragma unroll
     for (int t = 0; t < MT; t++) red[(t * waves + wave) * 64 + lane] = acc[t];
     __syncthreads();
