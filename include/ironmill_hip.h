@@ -104,7 +104,11 @@ int imh_fill_zero(imh_stream *stream, void *dst, size_t length);
  * with one launch -- the counterpart of encoding a whole decode step into one
  * Metal command buffer and committing it (pipeline.rs:336-343,1205-1213).
  * Scratch memory an op needs must already exist (run it once before capture);
- * capture fails with IMH_EINVAL otherwise. */
+ * capture fails with IMH_EINVAL otherwise.  A graph replays only on the stream
+ * it was captured on (IMH_EINVAL otherwise: its kernels use that stream's
+ * scratch memory), and must be freed before that stream.  Scratch that grows
+ * after a capture keeps its old blocks until imh_stream_free, so a replay
+ * never addresses freed memory. */
 typedef struct imh_graph imh_graph;
 int imh_stream_begin_capture(imh_stream *stream);
 int imh_stream_end_capture(imh_stream *stream, imh_graph **out);
@@ -419,10 +423,10 @@ int imh_encode_fp16_kv_cache_and_attention(imh_stream *stream, const imh_fp16_kv
  * the KV caches of every layer and the per-sequence positions, all in device
  * memory; weights stay caller-owned.  A step reads token_ids (device uint32
  * [batch]), writes logits (device f16 [batch][vocab_size]) and advances every
- * position by one on the device, so a captured step replays as the next token
- * (the caller keeps positions below max_seq_len across replays; the kernels
- * clamp rather than overrun).  attn_scale 0 = 1/sqrt(head_dim); embed_scale
- * 0 = 1. */
+ * position by one on the device, so a captured step replays as the next token.
+ * A replay with a sequence already at max_seq_len writes no cache row and is
+ * reported by imh_decoder_sync_positions.  attn_scale 0 = 1/sqrt(head_dim);
+ * embed_scale 0 = 1. */
 #define IMH_KV_TURBOQUANT 0
 #define IMH_KV_FP16 1
 typedef struct imh_decoder imh_decoder;
@@ -479,13 +483,30 @@ int imh_decoder_step(imh_decoder *d, imh_stream *stream, const uint32_t *token_i
  * prefill would run it). */
 int imh_decoder_write_kv(imh_decoder *d, imh_stream *stream, uint32_t layer, const uint16_t *k_proj,
                          const uint16_t *v_proj, uint32_t token_count, uint32_t base_pos);
-/* Host mirror of the positions after the encoded steps (host int32 [batch]). */
+/* Host mirror of the positions after the eager steps (host int32 [batch]).
+ * Steps encoded during capture and graph replays do not move it; see
+ * imh_decoder_sync_positions. */
 int imh_decoder_positions(const imh_decoder *d, int32_t *out);
+/* Synchronise the stream, read the device positions into the host mirror (and
+ * into out, host int32 [batch], when not NULL).  IMH_ERANGE when a step ran
+ * with a sequence already at max_seq_len -- a graph replayed past the cache
+ * (pipeline.rs:271-279 refuses that step): such a step writes no cache row,
+ * its logits are invalid, and the condition holds until imh_decoder_reset. */
+int imh_decoder_sync_positions(imh_decoder *d, imh_stream *stream, int32_t *out);
 /* The KV cache of one layer (a view; the decoder owns the memory). */
 int imh_decoder_kv_cache(const imh_decoder *d, uint32_t layer, imh_tq_kv_cache *tq_out,
                          imh_fp16_kv_cache *fp16_out);
-/* The TurboQuant tables the decoder created (NULL for an FP16 cache). */
+/* The TurboQuant tables the decoder uses (NULL for an FP16 cache). */
 int imh_decoder_tq_tables(const imh_decoder *d, imh_tq_tables **out);
+/* Use caller-built tables instead of the ones created from tq_seed -- the
+ * counterpart of MetalTurboQuantModel::new (metal/turboquant/mod.rs:221-287)
+ * handing its signs, codebooks and QJL matrix to the backend: build them with
+ * imh_tq_tables_create_from_host from the reference's own generators
+ * (turboquant/rotation.rs:13-49, codebook.rs:20-52) so the cache codes follow
+ * the reference's tables exactly.  The tables stay caller-owned and must
+ * outlive the decoder; set them before the first step (rows already in the
+ * cache were written under the previous tables). */
+int imh_decoder_set_tq_tables(imh_decoder *d, imh_tq_tables *t);
 
 #ifdef __cplusplus
 }

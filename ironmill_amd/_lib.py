@@ -249,6 +249,8 @@ SIGNATURES = {
     "imh_decoder_step": (I, [P, P, P, P]),
     "imh_decoder_write_kv": (I, [P, P, U32, P, P, U32, U32]),
     "imh_decoder_positions": (I, [P, P]),
+    "imh_decoder_sync_positions": (I, [P, P, P]),
+    "imh_decoder_set_tq_tables": (I, [P, P]),
     "imh_decoder_kv_cache": (I, [P, U32, C.POINTER(TqKvCache), C.POINTER(Fp16KvCache)]),
     "imh_decoder_tq_tables": (I, [P, C.POINTER(P)]),
 }

@@ -46,24 +46,41 @@ struct imh_decoder {
     void *arena = nullptr;  // activations, positions, RoPE tables
     uint16_t *hidden, *residual, *norm_out, *q, *k, *v, *attn_out, *ffn_down, *act;
     int32_t *positions, *seq_lens;
+    int32_t *status;        // set by a step past the cache's end, cleared by reset
     uint16_t *rope_cos, *rope_sin;
 
     void *kv_arena = nullptr;
-    imh_tq_tables *tq = nullptr;
+    imh_tq_tables *own_tq = nullptr;   // created from cfg.tq_seed
+    imh_tq_tables *tq = nullptr;       // in use: own_tq or the caller's (imh_decoder_set_tq_tables)
     std::vector<imh_tq_kv_cache> tq_caches;
     std::vector<imh_fp16_kv_cache> fp16_caches;
 
-    std::vector<int32_t> host_positions;  // mirror of positions for range checks
+    // mirror of positions for range checks: advanced by eager steps (not by
+    // capture), refreshed from the device by imh_decoder_sync_positions
+    std::vector<int32_t> host_positions;
 };
 
 namespace {
 
-__global__ void decoder_advance_kernel(int32_t *positions, int32_t *seq_lens, int batch, int max_seq) {
+// The step's last kernel: positions[b] is the row the step wrote.  When the
+// cache is full (the next position is max_seq) seq_lens[b] becomes 0, so a
+// further step -- a graph replayed once too often -- writes no cache row
+// (the TurboQuant writer skips an empty sequence, the FP16 scatter runs
+// without wrap) and attends over nothing; that step then raises the status
+// flag, which imh_decoder_sync_positions reports as IMH_ERANGE (the
+// reference refuses such a step, metal/pipeline.rs:271-279).
+__global__ void decoder_advance_kernel(int32_t *positions, int32_t *seq_lens, int32_t *status, int batch,
+                                       int max_seq) {
     const int b = blockIdx.x * blockDim.x + threadIdx.x;
     if (b >= batch) return;
-    const int p = positions[b] + 1;
-    positions[b] = p;
-    seq_lens[b] = p + 1 > max_seq ? max_seq : p + 1;
+    const int p = positions[b];
+    if (p >= max_seq) {
+        seq_lens[b] = 0;
+        __hip_atomic_store(status, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        return;
+    }
+    positions[b] = p + 1;
+    seq_lens[b] = p + 1 >= max_seq ? 0 : p + 2;
 }
 
 size_t align256(size_t x) { return (x + 255) & ~size_t(255); }
@@ -119,7 +136,7 @@ int imh_decoder_create(imh_device *dev, const imh_decoder_config *cfg, imh_decod
     const size_t o_hidden = take(B * H * 2), o_res = take(B * H * 2), o_norm = take(B * H * 2);
     const size_t o_q = take(B * qd * 2), o_k = take(B * kvd * 2), o_v = take(B * kvd * 2);
     const size_t o_attn = take(B * qd * 2), o_down = take(B * H * 2), o_act = take(B * F * 2);
-    const size_t o_pos = take(B * 4), o_sl = take(B * 4);
+    const size_t o_pos = take(B * 4), o_sl = take(B * 4), o_st = take(4);
     const size_t o_cos = take((size_t)c.max_seq_len * half_dim * 2), o_sin = take((size_t)c.max_seq_len * half_dim * 2);
     hipError_t e = hipMalloc(&d->arena, off);
     if (e != hipSuccess) {
@@ -138,6 +155,7 @@ int imh_decoder_create(imh_device *dev, const imh_decoder_config *cfg, imh_decod
     d->act = reinterpret_cast<uint16_t *>(base + o_act);
     d->positions = reinterpret_cast<int32_t *>(base + o_pos);
     d->seq_lens = reinterpret_cast<int32_t *>(base + o_sl);
+    d->status = reinterpret_cast<int32_t *>(base + o_st);
     d->rope_cos = reinterpret_cast<uint16_t *>(base + o_cos);
     d->rope_sin = reinterpret_cast<uint16_t *>(base + o_sin);
 
@@ -166,8 +184,9 @@ int imh_decoder_create(imh_device *dev, const imh_decoder_config *cfg, imh_decod
     const size_t rows = B * c.num_kv_heads * (size_t)c.max_seq_len;
     size_t per_layer = 0;
     if (c.kv_cache == IMH_KV_TURBOQUANT) {
-        rc = imh_tq_tables_create(dev, c.head_dim, 8, c.tq_seed, &d->tq);
+        rc = imh_tq_tables_create(dev, c.head_dim, 8, c.tq_seed, &d->own_tq);
         if (rc) return cleanup(rc);
+        d->tq = d->own_tq;
         per_layer = 2 * align256(rows * c.head_dim) + 3 * align256(rows * 4);
     } else {
         per_layer = 2 * align256(rows * c.head_dim * 2);
@@ -217,7 +236,7 @@ void imh_decoder_free(imh_decoder *d) {
     imh::use_device(d->dev);
     if (d->arena) (void)hipFree(d->arena);
     if (d->kv_arena) (void)hipFree(d->kv_arena);
-    if (d->tq) imh_tq_tables_free(d->tq);
+    if (d->own_tq) imh_tq_tables_free(d->own_tq);
     delete d;
 }
 
@@ -270,8 +289,10 @@ int imh_decoder_reset(imh_decoder *d, imh_stream *stream, const int32_t *positio
     }
     int rc = imh::use_device(d->dev);
     if (rc) return rc;
+    const int32_t zero = 0;
     IMH_HIP(hipMemcpyAsync(d->positions, pos.data(), B * 4, hipMemcpyHostToDevice, stream->stream));
     IMH_HIP(hipMemcpyAsync(d->seq_lens, sl.data(), B * 4, hipMemcpyHostToDevice, stream->stream));
+    IMH_HIP(hipMemcpyAsync(d->status, &zero, 4, hipMemcpyHostToDevice, stream->stream));
     IMH_HIP(hipStreamSynchronize(stream->stream));
     d->host_positions = pos;
     return IMH_OK;
@@ -353,8 +374,9 @@ int imh_decoder_step(imh_decoder *d, imh_stream *s, const uint32_t *token_ids, u
         } else {
             IMH_TRY(imh_encode_qk_norm_rope(s, &qp));
             const imh_fp16_kv_cache *kc = &d->fp16_caches[l];
-            IMH_TRY(imh_encode_kv_scatter(s, kc, d->k, 1, 0, d->positions, 1));
-            IMH_TRY(imh_encode_kv_scatter(s, kc, d->v, 1, 0, d->positions, 0));
+            // no ring wrap: a step past the cache's end writes nothing
+            IMH_TRY(imh::encode_kv_scatter_bounded(s, kc, d->k, d->positions, 1));
+            IMH_TRY(imh::encode_kv_scatter_bounded(s, kc, d->v, d->positions, 0));
             IMH_TRY(imh_encode_fp16_attention(s, kc, d->q, c.num_heads, 1, 0, d->seq_lens, c.attn_scale, d->attn_out,
                                               0));
         }
@@ -399,9 +421,11 @@ int imh_decoder_step(imh_decoder *d, imh_stream *s, const uint32_t *token_ids, u
     IMH_TRY(imh_encode_affine_projection_int4(s, d->norm_out, B, &d->lm_head, logits));
 #undef IMH_TRY
     hipLaunchKernelGGL(decoder_advance_kernel, dim3((B + 63) / 64), dim3(64), 0, s->stream, d->positions, d->seq_lens,
-                       (int)B, (int)c.max_seq_len);
+                       d->status, (int)B, (int)c.max_seq_len);
     IMH_HIP(hipGetLastError());
-    for (auto &p : d->host_positions) p++;
+    // a captured step runs only when replayed: the mirror follows eager steps
+    if (!s->capturing)
+        for (auto &p : d->host_positions) p++;
     return IMH_OK;
 }
 
@@ -426,6 +450,27 @@ int imh_decoder_positions(const imh_decoder *d, int32_t *out) {
     return IMH_OK;
 }
 
+int imh_decoder_sync_positions(imh_decoder *d, imh_stream *stream, int32_t *out) {
+    const char *who = "imh_decoder_sync_positions";
+    if (!d || !stream) return imh::fail(IMH_EINVAL, std::string(who) + ": NULL argument");
+    if (stream->capturing) return imh::fail(IMH_EINVAL, std::string(who) + ": not allowed while capturing");
+    int rc = imh::use_device(d->dev);
+    if (rc) return rc;
+    const uint32_t B = d->cfg.batch;
+    std::vector<int32_t> pos(B);
+    int32_t st = 0;
+    IMH_HIP(hipMemcpyAsync(pos.data(), d->positions, B * 4, hipMemcpyDeviceToHost, stream->stream));
+    IMH_HIP(hipMemcpyAsync(&st, d->status, 4, hipMemcpyDeviceToHost, stream->stream));
+    IMH_HIP(hipStreamSynchronize(stream->stream));
+    d->host_positions = pos;
+    if (out) std::memcpy(out, pos.data(), B * 4);
+    if (st)
+        return imh::fail(IMH_ERANGE, std::string(who) + ": a step ran with a sequence at max_seq_len " +
+                                         std::to_string(d->cfg.max_seq_len) +
+                                         " (its logits are invalid; reset the decoder)");
+    return IMH_OK;
+}
+
 int imh_decoder_kv_cache(const imh_decoder *d, uint32_t layer, imh_tq_kv_cache *tq_out, imh_fp16_kv_cache *fp16_out) {
     if (!d) return imh::fail(IMH_EINVAL, "imh_decoder_kv_cache: NULL decoder");
     if (layer >= d->cfg.num_layers) return imh::fail(IMH_EINVAL, "imh_decoder_kv_cache: layer out of range");
@@ -436,6 +481,21 @@ int imh_decoder_kv_cache(const imh_decoder *d, uint32_t layer, imh_tq_kv_cache *
         if (!fp16_out) return imh::fail(IMH_EINVAL, "imh_decoder_kv_cache: FP16 cache needs fp16_out");
         *fp16_out = d->fp16_caches[layer];
     }
+    return IMH_OK;
+}
+
+int imh_decoder_set_tq_tables(imh_decoder *d, imh_tq_tables *t) {
+    const char *who = "imh_decoder_set_tq_tables";
+    if (!d || !t) return imh::fail(IMH_EINVAL, std::string(who) + ": NULL argument");
+    if (d->cfg.kv_cache != IMH_KV_TURBOQUANT)
+        return imh::fail(IMH_EINVAL, std::string(who) + ": the decoder has an FP16 KV cache");
+    if (t->dev->ordinal != d->dev->ordinal)
+        return imh::fail(IMH_EINVAL, std::string(who) + ": tables live on another device");
+    if (t->head_dim != d->cfg.head_dim || t->n_bits != 8)
+        return imh::fail(IMH_EINVAL, std::string(who) + ": tables are for head_dim " + std::to_string(t->head_dim) +
+                                         ", " + std::to_string(t->n_bits) + " bits; the cache needs head_dim " +
+                                         std::to_string(d->cfg.head_dim) + ", 8 bits");
+    d->tq = t;
     return IMH_OK;
 }
 

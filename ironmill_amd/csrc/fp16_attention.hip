@@ -38,13 +38,16 @@ constexpr int kSplitQuantum = kChunk * kWaves;
 
 // grid (num_kv_heads, token_count, batch), block kD / 8: one 16-byte chunk of
 // the head vector per thread.
+// wrap = 0: positions at or past max_seq are skipped instead of wrapping.
 __global__ void __launch_bounds__(kD / 8) fp16_kv_scatter_kernel(const __half *__restrict__ proj, int tokens,
                                                                  int nkv, int max_seq, int base_pos,
                                                                  const int32_t *__restrict__ positions,
-                                                                 __half *__restrict__ cache) {
+                                                                 __half *__restrict__ cache, int wrap) {
     const int h = blockIdx.x, t = blockIdx.y, b = blockIdx.z;
     const int c = threadIdx.x;
-    long pos = ((long)(positions ? positions[b] : base_pos) + t) % max_seq;
+    long pos = (long)(positions ? positions[b] : base_pos) + t;
+    if (!wrap && (pos < 0 || pos >= max_seq)) return;
+    pos %= max_seq;
     if (pos < 0) pos += max_seq;
     const size_t src = (((size_t)b * tokens + t) * nkv + h) * kD + (size_t)c * 8;
     const size_t dst = (((size_t)b * nkv + h) * max_seq + (size_t)pos) * kD + (size_t)c * 8;
@@ -324,7 +327,7 @@ int imh_encode_kv_scatter(imh_stream *stream, const imh_fp16_kv_cache *cache, co
     hipLaunchKernelGGL(fp16_kv_scatter_kernel, grid, dim3(kD / 8), 0, stream->stream,
                        reinterpret_cast<const __half *>(proj), (int)token_count, (int)cache->num_kv_heads,
                        (int)cache->max_seq_len, (int)base_pos, positions,
-                       reinterpret_cast<__half *>(is_k ? cache->k : cache->v));
+                       reinterpret_cast<__half *>(is_k ? cache->k : cache->v), 1);
     IMH_HIP(hipGetLastError());
     return IMH_OK;
 }
@@ -415,3 +418,29 @@ int imh_encode_fp16_kv_cache_and_attention(imh_stream *stream, const imh_fp16_kv
 }
 
 }  // extern "C"
+
+namespace imh {
+
+// One token per sequence at device positions, without the ring wrap of
+// imh_encode_kv_scatter: a position at or past max_seq_len writes nothing
+// (the decoder's step past a full cache).
+int encode_kv_scatter_bounded(imh_stream *stream, const imh_fp16_kv_cache *cache, const uint16_t *proj,
+                              const int32_t *positions, int is_k) {
+    const char *who = "encode_kv_scatter_bounded";
+    if (!stream || !proj || !positions) return fail(IMH_EINVAL, std::string(who) + ": NULL argument");
+    int rc = check_cache(cache, who);
+    if (rc) return rc;
+    if (reinterpret_cast<uintptr_t>(proj) & 15)
+        return fail(IMH_EINVAL, std::string(who) + ": projection must be 16-byte aligned");
+    rc = use_device(stream->dev);
+    if (rc) return rc;
+    dim3 grid(cache->num_kv_heads, 1, cache->batch);
+    hipLaunchKernelGGL(fp16_kv_scatter_kernel, grid, dim3(kD / 8), 0, stream->stream,
+                       reinterpret_cast<const __half *>(proj), 1, (int)cache->num_kv_heads,
+                       (int)cache->max_seq_len, 0, positions,
+                       reinterpret_cast<__half *>(is_k ? cache->k : cache->v), 0);
+    IMH_HIP(hipGetLastError());
+    return IMH_OK;
+}
+
+}  // namespace imh

@@ -6,6 +6,7 @@
 #include <cstddef>
 #include <cstdint>
 #include <string>
+#include <vector>
 
 #include "../../include/ironmill_hip.h"
 
@@ -21,6 +22,11 @@ void clear_error();
         hipError_t e_ = (call);                        \
         if (e_ != hipSuccess) return imh::hip_fail(e_, #call); \
     } while (0)
+
+// One token per sequence scattered into an FP16 cache at device positions
+// without the ring wrap (positions at or past max_seq_len write nothing).
+int encode_kv_scatter_bounded(imh_stream *stream, const imh_fp16_kv_cache *cache, const uint16_t *proj,
+                              const int32_t *positions, int is_k);
 
 }  // namespace imh
 
@@ -40,6 +46,9 @@ struct imh_buffer {
 // the gate output of a prefill gate/up op; slot 2: GEMM split-K partials;
 // slot 3: arrival counters of split reductions (zeroed when allocated, left at
 // zero by every kernel that uses them).
+// A graph captured on the stream records the slots' addresses, so a slot that
+// grows later keeps its old block alive (`retired`) until the stream is freed:
+// a replay never touches freed memory.
 constexpr int kScratchSlots = 4;
 constexpr int kCounterSlot = 3;
 struct imh_stream {
@@ -48,12 +57,17 @@ struct imh_stream {
     void *scratch[kScratchSlots];
     size_t scratch_bytes[kScratchSlots];
     bool capturing;
+    std::vector<void *> retired;
 };
 
+// A captured graph replays on the stream it was captured on only: its kernels
+// use that stream's scratch slots (partials, arrival counters), which another
+// stream's work could use at the same time.
 struct imh_graph {
     imh_device *dev;
     hipGraph_t graph;
     hipGraphExec_t exec;
+    imh_stream *stream;
 };
 
 struct imh_event {
@@ -83,8 +97,8 @@ struct imh_tq_tables {
 
 namespace imh {
 
-// Ensure scratch slot `slot` of the stream holds at least `bytes`; synchronises
-// the stream before replacing a smaller allocation.
+// Ensure scratch slot `slot` of the stream holds at least `bytes`.  A smaller
+// block is replaced, not freed: graphs captured earlier may still address it.
 int stream_scratch(imh_stream *s, int slot, size_t bytes, void **out);
 
 // Make the stream's device current for the calling thread.
@@ -120,5 +134,10 @@ int encode_tq_write_attend(imh_stream *stream, const imh_tq_tables *t, const imh
                            const uint16_t *q, const uint16_t *k_proj, const uint16_t *v_proj, uint32_t num_heads,
                            const int32_t *seq_lens, float attn_scale, uint16_t *out,
                            const imh_qk_norm_rope_params *qk);
+
+// One token per sequence scattered into an FP16 cache at device positions
+// without the ring wrap (positions at or past max_seq_len write nothing).
+int encode_kv_scatter_bounded(imh_stream *stream, const imh_fp16_kv_cache *cache, const uint16_t *proj,
+                              const int32_t *positions, int is_k);
 
 }  // namespace imh

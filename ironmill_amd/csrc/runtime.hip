@@ -40,17 +40,33 @@ int stream_scratch(imh_stream *s, int slot, size_t bytes, void **out) {
                                     "with the same shapes before capturing it");
         int rc = use_device(s->dev);
         if (rc) return rc;
-        if (s->scratch[slot]) {
-            IMH_HIP(hipStreamSynchronize(s->stream));
-            IMH_HIP(hipFree(s->scratch[slot]));
-            s->scratch[slot] = nullptr;
-            s->scratch_bytes[slot] = 0;
-        }
+        // grow by at least 2x so a run of growing shapes retires few blocks
         size_t want = bytes < (1u << 20) ? (1u << 20) : bytes;
-        IMH_HIP(hipMalloc(&s->scratch[slot], want));
+        if (want < 2 * s->scratch_bytes[slot]) want = 2 * s->scratch_bytes[slot];
+        void *fresh = nullptr;
+        IMH_HIP(hipMalloc(&fresh, want));
+        // arrival counters start at zero; kernels leave them at zero.  The
+        // memset is synchronous, so it is complete before any kernel on the
+        // (non-blocking) stream can use the block.
+        if (slot == kCounterSlot) {
+            hipError_t e = hipMemset(fresh, 0, want);
+            if (e != hipSuccess) {
+                (void)hipFree(fresh);
+                return hip_fail(e, "hipMemset");
+            }
+        }
+        // the old block may be addressed by a captured graph: keep it until
+        // the stream is freed (never free memory a replay could touch)
+        if (s->scratch[slot]) {
+            try {
+                s->retired.push_back(s->scratch[slot]);
+            } catch (...) {
+                (void)hipFree(fresh);
+                return fail(IMH_ENOMEM, "stream_scratch: host allocation failed");
+            }
+        }
+        s->scratch[slot] = fresh;
         s->scratch_bytes[slot] = want;
-        // arrival counters start at zero; kernels leave them at zero
-        if (slot == kCounterSlot) IMH_HIP(hipMemset(s->scratch[slot], 0, want));
     }
     *out = s->scratch[slot];
     return IMH_OK;
@@ -214,7 +230,7 @@ int imh_stream_create(imh_device *dev, imh_stream **out) {
     if (rc) return rc;
     hipStream_t s;
     IMH_HIP(hipStreamCreateWithFlags(&s, hipStreamNonBlocking));
-    imh_stream *st = new (std::nothrow) imh_stream{dev, s, {}, {}, false};
+    imh_stream *st = new (std::nothrow) imh_stream{dev, s, {}, {}, false, {}};
     if (!st) {
         (void)hipStreamDestroy(s);
         return imh::fail(IMH_ENOMEM, "imh_stream_create: host allocation failed");
@@ -229,6 +245,7 @@ void imh_stream_free(imh_stream *stream) {
     (void)hipStreamSynchronize(stream->stream);
     for (int i = 0; i < kScratchSlots; i++)
         if (stream->scratch[i]) (void)hipFree(stream->scratch[i]);
+    for (void *p : stream->retired) (void)hipFree(p);
     (void)hipStreamDestroy(stream->stream);
     delete stream;
 }
@@ -278,7 +295,7 @@ int imh_stream_end_capture(imh_stream *stream, imh_graph **out) {
         (void)hipGraphDestroy(g);
         return imh::hip_fail(e, "hipGraphInstantiate");
     }
-    imh_graph *gr = new (std::nothrow) imh_graph{stream->dev, g, ex};
+    imh_graph *gr = new (std::nothrow) imh_graph{stream->dev, g, ex, stream};
     if (!gr) {
         (void)hipGraphExecDestroy(ex);
         (void)hipGraphDestroy(g);
@@ -290,6 +307,10 @@ int imh_stream_end_capture(imh_stream *stream, imh_graph **out) {
 
 int imh_graph_launch(imh_graph *graph, imh_stream *stream) {
     if (!graph || !stream) return imh::fail(IMH_EINVAL, "imh_graph_launch: NULL argument");
+    if (stream != graph->stream)
+        return imh::fail(IMH_EINVAL, "imh_graph_launch: a graph replays on the stream it was captured on "
+                                     "(its kernels use that stream's scratch memory)");
+    if (stream->capturing) return imh::fail(IMH_EINVAL, "imh_graph_launch: the stream is capturing");
     IMH_HIP(hipGraphLaunch(graph->exec, stream->stream));
     return IMH_OK;
 }

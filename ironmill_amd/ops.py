@@ -369,9 +369,22 @@ class Decoder:
                                        base_pos))
 
     def positions(self) -> np.ndarray:
+        """Host mirror of the positions (advanced by eager steps only)."""
         out = np.empty(self.cfg.batch, np.int32)
         check(lib.imh_decoder_positions(self._h, out.ctypes.data_as(C.c_void_p)))
         return out
+
+    def sync_positions(self, stream: Stream) -> np.ndarray:
+        """Device positions after every encoded step and graph replay; raises
+        IronmillError (IMH_ERANGE) if a step ran past the cache's end."""
+        out = np.empty(self.cfg.batch, np.int32)
+        check(lib.imh_decoder_sync_positions(self._h, stream.handle, out.ctypes.data_as(C.c_void_p)))
+        return out
+
+    def set_tq_tables(self, tables: "TurboQuantModel"):
+        """Use caller-built TurboQuant tables (TurboQuantModel(dev, host_tables=...))."""
+        check(lib.imh_decoder_set_tq_tables(self._h, tables.handle))
+        self._keep["tq_tables"] = tables
 
     def kv_cache(self, layer: int) -> dict:
         """Host copies of one layer's cache arrays."""

@@ -424,10 +424,24 @@ class DecoderReference:
 
     layers: list of dicts with input_norm, post_attn_norm, q_norm, k_norm (f16 arrays or None)
     and q_proj, k_proj, v_proj, o_proj, gate_proj, up_proj, down_proj (objects with data,
-    scales_f32, zeros_f32, awq, n, k)."""
+    scales_f32, zeros_f32, awq, n, k; for weights="exact" also scales / zeros f16).
+
+    Variants for sensitivity studies (the default is the reference's CPU path):
+      weights="exact": the GPU upload's weight semantics instead of the CPU dequant --
+        w = (q - z16) * s16 with the f16 scales and zero-points (metal/weights.rs:1064-1103,
+        core/dequant.rs:305-345), exact in f32, not rounded to f16;
+      acc="f64": projections accumulate in float64 (numpy) instead of a sequential f32 sum,
+        which changes only the rounding of the f32 result (weights="exact" only).
+    tables: TQTables to use instead of TQTables(head_dim, 8, tq_seed)."""
 
     def __init__(self, cfg: dict, layers, embedding16, final_norm16, lm_head, kv_cache="turboquant",
-                 tq_seed=42):
+                 tq_seed=42, weights="f16", acc="f32", tables=None):
+        if weights not in ("f16", "exact") or acc not in ("f32", "f64"):
+            raise ValueError("weights must be 'f16' or 'exact', acc 'f32' or 'f64'")
+        if weights == "f16" and acc != "f32":
+            raise ValueError("the f16-weight path accumulates in f32 (the reference's CPU path)")
+        self.exact = weights == "exact"
+        self.acc = np.float64 if acc == "f64" else np.float32
         self.cfg = dict(cfg)
         c = self.cfg
         self.B = c["batch"]
@@ -443,14 +457,12 @@ class DecoderReference:
         for L in layers:
             d = dict(L)
             for name in ("q_proj", "k_proj", "v_proj", "o_proj", "gate_proj", "up_proj", "down_proj"):
-                w = L[name]
-                d[name] = (dequant_affine_int4(w.data, w.scales_f32, w.zeros_f32, w.n, w.k), w.awq)
+                d[name] = self._dense(L[name])
             self.layers.append(d)
-        self.lm = (dequant_affine_int4(lm_head.data, lm_head.scales_f32, lm_head.zeros_f32, lm_head.n, lm_head.k),
-                   lm_head.awq)
+        self.lm = self._dense(lm_head)
         shp = (self.B, self.nkv, self.max_seq)
         if kv_cache == "turboquant":
-            self.tables = TQTables(self.hd, 8, tq_seed)
+            self.tables = tables if tables is not None else TQTables(self.hd, 8, tq_seed)
             self.caches = [dict(k_codes=np.zeros(shp + (self.hd,), np.uint8),
                                 v_codes=np.zeros(shp + (self.hd,), np.uint8),
                                 k_scales=np.zeros(shp, np.float32), v_scales=np.zeros(shp, np.float32),
@@ -460,10 +472,50 @@ class DecoderReference:
                            for _ in layers]
         self.positions = np.zeros(self.B, np.int32)
 
-    @staticmethod
-    def _proj(w, x16):
+    def _dense(self, w):
+        if not self.exact:
+            return (dequant_affine_int4(w.data, w.scales_f32, w.zeros_f32, w.n, w.k), w.awq)
+        q = unpack_int4(np.asarray(w.data).reshape(-1), w.n * w.k).reshape(w.n, w.k // 128, 128)
+        z = np.asarray(w.zeros, np.float16).astype(np.float32)[:, :, None]
+        s = np.asarray(w.scales, np.float16).astype(np.float32)[:, :, None]
+        return (((q.astype(np.float32) - z) * s).reshape(w.n, w.k).astype(self.acc), w.awq)
+
+    def _act(self, x16, awq):
+        x = np.asarray(x16, np.float16).astype(np.float32)
+        if awq is not None:
+            x = x / np.asarray(awq, np.float16).astype(np.float32)
+        return x
+
+    def _matvec(self, w, x16):
+        """f32 [B, N] of one projection (x16 [B, K] f16)."""
         dense, awq = w
-        return matvec_f16w(dense, x16, awq, nthreads=8).astype(np.float16)
+        if not self.exact:
+            return matvec_f16w(dense, x16, awq, nthreads=8)
+        return (self._act(x16, awq).astype(self.acc) @ dense.T).astype(np.float32)
+
+    def _proj(self, w, x16):
+        return self._matvec(w, x16).astype(np.float16)
+
+    def _gate_up_act(self, g_w, u_w, x16, act):
+        if not self.exact:
+            return gate_up_act(g_w[0], u_w[0], x16, g_w[1], act=act)
+        g = self._matvec((g_w[0], g_w[1]), x16)
+        u = self._matvec((u_w[0], g_w[1]), x16)
+        a = g / (np.float32(1.0) + np.exp(-g)) if act == "silu" else gelu_tanh(g)
+        return (a * u).astype(np.float32)
+
+    def _resnorm_matvec(self, a16, b16, gamma16, w, eps):
+        """fused_residual_norm_matvec (superblock_fused_norm.metal:37-124) -> (y, residual, normed)."""
+        if not self.exact:
+            return fused_residual_norm_matvec(a16, b16, gamma16, w[0], eps, w[1])
+        r = np.asarray(a16, np.float16).astype(np.float32) + np.asarray(b16, np.float16).astype(np.float32)
+        g = np.asarray(gamma16, np.float16).astype(np.float32)
+        rms_inv = (1.0 / np.sqrt((r.astype(np.float64) ** 2).mean(axis=-1, keepdims=True) + eps)).astype(np.float32)
+        x = r * g
+        if w[1] is not None:
+            x = x / np.asarray(w[1], np.float16).astype(np.float32)
+        y = (x.astype(self.acc) @ w[0].T).astype(np.float32) * rms_inv
+        return y, r.astype(np.float16), (r * rms_inv * g).astype(np.float16)
 
     def _write_cache(self, l, k16, v16):
         cache, pos = self.caches[l], self.positions
@@ -516,19 +568,17 @@ class DecoderReference:
             attn = self._attend(l, q)
             o = self._proj(L["o_proj"], attn.reshape(B, nh * hd))
             normed, residual = fused_residual_rms_norm(hidden, o, L["post_attn_norm"], eps)
-            (gd, gawq), (ud, _) = L["gate_proj"], L["up_proj"]
-            act = gate_up_act(gd, ud, normed, gawq,
-                              act="gelu" if self.cfg.get("use_gelu") else "silu").astype(np.float16)
+            act = self._gate_up_act(L["gate_proj"], L["up_proj"], normed,
+                                    "gelu" if self.cfg.get("use_gelu") else "silu").astype(np.float16)
             down = self._proj(L["down_proj"], act)
             if l + 1 < len(self.layers):
                 nL = self.layers[l + 1]
-                qd, qawq = nL["q_proj"]
-                y, hidden, normed = fused_residual_norm_matvec(residual, down, nL["input_norm"], qd, eps, qawq)
+                y, hidden, normed = self._resnorm_matvec(residual, down, nL["input_norm"], nL["q_proj"], eps)
                 q = y.astype(np.float16)
             else:
                 hidden = residual_add(residual, down)
                 q = None
         normed = rms_norm(hidden, self.final_norm, eps)
-        logits = matvec_f16w(self.lm[0], normed, self.lm[1], nthreads=8)
+        logits = self._matvec(self.lm, normed)
         self.positions = self.positions + 1
         return logits

@@ -194,12 +194,25 @@ def build_decoder(dev, model, kv_cache, cfg=CFG):
     return d
 
 
-@pytest.mark.parametrize("kv_cache", ["fp16", "turboquant"])
+@pytest.mark.parametrize("kv_cache", ["fp16", "turboquant", "turboquant-host-tables"])
 def test_decoder_matches_reference(dev, stream, kv_cache):
+    """turboquant-host-tables: the decoder uses caller-built tables (imh_decoder_set_tq_tables,
+    the path a binding takes to hand over the reference's own generator outputs), here the
+    oracle's tables for another seed, and the oracle runs on the same tables."""
     model = make_model(dev, 77)
+    host = kv_cache == "turboquant-host-tables"
+    kv_cache = "turboquant" if host else kv_cache
     d = build_decoder(dev, model, kv_cache)
     host_layers, _, emb, fnorm, lm = model
-    ref = O.DecoderReference(CFG, host_layers, emb, fnorm, lm, kv_cache=kv_cache)
+    tabs = None
+    if host:
+        tabs = O.TQTables(128, 8, 1234)
+        t = ops.TurboQuantModel(dev, 128, 8, host_tables=dict(
+            signs=tabs.signs, k_codebook=tabs.k_codebook, k_bounds=tabs.k_bounds, v_codebook=tabs.v_codebook,
+            v_bounds=tabs.v_bounds, qjl=tabs.qjl))
+        d.set_tq_tables(t)
+        assert np.array_equal(t.tables()["signs"], tabs.signs)
+    ref = O.DecoderReference(CFG, host_layers, emb, fnorm, lm, kv_cache=kv_cache, tables=tabs)
     start = np.array([0, 9], np.int32)
     d.reset(stream, start)
     ref.positions = start.copy()
@@ -256,39 +269,6 @@ def test_decoder_matches_reference(dev, stream, kv_cache):
             assert not got["k"][b, :, start[b] + 4:].view(np.uint16).any()
 
 
-@pytest.mark.parametrize("batch", [2, 8])
-def test_decoder_wide_matches_reference(dev, stream, batch):
-    """Hidden 2560: at batch 2 the projections build their operand in the
-    workgroup; at batch 8 the fused residual-norm projections (Q/K/V and
-    gate/up) take the operand-image path (prep kernel + image matvec).
-
-    Tolerance 3e-3 on the logits: each op is within 1e-3 of the oracle on its
-    own (test_gpu_int4.py), but two layers at K = 2560 compound the oracle's
-    f16 rounding of the dequantized weights (the kernels keep (q - z) * s
-    exact): measured 1.2e-3 to 1.5e-3 at both batch sizes with two layers, so
-    an error of the image path alone would show as a gap between the two."""
-    B = batch
-    # three layers: the end of layer 1 runs the segmented Q/K/V launch fused
-    # with the residual norm (layer 2 shares the AWQ scales across Q, K, V)
-    cfg = dict(CFG, hidden_size=2560, intermediate_size=1024, num_layers=3, batch=B, vocab_size=256)
-    model = make_model(dev, 81, cfg)
-    d = build_decoder(dev, model, "fp16", cfg)
-    host_layers, _, emb, fnorm, lm = model
-    ref = O.DecoderReference(cfg, host_layers, emb, fnorm, lm, kv_cache="fp16")
-    start = np.arange(B, dtype=np.int32) * 3
-    d.reset(stream, start)
-    ref.positions = start.copy()
-    rng = np.random.default_rng(6)
-    logits = dev.empty((B, cfg["vocab_size"]), np.float16)
-    for step in range(2):
-        tok = rng.integers(0, cfg["vocab_size"], B).astype(np.uint32)
-        d.step(stream, dev.upload(tok), logits)
-        stream.sync()
-        want = ref.step(tok.astype(np.int64))
-        r = rel_l2(logits.read(), want)
-        assert r <= 3e-3, f"batch {B} step {step}: logits rel-L2 {r:.3e}"
-
-
 def test_decoder_graph_replay_matches_eager(dev, stream):
     """A captured step replays as the next token: positions advance on the device."""
     model = make_model(dev, 78, qk_norm=False)
@@ -310,6 +290,45 @@ def test_decoder_graph_replay_matches_eager(dev, stream):
     ka, kb = eager.kv_cache(0), graphed.kv_cache(0)
     assert np.array_equal(ka["k_codes"], kb["k_codes"]) and np.array_equal(ka["v_scales"], kb["v_scales"])
     assert ka["k_scales"][:, :, :3].all() and not ka["k_scales"][:, :, 3:].any()
+
+
+@pytest.mark.parametrize("kv_cache", ["turboquant", "fp16"])
+def test_decoder_graph_replay_past_cache_end(dev, stream, kv_cache):
+    """Replays advance the device positions only: the host mirror stays where the eager
+    steps left it until imh_decoder_sync_positions reads the device.  A replay with a
+    sequence already at max_seq_len writes no cache row (the full cache's last row is kept,
+    no ring wrap), raises the decoder's status, and sync_positions reports IMH_ERANGE until
+    a reset -- the reference refuses such a step (pipeline.rs:271-279)."""
+    cfg = dict(CFG, max_seq_len=8, num_layers=2)
+    model = make_model(dev, 80, cfg)
+    d = build_decoder(dev, model, kv_cache, cfg)
+    tok = dev.upload(np.array([3, 4], np.uint32))
+    logits = dev.empty((2, cfg["vocab_size"]), np.float16)
+    d.reset(stream, np.array([5, 0], np.int32))
+    d.step(stream, tok, logits)          # sizes the stream's scratch before the capture
+    d.reset(stream, np.array([5, 0], np.int32))
+    graph = stream.capture(lambda: d.step(stream, tok, logits))
+    assert np.array_equal(d.positions(), [5, 0])      # capture runs nothing
+    for _ in range(3):
+        graph.launch(stream)
+    assert np.array_equal(d.sync_positions(stream), [8, 3])
+    assert np.array_equal(d.positions(), [8, 3])
+    before = d.kv_cache(1)
+    graph.launch(stream)                 # sequence 0 is full: its step is refused on the device
+    with pytest.raises(IronmillError, match="max_seq_len"):
+        d.sync_positions(stream)
+    after = d.kv_cache(1)
+    for name in before:
+        assert np.array_equal(after[name][0], before[name][0]), f"{name}: the full sequence's rows changed"
+        # sequence 1 (position 3) stepped normally: row 3 written, the others kept
+        other = np.arange(8) != 3
+        assert np.array_equal(after[name][1][:, other], before[name][1][:, other])
+    assert np.array_equal(d.positions(), [8, 4])
+    with pytest.raises(IronmillError, match="beyond max_seq_len"):
+        d.step(stream, tok, logits)      # the eager range check sees the refreshed mirror
+    d.reset(stream, np.array([0, 0], np.int32))
+    assert np.array_equal(d.sync_positions(stream), [0, 0])
+    graph.close()
 
 
 def test_decoder_errors(dev, stream):

@@ -66,6 +66,22 @@ def test_gemm_projection(dev, stream, m, n, k, awq):
     assert_close(yd.read(), ref, what=f"gemm m={m} n={n} k={k} awq={awq}", ulps=ulps_for(awq))
 
 
+@pytest.mark.parametrize("m,n,k", [(512, 9728, 2560), (512, 2560, 9728), (2048, 9728, 2560), (2048, 2560, 9728)])
+def test_gemm_configs3_full_shapes(dev, stream, m, n, k):
+    """BASELINE configs[3] at its full sizes (M = 512 / 2048, (K, N) = (2560, 9728) and
+    (9728, 2560)), AWQ, every output against the oracle."""
+    print(f"gemm configs[3] m={m} n={n} k={k}", flush=True)
+    w, s = weight(n, k, 7 * m + n, True)
+    x16 = acts(m, k, 11 * m + k)
+    wt = ops.AffineQuantizedWeight(dev, quant.quantize_int4(w, awq_scales=s))
+    xd, yd = dev.upload(x16), dev.empty((m, n), np.float16)
+    ops.encode_projection(stream, xd, wt, yd, m)
+    stream.sync()
+    wdq, awq16 = dense(w, s)
+    ref = O.matvec_f16w(wdq, x16, awq16, nthreads=16)
+    assert_close(yd.read(), ref, what=f"gemm m={m} n={n} k={k}", ulps=ulps_for(True))
+
+
 def test_gemm_matches_matvec_at_the_switch(dev, stream):
     """The same rows through the matvec (31 tokens) and the GEMM (32 tokens)."""
     n, k = 512, 1024

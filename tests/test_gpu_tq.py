@@ -195,6 +195,38 @@ def test_attention_full_size(dev, stream, tq, tables, batch, ctx):
     assert_close(got, ref, what=f"full size B={batch} ctx={ctx}")
 
 
+def fill_cache_blocks(dev, stream, tq, batch, nkv, ctx, block, seed):
+    """A cache of ctx positions per sequence written block by block (configs[2] data, one
+    seeded block of K/V rows per sequence, repeated every `block` positions)."""
+    cache = ops.TurboQuantKvCache(dev, batch, nkv, D, ctx)
+    cache.zero(stream)
+    k = kv_data(batch, block, nkv, seed)
+    v = kv_data(batch, block, nkv, seed + 1)
+    kd, vd = dev.upload(k), dev.upload(v)
+    for base in range(0, ctx, block):
+        ops.encode_turboquant_cache_write_kv(stream, tq, cache, kd, vd, min(block, ctx - base), base)
+    stream.sync()
+    return cache
+
+
+@pytest.mark.parametrize("batch,ctx", [(8, 2048), (8, 8192), (16, 8192), (16, 32768)])
+def test_attention_benchmarked_shapes(dev, stream, tq, tables, batch, ctx):
+    """Every (batch, context) of configs[2] that the benchmark reports beyond the cases
+    above: all rows against the oracle, and the automatic split against one split (the
+    split-combine identity, to f32 rounding)."""
+    nkv, nh = 8, 32
+    print(f"tq attention B={batch} ctx={ctx}", flush=True)
+    cache = fill_cache_blocks(dev, stream, tq, batch, nkv, ctx, min(ctx, 4096), seed=ctx // 7 + batch)
+    q16 = np.random.default_rng(14 + batch).standard_normal((batch, nh, D)).astype(np.float16)
+    got = run_attention(dev, stream, tq, cache, q16, nh, ctx)
+    one = run_attention(dev, stream, tq, cache, q16, nh, ctx, num_splits=1)
+    kc, vc, ks, vs, kr = read_cache(cache)
+    ref = O.tq_attention(q16, tables, kc, vc, ks, vs, kr, ctx, 1.0 / math.sqrt(D), nthreads=16)
+    assert_close(got, ref, what=f"B={batch} ctx={ctx}")
+    assert_close(one, ref, what=f"B={batch} ctx={ctx}, one split")
+    assert_close(got.astype(np.float32), one.astype(np.float32), rel=2e-3, max_abs=2e-3, what="split vs single")
+
+
 def test_attention_long_context_plain_normal(dev, stream, tq, tables):
     """Plain N(0,1) K/V at 30000 positions: the weights are nearly uniform, so the output
     shrinks as 1/sqrt(positions) while a rounding bias of the V codebook does not.  With the
@@ -270,6 +302,32 @@ def test_attention_multi_token_causal(dev, stream, tq, tables, nh, tokens, ragge
                 assert not got[bb, t].astype(np.float32).any()
             else:
                 assert_close(got[bb, t], ref[bb], rel=5e-4, what=f"token {t} of seq {bb} (len {lt[bb]})")
+
+
+def test_graph_replay_after_scratch_growth(dev, tq):
+    """A graph keeps addressing the stream scratch it was captured with: a larger eager op
+    that grows the scratch afterwards must not free it (the replay equals the eager run,
+    bit for bit), and the graph refuses a stream other than the capturing one."""
+    s1, s2 = dev.stream(), dev.stream()
+    small = fill_cache(dev, s1, tq, 1, 8, 1024, 1000, seed=71)
+    big = fill_cache(dev, s1, tq, 4, 8, 8192, 8192, seed=72)
+    q_small = dev.upload(np.random.default_rng(73).standard_normal((1, 32, D)).astype(np.float16))
+    q_big = dev.upload(np.random.default_rng(74).standard_normal((4, 32, D)).astype(np.float16))
+    eager, replay = dev.empty((1, 32, D), np.float16), dev.empty((1, 32, D), np.float16)
+    out_big = dev.empty((4, 32, D), np.float16)
+    ops.encode_turboquant_attention(s1, tq, small, q_small, 32, 1000, eager, num_splits=8)
+    s1.sync()
+    graph = s1.capture(lambda: ops.encode_turboquant_attention(s1, tq, small, q_small, 32, 1000, replay,
+                                                               num_splits=8))
+    # grows the split-partial and counter slots past the captured blocks
+    ops.encode_turboquant_attention(s1, tq, big, q_big, 32, 8192, out_big, num_splits=64)
+    for _ in range(3):
+        graph.launch(s1)
+        s1.sync()
+        assert np.array_equal(replay.read().view(np.uint16), eager.read().view(np.uint16))
+    with pytest.raises(IronmillError, match="captured on"):
+        graph.launch(s2)
+    graph.close()
 
 
 def test_attention_error_paths(dev, stream, tq):
