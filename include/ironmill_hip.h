@@ -276,6 +276,23 @@ int imh_encode_turboquant_attention(imh_stream *stream, const imh_tq_tables *t,
                                     const int32_t *seq_lens, float attn_scale, uint16_t *out,
                                     uint32_t num_splits);
 
+/* No counterpart in the reference: imh_encode_turboquant_attention for callers
+ * that cannot allocate device memory (code under HIP graph capture on a stream
+ * whose scratch has not grown yet, tight serving loops, harnesses that forbid
+ * hipMalloc).  Same arguments, kernels and results; the split partials and
+ * arrival counters live in a fixed per-GPU device array (4 MiB of partials --
+ * batch x num_heads x splits x 520 B -- and 4096 counters, batch x
+ * num_kv_heads) instead of the stream's scratch, so the call allocates
+ * nothing.  A shape that needs more returns IMH_EINVAL (pass fewer num_splits
+ * or a smaller batch).  Every call on one GPU shares that array: calls that
+ * overlap on one GPU (two streams at once) race; calls in one stream are
+ * ordered.  The counters are cleared by a fill kernel in each call. */
+int imh_encode_turboquant_attention_noalloc(imh_stream *stream, const imh_tq_tables *t,
+                                            const imh_tq_kv_cache *cache, const uint16_t *q,
+                                            uint32_t num_heads, uint32_t seq_len,
+                                            const int32_t *seq_lens, float attn_scale, uint16_t *out,
+                                            uint32_t num_splits);
+
 /* Causal attention of token_count query tokens per sequence (the prefill form
  * of turboquant_attention, turboquant.metal:202-462 with token_idx = tgid.y,
  * seq_len = base + token_idx + 1): q and out [batch][token_count][num_heads]

@@ -227,6 +227,8 @@ SIGNATURES = {
     "imh_encode_turboquant_cache_write_kv": (I, [P, P, C.POINTER(TqKvCache), P, P, U32, U32, P]),
     "imh_encode_turboquant_attention": (I, [P, P, C.POINTER(TqKvCache), P, U32, U32, P, C.c_float, P,
                                             U32]),
+    "imh_encode_turboquant_attention_noalloc": (I, [P, P, C.POINTER(TqKvCache), P, U32, U32, P, C.c_float, P,
+                                                    U32]),
     "imh_encode_turboquant_attention_tokens": (I, [P, P, C.POINTER(TqKvCache), P, U32, U32, U32, P, C.c_float, P,
                                             U32]),
     "imh_encode_kv_cache_and_attention": (I, [P, P, C.POINTER(TqKvCache), P, P, P, U32, U32, C.c_float,

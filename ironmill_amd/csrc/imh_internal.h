@@ -104,6 +104,10 @@ int stream_scratch(imh_stream *s, int slot, size_t bytes, void **out);
 // Make the stream's device current for the calling thread.
 int use_device(const imh_device *dev);
 
+// Look up, once per device, the address of the fixed scratch array that
+// imh_encode_turboquant_attention_noalloc uses (called when a device opens).
+int noalloc_scratch_init(int ordinal);
+
 // Projections of one activation by up to three INT4 weights that share k and
 // the AWQ scales (a layer's Q, K and V), as the row segments of one matvec
 // launch: out[i] = act . w[i]^T.  The activation is x, or, when rn is given,

@@ -125,6 +125,12 @@ int imh_device_open(int ordinal, imh_device **out) {
         return imh::fail(IMH_EUNSUPPORTED,
                          "imh_device_open: kernels are built for gfx950, device is " + arch);
     }
+    // per-device set-up: the no-alloc attention's fixed scratch address
+    int rc = imh::noalloc_scratch_init(ordinal);
+    if (rc) {
+        delete d;
+        return rc;
+    }
     *out = d;
     return IMH_OK;
 }

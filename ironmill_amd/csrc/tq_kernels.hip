@@ -29,6 +29,7 @@
 
 #include <algorithm>
 #include <cmath>
+#include <mutex>
 #include <string>
 
 #include "dpp_reduce.h"
@@ -915,11 +916,54 @@ int imh_encode_turboquant_cache_write_kv(imh_stream *stream, const imh_tq_tables
     return launch_cache_write(stream, t, cache, k_proj, v_proj, token_count, base_pos, positions, who);
 }
 
+}  // extern "C"
+
+// ---------------------------------------------------------------------------
+// Fixed scratch of imh_encode_turboquant_attention_noalloc: split partials
+// (o, max, sum per query row, head and split) then the groups' arrival
+// counters, in one device array per GPU, held until the process ends.  Host
+// code never passes the array's name to a kernel (on the host it is only a
+// stand-in); it uses the address hipGetSymbolAddress returns for the current
+// device, looked up once per device when the device is opened.
+// ---------------------------------------------------------------------------
+constexpr size_t kNoAllocPartBytes = size_t(4) << 20;   // partials
+constexpr size_t kNoAllocCounters = 4096;               // batch x kv heads
+static __device__ __align__(256) uint8_t scratch[kNoAllocPartBytes + kNoAllocCounters * 4];
+
+constexpr int kMaxDevices = 64;
+static void *g_scratch_ptr[kMaxDevices];
+static std::mutex g_scratch_mu;
+
+namespace imh {
+
+int noalloc_scratch_init(int ordinal) {
+    if (ordinal < 0 || ordinal >= kMaxDevices)
+        return fail(IMH_EUNSUPPORTED, "device ordinal above the library's limit of 64");
+    std::lock_guard<std::mutex> lock(g_scratch_mu);
+    if (g_scratch_ptr[ordinal]) return IMH_OK;
+    int cur = -1;
+    IMH_HIP(hipGetDevice(&cur));
+    if (cur != ordinal) IMH_HIP(hipSetDevice(ordinal));
+    void *ptr = nullptr;
+    hipError_t e = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+    if (e != hipSuccess) return hip_fail(e, "hipGetSymbolAddress(scratch)");
+    if (!ptr) return fail(IMH_EDEVICE, "hipGetSymbolAddress(scratch) returned NULL");
+    g_scratch_ptr[ordinal] = ptr;
+    return IMH_OK;
+}
+
+}  // namespace imh
+
+extern "C" {
+
+// fixed_scratch: the no-alloc entry point's per-device array (NULL: the
+// stream's scratch slots, grown on demand)
 static int run_attention(imh_stream *stream, const imh_tq_tables *t, const imh_tq_kv_cache *cache,
                          const uint16_t *q, uint32_t num_heads, uint32_t seq_len, const int32_t *seq_lens,
                          float attn_scale, uint16_t *out, uint32_t num_splits, const char *who,
                          const imh_qk_norm_rope_params *qk, const uint16_t *k_new = nullptr,
-                         const uint16_t *v_new = nullptr, uint32_t token_count = 1) {
+                         const uint16_t *v_new = nullptr, uint32_t token_count = 1,
+                         void *fixed_scratch = nullptr) {
     if (!stream || !q || !out) return imh::fail(IMH_EINVAL, std::string(who) + ": NULL argument");
     const bool fused = k_new != nullptr;   // the token's cache write in the same launch
     int rc = check_cache(t, cache, who);
@@ -968,10 +1012,28 @@ static int run_attention(imh_stream *stream, const imh_tq_tables *t, const imh_t
     int *ctr = nullptr;
     if (S > 1) {
         void *scr = nullptr, *cs = nullptr;
-        rc = imh::stream_scratch(stream, 1, nparts * kD * 4 + nparts * 8 + 512, &scr);
-        if (rc) return rc;
-        rc = imh::stream_scratch(stream, kCounterSlot, (size_t)B * nkv * 4, &cs);
-        if (rc) return rc;
+        const size_t part_bytes = nparts * kD * 4 + nparts * 8 + 512;
+        const size_t ctr_count = (size_t)B * nkv;
+        if (fixed_scratch) {
+            if (part_bytes > kNoAllocPartBytes || ctr_count > kNoAllocCounters)
+                return imh::fail(IMH_EINVAL,
+                                 std::string(who) + ": needs " + std::to_string(part_bytes) + " bytes of split "
+                                 "partials and " + std::to_string(ctr_count) + " counters; the fixed scratch holds " +
+                                 std::to_string(kNoAllocPartBytes) + " bytes and " +
+                                 std::to_string(kNoAllocCounters) + " counters (fewer num_splits or a smaller "
+                                 "batch fit)");
+            scr = fixed_scratch;
+            cs = static_cast<uint8_t *>(fixed_scratch) + kNoAllocPartBytes;
+            // the counters must start at zero: clear them with a fill kernel
+            // (the array keeps the previous call's contents)
+            rc = imh_fill_zero(stream, cs, ctr_count * 4);
+            if (rc) return rc;
+        } else {
+            rc = imh::stream_scratch(stream, 1, part_bytes, &scr);
+            if (rc) return rc;
+            rc = imh::stream_scratch(stream, kCounterSlot, ctr_count * 4, &cs);
+            if (rc) return rc;
+        }
         po = static_cast<float *>(scr);
         pm = po + nparts * kD;
         pl = pm + nparts;
@@ -1037,6 +1099,30 @@ int imh_encode_turboquant_attention(imh_stream *stream, const imh_tq_tables *t,
                                     float attn_scale, uint16_t *out, uint32_t num_splits) {
     return run_attention(stream, t, cache, q, num_heads, seq_len, seq_lens, attn_scale, out, num_splits,
                          "imh_encode_turboquant_attention", nullptr);
+}
+
+int imh_encode_turboquant_attention_noalloc(imh_stream *stream, const imh_tq_tables *t,
+                                            const imh_tq_kv_cache *cache, const uint16_t *q,
+                                            uint32_t num_heads, uint32_t seq_len, const int32_t *seq_lens,
+                                            float attn_scale, uint16_t *out, uint32_t num_splits) {
+    const char *who = "imh_encode_turboquant_attention_noalloc";
+    if (!stream) return imh::fail(IMH_EINVAL, std::string(who) + ": NULL stream");
+    const int ord = stream->dev->ordinal;
+    void *ptr = nullptr;
+    {
+        std::lock_guard<std::mutex> lock(g_scratch_mu);
+        ptr = (ord >= 0 && ord < kMaxDevices) ? g_scratch_ptr[ord] : nullptr;
+    }
+    if (!ptr) {   // imh_device_open looks it up; a device opened otherwise gets it here
+        int rc = imh::use_device(stream->dev);
+        if (rc) return rc;
+        rc = imh::noalloc_scratch_init(ord);
+        if (rc) return rc;
+        std::lock_guard<std::mutex> lock(g_scratch_mu);
+        ptr = g_scratch_ptr[ord];
+    }
+    return run_attention(stream, t, cache, q, num_heads, seq_len, seq_lens, attn_scale, out, num_splits, who,
+                         nullptr, nullptr, nullptr, 1, ptr);
 }
 
 int imh_encode_turboquant_attention_tokens(imh_stream *stream, const imh_tq_tables *t,
