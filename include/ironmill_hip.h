@@ -177,6 +177,22 @@ int imh_encode_ffn_block_int4(imh_stream *stream, const uint16_t *x, uint32_t to
                               const imh_affine_int4_weight *down, uint16_t *act_out, uint16_t *y,
                               int use_gelu);
 
+/* Prefill GEMM at a chosen matrix-core precision (superblock_matmul_int4,
+ * affine_matmul.metal:10-152):
+ *   y[m][n] = sum_k a[m][k] * (q[n][k] - z) * s,  f32 accumulate, a = x / awq.
+ * IMH_GEMM_F16: x and y f16 -- the projection op above (matvec below 32
+ *   tokens, the f16 GEMM from 32);
+ * IMH_GEMM_BF16: x and y bf16, a rounded once to bf16, bf16 matrix cores;
+ * IMH_GEMM_FP8_E4M3: x and y bf16, a rounded once to OCP e4m3 (saturating at
+ *   +-448), fp8 matrix cores.
+ * The weights are not rounded at any precision (exact codes, zero-point and
+ * scale applied in f32).  x [M][K], y [M][N]; M <= 65535. */
+#define IMH_GEMM_F16 0
+#define IMH_GEMM_BF16 1
+#define IMH_GEMM_FP8_E4M3 2
+int imh_affine_gemm_int4(imh_stream *stream, const void *x, uint32_t M, const imh_affine_int4_weight *w,
+                         void *y, int precision);
+
 /* FusedResidualNormAffineInt4Params (ops/fused.rs:45-66) with a token count. */
 typedef struct {
     const uint16_t *a;           /* [token_count][k] */

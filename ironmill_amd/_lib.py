@@ -217,6 +217,7 @@ SIGNATURES = {
                                                   C.POINTER(AffineInt4Weight), P, I]),
     "imh_encode_ffn_block_int4": (I, [P, P, U32, C.POINTER(AffineInt4Weight), C.POINTER(AffineInt4Weight),
                                       C.POINTER(AffineInt4Weight), P, P, I]),
+    "imh_affine_gemm_int4": (I, [P, P, U32, C.POINTER(AffineInt4Weight), P, I]),
     "imh_encode_fused_residual_norm_affine_matvec_int4": (I, [P, C.POINTER(FusedResidualNormParams)]),
     "imh_tq_tables_create": (I, [P, U32, U32, C.c_uint64, C.POINTER(P)]),
     "imh_tq_tables_create_from_host": (I, [P, U32, U32, P, P, P, P, P, P, C.POINTER(P)]),

@@ -1,0 +1,463 @@
+// int4_gemm_mx.hip -- the INT4-affine (group 128) prefill GEMM with bf16 or
+// fp8-e4m3 matrix-core operands (superblock_matmul_int4, affine_matmul.metal:
+// 10-152, at the precisions of BASELINE configs[3]):
+//
+//     C[m][n] = out( sum_g s[n][g] * sum_{k in g} a[m][k] * (q[n][k] - z[n][g]) ),  f32 accumulate
+//
+// with a = x / awq rounded once to the operand type (bf16, or e4m3 for the
+// fp8 variant) and C rounded to bf16.  The weights are never rounded: the
+// codes enter the matrix cores as exact small integers and the group's
+// zero-point and scale are applied in f32 to the group's partial sums.
+//
+// MI355X design (not the Metal kernel's structure):
+//  * A -- the activation -- goes through LDS; B -- the INT4 weights -- goes
+//    straight from memory into registers in the MFMA operand layout (lane =
+//    weight row + 16 x K quarter, one 16-byte load per lane per group and
+//    16-row fragment, the decode matvec's layout) and is expanded there, so a
+//    workgroup's weights never touch LDS and each is read once per workgroup.
+//  * bf16: a code byte q placed under the bf16 exponent byte 0x43 is the bf16
+//    value 128 + q exactly (one v_perm per two codes); the MFMA gives
+//    sum a (128 + q) and the group's correction subtracts (128 + z) sum a,
+//    with sum a the row's group sum of the rounded operand (exact products,
+//    f32 sums).  fp8: q is looked up as its e4m3 encoding (exact for 0..15)
+//    and the correction subtracts z sum a.  One v_mfma_f32_16x16x128_f8f6f4
+//    covers a whole group.
+//  * a prep kernel writes the operand rows (x / awq rounded, each 8-element
+//    chunk in the slot order the code unpack produces) and their group sums.
+//  * workgroup tile 64 (M) x 128 (bf16) or 256 (fp8) columns, four waves each
+//    owning a quarter of the columns; the
+//    next group's A (global -> registers -> other LDS buffer) and B (global ->
+//    registers) are loaded while the current group computes: one barrier per
+//    group.  K is split over workgroups when the tile grid is smaller than
+//    twice the CU count; the f32 partials are summed in split order by a
+//    second kernel (deterministic).
+#include <hip/hip_runtime.h>
+#include <hip/hip_fp16.h>
+
+#include <algorithm>
+#include <string>
+
+#include "dpp_reduce.h"
+#include "imh_internal.h"
+
+namespace {
+
+typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
+typedef int i32x8_t __attribute__((ext_vector_type(8)));
+typedef float float4_t __attribute__((ext_vector_type(4)));
+typedef float float2_t __attribute__((ext_vector_type(2)));
+typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
+
+constexpr int kGS = 128;
+constexpr int kBM = 64;          // workgroup rows (M)
+constexpr int kThreads = 256;    // 4 waves, each owning 16 x NJ columns
+// 16-column B fragments per wave: 2 for bf16 (its A fragments take 64
+// registers), 4 for fp8 (one f8f6f4 MFMA per group and fragment pair)
+template <int P> constexpr int frags_per_wave() { return 2; }
+template <int P> constexpr int wg_cols() { return 4 * 16 * frags_per_wave<P>(); }
+constexpr float kE4M3Max = 448.0f;
+
+enum Prec : int { PREC_BF16 = 1, PREC_FP8 = 2 };
+
+// e4m3 encodings of 0..7 (OCP E4M3: bias 7, 1.0 = 0x38); 8..15 are 0x48 + q
+constexpr uint32_t kE4m3Lo = 0x44403800u;   // e(3) e(2) e(1) e(0)
+constexpr uint32_t kE4m3Hi = 0x4E4C4A48u;   // e(7) e(6) e(5) e(4)
+
+// four codes (0..15, one per byte) -> their e4m3 encodings
+__device__ __forceinline__ uint32_t e4m3_of_codes(uint32_t q) {
+    const uint32_t small = __builtin_amdgcn_perm(kE4m3Hi, kE4m3Lo, q & 0x07070707u);
+    const uint32_t big = q + 0x48484848u;
+    // per byte 0xFF where q >= 8: v_perm selector 12 gives 0x00, 13 gives 0xFF
+    const uint32_t mask = __builtin_amdgcn_perm(0u, 0u, ((q >> 3) & 0x01010101u) + 0x0C0C0C0Cu);
+    return (big & mask) | (small & ~mask);
+}
+
+// grid (ceil(K / 8 / 256), M), block 256: chunk c (8 elements) of row m:
+// a = x / awq (no awq: x) rounded to the operand type, stored in slot order
+// {0, 2, 4, 6, 1, 3, 5, 7}; the 16 chunks of a group (16 consecutive lanes)
+// sum their rounded values into gsum[m][g].
+template <int P>
+__global__ void __launch_bounds__(256) gemm_mx_prep_kernel(const __bf16 *__restrict__ x,
+                                                           const __half *__restrict__ awq,
+                                                           uint8_t *__restrict__ aop, float *__restrict__ gsum,
+                                                           int K) {
+    const int m = blockIdx.y;
+    const int c_raw = blockIdx.x * blockDim.x + threadIdx.x;
+    const bool live = c_raw * 8 < K;
+    const int c = live ? c_raw : 0;
+    const size_t off = (size_t)m * K + (size_t)c * 8;
+    const u32x4_t xv = *reinterpret_cast<const u32x4_t *>(x + off);
+    const __bf16 *xb = reinterpret_cast<const __bf16 *>(&xv);
+    float v[8];
+#pragma unroll
+    for (int i = 0; i < 8; i++) v[i] = (float)xb[i];
+    if (awq) {
+        const u32x4_t wv = *reinterpret_cast<const u32x4_t *>(awq + (size_t)c * 8);
+        const _Float16 *wh = reinterpret_cast<const _Float16 *>(&wv);
+#pragma unroll
+        for (int i = 0; i < 8; i++) v[i] = v[i] / (float)wh[i];
+    }
+    constexpr int kSlot[8] = {0, 2, 4, 6, 1, 3, 5, 7};
+    float sum = 0.0f;
+    if (P == PREC_BF16) {
+        bf16x8_t o;
+#pragma unroll
+        for (int i = 0; i < 8; i++) {
+            o[i] = (__bf16)v[kSlot[i]];
+            sum += (float)o[i];
+        }
+        if (live) *reinterpret_cast<bf16x8_t *>(aop + off * 2) = o;
+    } else {
+        uint32_t w[2];
+#pragma unroll
+        for (int h = 0; h < 2; h++) {
+            float e[4];
+#pragma unroll
+            for (int i = 0; i < 4; i++) e[i] = fminf(fmaxf(v[kSlot[4 * h + i]], -kE4M3Max), kE4M3Max);
+            uint32_t p = __builtin_amdgcn_cvt_pk_fp8_f32(e[0], e[1], 0, false);
+            p = __builtin_amdgcn_cvt_pk_fp8_f32(e[2], e[3], p, true);
+            w[h] = p;
+            // the rounded values, back from the encoding
+            const float2_t r0 = __builtin_amdgcn_cvt_pk_f32_fp8(p, false);
+            const float2_t r1 = __builtin_amdgcn_cvt_pk_f32_fp8(p, true);
+            sum += r0[0];
+            sum += r0[1];
+            sum += r1[0];
+            sum += r1[1];
+        }
+        if (live) *reinterpret_cast<uint2 *>(aop + off) = make_uint2(w[0], w[1]);
+    }
+    sum = imh_dpp::row16_sum(sum);
+    if (live && (threadIdx.x & 15) == 0) gsum[(size_t)m * (K / kGS) + (size_t)c / 16] = sum;
+}
+
+// Tile order.  Workgroup ids go round-robin over the 8 XCDs, each with its
+// own L2, so the linear id is first turned into an index that is contiguous
+// per XCD; that index then walks bands of `band` row tiles (M) with the row
+// tile fastest, so the workgroups resident on one XCD share both their A rows
+// (one band) and their B columns (neighbouring column tiles) in its L2.
+struct TileOrder {
+    int tiles_m, tiles_n, band, splits;
+};
+__device__ __forceinline__ void tile_of(const TileOrder &o, int &mt, int &nt, int &split) {
+    const int T = o.tiles_m * o.tiles_n * o.splits;
+    const int L = blockIdx.x;
+    const int x = L & 7, j = L >> 3;
+    const int q = T >> 3, r = T & 7;
+    const int t = x * q + min(x, r) + j;             // contiguous per XCD
+    const int per_split = o.tiles_m * o.tiles_n;
+    split = t / per_split;
+    const int u = t - split * per_split;
+    const int per_band = o.band * o.tiles_n;
+    const int b = u / per_band, v = u - b * per_band;
+    mt = b * o.band + v % o.band;
+    nt = v / o.band;
+}
+
+// grid (tiles_m * tiles_n * splits), block 256; tile (mt, nt, split) from
+// tile_of.  Split z covers groups [z * per, min((z + 1) * per, G)).  Without a
+// split C is stored as bf16; with one the f32 partials go to part[z][M][N].
+template <int P>
+__global__ void __launch_bounds__(kThreads, 2) gemm_mx_kernel(
+    const uint8_t *__restrict__ aop, const float *__restrict__ gsum, const uint8_t *__restrict__ wdata,
+    const __half *__restrict__ scales, const __half *__restrict__ zeros, __bf16 *__restrict__ out,
+    float *__restrict__ part, int M, int N, int K, int per, TileOrder order) {
+    constexpr int EB = P == PREC_BF16 ? 2 : 1;     // operand bytes per element
+    constexpr int RB = kGS * EB + 16;              // LDS row bytes of one group (16-byte pad)
+    constexpr int ACH = kBM * kGS * EB / 16 / kThreads;   // 16-byte A chunks per thread per group
+    constexpr int NJ = frags_per_wave<P>();
+    __shared__ __attribute__((aligned(16))) uint8_t As[2][kBM * RB];
+    __shared__ __attribute__((aligned(16))) float Gs[2][kBM];
+
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int wave = tid >> 6;
+    const int n_l = lane & 15, kq = lane >> 4;
+    int mt, nt, split;
+    tile_of(order, mt, nt, split);
+    const int m0 = mt * kBM;
+    const int n0 = nt * wg_cols<P>() + wave * 16 * NJ;
+    const int G = K / kGS;
+    const int g_begin = split * per;
+    const int g_end = min(g_begin + per, G);
+
+    // B rows of this lane: fragment j holds row n0 + 16 j + n_l (clamped)
+    const uint8_t *brow[NJ];
+    size_t szrow[NJ];
+#pragma unroll
+    for (int j = 0; j < NJ; j++) {
+        const int n = min(n0 + 16 * j + n_l, N - 1);
+        brow[j] = wdata + (size_t)n * (K / 2) + kq * 16;
+        szrow[j] = (size_t)n * G;
+    }
+    // A staging: chunk c = i * 256 + tid of the group's 64 x (128 * EB) bytes
+    auto load_a = [&](int g, u32x4_t *ar, float &gs) __attribute__((always_inline)) {
+#pragma unroll
+        for (int i = 0; i < ACH; i++) {
+            const int c = i * kThreads + tid;
+            const int r = c / (kGS * EB / 16), cc = c - r * (kGS * EB / 16);
+            const int m = min(m0 + r, M - 1);
+            ar[i] = *reinterpret_cast<const u32x4_t *>(aop + ((size_t)m * K + (size_t)g * kGS) * EB + cc * 16);
+        }
+        gs = tid < kBM ? gsum[(size_t)min(m0 + tid, M - 1) * G + g] : 0.0f;
+    };
+    auto store_a = [&](int buf, const u32x4_t *ar, float gs) __attribute__((always_inline)) {
+#pragma unroll
+        for (int i = 0; i < ACH; i++) {
+            const int c = i * kThreads + tid;
+            const int r = c / (kGS * EB / 16), cc = c - r * (kGS * EB / 16);
+            *reinterpret_cast<u32x4_t *>(&As[buf][r * RB + cc * 16]) = ar[i];
+        }
+        if (tid < kBM) Gs[buf][tid] = gs;
+    };
+    // B codes, scales and zero-points of group g; the scale and zero stay
+    // apart until used, so nothing waits for these loads before the next group
+    struct BRegs {
+        u32x4_t w[NJ];
+        uint16_t s[NJ], z[NJ];
+    };
+    auto load_b = [&](int g, BRegs &b) __attribute__((always_inline)) {
+#pragma unroll
+        for (int j = 0; j < NJ; j++) {
+            b.w[j] = *reinterpret_cast<const u32x4_t *>(brow[j] + (size_t)g * 64);
+            b.s[j] = reinterpret_cast<const uint16_t *>(scales)[szrow[j] + g];
+            b.z[j] = reinterpret_cast<const uint16_t *>(zeros)[szrow[j] + g];
+        }
+    };
+
+    float4_t acc[4][NJ];
+#pragma unroll
+    for (int i = 0; i < 4; i++)
+#pragma unroll
+        for (int j = 0; j < NJ; j++) acc[i][j] = (float4_t){0.0f, 0.0f, 0.0f, 0.0f};
+
+    // One group: B fragment j expanded from its 16 code bytes, A fragment i
+    // (rows 16 i .. 16 i + 15) from LDS, the group's sums folded into acc with
+    // the scale and zero-point of column n_l of fragment j.
+    auto compute = [&](int buf, const BRegs &b) __attribute__((always_inline)) {
+        // D rows of this lane: 4 kq + r of each fragment; their group sums
+        float4_t rs[4];
+#pragma unroll
+        for (int i = 0; i < 4; i++) rs[i] = *reinterpret_cast<const float4_t *>(&Gs[buf][16 * i + 4 * kq]);
+        if (P == PREC_BF16) {
+#pragma unroll
+            for (int j = 0; j < NJ; j++) {
+                bf16x8_t bf[4];
+#pragma unroll
+                for (int ks = 0; ks < 4; ks++) {
+                    const uint32_t w = b.w[j][ks];
+                    const uint32_t lo = w & 0x0F0F0F0Fu, hi = (w >> 4) & 0x0F0F0F0Fu;
+                    const u32x4_t o = {__builtin_amdgcn_perm(lo, 0x43434343u, 0x00050004u),
+                                       __builtin_amdgcn_perm(lo, 0x43434343u, 0x00070006u),
+                                       __builtin_amdgcn_perm(hi, 0x43434343u, 0x00050004u),
+                                       __builtin_amdgcn_perm(hi, 0x43434343u, 0x00070006u)};
+                    bf[ks] = __builtin_bit_cast(bf16x8_t, o);
+                }
+                const float s = (float)__builtin_bit_cast(_Float16, b.s[j]);
+                const float cz = 128.0f + (float)__builtin_bit_cast(_Float16, b.z[j]);
+#pragma unroll
+                for (int i = 0; i < 4; i++) {
+                    // 8 elements of row 16 i + n_l at k = 32 kq + 8 ks (re-read per fragment j:
+                    // holding all of them would cost 64 registers and occupancy)
+                    bf16x8_t af[4];
+#pragma unroll
+                    for (int ks = 0; ks < 4; ks++)
+                        af[ks] = *reinterpret_cast<const bf16x8_t *>(&As[buf][(16 * i + n_l) * RB + (32 * kq + 8 * ks) * 2]);
+                    float4_t g = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+                    for (int ks = 0; ks < 4; ks++) g = __builtin_amdgcn_mfma_f32_16x16x32_bf16(af[ks], bf[ks], g, 0, 0, 0);
+#pragma unroll
+                    for (int r = 0; r < 4; r++) acc[i][j][r] = __builtin_fmaf(s, __builtin_fmaf(-cz, rs[i][r], g[r]), acc[i][j][r]);
+                }
+            }
+        } else {
+            i32x8_t af[4];   // [i]: 32 e4m3 bytes of row 16 i + n_l at k = 32 kq ..
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+                const uint8_t *p = &As[buf][(16 * i + n_l) * RB + 32 * kq];
+                const u32x4_t a0 = *reinterpret_cast<const u32x4_t *>(p);
+                const u32x4_t a1 = *reinterpret_cast<const u32x4_t *>(p + 16);
+                af[i] = (i32x8_t){(int)a0[0], (int)a0[1], (int)a0[2], (int)a0[3],
+                                  (int)a1[0], (int)a1[1], (int)a1[2], (int)a1[3]};
+            }
+#pragma unroll
+            for (int j = 0; j < NJ; j++) {
+                // code dword ks = codes 8 ks .. 8 ks + 7 -> e4m3 of the even codes, then the odd
+                i32x8_t bf;
+#pragma unroll
+                for (int ks = 0; ks < 4; ks++) {
+                    const uint32_t w = b.w[j][ks];
+                    bf[2 * ks] = (int)e4m3_of_codes(w & 0x0F0F0F0Fu);
+                    bf[2 * ks + 1] = (int)e4m3_of_codes((w >> 4) & 0x0F0F0F0Fu);
+                }
+                const float s = (float)__builtin_bit_cast(_Float16, b.s[j]);
+                const float z = (float)__builtin_bit_cast(_Float16, b.z[j]);
+#pragma unroll
+                for (int i = 0; i < 4; i++) {
+                    const float4_t zero = {0.0f, 0.0f, 0.0f, 0.0f};
+                    // formats 0 / 0: e4m3 x e4m3; scale exponents 127: x1
+                    const float4_t g = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(af[i], bf, zero, 0, 0, 0,
+                                                                                         0x7F7F7F7F, 0, 0x7F7F7F7F);
+#pragma unroll
+                    for (int r = 0; r < 4; r++) acc[i][j][r] = __builtin_fmaf(s, __builtin_fmaf(-z, rs[i][r], g[r]), acc[i][j][r]);
+                }
+            }
+        }
+    };
+
+    // Ping-pong over two B register sets (no copies between iterations): a
+    // group computes from LDS buffer buf and set `cur` while the next group's
+    // A (registers, stored to the other buffer after the MFMAs) and B (the
+    // other set) are in flight.
+    u32x4_t ar[ACH];
+    BRegs b0, b1;
+    float gsv = 0.0f;
+    if (g_begin < g_end) {
+        load_a(g_begin, ar, gsv);
+        load_b(g_begin, b0);
+        store_a(0, ar, gsv);
+        __syncthreads();
+    }
+    auto step = [&](int g, int buf, const BRegs &cur, BRegs &nxt) __attribute__((always_inline)) {
+        const bool more = g + 1 < g_end;
+        if (more) {
+            load_a(g + 1, ar, gsv);
+            load_b(g + 1, nxt);
+        }
+        compute(buf, cur);
+        if (more) store_a(buf ^ 1, ar, gsv);
+        __syncthreads();
+    };
+    for (int g = g_begin; g < g_end; g += 2) {
+        step(g, 0, b0, b1);
+        if (g + 1 < g_end) step(g + 1, 1, b1, b0);
+    }
+
+    // D of fragment (i, j): lane holds rows 16 i + 4 kq + r, column 16 j + n_l
+#pragma unroll
+    for (int j = 0; j < NJ; j++) {
+        const int n = n0 + 16 * j + n_l;
+        if (n >= N) continue;
+#pragma unroll
+        for (int i = 0; i < 4; i++)
+#pragma unroll
+            for (int r = 0; r < 4; r++) {
+                const int m = m0 + 16 * i + 4 * kq + r;
+                if (m >= M) continue;
+                if (part) part[((size_t)split * M + m) * N + n] = acc[i][j][r];
+                else out[(size_t)m * N + n] = (__bf16)acc[i][j][r];
+            }
+    }
+}
+
+// Sums the split partials in split order: grid ceil(M * N / 256), block 256.
+__global__ void __launch_bounds__(256) gemm_mx_reduce_kernel(const float *__restrict__ part, int splits, size_t count,
+                                                             __bf16 *__restrict__ out) {
+    const size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= count) return;
+    float s = part[i];
+    for (int z = 1; z < splits; z++) s += part[(size_t)z * count + i];
+    out[i] = (__bf16)s;
+}
+
+int check_gemm_weight(const imh_affine_int4_weight *w, const char *who) {
+    if (!w || !w->data || !w->scales || !w->zeros)
+        return imh::fail(IMH_EINVAL, std::string(who) + ": weight or one of its arrays is NULL");
+    if (w->group_size != kGS)
+        return imh::fail(IMH_EUNSUPPORTED, std::string(who) + ": group_size " + std::to_string(w->group_size) +
+                                               " not supported (built for 128)");
+    if (w->n == 0 || w->k == 0 || w->k % kGS)
+        return imh::fail(IMH_EUNSUPPORTED, std::string(who) + ": k must be a non-zero multiple of 128, n non-zero");
+    if ((reinterpret_cast<uintptr_t>(w->data) & 15) != 0)
+        return imh::fail(IMH_EINVAL, std::string(who) + ": weight data must be 16-byte aligned");
+    return IMH_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+int imh_affine_gemm_int4(imh_stream *stream, const void *x, uint32_t M, const imh_affine_int4_weight *w, void *y,
+                         int precision) {
+    const char *who = "imh_affine_gemm_int4";
+    if (!stream || !x || !y) return imh::fail(IMH_EINVAL, std::string(who) + ": NULL argument");
+    int rc = check_gemm_weight(w, who);
+    if (rc) return rc;
+    if (precision == IMH_GEMM_F16) {
+        // the f16 path is the projection op (matvec below 32 tokens, f16 GEMM from 32)
+        return imh_encode_affine_projection_int4(stream, static_cast<const uint16_t *>(x), M, w,
+                                                 static_cast<uint16_t *>(y));
+    }
+    if (precision != IMH_GEMM_BF16 && precision != IMH_GEMM_FP8_E4M3)
+        return imh::fail(IMH_EINVAL, std::string(who) + ": unknown precision " + std::to_string(precision));
+    if ((reinterpret_cast<uintptr_t>(x) & 15) || (w->awq_scales && (reinterpret_cast<uintptr_t>(w->awq_scales) & 15)))
+        return imh::fail(IMH_EINVAL, std::string(who) + ": x and awq_scales must be 16-byte aligned");
+    if (M == 0) return IMH_OK;
+    if (M > 65535u) return imh::fail(IMH_EINVAL, std::string(who) + ": M above 65535");
+    rc = imh::use_device(stream->dev);
+    if (rc) return rc;
+    const int N = (int)w->n, K = (int)w->k, G = K / kGS;
+    const int P = precision == IMH_GEMM_BF16 ? PREC_BF16 : PREC_FP8;
+    const int eb = P == PREC_BF16 ? 2 : 1;
+    // K split: about two workgroups per CU, at least 4 groups per split
+    const int cus = stream->dev->props.multiProcessorCount;
+    const int wgc = P == PREC_BF16 ? wg_cols<PREC_BF16>() : wg_cols<PREC_FP8>();
+    const int tiles = ((N + wgc - 1) / wgc) * (((int)M + kBM - 1) / kBM);
+    int splits = 1;
+    if (tiles < 2 * cus) splits = std::max(1, std::min((2 * cus + tiles - 1) / tiles, G / 4));
+    const int per = (G + splits - 1) / splits;
+    splits = (G + per - 1) / per;
+    // scratch slot 0: operand rows + group sums; slot 2: split partials
+    const size_t a_bytes = ((size_t)M * K * eb + 255) / 256 * 256;
+    void *scr = nullptr;
+    rc = imh::stream_scratch(stream, 0, a_bytes + (size_t)M * G * sizeof(float), &scr);
+    if (rc) return rc;
+    uint8_t *aop = static_cast<uint8_t *>(scr);
+    float *gsum = reinterpret_cast<float *>(aop + a_bytes);
+    float *part = nullptr;
+    if (splits > 1) {
+        void *p = nullptr;
+        rc = imh::stream_scratch(stream, 2, (size_t)splits * M * N * sizeof(float), &p);
+        if (rc) return rc;
+        part = static_cast<float *>(p);
+    }
+    const __bf16 *xb = static_cast<const __bf16 *>(x);
+    const __half *awq = reinterpret_cast<const __half *>(w->awq_scales);
+    dim3 pgrid((K / 8 + 255) / 256, M);
+    if (P == PREC_BF16)
+        hipLaunchKernelGGL(gemm_mx_prep_kernel<PREC_BF16>, pgrid, dim3(256), 0, stream->stream, xb, awq, aop, gsum, K);
+    else
+        hipLaunchKernelGGL(gemm_mx_prep_kernel<PREC_FP8>, pgrid, dim3(256), 0, stream->stream, xb, awq, aop, gsum, K);
+    IMH_HIP(hipGetLastError());
+    TileOrder order;
+    order.tiles_m = ((int)M + kBM - 1) / kBM;
+    order.tiles_n = (N + wgc - 1) / wgc;
+    order.splits = splits;
+    // band: the largest divisor of tiles_m that is at most tiles_m / 8 (so
+    // each XCD gets about one band), at least 1
+    order.band = 1;
+    for (int b = std::max(1, order.tiles_m / 8); b >= 1; b--)
+        if (order.tiles_m % b == 0) {
+            order.band = b;
+            break;
+        }
+    dim3 grid((unsigned)order.tiles_m * order.tiles_n * splits);
+    const __half *sc = reinterpret_cast<const __half *>(w->scales), *zr = reinterpret_cast<const __half *>(w->zeros);
+    __bf16 *out = static_cast<__bf16 *>(y);
+    if (P == PREC_BF16)
+        hipLaunchKernelGGL(gemm_mx_kernel<PREC_BF16>, grid, dim3(kThreads), 0, stream->stream, aop, gsum, w->data, sc, zr,
+                           out, part, (int)M, N, K, per, order);
+    else
+        hipLaunchKernelGGL(gemm_mx_kernel<PREC_FP8>, grid, dim3(kThreads), 0, stream->stream, aop, gsum, w->data, sc, zr,
+                           out, part, (int)M, N, K, per, order);
+    IMH_HIP(hipGetLastError());
+    if (splits > 1) {
+        const size_t count = (size_t)M * N;
+        hipLaunchKernelGGL(gemm_mx_reduce_kernel, dim3((unsigned)((count + 255) / 256)), dim3(256), 0, stream->stream,
+                           part, splits, count, out);
+        IMH_HIP(hipGetLastError());
+    }
+    return IMH_OK;
+}
+
+}  // extern "C"

@@ -60,6 +60,17 @@ def encode_projection(stream: Stream, x, weight: AffineQuantizedWeight, y, token
                                                 C.byref(weight.c), _ptr(y)))
 
 
+GEMM_F16, GEMM_BF16, GEMM_FP8_E4M3 = 0, 1, 2
+
+
+def encode_affine_gemm_int4(stream: Stream, x, token_count: int, weight: AffineQuantizedWeight, y,
+                            precision: int = GEMM_BF16):
+    """superblock_matmul_int4 (affine_matmul.metal:10-152) at a chosen matrix-core precision:
+    GEMM_F16 (x, y f16: the projection op), GEMM_BF16 (x, y bf16) or GEMM_FP8_E4M3 (x, y bf16,
+    x / awq rounded to e4m3).  bf16 data travels as uint16 bit patterns."""
+    check(lib.imh_affine_gemm_int4(stream.handle, _ptr(x), token_count, C.byref(weight.c), _ptr(y), precision))
+
+
 def encode_batched_affine_matvec_int4(stream: Stream, x, gate: AffineQuantizedWeight, gate_out,
                                       up: AffineQuantizedWeight, up_out, token_count: int = 1):
     """ops/quantized.rs:198-232."""
@@ -413,7 +424,8 @@ class Decoder:
 
 
 __all__ = [
-    "AffineQuantizedWeight", "encode_projection", "encode_batched_affine_matvec_int4",
+    "AffineQuantizedWeight", "encode_projection", "encode_affine_gemm_int4", "GEMM_F16", "GEMM_BF16",
+    "GEMM_FP8_E4M3", "encode_batched_affine_matvec_int4",
     "encode_fused_ffn_gate_up_act_int4", "encode_fused_residual_norm_affine_matvec_int4",
     "TurboQuantModel", "TurboQuantKvCache", "encode_turboquant_cache_write", "encode_turboquant_cache_write_kv",
     "encode_turboquant_attention", "encode_kv_cache_and_attention", "Fp16KvCache", "encode_kv_scatter",

@@ -165,6 +165,26 @@ def dequant_affine_int4_f16params(packed, scales16, zeros16, n, k, gs=128) -> np
     return out.view(np.float16)
 
 
+def bf16_round(x) -> np.ndarray:
+    """IEEE f32 -> bfloat16 with round-to-nearest-even, as uint16 bit patterns (finite inputs)."""
+    b = np.ascontiguousarray(x, np.float32).view(np.uint32).astype(np.uint64)
+    b = (b + 0x7FFF + ((b >> 16) & 1)) >> 16
+    return b.astype(np.uint16)
+
+
+def bf16_to_f32(bits) -> np.ndarray:
+    return (np.asarray(bits, np.uint16).astype(np.uint32) << 16).view(np.float32)
+
+
+def e4m3_round(x) -> np.ndarray:
+    """OCP FP8 E4M3 (bias 7, 3 mantissa bits, subnormal quantum 2^-9, largest finite 448):
+    f32 -> the nearest e4m3 value (ties to even), saturating at +-448, returned as f32."""
+    v = np.clip(np.asarray(x, np.float32).astype(np.float64), -448.0, 448.0)
+    _, e = np.frexp(v)                        # v = m 2^e, 0.5 <= |m| < 1
+    q = np.exp2(np.maximum(e - 4, -9))        # spacing of the binade (subnormal below 2^-6)
+    return (np.rint(v / q) * q).astype(np.float32)
+
+
 def matvec_f16w(w16, x16, awq16=None, nthreads=1) -> np.ndarray:
     """y[b, n] = sum_k (x[b,k] (/ awq[k])) * W[n,k], f32 accumulate -> f32 [B, N]."""
     w = _c(w16, np.float16).view(np.uint16)

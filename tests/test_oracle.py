@@ -639,3 +639,34 @@ def test_tq_index_rule_prefix_max_equals_scan(tabs):
         pos[np.isnan(u)] = 0
         fast = np.where(pos == 0, 0, pm[np.maximum(pos - 1, 0)])
         assert np.array_equal(scan, fast)
+
+
+# ------------------------------------------------- operand roundings of the bf16 / fp8 GEMM
+
+def test_bf16_round_matches_torch():
+    """bf16 RNE pinned by torch's float32 -> bfloat16 conversion (a library routine)."""
+    import torch
+    rng = np.random.default_rng(21)
+    x = np.concatenate([rng.standard_normal(100000).astype(np.float32) * 10.0 ** rng.integers(-8, 8, 100000),
+                        np.array([1.0, -1.0, 0.0, 1.00390625, 1.01171875, 65504.0], np.float32)])
+    want = torch.from_numpy(x).to(torch.bfloat16).view(torch.int16).numpy().view(np.uint16)
+    assert np.array_equal(O.bf16_round(x), want)
+    assert np.array_equal(O.bf16_to_f32(O.bf16_round(x)), torch.from_numpy(x).to(torch.bfloat16).float().numpy())
+
+
+def test_e4m3_round_matches_torch_and_closed_forms():
+    """OCP e4m3 rounding pinned by torch's float8_e4m3fn conversion on in-range values, and by
+    the format's fixed points: the integers 0..15 are exact (the GEMM's code operand), 448 is
+    the largest value, 2^-9 the smallest subnormal, and values beyond +-448 saturate."""
+    import torch
+    rng = np.random.default_rng(22)
+    x = (rng.standard_normal(200000) * 10.0 ** rng.uniform(-3, 2.5, 200000)).astype(np.float32)
+    x = np.clip(x, -448.0, 448.0)
+    want = torch.from_numpy(x).to(torch.float8_e4m3fn).float().numpy()
+    assert np.array_equal(O.e4m3_round(x), want)
+    ints = np.arange(-15, 16, dtype=np.float32)
+    assert np.array_equal(O.e4m3_round(ints), ints)
+    assert O.e4m3_round(np.float32(1e6)) == 448.0 and O.e4m3_round(np.float32(-500.0)) == -448.0
+    assert O.e4m3_round(np.float32(2.0 ** -9)) == 2.0 ** -9
+    assert O.e4m3_round(np.float32(2.0 ** -11)) == 0.0     # below half the smallest subnormal
+    assert O.e4m3_round(np.float32(17.0)) == 16.0 and O.e4m3_round(np.float32(19.0)) == 20.0   # ties to even
