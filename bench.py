@@ -351,7 +351,8 @@ def main():
         return
     if args.gpus != 1:
         print(f"bench.py: this build measures one GPU; --gpus {args.gpus} is not supported "
-              "(the hot path has no multi-GPU code, see DESIGN.md for how it would shard)",
+              "(the hot path has no multi-GPU code: each GPU would hold its own column shard of "
+              "every projection and its own heads of the KV cache)",
               file=sys.stderr)
         sys.exit(2)
 

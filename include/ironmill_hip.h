@@ -193,6 +193,44 @@ int imh_encode_ffn_block_int4(imh_stream *stream, const uint16_t *x, uint32_t to
 int imh_affine_gemm_int4(imh_stream *stream, const void *x, uint32_t M, const imh_affine_int4_weight *w,
                          void *y, int precision);
 
+/* INT8 "sensitive-layer" weight (quantize_tensor_int8, quantized.rs:852-901;
+ * uploaded like the INT4 weight, metal/weights.rs:1036-1114): data [n][k] code
+ * bytes 0..255, scales / zeros [n][k/128] f16 (raw zero-points), awq [k] f16
+ * or NULL.  group_size must be 128. */
+typedef struct {
+    const uint8_t *data;
+    const uint16_t *scales;
+    const uint16_t *zeros;
+    const uint16_t *awq_scales;
+    uint32_t n;
+    uint32_t k;
+    uint32_t group_size;
+} imh_affine_int8_weight;
+
+/* superblock_matvec_int8 (affine_matvec.metal:123-189) for token_count rows:
+ * y[t][r] = f16( sum_k (x[t][k] / awq[k]) * (q[r][k] - z) * s ), f32 accumulate.
+ * x [token_count][k] f16, y [token_count][n] f16. */
+int imh_encode_affine_projection_int8(imh_stream *stream, const uint16_t *x, uint32_t token_count,
+                                      const imh_affine_int8_weight *w, uint16_t *y);
+
+/* quantize_input_q8 (quantize.metal:21-52), per 128-element group of each row:
+ * scale = absmax / 127, q = clamp(rint(x * (127 / absmax)), -127, 127) (0 for
+ * an all-zero group).  x [token_count][k] f16 -> q8 [token_count][k] int8,
+ * q8_scales [token_count][k/128] f32.  (The reference reduces the absmax per
+ * 32-lane simdgroup while storing one scale per group; this is the per-group
+ * rule it states.) */
+int imh_encode_quantize_input_q8(imh_stream *stream, const uint16_t *x, uint32_t token_count, uint32_t k,
+                                 int8_t *q8, float *q8_scales);
+
+/* superblock_affine_matvec_int4xq8 (affine_fused.metal:115-176), the decode
+ * variant on Q8 activations (pipeline.rs:639-664, projection.rs:123-143):
+ * y[t][r] = f16( sum_g ws * as[t][g] * sum_{k in g} q8[t][k] * (q[r][k] - rint(z)) ),
+ * on the integer matrix cores (each group's sum exact in int32).  The Q8
+ * group is the weight group (128); w->awq_scales must be NULL (the reference
+ * takes this path only without AWQ). */
+int imh_encode_affine_matvec_int4xq8(imh_stream *stream, const int8_t *q8, const float *q8_scales,
+                                     uint32_t token_count, const imh_affine_int4_weight *w, uint16_t *y);
+
 /* FusedResidualNormAffineInt4Params (ops/fused.rs:45-66) with a token count. */
 typedef struct {
     const uint16_t *a;           /* [token_count][k] */

@@ -64,6 +64,12 @@ class AffineInt4Weight(C.Structure):
     ]
 
 
+class AffineInt8Weight(C.Structure):
+    """imh_affine_int8_weight (the INT8 weight, quantized.rs:852-901)."""
+
+    _fields_ = AffineInt4Weight._fields_
+
+
 class FusedResidualNormParams(C.Structure):
     """imh_fused_residual_norm_params (FusedResidualNormAffineInt4Params, ops/fused.rs:45-66)."""
 
@@ -218,6 +224,9 @@ SIGNATURES = {
     "imh_encode_ffn_block_int4": (I, [P, P, U32, C.POINTER(AffineInt4Weight), C.POINTER(AffineInt4Weight),
                                       C.POINTER(AffineInt4Weight), P, P, I]),
     "imh_affine_gemm_int4": (I, [P, P, U32, C.POINTER(AffineInt4Weight), P, I]),
+    "imh_encode_affine_projection_int8": (I, [P, P, U32, C.POINTER(AffineInt8Weight), P]),
+    "imh_encode_quantize_input_q8": (I, [P, P, U32, U32, P, P]),
+    "imh_encode_affine_matvec_int4xq8": (I, [P, P, P, U32, C.POINTER(AffineInt4Weight), P]),
     "imh_encode_fused_residual_norm_affine_matvec_int4": (I, [P, C.POINTER(FusedResidualNormParams)]),
     "imh_tq_tables_create": (I, [P, U32, U32, C.c_uint64, C.POINTER(P)]),
     "imh_tq_tables_create_from_host": (I, [P, U32, U32, P, P, P, P, P, P, C.POINTER(P)]),

@@ -1,0 +1,387 @@
+// int8_matvec.hip -- the INT8 "sensitive-layer" weight matvec and the
+// INT4 x Q8 decode variant:
+//
+//  * INT8 weights (superblock_matvec_int8, affine_matvec.metal:123-189, over
+//    quantize_tensor_int8, quantized.rs:852-901): codes [N][K] bytes 0..255,
+//    f16 scales / zero-points per 128-group,
+//        y[m][n] = f16( sum_g s * sum_{k in g} (x[m][k] / awq[k]) * (q - z) ).
+//    The matrix cores multiply the raw code bytes as f16 denormals (byte *
+//    2^-24, exact) against the activation split into f16 hi + lo (~22 bits);
+//    zero-point and scale are applied in f32 per group to the group sums, as
+//    in the INT4 matvec.
+//  * INT4 x Q8 (superblock_affine_matvec_int4xq8, affine_fused.metal:115-176,
+//    with quantize_input_q8, quantize.metal:21-52): the activation is first
+//    quantized to int8 per 128-group (scale = absmax / 127, q = rint(x * 127 /
+//    absmax) clamped to +-127), then
+//        y[m][n] = f16( sum_g ws * as * sum_{k in g} q8 * (q - rint(z)) ).
+//    On MI355X the group's dot product runs on the integer matrix cores
+//    (v_mfma_i32_16x16x64_i8): exact in int32, sum q8 q minus z sum q8, the
+//    two scales applied in f32.
+//
+// Both kernels: one workgroup per 16 weight rows, waves splitting the K
+// groups of each stage, the activation staged in LDS per stage (all of K when
+// it fits), each wave's weights loaded into registers before the staging so
+// they are in flight meanwhile; wave partials reduced through LDS in a fixed
+// order (deterministic).
+#include <hip/hip_runtime.h>
+#include <hip/hip_fp16.h>
+
+#include <algorithm>
+#include <string>
+
+#include "dpp_reduce.h"
+#include "imh_internal.h"
+
+namespace {
+
+typedef _Float16 half8_t __attribute__((ext_vector_type(8)));
+typedef float float4_t __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
+typedef int i32x4_t __attribute__((ext_vector_type(4)));
+
+constexpr int kGS = 128;
+constexpr int kMaxWaves = 8;
+constexpr int kNG = 8;                    // groups one wave holds per stage
+constexpr int kStageBytes = 48 * 1024;    // LDS for one stage's activation
+constexpr float kTwoM24 = 5.9604644775390625e-08f;
+constexpr float kTwo24 = 16777216.0f;
+
+// ---------------------------------------------------------------------------
+// INT8 weights x f16 activations
+// ---------------------------------------------------------------------------
+// grid (ceil(N / 16)), block 64 * waves; B <= 8 batch rows.  LDS: hi [B][SG *
+// 128] f16, lo [B][SG * 128] f16, group sums [SG][16] (A rows: hi sums of the
+// B rows, then lo sums, prescaled by 2^-24), then the wave partials.
+__global__ void __launch_bounds__(64 * kMaxWaves) int8w_matvec_kernel(
+    const __half *__restrict__ x, const __half *__restrict__ awq, const uint8_t *__restrict__ w,
+    const __half *__restrict__ scales, const __half *__restrict__ zeros, __half *__restrict__ y, int N, int K, int B,
+    int SG) {
+    extern __shared__ __attribute__((aligned(16))) uint8_t lds8[];
+    const int tid = threadIdx.x, nthr = blockDim.x;
+    const int lane = tid & 63, wave = tid >> 6, waves = nthr >> 6;
+    const int n_l = lane & 15, kq = lane >> 4;
+    const int G = K / kGS;
+    const int row0 = blockIdx.x * 16;
+    const int row = row0 + n_l;
+    const int row_c = min(row, N - 1);
+    const int RS = SG * kGS + 8;                         // LDS row stride (halfs), 16-byte pad
+    _Float16 *img = reinterpret_cast<_Float16 *>(lds8);  // hi rows, then lo rows
+    float *gsx = reinterpret_cast<float *>(lds8 + (size_t)2 * B * RS * 2);
+    // A row of this lane: plane n_l >> 3, batch row (n_l & 7) (rows past B reuse row 0)
+    const int ab = (n_l & 7) < B ? (n_l & 7) : 0;
+    const int arow = (n_l >> 3) * B + ab;
+
+    float4_t acc = {0.0f, 0.0f, 0.0f, 0.0f};
+    for (int s0 = 0; s0 < G; s0 += SG) {
+        const int SGs = min(SG, G - s0);
+        // (a) this wave's weights for its share of the stage's groups
+        const int g0 = s0 + (wave * SGs) / waves;
+        const int ng = s0 + ((wave + 1) * SGs) / waves - g0;
+        u32x4_t wq[kNG][2];
+#pragma unroll
+        for (int i = 0; i < kNG; i++) {
+            const int g = min(g0 + min(i, max(ng - 1, 0)), G - 1);
+            const uint8_t *p = w + (size_t)row_c * K + (size_t)g * kGS + kq * 32;
+            wq[i][0] = *reinterpret_cast<const u32x4_t *>(p);
+            wq[i][1] = *reinterpret_cast<const u32x4_t *>(p + 16);
+        }
+        // (b) the stage's activation image: chunk c (8 elements) of batch row b
+        const int cpr = SGs * 16;
+        for (int c = tid; c < B * cpr + (16 - (B * cpr) % 16) % 16; c += nthr) {
+            const bool live = c < B * cpr;
+            const int cc = live ? c : 0;
+            const int b = cc / cpr, ci = cc - b * cpr;
+            const size_t k = (size_t)s0 * kGS + (size_t)ci * 8;
+            const u32x4_t xv = *reinterpret_cast<const u32x4_t *>(x + (size_t)b * K + k);
+            const _Float16 *xh = reinterpret_cast<const _Float16 *>(&xv);
+            float v[8];
+#pragma unroll
+            for (int i = 0; i < 8; i++) v[i] = (float)xh[i];
+            if (awq) {
+                const u32x4_t av = *reinterpret_cast<const u32x4_t *>(awq + k);
+                const _Float16 *ah = reinterpret_cast<const _Float16 *>(&av);
+#pragma unroll
+                for (int i = 0; i < 8; i++) v[i] = v[i] * __builtin_amdgcn_rcpf((float)ah[i]);
+            }
+            half8_t hi, lo;
+            float sh = 0.0f, sl = 0.0f;
+#pragma unroll
+            for (int i = 0; i < 8; i++) {
+                hi[i] = (_Float16)v[i];
+                lo[i] = (_Float16)(v[i] - (float)hi[i]);
+                sh += (float)hi[i];
+                sl += (float)lo[i];
+            }
+            if (live) {
+                *reinterpret_cast<half8_t *>(img + (size_t)b * RS + ci * 8) = hi;
+                *reinterpret_cast<half8_t *>(img + (size_t)(B + b) * RS + ci * 8) = lo;
+            }
+            // the 16 chunks of a group are 16 consecutive lanes (cpr is a multiple of 16)
+            sh = imh_dpp::row16_sum(sh);
+            sl = imh_dpp::row16_sum(sl);
+            if (live && (tid & 15) == 0) {
+                const int g = ci / 16;
+                gsx[g * 16 + b] = sh * kTwoM24;
+                gsx[g * 16 + 8 + b] = sl * kTwoM24;
+            }
+        }
+        __syncthreads();
+        // (c) MFMA over the wave's groups: B = 8 code bytes of row n_l as f16
+        // denormals, A = 8 operand values of A row n_l (same k: 32 kq + 8 j)
+#pragma unroll
+        for (int i = 0; i < kNG; i++) {
+            if (i < ng) {
+                const int g = g0 + i;
+                const float s24 = __half2float(scales[(size_t)row_c * G + g]) * kTwo24;
+                const float z = __half2float(zeros[(size_t)row_c * G + g]);
+                const _Float16 *xa = img + (size_t)arow * RS + (g - s0) * kGS + kq * 32;
+                float4_t accg = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+                for (int j = 0; j < 4; j++) {
+                    const uint32_t w0 = wq[i][j >> 1][2 * (j & 1)], w1 = wq[i][j >> 1][2 * (j & 1) + 1];
+                    const u32x4_t bq = {__builtin_amdgcn_perm(0u, w0, 0x0C010C00u), __builtin_amdgcn_perm(0u, w0, 0x0C030C02u),
+                                        __builtin_amdgcn_perm(0u, w1, 0x0C010C00u), __builtin_amdgcn_perm(0u, w1, 0x0C030C02u)};
+                    const half8_t av = *reinterpret_cast<const half8_t *>(xa + j * 8);
+                    accg = __builtin_amdgcn_mfma_f32_16x16x32_f16(av, __builtin_bit_cast(half8_t, bq), accg, 0, 0, 0);
+                }
+                // D rows 4 kq + r: hi rows (< 8) and lo rows share the group's sums per A row
+                const float4_t sx = *reinterpret_cast<const float4_t *>(gsx + (g - s0) * 16 + 4 * kq);
+#pragma unroll
+                for (int r = 0; r < 4; r++) acc[r] = __builtin_fmaf(s24, __builtin_fmaf(-z, sx[r], accg[r]), acc[r]);
+            }
+        }
+        __syncthreads();
+    }
+    // reduce the waves (partials overlay the image), wave 0 stores: lane l < 32
+    // holds D rows 4 (l >> 4) + r (hi of batch rows), lane l + 32 the lo rows
+    float4_t *red = reinterpret_cast<float4_t *>(lds8);
+    red[wave * 64 + lane] = acc;
+    __syncthreads();
+    if (wave != 0 || lane >= 32 || row >= N) return;
+    float4_t s = red[lane] + red[lane + 32];
+    for (int wv = 1; wv < waves; wv++) s += red[wv * 64 + lane] + red[wv * 64 + lane + 32];
+#pragma unroll
+    for (int r = 0; r < 4; r++) {
+        const int b = 4 * (lane >> 4) + r;
+        if (b < B) y[(size_t)b * N + row] = __float2half(s[r]);
+    }
+}
+
+// ---------------------------------------------------------------------------
+// quantize_input_q8: grid (K / 128, B), block 128 (one thread per element)
+// ---------------------------------------------------------------------------
+__global__ void __launch_bounds__(kGS) q8_quantize_kernel(const __half *__restrict__ x, int8_t *__restrict__ q8,
+                                                          float *__restrict__ q8_scales, int K) {
+    __shared__ float wmax[2];
+    const int g = blockIdx.x, b = blockIdx.y, t = threadIdx.x;
+    const size_t i = (size_t)b * K + (size_t)g * kGS + t;
+    const float v = __half2float(x[i]);
+    float m = fabsf(v);
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) m = fmaxf(m, __shfl_xor(m, o));
+    if ((t & 63) == 0) wmax[t >> 6] = m;
+    __syncthreads();
+    m = fmaxf(wmax[0], wmax[1]);
+    const float scale = m / 127.0f;
+    const float inv = m > 0.0f ? 127.0f / m : 0.0f;
+    if (t == 0) q8_scales[(size_t)b * (K / kGS) + g] = scale;
+    q8[i] = (int8_t)fminf(fmaxf(rintf(v * inv), -127.0f), 127.0f);
+}
+
+// ---------------------------------------------------------------------------
+// INT4 weights x Q8 activations on the integer matrix cores
+// ---------------------------------------------------------------------------
+// grid (ceil(N / 16), ceil(B / 16)), block 64 * waves.  LDS per stage: q8
+// rows [16][SG * 128] (batch rows of the tile; rows past B read row 0), the
+// rows' group sums of q8 [SG][16] (int32) and scales [SG][16]; then partials.
+// Lane (n_l, kq) holds codes 32 kq .. 32 kq + 31 of its row's group (one
+// 16-byte load), MFMA j takes codes 32 kq + 16 j .. + 15 as int8 in natural
+// order, against the same 16 q8 bytes of A row n_l.
+__global__ void __launch_bounds__(64 * kMaxWaves) int4xq8_matvec_kernel(
+    const int8_t *__restrict__ q8, const float *__restrict__ q8_scales, const uint8_t *__restrict__ w,
+    const __half *__restrict__ scales, const __half *__restrict__ zeros, __half *__restrict__ y, int N, int K, int B,
+    int SG) {
+    extern __shared__ __attribute__((aligned(16))) uint8_t lds8[];
+    const int tid = threadIdx.x, nthr = blockDim.x;
+    const int lane = tid & 63, wave = tid >> 6, waves = nthr >> 6;
+    const int n_l = lane & 15, kq = lane >> 4;
+    const int G = K / kGS;
+    const int row0 = blockIdx.x * 16, m0 = blockIdx.y * 16;
+    const int bc = min(16, B - m0);
+    const int row = row0 + n_l, row_c = min(row, N - 1);
+    const int RS = SG * kGS + 16;                       // LDS row stride (bytes)
+    int8_t *img = reinterpret_cast<int8_t *>(lds8);
+    int *gsum = reinterpret_cast<int *>(lds8 + (size_t)16 * RS);
+    float *gscl = reinterpret_cast<float *>(gsum + SG * 16);
+
+    float4_t acc = {0.0f, 0.0f, 0.0f, 0.0f};
+    for (int s0 = 0; s0 < G; s0 += SG) {
+        const int SGs = min(SG, G - s0);
+        const int g0 = s0 + (wave * SGs) / waves;
+        const int ng = s0 + ((wave + 1) * SGs) / waves - g0;
+        u32x4_t wq[kNG];
+#pragma unroll
+        for (int i = 0; i < kNG; i++) {
+            const int g = min(g0 + min(i, max(ng - 1, 0)), G - 1);
+            wq[i] = *reinterpret_cast<const u32x4_t *>(w + (size_t)row_c * (K / 2) + (size_t)g * 64 + kq * 16);
+        }
+        // q8 rows of the stage: 16-byte chunks, 8 per group row; the 8 chunks
+        // of a (row, group) are 8 consecutive lanes
+        const int cpr = SGs * 8;
+        for (int c = tid; c < 16 * cpr; c += nthr) {
+            const int r = c / cpr, ci = c - r * cpr;
+            const int rb = r < bc ? r : 0;
+            const size_t k = (size_t)s0 * kGS + (size_t)ci * 16;
+            const u32x4_t v = *reinterpret_cast<const u32x4_t *>(q8 + (size_t)(m0 + rb) * K + k);
+            *reinterpret_cast<u32x4_t *>(img + (size_t)r * RS + ci * 16) = v;
+            int sum = 0;
+#pragma unroll
+            for (int d = 0; d < 4; d++) sum = __builtin_amdgcn_sdot4((int)v[d], 0x01010101, sum, false);
+            sum += __shfl_xor(sum, 1);
+            sum += __shfl_xor(sum, 2);
+            sum += __shfl_xor(sum, 4);
+            if ((ci & 7) == 0) {
+                const int g = ci / 8;
+                gsum[g * 16 + r] = sum;
+                gscl[g * 16 + r] = q8_scales[(size_t)(m0 + rb) * G + s0 + g];
+            }
+        }
+        __syncthreads();
+#pragma unroll
+        for (int i = 0; i < kNG; i++) {
+            if (i < ng) {
+                const int g = g0 + i;
+                const float ws = __half2float(scales[(size_t)row_c * G + g]);
+                const float iz = rintf(__half2float(zeros[(size_t)row_c * G + g]));
+                i32x4_t ai = {0, 0, 0, 0};
+#pragma unroll
+                for (int j = 0; j < 2; j++) {
+                    // codes 32 kq + 16 j .. + 15 in natural order: dword pairs (2 j, 2 j + 1)
+                    u32x4_t bq;
+#pragma unroll
+                    for (int h = 0; h < 2; h++) {
+                        const uint32_t wd = wq[i][2 * j + h];
+                        const uint32_t lo = wd & 0x0F0F0F0Fu, hi = (wd >> 4) & 0x0F0F0F0Fu;
+                        bq[2 * h] = __builtin_amdgcn_perm(hi, lo, 0x05010400u);
+                        bq[2 * h + 1] = __builtin_amdgcn_perm(hi, lo, 0x07030602u);
+                    }
+                    const u32x4_t av =
+                        *reinterpret_cast<const u32x4_t *>(img + (size_t)n_l * RS + (g - s0) * kGS + kq * 32 + j * 16);
+                    ai = __builtin_amdgcn_mfma_i32_16x16x64_i8(__builtin_bit_cast(i32x4_t, av), __builtin_bit_cast(i32x4_t, bq),
+                                                               ai, 0, 0, 0);
+                }
+                // D rows 4 kq + r are batch rows; column n_l is this lane's weight row
+                const i32x4_t gs4 = *reinterpret_cast<const i32x4_t *>(gsum + (g - s0) * 16 + 4 * kq);
+                const float4_t as4 = *reinterpret_cast<const float4_t *>(gscl + (g - s0) * 16 + 4 * kq);
+#pragma unroll
+                for (int r = 0; r < 4; r++)
+                    acc[r] = __builtin_fmaf(ws * as4[r], (float)(ai[r] - (int)iz * gs4[r]), acc[r]);
+            }
+        }
+        __syncthreads();
+    }
+    float4_t *red = reinterpret_cast<float4_t *>(lds8);
+    red[wave * 64 + lane] = acc;
+    __syncthreads();
+    if (wave != 0 || row >= N) return;
+    float4_t s = red[lane];
+    for (int wv = 1; wv < waves; wv++) s += red[wv * 64 + lane];
+#pragma unroll
+    for (int r = 0; r < 4; r++) {
+        const int b = 4 * kq + r;
+        if (b < bc) y[(size_t)(m0 + b) * N + row] = __float2half(s[r]);
+    }
+}
+
+int check_w(const imh_affine_int4_weight *w, const char *who) {
+    if (!w || !w->data || !w->scales || !w->zeros)
+        return imh::fail(IMH_EINVAL, std::string(who) + ": weight or one of its arrays is NULL");
+    if (w->group_size != kGS)
+        return imh::fail(IMH_EUNSUPPORTED, std::string(who) + ": group_size " + std::to_string(w->group_size) +
+                                               " not supported (built for 128)");
+    if (w->n == 0 || w->k == 0 || w->k % kGS)
+        return imh::fail(IMH_EUNSUPPORTED, std::string(who) + ": k must be a non-zero multiple of 128, n non-zero");
+    if ((reinterpret_cast<uintptr_t>(w->data) & 15) != 0)
+        return imh::fail(IMH_EINVAL, std::string(who) + ": weight data must be 16-byte aligned");
+    return IMH_OK;
+}
+
+int waves_for(int G) { return std::max(1, std::min(kMaxWaves, (G + 3) / 4)); }
+
+}  // namespace
+
+extern "C" {
+
+int imh_encode_affine_projection_int8(imh_stream *stream, const uint16_t *x, uint32_t token_count,
+                                      const imh_affine_int8_weight *w8, uint16_t *y) {
+    const char *who = "imh_encode_affine_projection_int8";
+    if (!stream || !x || !y || !w8) return imh::fail(IMH_EINVAL, std::string(who) + ": NULL argument");
+    const imh_affine_int4_weight *w = reinterpret_cast<const imh_affine_int4_weight *>(w8);
+    int rc = check_w(w, who);
+    if (rc) return rc;
+    if ((reinterpret_cast<uintptr_t>(x) | reinterpret_cast<uintptr_t>(w->awq_scales)) & 15)
+        return imh::fail(IMH_EINVAL, std::string(who) + ": x and awq_scales must be 16-byte aligned");
+    if (token_count == 0) return IMH_OK;
+    rc = imh::use_device(stream->dev);
+    if (rc) return rc;
+    const int N = (int)w->n, K = (int)w->k, G = K / kGS;
+    const int waves = waves_for(G);
+    // batch rows in launches of up to 8 (rows 0-7 of the MFMA tile hi, 8-15 lo)
+    for (uint32_t b0 = 0; b0 < token_count; b0 += 8) {
+        const int B = (int)std::min<uint32_t>(8, token_count - b0);
+        int SG = std::max(1, std::min(G, kStageBytes / (2 * B * (kGS + 8) * 2)));
+        SG = std::min(SG, waves * kNG);
+        const size_t lds = std::max((size_t)2 * B * (SG * kGS + 8) * 2 + (size_t)SG * 16 * 4,
+                                    (size_t)waves * 64 * sizeof(float4_t));
+        hipLaunchKernelGGL(int8w_matvec_kernel, dim3((N + 15) / 16), dim3(64 * waves), lds, stream->stream,
+                           reinterpret_cast<const __half *>(x) + (size_t)b0 * K,
+                           reinterpret_cast<const __half *>(w->awq_scales), w->data,
+                           reinterpret_cast<const __half *>(w->scales), reinterpret_cast<const __half *>(w->zeros),
+                           reinterpret_cast<__half *>(y) + (size_t)b0 * N, N, K, B, SG);
+        IMH_HIP(hipGetLastError());
+    }
+    return IMH_OK;
+}
+
+int imh_encode_quantize_input_q8(imh_stream *stream, const uint16_t *x, uint32_t token_count, uint32_t k,
+                                 int8_t *q8, float *q8_scales) {
+    const char *who = "imh_encode_quantize_input_q8";
+    if (!stream || !x || !q8 || !q8_scales) return imh::fail(IMH_EINVAL, std::string(who) + ": NULL argument");
+    if (k == 0 || k % kGS) return imh::fail(IMH_EUNSUPPORTED, std::string(who) + ": k must be a multiple of 128");
+    if (token_count == 0) return IMH_OK;
+    if (token_count > 65535) return imh::fail(IMH_EINVAL, std::string(who) + ": token_count above 65535");
+    int rc = imh::use_device(stream->dev);
+    if (rc) return rc;
+    hipLaunchKernelGGL(q8_quantize_kernel, dim3(k / kGS, token_count), dim3(kGS), 0, stream->stream,
+                       reinterpret_cast<const __half *>(x), q8, q8_scales, (int)k);
+    IMH_HIP(hipGetLastError());
+    return IMH_OK;
+}
+
+int imh_encode_affine_matvec_int4xq8(imh_stream *stream, const int8_t *q8, const float *q8_scales,
+                                     uint32_t token_count, const imh_affine_int4_weight *w, uint16_t *y) {
+    const char *who = "imh_encode_affine_matvec_int4xq8";
+    if (!stream || !q8 || !q8_scales || !y) return imh::fail(IMH_EINVAL, std::string(who) + ": NULL argument");
+    int rc = check_w(w, who);
+    if (rc) return rc;
+    if (reinterpret_cast<uintptr_t>(q8) & 15) return imh::fail(IMH_EINVAL, std::string(who) + ": q8 must be 16-byte aligned");
+    if (w->awq_scales)
+        return imh::fail(IMH_EINVAL, std::string(who) + ": the Q8 path has no AWQ division (pipeline.rs:639-664)");
+    if (token_count == 0) return IMH_OK;
+    if (token_count > 65535u * 16) return imh::fail(IMH_EINVAL, std::string(who) + ": token_count too large");
+    rc = imh::use_device(stream->dev);
+    if (rc) return rc;
+    const int N = (int)w->n, K = (int)w->k, G = K / kGS;
+    const int waves = waves_for(G);
+    int SG = std::max(1, std::min(G, kStageBytes / (16 * (kGS + 16))));
+    SG = std::min(SG, waves * kNG);
+    const size_t lds = std::max((size_t)16 * (SG * kGS + 16) + (size_t)SG * 16 * 8, (size_t)waves * 64 * sizeof(float4_t));
+    hipLaunchKernelGGL(int4xq8_matvec_kernel, dim3((N + 15) / 16, (token_count + 15) / 16), dim3(64 * waves), lds,
+                       stream->stream, q8, q8_scales, w->data, reinterpret_cast<const __half *>(w->scales),
+                       reinterpret_cast<const __half *>(w->zeros), reinterpret_cast<__half *>(y), N, K,
+                       (int)token_count, SG);
+    IMH_HIP(hipGetLastError());
+    return IMH_OK;
+}
+
+}  // extern "C"

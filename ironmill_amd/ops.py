@@ -14,9 +14,10 @@ import math
 import numpy as np
 
 from . import _lib
+from ._lib import AffineInt8Weight as _AffineInt8Weight
 from ._lib import (AffineInt4Weight, DecoderConfig, DecoderLayerWeights, FusedResidualNormParams, QkNormRopeParams,
                    TqKvCache, check, lib)
-from .quant import QuantizedInt4
+from .quant import QuantizedInt4, QuantizedInt8
 from .runtime import Buffer, Device, Stream
 
 
@@ -58,6 +59,40 @@ def encode_projection(stream: Stream, x, weight: AffineQuantizedWeight, y, token
     """encode_projection -> encode_affine_projection (projection.rs:35-56,227-312)."""
     check(lib.imh_encode_affine_projection_int4(stream.handle, _ptr(x), token_count,
                                                 C.byref(weight.c), _ptr(y)))
+
+
+class AffineInt8Weight:
+    """Device copy of an INT8 weight (quantize_tensor_int8, quantized.rs:852-901)."""
+
+    def __init__(self, dev: Device, q: QuantizedInt8):
+        self.n, self.k, self.group_size = q.n, q.k, q.group_size
+        self.data = dev.upload(q.data)
+        self.scales = dev.upload(q.scales)
+        self.zeros = dev.upload(q.zeros)
+        self.awq_scales = dev.upload(q.awq) if q.awq is not None else None
+        self._c = _AffineInt8Weight(self.data.ptr, self.scales.ptr, self.zeros.ptr,
+                                    self.awq_scales.ptr if self.awq_scales is not None else None,
+                                    self.n, self.k, self.group_size)
+
+    @property
+    def c(self) -> _AffineInt8Weight:
+        return self._c
+
+
+def encode_projection_int8(stream: Stream, x, weight: AffineInt8Weight, y, token_count: int):
+    """superblock_matvec_int8 (affine_matvec.metal:123-189) over token_count rows, f16 in and out."""
+    check(lib.imh_encode_affine_projection_int8(stream.handle, _ptr(x), token_count, C.byref(weight.c), _ptr(y)))
+
+
+def encode_quantize_input_q8(stream: Stream, x, token_count: int, k: int, q8, q8_scales):
+    """quantize_input_q8 (quantize.metal:21-52) per 128-element group of each row."""
+    check(lib.imh_encode_quantize_input_q8(stream.handle, _ptr(x), token_count, k, _ptr(q8), _ptr(q8_scales)))
+
+
+def encode_affine_matvec_int4xq8(stream: Stream, q8, q8_scales, token_count: int, weight: AffineQuantizedWeight, y):
+    """superblock_affine_matvec_int4xq8 (affine_fused.metal:115-176) on Q8 activations."""
+    check(lib.imh_encode_affine_matvec_int4xq8(stream.handle, _ptr(q8), _ptr(q8_scales), token_count,
+                                               C.byref(weight.c), _ptr(y)))
 
 
 GEMM_F16, GEMM_BF16, GEMM_FP8_E4M3 = 0, 1, 2

@@ -75,6 +75,39 @@ class QuantizedInt4:
     group_size: int = GROUP_SIZE
 
 
+@dataclass
+class QuantizedInt8:
+    """Host copy of one INT8 weight in the GPU upload layout (one code byte per element)."""
+
+    data: np.ndarray       # u8 [n, k]
+    scales: np.ndarray     # f16 [n, k/gs]
+    zeros: np.ndarray      # f16 [n, k/gs]
+    scales_f32: np.ndarray
+    zeros_f32: np.ndarray
+    awq: np.ndarray | None
+    n: int
+    k: int
+    group_size: int = GROUP_SIZE
+
+
+def quantize_int8(w: np.ndarray, group_size: int = GROUP_SIZE, awq_scales=None) -> QuantizedInt8:
+    """quantize_tensor_int8 (quantized.rs:852-901): the INT4 rule with qmax 255, no packing."""
+    w = np.asarray(w, np.float32)
+    n, k = w.shape
+    if k % group_size:
+        raise ValueError(f"k={k} must be a multiple of group_size={group_size}")
+    awq16 = None
+    if awq_scales is not None:
+        s = np.asarray(awq_scales, np.float32)
+        w = (w * s[None, :]).astype(np.float32)
+        awq16 = s.astype(np.float16)
+    q, sc, zp = quantize_groups(w.reshape(n * (k // group_size), group_size), qmax=255.0)
+    sc = sc.reshape(n, k // group_size)
+    zp = zp.reshape(n, k // group_size)
+    return QuantizedInt8(data=q.reshape(n, k), scales=sc.astype(np.float16), zeros=zp.astype(np.float16),
+                         scales_f32=sc, zeros_f32=zp, awq=awq16, n=n, k=k, group_size=group_size)
+
+
 def quantize_int4(w: np.ndarray, group_size: int = GROUP_SIZE, awq_scales=None) -> QuantizedInt4:
     """quantize_tensor_int4 (+ AWQ): w f32/f16 [n, k], k a multiple of group_size."""
     w = np.asarray(w, np.float32)

@@ -193,6 +193,92 @@ void orc_quantize_tensor_int4(const float *w, size_t rows, size_t k, size_t gs,
     free(codes);
 }
 
+static inline float read_q4(const uint8_t *packed, size_t i);
+
+/* quantize_tensor_int8 (ironmill-compile/src/weights/quantized.rs:852-901):
+ * the INT4 walk with qmax 255 and one code byte per element (no packing). */
+void orc_quantize_tensor_int8(const float *w, size_t rows, size_t k, size_t gs,
+                              uint8_t *codes, float *scales, float *zeros) {
+    size_t ngroups = (k + gs - 1) / gs;
+    size_t pi = 0;
+    for (size_t r = 0; r < rows; r++) {
+        size_t row_start = r * k;
+        for (size_t g = 0; g < ngroups; g++) {
+            size_t g_start = row_start + g * gs;
+            size_t g_end = g_start + gs;
+            if (g_end > row_start + k) g_end = row_start + k;
+            orc_quantize_affine(w + g_start, g_end - g_start, 255.0f, codes + g_start,
+                                &scales[pi], &zeros[pi]);
+            pi++;
+        }
+    }
+}
+
+/* dequant_affine for 8-bit codes (ironmill-core/src/dequant.rs:122-142 with
+ * bit_width 8: one byte per element): f16((q - z) * s), f32 arithmetic. */
+void orc_dequant_affine_int8(const uint8_t *codes, const float *scales, const float *zeros,
+                             size_t n, size_t k, size_t gs, uint16_t *w_out) {
+    size_t ng = (k + gs - 1) / gs;
+    for (size_t r = 0; r < n; r++)
+        for (size_t c = 0; c < k; c++) {
+            size_t pi = r * ng + c / gs;
+            w_out[r * k + c] = orc_f32_to_f16(((float)codes[r * k + c] - zeros[pi]) * scales[pi]);
+        }
+}
+
+/* quantize_input_q8 (quantize.metal:21-52) per group of gs elements of each
+ * row: scale = absmax / 127, inv = absmax > 0 ? 127 / absmax : 0,
+ * q = clamp(rint(x * inv), -127, 127), f32 arithmetic.  The group's absmax is
+ * taken over the whole group (the kernel's stated rule; its simdgroup-scope
+ * reduction is not reproduced). */
+void orc_quantize_input_q8(const uint16_t *x, size_t rows, size_t k, size_t gs, int8_t *q8,
+                           float *scales) {
+    size_t ng = k / gs;
+    for (size_t r = 0; r < rows; r++)
+        for (size_t g = 0; g < ng; g++) {
+            const uint16_t *xg = x + r * k + g * gs;
+            float m = 0.0f;
+            for (size_t i = 0; i < gs; i++) {
+                float a = fabsf(orc_f16_to_f32(xg[i]));
+                if (a > m) m = a;
+            }
+            scales[r * ng + g] = m / 127.0f;
+            float inv = m > 0.0f ? 127.0f / m : 0.0f;
+            for (size_t i = 0; i < gs; i++) {
+                float v = rintf(orc_f16_to_f32(xg[i]) * inv);
+                if (v < -127.0f) v = -127.0f;
+                if (v > 127.0f) v = 127.0f;
+                q8[r * k + g * gs + i] = (int8_t)v;
+            }
+        }
+}
+
+/* superblock_affine_matvec_int4xq8 (affine_fused.metal:115-176) with the Q8
+ * group equal to the weight group: y = sum_g ws * as * sum q8 (q - rint(z)),
+ * f64 accumulation (the reference's per-term f32 products differ from this
+ * by f32 rounding only).  Scales and zero-points as uploaded (f16). */
+void orc_matvec_int4xq8(const int8_t *q8, const float *q8_scales, const uint8_t *packed,
+                        const uint16_t *scales, const uint16_t *zeros, size_t batch, size_t n,
+                        size_t k, size_t gs, double *y) {
+    size_t ng = k / gs;
+    for (size_t b = 0; b < batch; b++)
+        for (size_t r = 0; r < n; r++) {
+            double acc = 0.0;
+            for (size_t g = 0; g < ng; g++) {
+                double ws = orc_f16_to_f32(scales[r * ng + g]);
+                double iz = rintf(orc_f16_to_f32(zeros[r * ng + g]));
+                long long s = 0;
+                for (size_t i = 0; i < gs; i++) {
+                    size_t c = g * gs + i;
+                    long long q = (long long)read_q4(packed, r * k + c);
+                    s += (long long)q8[b * k + c] * (q - (long long)iz);
+                }
+                acc += ws * (double)q8_scales[b * ng + g] * (double)s;
+            }
+            y[b * n + r] = acc;
+        }
+}
+
 void orc_convert_params_to_f16(const float *params, size_t n, uint16_t *out) {
     for (size_t i = 0; i < n; i++) out[i] = orc_f32_to_f16(params[i]);
 }

@@ -54,6 +54,15 @@ void orc_quantize_tensor_int4(const float *w, size_t rows, size_t k, size_t gs,
                               uint8_t *packed, float *scales, float *zeros);
 
 /* ---- f32 params -> f16 (ironmill-core/src/dequant.rs:305-345) ---- */
+void orc_quantize_tensor_int8(const float *w, size_t rows, size_t k, size_t gs,
+                              uint8_t *codes, float *scales, float *zeros);
+void orc_dequant_affine_int8(const uint8_t *codes, const float *scales, const float *zeros,
+                             size_t n, size_t k, size_t gs, uint16_t *w_out);
+void orc_quantize_input_q8(const uint16_t *x, size_t rows, size_t k, size_t gs, int8_t *q8,
+                           float *scales);
+void orc_matvec_int4xq8(const int8_t *q8, const float *q8_scales, const uint8_t *packed,
+                        const uint16_t *scales, const uint16_t *zeros, size_t batch, size_t n,
+                        size_t k, size_t gs, double *y);
 void orc_convert_params_to_f16(const float *params, size_t n, uint16_t *out);
 
 /* ---- CPU dequant to dense f16 (ironmill-core/src/dequant.rs:85-180, group

@@ -51,6 +51,10 @@ def _declare(L):
         "orc_pack_int4_u32": (None, [P, SZ, P]),
         "orc_quantize_tensor_int4": (None, [P, SZ, SZ, SZ, P, P, P]),
         "orc_convert_params_to_f16": (None, [P, SZ, P]),
+        "orc_quantize_tensor_int8": (None, [P, SZ, SZ, SZ, P, P, P]),
+        "orc_dequant_affine_int8": (None, [P, P, P, SZ, SZ, SZ, P]),
+        "orc_quantize_input_q8": (None, [P, SZ, SZ, SZ, P, P]),
+        "orc_matvec_int4xq8": (None, [P, P, P, P, P, SZ, SZ, SZ, SZ, P]),
         "orc_dequant_affine_int4": (None, [P, P, P, SZ, SZ, SZ, P]),
         "orc_dequant_affine_int4_f16params": (None, [P, P, P, SZ, SZ, SZ, P]),
         "orc_matvec_f16w": (None, [P, P, P, SZ, SZ, SZ, P, C.c_int]),
@@ -137,6 +141,49 @@ def quantize_tensor_int4(w, gs=128):
     zeros = np.zeros((rows, ng), np.float32)
     lib().orc_quantize_tensor_int4(_p(w), rows, k, gs, _p(packed), _p(scales), _p(zeros))
     return packed, scales, zeros
+
+
+def quantize_tensor_int8(w, gs=128):
+    """quantized.rs:852-901 -> (codes u8 [rows, k], scales f32 [rows, G], zeros f32 [rows, G])."""
+    w = _c(w, np.float32)
+    rows, k = w.shape
+    ng = -(-k // gs)
+    codes = np.zeros((rows, k), np.uint8)
+    scales = np.zeros((rows, ng), np.float32)
+    zeros = np.zeros((rows, ng), np.float32)
+    lib().orc_quantize_tensor_int8(_p(w), rows, k, gs, _p(codes), _p(scales), _p(zeros))
+    return codes, scales, zeros
+
+
+def dequant_affine_int8(codes, scales, zeros, n, k, gs=128) -> np.ndarray:
+    """dequant.rs:122-142 for 8-bit codes, f32 params -> dense f16 [n, k]."""
+    out = np.zeros((n, k), np.uint16)
+    lib().orc_dequant_affine_int8(_p(_c(codes, np.uint8)), _p(_c(scales, np.float32)), _p(_c(zeros, np.float32)),
+                                  n, k, gs, _p(out))
+    return out.view(np.float16)
+
+
+def quantize_input_q8(x16, gs=128):
+    """quantize.metal:21-52 per row -> (q8 int8 [rows, k], scales f32 [rows, k/gs])."""
+    x = _c(x16, np.float16).view(np.uint16)
+    if x.ndim == 1:
+        x = x[None, :]
+    rows, k = x.shape
+    q8 = np.zeros((rows, k), np.int8)
+    sc = np.zeros((rows, k // gs), np.float32)
+    lib().orc_quantize_input_q8(_p(x), rows, k, gs, _p(q8), _p(sc))
+    return q8, sc
+
+
+def matvec_int4xq8(q8, q8_scales, packed, scales16, zeros16, n, k, gs=128) -> np.ndarray:
+    """affine_fused.metal:115-176 restated exactly (integer group sums) -> f64 [rows, n]."""
+    q8 = _c(q8, np.int8)
+    rows = q8.shape[0]
+    y = np.zeros((rows, n), np.float64)
+    lib().orc_matvec_int4xq8(_p(q8), _p(_c(q8_scales, np.float32)), _p(_c(packed, np.uint8)),
+                             _p(_c(scales16, np.float16).view(np.uint16)), _p(_c(zeros16, np.float16).view(np.uint16)),
+                             rows, n, k, gs, _p(y))
+    return y
 
 
 def convert_params_to_f16(p) -> np.ndarray:
