@@ -125,29 +125,38 @@ def eager_loop(dev, stream, fn, steps, warmup):
     return s.elapsed_ms(e)
 
 
-def cpu_baseline(qg, qu, qd, seconds):
+def cpu_baseline(qg, qu, qd, seconds, single_seconds=4.0):
+    """The reference's CPU path (dequantize to f16 once, then f32 matvecs) on the host cores:
+    a bounded multi-threaded sample, then a single-thread one."""
     import oracle as O
-    threads = min(os.cpu_count() or 1, 16)
+    cores = os.cpu_count() or 1
+    threads = min(cores, 16)   # the GPU box's CPU share is 16 threads
     wg = O.dequant_affine_int4(qg.data, qg.scales_f32, qg.zeros_f32, F, H)
     wu = O.dequant_affine_int4(qu.data, qu.scales_f32, qu.zeros_f32, F, H)
     wd = O.dequant_affine_int4(qd.data, qd.scales_f32, qd.zeros_f32, H, F)
     x = make_x(1, H, 7)
-    reps, t0 = 0, time.perf_counter()
-    while True:
-        g = O.matvec_f16w(wg, x, qg.awq, nthreads=threads)
-        u = O.matvec_f16w(wu, x, qg.awq, nthreads=threads)
-        act = (g / (1.0 + np.exp(-g)) * u).astype(np.float16)
-        O.matvec_f16w(wd, act, qd.awq, nthreads=threads)
-        reps += 1
-        if time.perf_counter() - t0 >= seconds:
-            break
-    dt = (time.perf_counter() - t0) / reps
-    gbs = (gate_up_bytes(1) + down_bytes(1)) / dt / 1e9
-    return {"value": round(gbs, 3), "unit": "GB/s (INT4 bytes model, FFN step batch 1)",
-            "cores": threads, "kind": "port",
-            "sample": f"{reps} Qwen3-4B FFN steps (gate+up+SiLU+down, batch 1) in {reps * dt:.1f} s; "
-                      f"C oracle, weights dequantized to f16 once outside the timing, "
-                      f"{1e3 * dt:.1f} ms/step"}
+
+    def run(nthreads, budget):
+        reps, t0 = 0, time.perf_counter()
+        while True:
+            g = O.matvec_f16w(wg, x, qg.awq, nthreads=nthreads)
+            u = O.matvec_f16w(wu, x, qg.awq, nthreads=nthreads)
+            act = (g / (1.0 + np.exp(-g)) * u).astype(np.float16)
+            O.matvec_f16w(wd, act, qd.awq, nthreads=nthreads)
+            reps += 1
+            if time.perf_counter() - t0 >= budget:
+                return reps, (time.perf_counter() - t0) / reps
+
+    reps, dt = run(threads, seconds)
+    reps1, dt1 = run(1, single_seconds)
+    nbytes = gate_up_bytes(1) + down_bytes(1)
+    return {"value": round(nbytes / dt / 1e9, 3), "unit": "GB/s (INT4 bytes model, FFN step batch 1)",
+            "cores": cores, "threads": threads, "kind": "port",
+            "single_thread": {"value": round(nbytes / dt1 / 1e9, 3), "ms_per_step": round(1e3 * dt1, 2),
+                              "steps": reps1},
+            "sample": f"{reps} Qwen3-4B FFN steps (gate+up+SiLU+down, batch 1) in {reps * dt:.1f} s on "
+                      f"{threads} of {cores} host threads, {1e3 * dt:.1f} ms/step; C oracle, weights "
+                      f"dequantized to f16 once outside the timing"}
 
 
 def bench_attention(dev, stream, ops, batch, ctx, steps, warmup, layers, eager=False):
@@ -207,6 +216,86 @@ def bench_fp16_attention(dev, stream, ops, batch, ctx, steps, warmup, layers, ea
     gbs = nbytes / (ms * 1e-3) / 1e9
     return {"batch": batch, "ctx": ctx, "us": round(ms * 1e3, 2), "GB/s": round(gbs, 1),
             "frac": round(gbs / HBM_PEAK_GBS, 4), "bytes": nbytes}
+
+
+GEMM_PEAK_TFS = {"f16": 2500.0, "bf16": 2500.0, "fp8": 5000.0}   # MI355X dense MFMA peaks
+
+
+def bf16_bits(x32):
+    """float32 -> bf16 bit patterns (uint16), round to nearest even."""
+    u = np.ascontiguousarray(x32, np.float32).view(np.uint32).astype(np.uint64)
+    return ((u + 0x7FFF + ((u >> 16) & 1)) >> 16).astype(np.uint16)
+
+
+def bench_gemm(dev, stream, ops, m, kk, nn, prec, steps, warmup, eager=False, replicas=2):
+    """Prefill INT4 GEMM: X [m, kk] N(0,1), W INT4 g128 [nn, kk] without AWQ, through
+    imh_affine_gemm_int4 at `prec` (f16: x / y f16; bf16 and fp8: x / y bf16)."""
+    rng = np.random.default_rng(31 * m + kk)
+    Ws = [random_int4(dev, ops, rng, nn, kk, awq=False) for _ in range(replicas)]
+    x32 = rng.standard_normal((m, kk)).astype(np.float32)
+    xm = dev.upload(x32.astype(np.float16) if prec == "f16" else bf16_bits(x32))
+    ym = dev.empty((m, nn), np.uint16)
+    code = {"f16": ops.GEMM_F16, "bf16": ops.GEMM_BF16, "fp8": ops.GEMM_FP8_E4M3}[prec]
+
+    def gm(i):
+        ops.encode_affine_gemm_int4(stream, xm, m, Ws[i % replicas], ym, code)
+
+    us = 1e3 * (eager_loop if eager else time_loop)(dev, stream, gm, steps, warmup) / steps
+    tfs = 2.0 * m * nn * kk / (us * 1e-6) / 1e12
+    return {"precision": prec, "us": round(us, 2), "TFLOP/s": round(tfs, 1),
+            "frac": round(tfs / GEMM_PEAK_TFS[prec], 4), "peak_TFLOP/s": GEMM_PEAK_TFS[prec]}
+
+
+def bench_probe(dev, stream, ops, steps, warmup, sweep=True):
+    """Streaming probe (imh_diag_stream_read): the batch-1 gate+up and down weight bytes read
+    with no compute, rotating over >= 512 MB of buffers like the matvec measurement.  `kernel`:
+    the matvec's own launch (gate+up: 608 workgroups, each one 16-row tile of both weights with 4
+    waves per weight; down: 160 workgroups of one 16-row tile, 16 waves).  With `sweep`: TILE
+    shapes of 8 / 16 rows, 1-4 tiles per workgroup and 1-16 waves, and FLAT grids of contiguous
+    runs (the best of each reported as *_best)."""
+    sink = dev.empty((1,), np.uint32)
+    out = {}
+    # per-launch floor: 256 workgroups reading 4 KiB in all
+    tiny = dev.empty((4096,), np.uint8)
+    us = 1e3 * time_loop(dev, stream, lambda i: ops.diag_stream_read(
+        stream, tiny, 64, 128, sink, mode=ops.PROBE_FLAT, grid=256, threads=256), steps, warmup) / steps
+    out["launch_floor"] = {"us": round(us, 2), "bytes": 4096, "grid": 256, "threads": 256}
+    cases = [("gate_up", F, H, 2, (16, 1, 4)), ("down", H, F, 1, (16, 1, 16))]
+    for name, n, k, nmat, own in cases:
+        nbytes = nmat * n * k // 2
+        reps = max(2, math.ceil(512e6 / nbytes))
+        bufs = [dev.empty((nbytes,), np.uint8) for _ in range(reps)]
+        G = k // 128
+        runs = [("kernel", dict(mode=ops.PROBE_TILE, nmat=nmat, rows=own[0], tiles=own[1], waves=own[2]))]
+        if sweep:
+            for rows in (16, 8):
+                for tiles in (1, 2, 4):
+                    for waves in (1, 2, 4, 8, 16):
+                        units = tiles * (G if rows == 16 else G // 2)
+                        if waves * nmat > 16 or -(-units // waves) > 32 or -(-units // waves) < 2:
+                            continue
+                        runs.append((f"tile_r{rows}_t{tiles}_w{waves}",
+                                     dict(mode=ops.PROBE_TILE, nmat=nmat, rows=rows, tiles=tiles, waves=waves)))
+            runs += [(f"flat_g{g}_t{t}", dict(mode=ops.PROBE_FLAT, grid=g, threads=t))
+                     for t in (256, 512, 1024) for g in (256, 512, 1024, 2048)]
+        best = {}
+        for label, shp in runs:
+            def fn(i, shp=shp):
+                ops.diag_stream_read(stream, bufs[i % reps], nmat * n if shp["mode"] == ops.PROBE_FLAT else n, k,
+                                     sink, **shp)
+
+            us = 1e3 * time_loop(dev, stream, fn, steps, warmup) / steps
+            gbs = nbytes / (us * 1e-6) / 1e9
+            key = f"{name}_{label}"
+            out[key] = {"us": round(us, 2), "GB/s": round(gbs, 1), "frac": round(gbs / HBM_PEAK_GBS, 4),
+                        "bytes": nbytes, **{k_: v for k_, v in shp.items() if k_ != "mode"}}
+            kind = label.split("_")[0]
+            if kind != "kernel" and (kind not in best or us < out[best[kind]]["us"]):
+                best[kind] = key
+        for kind, key in best.items():
+            out[f"{name}_{kind}_best"] = dict(out[key], case=key)
+        del bufs
+    return out
 
 
 # Qwen3-4B shape of the decode-step measurement (cfg 5)
@@ -330,12 +419,20 @@ def main():
     ap.add_argument("--attention-only", choices=["tq", "fp16"],
                     help="only the decode attention at ctx 32k and --batch (for rocprofv3 runs)")
     ap.add_argument("--eager", action="store_true",
-                    help="with --attention-only: host launches instead of a graph (counter runs)")
+                    help="with --attention-only / --kernel: host launches instead of a graph (counter runs)")
     ap.add_argument("--decode-batches", type=int, nargs="+", default=[1, 8])
     ap.add_argument("--decode-eager", action="store_true",
                     help="with --decode-only: time 5 eager steps only (no graph capture; for kernel traces)")
     ap.add_argument("--kernel-only", action="store_true",
-                    help="only the prepared fused gate+up kernel loop (for rocprofv3 counter runs)")
+                    help="only the prepared fused gate+up kernel loop (same as --kernel gate_up)")
+    ap.add_argument("--kernel", choices=["gate_up", "down", "gemm", "probe"],
+                    help="one kernel alone, for rocprofv3 runs: the batch-B fused gate+up or down "
+                         "matvec, the prefill GEMM (--gemm-*), or the streaming probe; with --eager "
+                         "the launches are host launches (counter runs see only those)")
+    ap.add_argument("--gemm-m", type=int, default=2048)
+    ap.add_argument("--gemm-shape", choices=["gate", "down"], default="gate",
+                    help="K=2560 N=9728 (gate) or K=9728 N=2560 (down)")
+    ap.add_argument("--gemm-precision", choices=["f16", "bf16", "fp8"], default="bf16")
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="only 5 device-to-device copies of 256 MiB (calibrates rocprofv3 "
                          "FETCH_SIZE / WRITE_SIZE against a known byte count), then exit")
@@ -377,6 +474,22 @@ def main():
             print(json.dumps({f"decode_step_b{bb}_ctx8k": r}), flush=True)
         return
 
+    if args.kernel_only:
+        args.kernel = "gate_up"
+    if args.kernel == "gemm":
+        kk, nn = (H, F) if args.gemm_shape == "gate" else (F, H)
+        r = bench_gemm(dev, stream, ops, args.gemm_m, kk, nn, args.gemm_precision, args.steps, args.warmup,
+                       eager=args.eager)
+        log(f"GEMM {args.gemm_precision} M={args.gemm_m} K={kk} N={nn}: {r['us']} us {r['TFLOP/s']} TFLOP/s")
+        print(json.dumps({f"gemm_{args.gemm_precision}_m{args.gemm_m}_k{kk}_n{nn}": r}), flush=True)
+        return
+    if args.kernel == "probe":
+        r = bench_probe(dev, stream, ops, args.steps, args.warmup)
+        for k_, v in r.items():
+            log(f"probe {k_}: {v['us']} us {v.get('GB/s', '-')} GB/s")
+        print(json.dumps({"stream_probe": r}), flush=True)
+        return
+
     B = args.batch
     qg, qu, qd = make_weights(1234)
     per_copy = (qg.data.nbytes + qg.scales.nbytes * 2) * 3
@@ -393,15 +506,29 @@ def main():
         g, u, _ = W[i % reps]
         ops.encode_fused_ffn_gate_up_act_int4(stream, x, g, u, act, B)
 
-    ksteps = args.steps if not args.kernel_only else max(args.steps, 500)
-    tot = time_loop(dev, stream, gate_up_kernel, ksteps, args.warmup)
+    if args.kernel == "down":
+        a0 = dev.upload(make_x(B, F, 98))
+
+        def down_only(i):
+            ops.encode_projection(stream, a0, W[i % reps][2], y, B)
+
+        tot = (eager_loop if args.eager else time_loop)(dev, stream, down_only, args.steps, args.warmup)
+        us = 1e3 * tot / args.steps
+        gbs = down_bytes(B) / (us * 1e-6) / 1e9
+        log(f"down kernel B={B}: {us:.2f} us  {gbs:.0f} GB/s ({100 * gbs / HBM_PEAK_GBS:.1f} %)")
+        print(json.dumps({"kernel": "int4_matvec_kernel (down projection)", "batch": B, "us": round(us, 3),
+                          "GB/s": round(gbs, 1), "launches": args.steps, "eager": args.eager}))
+        return
+
+    ksteps = args.steps if args.kernel != "gate_up" else max(args.steps, 500)
+    tot = (eager_loop if args.eager and args.kernel else time_loop)(dev, stream, gate_up_kernel, ksteps, args.warmup)
     k_us = 1e3 * tot / ksteps
     k_bytes = gate_up_bytes(B)
     k_gbs = k_bytes / (k_us * 1e-6) / 1e9
     log(f"gate+up kernel: {k_us:.2f} us  {k_gbs:.0f} GB/s ({100 * k_gbs / HBM_PEAK_GBS:.1f} %)")
-    if args.kernel_only:
-        print(json.dumps({"kernel": "int4_matvec_kernel<2,SILU>", "us": round(k_us, 3),
-                          "GB/s": round(k_gbs, 1), "launches": ksteps}))
+    if args.kernel == "gate_up":
+        print(json.dumps({"kernel": "int4_matvec_kernel<2,SILU>", "batch": B, "us": round(k_us, 3),
+                          "GB/s": round(k_gbs, 1), "launches": ksteps, "eager": args.eager}))
         return
 
     # ---- the step: FFN block through the public ops ----
@@ -454,22 +581,15 @@ def main():
             us = 1e3 * t / args.steps
             details[f"down_kernel_b{bb}"] = {"us": round(us, 2),
                                              "GB/s": round(down_bytes(bb) / (us * 1e-6) / 1e9, 1)}
-        # prefill INT4 GEMM: M tokens through the projection op
+        # prefill INT4 GEMM: M tokens, bf16 and fp8-e4m3 (and f16, the projection op)
         for mm in (512, 2048):
-            for (kk, nn, wi) in ((H, F, 0), (F, H, 2)):
-                xm = dev.upload(make_x(mm, kk, 11 + mm))
-                ym = dev.empty((mm, nn), np.float16)
-
-                def gm(i, xm=xm, ym=ym, mm=mm, wi=wi):
-                    ops.encode_projection(stream, xm, W[i % reps][wi], ym, mm)
-
-                t = time_loop(dev, stream, gm, max(20, args.steps // 4), 3)
-                us = 1e3 * t / max(20, args.steps // 4)
-                tfs = 2.0 * mm * nn * kk / (us * 1e-6) / 1e12
-                details[f"gemm_m{mm}_k{kk}_n{nn}"] = {"us": round(us, 2), "TFLOP/s": round(tfs, 1),
-                                                      "frac": round(tfs / MFMA_F16_PEAK_TFS, 4)}
-                log(f"prefill GEMM M={mm} K={kk} N={nn}: {us:.1f} us {tfs:.0f} TFLOP/s "
-                    f"({100 * tfs / MFMA_F16_PEAK_TFS:.1f} % of dense f16 MFMA)")
+            for (kk, nn) in ((H, F), (F, H)):
+                for prec in ("bf16", "fp8", "f16"):
+                    r = bench_gemm(dev, stream, ops, mm, kk, nn, prec, max(20, args.steps // 4), 3)
+                    details[f"gemm_{prec}_m{mm}_k{kk}_n{nn}"] = r
+                    log(f"prefill GEMM {prec} M={mm} K={kk} N={nn}: {r['us']} us {r['TFLOP/s']} TFLOP/s "
+                        f"({100 * r['frac']:.1f} % of dense {prec} MFMA)")
+        details["stream_probe"] = bench_probe(dev, stream, ops, max(50, args.steps // 2), args.warmup, sweep=False)
         del W
         stream.sync()
         # sustained rates: a warmup graph long enough for the clocks to settle

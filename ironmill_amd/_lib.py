@@ -70,6 +70,12 @@ class AffineInt8Weight(C.Structure):
     _fields_ = AffineInt4Weight._fields_
 
 
+class ProbeShape(C.Structure):
+    """imh_probe_shape (the streaming probe's launch shape; no reference counterpart)."""
+
+    _fields_ = [(f, C.c_uint32) for f in ("mode", "nmat", "rows", "tiles", "waves", "grid", "threads")]
+
+
 class FusedResidualNormParams(C.Structure):
     """imh_fused_residual_norm_params (FusedResidualNormAffineInt4Params, ops/fused.rs:45-66)."""
 
@@ -225,6 +231,7 @@ SIGNATURES = {
                                       C.POINTER(AffineInt4Weight), P, P, I]),
     "imh_affine_gemm_int4": (I, [P, P, U32, C.POINTER(AffineInt4Weight), P, I]),
     "imh_encode_affine_projection_int8": (I, [P, P, U32, C.POINTER(AffineInt8Weight), P]),
+    "imh_diag_stream_read": (I, [P, P, U32, U32, C.POINTER(ProbeShape), P]),
     "imh_encode_quantize_input_q8": (I, [P, P, U32, U32, P, P]),
     "imh_encode_affine_matvec_int4xq8": (I, [P, P, P, U32, C.POINTER(AffineInt4Weight), P]),
     "imh_encode_fused_residual_norm_affine_matvec_int4": (I, [P, C.POINTER(FusedResidualNormParams)]),

@@ -95,6 +95,19 @@ def encode_affine_matvec_int4xq8(stream: Stream, q8, q8_scales, token_count: int
                                                C.byref(weight.c), _ptr(y)))
 
 
+PROBE_TILE, PROBE_FLAT = 0, 1
+
+
+def diag_stream_read(stream: Stream, src, n: int, k: int, sink, mode=PROBE_TILE, nmat=1, rows=16, tiles=1,
+                     waves=4, grid=0, threads=0):
+    """Streaming probe (no reference counterpart): reads the INT4 weight bytes at src with no
+    compute.  TILE: `tiles` tiles of `rows` rows of each of `nmat` n x k weights per workgroup,
+    `waves` waves per weight (rows 16 is the INT4 matvec's own pattern).  FLAT: `grid`
+    workgroups of `threads` threads reading contiguous runs of the n x k weight."""
+    shape = _lib.ProbeShape(mode, nmat, rows, tiles, waves, grid, threads)
+    check(lib.imh_diag_stream_read(stream.handle, _ptr(src), n, k, C.byref(shape), _ptr(sink)))
+
+
 GEMM_F16, GEMM_BF16, GEMM_FP8_E4M3 = 0, 1, 2
 
 

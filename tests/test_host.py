@@ -2,6 +2,7 @@
 the weight layout contract, and the C ABI surface (symbols, error paths that
 need no GPU)."""
 import ctypes as C
+import glob
 import os
 import re
 
@@ -78,9 +79,12 @@ def test_layout_contract():
 
 
 def _header_functions():
-    src = open(os.path.join(REPO, "include", "ironmill_hip.h")).read()
-    src = re.sub(r"/\*.*?\*/", "", src, flags=re.S)
-    return sorted(set(re.findall(r"\b(imh_[a-z0-9_]+)\s*\(", src)))
+    """Every function the headers under include/ declare."""
+    names = set()
+    for h in sorted(glob.glob(os.path.join(REPO, "include", "*.h"))):
+        src = re.sub(r"/\*.*?\*/", "", open(h).read(), flags=re.S)
+        names.update(re.findall(r"\b(imh_[a-z0-9_]+)\s*\(", src))
+    return sorted(names)
 
 
 def test_library_exports_every_declared_symbol():
