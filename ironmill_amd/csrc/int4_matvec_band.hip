@@ -1,0 +1,360 @@
+// int4_matvec_band.hip -- the INT4-affine (group 128) decode matvec for one
+// or two batch rows over a grid balanced on the compute units.
+//
+// Same semantics and arithmetic as int4_matvec_kernel (int4_matvec_kernel.h):
+//     y[m][r] = sum_g s[r][g] * (sum_{k in g} xe[m][k] q[r][k] - z[r][g] sum xe),
+// xe = x / awq, the raw code bytes entering v_mfma_f32_16x16x32_f16 as f16
+// denormals against the slot-ordered activation split into f16 hi + lo, the
+// zero point applied to the per-group operand sums, f32 accumulation.  What
+// differs is the shape of the work, taken from the streaming probe
+// (imh_diag_stream_read): one launch moves the most bytes when every compute
+// unit gets the same share (grids of a multiple of the CU count beat the
+// 608 / 160 workgroups that one 16-row tile per workgroup gives the Qwen3-4B
+// gate+up / down weights), and a wave-wide load of 8 rows x 128 contiguous
+// bytes beats 16 rows x 64.
+//
+//  * Workgroup b of NWG owns the row band [N b / NWG, N (b+1) / NWG) of each
+//    matrix (one matrix, or the gate/up pair whose rows the epilogue joins),
+//    cut into tiles of 8 rows (the last one masked).  Its waves split the K
+//    groups of every tile: wave (mat, part) takes group pairs [p0, p0 + np)
+//    of matrix mat in every tile, all of its weight loads issued up front.
+//  * MFMA mapping.  B column j = r + 8h: row r of the tile, group h of the
+//    pair (one 16-byte load per lane: row j & 7, group j >> 3, quarter lane >>
+//    4).  A row i = 8h + 4·plane + b: batch row b, f16 hi (plane 0) or lo
+//    (plane 1) half of group h's operand.  Of the 16 x 16 result only the
+//    entries whose row and column share h are used; lane l holds rows
+//    4(l >> 4) .. +3 of column l & 15, i.e. the batch rows of one (h, plane)
+//    for one (r, h) when (l >> 5) == ((l >> 3) & 1).
+//  * The activation operand image (all of K) and the band's scales / zeros
+//    are staged once per workgroup in LDS, from loads issued ahead of the
+//    weight loads; one barrier, then the MFMAs consume the weights as they
+//    arrive; a second barrier joins the waves' partial rows (in part order:
+//    deterministic).
+#include <hip/hip_runtime.h>
+#include <hip/hip_fp16.h>
+
+#include <algorithm>
+
+#include "imh_internal.h"
+#include "int4_matvec_kernel.h"
+
+namespace imh_int4 {
+
+namespace {
+
+constexpr int kRS = kGS + 8;   // halfs per operand row in LDS (16-byte pad)
+constexpr int kSZC = 2;        // scale/zero words per thread loaded ahead of the weights
+
+struct BandLds {
+    size_t img, gs, sz, red, total;
+};
+
+__host__ __device__ inline BandLds band_lds(int G, int BM, int NMAT, int TM, int waves) {
+    BandLds L;
+    L.img = 0;
+    L.gs = L.img + (size_t)G * 2 * BM * kRS * 2;
+    L.sz = L.gs + (size_t)G * 2 * BM * 4;
+    L.red = L.sz + (size_t)NMAT * G * TM * 8 * 4;
+    L.red = (L.red + 15) & ~(size_t)15;
+    L.total = L.red + (size_t)waves * TM * 8 * 16;
+    return L;
+}
+
+// grid NWG; block 64 * NMAT * W.
+template <int NMAT, int EPI, int TM, int NP, int BM, int XC, int PD = 1>
+__global__ void __launch_bounds__(512) int4_band_kernel(MatPtrs mp, const __half *__restrict__ x,
+                                                       const __half *__restrict__ awq, int N, int K, int B, int W) {
+    extern __shared__ __attribute__((aligned(16))) uint8_t lds_b[];
+    const int tid = threadIdx.x, nthr = blockDim.x;
+    const int lane = tid & 63, wave = tid >> 6, waves = nthr >> 6;
+    const int mat = wave / W, part = wave - mat * W;
+    const int G = K / kGS, P = G / 2;
+    const int p0 = (part * P) / W;
+    const int np = ((part + 1) * P) / W - p0;
+    // (the host keeps N * NWG below 2^32)
+    const int rb = (int)(((uint32_t)N * blockIdx.x) / gridDim.x);
+    const int re = (int)(((uint32_t)N * (blockIdx.x + 1)) / gridDim.x);
+    const int nrows = re - rb;
+    const int RT = TM * 8;                     // band rows held in LDS (padded)
+
+    const BandLds L = band_lds(G, BM, NMAT, TM, waves);
+    _Float16 *img = reinterpret_cast<_Float16 *>(lds_b + L.img);
+    float *gsl = reinterpret_cast<float *>(lds_b + L.gs);
+    uint32_t *szs = reinterpret_cast<uint32_t *>(lds_b + L.sz);
+    float4_t *red = reinterpret_cast<float4_t *>(lds_b + L.red);
+
+    // (a) activation chunks: chunk c = group c >> 4, elements (c & 15) * 8 ..
+    // +7; 16 consecutive threads (one DPP row) hold one group
+    // Loads that may have nothing to read go through buffer resources (an
+    // out-of-range lane reads zeros and touches no memory): a branch around a
+    // load makes the compiler wait for every load in flight where it joins.
+    constexpr uint32_t kRsrcWord3 = 0x00020000u;
+    const int nchunks = G * 16;
+    const __amdgpu_buffer_rsrc_t awq_r =
+        __builtin_amdgcn_make_buffer_rsrc((void *)awq, 0, awq ? K * 2 : 0, kRsrcWord3);
+    u32x4_t xv[XC][BM], wv[XC];
+#pragma unroll
+    for (int i = 0; i < XC; i++) {
+        const int c = min(i * nthr + tid, nchunks - 1);
+        const size_t e = (size_t)c * 8;
+#pragma unroll
+        for (int b = 0; b < BM; b++) xv[i][b] = *reinterpret_cast<const u32x4_t *>(x + (size_t)min(b, B - 1) * K + e);
+        wv[i] = __builtin_bit_cast(u32x4_t, __builtin_amdgcn_raw_buffer_load_b128(awq_r, (int)(e * 2), 0, 0));
+    }
+    // (b) scale / zero words of the band: word w of matrix m covers groups
+    // 2p, 2p + 1 of band row w / P (the band's rows are contiguous)
+    const int szw = nrows * P;
+    uint32_t sv[kSZC], zv[kSZC];
+#pragma unroll
+    for (int i = 0; i < kSZC; i++) {
+        const int w = min(i * nthr + tid, NMAT * szw - 1);
+        const int m = (NMAT == 2 && w >= szw) ? 1 : 0;
+        const size_t src = (size_t)rb * P + (w - m * szw);
+        sv[i] = reinterpret_cast<const uint32_t *>(m ? mp.scales[1] : mp.scales[0])[src];
+        zv[i] = reinterpret_cast<const uint32_t *>(m ? mp.zeros[1] : mp.zeros[0])[src];
+    }
+    // issue order: every wave's small loads ahead of any weight load in the
+    // CU's memory pipeline, which returns them in order (an execution barrier
+    // only: nothing waits for the loads here)
+    asm volatile("" ::: "memory");
+    __builtin_amdgcn_s_barrier();
+    asm volatile("" ::: "memory");
+    // (c) weights: lane (j = lane & 15, kq = lane >> 4), row j & 7 of each
+    // tile, group j >> 3 of each pair; rows past the band load nothing
+    const int jr = lane & 7, jh = (lane >> 3) & 1, kq = lane >> 4;
+    const uint8_t *wdata = (NMAT == 2 && mat) ? mp.data[1] : mp.data[0];
+    // Issued pair by pair, tiles inner (the order the MFMAs consume them):
+    // the first PD pairs now, each later one PD pairs ahead of its MFMAs, so
+    // the MFMAs run while the rest streams in (a wave whose next load cannot
+    // issue waits there, in order).
+    const __amdgpu_buffer_rsrc_t w_r = __builtin_amdgcn_make_buffer_rsrc(
+        (void *)(wdata + (size_t)rb * (K / 2)), 0, nrows * (K / 2), kRsrcWord3);
+    const int woff = jr * (K / 2) + jh * 64 + kq * 16;
+    u32x4_t wq[TM][NP];
+    auto load_pair = [&](int i) __attribute__((always_inline)) {
+#pragma unroll
+        for (int t = 0; t < TM; t++)
+            wq[t][i] = __builtin_bit_cast(u32x4_t, __builtin_amdgcn_raw_buffer_load_b128(
+                                                       w_r, woff + t * 8 * (K / 2) + (p0 + min(i, np - 1)) * 128, 0, 0));
+    };
+#pragma unroll
+    for (int i = 0; i < PD && i < NP; i++) load_pair(i);
+
+    // (d) scale/zero words -> LDS [mat][g][band row] (s | z << 16)
+    auto sz_store = [&](int w, uint32_t s2, uint32_t z2) __attribute__((always_inline)) {
+        const int m = (NMAT == 2 && w >= szw) ? 1 : 0;
+        const int wl = w - m * szw;
+        const int rr = wl / P, p = wl - rr * P;
+        szs[(m * G + 2 * p) * RT + rr] = (s2 & 0xFFFFu) | (z2 << 16);
+        szs[(m * G + 2 * p + 1) * RT + rr] = (s2 >> 16) | (z2 & 0xFFFF0000u);
+    };
+#pragma unroll
+    for (int i = 0; i < kSZC; i++) sz_store(min(i * nthr + tid, NMAT * szw - 1), sv[i], zv[i]);   // host: all fit
+    // (e) operand image -> LDS [g][plane][b][kRS], group sums [g][plane][b]
+#pragma unroll
+    for (int i = 0; i < XC; i++) {
+        const int c = min(i * nthr + tid, nchunks - 1);
+        const bool live = i * nthr + tid < nchunks;   // uniform over the 16-thread row
+        const int g = c >> 4;
+        const _Float16 *wh = reinterpret_cast<const _Float16 *>(&wv[i]);
+#pragma unroll
+        for (int b = 0; b < BM; b++) {
+            const _Float16 *xh = reinterpret_cast<const _Float16 *>(&xv[i][b]);
+            float v[8];
+#pragma unroll
+            for (int e = 0; e < 8; e++) v[e] = awq ? div_awq((float)xh[e], (float)wh[e]) : (float)xh[e];
+            half8_t hi, lo;
+            float sh, sl;
+            chunk_operands(v, hi, lo, sh, sl);
+            _Float16 *dst = img + ((size_t)(g * 2) * BM + b) * kRS + (c & 15) * 8;
+            if (live) {
+                *reinterpret_cast<half8_t *>(dst) = hi;
+                *reinterpret_cast<half8_t *>(dst + BM * kRS) = lo;
+            }
+            sh = row16_sum(sh);
+            sl = row16_sum(sl);
+            if (live && (c & 15) == 0) {
+                gsl[(g * 2) * BM + b] = sh * kTwoM24;
+                gsl[(g * 2 + 1) * BM + b] = sl * kTwoM24;
+            }
+        }
+    }
+    // LDS-only barrier: the weight loads stay in flight across it
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
+    __builtin_amdgcn_s_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+
+    // (f) MFMA.  A row of this lane: i = lane & 15 -> (ah, aplane, ab); the
+    // lane's result rows: (h, plane) = (lane >> 5, (lane >> 4) & 1)
+    const int ai = lane & 15;
+    const int ah = ai >> 3, aplane = (ai >> 2) & 1, ab = ai & 3;
+    const bool a_live = ab < BM;
+    const int dplane = (lane >> 4) & 1;
+    const int ntile = (nrows + 7) >> 3;
+    float acc[TM][BM];
+#pragma unroll
+    for (int t = 0; t < TM; t++)
+#pragma unroll
+        for (int b = 0; b < BM; b++) acc[t][b] = 0.0f;
+#pragma unroll
+    for (int i = 0; i < NP; i++) {
+        if (i + PD < NP) load_pair(i + PD);
+        if (i < np) {
+            const int g = 2 * (p0 + i) + jh;             // this lane's column group
+            const int ga = 2 * (p0 + i) + ah;            // this lane's A-row group
+            const _Float16 *xa = img + ((size_t)(ga * 2 + aplane) * BM + min(ab, BM - 1)) * kRS + kq * 32;
+            half8_t av[4];
+#pragma unroll
+            for (int m = 0; m < 4; m++) {
+                av[m] = *reinterpret_cast<const half8_t *>(xa + m * 8);
+                if (!a_live) av[m] = (half8_t){0, 0, 0, 0, 0, 0, 0, 0};
+            }
+            const float *gp = gsl + (g * 2 + dplane) * BM;
+            float gsv[BM];
+#pragma unroll
+            for (int b = 0; b < BM; b++) gsv[b] = gp[b];
+#pragma unroll
+            for (int t = 0; t < TM; t++) {
+                if (t < ntile) {
+                    const uint32_t sz = szs[(mat * G + g) * RT + t * 8 + jr];
+                    const float s24 = (float)__builtin_bit_cast(_Float16, (uint16_t)(sz & 0xFFFFu)) * kTwo24;
+                    const float z = (float)__builtin_bit_cast(_Float16, (uint16_t)(sz >> 16));
+                    float4_t accg = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+                    for (int m = 0; m < 4; m++) {
+                        const uint32_t w = wq[t][i][m];
+                        const uint32_t q0 = __builtin_amdgcn_perm(w, 0u, 0x0C050C04u);  // b0, b1
+                        const uint32_t q1 = __builtin_amdgcn_perm(w, 0u, 0x0C070C06u);  // b2, b3
+                        const u32x4_t bq = (u32x4_t){q0, q1, q0 & 0x00F000F0u, q1 & 0x00F000F0u};
+                        accg = __builtin_amdgcn_mfma_f32_16x16x32_f16(av[m], __builtin_bit_cast(half8_t, bq), accg,
+                                                                      0, 0, 0);
+                    }
+#pragma unroll
+                    for (int b = 0; b < BM; b++)
+                        acc[t][b] = __builtin_fmaf(s24, __builtin_fmaf(-z, gsv[b], accg[b]), acc[t][b]);
+                }
+            }
+        }
+    }
+    // (g) rows r = lane & 7 of each tile sit at lanes r (h 0, hi), r + 16
+    // (h 0, lo), r + 40 (h 1, hi), r + 56 (h 1, lo)
+#pragma unroll
+    for (int t = 0; t < TM; t++) {
+        float4_t v = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+        for (int b = 0; b < BM; b++) {
+            float a = acc[t][b];
+            a += __shfl_down(a, 16);
+            a += __shfl_down(a, 40);
+            v[b] = a;
+        }
+        if (lane < 8) red[(wave * TM + t) * 8 + lane] = v;
+    }
+    __syncthreads();
+    for (int o = tid; o < RT * BM; o += nthr) {
+        const int r = o % RT, b = o / RT;
+        const int row = rb + r;
+        if (r >= nrows || b >= B) continue;
+        const int t = r >> 3, rl = r & 7;
+        float sum[NMAT];
+#pragma unroll
+        for (int mt = 0; mt < NMAT; mt++) {
+            float s = 0.0f;
+            for (int p = 0; p < W; p++) s += red[((mt * W + p) * TM + t) * 8 + rl][b];
+            sum[mt] = s;
+        }
+        if (EPI == EPI_SILU || EPI == EPI_GELU) {
+            const float g = sum[0], u = sum[NMAT - 1];
+            float act;
+            if (EPI == EPI_SILU) {
+                act = g / (1.0f + __expf(-g));
+            } else {
+                float inner = 0.7978845608f * (g + 0.044715f * g * g * g);
+                inner = fminf(fmaxf(inner, -10.0f), 10.0f);
+                act = 0.5f * g * (1.0f + tanhf(inner));
+            }
+            mp.out[0][(size_t)b * N + row] = __float2half(act * u);
+        } else {
+#pragma unroll
+            for (int mt = 0; mt < NMAT; mt++) mp.out[mt][(size_t)b * N + row] = __float2half(sum[mt]);
+        }
+    }
+}
+
+struct BandLaunch {
+    dim3 grid, block;
+    size_t lds;
+    hipStream_t st;
+    int N, K, B, W;
+};
+
+template <int NMAT, int EPI, int TM, int NP, int BM>
+void launch_xc(int xc, const BandLaunch &L, const MatPtrs &mp, const __half *x, const __half *awq) {
+    if (xc == 1)
+        hipLaunchKernelGGL((int4_band_kernel<NMAT, EPI, TM, NP, BM, 1>), L.grid, L.block, L.lds, L.st, mp, x, awq, L.N,
+                           L.K, L.B, L.W);
+    else
+        hipLaunchKernelGGL((int4_band_kernel<NMAT, EPI, TM, NP, BM, 3>), L.grid, L.block, L.lds, L.st, mp, x, awq, L.N,
+                           L.K, L.B, L.W);
+}
+
+template <int NMAT, int EPI, int TM, int NP>
+void launch_bm(int bm, int xc, const BandLaunch &L, const MatPtrs &mp, const __half *x, const __half *awq) {
+    if (bm == 1) launch_xc<NMAT, EPI, TM, NP, 1>(xc, L, mp, x, awq);
+    else launch_xc<NMAT, EPI, TM, NP, 2>(xc, L, mp, x, awq);
+}
+
+// (TM, NP) instantiated: (2, 5), (3, 5) and (5, 3); the host picks the
+// smallest TM that holds the band.
+template <int NMAT, int EPI>
+void launch_shape(int tm, int bm, int xc, const BandLaunch &L, const MatPtrs &mp, const __half *x, const __half *awq) {
+    if (tm <= 2) launch_bm<NMAT, EPI, 2, 5>(bm, xc, L, mp, x, awq);
+    else if (tm <= 3) launch_bm<NMAT, EPI, 3, 5>(bm, xc, L, mp, x, awq);
+    else launch_bm<NMAT, EPI, 5, 3>(bm, xc, L, mp, x, awq);
+}
+
+}  // namespace
+
+// Launches the band kernel when it applies (plain x / awq source, B <= 2, no
+// row segments, an even number of groups, the shape within the instantiated
+// tiles and the LDS budget); *used reports whether it did.
+int launch_band_matvec(hipStream_t st, int cus, int B, int nmat, int epi, int N, int K, const MatPtrs &mp,
+                       const __half *x, const __half *awq, bool *used) {
+    *used = false;
+    const int G = K / kGS;
+    if (B < 1 || B > 2 || mp.seg[0] != 0 || G % 2 || G < 2) return IMH_OK;
+    for (int i = 0; i < nmat; i++)
+        if ((reinterpret_cast<uintptr_t>(mp.scales[i]) | reinterpret_cast<uintptr_t>(mp.zeros[i])) & 3) return IMH_OK;
+    const int P = G / 2;
+    const int ntiles = (N + 7) / 8;
+    // workgroups: one band per CU, more (bands of up to 5 tiles) for tall matrices
+    const int nwg = std::min(std::max(cus, (ntiles + 4) / 5), N);
+    if ((uint64_t)N * nwg >= (1ull << 32)) return IMH_OK;
+    const int rows = (N + nwg - 1) / nwg;
+    const int tm = (rows + 7) / 8;
+    if (tm > 5) return IMH_OK;
+    const int TM = tm <= 2 ? 2 : tm <= 3 ? 3 : 5, NPmax = tm <= 3 ? 5 : 3;
+    // waves per matrix: as few as keep each wave within NPmax pairs
+    const int W = std::min((P + NPmax - 1) / NPmax, 8 / nmat);
+    const int np = (P + W - 1) / W;
+    if (np > NPmax) return IMH_OK;
+    const int nthr = 64 * W * nmat;
+    const int xc = (G * 16 + nthr - 1) / nthr;
+    if (xc > 3 || nmat * rows * P > kSZC * nthr) return IMH_OK;
+    const size_t lds = band_lds(G, B, nmat, TM, W * nmat).total;
+    if (lds > 64 * 1024) return IMH_OK;
+    BandLaunch L{dim3(nwg), dim3(nthr), lds, st, N, K, B, W};
+    if (nmat == 1)
+        launch_shape<1, EPI_STORE>(tm, B, xc, L, mp, x, awq);
+    else if (epi == EPI_SILU)
+        launch_shape<2, EPI_SILU>(tm, B, xc, L, mp, x, awq);
+    else if (epi == EPI_GELU)
+        launch_shape<2, EPI_GELU>(tm, B, xc, L, mp, x, awq);
+    else
+        launch_shape<2, EPI_STORE>(tm, B, xc, L, mp, x, awq);
+    IMH_HIP(hipGetLastError());
+    *used = true;
+    return IMH_OK;
+}
+
+}  // namespace imh_int4

@@ -67,6 +67,13 @@ def gpu_layout_y(q, x16, awq16=None):
     (2560, 9728, 1, True),    # Qwen3-4B down projection
     (2560, 9728, 8, True),
     (4096, 2560, 1, False),   # Qwen3-4B Q projection
+    (1003, 1024, 2, True),    # batch 2, ragged N (not a multiple of 8)
+    (1003, 384, 1, False),    # an odd number of groups
+    (24, 256, 1, True),       # one group pair
+    (2560, 4096, 1, True),    # Qwen3-4B O projection
+    (1024, 2560, 2, False),   # Qwen3-4B K / V projection, batch 2
+    (5000, 1024, 1, True),    # bands of 17-24 rows
+    (151936 // 8, 2560, 1, False),   # an LM-head-like tall matrix (bands of 5 tiles)
 ])
 def test_projection_matches_oracle(dev, stream, n, k, batch, awq):
     w, s = make_weight(n, k, seed=n + k + batch, awq=awq)
@@ -84,7 +91,7 @@ def test_projection_matches_oracle(dev, stream, n, k, batch, awq):
     assert_close(got, lay, what="projection vs GPU-layout semantics")
 
 
-@pytest.mark.parametrize("batch", [1, 4, 8])
+@pytest.mark.parametrize("batch", [1, 2, 4, 8])
 @pytest.mark.parametrize("act", ["silu", "gelu"])
 def test_fused_gate_up_qwen_shape(dev, stream, batch, act):
     n, k = 9728, 2560
@@ -185,7 +192,7 @@ def test_ffn_block_repeated_launches(dev, stream):
         stream.sync()
 
 
-@pytest.mark.parametrize("batch,awq", [(1, True), (8, False)])
+@pytest.mark.parametrize("batch,awq", [(1, True), (2, False), (8, False)])
 def test_batched_gate_up(dev, stream, batch, awq):
     n, k = 9728, 2560
     wg, s = make_weight(n, k, seed=21, awq=awq)
