@@ -249,8 +249,8 @@ def bench_gemm(dev, stream, ops, m, kk, nn, prec, steps, warmup, eager=False, re
 def bench_probe(dev, stream, ops, steps, warmup, sweep=True):
     """Streaming probe (imh_diag_stream_read): the batch-1 gate+up and down weight bytes read
     with no compute, rotating over >= 512 MB of buffers like the matvec measurement.  `kernel`:
-    the matvec's own launch (gate+up: 608 workgroups, each one 16-row tile of both weights with 4
-    waves per weight; down: 160 workgroups of one 16-row tile, 16 waves).  With `sweep`: TILE
+    the row-band matvec's own launch (one band of rows per CU; gate+up: 4 waves per weight,
+    down: 8).  With `sweep`: TILE
     shapes of 8 / 16 rows, 1-4 tiles per workgroup and 1-16 waves, and FLAT grids of contiguous
     runs (the best of each reported as *_best)."""
     sink = dev.empty((1,), np.uint32)
@@ -260,13 +260,14 @@ def bench_probe(dev, stream, ops, steps, warmup, sweep=True):
     us = 1e3 * time_loop(dev, stream, lambda i: ops.diag_stream_read(
         stream, tiny, 64, 128, sink, mode=ops.PROBE_FLAT, grid=256, threads=256), steps, warmup) / steps
     out["launch_floor"] = {"us": round(us, 2), "bytes": 4096, "grid": 256, "threads": 256}
-    cases = [("gate_up", F, H, 2, (16, 1, 4)), ("down", H, F, 1, (16, 1, 16))]
+    cus = dev.info()["compute_units"]
+    cases = [("gate_up", F, H, 2, 4), ("down", H, F, 1, 8)]
     for name, n, k, nmat, own in cases:
         nbytes = nmat * n * k // 2
         reps = max(2, math.ceil(512e6 / nbytes))
         bufs = [dev.empty((nbytes,), np.uint8) for _ in range(reps)]
         G = k // 128
-        runs = [("kernel", dict(mode=ops.PROBE_TILE, nmat=nmat, rows=own[0], tiles=own[1], waves=own[2]))]
+        runs = [("kernel", dict(mode=ops.PROBE_BAND, nmat=nmat, waves=own, grid=cus))]
         if sweep:
             for rows in (16, 8):
                 for tiles in (1, 2, 4):

@@ -12,6 +12,7 @@ extern "C" {
 
 #define IMH_PROBE_TILE 0
 #define IMH_PROBE_FLAT 1
+#define IMH_PROBE_BAND 2
 
 /* Launch shape of the streaming probe.  TILE: ceil(n / (rows * tiles))
  * workgroups of 64 * waves * nmat threads; each owns `tiles` tiles of `rows`
@@ -19,7 +20,10 @@ extern "C" {
  * back, `waves` waves per weight splitting the tiles' loads (16 rows: one
  * 64-byte group run per row per wave-load, the INT4 matvec's pattern; 8 rows:
  * two adjacent groups, 128 bytes per row).  FLAT: `grid` workgroups of
- * `threads` threads, each reading one contiguous run of the bytes. */
+ * `threads` threads, each reading one contiguous run of the bytes.  BAND:
+ * the row-band matvec's launch -- `grid` workgroups of 64 * waves * nmat
+ * threads, workgroup b reading rows [n b / grid, n (b+1) / grid) of each
+ * weight in 8-row tiles, 128 bytes per row per wave-load (k / 128 even). */
 typedef struct {
     uint32_t mode;
     uint32_t nmat;

@@ -448,6 +448,26 @@ typedef struct {
     uint32_t max_seq_len;
 } imh_fp16_kv_cache;
 
+/* Cache positions of one step of token_count tokens from seq_pos on, for a
+ * layer with the given sliding window (0 = full attention): the arithmetic of
+ * KvCacheAndAttentionParams (attention.rs:141-163) and the cache's ring_pos /
+ * effective_max_seq_len (turboquant/cache.rs:382-400):
+ *   stride    = window_size ? window_size : max_seq_len  (the layer cache's max_seq_len)
+ *   write_pos = window_size ? seq_pos % window_size : seq_pos  (base_pos of the cache writes)
+ *   attn_base = window_size ? min(min(seq_pos + T, W) - T, W - T), saturating at 0 : seq_pos
+ *   attn_len  = attn_base + token_count  (seq_len of the attention ops; token t
+ *               attends to slots [0, attn_base + t + 1))
+ * IMH_ERANGE when seq_pos + token_count exceeds max_seq_len (the step guard of
+ * pipeline.rs:270-279), IMH_EINVAL for token_count 0 or above the stride. */
+typedef struct {
+    uint32_t stride;
+    uint32_t write_pos;
+    uint32_t attn_base;
+    uint32_t attn_len;
+} imh_kv_positions;
+int imh_kv_positions_for(uint32_t seq_pos, uint32_t token_count, uint32_t window_size, uint32_t max_seq_len,
+                         imh_kv_positions *out);
+
 /* encode_kv_scatter (ops/kv.rs:35-58, kv_scatter.metal:20-45) for the K
  * (is_k = 1) or V (is_k = 0) array: proj [batch][token_count][num_kv_heads][head_dim]
  * f16; token t of sequence b goes to position
@@ -519,6 +539,12 @@ typedef struct {
     int kv_cache;       /* IMH_KV_TURBOQUANT or IMH_KV_FP16 */
     double rope_theta;
     uint64_t tq_seed;   /* TurboQuant rotation seed (QJL uses seed + 1) */
+    /* per-layer sliding-window sizes, 0 = full attention, or NULL for none
+     * (TurboQuantMetalConfig::window_sizes, turboquant/cache.rs:92-135): a
+     * windowed layer's cache is a ring of window_size positions, written at
+     * position % window_size, and attends over min(position + 1, window_size)
+     * slots (attention.rs:141-163).  Copied at creation. */
+    const uint32_t *window_sizes;
 } imh_decoder_config;
 
 /* The weights of one layer (LayerWeights of metal/weights.rs) as the schedule

@@ -165,7 +165,14 @@ class DecoderConfig(C.Structure):
         ("kv_cache", C.c_int),
         ("rope_theta", C.c_double),
         ("tq_seed", C.c_uint64),
+        ("window_sizes", C.c_void_p),
     ]
+
+
+class KvPositions(C.Structure):
+    """imh_kv_positions (KvCacheAndAttentionParams positions, attention.rs:141-163)."""
+
+    _fields_ = [(f, C.c_uint32) for f in ("stride", "write_pos", "attn_base", "attn_len")]
 
 
 class DecoderLayerWeights(C.Structure):
@@ -231,6 +238,7 @@ SIGNATURES = {
                                       C.POINTER(AffineInt4Weight), P, P, I]),
     "imh_affine_gemm_int4": (I, [P, P, U32, C.POINTER(AffineInt4Weight), P, I]),
     "imh_encode_affine_projection_int8": (I, [P, P, U32, C.POINTER(AffineInt8Weight), P]),
+    "imh_kv_positions_for": (I, [U32, U32, U32, U32, C.POINTER(KvPositions)]),
     "imh_diag_stream_read": (I, [P, P, U32, U32, C.POINTER(ProbeShape), P]),
     "imh_encode_quantize_input_q8": (I, [P, P, U32, U32, P, P]),
     "imh_encode_affine_matvec_int4xq8": (I, [P, P, P, U32, C.POINTER(AffineInt4Weight), P]),

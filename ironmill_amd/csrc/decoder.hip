@@ -54,6 +54,9 @@ struct imh_decoder {
     imh_tq_tables *tq = nullptr;       // in use: own_tq or the caller's (imh_decoder_set_tq_tables)
     std::vector<imh_tq_kv_cache> tq_caches;
     std::vector<imh_fp16_kv_cache> fp16_caches;
+    // per layer: sliding-window size (0 = full attention); a windowed layer's
+    // cache is a ring of that many positions
+    std::vector<uint32_t> windows;
 
     // mirror of positions for range checks: advanced by eager steps (not by
     // capture), refreshed from the device by imh_decoder_sync_positions
@@ -112,10 +115,18 @@ int imh_decoder_create(imh_device *dev, const imh_decoder_config *cfg, imh_decod
     if (c.kv_cache != IMH_KV_TURBOQUANT && c.kv_cache != IMH_KV_FP16)
         return imh::fail(IMH_EINVAL, std::string(who) + ": unknown kv_cache kind");
     if (c.batch > 65535) return imh::fail(IMH_EINVAL, std::string(who) + ": batch above 65535");
+    if (c.window_sizes)
+        for (uint32_t l = 0; l < c.num_layers; l++)
+            if (c.window_sizes[l] > c.max_seq_len)
+                return imh::fail(IMH_EINVAL, std::string(who) + ": layer " + std::to_string(l) +
+                                                 " window_size above max_seq_len");
     int rc = imh::use_device(dev);
     if (rc) return rc;
 
     imh_decoder *d = new imh_decoder();
+    d->windows.assign(c.num_layers, 0);
+    if (c.window_sizes) d->windows.assign(c.window_sizes, c.window_sizes + c.num_layers);
+    d->cfg.window_sizes = nullptr;   // the decoder keeps its own copy
     d->dev = dev;
     d->cfg = c;
     if (d->cfg.attn_scale == 0.0f) d->cfg.attn_scale = 1.0f / std::sqrt((float)c.head_dim);
@@ -180,18 +191,22 @@ int imh_decoder_create(imh_device *dev, const imh_decoder_config *cfg, imh_decod
         if (e != hipSuccess) return cleanup(imh::hip_fail(e, "imh_decoder_create: seq_lens"));
     }
 
-    // KV caches: one allocation for every layer, zeroed
-    const size_t rows = B * c.num_kv_heads * (size_t)c.max_seq_len;
-    size_t per_layer = 0;
+    // KV caches: one allocation for every layer, zeroed; a layer's positions:
+    // max_seq_len, or its window (the buffer stride of a sliding-window layer,
+    // effective_max_seq_len, turboquant/cache.rs:394-400)
     if (c.kv_cache == IMH_KV_TURBOQUANT) {
         rc = imh_tq_tables_create(dev, c.head_dim, 8, c.tq_seed, &d->own_tq);
         if (rc) return cleanup(rc);
         d->tq = d->own_tq;
-        per_layer = 2 * align256(rows * c.head_dim) + 3 * align256(rows * 4);
-    } else {
-        per_layer = 2 * align256(rows * c.head_dim * 2);
     }
-    const size_t kv_bytes = per_layer * c.num_layers;
+    auto stride_of = [&](uint32_t l) { return d->windows[l] ? d->windows[l] : c.max_seq_len; };
+    auto layer_bytes = [&](uint32_t l) {
+        const size_t rows = B * c.num_kv_heads * (size_t)stride_of(l);
+        return c.kv_cache == IMH_KV_TURBOQUANT ? 2 * align256(rows * c.head_dim) + 3 * align256(rows * 4)
+                                               : 2 * align256(rows * c.head_dim * 2);
+    };
+    size_t kv_bytes = 0;
+    for (uint32_t l = 0; l < c.num_layers; l++) kv_bytes += layer_bytes(l);
     e = hipMalloc(&d->kv_arena, kv_bytes);
     if (e != hipSuccess)
         return cleanup(imh::fail(IMH_ENOMEM, std::string(who) + ": KV cache of " + std::to_string(kv_bytes) + " bytes"));
@@ -199,7 +214,9 @@ int imh_decoder_create(imh_device *dev, const imh_decoder_config *cfg, imh_decod
     if (e != hipSuccess) return cleanup(imh::hip_fail(e, "imh_decoder_create: KV clear"));
     char *kv = static_cast<char *>(d->kv_arena);
     for (uint32_t l = 0; l < c.num_layers; l++) {
-        char *p = kv + per_layer * l;
+        char *p = kv;
+        kv += layer_bytes(l);
+        const size_t rows = B * c.num_kv_heads * (size_t)stride_of(l);
         if (c.kv_cache == IMH_KV_TURBOQUANT) {
             imh_tq_kv_cache t{};
             t.k_codes = reinterpret_cast<uint8_t *>(p);
@@ -214,7 +231,7 @@ int imh_decoder_create(imh_device *dev, const imh_decoder_config *cfg, imh_decod
             t.batch = c.batch;
             t.num_kv_heads = c.num_kv_heads;
             t.head_dim = c.head_dim;
-            t.max_seq_len = c.max_seq_len;
+            t.max_seq_len = stride_of(l);
             d->tq_caches.push_back(t);
         } else {
             imh_fp16_kv_cache f{};
@@ -223,7 +240,7 @@ int imh_decoder_create(imh_device *dev, const imh_decoder_config *cfg, imh_decod
             f.batch = c.batch;
             f.num_kv_heads = c.num_kv_heads;
             f.head_dim = c.head_dim;
-            f.max_seq_len = c.max_seq_len;
+            f.max_seq_len = stride_of(l);
             d->fp16_caches.push_back(f);
         }
     }
@@ -365,9 +382,28 @@ int imh_decoder_step(imh_decoder *d, imh_stream *s, const uint32_t *token_ids, u
         // TurboQuant: the token's cache write runs inside the attention launch;
         // with QK-norms at head_dim = rotary_dim = 128 so do the norm and
         // rotation of K (in the writing workgroup) and Q (in the prologue)
+        const uint32_t win = d->windows[l];
         const bool fold = c.kv_cache == IMH_KV_TURBOQUANT && w.q_norm && w.k_norm && c.head_dim == 128 &&
-                          (c.rotary_dim == 0 || c.rotary_dim == 128);
-        if (c.kv_cache == IMH_KV_TURBOQUANT) {
+                          (c.rotary_dim == 0 || c.rotary_dim == 128) && win == 0;
+        if (win) {
+            // sliding window (attention.rs:141-163): the cache is a ring of
+            // `win` positions; the token goes to positions[b] % win and the
+            // attention covers min(seq_lens[b], win) slots, the bound being the
+            // ring's size.  RoPE uses the absolute position.
+            IMH_TRY(imh_encode_qk_norm_rope(s, &qp));
+            if (c.kv_cache == IMH_KV_TURBOQUANT) {
+                IMH_TRY(imh_encode_turboquant_cache_write_kv(s, d->tq, &d->tq_caches[l], d->k, d->v, 1, 0,
+                                                             d->positions));
+                IMH_TRY(imh_encode_turboquant_attention(s, d->tq, &d->tq_caches[l], d->q, c.num_heads, 0,
+                                                        d->seq_lens, c.attn_scale, d->attn_out, 0));
+            } else {
+                const imh_fp16_kv_cache *kc = &d->fp16_caches[l];
+                IMH_TRY(imh_encode_kv_scatter(s, kc, d->k, 1, 0, d->positions, 1));
+                IMH_TRY(imh_encode_kv_scatter(s, kc, d->v, 1, 0, d->positions, 0));
+                IMH_TRY(imh_encode_fp16_attention(s, kc, d->q, c.num_heads, 1, 0, d->seq_lens, c.attn_scale,
+                                                  d->attn_out, 0));
+            }
+        } else if (c.kv_cache == IMH_KV_TURBOQUANT) {
             if (!fold) IMH_TRY(imh_encode_qk_norm_rope(s, &qp));
             IMH_TRY(imh::encode_tq_write_attend(s, d->tq, &d->tq_caches[l], d->q, d->k, d->v, c.num_heads,
                                                 d->seq_lens, c.attn_scale, d->attn_out, fold ? &qp : nullptr));
@@ -435,6 +471,11 @@ int imh_decoder_write_kv(imh_decoder *d, imh_stream *s, uint32_t layer, const ui
     if (layer >= d->cfg.num_layers) return imh::fail(IMH_EINVAL, "imh_decoder_write_kv: layer out of range");
     if ((uint64_t)base_pos + token_count > d->cfg.max_seq_len)
         return imh::fail(IMH_ERANGE, "imh_decoder_write_kv: base_pos + token_count beyond max_seq_len");
+    // a windowed layer's ring takes positions modulo its window (the cache
+    // write wraps at the cache's max_seq_len); more tokens than the ring holds
+    // would overwrite each other within one write
+    if (d->windows[layer] && token_count > d->windows[layer])
+        return imh::fail(IMH_EINVAL, "imh_decoder_write_kv: token_count above the layer's window");
     if (d->cfg.kv_cache == IMH_KV_TURBOQUANT) {
         return imh_encode_turboquant_cache_write_kv(s, d->tq, &d->tq_caches[layer], k_proj, v_proj, token_count,
                                                     base_pos, nullptr);

@@ -61,6 +61,37 @@ __global__ void __launch_bounds__(1024) probe_tile_kernel(const uint8_t *__restr
     if (x == key) sink[0] = x;
 }
 
+// BAND: the row-band matvec's launch -- workgroup b of gridDim.x reads rows
+// [N b / NWG, N (b+1) / NWG) of each of NMAT weights, in tiles of 8 rows x
+// 128 bytes per wave-load, `waves` waves per weight splitting the group
+// pairs; loads past the band read nothing (buffer-resource bounds).
+template <int TM, int NP, int NMAT>
+__global__ void __launch_bounds__(1024) probe_band_kernel(const uint8_t *__restrict__ w, int N, int K, uint32_t key,
+                                                         uint32_t *__restrict__ sink) {
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, waves = (blockDim.x >> 6) / NMAT;
+    const int mat = wave / waves, part = wave - mat * waves;
+    const int P = K / 256;
+    const int p0 = (part * P) / waves, np = ((part + 1) * P) / waves - p0;
+    const int rb = (int)(((uint32_t)N * blockIdx.x) / gridDim.x);
+    const int re = (int)(((uint32_t)N * (blockIdx.x + 1)) / gridDim.x);
+    const __amdgpu_buffer_rsrc_t r = __builtin_amdgcn_make_buffer_rsrc(
+        (void *)(w + (size_t)mat * N * (K / 2) + (size_t)rb * (K / 2)), 0, (re - rb) * (K / 2), 0x00020000u);
+    const int off = (lane & 7) * (K / 2) + ((lane >> 3) & 1) * 64 + (lane >> 4) * 16;
+    u32x4_t v[TM][NP];
+#pragma unroll
+    for (int i = 0; i < NP; i++)
+#pragma unroll
+        for (int t = 0; t < TM; t++)
+            v[t][i] = __builtin_bit_cast(u32x4_t, __builtin_amdgcn_raw_buffer_load_b128(
+                                                      r, off + t * 8 * (K / 2) + (p0 + min(i, np - 1)) * 128, 0, 0));
+    uint32_t x = 0;
+#pragma unroll
+    for (int i = 0; i < NP; i++)
+#pragma unroll
+        for (int t = 0; t < TM; t++) x ^= fold(v[t][i]);
+    if (x == key) sink[0] = x;
+}
+
 __global__ void __launch_bounds__(1024) probe_flat_kernel(const u32x4_t *__restrict__ src, size_t n16,
                                                           uint32_t key, uint32_t *__restrict__ sink) {
     const size_t per_wg = (n16 + gridDim.x - 1) / gridDim.x;
@@ -87,6 +118,14 @@ void launch_tile(int rows, dim3 grid, dim3 block, hipStream_t s, const uint8_t *
         hipLaunchKernelGGL((probe_tile_kernel<NL, NMAT, 16>), grid, block, 0, s, w, N, K, T, 0x9E3779B9u, sink);
     else
         hipLaunchKernelGGL((probe_tile_kernel<NL, NMAT, 8>), grid, block, 0, s, w, N, K, T, 0x9E3779B9u, sink);
+}
+
+template <int TM, int NP>
+void launch_band(int nmat, dim3 grid, dim3 block, hipStream_t s, const uint8_t *w, int N, int K, uint32_t *sink) {
+    if (nmat == 2)
+        hipLaunchKernelGGL((probe_band_kernel<TM, NP, 2>), grid, block, 0, s, w, N, K, 0x9E3779B9u, sink);
+    else
+        hipLaunchKernelGGL((probe_band_kernel<TM, NP, 1>), grid, block, 0, s, w, N, K, 0x9E3779B9u, sink);
 }
 
 template <int NMAT>
@@ -133,6 +172,21 @@ int imh_diag_stream_read(imh_stream *stream, const void *src, uint32_t n, uint32
                             : launch_tile_nl<1>(nl, (int)sh->rows, grid, block, stream->stream, w, (int)n, (int)k,
                                                 (int)sh->tiles, sink);
         if (bad) return imh::fail(IMH_EINVAL, std::string(who) + ": more than 32 loads per lane");
+    } else if (sh->mode == IMH_PROBE_BAND) {
+        const int G = (int)k / 128;
+        if (sh->nmat < 1 || sh->nmat > 2 || sh->waves < 1 || sh->waves * sh->nmat > 16 || sh->grid == 0 ||
+            sh->grid > n || G % 2 || (uint64_t)n * sh->grid >= (1ull << 32))
+            return imh::fail(IMH_EINVAL, std::string(who) + ": nmat 1-2, waves * nmat <= 16, 0 < grid <= n, "
+                                                            "k / 128 even");
+        const int rows = (int)((n + sh->grid - 1) / sh->grid), tm = (rows + 7) / 8;
+        const int np = (G / 2 + (int)sh->waves - 1) / (int)sh->waves;
+        const dim3 grid(sh->grid), block(64 * sh->waves * sh->nmat);
+        const uint8_t *w = static_cast<const uint8_t *>(src);
+        hipStream_t st = stream->stream;
+        if (tm <= 2 && np <= 5) launch_band<2, 5>(sh->nmat, grid, block, st, w, (int)n, (int)k, sink);
+        else if (tm <= 3 && np <= 5) launch_band<3, 5>(sh->nmat, grid, block, st, w, (int)n, (int)k, sink);
+        else if (tm <= 5 && np <= 3) launch_band<5, 3>(sh->nmat, grid, block, st, w, (int)n, (int)k, sink);
+        else return imh::fail(IMH_EINVAL, std::string(who) + ": band shape beyond (tiles, pairs) (2,5) (3,5) (5,3)");
     } else if (sh->mode == IMH_PROBE_FLAT) {
         if (sh->grid == 0 || sh->threads == 0 || sh->threads > 1024 || sh->threads % 64)
             return imh::fail(IMH_EINVAL, std::string(who) + ": grid > 0 and threads a multiple of 64 up to 1024");

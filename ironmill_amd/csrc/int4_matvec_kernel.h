@@ -169,11 +169,12 @@ __device__ __forceinline__ float div_awq(float v, float w) { return v * __builti
 // right after them, before anything waits.  The first stage is peeled so no
 // loop-carried wait sits ahead of the first weight loads.
 // Occupancy target (waves per SIMD) the register allocator works to: 6 where
-// the live state fits 80 VGPRs without spilling, fewer for the heavier shapes.
+// the live state fits 80 VGPRs without spilling, fewer for the heavier shapes
+// (every instantiation compiles without scratch).
 constexpr int waves_per_simd(int NG, int MT, int XC, int SRC) {
-    return (SRC == SRC_RAW_RN && XC == 2 && NG >= 6) ? 4
-           : (NG <= 5 && (MT == 1 || XC == 1) && (SRC == SRC_IMAGE || XC == 1)) ? 6
-                                                                                 : 5;
+    return ((SRC == SRC_RAW_RN && XC == 2) || (NG >= 8 && XC == 2)) ? 4
+           : (NG <= 5 && (MT == 1 || XC == 1) && (SRC == SRC_IMAGE || (XC == 1 && SRC == SRC_RAW))) ? 6
+                                                                                                   : 5;
 }
 
 template <int NMAT, int EPI, int MT, int NG, int XC, int SRC>

@@ -5,6 +5,7 @@
 #include <cstdio>
 #include <cstring>
 #include <new>
+#include <algorithm>
 #include <string>
 
 #include "imh_internal.h"
@@ -360,6 +361,30 @@ int imh_event_elapsed_ms(imh_event *start, imh_event *end, float *ms) {
     if (!start || !end || !ms) return imh::fail(IMH_EINVAL, "imh_event_elapsed_ms: NULL argument");
     IMH_HIP(hipEventSynchronize(end->ev));
     IMH_HIP(hipEventElapsedTime(ms, start->ev, end->ev));
+    return IMH_OK;
+}
+
+int imh_kv_positions_for(uint32_t seq_pos, uint32_t token_count, uint32_t window_size, uint32_t max_seq_len,
+                         imh_kv_positions *out) {
+    const char *who = "imh_kv_positions_for";
+    if (!out) return imh::fail(IMH_EINVAL, std::string(who) + ": NULL output");
+    if ((uint64_t)seq_pos + token_count > max_seq_len)
+        return imh::fail(IMH_ERANGE, std::string(who) + ": seq_pos " + std::to_string(seq_pos) + " + token_count " +
+                                         std::to_string(token_count) + " exceeds max_seq_len " +
+                                         std::to_string(max_seq_len));
+    const uint32_t stride = window_size ? window_size : max_seq_len;
+    if (token_count == 0 || token_count > stride)
+        return imh::fail(IMH_EINVAL, std::string(who) + ": token_count must be 1..stride");
+    out->stride = stride;
+    if (window_size) {
+        out->write_pos = seq_pos % window_size;
+        const uint32_t effective = std::min<uint64_t>((uint64_t)seq_pos + token_count, window_size);
+        out->attn_base = std::min(effective - token_count, stride - token_count);   // effective >= token_count
+    } else {
+        out->write_pos = seq_pos;
+        out->attn_base = seq_pos;
+    }
+    out->attn_len = out->attn_base + token_count;
     return IMH_OK;
 }
 

@@ -296,8 +296,10 @@ __device__ __forceinline__ float tab_f32(uint32_t e) {
            (float)__builtin_bit_cast(_Float16, (uint16_t)(e >> 16));
 }
 
+// Occupancy: 3 waves per SIMD (168 VGPRs); the fused token writer's extra
+// live state needs more than that, so it runs at 2 rather than spill.
 template <int GQA, bool FUSED>
-__global__ void __launch_bounds__(64 * kWaves) __attribute__((amdgpu_waves_per_eu(3))) tq_attention_kernel(
+__global__ void __launch_bounds__(64 * kWaves) __attribute__((amdgpu_waves_per_eu(FUSED ? 2 : 3))) tq_attention_kernel(
     const __half *__restrict__ q, int nh, int nkv, int max_seq, int seq_len, int T,
     const int32_t *__restrict__ seq_lens, float attn_scale, const float *__restrict__ signs,
     const float *__restrict__ qjl_t, const float *__restrict__ kcb, const float *__restrict__ vcb,

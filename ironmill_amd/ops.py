@@ -95,7 +95,7 @@ def encode_affine_matvec_int4xq8(stream: Stream, q8, q8_scales, token_count: int
                                                C.byref(weight.c), _ptr(y)))
 
 
-PROBE_TILE, PROBE_FLAT = 0, 1
+PROBE_TILE, PROBE_FLAT, PROBE_BAND = 0, 1, 2
 
 
 def diag_stream_read(stream: Stream, src, n: int, k: int, sink, mode=PROBE_TILE, nmat=1, rows=16, tiles=1,
@@ -103,9 +103,19 @@ def diag_stream_read(stream: Stream, src, n: int, k: int, sink, mode=PROBE_TILE,
     """Streaming probe (no reference counterpart): reads the INT4 weight bytes at src with no
     compute.  TILE: `tiles` tiles of `rows` rows of each of `nmat` n x k weights per workgroup,
     `waves` waves per weight (rows 16 is the INT4 matvec's own pattern).  FLAT: `grid`
-    workgroups of `threads` threads reading contiguous runs of the n x k weight."""
+    workgroups of `threads` threads reading contiguous runs of the n x k weight.  BAND: the
+    row-band matvec's launch, `grid` workgroups each reading one band of rows of each weight."""
     shape = _lib.ProbeShape(mode, nmat, rows, tiles, waves, grid, threads)
     check(lib.imh_diag_stream_read(stream.handle, _ptr(src), n, k, C.byref(shape), _ptr(sink)))
+
+
+def kv_positions(seq_pos: int, token_count: int, window_size: int, max_seq_len: int) -> dict:
+    """The cache positions of one step (imh_kv_positions_for; attention.rs:141-163): the
+    layer cache's stride (its max_seq_len), the write position, the attention base and the
+    seq_len to give the attention ops."""
+    out = _lib.KvPositions()
+    check(lib.imh_kv_positions_for(seq_pos, token_count, window_size, max_seq_len, C.byref(out)))
+    return {"stride": out.stride, "write_pos": out.write_pos, "attn_base": out.attn_base, "attn_len": out.attn_len}
 
 
 GEMM_F16, GEMM_BF16, GEMM_FP8_E4M3 = 0, 1, 2
@@ -384,13 +394,19 @@ class Decoder:
 
     def __init__(self, dev: Device, *, hidden_size, intermediate_size, num_layers, num_heads, num_kv_heads,
                  head_dim, vocab_size, max_seq_len, batch=1, rotary_dim=0, rms_eps=1e-6, rope_theta=1e6,
-                 attn_scale=0.0, embed_scale=0.0, use_gelu=False, kv_cache="turboquant", tq_seed=42):
+                 attn_scale=0.0, embed_scale=0.0, use_gelu=False, kv_cache="turboquant", tq_seed=42,
+                 window_sizes=None):
         self.dev = dev
         kind = {"turboquant": _lib.IMH_KV_TURBOQUANT, "fp16": _lib.IMH_KV_FP16}[kv_cache]
         self.kv_kind = kv_cache
+        # per-layer sliding windows (0 = full attention), copied by the library at creation
+        win = None if window_sizes is None else np.ascontiguousarray(window_sizes, np.uint32)
+        if win is not None and win.size != num_layers:
+            raise ValueError("window_sizes needs one entry per layer")
         self.cfg = DecoderConfig(hidden_size, intermediate_size, num_layers, num_heads, num_kv_heads, head_dim,
                                  vocab_size, max_seq_len, batch, rotary_dim, rms_eps, attn_scale, embed_scale,
-                                 int(bool(use_gelu)), kind, rope_theta, tq_seed)
+                                 int(bool(use_gelu)), kind, rope_theta, tq_seed,
+                                 None if win is None else win.ctypes.data)
         h = C.c_void_p()
         check(lib.imh_decoder_create(dev.handle, C.byref(self.cfg), C.byref(h)))
         self._h = h
@@ -446,12 +462,13 @@ class Decoder:
         self._keep["tq_tables"] = tables
 
     def kv_cache(self, layer: int) -> dict:
-        """Host copies of one layer's cache arrays."""
+        """Host copies of one layer's cache arrays ([batch, kv heads, slots, ...]; a windowed
+        layer has window_size slots)."""
         c = self.cfg
-        shp = (c.batch, c.num_kv_heads, c.max_seq_len)
         if self.kv_kind == "turboquant":
             t = TqKvCache()
             check(lib.imh_decoder_kv_cache(self._h, layer, C.byref(t), None))
+            shp = (c.batch, c.num_kv_heads, t.max_seq_len)
             return {"k_codes": read_device(self.dev, t.k_codes, shp + (c.head_dim,), np.uint8),
                     "v_codes": read_device(self.dev, t.v_codes, shp + (c.head_dim,), np.uint8),
                     "k_scales": read_device(self.dev, t.k_scales, shp, np.float32),
@@ -459,6 +476,7 @@ class Decoder:
                     "k_r_norms": read_device(self.dev, t.k_r_norms, shp, np.float32)}
         f = _lib.Fp16KvCache()
         check(lib.imh_decoder_kv_cache(self._h, layer, None, C.byref(f)))
+        shp = (c.batch, c.num_kv_heads, f.max_seq_len)
         return {"k": read_device(self.dev, f.k, shp + (c.head_dim,), np.float16),
                 "v": read_device(self.dev, f.v, shp + (c.head_dim,), np.float16)}
 

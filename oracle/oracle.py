@@ -499,10 +499,13 @@ class DecoderReference:
         core/dequant.rs:305-345), exact in f32, not rounded to f16;
       acc="f64": projections accumulate in float64 (numpy) instead of a sequential f32 sum,
         which changes only the rounding of the f32 result (weights="exact" only).
-    tables: TQTables to use instead of TQTables(head_dim, 8, tq_seed)."""
+    tables: TQTables to use instead of TQTables(head_dim, 8, tq_seed).
+    window_sizes: per-layer sliding windows (0 = full attention): a windowed layer attends, at
+      position p, to the positions [max(0, p + 1 - W), p] -- the definition the reference's ring
+      buffer of W slots implements (attention.rs:141-163); this cache stays linear."""
 
     def __init__(self, cfg: dict, layers, embedding16, final_norm16, lm_head, kv_cache="turboquant",
-                 tq_seed=42, weights="f16", acc="f32", tables=None):
+                 tq_seed=42, weights="f16", acc="f32", tables=None, window_sizes=None):
         if weights not in ("f16", "exact") or acc not in ("f32", "f64"):
             raise ValueError("weights must be 'f16' or 'exact', acc 'f32' or 'f64'")
         if weights == "f16" and acc != "f32":
@@ -538,6 +541,7 @@ class DecoderReference:
             self.caches = [dict(k=np.zeros(shp + (self.hd,), np.float16), v=np.zeros(shp + (self.hd,), np.float16))
                            for _ in layers]
         self.positions = np.zeros(self.B, np.int32)
+        self.windows = list(window_sizes) if window_sizes is not None else [0] * len(layers)
 
     def _dense(self, w):
         if not self.exact:
@@ -603,6 +607,20 @@ class DecoderReference:
 
     def _attend(self, l, q16):
         cache = self.caches[l]
+        W = self.windows[l]
+        if W:   # the last W positions of each sequence
+            rows = []
+            for b in range(self.B):
+                e = int(min(self.positions[b] + 1, self.max_seq))
+                s0 = max(0, e - W)
+                sl = {k: v[b:b + 1, :, s0:e] for k, v in cache.items()}
+                if self.kv == "turboquant":
+                    o = tq_attention(q16[b:b + 1], self.tables, sl["k_codes"], sl["v_codes"], sl["k_scales"],
+                                     sl["v_scales"], sl["k_r_norms"], e - s0, self.scale, nthreads=8)
+                else:
+                    o = fp16_attention(q16[b:b + 1], sl["k"], sl["v"], e - s0, self.scale, nthreads=8)
+                rows.append(o)
+            return np.concatenate(rows, axis=0).astype(np.float16)
         lens = np.minimum(self.positions + 1, self.max_seq).astype(np.int32)
         if self.kv == "turboquant":
             out = tq_attention(q16, self.tables, cache["k_codes"], cache["v_codes"], cache["k_scales"],

@@ -120,3 +120,35 @@ def test_rope_cache_is_bit_exact_with_oracle():
         c2, s2 = O.rope_cache(hd, mp, theta, rd or None)
         assert np.array_equal(c.view(np.uint16), c2.view(np.uint16))
         assert np.array_equal(s.view(np.uint16), s2.view(np.uint16))
+
+
+def test_kv_positions_sliding_window_semantics():
+    """imh_kv_positions_for (attention.rs:141-163) against what a ring of W slots must show:
+    decoding one token at a time, writing token p at write_pos, the slots [0, attn_len) hold
+    exactly the last min(p + 1, W) tokens; full-attention layers keep the linear positions."""
+    from ironmill_amd import ops
+    for W in (1, 3, 8):
+        ring = [None] * W
+        for p in range(3 * W + 2):
+            kp = ops.kv_positions(p, 1, W, 1000)
+            assert kp["stride"] == W
+            ring[kp["write_pos"]] = p
+            visible = sorted(ring[:kp["attn_len"]])
+            assert visible == list(range(max(0, p + 1 - W), p + 1)), (W, p, visible)
+    kp = ops.kv_positions(17, 4, 0, 64)
+    assert kp == {"stride": 64, "write_pos": 17, "attn_base": 17, "attn_len": 21}
+    # a prefill chunk inside a window that has not wrapped: the linear positions
+    assert ops.kv_positions(2, 3, 8, 64) == {"stride": 8, "write_pos": 2, "attn_base": 2, "attn_len": 5}
+    # a chunk that reaches past the window: the attention base clamps so base + T <= W
+    kp = ops.kv_positions(7, 3, 8, 64)
+    assert kp["write_pos"] == 7 and kp["attn_base"] == 5 and kp["attn_len"] == 8
+
+
+def test_kv_positions_errors():
+    from ironmill_amd import IronmillError, ops
+    with pytest.raises(IronmillError, match="exceeds max_seq_len"):
+        ops.kv_positions(62, 3, 0, 64)
+    with pytest.raises(IronmillError, match="token_count"):
+        ops.kv_positions(0, 0, 0, 64)
+    with pytest.raises(IronmillError, match="token_count"):
+        ops.kv_positions(0, 5, 4, 64)
