@@ -574,6 +574,23 @@ int imh_decoder_reset(imh_decoder *d, imh_stream *stream, const int32_t *positio
 /* Encode one step (pipeline.rs:424-1172 for token_count 1).  IMH_ERANGE when a
  * position has reached max_seq_len (cache.rs:494-504). */
 int imh_decoder_step(imh_decoder *d, imh_stream *stream, const uint32_t *token_ids, uint16_t *logits);
+
+/* Prefill of token_count tokens per sequence (run_pipeline_inner with
+ * token_count > 1, metal/pipeline.rs:228-1313, as the chunked prefill of
+ * metal/engine.rs:182-228 runs it): token_ids [batch][token_count]; token t of
+ * sequence b goes to position positions[b] + t and attends causally to
+ * [0, positions[b] + t + 1).  A sliding-window layer (token_count <=
+ * window_size W) writes its ring at (p + t) % W and token t attends to slots
+ * [0, min(p + T, W) - T + t + 1) (attention.rs:141-163): the last W positions
+ * while p + T <= W; past that the reference's clamp, under which a chunk's
+ * early tokens see slots its later tokens rewrote.  logits [batch][vocab] f16 of each
+ * sequence's last token; the positions advance by token_count.  The
+ * projections of batch x token_count >= 32 rows run on the GEMM ops.
+ * Activation rows for batch x token_count tokens are allocated on the first
+ * call of a size (IMH_EINVAL while capturing before that); token_count 1 is
+ * imh_decoder_step.  IMH_ERANGE when a sequence would pass max_seq_len. */
+int imh_decoder_prefill(imh_decoder *d, imh_stream *stream, const uint32_t *token_ids, uint32_t token_count,
+                        uint16_t *logits);
 /* Write token_count K/V projections ([batch][token_count][num_kv_heads][head_dim]
  * f16) of one layer into its cache at positions base_pos.. (the cache-write half
  * of encode_kv_cache_and_attention, attention.rs:344-391 / :497-525, as a

@@ -274,6 +274,7 @@ SIGNATURES = {
     "imh_decoder_set_model": (I, [P, P, P, C.POINTER(AffineInt4Weight)]),
     "imh_decoder_reset": (I, [P, P, P]),
     "imh_decoder_step": (I, [P, P, P, P]),
+    "imh_decoder_prefill": (I, [P, P, P, U32, P]),
     "imh_decoder_write_kv": (I, [P, P, U32, P, P, U32, U32]),
     "imh_decoder_positions": (I, [P, P]),
     "imh_decoder_sync_positions": (I, [P, P, P]),

@@ -54,6 +54,8 @@ struct imh_decoder {
     imh_tq_tables *tq = nullptr;       // in use: own_tq or the caller's (imh_decoder_set_tq_tables)
     std::vector<imh_tq_kv_cache> tq_caches;
     std::vector<imh_fp16_kv_cache> fp16_caches;
+    void *prefill_arena = nullptr;   // activation rows of imh_decoder_prefill
+    size_t prefill_bytes = 0;
     // per layer: sliding-window size (0 = full attention); a windowed layer's
     // cache is a ring of that many positions
     std::vector<uint32_t> windows;
@@ -73,17 +75,17 @@ namespace {
 // flag, which imh_decoder_sync_positions reports as IMH_ERANGE (the
 // reference refuses such a step, metal/pipeline.rs:271-279).
 __global__ void decoder_advance_kernel(int32_t *positions, int32_t *seq_lens, int32_t *status, int batch,
-                                       int max_seq) {
+                                       int max_seq, int T) {
     const int b = blockIdx.x * blockDim.x + threadIdx.x;
     if (b >= batch) return;
     const int p = positions[b];
-    if (p >= max_seq) {
+    if (p + T > max_seq) {
         seq_lens[b] = 0;
         __hip_atomic_store(status, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         return;
     }
-    positions[b] = p + 1;
-    seq_lens[b] = p + 1 >= max_seq ? 0 : p + 2;
+    positions[b] = p + T;
+    seq_lens[b] = p + T >= max_seq ? 0 : p + T + 1;
 }
 
 size_t align256(size_t x) { return (x + 255) & ~size_t(255); }
@@ -95,6 +97,191 @@ int check_weight(const imh_affine_int4_weight &w, uint32_t n, uint32_t k, const 
         return imh::fail(IMH_EINVAL, std::string("imh_decoder: ") + name + " is " + std::to_string(w.n) + "x" +
                                          std::to_string(w.k) + ", expected " + std::to_string(n) + "x" +
                                          std::to_string(k));
+    return IMH_OK;
+}
+
+// The activation buffers of one schedule run (decode: the arena's B rows;
+// prefill: B x T rows), T tokens per sequence, the attention lengths.
+struct Rows {
+    uint16_t *hidden, *residual, *norm_out, *q, *k, *v, *attn_out, *ffn_down, *act;
+    uint32_t T;
+    const int32_t *attn_lens;
+};
+
+int check_ready(const imh_decoder *d, const imh_stream *s, const uint32_t *token_ids, const uint16_t *logits,
+                uint32_t token_count, const char *who) {
+    if (!d || !s || !token_ids || !logits) return imh::fail(IMH_EINVAL, std::string(who) + ": NULL argument");
+    if (token_count == 0) return imh::fail(IMH_EINVAL, std::string(who) + ": token_count 0");
+    if (!d->model_set) return imh::fail(IMH_EINVAL, std::string(who) + ": model weights not set");
+    for (uint32_t l = 0; l < d->cfg.num_layers; l++)
+        if (!d->layer_set[l])
+            return imh::fail(IMH_EINVAL, std::string(who) + ": layer " + std::to_string(l) + " weights not set");
+    // the step guard of pipeline.rs:270-279 (and cache.rs:494-504)
+    for (int32_t p : d->host_positions)
+        if ((uint64_t)(uint32_t)p + token_count > d->cfg.max_seq_len)
+            return imh::fail(IMH_ERANGE, std::string(who) + ": sequence position " + std::to_string(p) + " + " +
+                                             std::to_string(token_count) + " token(s) beyond max_seq_len " +
+                                             std::to_string(d->cfg.max_seq_len));
+    return IMH_OK;
+}
+
+__global__ void prefill_lens_kernel(const int32_t *positions, int32_t *lens, int batch, int T) {
+    const int b = blockIdx.x * blockDim.x + threadIdx.x;
+    if (b < batch) lens[b] = positions[b] + T;
+}
+
+// out[b] = rows[b * T + T - 1] (H halfs each)
+__global__ void gather_last_rows_kernel(const uint16_t *rows, uint16_t *out, int T, int H) {
+    const int b = blockIdx.x;
+    const uint16_t *src = rows + ((size_t)b * T + T - 1) * H;
+    for (int i = threadIdx.x; i < H; i += blockDim.x) out[(size_t)b * H + i] = src[i];
+}
+
+// The per-layer schedule for T tokens per sequence (rows b * T + t) over the
+// activation rows in r, attention lengths from r.attn_lens; logits of each
+// sequence's last token.  T = 1 is the decode step.
+int run_schedule(imh_decoder *d, imh_stream *s, const uint32_t *token_ids, const Rows &r, uint16_t *logits) {
+    const imh_decoder_config &c = d->cfg;
+    const uint32_t T = r.T, R = c.batch * r.T, H = c.hidden_size;
+#define IMH_TRY(call)            \
+    do {                         \
+        int rc_ = (call);        \
+        if (rc_) return rc_;     \
+    } while (0)
+
+    IMH_TRY(imh_encode_fused_embedding_norm(s, token_ids, d->embedding, d->layers[0].input_norm, r.norm_out,
+                                            r.hidden, H, R, c.vocab_size, c.rms_eps, c.embed_scale));
+    // Q, K and V read the same activation: when they share the AWQ scales
+    // (or have none) they run as the row segments of one launch, which at a
+    // layer's end also does the residual add and the input norm
+    auto shared_awq = [](const imh_decoder_layer_weights &w) {
+        return w.q_proj.awq_scales == w.k_proj.awq_scales && w.k_proj.awq_scales == w.v_proj.awq_scales;
+    };
+    uint16_t *qkv_out[3] = {r.q, r.k, r.v};
+    bool q_done = false, kv_done = false;
+    for (uint32_t l = 0; l < c.num_layers; l++) {
+        const imh_decoder_layer_weights &w = d->layers[l];
+        const imh_affine_int4_weight *qkv[3] = {&w.q_proj, &w.k_proj, &w.v_proj};
+        if (!q_done && shared_awq(w)) {
+            IMH_TRY(imh::encode_segmented_matvec_int4(s, r.norm_out, nullptr, R, 3, qkv, qkv_out));
+            kv_done = true;
+        } else if (!q_done) {
+            IMH_TRY(imh_encode_affine_projection_int4(s, r.norm_out, R, &w.q_proj, r.q));
+        }
+        if (!kv_done) {
+            if (w.k_proj.awq_scales == w.v_proj.awq_scales)
+                IMH_TRY(imh::encode_segmented_matvec_int4(s, r.norm_out, nullptr, R, 2, qkv + 1, qkv_out + 1));
+            else {
+                IMH_TRY(imh_encode_affine_projection_int4(s, r.norm_out, R, &w.k_proj, r.k));
+                IMH_TRY(imh_encode_affine_projection_int4(s, r.norm_out, R, &w.v_proj, r.v));
+            }
+        }
+        imh_qk_norm_rope_params qp{};
+        qp.q = r.q;
+        qp.k = r.k;
+        qp.q_norm = w.q_norm;
+        qp.k_norm = w.k_norm;
+        qp.cos_cache = d->rope_cos;
+        qp.sin_cache = d->rope_sin;
+        qp.num_heads = c.num_heads;
+        qp.num_kv_heads = c.num_kv_heads;
+        qp.head_dim = c.head_dim;
+        qp.rotary_dim = c.rotary_dim;
+        qp.max_pos = c.max_seq_len;
+        qp.positions = d->positions;
+        qp.batch = c.batch;
+        qp.token_count = T;
+        qp.eps = c.rms_eps;
+        // TurboQuant: the token's cache write runs inside the attention launch;
+        // with QK-norms at head_dim = rotary_dim = 128 so do the norm and
+        // rotation of K (in the writing workgroup) and Q (in the prologue)
+        const uint32_t win = d->windows[l];
+        const bool fold = c.kv_cache == IMH_KV_TURBOQUANT && w.q_norm && w.k_norm && c.head_dim == 128 &&
+                          (c.rotary_dim == 0 || c.rotary_dim == 128) && win == 0 && T == 1;
+        if (win || T > 1) {
+            // separate cache write and attention: a sliding-window layer
+            // (attention.rs:141-163; its cache is a ring of `win` positions,
+            // written at position % win, the attention bound being the ring's
+            // size) or several tokens per sequence (token t at positions[b] + t
+            // attends causally to [0, positions[b] + t + 1)).  RoPE uses the
+            // absolute position.
+            IMH_TRY(imh_encode_qk_norm_rope(s, &qp));
+            if (c.kv_cache == IMH_KV_TURBOQUANT) {
+                IMH_TRY(imh_encode_turboquant_cache_write_kv(s, d->tq, &d->tq_caches[l], r.k, r.v, T, 0,
+                                                             d->positions));
+                if (T == 1)
+                    IMH_TRY(imh_encode_turboquant_attention(s, d->tq, &d->tq_caches[l], r.q, c.num_heads, 0,
+                                                            r.attn_lens, c.attn_scale, r.attn_out, 0));
+                else
+                    IMH_TRY(imh_encode_turboquant_attention_tokens(s, d->tq, &d->tq_caches[l], r.q, c.num_heads, T,
+                                                                   0, r.attn_lens, c.attn_scale, r.attn_out, 0));
+            } else {
+                const imh_fp16_kv_cache *kc = &d->fp16_caches[l];
+                IMH_TRY(imh_encode_kv_scatter(s, kc, r.k, T, 0, d->positions, 1));
+                IMH_TRY(imh_encode_kv_scatter(s, kc, r.v, T, 0, d->positions, 0));
+                IMH_TRY(imh_encode_fp16_attention(s, kc, r.q, c.num_heads, T, 0, r.attn_lens, c.attn_scale,
+                                                  r.attn_out, 0));
+            }
+        } else if (c.kv_cache == IMH_KV_TURBOQUANT) {
+            if (!fold) IMH_TRY(imh_encode_qk_norm_rope(s, &qp));
+            IMH_TRY(imh::encode_tq_write_attend(s, d->tq, &d->tq_caches[l], r.q, r.k, r.v, c.num_heads,
+                                                r.attn_lens, c.attn_scale, r.attn_out, fold ? &qp : nullptr));
+        } else {
+            IMH_TRY(imh_encode_qk_norm_rope(s, &qp));
+            const imh_fp16_kv_cache *kc = &d->fp16_caches[l];
+            // no ring wrap: a step past the cache's end writes nothing
+            IMH_TRY(imh::encode_kv_scatter_bounded(s, kc, r.k, d->positions, 1));
+            IMH_TRY(imh::encode_kv_scatter_bounded(s, kc, r.v, d->positions, 0));
+            IMH_TRY(imh_encode_fp16_attention(s, kc, r.q, c.num_heads, 1, 0, r.attn_lens, c.attn_scale,
+                                              r.attn_out, 0));
+        }
+        IMH_TRY(imh_encode_affine_projection_int4(s, r.attn_out, R, &w.o_proj, r.ffn_down));
+        {   // post-attention residual + norm, then gate + up + activation: one launch
+            imh_fused_residual_norm_params rp{};
+            rp.a = r.hidden;
+            rp.b = r.ffn_down;
+            rp.norm_weight = w.post_attn_norm;
+            rp.residual_output = r.residual;
+            rp.normed_output = r.norm_out;
+            rp.token_count = R;
+            rp.eps = c.rms_eps;
+            IMH_TRY(imh::encode_resnorm_gate_up_act_int4(s, &rp, R, &w.gate_proj, &w.up_proj, r.act, c.use_gelu));
+        }
+        IMH_TRY(imh_encode_affine_projection_int4(s, r.act, R, &w.down_proj, r.ffn_down));
+        if (l + 1 < c.num_layers) {
+            const imh_decoder_layer_weights &nw = d->layers[l + 1];
+            imh_fused_residual_norm_params fp{};
+            fp.a = r.residual;
+            fp.b = r.ffn_down;
+            fp.norm_weight = nw.input_norm;
+            fp.residual_output = r.hidden;
+            fp.weight = &nw.q_proj;
+            fp.output = r.q;
+            fp.normed_output = r.norm_out;
+            fp.token_count = R;
+            fp.eps = c.rms_eps;
+            kv_done = shared_awq(nw);
+            if (kv_done) {
+                const imh_affine_int4_weight *nqkv[3] = {&nw.q_proj, &nw.k_proj, &nw.v_proj};
+                IMH_TRY(imh::encode_segmented_matvec_int4(s, nullptr, &fp, R, 3, nqkv, qkv_out));
+            } else {
+                IMH_TRY(imh_encode_fused_residual_norm_affine_matvec_int4(s, &fp));
+            }
+            q_done = true;
+        } else {
+            IMH_TRY(imh_encode_residual_add(s, r.residual, r.ffn_down, r.hidden, (size_t)R * H));
+        }
+    }
+    const uint16_t *last = r.hidden;
+    if (T > 1) {   // each sequence's last token
+        hipLaunchKernelGGL(gather_last_rows_kernel, dim3(c.batch), dim3(256), 0, s->stream, r.hidden, d->hidden,
+                           (int)T, (int)H);
+        IMH_HIP(hipGetLastError());
+        last = d->hidden;
+    }
+    IMH_TRY(imh_encode_rms_norm(s, last, d->final_norm, d->norm_out, H, c.batch, c.rms_eps));
+    IMH_TRY(imh_encode_affine_projection_int4(s, d->norm_out, c.batch, &d->lm_head, logits));
+#undef IMH_TRY
     return IMH_OK;
 }
 
@@ -253,6 +440,7 @@ void imh_decoder_free(imh_decoder *d) {
     imh::use_device(d->dev);
     if (d->arena) (void)hipFree(d->arena);
     if (d->kv_arena) (void)hipFree(d->kv_arena);
+    if (d->prefill_arena) (void)hipFree(d->prefill_arena);
     if (d->own_tq) imh_tq_tables_free(d->own_tq);
     delete d;
 }
@@ -317,151 +505,90 @@ int imh_decoder_reset(imh_decoder *d, imh_stream *stream, const int32_t *positio
 
 int imh_decoder_step(imh_decoder *d, imh_stream *s, const uint32_t *token_ids, uint16_t *logits) {
     const char *who = "imh_decoder_step";
-    if (!d || !s || !token_ids || !logits) return imh::fail(IMH_EINVAL, std::string(who) + ": NULL argument");
-    if (!d->model_set) return imh::fail(IMH_EINVAL, std::string(who) + ": model weights not set");
-    for (uint32_t l = 0; l < d->cfg.num_layers; l++)
-        if (!d->layer_set[l])
-            return imh::fail(IMH_EINVAL, std::string(who) + ": layer " + std::to_string(l) + " weights not set");
-    for (int32_t p : d->host_positions)
-        if ((uint32_t)p >= d->cfg.max_seq_len)
-            return imh::fail(IMH_ERANGE, std::string(who) + ": sequence position " + std::to_string(p) +
-                                             " beyond max_seq_len (cache.rs:494-504)");
-    const imh_decoder_config &c = d->cfg;
-    const uint32_t B = c.batch, H = c.hidden_size;
-    int rc = imh::use_device(d->dev);
+    int rc = check_ready(d, s, token_ids, logits, 1, who);
     if (rc) return rc;
-#define IMH_TRY(call)            \
-    do {                         \
-        int rc_ = (call);        \
-        if (rc_) return rc_;     \
-    } while (0)
-
-    IMH_TRY(imh_encode_fused_embedding_norm(s, token_ids, d->embedding, d->layers[0].input_norm, d->norm_out,
-                                            d->hidden, H, B, c.vocab_size, c.rms_eps, c.embed_scale));
-    // Q, K and V read the same activation: when they share the AWQ scales
-    // (or have none) they run as the row segments of one launch, which at a
-    // layer's end also does the residual add and the input norm
-    auto shared_awq = [](const imh_decoder_layer_weights &w) {
-        return w.q_proj.awq_scales == w.k_proj.awq_scales && w.k_proj.awq_scales == w.v_proj.awq_scales;
-    };
-    uint16_t *qkv_out[3] = {d->q, d->k, d->v};
-    bool q_done = false, kv_done = false;
-    for (uint32_t l = 0; l < c.num_layers; l++) {
-        const imh_decoder_layer_weights &w = d->layers[l];
-        const imh_affine_int4_weight *qkv[3] = {&w.q_proj, &w.k_proj, &w.v_proj};
-        if (!q_done && shared_awq(w)) {
-            IMH_TRY(imh::encode_segmented_matvec_int4(s, d->norm_out, nullptr, B, 3, qkv, qkv_out));
-            kv_done = true;
-        } else if (!q_done) {
-            IMH_TRY(imh_encode_affine_projection_int4(s, d->norm_out, B, &w.q_proj, d->q));
-        }
-        if (!kv_done) {
-            if (w.k_proj.awq_scales == w.v_proj.awq_scales)
-                IMH_TRY(imh::encode_segmented_matvec_int4(s, d->norm_out, nullptr, B, 2, qkv + 1, qkv_out + 1));
-            else {
-                IMH_TRY(imh_encode_affine_projection_int4(s, d->norm_out, B, &w.k_proj, d->k));
-                IMH_TRY(imh_encode_affine_projection_int4(s, d->norm_out, B, &w.v_proj, d->v));
-            }
-        }
-        imh_qk_norm_rope_params qp{};
-        qp.q = d->q;
-        qp.k = d->k;
-        qp.q_norm = w.q_norm;
-        qp.k_norm = w.k_norm;
-        qp.cos_cache = d->rope_cos;
-        qp.sin_cache = d->rope_sin;
-        qp.num_heads = c.num_heads;
-        qp.num_kv_heads = c.num_kv_heads;
-        qp.head_dim = c.head_dim;
-        qp.rotary_dim = c.rotary_dim;
-        qp.max_pos = c.max_seq_len;
-        qp.positions = d->positions;
-        qp.batch = B;
-        qp.token_count = 1;
-        qp.eps = c.rms_eps;
-        // TurboQuant: the token's cache write runs inside the attention launch;
-        // with QK-norms at head_dim = rotary_dim = 128 so do the norm and
-        // rotation of K (in the writing workgroup) and Q (in the prologue)
-        const uint32_t win = d->windows[l];
-        const bool fold = c.kv_cache == IMH_KV_TURBOQUANT && w.q_norm && w.k_norm && c.head_dim == 128 &&
-                          (c.rotary_dim == 0 || c.rotary_dim == 128) && win == 0;
-        if (win) {
-            // sliding window (attention.rs:141-163): the cache is a ring of
-            // `win` positions; the token goes to positions[b] % win and the
-            // attention covers min(seq_lens[b], win) slots, the bound being the
-            // ring's size.  RoPE uses the absolute position.
-            IMH_TRY(imh_encode_qk_norm_rope(s, &qp));
-            if (c.kv_cache == IMH_KV_TURBOQUANT) {
-                IMH_TRY(imh_encode_turboquant_cache_write_kv(s, d->tq, &d->tq_caches[l], d->k, d->v, 1, 0,
-                                                             d->positions));
-                IMH_TRY(imh_encode_turboquant_attention(s, d->tq, &d->tq_caches[l], d->q, c.num_heads, 0,
-                                                        d->seq_lens, c.attn_scale, d->attn_out, 0));
-            } else {
-                const imh_fp16_kv_cache *kc = &d->fp16_caches[l];
-                IMH_TRY(imh_encode_kv_scatter(s, kc, d->k, 1, 0, d->positions, 1));
-                IMH_TRY(imh_encode_kv_scatter(s, kc, d->v, 1, 0, d->positions, 0));
-                IMH_TRY(imh_encode_fp16_attention(s, kc, d->q, c.num_heads, 1, 0, d->seq_lens, c.attn_scale,
-                                                  d->attn_out, 0));
-            }
-        } else if (c.kv_cache == IMH_KV_TURBOQUANT) {
-            if (!fold) IMH_TRY(imh_encode_qk_norm_rope(s, &qp));
-            IMH_TRY(imh::encode_tq_write_attend(s, d->tq, &d->tq_caches[l], d->q, d->k, d->v, c.num_heads,
-                                                d->seq_lens, c.attn_scale, d->attn_out, fold ? &qp : nullptr));
-        } else {
-            IMH_TRY(imh_encode_qk_norm_rope(s, &qp));
-            const imh_fp16_kv_cache *kc = &d->fp16_caches[l];
-            // no ring wrap: a step past the cache's end writes nothing
-            IMH_TRY(imh::encode_kv_scatter_bounded(s, kc, d->k, d->positions, 1));
-            IMH_TRY(imh::encode_kv_scatter_bounded(s, kc, d->v, d->positions, 0));
-            IMH_TRY(imh_encode_fp16_attention(s, kc, d->q, c.num_heads, 1, 0, d->seq_lens, c.attn_scale, d->attn_out,
-                                              0));
-        }
-        IMH_TRY(imh_encode_affine_projection_int4(s, d->attn_out, B, &w.o_proj, d->ffn_down));
-        {   // post-attention residual + norm, then gate + up + activation: one launch
-            imh_fused_residual_norm_params rp{};
-            rp.a = d->hidden;
-            rp.b = d->ffn_down;
-            rp.norm_weight = w.post_attn_norm;
-            rp.residual_output = d->residual;
-            rp.normed_output = d->norm_out;
-            rp.token_count = B;
-            rp.eps = c.rms_eps;
-            IMH_TRY(imh::encode_resnorm_gate_up_act_int4(s, &rp, B, &w.gate_proj, &w.up_proj, d->act, c.use_gelu));
-        }
-        IMH_TRY(imh_encode_affine_projection_int4(s, d->act, B, &w.down_proj, d->ffn_down));
-        if (l + 1 < c.num_layers) {
-            const imh_decoder_layer_weights &nw = d->layers[l + 1];
-            imh_fused_residual_norm_params fp{};
-            fp.a = d->residual;
-            fp.b = d->ffn_down;
-            fp.norm_weight = nw.input_norm;
-            fp.residual_output = d->hidden;
-            fp.weight = &nw.q_proj;
-            fp.output = d->q;
-            fp.normed_output = d->norm_out;
-            fp.token_count = B;
-            fp.eps = c.rms_eps;
-            kv_done = shared_awq(nw);
-            if (kv_done) {
-                const imh_affine_int4_weight *nqkv[3] = {&nw.q_proj, &nw.k_proj, &nw.v_proj};
-                IMH_TRY(imh::encode_segmented_matvec_int4(s, nullptr, &fp, B, 3, nqkv, qkv_out));
-            } else {
-                IMH_TRY(imh_encode_fused_residual_norm_affine_matvec_int4(s, &fp));
-            }
-            q_done = true;
-        } else {
-            IMH_TRY(imh_encode_residual_add(s, d->residual, d->ffn_down, d->hidden, (size_t)B * H));
-        }
-    }
-    IMH_TRY(imh_encode_rms_norm(s, d->hidden, d->final_norm, d->norm_out, H, B, c.rms_eps));
-    IMH_TRY(imh_encode_affine_projection_int4(s, d->norm_out, B, &d->lm_head, logits));
-#undef IMH_TRY
+    rc = imh::use_device(d->dev);
+    if (rc) return rc;
+    const imh_decoder_config &c = d->cfg;
+    const uint32_t B = c.batch;
+    Rows r{d->hidden, d->residual, d->norm_out, d->q, d->k, d->v, d->attn_out, d->ffn_down, d->act, 1, d->seq_lens};
+    rc = run_schedule(d, s, token_ids, r, logits);
+    if (rc) return rc;
     hipLaunchKernelGGL(decoder_advance_kernel, dim3((B + 63) / 64), dim3(64), 0, s->stream, d->positions, d->seq_lens,
-                       d->status, (int)B, (int)c.max_seq_len);
+                       d->status, (int)B, (int)c.max_seq_len, 1);
     IMH_HIP(hipGetLastError());
     // a captured step runs only when replayed: the mirror follows eager steps
     if (!s->capturing)
         for (auto &p : d->host_positions) p++;
+    return IMH_OK;
+}
+
+int imh_decoder_prefill(imh_decoder *d, imh_stream *s, const uint32_t *token_ids, uint32_t token_count,
+                        uint16_t *logits) {
+    const char *who = "imh_decoder_prefill";
+    int rc = check_ready(d, s, token_ids, logits, token_count, who);
+    if (rc) return rc;
+    if (token_count == 1) return imh_decoder_step(d, s, token_ids, logits);
+    const imh_decoder_config &c = d->cfg;
+    for (uint32_t l = 0; l < c.num_layers; l++)
+        if (d->windows[l] && token_count > d->windows[l])
+            return imh::fail(IMH_EINVAL, std::string(who) + ": token_count above layer " + std::to_string(l) +
+                                             "'s window (" + std::to_string(d->windows[l]) + ")");
+    const uint32_t B = c.batch, T = token_count, R = B * T;
+    if (R > 65535) return imh::fail(IMH_EINVAL, std::string(who) + ": batch x token_count above 65535");
+    rc = imh::use_device(d->dev);
+    if (rc) return rc;
+    // activation rows for R tokens, grown on demand (not while capturing)
+    const size_t H = c.hidden_size, F = c.intermediate_size;
+    const size_t qd = (size_t)c.num_heads * c.head_dim, kvd = (size_t)c.num_kv_heads * c.head_dim;
+    const size_t need = align256(R * H * 2) * 4 + align256(R * qd * 2) * 2 + align256(R * kvd * 2) * 2 +
+                        align256(R * F * 2) + align256(B * 4);
+    if (need > d->prefill_bytes) {
+        if (s->capturing)
+            return imh::fail(IMH_EINVAL, std::string(who) + ": needs " + std::to_string(need) +
+                                             " bytes of activation rows; run a prefill of this size before capturing");
+        if (d->prefill_arena) {
+            // earlier work on any stream may still read the old rows
+            IMH_HIP(hipDeviceSynchronize());
+            (void)hipFree(d->prefill_arena);
+            d->prefill_arena = nullptr;
+            d->prefill_bytes = 0;
+        }
+        hipError_t e = hipMalloc(&d->prefill_arena, need);
+        if (e != hipSuccess)
+            return imh::fail(IMH_ENOMEM, std::string(who) + ": activation rows of " + std::to_string(need) + " bytes");
+        d->prefill_bytes = need;
+    }
+    char *p = static_cast<char *>(d->prefill_arena);
+    auto take = [&](size_t bytes) {
+        char *o = p;
+        p += align256(bytes);
+        return o;
+    };
+    Rows r{};
+    r.hidden = reinterpret_cast<uint16_t *>(take(R * H * 2));
+    r.residual = reinterpret_cast<uint16_t *>(take(R * H * 2));
+    r.norm_out = reinterpret_cast<uint16_t *>(take(R * H * 2));
+    r.q = reinterpret_cast<uint16_t *>(take(R * qd * 2));
+    r.k = reinterpret_cast<uint16_t *>(take(R * kvd * 2));
+    r.v = reinterpret_cast<uint16_t *>(take(R * kvd * 2));
+    r.attn_out = reinterpret_cast<uint16_t *>(take(R * qd * 2));
+    r.ffn_down = reinterpret_cast<uint16_t *>(take(R * H * 2));
+    r.act = reinterpret_cast<uint16_t *>(take(R * F * 2));
+    r.T = T;
+    int32_t *lens = reinterpret_cast<int32_t *>(take(B * 4));
+    r.attn_lens = lens;
+    // the chunk's attention length: positions[b] + T
+    hipLaunchKernelGGL(prefill_lens_kernel, dim3((B + 63) / 64), dim3(64), 0, s->stream, d->positions, lens, (int)B,
+                       (int)T);
+    IMH_HIP(hipGetLastError());
+    rc = run_schedule(d, s, token_ids, r, logits);
+    if (rc) return rc;
+    hipLaunchKernelGGL(decoder_advance_kernel, dim3((B + 63) / 64), dim3(64), 0, s->stream, d->positions, d->seq_lens,
+                       d->status, (int)B, (int)c.max_seq_len, (int)T);
+    IMH_HIP(hipGetLastError());
+    if (!s->capturing)
+        for (auto &q : d->host_positions) q += (int32_t)T;
     return IMH_OK;
 }
 

@@ -438,6 +438,11 @@ class Decoder:
     def step(self, stream: Stream, token_ids, logits):
         check(lib.imh_decoder_step(self._h, stream.handle, _ptr(token_ids), _ptr(logits)))
 
+    def prefill(self, stream: Stream, token_ids, token_count: int, logits):
+        """token_count tokens per sequence (token_ids [batch, token_count]) at the current
+        positions; logits of each sequence's last token (run_pipeline_inner, token_count > 1)."""
+        check(lib.imh_decoder_prefill(self._h, stream.handle, _ptr(token_ids), token_count, _ptr(logits)))
+
     def write_kv(self, stream: Stream, layer: int, k_proj, v_proj, token_count: int, base_pos: int = 0):
         """Write K/V projections [batch, token_count, nkv, head_dim] of one layer into its cache."""
         check(lib.imh_decoder_write_kv(self._h, stream.handle, layer, _ptr(k_proj), _ptr(v_proj), token_count,
