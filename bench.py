@@ -517,7 +517,8 @@ def main():
         us = 1e3 * tot / args.steps
         gbs = down_bytes(B) / (us * 1e-6) / 1e9
         log(f"down kernel B={B}: {us:.2f} us  {gbs:.0f} GB/s ({100 * gbs / HBM_PEAK_GBS:.1f} %)")
-        print(json.dumps({"kernel": "int4_matvec_kernel (down projection)", "batch": B, "us": round(us, 3),
+        print(json.dumps({"kernel": ("int4_band_kernel" if B <= 2 else "int4_matvec_kernel") + " (down projection)",
+                          "batch": B, "us": round(us, 3),
                           "GB/s": round(gbs, 1), "launches": args.steps, "eager": args.eager}))
         return
 
@@ -528,7 +529,8 @@ def main():
     k_gbs = k_bytes / (k_us * 1e-6) / 1e9
     log(f"gate+up kernel: {k_us:.2f} us  {k_gbs:.0f} GB/s ({100 * k_gbs / HBM_PEAK_GBS:.1f} %)")
     if args.kernel == "gate_up":
-        print(json.dumps({"kernel": "int4_matvec_kernel<2,SILU>", "batch": B, "us": round(k_us, 3),
+        print(json.dumps({"kernel": ("int4_band_kernel" if B <= 2 else "int4_matvec_kernel") + "<2, SILU> (gate+up)",
+                          "batch": B, "us": round(k_us, 3),
                           "GB/s": round(k_gbs, 1), "launches": ksteps, "eager": args.eager}))
         return
 
@@ -582,6 +584,36 @@ def main():
             us = 1e3 * t / args.steps
             details[f"down_kernel_b{bb}"] = {"us": round(us, 2),
                                              "GB/s": round(down_bytes(bb) / (us * 1e-6) / 1e9, 1)}
+        # INT8 sensitive-layer weights (down shape) and the INT4 x Q8 decode variant (gate shape)
+        from ironmill_amd import quant as Q
+        rng8 = np.random.default_rng(8)
+        q8w = Q.quantize_int8((rng8.standard_normal((H, F)) * 0.02).astype(np.float32))
+        W8 = [ops.AffineInt8Weight(dev, q8w) for _ in range(max(2, math.ceil(512e6 / q8w.data.nbytes)))]
+        a1 = dev.upload(make_x(1, F, 97))
+        t = time_loop(dev, stream, lambda i: ops.encode_projection_int8(stream, a1, W8[i % len(W8)], y, 1),
+                      args.steps, args.warmup)
+        us = 1e3 * t / args.steps
+        nb = q8w.data.nbytes + q8w.scales.nbytes * 2 + 2 * F + 2 * H
+        details["int8_down_kernel_b1"] = {"us": round(us, 2), "GB/s": round(nb / (us * 1e-6) / 1e9, 1),
+                                          "bytes": nb}
+        del W8
+        qg0 = Q.quantize_int4((rng8.standard_normal((F, H)) * 0.02).astype(np.float32))
+        W4 = [ops.AffineQuantizedWeight(dev, qg0) for _ in range(reps)]
+        q8d, q8s = dev.empty((1, H), np.int8), dev.empty((1, H // 128), np.float32)
+        g1 = dev.empty((1, F), np.float16)
+
+        def q8_step(i):
+            ops.encode_quantize_input_q8(stream, x, 1, H, q8d, q8s)
+            ops.encode_affine_matvec_int4xq8(stream, q8d, q8s, 1, W4[i % reps], g1)
+
+        t = time_loop(dev, stream, q8_step, args.steps, args.warmup)
+        us = 1e3 * t / args.steps
+        nb = F * H * INT4_BYTES_PER_ELEM + 2 * H + 2 * F
+        details["int4xq8_gate_b1"] = {"us": round(us, 2), "GB/s": round(nb / (us * 1e-6) / 1e9, 1),
+                                      "launches": 2, "bytes": int(nb)}
+        del W4
+        log(f"INT8 down B=1: {details['int8_down_kernel_b1']['us']} us; INT4xQ8 gate (quantize + matvec) "
+            f"B=1: {details['int4xq8_gate_b1']['us']} us")
         # prefill INT4 GEMM: M tokens, bf16 and fp8-e4m3 (and f16, the projection op)
         for mm in (512, 2048):
             for (kk, nn) in ((H, F), (F, H)):
@@ -635,7 +667,7 @@ def main():
                    "awq": True, "weight_replicas": reps},
         "roofline": {"bound": "hbm", "achieved": round(k_gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(k_gbs / HBM_PEAK_GBS, 4), "traffic": traffic,
-                     "kernel": "int4_matvec_kernel (fused gate+up, SiLU, AWQ)",
+                     "kernel": ("int4_band_kernel" if B <= 2 else "int4_matvec_kernel") + " (fused gate+up, SiLU, AWQ)",
                      "bytes_per_launch": k_bytes, "us_per_launch": round(k_us, 3)},
         "cpu_baseline": cpu,
         "details": details,

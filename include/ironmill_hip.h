@@ -178,7 +178,7 @@ int imh_encode_ffn_block_int4(imh_stream *stream, const uint16_t *x, uint32_t to
                               int use_gelu);
 
 /* Prefill GEMM at a chosen matrix-core precision (superblock_matmul_int4,
- * affine_matmul.metal:10-152):
+ * affine_matmul.metal:10-152, at the precisions of the prefill workload):
  *   y[m][n] = sum_k a[m][k] * (q[n][k] - z) * s,  f32 accumulate, a = x / awq.
  * IMH_GEMM_F16: x and y f16 -- the projection op above (matvec below 32
  *   tokens, the f16 GEMM from 32);

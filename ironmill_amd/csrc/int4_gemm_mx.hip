@@ -1,6 +1,6 @@
 // int4_gemm_mx.hip -- the INT4-affine (group 128) prefill GEMM with bf16 or
 // fp8-e4m3 matrix-core operands (superblock_matmul_int4, affine_matmul.metal:
-// 10-152, at the precisions of BASELINE configs[3]):
+// 10-152, at the bf16 / fp8 precisions of the prefill workload):
 //
 //     C[m][n] = out( sum_g s[n][g] * sum_{k in g} a[m][k] * (q[n][k] - z[n][g]) ),  f32 accumulate
 //
@@ -24,8 +24,8 @@
 //    covers a whole group.
 //  * a prep kernel writes the operand rows (x / awq rounded, each 8-element
 //    chunk in the slot order the code unpack produces) and their group sums.
-//  * workgroup tile 64 (M) x 128 (bf16) or 256 (fp8) columns, four waves each
-//    owning a quarter of the columns; the
+//  * workgroup tile 64 (M) x 128 columns, four waves each owning a quarter
+//    of the columns; the
 //    next group's A (global -> registers -> other LDS buffer) and B (global ->
 //    registers) are loaded while the current group computes: one barrier per
 //    group.  K is split over workgroups when the tile grid is smaller than
@@ -51,8 +51,8 @@ typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
 constexpr int kGS = 128;
 constexpr int kBM = 64;          // workgroup rows (M)
 constexpr int kThreads = 256;    // 4 waves, each owning 16 x NJ columns
-// 16-column B fragments per wave: 2 for bf16 (its A fragments take 64
-// registers), 4 for fp8 (one f8f6f4 MFMA per group and fragment pair)
+// 16-column B fragments per wave (more spill: the bf16 A fragments take 64
+// registers)
 template <int P> constexpr int frags_per_wave() { return 2; }
 template <int P> constexpr int wg_cols() { return 4 * 16 * frags_per_wave<P>(); }
 constexpr float kE4M3Max = 448.0f;
