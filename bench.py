@@ -190,6 +190,33 @@ def bench_attention(dev, stream, ops, batch, ctx, steps, warmup, layers, eager=F
             "frac": round(gbs / HBM_PEAK_GBS, 4), "bytes": tq_bytes(batch, ctx)}
 
 
+def bench_tq_prefill(dev, stream, ops, batch, ctx, tokens, steps, warmup, eager=False):
+    """TurboQuant causal attention of a prefill chunk: the last `tokens` positions of a
+    ctx-position cache attend to their prefixes (imh_encode_turboquant_attention_tokens)."""
+    nkv, nh, d = 8, 32, 128
+    tq = ops.TurboQuantModel(dev, d, 8, 42)
+    rng = np.random.default_rng(ctx + tokens)
+    c = ops.TurboQuantKvCache(dev, batch, nkv, d, ctx)
+    for p0 in range(0, ctx, 4096):
+        t = min(4096, ctx - p0)
+        kd = dev.upload(rng.standard_normal((batch, t, nkv, d)).astype(np.float16))
+        ops.encode_turboquant_cache_write(stream, tq, c, kd, t, p0, True)
+        ops.encode_turboquant_cache_write(stream, tq, c, kd, t, p0, False)
+        stream.sync()
+    q = dev.upload(rng.standard_normal((batch, tokens, nh, d)).astype(np.float16))
+    out = dev.empty((batch, tokens, nh, d), np.float16)
+
+    def step(i):
+        ops.encode_turboquant_attention(stream, tq, c, q, nh, ctx, out, 1.0 / math.sqrt(d), token_count=tokens)
+
+    ms = (eager_loop if eager else time_loop)(dev, stream, step, steps, warmup) / steps
+    # (query row, position) pairs attended: sum over tokens of their causal lengths
+    pairs = batch * nh * sum(ctx - tokens + t + 1 for t in range(tokens))
+    return {"batch": batch, "ctx": ctx, "tokens": tokens, "us": round(ms * 1e3, 2),
+            "Gpairs/s": round(pairs / (ms * 1e-3) / 1e9, 2),
+            "cache_passes_GB/s": round(tq_bytes(batch, ctx) / (ms * 1e-3) / 1e9, 1)}
+
+
 def bench_fp16_attention(dev, stream, ops, batch, ctx, steps, warmup, layers, eager=False):
     """FP16-KV decode attention (fused_sdpa / FlashDecoding) over `layers` distinct caches."""
     nkv, nh, d = 8, 32, 128
@@ -417,8 +444,8 @@ def main():
                          "256 MB Infinity Cache; 1 measures a cache-resident matrix)")
     ap.add_argument("--decode-only", action="store_true",
                     help="only the Qwen3-4B decode-step lines (B=1 and 8, ctx 8k), for profiling")
-    ap.add_argument("--attention-only", choices=["tq", "fp16"],
-                    help="only the decode attention at ctx 32k and --batch (for rocprofv3 runs)")
+    ap.add_argument("--attention-only", choices=["tq", "fp16", "tq_prefill"],
+                    help="only the decode attention at ctx 32k and --batch (tq_prefill: the causal attention of a 512- or 64-token chunk at ctx 2k / 8k)")
     ap.add_argument("--eager", action="store_true",
                     help="with --attention-only / --kernel: host launches instead of a graph (counter runs)")
     ap.add_argument("--decode-batches", type=int, nargs="+", default=[1, 8])
@@ -460,6 +487,13 @@ def main():
     info = dev.info()
     log(f"device {info['arch']} CUs={info['compute_units']}")
 
+    if args.attention_only == "tq_prefill":
+        for ctx, tokens in ((2048, 512), (8192, 512), (8192, 64)):
+            r = bench_tq_prefill(dev, stream, ops, args.batch, ctx, tokens, max(5, args.steps // 10), 3,
+                                 eager=args.eager)
+            log(f"tq prefill attention B={args.batch} ctx={ctx} T={tokens}: {r['us']} us")
+            print(json.dumps({f"tq_prefill_attention_b{args.batch}_ctx{ctx}_t{tokens}": r}), flush=True)
+        return
     if args.attention_only:
         fn = bench_attention if args.attention_only == "tq" else bench_fp16_attention
         layers = max(1, min(8, 16 // args.batch))

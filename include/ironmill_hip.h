@@ -353,7 +353,13 @@ int imh_encode_turboquant_attention_noalloc(imh_stream *stream, const imh_tq_tab
  * [head_dim] f16; token t of sequence b attends to positions
  * [0, L_b - token_count + t + 1) with L_b as in imh_encode_turboquant_attention
  * (the length including the new tokens, whose K / V the cache already holds).
- * batch x token_count <= 65535. */
+ * One workgroup serves 16 / GQA consecutive tokens x the GQA group's heads
+ * (each KV chunk is read and decoded once for all of them), after a query
+ * prep launch; num_splits as in imh_encode_turboquant_attention (0: automatic,
+ * over the longest causal range), with a combine launch when there are
+ * several.  Uses the stream's scratch (batch x token_count x num_heads KB of
+ * query operands, plus the split partials).  batch x ceil(token_count x GQA /
+ * 16) <= 65535. */
 int imh_encode_turboquant_attention_tokens(imh_stream *stream, const imh_tq_tables *t,
                                            const imh_tq_kv_cache *cache, const uint16_t *q,
                                            uint32_t num_heads, uint32_t token_count, uint32_t seq_len,

@@ -42,7 +42,8 @@ struct imh_buffer {
 };
 
 // Per-stream scratch memory, grown on demand by the host code of an op.
-// Slot 0: INT4 activation operand images; slot 1: attention split partials,
+// Slot 0: INT4 activation operand images, the query operand planes of the
+// TurboQuant prefill attention; slot 1: attention split partials,
 // the gate output of a prefill gate/up op; slot 2: GEMM split-K partials;
 // slot 3: arrival counters of split reductions (zeroed when allocated, left at
 // zero by every kernel that uses them).

@@ -296,6 +296,96 @@ __device__ __forceinline__ float tab_f32(uint32_t e) {
            (float)__builtin_bit_cast(_Float16, (uint16_t)(e >> 16));
 }
 
+// Codebook entry c as (f16 hi | f16 lo << 16): the LDS tables of the
+// attention kernels (an f16 V entry alone would bias every output by its
+// rounding error, a bias that does not average out over positions while the
+// output itself shrinks as 1/sqrt(positions): rel-L2 1.9e-3 at 30k positions
+// of random V).
+__device__ __forceinline__ uint32_t tab_entry(float v) {
+    const _Float16 hi = (_Float16)v;
+    const _Float16 lo = (_Float16)(v - (float)hi);
+    return (uint32_t)__builtin_bit_cast(uint16_t, hi) | ((uint32_t)__builtin_bit_cast(uint16_t, lo) << 16);
+}
+
+// One 16-position chunk of a (sequence, kv head)'s cache as the attention
+// loops read it.  Lane (n, g) = (lane & 15, lane >> 4) takes K code bytes
+// 32 g .. 32 g + 31 of position p0 + n and that position's scales, and V code
+// bytes 8 n .. 8 n + 7 of positions p0 + 4 g .. p0 + 4 g + 3 (the P.V
+// operand's transpose).  Loads go through buffer resources bounded at the
+// range's end: rows at or past it read as zeros and fetch nothing.
+struct ChunkIn {
+    uint4 k0, k1;
+    uint2 v[4];
+    float ksc, krn, vsc;
+};
+struct ChunkRsrc {
+    __amdgpu_buffer_rsrc_t kc, vc, ks, kr, vs;
+};
+__device__ __forceinline__ ChunkRsrc chunk_rsrc(const uint8_t *kcodes, const uint8_t *vcodes, const float *kscales,
+                                                const float *krnorm, const float *vscales, size_t head_base,
+                                                int rows) {
+    constexpr uint32_t kRsrcWord3 = 0x00020000u;
+    ChunkRsrc r;
+    r.kc = __builtin_amdgcn_make_buffer_rsrc((void *)(kcodes + head_base * kD), 0, rows * kD, kRsrcWord3);
+    r.vc = __builtin_amdgcn_make_buffer_rsrc((void *)(vcodes + head_base * kD), 0, rows * kD, kRsrcWord3);
+    r.ks = __builtin_amdgcn_make_buffer_rsrc((void *)(kscales + head_base), 0, rows * 4, kRsrcWord3);
+    r.kr = __builtin_amdgcn_make_buffer_rsrc((void *)(krnorm + head_base), 0, rows * 4, kRsrcWord3);
+    r.vs = __builtin_amdgcn_make_buffer_rsrc((void *)(vscales + head_base), 0, rows * 4, kRsrcWord3);
+    return r;
+}
+__device__ __forceinline__ void load_chunk(const ChunkRsrc &r, int p0, int n_l, int kg, ChunkIn &c) {
+    const int koff = (p0 + n_l) * kD + kg * 32;
+    c.k0 = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(r.kc, koff, 0, 0));
+    c.k1 = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(r.kc, koff + 16, 0, 0));
+    const int voff = (p0 + 4 * kg) * kD + n_l * 8;
+#pragma unroll
+    for (int i = 0; i < 4; i++)
+        c.v[i] = __builtin_bit_cast(uint2, __builtin_amdgcn_raw_buffer_load_b64(r.vc, voff + i * kD, 0, 0));
+    const int soff = (p0 + n_l) * 4;
+    c.ksc = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(r.ks, soff, 0, 0));
+    c.krn = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(r.kr, soff, 0, 0));
+    c.vsc = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(r.vs, soff, 0, 0));
+}
+
+// Score operands B of k-slice j from the lane's code words kw[2j], kw[2j+1]
+// (dims 32 g + 8 j .. + 7, k-slot order {0, 2, 1, 3} within each word): the
+// codebook entries' f16 hi and lo parts (one LDS lookup per byte) and the
+// +-1 QJL signs straight from bit 7.
+__device__ __forceinline__ void k_operands(const uint32_t *kw2, const uint32_t *ktab, half8_t &Bh, half8_t &Bl,
+                                           half8_t &Bs) {
+    uint32_t bh[4], bl[4], bs[4];
+#pragma unroll
+    for (int hw = 0; hw < 2; hw++) {
+        const uint32_t w = kw2[hw];
+        const uint32_t t0 = ktab[w & 0xFF];
+        const uint32_t t1 = ktab[(w >> 8) & 0xFF];
+        const uint32_t t2 = ktab[(w >> 16) & 0xFF];
+        const uint32_t t3 = ktab[w >> 24];
+        bh[2 * hw] = __builtin_amdgcn_perm(t2, t0, 0x05040100u);
+        bl[2 * hw] = __builtin_amdgcn_perm(t2, t0, 0x07060302u);
+        bh[2 * hw + 1] = __builtin_amdgcn_perm(t3, t1, 0x05040100u);
+        bl[2 * hw + 1] = __builtin_amdgcn_perm(t3, t1, 0x07060302u);
+        // +1 (0x3C00) where bit 7 of the code is set, -1 (0xBC00) where not
+        bs[2 * hw] = ((w << 8) & 0x80008000u) ^ 0xBC00BC00u;
+        bs[2 * hw + 1] = (w & 0x80008000u) ^ 0xBC00BC00u;
+    }
+    Bh = __builtin_bit_cast(half8_t, make_uint4(bh[0], bh[1], bh[2], bh[3]));
+    Bl = __builtin_bit_cast(half8_t, make_uint4(bl[0], bl[1], bl[2], bl[3]));
+    Bs = __builtin_bit_cast(half8_t, make_uint4(bs[0], bs[1], bs[2], bs[3]));
+}
+
+// P.V operand B of dim block j: codebook values (hi, lo) of byte j of the
+// lane's four V position rows
+__device__ __forceinline__ half8_t v_operand(const ChunkIn &c, int j, const uint32_t *vtab) {
+    uint32_t e[4];
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+        const uint32_t word = j < 4 ? c.v[i].x : c.v[i].y;
+        e[i] = vtab[(word >> (8 * (j & 3))) & 0xFF];
+    }
+    return __builtin_bit_cast(half8_t, make_uint4(e[0], e[1], e[2], e[3]));
+}
+
 // Occupancy: 3 waves per SIMD (168 VGPRs); the fused token writer's extra
 // live state needs more than that, so it runs at 2 rather than spill.
 template <int GQA, bool FUSED>
@@ -357,39 +447,10 @@ __global__ void __launch_bounds__(64 * kWaves) __attribute__((amdgpu_waves_per_e
     const int n_l = lane & 15;   // score layout: position; P.V layout: column c
     const int kg = lane >> 4;    // lane group: K dims block / head / V position quad
 
-    // Loads go through buffer resources bounded at p_end: rows at or past the
-    // split's end read as zeros (their weights are zero), so no clamping, and
-    // each lane's offsets advance by one add per chunk.
-    constexpr uint32_t kRsrcWord3 = 0x00020000u;
-    const int rows = p_end > 0 ? p_end : 0;
-    const __amdgpu_buffer_rsrc_t kc_r = __builtin_amdgcn_make_buffer_rsrc(
-        (void *)(kcodes + head_base * kD), 0, rows * kD, kRsrcWord3);
-    const __amdgpu_buffer_rsrc_t vc_r = __builtin_amdgcn_make_buffer_rsrc(
-        (void *)(vcodes + head_base * kD), 0, rows * kD, kRsrcWord3);
-    const __amdgpu_buffer_rsrc_t ks_r = __builtin_amdgcn_make_buffer_rsrc(
-        (void *)(kscales + head_base), 0, rows * 4, kRsrcWord3);
-    const __amdgpu_buffer_rsrc_t kr_r = __builtin_amdgcn_make_buffer_rsrc(
-        (void *)(krnorm + head_base), 0, rows * 4, kRsrcWord3);
-    const __amdgpu_buffer_rsrc_t vs_r = __builtin_amdgcn_make_buffer_rsrc(
-        (void *)(vscales + head_base), 0, rows * 4, kRsrcWord3);
-    struct ChunkIn {
-        uint4 k0, k1;
-        uint2 v[4];
-        float ksc, krn, vsc;
-    };
-    auto load_chunk = [&](int p0, ChunkIn &c) __attribute__((always_inline)) {
-        const int koff = (p0 + n_l) * kD + kg * 32;
-        c.k0 = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(kc_r, koff, 0, 0));
-        c.k1 = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(kc_r, koff + 16, 0, 0));
-        const int voff = (p0 + 4 * kg) * kD + n_l * 8;
-#pragma unroll
-        for (int i = 0; i < 4; i++)
-            c.v[i] = __builtin_bit_cast(uint2, __builtin_amdgcn_raw_buffer_load_b64(vc_r, voff + i * kD, 0, 0));
-        const int soff = (p0 + n_l) * 4;
-        c.ksc = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(ks_r, soff, 0, 0));
-        c.krn = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(kr_r, soff, 0, 0));
-        c.vsc = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(vs_r, soff, 0, 0));
-    };
+    // loads bounded at p_end: rows at or past the split's end read as zeros
+    // (their weights are zero), so no clamping, and each lane's offsets
+    // advance by one add per chunk
+    const ChunkRsrc crs = chunk_rsrc(kcodes, vcodes, kscales, krnorm, vscales, head_base, p_end > 0 ? p_end : 0);
     // wave w takes chunks p_begin + 16 w + 64 i of the split, one chunk in
     // flight; loads past the split's end read zeros and fetch nothing, so
     // they are issued unconditionally
@@ -420,21 +481,12 @@ __global__ void __launch_bounds__(64 * kWaves) __attribute__((amdgpu_waves_per_e
     }
     ChunkIn cur;
     const int p_first = p_begin + wave * kChunk;
-    load_chunk(p_first, cur);
+    load_chunk(crs, p_first, n_l, kg, cur);
     __builtin_amdgcn_sched_barrier(0);   // every load above issues before the first wait
 
-    // tables: K and V codebooks as (f16 hi | f16 lo << 16).  An f16 V entry
-    // alone would bias every output by its rounding error, a bias that does
-    // not average out over positions while the output itself shrinks as
-    // 1/sqrt(positions) (rel-L2 1.9e-3 at 30k positions of random V).
-    {
-        const _Float16 hi = (_Float16)kc;
-        const _Float16 lo = (_Float16)(kc - (float)hi);
-        ktab[tid] = (uint32_t)__builtin_bit_cast(uint16_t, hi) | ((uint32_t)__builtin_bit_cast(uint16_t, lo) << 16);
-        const _Float16 vh = (_Float16)vc;
-        const _Float16 vl = (_Float16)(vc - (float)vh);
-        vtab[tid] = (uint32_t)__builtin_bit_cast(uint16_t, vh) | ((uint32_t)__builtin_bit_cast(uint16_t, vl) << 16);
-    }
+    // tables: K and V codebooks as f16 hi + lo pairs
+    ktab[tid] = tab_entry(kc);
+    vtab[tid] = tab_entry(vc);
     // q_rot = D.H.D/sqrt(d) q: wave hh rotates head hh in registers (lane
     // holds elements lane and lane + 64; butterfly strides 1..32 by xor
     // shuffles, stride 64 in the lane) into qs[hh][0]
@@ -630,25 +682,8 @@ __global__ void __launch_bounds__(64 * kWaves) __attribute__((amdgpu_waves_per_e
             float4_t d1 = {0, 0, 0, 0};
     #pragma unroll
             for (int j = 0; j < 4; j++) {
-                uint32_t bh[4], bl[4], bs[4];
-    #pragma unroll
-                for (int hw = 0; hw < 2; hw++) {
-                    const uint32_t w = kw[2 * j + hw];
-                    const uint32_t t0 = ktab[w & 0xFF];
-                    const uint32_t t1 = ktab[(w >> 8) & 0xFF];
-                    const uint32_t t2 = ktab[(w >> 16) & 0xFF];
-                    const uint32_t t3 = ktab[w >> 24];
-                    bh[2 * hw] = __builtin_amdgcn_perm(t2, t0, 0x05040100u);
-                    bl[2 * hw] = __builtin_amdgcn_perm(t2, t0, 0x07060302u);
-                    bh[2 * hw + 1] = __builtin_amdgcn_perm(t3, t1, 0x05040100u);
-                    bl[2 * hw + 1] = __builtin_amdgcn_perm(t3, t1, 0x07060302u);
-                    // +1 (0x3C00) where bit 7 of the code is set, -1 (0xBC00) where not
-                    bs[2 * hw] = ((w << 8) & 0x80008000u) ^ 0xBC00BC00u;
-                    bs[2 * hw + 1] = (w & 0x80008000u) ^ 0xBC00BC00u;
-                }
-                const half8_t Bh = __builtin_bit_cast(half8_t, make_uint4(bh[0], bh[1], bh[2], bh[3]));
-                const half8_t Bl = __builtin_bit_cast(half8_t, make_uint4(bl[0], bl[1], bl[2], bl[3]));
-                const half8_t Bs = __builtin_bit_cast(half8_t, make_uint4(bs[0], bs[1], bs[2], bs[3]));
+                half8_t Bh, Bl, Bs;
+                k_operands(&kw[2 * j], ktab, Bh, Bl, Bs);
                 d1 = __builtin_amdgcn_mfma_f32_16x16x32_f16(aqk[j], Bh, d1, 0, 0, 0);
                 d1 = __builtin_amdgcn_mfma_f32_16x16x32_f16(aqh[j], Bl, d1, 0, 0, 0);
                 d1 = __builtin_amdgcn_mfma_f32_16x16x32_f16(aqs[j], Bs, d1, 0, 0, 0);
@@ -680,20 +715,14 @@ __global__ void __launch_bounds__(64 * kWaves) __attribute__((amdgpu_waves_per_e
             // byte j of the four position rows ----
     #pragma unroll
             for (int j = 0; j < 8; j++) {
-                uint32_t e[4];
-    #pragma unroll
-                for (int i = 0; i < 4; i++) {
-                    const uint32_t word = j < 4 ? c.v[i].x : c.v[i].y;
-                    e[i] = vtab[(word >> (8 * (j & 3))) & 0xFF];
-                }
-                const half8_t bv = __builtin_bit_cast(half8_t, make_uint4(e[0], e[1], e[2], e[3]));
+                const half8_t bv = v_operand(c, j, vtab);
                 acc[j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(wa, bv, acc[j], 0, 0, 0);
             }
             __builtin_amdgcn_wave_barrier();   // wbuf is rewritten next chunk
         };
         for (int p0 = p_first; p0 < p_end; p0 += kChunk * kWaves) {
             const ChunkIn c = cur;
-            load_chunk(p0 + kChunk * kWaves, cur);
+            load_chunk(crs, p0 + kChunk * kWaves, n_l, kg, cur);
             process(c, p0);
         }
 
@@ -844,6 +873,351 @@ __global__ void __launch_bounds__(64 * kWaves) __attribute__((amdgpu_waves_per_e
     }
 }
 
+// ---------------------------------------------------------------------------
+// Attention of a prefill chunk (token_count > 1).  The decode kernel fills the
+// 16 rows of its score MFMA with one token's GQA heads times four partial
+// products (query hi / lo against codebook hi / lo, QJL hi / lo), and uses 4
+// of the 16 rows of its P.V MFMA; it runs once per query token, decoding and
+// reading every KV chunk T times.  Here the 16 MFMA rows are 16 / GQA
+// consecutive tokens x the GQA heads: a KV chunk's codes are looked up once
+// for all of them, the partial products go to separate MFMAs (20 per chunk
+// instead of 12 per token), and P.V fills every row.
+//   * tq_query_prep_kernel rotates each query row and projects it onto the
+//     QJL matrix (the decode prologue's arithmetic, same f32 order) and
+//     stores the four f16 operand planes q_hi, q_lo, s_hi, s_lo in MFMA
+//     k-slot order;
+//   * tq_prefill_attention_kernel<GQA>, one workgroup per (split, kv head,
+//     token block of a sequence), keeps a per-row online softmax; each row
+//     has its own causal bound (turboquant.metal:268);
+//   * with several splits, tq_split_combine_kernel merges the partials
+//     (log-sum-exp, fused_sdpa_reduce, flash_decode.metal:163-215) and
+//     rotates back; with one, the attention kernel does.
+// ---------------------------------------------------------------------------
+constexpr int kQPlanes = 4;   // q_hi, q_lo, s_hi, s_lo, kD halfs each
+
+// element p of an operand plane holds dimension (p & ~7) | slot(p & 7): the
+// k-slot order {0, 2, 1, 3, 4, 6, 5, 7} of the code-byte unpack (bits 0 and 1
+// swapped)
+__device__ __forceinline__ int plane_dim(int p) { return (p & ~7) | ((p & 1) << 1) | ((p >> 1) & 1) | (p & 4); }
+
+// grid ceil(rows / 4), block 256: wave w rotates query row 4 blockIdx.x + w
+// (rows = batch x tokens x heads, [row][kD] f16), then the workgroup projects
+// its four rows and writes their planes ([row][kQPlanes][kD] f16).
+__global__ void __launch_bounds__(256) tq_query_prep_kernel(const __half *__restrict__ q, int rows,
+                                                            const float *__restrict__ signs,
+                                                            const float *__restrict__ qjl_t,
+                                                            _Float16 *__restrict__ planes) {
+    __shared__ float qs[4][2][kD];
+    __shared__ float om[4][4][kD];
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int row0 = blockIdx.x * 4;
+    const int kr = tid >> 5, dq = tid & 31;
+    const float rscale = 1.0f / sqrtf((float)kD);
+    const __half *qh = q + (size_t)min(row0 + wave, rows - 1) * kD;
+    const float sg0 = signs[lane], sg1 = signs[lane + 64];
+    float x0 = __half2float(qh[lane]) * sg0, x1 = __half2float(qh[lane + 64]) * sg1;
+    float4 st[16];
+    {
+        const float4 *s4 = reinterpret_cast<const float4 *>(qjl_t) + (size_t)kr * 16 * (kD / 4) + dq;
+#pragma unroll
+        for (int i = 0; i < 16; i++) st[i] = s4[(size_t)i * (kD / 4)];
+    }
+    x0 = hadamard64(x0, lane);
+    x1 = hadamard64(x1, lane);
+    qs[wave][0][lane] = (x0 + x1) * (sg0 * rscale);
+    qs[wave][0][lane + 64] = (x0 - x1) * (sg1 * rscale);
+    __syncthreads();
+    float4 pr[4];
+#pragma unroll
+    for (int hh = 0; hh < 4; hh++) pr[hh] = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+#pragma unroll
+    for (int i = 0; i < 16; i++) {
+#pragma unroll
+        for (int hh = 0; hh < 4; hh++) {
+            const float qv = qs[hh][0][kr * 16 + i];
+            pr[hh].x = __builtin_fmaf(st[i].x, qv, pr[hh].x);
+            pr[hh].y = __builtin_fmaf(st[i].y, qv, pr[hh].y);
+            pr[hh].z = __builtin_fmaf(st[i].z, qv, pr[hh].z);
+            pr[hh].w = __builtin_fmaf(st[i].w, qv, pr[hh].w);
+        }
+    }
+#pragma unroll
+    for (int hh = 0; hh < 4; hh++) {
+        pr[hh].x += __shfl_xor(pr[hh].x, 32);
+        pr[hh].y += __shfl_xor(pr[hh].y, 32);
+        pr[hh].z += __shfl_xor(pr[hh].z, 32);
+        pr[hh].w += __shfl_xor(pr[hh].w, 32);
+        if (lane < 32) reinterpret_cast<float4 *>(&om[wave][hh][0])[dq] = pr[hh];
+    }
+    __syncthreads();
+    for (int e = tid; e < 4 * kD; e += 256) {
+        const int hh = e / kD, d = e % kD;
+        qs[hh][1][d] = (om[0][hh][d] + om[1][hh][d]) + (om[2][hh][d] + om[3][hh][d]);
+    }
+    __syncthreads();
+    for (int e = tid; e < 4 * kD; e += 256) {
+        const int hh = e / kD, p = e % kD;
+        if (row0 + hh >= rows) continue;
+        const int d = plane_dim(p);
+        const float vq = qs[hh][0][d], vs = qs[hh][1][d];
+        const _Float16 qhi = (_Float16)vq, shi = (_Float16)vs;
+        _Float16 *dst = planes + (size_t)(row0 + hh) * kQPlanes * kD + p;
+        dst[0] = qhi;
+        dst[kD] = (_Float16)(vq - (float)qhi);
+        dst[2 * kD] = shi;
+        dst[3 * kD] = (_Float16)(vs - (float)shi);
+    }
+}
+
+// grid (S, nkv, batch x ceil(T / TB)), block 256; TB = 16 / GQA tokens per
+// workgroup.  MFMA row r = TB-local token r / GQA, head r % GQA; lane (n, g)
+// holds output rows 4 g .. 4 g + 3 at column n.
+template <int GQA>
+__global__ void __launch_bounds__(64 * kWaves) __attribute__((amdgpu_waves_per_eu(2))) tq_prefill_attention_kernel(
+    const _Float16 *__restrict__ planes, int nh, int nkv, int max_seq, int seq_len, int T,
+    const int32_t *__restrict__ seq_lens, float attn_scale, const float *__restrict__ signs,
+    const float *__restrict__ kcb, const float *__restrict__ vcb, const uint8_t *__restrict__ kcodes,
+    const uint8_t *__restrict__ vcodes, const float *__restrict__ kscales, const float *__restrict__ vscales,
+    const float *__restrict__ krnorm, int split_len, float *__restrict__ part_o, float *__restrict__ part_m,
+    float *__restrict__ part_l, __half *__restrict__ out) {
+    constexpr int TB = 16 / GQA;
+    __shared__ uint32_t ktab[256];
+    __shared__ uint32_t vtab[256];
+    __shared__ _Float16 wbuf[kWaves][16][16];
+    __shared__ float om[kWaves][16][kD];
+    __shared__ float mm[kWaves][16];
+    __shared__ float ll[kWaves][16];
+
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int wave = tid >> 6;
+    const int S = gridDim.x, split = blockIdx.x, kvh = blockIdx.y;
+    const int ntb = (T + TB - 1) / TB;
+    const int b = blockIdx.z / ntb;
+    const int t0 = (blockIdx.z - b * ntb) * TB;
+    int L = seq_lens ? min(seq_lens[b], seq_len) : seq_len;
+    L = L < 0 ? 0 : (L > max_seq ? max_seq : L);
+    // token t sees positions < L - T + t + 1 (turboquant.metal:268)
+    auto bound = [&](int r) {
+        const int t = t0 + r / GQA;
+        return t < T ? max(0, L - (T - 1 - t)) : 0;
+    };
+    const int Lmax = max(0, L - (T - min(t0 + TB, T)));
+    const int p_begin = split * split_len;
+    const int p_end = min(p_begin + split_len, Lmax);
+    const size_t head_base = ((size_t)b * nkv + kvh) * (size_t)max_seq;
+    const int n_l = lane & 15;
+    const int kg = lane >> 4;
+    const ChunkRsrc crs = chunk_rsrc(kcodes, vcodes, kscales, krnorm, vscales, head_base, p_end > 0 ? p_end : 0);
+
+    // operands A: row am = lane & 15, k-slice j = the 8 halfs at plane
+    // offset 32 g + 8 j (rows past the chunk's tokens repeat the last one and
+    // are masked)
+    const int am = lane & 15;
+    const int at = min(t0 + am / GQA, T - 1);
+    const _Float16 *pa =
+        planes + (((size_t)b * T + at) * nh + kvh * GQA + am % GQA) * (kQPlanes * kD) + kg * 32;
+    half8_t aqh[4], aql[4], ash[4], asl[4];
+#pragma unroll
+    for (int j = 0; j < 4; j++) {
+        aqh[j] = *reinterpret_cast<const half8_t *>(pa + 8 * j);
+        aql[j] = *reinterpret_cast<const half8_t *>(pa + kD + 8 * j);
+        ash[j] = *reinterpret_cast<const half8_t *>(pa + 2 * kD + 8 * j);
+        asl[j] = *reinterpret_cast<const half8_t *>(pa + 3 * kD + 8 * j);
+    }
+    const float kc = kcb[tid & 0x7F], vc = vcb[tid];
+    ChunkIn cur, nxt;
+    const int p_first = p_begin + wave * kChunk;
+    load_chunk(crs, p_first, n_l, kg, cur);
+    __builtin_amdgcn_sched_barrier(0);   // every load above issues before the first wait
+    ktab[tid] = tab_entry(kc);
+    vtab[tid] = tab_entry(vc);
+    int bnd[4];
+#pragma unroll
+    for (int rr = 0; rr < 4; rr++) bnd[rr] = min(bound(4 * kg + rr), p_end);
+    __syncthreads();
+
+    // scores in log2 units (attn_scale * log2(e) folded into the per-position
+    // scales): the softmax exponentials are single exp2s
+    const float sl2 = attn_scale * 1.44269504f;
+    const float qf2 = sqrtf(2.0f / 3.14159265f) / (float)kD * sl2;
+    // per row: the running maximum (uniform over the row's 16 lanes) and this
+    // lane's share of the running sum (the row's sum is reduced once, after
+    // the loop: every lane of a row rescales by the same factor)
+    float m_run[4], l_run[4];
+    float4_t acc[8];
+#pragma unroll
+    for (int rr = 0; rr < 4; rr++) {
+        m_run[rr] = -INFINITY;
+        l_run[rr] = 0.0f;
+    }
+#pragma unroll
+    for (int j = 0; j < 8; j++) acc[j] = float4_t{0, 0, 0, 0};
+
+    auto process = [&](const ChunkIn &c, const int p0) __attribute__((always_inline)) {
+        // ---- scores of 16 rows x 16 positions ----
+        const uint32_t kw[8] = {c.k0.x, c.k0.y, c.k0.z, c.k0.w, c.k1.x, c.k1.y, c.k1.z, c.k1.w};
+        float4_t dq = {0, 0, 0, 0}, ds = {0, 0, 0, 0};
+#pragma unroll
+        for (int j = 0; j < 4; j++) {
+            half8_t Bh, Bl, Bs;
+            k_operands(&kw[2 * j], ktab, Bh, Bl, Bs);
+            dq = __builtin_amdgcn_mfma_f32_16x16x32_f16(aqh[j], Bh, dq, 0, 0, 0);
+            ds = __builtin_amdgcn_mfma_f32_16x16x32_f16(ash[j], Bs, ds, 0, 0, 0);
+            dq = __builtin_amdgcn_mfma_f32_16x16x32_f16(aqh[j], Bl, dq, 0, 0, 0);
+            ds = __builtin_amdgcn_mfma_f32_16x16x32_f16(asl[j], Bs, ds, 0, 0, 0);
+            dq = __builtin_amdgcn_mfma_f32_16x16x32_f16(aql[j], Bh, dq, 0, 0, 0);
+        }
+        const float ks2 = c.ksc * sl2;
+        const float qw2 = c.krn * qf2 * c.ksc;
+        float corr[4];
+        bool grew = false;
+#pragma unroll
+        for (int rr = 0; rr < 4; rr++) {
+            const bool valid = (p0 + n_l) < bnd[rr];
+            const float sc = valid ? __builtin_fmaf(dq[rr], ks2, ds[rr] * qw2) : -INFINITY;
+            const float nm = fmaxf(m_run[rr], imh_dpp::row16_max(sc));
+            const bool live = nm != -INFINITY;   // a row with no position yet keeps weight 0
+            corr[rr] = live ? __builtin_amdgcn_exp2f(m_run[rr] - nm) : 1.0f;
+            const float w = live ? __builtin_amdgcn_exp2f(sc - nm) : 0.0f;
+            l_run[rr] = __builtin_fmaf(l_run[rr], corr[rr], w);
+            m_run[rr] = nm;
+            grew |= corr[rr] != 1.0f;
+            wbuf[wave][4 * kg + rr][n_l] = (_Float16)(w * c.vsc);
+        }
+        if (__builtin_amdgcn_ballot_w64(grew)) {   // some row's max grew
+#pragma unroll
+            for (int j = 0; j < 8; j++)
+#pragma unroll
+                for (int rr = 0; rr < 4; rr++) acc[j][rr] *= corr[rr];
+        }
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+        // operand A of P.V: row am's weights at positions 4 g .. 4 g + 3, each
+        // twice (against the V entries' hi and lo halves)
+        const half4_t w4 = *reinterpret_cast<const half4_t *>(&wbuf[wave][am][4 * kg]);
+        const half8_t wa = {w4[0], w4[0], w4[1], w4[1], w4[2], w4[2], w4[3], w4[3]};
+#pragma unroll
+        for (int j = 0; j < 8; j++)
+            acc[j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(wa, v_operand(c, j, vtab), acc[j], 0, 0, 0);
+        __builtin_amdgcn_wave_barrier();   // wbuf is rewritten next chunk
+    };
+    // two chunk register sets in turn (no copies): the next chunk's loads are
+    // in flight while one is processed
+    constexpr int kStep = kChunk * kWaves;
+    for (int p0 = p_first; p0 < p_end; p0 += 2 * kStep) {
+        load_chunk(crs, p0 + kStep, n_l, kg, nxt);
+        process(cur, p0);
+        if (p0 + kStep >= p_end) break;
+        load_chunk(crs, p0 + 2 * kStep, n_l, kg, cur);
+        process(nxt, p0 + kStep);
+    }
+#pragma unroll
+    for (int rr = 0; rr < 4; rr++) l_run[rr] = imh_dpp::row16_sum(l_run[rr]);
+
+    // lane (c, g): acc[j][rr] = o[row 4 g + rr][dim 8 c + j]
+#pragma unroll
+    for (int rr = 0; rr < 4; rr++) {
+        float4 *dst = reinterpret_cast<float4 *>(&om[wave][4 * kg + rr][n_l * 8]);
+        dst[0] = make_float4(acc[0][rr], acc[1][rr], acc[2][rr], acc[3][rr]);
+        dst[1] = make_float4(acc[4][rr], acc[5][rr], acc[6][rr], acc[7][rr]);
+        if (n_l == 0) {
+            mm[wave][4 * kg + rr] = m_run[rr];
+            ll[wave][4 * kg + rr] = l_run[rr];
+        }
+    }
+    __syncthreads();
+    // combine the waves (maxima in log2 units); with one split normalise (in
+    // place: element (r, d) of om[0] is read and written by one thread), else
+    // publish the partial
+    for (int e = tid; e < 16 * kD; e += 64 * kWaves) {
+        const int r = e / kD, d = e % kD;
+        float M = -INFINITY;
+        for (int w = 0; w < kWaves; w++) M = fmaxf(M, mm[w][r]);
+        float ov = 0.0f, lv = 0.0f;
+        if (M != -INFINITY) {
+            for (int w = 0; w < kWaves; w++) {
+                if (mm[w][r] == -INFINITY) continue;
+                const float f = __builtin_amdgcn_exp2f(mm[w][r] - M);
+                ov += om[w][r][d] * f;
+                lv += ll[w][r] * f;
+            }
+        }
+        if (S == 1) {
+            om[0][r][d] = (ov / fmaxf(lv, 1e-10f)) * signs[d];
+        } else if (t0 + r / GQA < T) {
+            const size_t pidx = (((size_t)b * T + t0 + r / GQA) * nh + kvh * GQA + r % GQA) * S + split;
+            part_o[pidx * kD + d] = ov;
+            if (d == 0) {
+                part_m[pidx] = M;
+                part_l[pidx] = lv;
+            }
+        }
+    }
+    if (S > 1) return;
+    __syncthreads();
+    // rotate back: o = D.H.D/sqrt(d) o_rot, wave w on rows w, w + 4, ..
+    const float rscale = 1.0f / sqrtf((float)kD);
+    const float sg0 = signs[lane], sg1 = signs[lane + 64];
+    for (int r = wave; r < 16; r += kWaves) {
+        const int t = t0 + r / GQA;
+        if (t >= T) break;   // rows grow with t
+        float x0 = om[0][r][lane], x1 = om[0][r][lane + 64];
+        x0 = hadamard64(x0, lane);
+        x1 = hadamard64(x1, lane);
+        __half *o = out + (((size_t)b * T + t) * nh + kvh * GQA + r % GQA) * kD;
+        o[lane] = __float2half((x0 + x1) * (sg0 * rscale));
+        o[lane + 64] = __float2half((x0 - x1) * (sg1 * rscale));
+    }
+}
+
+// grid ceil(rows / 4), block 256: wave w merges the S split partials of row
+// 4 blockIdx.x + w ([row][S] maxima in log2 units and sums, [row][S][kD]
+// outputs) and rotates the result back into out[row].
+__global__ void __launch_bounds__(256) tq_split_combine_kernel(const float *__restrict__ part_o,
+                                                               const float *__restrict__ part_m,
+                                                               const float *__restrict__ part_l, int rows, int S,
+                                                               const float *__restrict__ signs,
+                                                               __half *__restrict__ out) {
+    __shared__ float fs[4][kMaxSplits];
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int row = blockIdx.x * 4 + wave;
+    if (row >= rows) return;   // no workgroup barrier below
+    const float *pm = part_m + (size_t)row * S;
+    const float *pl = part_l + (size_t)row * S;
+    float mx = -INFINITY;
+    for (int sp = lane; sp < S; sp += 64) mx = fmaxf(mx, pm[sp]);
+#pragma unroll
+    for (int st = 32; st >= 1; st >>= 1) mx = fmaxf(mx, __shfl_xor(mx, st));
+    float lsum = 0.0f;
+    for (int sp = lane; sp < S; sp += 64) {
+        const float m = pm[sp];
+        const float f = (mx == -INFINITY || m == -INFINITY) ? 0.0f : __builtin_amdgcn_exp2f(m - mx);
+        fs[wave][sp] = f;
+        lsum = __builtin_fmaf(f, pl[sp], lsum);
+    }
+    lsum = imh_qk::wave_sum64(lsum);
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    const float *po = part_o + (size_t)row * S * kD;
+    float o0 = 0.0f, o1 = 0.0f;
+    for (int sp = 0; sp < S; sp++) {
+        const float f = fs[wave][sp];
+        o0 = __builtin_fmaf(po[(size_t)sp * kD + lane], f, o0);
+        o1 = __builtin_fmaf(po[(size_t)sp * kD + lane + 64], f, o1);
+    }
+    const float inv = 1.0f / fmaxf(lsum, 1e-10f);
+    const float sg0 = signs[lane], sg1 = signs[lane + 64];
+    float x0 = o0 * inv * sg0, x1 = o1 * inv * sg1;
+    x0 = hadamard64(x0, lane);
+    x1 = hadamard64(x1, lane);
+    const float rscale = 1.0f / sqrtf((float)kD);
+    out[(size_t)row * kD + lane] = __float2half((x0 + x1) * (sg0 * rscale));
+    out[(size_t)row * kD + lane + 64] = __float2half((x0 - x1) * (sg1 * rscale));
+}
+
 int check_cache(const imh_tq_tables *t, const imh_tq_kv_cache *c, const char *who) {
     if (!t || !c) return imh::fail(IMH_EINVAL, std::string(who) + ": NULL tables or cache");
     if (!c->k_codes || !c->v_codes || !c->k_scales || !c->v_scales || !c->k_r_norms)
@@ -958,6 +1332,68 @@ int noalloc_scratch_init(int ordinal) {
 
 extern "C" {
 
+// token_count > 1: query prep, the token-block kernel and, with several
+// splits, the combine.  Splits as for decode (~512 workgroups, none shorter
+// than 256 positions unless num_splits asks), over the longest causal range.
+static int run_prefill_attention(imh_stream *stream, const imh_tq_tables *t, const imh_tq_kv_cache *cache,
+                                 const uint16_t *q, uint32_t num_heads, uint32_t gqa, uint32_t L,
+                                 const int32_t *seq_lens, float attn_scale, uint16_t *out,
+                                 uint32_t num_splits, uint32_t T, const char *who) {
+    const uint32_t nkv = cache->num_kv_heads;
+    const uint32_t TB = 16 / gqa;
+    const uint32_t ntb = (T + TB - 1) / TB;
+    if ((uint64_t)cache->batch * ntb > 65535)
+        return imh::fail(IMH_EINVAL, std::string(who) + ": batch x token blocks above 65535");
+    const size_t rows = (size_t)cache->batch * T * num_heads;
+    if (rows > (size_t)INT32_MAX / 4)
+        return imh::fail(IMH_EINVAL, std::string(who) + ": batch x token_count x num_heads too large");
+    uint32_t want = num_splits;
+    if (want == 0) {
+        const uint32_t groups = cache->batch * ntb * nkv;
+        want = std::min<uint32_t>((512 + groups - 1) / groups, std::max<uint32_t>(1, L / kAutoSplitLen));
+    }
+    const uint32_t max_splits = std::max<uint32_t>(1, (L + kSplitQuantum - 1) / kSplitQuantum);
+    want = std::max<uint32_t>(1, std::min(want, std::min<uint32_t>(max_splits, kMaxSplits)));
+    uint32_t split_len = (L + want - 1) / want;
+    split_len = std::max<uint32_t>(kSplitQuantum, (split_len + kSplitQuantum - 1) / kSplitQuantum * kSplitQuantum);
+    const uint32_t S = std::max<uint32_t>(1, (L + split_len - 1) / split_len);
+
+    void *pl_scr = nullptr, *part = nullptr;
+    int rc = imh::stream_scratch(stream, 0, rows * kQPlanes * kD * sizeof(_Float16), &pl_scr);
+    if (rc) return rc;
+    float *po = nullptr, *pm = nullptr, *pls = nullptr;
+    if (S > 1) {
+        rc = imh::stream_scratch(stream, 1, rows * S * (kD + 2) * sizeof(float), &part);
+        if (rc) return rc;
+        po = static_cast<float *>(part);
+        pm = po + rows * S * kD;
+        pls = pm + rows * S;
+    }
+    _Float16 *planes = static_cast<_Float16 *>(pl_scr);
+    const unsigned qblocks = (unsigned)((rows + 3) / 4);
+    hipLaunchKernelGGL(tq_query_prep_kernel, dim3(qblocks), dim3(256), 0, stream->stream,
+                       reinterpret_cast<const __half *>(q), (int)rows, t->signs, t->qjl_t, planes);
+    IMH_HIP(hipGetLastError());
+    dim3 grid(S, nkv, cache->batch * ntb);
+#define IMH_TQ_PREFILL(G)                                                                                       \
+    hipLaunchKernelGGL((tq_prefill_attention_kernel<G>), grid, dim3(64 * kWaves), 0, stream->stream, planes,      \
+                       (int)num_heads, (int)nkv, (int)cache->max_seq_len, (int)L, (int)T, seq_lens, attn_scale,   \
+                       t->signs, t->k_codebook, t->v_codebook, cache->k_codes, cache->v_codes, cache->k_scales,   \
+                       cache->v_scales, cache->k_r_norms, (int)split_len, po, pm, pls,                           \
+                       reinterpret_cast<__half *>(out))
+    if (gqa == 4) IMH_TQ_PREFILL(4);
+    else if (gqa == 2) IMH_TQ_PREFILL(2);
+    else IMH_TQ_PREFILL(1);
+#undef IMH_TQ_PREFILL
+    IMH_HIP(hipGetLastError());
+    if (S > 1) {
+        hipLaunchKernelGGL(tq_split_combine_kernel, dim3(qblocks), dim3(256), 0, stream->stream, po, pm, pls,
+                           (int)rows, (int)S, t->signs, reinterpret_cast<__half *>(out));
+        IMH_HIP(hipGetLastError());
+    }
+    return IMH_OK;
+}
+
 // fixed_scratch: the no-alloc entry point's per-device array (NULL: the
 // stream's scratch slots, grown on demand)
 static int run_attention(imh_stream *stream, const imh_tq_tables *t, const imh_tq_kv_cache *cache,
@@ -992,6 +1428,9 @@ static int run_attention(imh_stream *stream, const imh_tq_tables *t, const imh_t
     if (token_count == 0 || (token_count > 1 && (fused || qk)))
         return imh::fail(IMH_EINVAL, std::string(who) + ": token_count must be 1 with the cache write or "
                                                          "QK-norm, and at least 1");
+    if (token_count > 1)
+        return run_prefill_attention(stream, t, cache, q, num_heads, gqa, L, seq_lens, attn_scale, out,
+                                     num_splits, token_count, who);
     // query rows: token t of sequence b is row b * token_count + t
     const uint32_t B = cache->batch * token_count;
     if (B > 65535) return imh::fail(IMH_EINVAL, std::string(who) + ": batch x token_count above 65535");

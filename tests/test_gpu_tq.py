@@ -304,6 +304,38 @@ def test_attention_multi_token_causal(dev, stream, tq, tables, nh, tokens, ragge
                 assert_close(got[bb, t], ref[bb], rel=5e-4, what=f"token {t} of seq {bb} (len {lt[bb]})")
 
 
+@pytest.mark.parametrize("nh,tokens,num_splits,lens", [
+    (32, 64, 0, (900, 283)),   # GQA 4: 16 token blocks, automatic splits
+    (32, 37, 1, (900, 283)),   # a partial last block, normalised in the kernel
+    (16, 20, 3, (900, 283)),   # GQA 2, merged by the combine
+    (8, 33, 1, (900, 40)),     # GQA 1 (16 tokens per block), a range shorter than the chunk
+    (32, 16, 0, None),         # one seq_len for both sequences
+])
+def test_attention_prefill_token_blocks(dev, stream, tq, tables, nh, tokens, num_splits, lens):
+    """The token-block prefill kernel (16 / GQA tokens x the GQA heads per workgroup, each
+    row with its own causal bound): every token equals the one-token oracle at its own
+    length (turboquant.metal:268), for full and partial blocks, one split and several."""
+    nkv, batch, max_seq = 8, 2, 1024
+    cache = fill_cache(dev, stream, tq, batch, nkv, max_seq, 900, seed=81 + tokens)
+    q16 = np.random.default_rng(82 + tokens).standard_normal((batch, tokens, nh, D)).astype(np.float16)
+    out = dev.empty((batch, tokens, nh, D), np.float16)
+    if lens is None:
+        seq_len, sl, lens = 500, None, np.array([500, 500], np.int32)
+    else:
+        lens = np.array(lens, np.int32)
+        seq_len, sl = 0, dev.upload(lens)
+    ops.encode_turboquant_attention(stream, tq, cache, dev.upload(q16), nh, seq_len, out, 1.0 / math.sqrt(D),
+                                    seq_lens=sl, num_splits=num_splits, token_count=tokens)
+    stream.sync()
+    got = out.read()
+    kc, vc, ks, vs, kr = read_cache(cache)
+    for t in range(tokens):
+        lt = np.maximum(lens - tokens + t + 1, 0).astype(np.int32)
+        ref = O.tq_attention(q16[:, t], tables, kc, vc, ks, vs, kr, max_seq, 1.0 / math.sqrt(D),
+                             seq_lens=lt, nthreads=8)
+        assert_close(got[:, t], ref, rel=5e-4, what=f"token {t} (lengths {lt.tolist()})")
+
+
 def test_graph_replay_after_scratch_growth(dev, tq):
     """A graph keeps addressing the stream scratch it was captured with: a larger eager op
     that grows the scratch afterwards must not free it (the replay equals the eager run,
