@@ -304,10 +304,10 @@ int run_gemm(imh_stream *s, const ActIn &in, int M, const imh_affine_int4_weight
 int run_matvec(imh_stream *s, ActIn in, uint32_t B, int nmat, int epi, int N, int K, const MatPtrs &mp,
                const char *who) {
     const bool rn = in.b != nullptr;
-    if (!rn) {
+    {
         bool used = false;
-        const int rc = launch_band_matvec(s->stream, s->dev->props.multiProcessorCount, (int)B, nmat, epi, N, K, mp,
-                                          in.a, in.awq, &used);
+        const int rc =
+            launch_band_matvec(s->stream, s->dev->props.multiProcessorCount, (int)B, nmat, epi, N, K, mp, in, &used);
         if (rc || used) return rc;
     }
     Plan p;

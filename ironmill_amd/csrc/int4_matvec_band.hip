@@ -30,6 +30,13 @@
 //    weight loads; one barrier, then the MFMAs consume the weights as they
 //    arrive; a second barrier joins the waves' partial rows (in part order:
 //    deterministic).
+//  * Residual-norm source (RN): r = a + b, every workgroup reduces the row's
+//    sum of squares itself (per-group sums through LDS, one barrier, then
+//    each thread adds them in the order of int4_matvec_kernel's row_rms) and
+//    builds the operand r * gamma (round_mode 0, rms_inv scaling the output)
+//    or f16(r * rms_inv * gamma) (round_mode 1) divided by awq; workgroup 0
+//    also writes residual_out = f16(r) and normed_out = f16(r * rms_inv *
+//    gamma).
 #include <hip/hip_runtime.h>
 #include <hip/hip_fp16.h>
 
@@ -46,24 +53,26 @@ constexpr int kRS = kGS + 8;   // halfs per operand row in LDS (16-byte pad)
 constexpr int kSZC = 2;        // scale/zero words per thread loaded ahead of the weights
 
 struct BandLds {
-    size_t img, gs, sz, red, total;
+    size_t img, gs, sz, rsq, red, total;
 };
 
-__host__ __device__ inline BandLds band_lds(int G, int BM, int NMAT, int TM, int waves) {
+__host__ __device__ inline BandLds band_lds(int G, int BM, int NMAT, int TM, int waves, bool rn) {
     BandLds L;
     L.img = 0;
     L.gs = L.img + (size_t)G * 2 * BM * kRS * 2;
     L.sz = L.gs + (size_t)G * 2 * BM * 4;
-    L.red = L.sz + (size_t)NMAT * G * TM * 8 * 4;
+    L.rsq = L.sz + (size_t)NMAT * G * TM * 8 * 4;
+    L.red = L.rsq + (rn ? (size_t)G * BM * 4 : 0);
     L.red = (L.red + 15) & ~(size_t)15;
     L.total = L.red + (size_t)waves * TM * 8 * 16;
     return L;
 }
 
 // grid NWG; block 64 * NMAT * W.
-template <int NMAT, int EPI, int TM, int NP, int BM, int XC, int PD = 1>
-__global__ void __launch_bounds__(512) int4_band_kernel(MatPtrs mp, const __half *__restrict__ x,
-                                                       const __half *__restrict__ awq, int N, int K, int B, int W) {
+template <int NMAT, int EPI, int TM, int NP, int BM, int XC, bool RN, int PD = 1>
+__global__ void __launch_bounds__(512) int4_band_kernel(MatPtrs mp, const ActIn in, int N, int K, int B, int W) {
+    const __half *__restrict__ x = in.a;
+    const __half *__restrict__ awq = in.awq;
     extern __shared__ __attribute__((aligned(16))) uint8_t lds_b[];
     const int tid = threadIdx.x, nthr = blockDim.x;
     const int lane = tid & 63, wave = tid >> 6, waves = nthr >> 6;
@@ -77,10 +86,11 @@ __global__ void __launch_bounds__(512) int4_band_kernel(MatPtrs mp, const __half
     const int nrows = re - rb;
     const int RT = TM * 8;                     // band rows held in LDS (padded)
 
-    const BandLds L = band_lds(G, BM, NMAT, TM, waves);
+    const BandLds L = band_lds(G, BM, NMAT, TM, waves, RN);
     _Float16 *img = reinterpret_cast<_Float16 *>(lds_b + L.img);
     float *gsl = reinterpret_cast<float *>(lds_b + L.gs);
     uint32_t *szs = reinterpret_cast<uint32_t *>(lds_b + L.sz);
+    float *rsq = reinterpret_cast<float *>(lds_b + L.rsq);
     float4_t *red = reinterpret_cast<float4_t *>(lds_b + L.red);
 
     // (a) activation chunks: chunk c = group c >> 4, elements (c & 15) * 8 ..
@@ -93,12 +103,19 @@ __global__ void __launch_bounds__(512) int4_band_kernel(MatPtrs mp, const __half
     const __amdgpu_buffer_rsrc_t awq_r =
         __builtin_amdgcn_make_buffer_rsrc((void *)awq, 0, awq ? K * 2 : 0, kRsrcWord3);
     u32x4_t xv[XC][BM], wv[XC];
+    u32x4_t bv[RN ? XC : 1][BM], gv[RN ? XC : 1];   // RN: b rows and gamma
 #pragma unroll
     for (int i = 0; i < XC; i++) {
         const int c = min(i * nthr + tid, nchunks - 1);
         const size_t e = (size_t)c * 8;
 #pragma unroll
         for (int b = 0; b < BM; b++) xv[i][b] = *reinterpret_cast<const u32x4_t *>(x + (size_t)min(b, B - 1) * K + e);
+        if (RN) {
+#pragma unroll
+            for (int b = 0; b < BM; b++)
+                bv[i][b] = *reinterpret_cast<const u32x4_t *>(in.b + (size_t)min(b, B - 1) * K + e);
+            gv[i] = *reinterpret_cast<const u32x4_t *>(in.gamma + e);
+        }
         wv[i] = __builtin_bit_cast(u32x4_t, __builtin_amdgcn_raw_buffer_load_b128(awq_r, (int)(e * 2), 0, 0));
     }
     // (b) scale / zero words of the band: word w of matrix m covers groups
@@ -150,7 +167,48 @@ __global__ void __launch_bounds__(512) int4_band_kernel(MatPtrs mp, const __half
     };
 #pragma unroll
     for (int i = 0; i < kSZC; i++) sz_store(min(i * nthr + tid, NMAT * szw - 1), sv[i], zv[i]);   // host: all fit
-    // (e) operand image -> LDS [g][plane][b][kRS], group sums [g][plane][b]
+    // (e) RN: r = a + b, per-group sums of r^2 -> LDS, then every thread's
+    // rms_inv per batch row (groups j, j + 8, .. summed in order, then the
+    // eight partial sums pairwise: row_rms's order)
+    float ri[BM];
+    const bool rnd = RN && in.round_mode == 1;
+    if (RN) {
+#pragma unroll
+        for (int i = 0; i < XC; i++) {
+            const int c = min(i * nthr + tid, nchunks - 1);
+            const bool live = i * nthr + tid < nchunks;
+#pragma unroll
+            for (int b = 0; b < BM; b++) {
+                const _Float16 *ah = reinterpret_cast<const _Float16 *>(&xv[i][b]);
+                const _Float16 *bh = reinterpret_cast<const _Float16 *>(&bv[i][b]);
+                float sq = 0.0f;
+#pragma unroll
+                for (int e = 0; e < 8; e++) {
+                    const float r = (float)ah[e] + (float)bh[e];
+                    sq = __builtin_fmaf(r, r, sq);
+                }
+                sq = row16_sum(sq);
+                if (live && (c & 15) == 0) rsq[(c >> 4) * BM + b] = sq;
+            }
+        }
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
+        __builtin_amdgcn_s_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+#pragma unroll
+        for (int b = 0; b < BM; b++) {
+            float t8[8];
+#pragma unroll
+            for (int j = 0; j < 8; j++) {
+                float ss = 0.0f;
+                for (int g = j; g < G; g += 8) ss += rsq[g * BM + b];
+                t8[j] = ss;
+            }
+            const float ss = ((t8[0] + t8[1]) + (t8[2] + t8[3])) + ((t8[4] + t8[5]) + (t8[6] + t8[7]));
+            ri[b] = 1.0f / __builtin_sqrtf(ss / (float)K + in.eps);
+        }
+    }
+    // (f) operand image -> LDS [g][plane][b][kRS], group sums [g][plane][b];
+    // RN: workgroup 0 writes the residual and normed rows
 #pragma unroll
     for (int i = 0; i < XC; i++) {
         const int c = min(i * nthr + tid, nchunks - 1);
@@ -161,8 +219,30 @@ __global__ void __launch_bounds__(512) int4_band_kernel(MatPtrs mp, const __half
         for (int b = 0; b < BM; b++) {
             const _Float16 *xh = reinterpret_cast<const _Float16 *>(&xv[i][b]);
             float v[8];
+            if (RN) {
+                const _Float16 *bh = reinterpret_cast<const _Float16 *>(&bv[i][b]);
+                const _Float16 *gh = reinterpret_cast<const _Float16 *>(&gv[i]);
+                half8_t res, nrm;
 #pragma unroll
-            for (int e = 0; e < 8; e++) v[e] = awq ? div_awq((float)xh[e], (float)wh[e]) : (float)xh[e];
+                for (int e = 0; e < 8; e++) {
+                    const float r = (float)xh[e] + (float)bh[e];
+                    res[e] = (_Float16)r;
+                    nrm[e] = (_Float16)(r * ri[b] * (float)gh[e]);
+                    v[e] = rnd ? (float)nrm[e] : r * (float)gh[e];
+                }
+                if (blockIdx.x == 0 && live && b < B) {
+                    const size_t off = (size_t)b * K + (size_t)c * 8;
+                    *reinterpret_cast<half8_t *>(in.residual_out + off) = res;
+                    *reinterpret_cast<half8_t *>(in.normed_out + off) = nrm;
+                }
+            } else {
+#pragma unroll
+                for (int e = 0; e < 8; e++) v[e] = (float)xh[e];
+            }
+            if (awq) {
+#pragma unroll
+                for (int e = 0; e < 8; e++) v[e] = div_awq(v[e], (float)wh[e]);
+            }
             half8_t hi, lo;
             float sh, sl;
             chunk_operands(v, hi, lo, sh, sl);
@@ -184,7 +264,7 @@ __global__ void __launch_bounds__(512) int4_band_kernel(MatPtrs mp, const __half
     __builtin_amdgcn_s_barrier();
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
 
-    // (f) MFMA.  A row of this lane: i = lane & 15 -> (ah, aplane, ab); the
+    // (g) MFMA.  A row of this lane: i = lane & 15 -> (ah, aplane, ab); the
     // lane's result rows: (h, plane) = (lane >> 5, (lane >> 4) & 1)
     const int ai = lane & 15;
     const int ah = ai >> 3, aplane = (ai >> 2) & 1, ab = ai & 3;
@@ -236,7 +316,7 @@ __global__ void __launch_bounds__(512) int4_band_kernel(MatPtrs mp, const __half
             }
         }
     }
-    // (g) rows r = lane & 7 of each tile sit at lanes r (h 0, hi), r + 16
+    // (h) rows r = lane & 7 of each tile sit at lanes r (h 0, hi), r + 16
     // (h 0, lo), r + 40 (h 1, hi), r + 56 (h 1, lo)
 #pragma unroll
     for (int t = 0; t < TM; t++) {
@@ -261,6 +341,8 @@ __global__ void __launch_bounds__(512) int4_band_kernel(MatPtrs mp, const __half
         for (int mt = 0; mt < NMAT; mt++) {
             float s = 0.0f;
             for (int p = 0; p < W; p++) s += red[((mt * W + p) * TM + t) * 8 + rl][b];
+            // round_mode 0: the row's rms_inv scales both projections, ahead of the activation
+            if (RN && !rnd) s *= b == 0 ? ri[0] : ri[BM - 1];
             sum[mt] = s;
         }
         if (EPI == EPI_SILU || EPI == EPI_GELU) {
@@ -288,41 +370,44 @@ struct BandLaunch {
     int N, K, B, W;
 };
 
-template <int NMAT, int EPI, int TM, int NP, int BM>
-void launch_xc(int xc, const BandLaunch &L, const MatPtrs &mp, const __half *x, const __half *awq) {
+template <int NMAT, int EPI, int TM, int NP, int BM, bool RN>
+void launch_xc(int xc, const BandLaunch &L, const MatPtrs &mp, const ActIn &in) {
     if (xc == 1)
-        hipLaunchKernelGGL((int4_band_kernel<NMAT, EPI, TM, NP, BM, 1>), L.grid, L.block, L.lds, L.st, mp, x, awq, L.N,
+        hipLaunchKernelGGL((int4_band_kernel<NMAT, EPI, TM, NP, BM, 1, RN>), L.grid, L.block, L.lds, L.st, mp, in, L.N,
                            L.K, L.B, L.W);
     else
-        hipLaunchKernelGGL((int4_band_kernel<NMAT, EPI, TM, NP, BM, 3>), L.grid, L.block, L.lds, L.st, mp, x, awq, L.N,
+        hipLaunchKernelGGL((int4_band_kernel<NMAT, EPI, TM, NP, BM, 3, RN>), L.grid, L.block, L.lds, L.st, mp, in, L.N,
                            L.K, L.B, L.W);
 }
 
-template <int NMAT, int EPI, int TM, int NP>
-void launch_bm(int bm, int xc, const BandLaunch &L, const MatPtrs &mp, const __half *x, const __half *awq) {
-    if (bm == 1) launch_xc<NMAT, EPI, TM, NP, 1>(xc, L, mp, x, awq);
-    else launch_xc<NMAT, EPI, TM, NP, 2>(xc, L, mp, x, awq);
+template <int NMAT, int EPI, int TM, int NP, bool RN>
+void launch_bm(int bm, int xc, const BandLaunch &L, const MatPtrs &mp, const ActIn &in) {
+    if (bm == 1) launch_xc<NMAT, EPI, TM, NP, 1, RN>(xc, L, mp, in);
+    else launch_xc<NMAT, EPI, TM, NP, 2, RN>(xc, L, mp, in);
 }
 
 // (TM, NP) instantiated: (2, 5), (3, 5) and (5, 3); the host picks the
 // smallest TM that holds the band.
-template <int NMAT, int EPI>
-void launch_shape(int tm, int bm, int xc, const BandLaunch &L, const MatPtrs &mp, const __half *x, const __half *awq) {
-    if (tm <= 2) launch_bm<NMAT, EPI, 2, 5>(bm, xc, L, mp, x, awq);
-    else if (tm <= 3) launch_bm<NMAT, EPI, 3, 5>(bm, xc, L, mp, x, awq);
-    else launch_bm<NMAT, EPI, 5, 3>(bm, xc, L, mp, x, awq);
+template <int NMAT, int EPI, bool RN>
+void launch_shape(int tm, int bm, int xc, const BandLaunch &L, const MatPtrs &mp, const ActIn &in) {
+    if (tm <= 2) launch_bm<NMAT, EPI, 2, 5, RN>(bm, xc, L, mp, in);
+    else if (tm <= 3) launch_bm<NMAT, EPI, 3, 5, RN>(bm, xc, L, mp, in);
+    else launch_bm<NMAT, EPI, 5, 3, RN>(bm, xc, L, mp, in);
 }
 
 }  // namespace
 
-// Launches the band kernel when it applies (plain x / awq source, B <= 2, no
-// row segments, an even number of groups, the shape within the instantiated
-// tiles and the LDS budget); *used reports whether it did.
+// Launches the band kernel when it applies (B <= 2, no row segments, an even
+// number of groups, the shape within the instantiated tiles and the LDS
+// budget; a residual-norm source with round_mode 0 or 1, as nmat 1 with
+// EPI_STORE or nmat 2 with an activation); *used reports whether it did.
 int launch_band_matvec(hipStream_t st, int cus, int B, int nmat, int epi, int N, int K, const MatPtrs &mp,
-                       const __half *x, const __half *awq, bool *used) {
+                       const ActIn &in, bool *used) {
     *used = false;
+    const bool rn = in.b != nullptr;
     const int G = K / kGS;
     if (B < 1 || B > 2 || mp.seg[0] != 0 || G % 2 || G < 2) return IMH_OK;
+    if (rn && (in.round_mode > 1 || (nmat == 2) != (epi != EPI_STORE))) return IMH_OK;
     for (int i = 0; i < nmat; i++)
         if ((reinterpret_cast<uintptr_t>(mp.scales[i]) | reinterpret_cast<uintptr_t>(mp.zeros[i])) & 3) return IMH_OK;
     const int P = G / 2;
@@ -341,17 +426,25 @@ int launch_band_matvec(hipStream_t st, int cus, int B, int nmat, int epi, int N,
     const int nthr = 64 * W * nmat;
     const int xc = (G * 16 + nthr - 1) / nthr;
     if (xc > 3 || nmat * rows * P > kSZC * nthr) return IMH_OK;
-    const size_t lds = band_lds(G, B, nmat, TM, W * nmat).total;
+    const size_t lds = band_lds(G, B, nmat, TM, W * nmat, rn).total;
     if (lds > 64 * 1024) return IMH_OK;
     BandLaunch L{dim3(nwg), dim3(nthr), lds, st, N, K, B, W};
-    if (nmat == 1)
-        launch_shape<1, EPI_STORE>(tm, B, xc, L, mp, x, awq);
-    else if (epi == EPI_SILU)
-        launch_shape<2, EPI_SILU>(tm, B, xc, L, mp, x, awq);
-    else if (epi == EPI_GELU)
-        launch_shape<2, EPI_GELU>(tm, B, xc, L, mp, x, awq);
-    else
-        launch_shape<2, EPI_STORE>(tm, B, xc, L, mp, x, awq);
+    if (rn) {
+        if (nmat == 1)
+            launch_shape<1, EPI_STORE, true>(tm, B, xc, L, mp, in);
+        else if (epi == EPI_SILU)
+            launch_shape<2, EPI_SILU, true>(tm, B, xc, L, mp, in);
+        else
+            launch_shape<2, EPI_GELU, true>(tm, B, xc, L, mp, in);
+    } else if (nmat == 1) {
+        launch_shape<1, EPI_STORE, false>(tm, B, xc, L, mp, in);
+    } else if (epi == EPI_SILU) {
+        launch_shape<2, EPI_SILU, false>(tm, B, xc, L, mp, in);
+    } else if (epi == EPI_GELU) {
+        launch_shape<2, EPI_GELU, false>(tm, B, xc, L, mp, in);
+    } else {
+        launch_shape<2, EPI_STORE, false>(tm, B, xc, L, mp, in);
+    }
     IMH_HIP(hipGetLastError());
     *used = true;
     return IMH_OK;

@@ -631,9 +631,10 @@ void launch_ng(const Launch &L, const MatPtrs &mp, const ActIn &in) {
 void launch_raw(int nmat, int epi, bool rn, const Launch &L, const MatPtrs &mp, const ActIn &in);
 // IMAGE-source launches with two MFMA tiles (int4_matvec_mt2.hip).
 void launch_image_mt2(int nmat, int epi, const Launch &L, const MatPtrs &mp, const ActIn &in);
-// The CU-balanced row-band kernel for plain sources at batch 1-2
-// (int4_matvec_band.hip); *used is false where it does not apply.
+// The CU-balanced row-band kernel at batch 1-2 (int4_matvec_band.hip), for
+// plain sources and residual-norm sources of round_mode 0 or 1 (in.b set);
+// *used is false where it does not apply.
 int launch_band_matvec(hipStream_t st, int cus, int B, int nmat, int epi, int N, int K, const MatPtrs &mp,
-                       const __half *x, const __half *awq, bool *used);
+                       const ActIn &in, bool *used);
 
 }  // namespace imh_int4

@@ -210,7 +210,7 @@ def test_batched_gate_up(dev, stream, batch, awq):
     assert_close(uo.read(), O.matvec_f16w(wdq_u, x16, awq16, nthreads=8), what="up", ulps=2)
 
 
-@pytest.mark.parametrize("batch,awq", [(1, False), (1, True), (3, True)])
+@pytest.mark.parametrize("batch,awq", [(1, False), (1, True), (2, True), (3, True)])
 def test_fused_residual_norm_projection(dev, stream, batch, awq):
     n, k, eps = 4096, 2560, 1e-6
     w, s = make_weight(n, k, seed=31, awq=awq)
