@@ -273,6 +273,35 @@ def bench_gemm(dev, stream, ops, m, kk, nn, prec, steps, warmup, eager=False, re
             "frac": round(tfs / GEMM_PEAK_TFS[prec], 4), "peak_TFLOP/s": GEMM_PEAK_TFS[prec]}
 
 
+def bench_valu_ab(dev, stream, ops, steps, warmup, eager=False, only=None):
+    """Design A/B of the decode matvec: the library's MFMA kernels (imh_encode_affine_projection_int4)
+    against the VALU-dot wavefront-reduction matvec (imh_diag_valu_matvec) on the same weights
+    (rotating over >= 512 MB), Qwen3-4B gate (2560 -> 9728) at batch 1, 4 and 8 and O
+    (4096 -> 2560) at batch 1; the two outputs' rel-L2 distance as a check."""
+    out = {}
+    rng = np.random.default_rng(77)
+    for n, k, batches in ((F, H, (1, 4, 8)), (H, 4096, (1,))):
+        nbytes = n * k // 2
+        reps = max(2, math.ceil(512e6 / nbytes))
+        Ws = [random_int4(dev, ops, rng, n, k) for _ in range(reps)]
+        for b in batches:
+            if only and (n, k, b) != only:
+                continue
+            x = dev.upload(make_x(b, k, 5 + b))
+            ys = [dev.empty((b, n), np.float16) for _ in range(2)]
+            for name, fn in (("mfma", ops.encode_projection), ("valu", ops.diag_valu_matvec)):
+                y = ys[0 if name == "mfma" else 1]
+                us = 1e3 * (eager_loop if eager else time_loop)(
+                    dev, stream, lambda i, fn=fn, y=y: fn(stream, x, Ws[i % reps], y, b), steps, warmup) / steps
+                gbs = (nbytes + n * (k // 128) * 4 + 2 * b * (k + n) + 2 * k) / (us * 1e-6) / 1e9
+                out[f"{name}_n{n}_k{k}_b{b}"] = {"us": round(us, 2), "GB/s": round(gbs, 1),
+                                                 "frac": round(gbs / HBM_PEAK_GBS, 4)}
+            stream.sync()
+            a, v = ys[0].read().astype(np.float64), ys[1].read().astype(np.float64)
+            out[f"rel_l2_n{n}_k{k}_b{b}"] = float(np.linalg.norm(a - v) / max(np.linalg.norm(a), 1e-30))
+    return out
+
+
 def bench_probe(dev, stream, ops, steps, warmup, sweep=True):
     """Streaming probe (imh_diag_stream_read): the batch-1 gate+up and down weight bytes read
     with no compute, rotating over >= 512 MB of buffers like the matvec measurement.  `kernel`:
@@ -453,10 +482,13 @@ def main():
                     help="with --decode-only: time 5 eager steps only (no graph capture; for kernel traces)")
     ap.add_argument("--kernel-only", action="store_true",
                     help="only the prepared fused gate+up kernel loop (same as --kernel gate_up)")
-    ap.add_argument("--kernel", choices=["gate_up", "down", "gemm", "probe"],
+    ap.add_argument("--kernel", choices=["gate_up", "down", "gemm", "probe", "valu_ab"],
                     help="one kernel alone, for rocprofv3 runs: the batch-B fused gate+up or down "
-                         "matvec, the prefill GEMM (--gemm-*), or the streaming probe; with --eager "
-                         "the launches are host launches (counter runs see only those)")
+                         "matvec, the prefill GEMM (--gemm-*), the streaming probe, or the MFMA / "
+                         "VALU-dot matvec A/B; with --eager the launches are host launches (counter "
+                         "runs see only those)")
+    ap.add_argument("--ab-case", type=int, nargs=3, metavar=("N", "K", "B"),
+                    help="with --kernel valu_ab: only this shape (counter runs)")
     ap.add_argument("--gemm-m", type=int, default=2048)
     ap.add_argument("--gemm-shape", choices=["gate", "down"], default="gate",
                     help="K=2560 N=9728 (gate) or K=9728 N=2560 (down)")
@@ -517,6 +549,13 @@ def main():
                        eager=args.eager)
         log(f"GEMM {args.gemm_precision} M={args.gemm_m} K={kk} N={nn}: {r['us']} us {r['TFLOP/s']} TFLOP/s")
         print(json.dumps({f"gemm_{args.gemm_precision}_m{args.gemm_m}_k{kk}_n{nn}": r}), flush=True)
+        return
+    if args.kernel == "valu_ab":
+        only = tuple(args.ab_case) if args.ab_case else None
+        r = bench_valu_ab(dev, stream, ops, args.steps, args.warmup, eager=args.eager, only=only)
+        for k_, v in r.items():
+            log(f"{k_}: {v}")
+        print(json.dumps({"matvec_mfma_vs_valu": r}), flush=True)
         return
     if args.kernel == "probe":
         r = bench_probe(dev, stream, ops, args.steps, args.warmup)

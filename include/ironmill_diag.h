@@ -40,6 +40,18 @@ typedef struct {
 int imh_diag_stream_read(imh_stream *stream, const void *src, uint32_t n, uint32_t k, const imh_probe_shape *shape,
                          uint32_t *sink);
 
+/* VALU-dot INT4 matvec, for a counter A/B against the MFMA decode kernels:
+ * y [batch][n] = the affine INT4 projection of x [batch][k] (the semantics of
+ * imh_encode_affine_projection_int4: x / awq, (q - z) * s per group of 128,
+ * f32 accumulation, f16 out) computed as a wavefront-reduction matvec -- 16
+ * lanes per row reading 16-byte code chunks, nibble pairs dequantized in
+ * registers into v_dot2_f32_f16 against the f16 hi and lo halves of x / awq,
+ * a DPP row sum per row, one band of rows per compute unit.  k of 2560 or
+ * 4096; batch <= 8 with batch x k x 4.125 bytes within the device's LDS per
+ * workgroup. */
+int imh_diag_valu_matvec(imh_stream *stream, const uint16_t *x, uint32_t batch, const imh_affine_int4_weight *w,
+                         uint16_t *y);
+
 #ifdef __cplusplus
 }
 #endif

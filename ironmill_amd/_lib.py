@@ -240,6 +240,7 @@ SIGNATURES = {
     "imh_encode_affine_projection_int8": (I, [P, P, U32, C.POINTER(AffineInt8Weight), P]),
     "imh_kv_positions_for": (I, [U32, U32, U32, U32, C.POINTER(KvPositions)]),
     "imh_diag_stream_read": (I, [P, P, U32, U32, C.POINTER(ProbeShape), P]),
+    "imh_diag_valu_matvec": (I, [P, P, U32, C.POINTER(AffineInt4Weight), P]),
     "imh_encode_quantize_input_q8": (I, [P, P, U32, U32, P, P]),
     "imh_encode_affine_matvec_int4xq8": (I, [P, P, P, U32, C.POINTER(AffineInt4Weight), P]),
     "imh_encode_fused_residual_norm_affine_matvec_int4": (I, [P, C.POINTER(FusedResidualNormParams)]),

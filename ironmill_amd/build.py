@@ -20,7 +20,7 @@ SOURCES = ["runtime.hip", "int4_matvec.hip", "int4_matvec_raw.hip", "int4_matvec
            "int4_gemm.hip",
            "int4_gemm_mx.hip", "int8_matvec.hip",
            "tq_kernels.hip", "fp16_attention.hip", "glue_kernels.hip", "decoder.hip",
-           "tq_tables.cpp", "diag_probe.hip"]
+           "tq_tables.cpp", "diag_probe.hip", "diag_valu_matvec.hip"]
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 # -packed-fp32-ops: hipcc must not emit packed f32 VALU ops (they have given
 # silent wrong results on these machines); the host pass ignores the feature.

@@ -109,6 +109,13 @@ def diag_stream_read(stream: Stream, src, n: int, k: int, sink, mode=PROBE_TILE,
     check(lib.imh_diag_stream_read(stream.handle, _ptr(src), n, k, C.byref(shape), _ptr(sink)))
 
 
+def diag_valu_matvec(stream: Stream, x, weight: AffineQuantizedWeight, y, token_count: int):
+    """VALU-dot INT4 matvec (no reference counterpart): the projection's semantics computed
+    as a wavefront-reduction matvec with in-register dequant, for the counter A/B against the
+    MFMA kernels.  k in {2560, 4096}, token_count <= 8."""
+    check(lib.imh_diag_valu_matvec(stream.handle, _ptr(x), token_count, C.byref(weight.c), _ptr(y)))
+
+
 def kv_positions(seq_pos: int, token_count: int, window_size: int, max_seq_len: int) -> dict:
     """The cache positions of one step (imh_kv_positions_for; attention.rs:141-163): the
     layer cache's stride (its max_seq_len), the write position, the attention base and the
