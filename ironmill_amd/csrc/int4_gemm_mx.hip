@@ -12,22 +12,27 @@
 // MI355X design (not the Metal kernel's structure):
 //  * A -- the activation -- goes through LDS; B -- the INT4 weights -- goes
 //    straight from memory into registers in the MFMA operand layout (lane =
-//    weight row + 16 x K quarter, one 16-byte load per lane per group and
-//    16-row fragment, the decode matvec's layout) and is expanded there, so a
-//    workgroup's weights never touch LDS and each is read once per workgroup.
+//    weight column + 32 x K half, two 16-byte loads per lane per group and
+//    32-column fragment) and is expanded there, so a workgroup's weights
+//    never touch LDS and each is read once per workgroup.
 //  * bf16: a code byte q placed under the bf16 exponent byte 0x43 is the bf16
 //    value 128 + q exactly (one v_perm per two codes); the MFMA gives
 //    sum a (128 + q) and the group's correction subtracts (128 + z) sum a,
 //    with sum a the row's group sum of the rounded operand (exact products,
 //    f32 sums).  fp8: q is looked up as its e4m3 encoding (exact for 0..15)
-//    and the correction subtracts z sum a.  One v_mfma_f32_16x16x128_f8f6f4
-//    covers a whole group.
+//    and the correction subtracts z sum a.  The correction is the group's
+//    first matrix-core product (the row sum split into three exact bf16
+//    pieces against -c), so the fold of a group is one multiply-add.
 //  * a prep kernel writes the operand rows (x / awq rounded, each 8-element
 //    chunk in the slot order the code unpack produces) and their group sums.
-//  * workgroup tile 64 (M) x 128 columns, four waves each owning a quarter
-//    of the columns; the
-//    next group's A (global -> registers -> other LDS buffer) and B (global ->
-//    registers) are loaded while the current group computes: one barrier per
+//  * the 32 x 32 matrix-core shapes (v_mfma_f32_32x32x16_bf16,
+//    v_mfma_scale_f32_32x32x64_f8f6f4): measured on the MI355X they sustain
+//    ~2.3 / ~4.9 PFLOP/s where the 16 x 16 bf16 shape stops at ~1.7.
+//  * workgroup tile 64 (M) x 256 columns, four waves each owning 64 x 64
+//    (2 x 2 MFMA tiles of 32 x 32); the next group's A (global -> registers
+//    -> other LDS buffer) and B (global -> registers) are loaded while the
+//    current group computes, unconditionally (the last group re-loads
+//    itself), so no wait for them sits inside the compute: one barrier per
 //    group.  K is split over workgroups when the tile grid is smaller than
 //    twice the CU count; the f32 partials are summed in split order by a
 //    second kernel (deterministic).
@@ -46,15 +51,14 @@ typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
 typedef int i32x8_t __attribute__((ext_vector_type(8)));
 typedef float float4_t __attribute__((ext_vector_type(4)));
 typedef float float2_t __attribute__((ext_vector_type(2)));
+typedef float float16_t __attribute__((ext_vector_type(16)));
 typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
 
 constexpr int kGS = 128;
 constexpr int kBM = 64;          // workgroup rows (M)
-constexpr int kThreads = 256;    // 4 waves, each owning 16 x NJ columns
-// 16-column B fragments per wave (more spill: the bf16 A fragments take 64
-// registers)
-template <int P> constexpr int frags_per_wave() { return 2; }
-template <int P> constexpr int wg_cols() { return 4 * 16 * frags_per_wave<P>(); }
+constexpr int kThreads = 256;    // 4 waves, each owning 64 rows x 64 columns
+constexpr int kWaveCols = 64;    // two 32-column B fragments per wave
+template <int P> constexpr int wg_cols() { return 4 * kWaveCols; }
 constexpr float kE4M3Max = 448.0f;
 
 enum Prec : int { PREC_BF16 = 1, PREC_FP8 = 2 };
@@ -157,6 +161,16 @@ __device__ __forceinline__ void tile_of(const TileOrder &o, int &mt, int &nt, in
 // grid (tiles_m * tiles_n * splits), block 256; tile (mt, nt, split) from
 // tile_of.  Split z covers groups [z * per, min((z + 1) * per, G)).  Without a
 // split C is stored as bf16; with one the f32 partials go to part[z][M][N].
+//
+// Operand layouts of the 32 x 32 MFMAs (lane l: n or m = l & 31, h = l >> 5):
+//   bf16 32x32x16, k step s (0..7) of a group: lane (n, h) holds the 8 codes
+//     [64 h + 8 s, +8) of column n -- dword s of the 32 code bytes
+//     [32 h, 32 h + 32) of the group row -- and A lane (m, h) the operand
+//     chunk 8 h + s of row m (8 elements in the code unpack's slot order);
+//   fp8 32x32x64, k step t (0..1): lane (n, h) the 32 codes [64 t + 32 h, +32)
+//     (code bytes [32 t + 16 h, +16)), A lane (m, h) the 32 operand bytes at
+//     64 t + 32 h of row m;
+//   D: lane l, value i: row 8 (i >> 2) + 4 h + (i & 3), column l & 31.
 template <int P>
 __global__ void __launch_bounds__(kThreads, 2) gemm_mx_kernel(
     const uint8_t *__restrict__ aop, const float *__restrict__ gsum, const uint8_t *__restrict__ wdata,
@@ -165,29 +179,28 @@ __global__ void __launch_bounds__(kThreads, 2) gemm_mx_kernel(
     constexpr int EB = P == PREC_BF16 ? 2 : 1;     // operand bytes per element
     constexpr int RB = kGS * EB + 16;              // LDS row bytes of one group (16-byte pad)
     constexpr int ACH = kBM * kGS * EB / 16 / kThreads;   // 16-byte A chunks per thread per group
-    constexpr int NJ = frags_per_wave<P>();
     __shared__ __attribute__((aligned(16))) uint8_t As[2][kBM * RB];
     __shared__ __attribute__((aligned(16))) float Gs[2][kBM];
 
     const int tid = threadIdx.x;
     const int lane = tid & 63;
     const int wave = tid >> 6;
-    const int n_l = lane & 15, kq = lane >> 4;
+    const int nl = lane & 31, h = lane >> 5;
     int mt, nt, split;
     tile_of(order, mt, nt, split);
     const int m0 = mt * kBM;
-    const int n0 = nt * wg_cols<P>() + wave * 16 * NJ;
+    const int n0 = nt * wg_cols<P>() + wave * kWaveCols;
     const int G = K / kGS;
     const int g_begin = split * per;
     const int g_end = min(g_begin + per, G);
 
-    // B rows of this lane: fragment j holds row n0 + 16 j + n_l (clamped)
-    const uint8_t *brow[NJ];
-    size_t szrow[NJ];
+    // B rows of this lane: fragment j holds column n0 + 32 j + nl (clamped)
+    const uint8_t *brow[2];
+    size_t szrow[2];
 #pragma unroll
-    for (int j = 0; j < NJ; j++) {
-        const int n = min(n0 + 16 * j + n_l, N - 1);
-        brow[j] = wdata + (size_t)n * (K / 2) + kq * 16;
+    for (int j = 0; j < 2; j++) {
+        const int n = min(n0 + 32 * j + nl, N - 1);
+        brow[j] = wdata + (size_t)n * (K / 2) + (P == PREC_BF16 ? 32 * h : 16 * h);
         szrow[j] = (size_t)n * G;
     }
     // A staging: chunk c = i * 256 + tid of the group's 64 x (128 * EB) bytes
@@ -210,96 +223,135 @@ __global__ void __launch_bounds__(kThreads, 2) gemm_mx_kernel(
         }
         if (tid < kBM) Gs[buf][tid] = gs;
     };
-    // B codes, scales and zero-points of group g; the scale and zero stay
-    // apart until used, so nothing waits for these loads before the next group
+    // B codes (32 bytes per fragment and lane), scales and zero-points of
+    // group g; the scale and zero stay apart until used
     struct BRegs {
-        u32x4_t w[NJ];
-        uint16_t s[NJ], z[NJ];
+        u32x4_t w[2][2];
+        uint16_t s[2], z[2];
     };
     auto load_b = [&](int g, BRegs &b) __attribute__((always_inline)) {
 #pragma unroll
-        for (int j = 0; j < NJ; j++) {
-            b.w[j] = *reinterpret_cast<const u32x4_t *>(brow[j] + (size_t)g * 64);
+        for (int j = 0; j < 2; j++) {
+            const uint8_t *p = brow[j] + (size_t)g * 64;
+            b.w[j][0] = *reinterpret_cast<const u32x4_t *>(p);
+            b.w[j][1] = *reinterpret_cast<const u32x4_t *>(p + (P == PREC_BF16 ? 16 : 32));
             b.s[j] = reinterpret_cast<const uint16_t *>(scales)[szrow[j] + g];
             b.z[j] = reinterpret_cast<const uint16_t *>(zeros)[szrow[j] + g];
         }
     };
 
-    float4_t acc[4][NJ];
+    float16_t acc[2][2];
 #pragma unroll
-    for (int i = 0; i < 4; i++)
+    for (int mi = 0; mi < 2; mi++)
 #pragma unroll
-        for (int j = 0; j < NJ; j++) acc[i][j] = (float4_t){0.0f, 0.0f, 0.0f, 0.0f};
+        for (int j = 0; j < 2; j++)
+#pragma unroll
+            for (int i = 0; i < 16; i++) acc[mi][j][i] = 0.0f;
 
-    // One group: B fragment j expanded from its 16 code bytes, A fragment i
-    // (rows 16 i .. 16 i + 15) from LDS, the group's sums folded into acc with
-    // the scale and zero-point of column n_l of fragment j.
+    // One group: the MFMAs of the four 32 x 32 tiles over the group's k
+    // steps, then each tile's group partial folded into acc with the scale
+    // and zero-point of the lane's column and the group sums of its rows.
     auto compute = [&](int buf, const BRegs &b) __attribute__((always_inline)) {
-        // D rows of this lane: 4 kq + r of each fragment; their group sums
-        float4_t rs[4];
+        // The group's zero-point correction -c * rowsum (c = 128 + z for the
+        // bf16 codes, which carry 128; z for fp8) starts each tile's
+        // accumulator, on the matrix core: A lane (m, 0) holds the row sum
+        // split into three bf16 pieces (hi + mid + lo == rowsum exactly), B
+        // lane (n, 0) -c three times (exact in bf16), all other k slots zero
+        // -- so the fold is one multiply-add per output.
+        bf16x8_t ca[2], cb[2];
+        {
+            const __bf16 z0 = (__bf16)0.0f;
 #pragma unroll
-        for (int i = 0; i < 4; i++) rs[i] = *reinterpret_cast<const float4_t *>(&Gs[buf][16 * i + 4 * kq]);
+            for (int mi = 0; mi < 2; mi++) {
+                const float rs = Gs[buf][32 * mi + nl];
+                const __bf16 r0 = (__bf16)rs;
+                const float e1 = rs - (float)r0;
+                const __bf16 r1 = (__bf16)e1;
+                const __bf16 r2 = (__bf16)(e1 - (float)r1);
+                ca[mi] = h == 0 ? (bf16x8_t){r0, r1, r2, z0, z0, z0, z0, z0} : (bf16x8_t){z0, z0, z0, z0, z0, z0, z0, z0};
+            }
+#pragma unroll
+            for (int j = 0; j < 2; j++) {
+                const __bf16 c = (__bf16)((P == PREC_BF16 ? -128.0f : 0.0f) - (float)__builtin_bit_cast(_Float16, b.z[j]));
+                cb[j] = h == 0 ? (bf16x8_t){c, c, c, z0, z0, z0, z0, z0} : (bf16x8_t){z0, z0, z0, z0, z0, z0, z0, z0};
+            }
+        }
+        const float16_t zero16 = {};
         if (P == PREC_BF16) {
+            float16_t gg[2][2];
 #pragma unroll
-            for (int j = 0; j < NJ; j++) {
-                bf16x8_t bf[4];
+            for (int mi = 0; mi < 2; mi++)
 #pragma unroll
-                for (int ks = 0; ks < 4; ks++) {
-                    const uint32_t w = b.w[j][ks];
+                for (int j = 0; j < 2; j++)
+                    gg[mi][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(ca[mi], cb[j], zero16, 0, 0, 0);
+#pragma unroll
+            for (int st = 0; st < 8; st++) {
+                bf16x8_t af[2], bf[2];
+#pragma unroll
+                for (int mi = 0; mi < 2; mi++)
+                    af[mi] = *reinterpret_cast<const bf16x8_t *>(&As[buf][(32 * mi + nl) * RB + (8 * h + st) * 16]);
+#pragma unroll
+                for (int j = 0; j < 2; j++) {
+                    // 8 codes -> bf16 128 + q in slot order {0, 2, 4, 6, 1, 3, 5, 7}
+                    const uint32_t w = b.w[j][st >> 2][st & 3];
                     const uint32_t lo = w & 0x0F0F0F0Fu, hi = (w >> 4) & 0x0F0F0F0Fu;
                     const u32x4_t o = {__builtin_amdgcn_perm(lo, 0x43434343u, 0x00050004u),
                                        __builtin_amdgcn_perm(lo, 0x43434343u, 0x00070006u),
                                        __builtin_amdgcn_perm(hi, 0x43434343u, 0x00050004u),
                                        __builtin_amdgcn_perm(hi, 0x43434343u, 0x00070006u)};
-                    bf[ks] = __builtin_bit_cast(bf16x8_t, o);
+                    bf[j] = __builtin_bit_cast(bf16x8_t, o);
                 }
-                const float s = (float)__builtin_bit_cast(_Float16, b.s[j]);
-                const float cz = 128.0f + (float)__builtin_bit_cast(_Float16, b.z[j]);
 #pragma unroll
-                for (int i = 0; i < 4; i++) {
-                    // 8 elements of row 16 i + n_l at k = 32 kq + 8 ks (re-read per fragment j:
-                    // holding all of them would cost 64 registers and occupancy)
-                    bf16x8_t af[4];
+                for (int mi = 0; mi < 2; mi++)
 #pragma unroll
-                    for (int ks = 0; ks < 4; ks++)
-                        af[ks] = *reinterpret_cast<const bf16x8_t *>(&As[buf][(16 * i + n_l) * RB + (32 * kq + 8 * ks) * 2]);
-                    float4_t g = {0.0f, 0.0f, 0.0f, 0.0f};
-#pragma unroll
-                    for (int ks = 0; ks < 4; ks++) g = __builtin_amdgcn_mfma_f32_16x16x32_bf16(af[ks], bf[ks], g, 0, 0, 0);
-#pragma unroll
-                    for (int r = 0; r < 4; r++) acc[i][j][r] = __builtin_fmaf(s, __builtin_fmaf(-cz, rs[i][r], g[r]), acc[i][j][r]);
-                }
+                    for (int j = 0; j < 2; j++)
+                        gg[mi][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af[mi], bf[j], gg[mi][j], 0, 0, 0);
             }
+#pragma unroll
+            for (int mi = 0; mi < 2; mi++)
+#pragma unroll
+                for (int j = 0; j < 2; j++) {
+                    const float sj = (float)__builtin_bit_cast(_Float16, b.s[j]);
+#pragma unroll
+                    for (int i = 0; i < 16; i++) acc[mi][j][i] = __builtin_fmaf(sj, gg[mi][j][i], acc[mi][j][i]);
+                }
         } else {
-            i32x8_t af[4];   // [i]: 32 e4m3 bytes of row 16 i + n_l at k = 32 kq ..
+            // both k steps' A fragments, then per column fragment its B
+            // fragments and the two tiles' MFMAs: one tile's partial live at a time
+            i32x8_t af[2][2];
 #pragma unroll
-            for (int i = 0; i < 4; i++) {
-                const uint8_t *p = &As[buf][(16 * i + n_l) * RB + 32 * kq];
-                const u32x4_t a0 = *reinterpret_cast<const u32x4_t *>(p);
-                const u32x4_t a1 = *reinterpret_cast<const u32x4_t *>(p + 16);
-                af[i] = (i32x8_t){(int)a0[0], (int)a0[1], (int)a0[2], (int)a0[3],
-                                  (int)a1[0], (int)a1[1], (int)a1[2], (int)a1[3]};
-            }
+            for (int t = 0; t < 2; t++)
 #pragma unroll
-            for (int j = 0; j < NJ; j++) {
-                // code dword ks = codes 8 ks .. 8 ks + 7 -> e4m3 of the even codes, then the odd
-                i32x8_t bf;
-#pragma unroll
-                for (int ks = 0; ks < 4; ks++) {
-                    const uint32_t w = b.w[j][ks];
-                    bf[2 * ks] = (int)e4m3_of_codes(w & 0x0F0F0F0Fu);
-                    bf[2 * ks + 1] = (int)e4m3_of_codes((w >> 4) & 0x0F0F0F0Fu);
+                for (int mi = 0; mi < 2; mi++) {
+                    const uint8_t *p = &As[buf][(32 * mi + nl) * RB + 64 * t + 32 * h];
+                    const u32x4_t a0 = *reinterpret_cast<const u32x4_t *>(p);
+                    const u32x4_t a1 = *reinterpret_cast<const u32x4_t *>(p + 16);
+                    af[mi][t] = (i32x8_t){(int)a0[0], (int)a0[1], (int)a0[2], (int)a0[3],
+                                          (int)a1[0], (int)a1[1], (int)a1[2], (int)a1[3]};
                 }
-                const float s = (float)__builtin_bit_cast(_Float16, b.s[j]);
-                const float z = (float)__builtin_bit_cast(_Float16, b.z[j]);
 #pragma unroll
-                for (int i = 0; i < 4; i++) {
-                    const float4_t zero = {0.0f, 0.0f, 0.0f, 0.0f};
-                    // formats 0 / 0: e4m3 x e4m3; scale exponents 127: x1
-                    const float4_t g = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(af[i], bf, zero, 0, 0, 0,
-                                                                                         0x7F7F7F7F, 0, 0x7F7F7F7F);
+            for (int j = 0; j < 2; j++) {
+                i32x8_t bf[2];
 #pragma unroll
-                    for (int r = 0; r < 4; r++) acc[i][j][r] = __builtin_fmaf(s, __builtin_fmaf(-z, rs[i][r], g[r]), acc[i][j][r]);
+                for (int t = 0; t < 2; t++)
+                    // code dword d = codes 8 d .. 8 d + 7 -> e4m3 of the even codes, then the odd
+#pragma unroll
+                    for (int d = 0; d < 4; d++) {
+                        const uint32_t w = b.w[j][t][d];
+                        bf[t][2 * d] = (int)e4m3_of_codes(w & 0x0F0F0F0Fu);
+                        bf[t][2 * d + 1] = (int)e4m3_of_codes((w >> 4) & 0x0F0F0F0Fu);
+                    }
+                const float sj = (float)__builtin_bit_cast(_Float16, b.s[j]);
+#pragma unroll
+                for (int mi = 0; mi < 2; mi++) {
+                    float16_t g = __builtin_amdgcn_mfma_f32_32x32x16_bf16(ca[mi], cb[j], zero16, 0, 0, 0);
+#pragma unroll
+                    for (int t = 0; t < 2; t++)
+                        // formats 0 / 0: e4m3 x e4m3; scale exponents 127: x1
+                        g = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(af[mi][t], bf[t], g, 0, 0, 0, 0x7F7F7F7F, 0,
+                                                                            0x7F7F7F7F);
+#pragma unroll
+                    for (int i = 0; i < 16; i++) acc[mi][j][i] = __builtin_fmaf(sj, g[i], acc[mi][j][i]);
                 }
             }
         }
@@ -308,7 +360,9 @@ __global__ void __launch_bounds__(kThreads, 2) gemm_mx_kernel(
     // Ping-pong over two B register sets (no copies between iterations): a
     // group computes from LDS buffer buf and set `cur` while the next group's
     // A (registers, stored to the other buffer after the MFMAs) and B (the
-    // other set) are in flight.
+    // other set) are in flight.  The prefetch is unconditional -- the last
+    // group loads itself again -- so the compiler's wait for the current
+    // set never has to cover the prefetch.
     u32x4_t ar[ACH];
     BRegs b0, b1;
     float gsv = 0.0f;
@@ -319,13 +373,11 @@ __global__ void __launch_bounds__(kThreads, 2) gemm_mx_kernel(
         __syncthreads();
     }
     auto step = [&](int g, int buf, const BRegs &cur, BRegs &nxt) __attribute__((always_inline)) {
-        const bool more = g + 1 < g_end;
-        if (more) {
-            load_a(g + 1, ar, gsv);
-            load_b(g + 1, nxt);
-        }
+        const int gn = min(g + 1, g_end - 1);
+        load_a(gn, ar, gsv);
+        load_b(gn, nxt);
         compute(buf, cur);
-        if (more) store_a(buf ^ 1, ar, gsv);
+        store_a(buf ^ 1, ar, gsv);
         __syncthreads();
     };
     for (int g = g_begin; g < g_end; g += 2) {
@@ -333,19 +385,19 @@ __global__ void __launch_bounds__(kThreads, 2) gemm_mx_kernel(
         if (g + 1 < g_end) step(g + 1, 1, b1, b0);
     }
 
-    // D of fragment (i, j): lane holds rows 16 i + 4 kq + r, column 16 j + n_l
+    // D of tile (mi, j): lane holds rows 32 mi + 8 (i >> 2) + 4 h + (i & 3), column 32 j + nl
 #pragma unroll
-    for (int j = 0; j < NJ; j++) {
-        const int n = n0 + 16 * j + n_l;
+    for (int j = 0; j < 2; j++) {
+        const int n = n0 + 32 * j + nl;
         if (n >= N) continue;
 #pragma unroll
-        for (int i = 0; i < 4; i++)
+        for (int mi = 0; mi < 2; mi++)
 #pragma unroll
-            for (int r = 0; r < 4; r++) {
-                const int m = m0 + 16 * i + 4 * kq + r;
+            for (int i = 0; i < 16; i++) {
+                const int m = m0 + 32 * mi + 8 * (i >> 2) + 4 * h + (i & 3);
                 if (m >= M) continue;
-                if (part) part[((size_t)split * M + m) * N + n] = acc[i][j][r];
-                else out[(size_t)m * N + n] = (__bf16)acc[i][j][r];
+                if (part) part[((size_t)split * M + m) * N + n] = acc[mi][j][i];
+                else out[(size_t)m * N + n] = (__bf16)acc[mi][j][i];
             }
     }
 }
