@@ -44,14 +44,11 @@ struct imh_buffer {
 // Per-stream scratch memory, grown on demand by the host code of an op.
 // Slot 0: INT4 activation operand images, the query operand planes of the
 // TurboQuant prefill attention; slot 1: attention split partials,
-// the gate output of a prefill gate/up op; slot 2: GEMM split-K partials;
-// slot 3: arrival counters of split reductions (zeroed when allocated, left at
-// zero by every kernel that uses them).
+// the gate output of a prefill gate/up op; slot 2: GEMM split-K partials.
 // A graph captured on the stream records the slots' addresses, so a slot that
 // grows later keeps its old block alive (`retired`) until the stream is freed:
 // a replay never touches freed memory.
-constexpr int kScratchSlots = 4;
-constexpr int kCounterSlot = 3;
+constexpr int kScratchSlots = 3;
 struct imh_stream {
     imh_device *dev;
     hipStream_t stream;

@@ -46,16 +46,6 @@ int stream_scratch(imh_stream *s, int slot, size_t bytes, void **out) {
         if (want < 2 * s->scratch_bytes[slot]) want = 2 * s->scratch_bytes[slot];
         void *fresh = nullptr;
         IMH_HIP(hipMalloc(&fresh, want));
-        // arrival counters start at zero; kernels leave them at zero.  The
-        // memset is synchronous, so it is complete before any kernel on the
-        // (non-blocking) stream can use the block.
-        if (slot == kCounterSlot) {
-            hipError_t e = hipMemset(fresh, 0, want);
-            if (e != hipSuccess) {
-                (void)hipFree(fresh);
-                return hip_fail(e, "hipMemset");
-            }
-        }
         // the old block may be addressed by a captured graph: keep it until
         // the stream is freed (never free memory a replay could touch)
         if (s->scratch[slot]) {

@@ -21,9 +21,10 @@
 //     index, each position twice: against the f16 hi and lo halves of its
 //     codebook value) from V codes transposed in registers, with the weights
 //     (times the V scale) as f16.
-// Waves combine through LDS; the last workgroup of a group to finish combines
-// the splits (log-sum-exp, fused_sdpa_reduce, flash_decode.metal:163-215) and
-// rotates the result back.
+// Waves combine through LDS; with one split the workgroup normalises and
+// rotates the result back, with several each publishes its split's partial
+// (o, max, sum) and a second kernel merges the splits (log-sum-exp,
+// fused_sdpa_reduce, flash_decode.metal:163-215) and rotates back.
 #include <hip/hip_runtime.h>
 #include <hip/hip_fp16.h>
 
@@ -46,7 +47,7 @@ constexpr int kD = 128;          // head_dim the kernels are built for
 constexpr int kChunk = 16;       // positions per MFMA block
 constexpr int kWaves = 4;        // waves per attention workgroup
 constexpr int kSplitQuantum = kChunk * kWaves;
-constexpr int kMaxSplits = 512;     // the combining workgroup stages every split's (max, sum) in LDS
+constexpr int kMaxSplits = 512;     // the combine kernel stages every split's weight in LDS
 constexpr int kAutoSplitLen = 256;  // shortest split the automatic split count makes
 
 // Strides 1..32 of the unnormalised fast Walsh-Hadamard transform of a
@@ -276,8 +277,8 @@ struct QkRope {
 // RoPE when k_norm is set, with qr's tables) and V as the cache write does,
 // stores the codes at row L - 1 (L = the sequence's length with the token),
 // and publishes that one position as its split's partial; the other splits
-// cover [0, L - 1).  Its work overlaps theirs, and the last-arriving combine
-// merges it like any split.
+// cover [0, L - 1).  Its work overlaps theirs, and the combine kernel merges
+// it like any split.
 struct TqFuse {
     const __half *k_new, *v_new;   // [batch][nkv][kD]
     uint8_t *kcodes, *vcodes;      // the cache, writable
@@ -396,7 +397,7 @@ __global__ void __launch_bounds__(64 * kWaves) __attribute__((amdgpu_waves_per_e
     const uint8_t *__restrict__ kcodes, const uint8_t *__restrict__ vcodes,
     const float *__restrict__ kscales, const float *__restrict__ vscales,
     const float *__restrict__ krnorm, int split_len, float *__restrict__ part_o,
-    float *__restrict__ part_m, float *__restrict__ part_l, int *__restrict__ counters,
+    float *__restrict__ part_m, float *__restrict__ part_l,
     __half *__restrict__ out, const QkRope qr, const TqFuse fz) {
     __shared__ float qs[GQA][2][kD];
     __shared__ float wtab[2][256];     // token writer: sorted boundaries
@@ -407,10 +408,7 @@ __global__ void __launch_bounds__(64 * kWaves) __attribute__((amdgpu_waves_per_e
     __shared__ float om[kWaves][GQA][kD];
     __shared__ float mm[kWaves][GQA];
     __shared__ float ll[kWaves][GQA];
-    __shared__ int is_last;
-    __shared__ float tail_f[GQA][kMaxSplits];   // exp(m_s - M) per head and split
-    __shared__ float tail_l[GQA];
-    __shared__ float tail_o[8][kD];              // split-subset sums, [part * GQA + head]
+    __shared__ float wres[2][kD];      // token writer: K residual, then its QJL projection
 
     const int tid = threadIdx.x;
     const int lane = tid & 63;
@@ -576,8 +574,8 @@ __global__ void __launch_bounds__(64 * kWaves) __attribute__((amdgpu_waves_per_e
             tc = tq_quantize_vec(f0, f1, wl, sg0, sg1, wtab[wave], wpm[wave], fz.n_search[wave],
                                  wave == 0 ? kcb : nullptr);
             if (wave == 0) {
-                tail_o[0][wl] = tc.r0;
-                tail_o[0][wl + 64] = tc.r1;
+                wres[0][wl] = tc.r0;
+                wres[0][wl + 64] = tc.r1;
             }
         }
         __syncthreads();
@@ -589,23 +587,23 @@ __global__ void __launch_bounds__(64 * kWaves) __attribute__((amdgpu_waves_per_e
         for (int blk = 0; blk < 8; blk++) {
             if (kr == blk) {
                 float4 a4 = blk == 0 ? make_float4(0.0f, 0.0f, 0.0f, 0.0f)
-                                     : reinterpret_cast<const float4 *>(tail_o[1])[dq];
+                                     : reinterpret_cast<const float4 *>(wres[1])[dq];
 #pragma unroll
                 for (int i = 0; i < 16; i++) {
-                    const float rk = tail_o[0][16 * blk + i];
+                    const float rk = wres[0][16 * blk + i];
                     a4.x = __builtin_fmaf(sw[i].x, rk, a4.x);
                     a4.y = __builtin_fmaf(sw[i].y, rk, a4.y);
                     a4.z = __builtin_fmaf(sw[i].z, rk, a4.z);
                     a4.w = __builtin_fmaf(sw[i].w, rk, a4.w);
                 }
-                reinterpret_cast<float4 *>(tail_o[1])[dq] = a4;
+                reinterpret_cast<float4 *>(wres[1])[dq] = a4;
             }
             __syncthreads();
         }
         const size_t slot = head_base + (size_t)(has ? row : 0);
         if (wave == 0 && has) {
-            const uint32_t c0 = tc.c0 | (tail_o[1][wl] >= 0.0f ? 0x80u : 0u);
-            const uint32_t c1 = tc.c1 | (tail_o[1][wl + 64] >= 0.0f ? 0x80u : 0u);
+            const uint32_t c0 = tc.c0 | (wres[1][wl] >= 0.0f ? 0x80u : 0u);
+            const uint32_t c1 = tc.c1 | (wres[1][wl + 64] >= 0.0f ? 0x80u : 0u);
             fz.kcodes[slot * kD + wl] = (uint8_t)c0;
             fz.kcodes[slot * kD + wl + 64] = (uint8_t)c1;
             if (wl == 0) {
@@ -756,107 +754,16 @@ __global__ void __launch_bounds__(64 * kWaves) __attribute__((amdgpu_waves_per_e
         if (S == 1) {
             qs[hh][0][d] = (ov / fmaxf(lv, 1e-10f)) * signs[d];
         } else {
-            // agent-scope stores write through to memory, so the workgroup that
-            // combines the splits sees them from any XCD without flushing L2
+            // the split's partial; tq_split_combine_kernel merges the splits
             const size_t pidx = ((size_t)z * nh + kvh * GQA + hh) * S + split;
-            __hip_atomic_store(&part_o[pidx * kD + d], ov, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            part_o[pidx * kD + d] = ov;
             if (d == 0) {
-                __hip_atomic_store(&part_m[pidx], M, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-                __hip_atomic_store(&part_l[pidx], lv, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                part_m[pidx] = M;
+                part_l[pidx] = lv;
             }
         }
     }
-    if (S > 1) {
-        // the last of the group's S workgroups to arrive combines every split
-        // (log-sum-exp, fused_sdpa_reduce semantics); nobody waits, so the
-        // grid needs no co-residency.  Each thread's partial stores complete
-        // before the arrival is counted; the counter is left at zero.
-        __builtin_amdgcn_s_waitcnt(0);
-        __syncthreads();
-        if (tid == 0)
-            is_last = __hip_atomic_fetch_add(&counters[z * nkv + kvh], 1, __ATOMIC_RELAXED,
-                                             __HIP_MEMORY_SCOPE_AGENT) == S - 1;
-        __syncthreads();
-        if (!is_last) return;
-        // one invalidation of this XCD's caches, then ordinary loads, issued
-        // together: each thread's first batch of partial outputs (o[h][4q..4q+3]
-        // of its split subset: 256 threads = GQA heads x 32 dim quads x 8 / GQA
-        // subsets) and, per head (one wave), the split maxima and sums
-        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
-        const size_t gbase = ((size_t)z * nh + kvh * GQA) * S;   // head hh at gbase + hh * S
-        constexpr int kParts = 8 / GQA;
-        constexpr int kBatch = 16;
-        const int quad = tid & 31, hh = (tid >> 5) % GQA, part = (tid >> 5) / GQA;
-        const float4 *po4 = reinterpret_cast<const float4 *>(part_o + (gbase + (size_t)hh * S) * kD) + quad;
-        float4 ov[kBatch];
-#pragma unroll
-        for (int i = 0; i < kBatch; i++) {
-            const int sp = part + i * kParts;
-            ov[i] = sp < S ? po4[(size_t)sp * (kD / 4)] : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
-        }
-        // per head: M = max over splits, f_s = exp(m_s - M), l = sum f_s l_s
-        // (lanes stride the splits, then DPP/shuffle reductions)
-        if (wave < GQA) {
-            constexpr int kPer = kMaxSplits / 64;
-            float mv[kPer], lv[kPer];
-            const float *pm = part_m + gbase + (size_t)wave * S;
-            const float *pl = part_l + gbase + (size_t)wave * S;
-#pragma unroll
-            for (int i = 0; i < kPer; i++) {
-                const int sp = lane + 64 * i;
-                mv[i] = sp < S ? pm[sp] : -INFINITY;
-                lv[i] = sp < S ? pl[sp] : 0.0f;
-            }
-            float mx = -INFINITY;
-#pragma unroll
-            for (int i = 0; i < kPer; i++) mx = fmaxf(mx, mv[i]);
-            mx = fmaxf(mx, __shfl_xor(mx, 32));
-            mx = fmaxf(mx, __shfl_xor(mx, 16));
-            mx = imh_dpp::row16_max(mx);
-            float lsum = 0.0f;
-#pragma unroll
-            for (int i = 0; i < kPer; i++) {
-                const int sp = lane + 64 * i;
-                const float f = (mx == -INFINITY || mv[i] == -INFINITY) ? 0.0f : __expf(mv[i] - mx);
-                if (sp < S) tail_f[wave][sp] = f;
-                lsum = __builtin_fmaf(f, lv[i], lsum);
-            }
-            lsum = imh_dpp::row16_sum(lsum);
-            lsum += __shfl_xor(lsum, 16);
-            lsum += __shfl_xor(lsum, 32);
-            if (lane == 0) tail_l[wave] = lsum;
-        }
-        __syncthreads();
-        float4 acc4 = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
-#pragma unroll
-        for (int i = 0; i < kBatch; i++) {
-            const int sp = part + i * kParts;
-            const float f = sp < S ? tail_f[hh][sp] : 0.0f;
-            acc4.x = __builtin_fmaf(ov[i].x, f, acc4.x);
-            acc4.y = __builtin_fmaf(ov[i].y, f, acc4.y);
-            acc4.z = __builtin_fmaf(ov[i].z, f, acc4.z);
-            acc4.w = __builtin_fmaf(ov[i].w, f, acc4.w);
-        }
-        // more splits than one batch: the rest, 16 loads in flight per thread
-#pragma unroll 16
-        for (int sp = part + kBatch * kParts; sp < S; sp += kParts) {
-            const float4 v = po4[(size_t)sp * (kD / 4)];
-            const float f = tail_f[hh][sp];
-            acc4.x = __builtin_fmaf(v.x, f, acc4.x);
-            acc4.y = __builtin_fmaf(v.y, f, acc4.y);
-            acc4.z = __builtin_fmaf(v.z, f, acc4.z);
-            acc4.w = __builtin_fmaf(v.w, f, acc4.w);
-        }
-        reinterpret_cast<float4 *>(&tail_o[part * GQA + hh][0])[quad] = acc4;
-        __syncthreads();
-        for (int e = tid; e < GQA * kD; e += 64 * kWaves) {
-            const int h2 = e / kD, d = e % kD;
-            float ov = 0.0f;
-            for (int pp = 0; pp < kParts; pp++) ov += tail_o[pp * GQA + h2][d];
-            qs[h2][0][d] = (ov / fmaxf(tail_l[h2], 1e-10f)) * signs[d];
-        }
-        if (tid == 0) __hip_atomic_store(&counters[z * nkv + kvh], 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    }
+    if (S > 1) return;   // uniform: no workgroup barrier follows for these
     __syncthreads();
     // rotate back: o = D.H.D/sqrt(d) o_rot, wave hh on head hh in registers
     // (lane id from mbcnt, so the prologue's shuffle addresses are not held
@@ -1173,8 +1080,11 @@ __global__ void __launch_bounds__(64 * kWaves) __attribute__((amdgpu_waves_per_e
 }
 
 // grid ceil(rows / 4), block 256: wave w merges the S split partials of row
-// 4 blockIdx.x + w ([row][S] maxima in log2 units and sums, [row][S][kD]
-// outputs) and rotates the result back into out[row].
+// 4 blockIdx.x + w ([row][S] maxima -- in log2 units for the prefill kernel,
+// natural for the decode kernel -- and sums, [row][S][kD] outputs) and
+// rotates the result back into out[row].  Split s weighs exp(m_s - M); the
+// outputs are summed in split order, loads several splits ahead.
+template <bool LOG2>
 __global__ void __launch_bounds__(256) tq_split_combine_kernel(const float *__restrict__ part_o,
                                                                const float *__restrict__ part_m,
                                                                const float *__restrict__ part_l, int rows, int S,
@@ -1193,7 +1103,8 @@ __global__ void __launch_bounds__(256) tq_split_combine_kernel(const float *__re
     float lsum = 0.0f;
     for (int sp = lane; sp < S; sp += 64) {
         const float m = pm[sp];
-        const float f = (mx == -INFINITY || m == -INFINITY) ? 0.0f : __builtin_amdgcn_exp2f(m - mx);
+        const float f = (mx == -INFINITY || m == -INFINITY) ? 0.0f
+                                                            : (LOG2 ? __builtin_amdgcn_exp2f(m - mx) : __expf(m - mx));
         fs[wave][sp] = f;
         lsum = __builtin_fmaf(f, pl[sp], lsum);
     }
@@ -1203,6 +1114,7 @@ __global__ void __launch_bounds__(256) tq_split_combine_kernel(const float *__re
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
     const float *po = part_o + (size_t)row * S * kD;
     float o0 = 0.0f, o1 = 0.0f;
+#pragma unroll 8
     for (int sp = 0; sp < S; sp++) {
         const float f = fs[wave][sp];
         o0 = __builtin_fmaf(po[(size_t)sp * kD + lane], f, o0);
@@ -1296,15 +1208,14 @@ int imh_encode_turboquant_cache_write_kv(imh_stream *stream, const imh_tq_tables
 
 // ---------------------------------------------------------------------------
 // Fixed scratch of imh_encode_turboquant_attention_noalloc: split partials
-// (o, max, sum per query row, head and split) then the groups' arrival
-// counters, in one device array per GPU, held until the process ends.  Host
+// (o, max, sum per query row, head and split), in one device array per GPU,
+// held until the process ends.  Host
 // code never passes the array's name to a kernel (on the host it is only a
 // stand-in); it uses the address hipGetSymbolAddress returns for the current
 // device, looked up once per device when the device is opened.
 // ---------------------------------------------------------------------------
 constexpr size_t kNoAllocPartBytes = size_t(4) << 20;   // partials
-constexpr size_t kNoAllocCounters = 4096;               // batch x kv heads
-static __device__ __align__(256) uint8_t scratch[kNoAllocPartBytes + kNoAllocCounters * 4];
+static __device__ __align__(256) uint8_t scratch[kNoAllocPartBytes];
 
 constexpr int kMaxDevices = 64;
 static void *g_scratch_ptr[kMaxDevices];
@@ -1387,7 +1298,7 @@ static int run_prefill_attention(imh_stream *stream, const imh_tq_tables *t, con
 #undef IMH_TQ_PREFILL
     IMH_HIP(hipGetLastError());
     if (S > 1) {
-        hipLaunchKernelGGL(tq_split_combine_kernel, dim3(qblocks), dim3(256), 0, stream->stream, po, pm, pls,
+        hipLaunchKernelGGL(tq_split_combine_kernel<true>, dim3(qblocks), dim3(256), 0, stream->stream, po, pm, pls,
                            (int)rows, (int)S, t->signs, reinterpret_cast<__half *>(out));
         IMH_HIP(hipGetLastError());
     }
@@ -1447,38 +1358,28 @@ static int run_attention(imh_stream *stream, const imh_tq_tables *t, const imh_t
     // <= kMaxSplits, with the token writer's split
     const uint32_t S = std::max<uint32_t>(1, (L + split_len - 1) / split_len) + (fused ? 1 : 0);
 
-    // scratch: split partials and the groups' arrival counters (none for one split)
+    // scratch: split partials (none for one split); every workgroup of the
+    // attention writes its own, so the fixed array's leftover contents never
+    // reach the combine
     const size_t nparts = (size_t)B * num_heads * S;
     float *po = nullptr, *pm = nullptr, *pl = nullptr;
-    int *ctr = nullptr;
     if (S > 1) {
-        void *scr = nullptr, *cs = nullptr;
+        void *scr = nullptr;
         const size_t part_bytes = nparts * kD * 4 + nparts * 8 + 512;
-        const size_t ctr_count = (size_t)B * nkv;
         if (fixed_scratch) {
-            if (part_bytes > kNoAllocPartBytes || ctr_count > kNoAllocCounters)
+            if (part_bytes > kNoAllocPartBytes)
                 return imh::fail(IMH_EINVAL,
                                  std::string(who) + ": needs " + std::to_string(part_bytes) + " bytes of split "
-                                 "partials and " + std::to_string(ctr_count) + " counters; the fixed scratch holds " +
-                                 std::to_string(kNoAllocPartBytes) + " bytes and " +
-                                 std::to_string(kNoAllocCounters) + " counters (fewer num_splits or a smaller "
-                                 "batch fit)");
+                                 "partials; the fixed scratch holds " + std::to_string(kNoAllocPartBytes) +
+                                 " bytes (fewer num_splits or a smaller batch fit)");
             scr = fixed_scratch;
-            cs = static_cast<uint8_t *>(fixed_scratch) + kNoAllocPartBytes;
-            // the counters must start at zero: clear them with a fill kernel
-            // (the array keeps the previous call's contents)
-            rc = imh_fill_zero(stream, cs, ctr_count * 4);
-            if (rc) return rc;
         } else {
             rc = imh::stream_scratch(stream, 1, part_bytes, &scr);
-            if (rc) return rc;
-            rc = imh::stream_scratch(stream, kCounterSlot, ctr_count * 4, &cs);
             if (rc) return rc;
         }
         po = static_cast<float *>(scr);
         pm = po + nparts * kD;
         pl = pm + nparts;
-        ctr = static_cast<int *>(cs);
     }
     const __half *qh = reinterpret_cast<const __half *>(q);
     dim3 grid(S, nkv, B);
@@ -1487,7 +1388,7 @@ static int run_attention(imh_stream *stream, const imh_tq_tables *t, const imh_t
                        (int)nkv, (int)cache->max_seq_len, (int)L, (int)token_count, seq_lens, attn_scale,       \
                        t->signs, t->qjl_t,                                                                      \
                        t->k_codebook, t->v_codebook, cache->k_codes, cache->v_codes, cache->k_scales,           \
-                       cache->v_scales, cache->k_r_norms, (int)split_len, po, pm, pl, ctr,                      \
+                       cache->v_scales, cache->k_r_norms, (int)split_len, po, pm, pl,                           \
                        reinterpret_cast<__half *>(out), qr, fz)
     // without the QK-norm the kernel still reads (and discards) one position
     // and 64 table entries: point them at the codebook
@@ -1531,6 +1432,12 @@ static int run_attention(imh_stream *stream, const imh_tq_tables *t, const imh_t
     }
 #undef IMH_TQ_LAUNCH
     IMH_HIP(hipGetLastError());
+    if (S > 1) {   // the splits' merge, in stream order after every partial
+        const int rows = (int)(B * num_heads);
+        hipLaunchKernelGGL(tq_split_combine_kernel<false>, dim3((rows + 3) / 4), dim3(256), 0, stream->stream, po, pm,
+                           pl, rows, (int)S, t->signs, reinterpret_cast<__half *>(out));
+        IMH_HIP(hipGetLastError());
+    }
     return IMH_OK;
 }
 

@@ -1,11 +1,11 @@
 """The allocation-free TurboQuant attention entry point against the ordinary one.
 
-imh_encode_turboquant_attention_noalloc keeps its split partials and arrival
-counters in a fixed per-GPU device array instead of the stream's scratch.  It
-runs the same kernels with the same split count, so its output must equal
+imh_encode_turboquant_attention_noalloc keeps its split partials in a fixed
+per-GPU device array instead of the stream's scratch.  It runs the same
+kernels with the same split count, so its output must equal
 imh_encode_turboquant_attention's bit for bit.  Two calls in a row, the second
-on a smaller input, check that the array's leftover contents (partials and
-counters of the first call) do not leak into the second.  Both calls go
+on a smaller input, check that the array's leftover contents (the first call's
+partials) do not leak into the second.  Both calls go
 through the C ABI (ctypes), as a binding would make them.
 """
 import ctypes as C
