@@ -333,14 +333,13 @@ int imh_encode_turboquant_attention(imh_stream *stream, const imh_tq_tables *t,
 /* No counterpart in the reference: imh_encode_turboquant_attention for callers
  * that cannot allocate device memory (code under HIP graph capture on a stream
  * whose scratch has not grown yet, tight serving loops, harnesses that forbid
- * hipMalloc).  Same arguments, kernels and results; the split partials and
- * arrival counters live in a fixed per-GPU device array (4 MiB of partials --
- * batch x num_heads x splits x 520 B -- and 4096 counters, batch x
- * num_kv_heads) instead of the stream's scratch, so the call allocates
- * nothing.  A shape that needs more returns IMH_EINVAL (pass fewer num_splits
- * or a smaller batch).  Every call on one GPU shares that array: calls that
+ * hipMalloc).  Same arguments, kernels and results; the split partials live
+ * in a fixed per-GPU device array (4 MiB -- batch x num_heads x splits x
+ * 520 B) instead of the stream's scratch, so the call allocates nothing.  A
+ * shape that needs more returns IMH_EINVAL (pass fewer num_splits or a
+ * smaller batch).  Every call on one GPU shares that array: calls that
  * overlap on one GPU (two streams at once) race; calls in one stream are
- * ordered.  The counters are cleared by a fill kernel in each call. */
+ * ordered.  Each call writes every partial it reads, so nothing is cleared. */
 int imh_encode_turboquant_attention_noalloc(imh_stream *stream, const imh_tq_tables *t,
                                             const imh_tq_kv_cache *cache, const uint16_t *q,
                                             uint32_t num_heads, uint32_t seq_len,
