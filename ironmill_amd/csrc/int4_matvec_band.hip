@@ -75,7 +75,9 @@ __global__ void __launch_bounds__(512) int4_band_kernel(MatPtrs mp, const ActIn 
     const __half *__restrict__ awq = in.awq;
     extern __shared__ __attribute__((aligned(16))) uint8_t lds_b[];
     const int tid = threadIdx.x, nthr = blockDim.x;
-    const int lane = tid & 63, wave = tid >> 6, waves = nthr >> 6;
+    // the wave index as a scalar, so the weight pointer it selects is uniform
+    // and the buffer resources stay in scalar registers
+    const int lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6), waves = nthr >> 6;
     const int mat = wave / W, part = wave - mat * W;
     const int G = K / kGS, P = G / 2;
     const int p0 = (part * P) / W;
