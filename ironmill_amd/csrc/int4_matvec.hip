@@ -304,11 +304,26 @@ int run_gemm(imh_stream *s, const ActIn &in, int M, const imh_affine_int4_weight
 int run_matvec(imh_stream *s, ActIn in, uint32_t B, int nmat, int epi, int N, int K, const MatPtrs &mp,
                const char *who) {
     const bool rn = in.b != nullptr;
+    const int cus = s->dev->props.multiProcessorCount;
     {
         bool used = false;
-        const int rc =
-            launch_band_matvec(s->stream, s->dev->props.multiProcessorCount, (int)B, nmat, epi, N, K, mp, in, &used);
+        const int rc = launch_band_matvec(s->stream, cus, (int)B, nmat, epi, N, K, mp, in, &used);
         if (rc || used) return rc;
+    }
+    if (rn && in.round_mode == 1 && B > 2) {
+        // 3-8 rows reading the f16 normed rows: the rows kernel writes the
+        // residual and normed rows, then the band kernel projects the normed
+        // rows as a plain source (one band launch instead of a prep + tile pair)
+        ActIn pin = {};
+        pin.a = in.normed_out;
+        pin.awq = in.awq;
+        bool fits = false;
+        int rc = launch_band_matvec(s->stream, cus, (int)B, nmat, epi, N, K, mp, pin, &fits, true);
+        if (rc) return rc;
+        if (fits) {
+            rc = encode_resnorm_rows(s, in.a, in.b, in.gamma, in.eps, in.residual_out, in.normed_out, (int)B, K);
+            return rc ? rc : run_matvec(s, pin, B, nmat, epi, N, K, mp, who);
+        }
     }
     Plan p;
     int rc = plan_launch(s, nmat, rn, N, K, (int)B, who, p);

@@ -58,13 +58,14 @@ struct BandLds {
 
 __host__ __device__ inline BandLds band_lds(int G, int BM, int NMAT, int TM, int waves, bool rn) {
     BandLds L;
+    const int NH = (BM + 3) / 4;   // MFMA passes of up to 4 batch rows
     L.img = 0;
     L.gs = L.img + (size_t)G * 2 * BM * kRS * 2;
     L.sz = L.gs + (size_t)G * 2 * BM * 4;
     L.rsq = L.sz + (size_t)NMAT * G * TM * 8 * 4;
-    L.red = L.rsq + (rn ? (size_t)G * BM * 4 : 0);
+    L.red = L.rsq + (rn ? (size_t)G * BM * 4 + (size_t)BM * 4 : 0);
     L.red = (L.red + 15) & ~(size_t)15;
-    L.total = L.red + (size_t)waves * TM * 8 * 16;
+    L.total = L.red + (size_t)waves * TM * 8 * 16 * NH;
     return L;
 }
 
@@ -93,7 +94,9 @@ __global__ void __launch_bounds__(512) int4_band_kernel(MatPtrs mp, const ActIn 
     float *gsl = reinterpret_cast<float *>(lds_b + L.gs);
     uint32_t *szs = reinterpret_cast<uint32_t *>(lds_b + L.sz);
     float *rsq = reinterpret_cast<float *>(lds_b + L.rsq);
+    float *rinv = rsq + G * BM;   // RN: rms_inv per batch row (the epilogue's copy)
     float4_t *red = reinterpret_cast<float4_t *>(lds_b + L.red);
+    constexpr int NH = (BM + 3) / 4, BMH = BM < 4 ? BM : 4;   // MFMA passes, batch rows per pass
 
     // (a) activation chunks: chunk c = group c >> 4, elements (c & 15) * 8 ..
     // +7; 16 consecutive threads (one DPP row) hold one group
@@ -208,6 +211,12 @@ __global__ void __launch_bounds__(512) int4_band_kernel(MatPtrs mp, const ActIn 
             const float ss = ((t8[0] + t8[1]) + (t8[2] + t8[3])) + ((t8[4] + t8[5]) + (t8[6] + t8[7]));
             ri[b] = 1.0f / __builtin_sqrtf(ss / (float)K + in.eps);
         }
+        if (BM > 2 && tid < BM) {
+            float r = ri[0];
+#pragma unroll
+            for (int b = 1; b < BM; b++) r = tid == b ? ri[b] : r;
+            rinv[tid] = r;
+        }
     }
     // (f) operand image -> LDS [g][plane][b][kRS], group sums [g][plane][b];
     // RN: workgroup 0 writes the residual and normed rows
@@ -267,10 +276,12 @@ __global__ void __launch_bounds__(512) int4_band_kernel(MatPtrs mp, const ActIn 
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
 
     // (g) MFMA.  A row of this lane: i = lane & 15 -> (ah, aplane, ab); the
-    // lane's result rows: (h, plane) = (lane >> 5, (lane >> 4) & 1)
+    // lane's result rows: (h, plane) = (lane >> 5, (lane >> 4) & 1).  Above 4
+    // batch rows the MFMAs run in passes of 4 (pass ph: batch rows 4 ph ..),
+    // each weight operand used by every pass.
     const int ai = lane & 15;
     const int ah = ai >> 3, aplane = (ai >> 2) & 1, ab = ai & 3;
-    const bool a_live = ab < BM;
+    const bool a_live = ab < BMH;
     const int dplane = (lane >> 4) & 1;
     const int ntile = (nrows + 7) >> 3;
     float acc[TM][BM];
@@ -284,12 +295,16 @@ __global__ void __launch_bounds__(512) int4_band_kernel(MatPtrs mp, const ActIn 
         if (i < np) {
             const int g = 2 * (p0 + i) + jh;             // this lane's column group
             const int ga = 2 * (p0 + i) + ah;            // this lane's A-row group
-            const _Float16 *xa = img + ((size_t)(ga * 2 + aplane) * BM + min(ab, BM - 1)) * kRS + kq * 32;
-            half8_t av[4];
+            half8_t av[NH][4];
 #pragma unroll
-            for (int m = 0; m < 4; m++) {
-                av[m] = *reinterpret_cast<const half8_t *>(xa + m * 8);
-                if (!a_live) av[m] = (half8_t){0, 0, 0, 0, 0, 0, 0, 0};
+            for (int ph = 0; ph < NH; ph++) {
+                const _Float16 *xa =
+                    img + ((size_t)(ga * 2 + aplane) * BM + min(4 * ph + ab, BM - 1)) * kRS + kq * 32;
+#pragma unroll
+                for (int m = 0; m < 4; m++) {
+                    av[ph][m] = *reinterpret_cast<const half8_t *>(xa + m * 8);
+                    if (!a_live) av[ph][m] = (half8_t){0, 0, 0, 0, 0, 0, 0, 0};
+                }
             }
             const float *gp = gsl + (g * 2 + dplane) * BM;
             float gsv[BM];
@@ -301,19 +316,26 @@ __global__ void __launch_bounds__(512) int4_band_kernel(MatPtrs mp, const ActIn 
                     const uint32_t sz = szs[(mat * G + g) * RT + t * 8 + jr];
                     const float s24 = (float)__builtin_bit_cast(_Float16, (uint16_t)(sz & 0xFFFFu)) * kTwo24;
                     const float z = (float)__builtin_bit_cast(_Float16, (uint16_t)(sz >> 16));
-                    float4_t accg = {0.0f, 0.0f, 0.0f, 0.0f};
+                    u32x4_t bq[4];
 #pragma unroll
                     for (int m = 0; m < 4; m++) {
                         const uint32_t w = wq[t][i][m];
                         const uint32_t q0 = __builtin_amdgcn_perm(w, 0u, 0x0C050C04u);  // b0, b1
                         const uint32_t q1 = __builtin_amdgcn_perm(w, 0u, 0x0C070C06u);  // b2, b3
-                        const u32x4_t bq = (u32x4_t){q0, q1, q0 & 0x00F000F0u, q1 & 0x00F000F0u};
-                        accg = __builtin_amdgcn_mfma_f32_16x16x32_f16(av[m], __builtin_bit_cast(half8_t, bq), accg,
-                                                                      0, 0, 0);
+                        bq[m] = (u32x4_t){q0, q1, q0 & 0x00F000F0u, q1 & 0x00F000F0u};
                     }
 #pragma unroll
-                    for (int b = 0; b < BM; b++)
-                        acc[t][b] = __builtin_fmaf(s24, __builtin_fmaf(-z, gsv[b], accg[b]), acc[t][b]);
+                    for (int ph = 0; ph < NH; ph++) {
+                        float4_t accg = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+                        for (int m = 0; m < 4; m++)
+                            accg = __builtin_amdgcn_mfma_f32_16x16x32_f16(av[ph][m], __builtin_bit_cast(half8_t, bq[m]),
+                                                                          accg, 0, 0, 0);
+#pragma unroll
+                        for (int b = 0; b < BMH; b++)
+                            acc[t][4 * ph + b] =
+                                __builtin_fmaf(s24, __builtin_fmaf(-z, gsv[4 * ph + b], accg[b]), acc[t][4 * ph + b]);
+                    }
                 }
             }
         }
@@ -322,15 +344,18 @@ __global__ void __launch_bounds__(512) int4_band_kernel(MatPtrs mp, const ActIn 
     // (h 0, lo), r + 40 (h 1, hi), r + 56 (h 1, lo)
 #pragma unroll
     for (int t = 0; t < TM; t++) {
-        float4_t v = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
-        for (int b = 0; b < BM; b++) {
-            float a = acc[t][b];
-            a += __shfl_down(a, 16);
-            a += __shfl_down(a, 40);
-            v[b] = a;
+        for (int ph = 0; ph < NH; ph++) {
+            float4_t v = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+            for (int b = 0; b < BMH; b++) {
+                float a = acc[t][4 * ph + b];
+                a += __shfl_down(a, 16);
+                a += __shfl_down(a, 40);
+                v[b] = a;
+            }
+            if (lane < 8) red[((wave * TM + t) * NH + ph) * 8 + lane] = v;
         }
-        if (lane < 8) red[(wave * TM + t) * 8 + lane] = v;
     }
     __syncthreads();
     for (int o = tid; o < RT * BM; o += nthr) {
@@ -342,9 +367,9 @@ __global__ void __launch_bounds__(512) int4_band_kernel(MatPtrs mp, const ActIn 
 #pragma unroll
         for (int mt = 0; mt < NMAT; mt++) {
             float s = 0.0f;
-            for (int p = 0; p < W; p++) s += red[((mt * W + p) * TM + t) * 8 + rl][b];
+            for (int p = 0; p < W; p++) s += red[(((mt * W + p) * TM + t) * NH + (b >> 2)) * 8 + rl][b & 3];
             // round_mode 0: the row's rms_inv scales both projections, ahead of the activation
-            if (RN && !rnd) s *= b == 0 ? ri[0] : ri[BM - 1];
+            if (RN && !rnd) s *= BM <= 2 ? (b == 0 ? ri[0] : ri[BM - 1]) : rinv[b];
             sum[mt] = s;
         }
         if (EPI == EPI_SILU || EPI == EPI_GELU) {
@@ -372,43 +397,69 @@ struct BandLaunch {
     int N, K, B, W;
 };
 
-template <int NMAT, int EPI, int TM, int NP, int BM, bool RN>
-void launch_xc(int xc, const BandLaunch &L, const MatPtrs &mp, const ActIn &in) {
-    if (xc == 1)
-        hipLaunchKernelGGL((int4_band_kernel<NMAT, EPI, TM, NP, BM, 1, RN>), L.grid, L.block, L.lds, L.st, mp, in, L.N,
-                           L.K, L.B, L.W);
-    else
-        hipLaunchKernelGGL((int4_band_kernel<NMAT, EPI, TM, NP, BM, 3, RN>), L.grid, L.block, L.lds, L.st, mp, in, L.N,
-                           L.K, L.B, L.W);
+// Above 64 KB of LDS a kernel must be allowed the larger size first (gfx950
+// has 160 KB per CU); false if the runtime refuses.
+template <typename F>
+bool allow_lds(F kernel, size_t lds) {
+    return lds <= 64 * 1024 ||
+           hipFuncSetAttribute(reinterpret_cast<const void *>(kernel), hipFuncAttributeMaxDynamicSharedMemorySize,
+                               (int)lds) == hipSuccess;
 }
 
+template <int NMAT, int EPI, int TM, int NP, int BM, bool RN>
+bool launch_xc(int xc, const BandLaunch &L, const MatPtrs &mp, const ActIn &in) {
+    if (xc == 1) {
+        if (!allow_lds(int4_band_kernel<NMAT, EPI, TM, NP, BM, 1, RN>, L.lds)) return false;
+        hipLaunchKernelGGL((int4_band_kernel<NMAT, EPI, TM, NP, BM, 1, RN>), L.grid, L.block, L.lds, L.st, mp, in, L.N,
+                           L.K, L.B, L.W);
+    } else if (BM <= 2) {   // three activation chunks per thread: 1-2 batch rows only
+        if (!allow_lds(int4_band_kernel<NMAT, EPI, TM, NP, BM, BM <= 2 ? 3 : 1, RN>, L.lds)) return false;
+        hipLaunchKernelGGL((int4_band_kernel<NMAT, EPI, TM, NP, BM, BM <= 2 ? 3 : 1, RN>), L.grid, L.block, L.lds,
+                           L.st, mp, in, L.N, L.K, L.B, L.W);
+    }
+    return true;
+}
+
+// batch rows per instantiation: 1, 2, 4 (3-4 rows) and 8 (5-8 rows; plain
+// sources only)
 template <int NMAT, int EPI, int TM, int NP, bool RN>
-void launch_bm(int bm, int xc, const BandLaunch &L, const MatPtrs &mp, const ActIn &in) {
-    if (bm == 1) launch_xc<NMAT, EPI, TM, NP, 1, RN>(xc, L, mp, in);
-    else launch_xc<NMAT, EPI, TM, NP, 2, RN>(xc, L, mp, in);
+bool launch_bm(int bm, int xc, const BandLaunch &L, const MatPtrs &mp, const ActIn &in) {
+    if (bm == 1) return launch_xc<NMAT, EPI, TM, NP, 1, RN>(xc, L, mp, in);
+    if (bm == 2) return launch_xc<NMAT, EPI, TM, NP, 2, RN>(xc, L, mp, in);
+    if constexpr (!RN) {
+        if (bm == 4) return launch_xc<NMAT, EPI, TM, NP, 4, RN>(xc, L, mp, in);
+        return launch_xc<NMAT, EPI, TM, NP, 8, RN>(xc, L, mp, in);
+    }
+    return false;
 }
 
 // (TM, NP) instantiated: (2, 5), (3, 5) and (5, 3); the host picks the
 // smallest TM that holds the band.
 template <int NMAT, int EPI, bool RN>
-void launch_shape(int tm, int bm, int xc, const BandLaunch &L, const MatPtrs &mp, const ActIn &in) {
-    if (tm <= 2) launch_bm<NMAT, EPI, 2, 5, RN>(bm, xc, L, mp, in);
-    else if (tm <= 3) launch_bm<NMAT, EPI, 3, 5, RN>(bm, xc, L, mp, in);
-    else launch_bm<NMAT, EPI, 5, 3, RN>(bm, xc, L, mp, in);
+bool launch_shape(int tm, int bm, int xc, const BandLaunch &L, const MatPtrs &mp, const ActIn &in) {
+    if (tm <= 2) return launch_bm<NMAT, EPI, 2, 5, RN>(bm, xc, L, mp, in);
+    if (tm <= 3) return launch_bm<NMAT, EPI, 3, 5, RN>(bm, xc, L, mp, in);
+    return launch_bm<NMAT, EPI, 5, 3, RN>(bm, xc, L, mp, in);
 }
 
 }  // namespace
 
-// Launches the band kernel when it applies (B <= 2, no row segments, an even
+// Launches the band kernel when it applies (B <= 8, no row segments, an even
 // number of groups, the shape within the instantiated tiles and the LDS
-// budget; a residual-norm source with round_mode 0 or 1, as nmat 1 with
-// EPI_STORE or nmat 2 with an activation); *used reports whether it did.
+// budget -- 64 KB for 1-2 batch rows, 160 KB with one activation chunk per
+// thread above; a residual-norm source only at 1-2 batch rows, with
+// round_mode 0 or 1, as nmat 1 with EPI_STORE or nmat 2 with an activation);
+// *used reports whether it did.  probe: only whether it would apply.
 int launch_band_matvec(hipStream_t st, int cus, int B, int nmat, int epi, int N, int K, const MatPtrs &mp,
-                       const ActIn &in, bool *used) {
+                       const ActIn &in, bool *used, bool probe) {
     *used = false;
     const bool rn = in.b != nullptr;
     const int G = K / kGS;
-    if (B < 1 || B > 2 || mp.seg[0] != 0 || G % 2 || G < 2) return IMH_OK;
+    if (B < 1 || B > 8 || mp.seg[0] != 0 || G % 2 || G < 2) return IMH_OK;
+    const int bm = B <= 2 ? B : B <= 4 ? 4 : 8;
+    // above two rows every workgroup would redo the whole residual + norm of
+    // every row (measured slower than the rows kernel + the plain band)
+    if (bm > 2 && rn) return IMH_OK;
     if (rn && (in.round_mode > 1 || (nmat == 2) != (epi != EPI_STORE))) return IMH_OK;
     for (int i = 0; i < nmat; i++)
         if ((reinterpret_cast<uintptr_t>(mp.scales[i]) | reinterpret_cast<uintptr_t>(mp.zeros[i])) & 3) return IMH_OK;
@@ -421,32 +472,39 @@ int launch_band_matvec(hipStream_t st, int cus, int B, int nmat, int epi, int N,
     const int tm = (rows + 7) / 8;
     if (tm > 5) return IMH_OK;
     const int TM = tm <= 2 ? 2 : tm <= 3 ? 3 : 5, NPmax = tm <= 3 ? 5 : 3;
-    // waves per matrix: as few as keep each wave within NPmax pairs
-    const int W = std::min((P + NPmax - 1) / NPmax, 8 / nmat);
+    // waves per matrix: as few as keep each wave within NPmax pairs (1-2
+    // rows); all eight above, so one activation chunk per thread covers K
+    const int W = bm > 2 ? std::min(8 / nmat, P) : std::min((P + NPmax - 1) / NPmax, 8 / nmat);
     const int np = (P + W - 1) / W;
     if (np > NPmax) return IMH_OK;
     const int nthr = 64 * W * nmat;
     const int xc = (G * 16 + nthr - 1) / nthr;
-    if (xc > 3 || nmat * rows * P > kSZC * nthr) return IMH_OK;
-    const size_t lds = band_lds(G, B, nmat, TM, W * nmat, rn).total;
-    if (lds > 64 * 1024) return IMH_OK;
+    if (xc > 3 || (bm > 2 && xc > 1) || nmat * rows * P > kSZC * nthr) return IMH_OK;
+    const size_t lds = band_lds(G, bm, nmat, TM, W * nmat, rn).total;
+    if (lds > (bm <= 2 ? 64 : 160) * 1024) return IMH_OK;
+    if (probe) {
+        *used = true;
+        return IMH_OK;
+    }
     BandLaunch L{dim3(nwg), dim3(nthr), lds, st, N, K, B, W};
+    bool ok;
     if (rn) {
         if (nmat == 1)
-            launch_shape<1, EPI_STORE, true>(tm, B, xc, L, mp, in);
+            ok = launch_shape<1, EPI_STORE, true>(tm, bm, xc, L, mp, in);
         else if (epi == EPI_SILU)
-            launch_shape<2, EPI_SILU, true>(tm, B, xc, L, mp, in);
+            ok = launch_shape<2, EPI_SILU, true>(tm, bm, xc, L, mp, in);
         else
-            launch_shape<2, EPI_GELU, true>(tm, B, xc, L, mp, in);
+            ok = launch_shape<2, EPI_GELU, true>(tm, bm, xc, L, mp, in);
     } else if (nmat == 1) {
-        launch_shape<1, EPI_STORE, false>(tm, B, xc, L, mp, in);
+        ok = launch_shape<1, EPI_STORE, false>(tm, bm, xc, L, mp, in);
     } else if (epi == EPI_SILU) {
-        launch_shape<2, EPI_SILU, false>(tm, B, xc, L, mp, in);
+        ok = launch_shape<2, EPI_SILU, false>(tm, bm, xc, L, mp, in);
     } else if (epi == EPI_GELU) {
-        launch_shape<2, EPI_GELU, false>(tm, B, xc, L, mp, in);
+        ok = launch_shape<2, EPI_GELU, false>(tm, bm, xc, L, mp, in);
     } else {
-        launch_shape<2, EPI_STORE, false>(tm, B, xc, L, mp, in);
+        ok = launch_shape<2, EPI_STORE, false>(tm, bm, xc, L, mp, in);
     }
+    if (!ok) return IMH_OK;   // the LDS size was refused: the tile kernel runs the op
     IMH_HIP(hipGetLastError());
     *used = true;
     return IMH_OK;

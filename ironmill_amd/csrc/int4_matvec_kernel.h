@@ -635,6 +635,6 @@ void launch_image_mt2(int nmat, int epi, const Launch &L, const MatPtrs &mp, con
 // plain sources and residual-norm sources of round_mode 0 or 1 (in.b set);
 // *used is false where it does not apply.
 int launch_band_matvec(hipStream_t st, int cus, int B, int nmat, int epi, int N, int K, const MatPtrs &mp,
-                       const ActIn &in, bool *used);
+                       const ActIn &in, bool *used, bool probe = false);
 
 }  // namespace imh_int4
