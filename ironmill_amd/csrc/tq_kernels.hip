@@ -47,7 +47,7 @@ constexpr int kD = 128;          // head_dim the kernels are built for
 constexpr int kChunk = 16;       // positions per MFMA block
 constexpr int kWaves = 4;        // waves per attention workgroup
 constexpr int kSplitQuantum = kChunk * kWaves;
-constexpr int kMaxSplits = 512;     // the combine kernel stages every split's weight in LDS
+constexpr int kMaxSplits = 512;     // split count cap
 constexpr int kAutoSplitLen = 256;  // shortest split the automatic split count makes
 
 // Strides 1..32 of the unnormalised fast Walsh-Hadamard transform of a
@@ -1079,47 +1079,47 @@ __global__ void __launch_bounds__(64 * kWaves) __attribute__((amdgpu_waves_per_e
     }
 }
 
-// grid ceil(rows / 4), block 256: wave w merges the S split partials of row
-// 4 blockIdx.x + w ([row][S] maxima -- in log2 units for the prefill kernel,
-// natural for the decode kernel -- and sums, [row][S][kD] outputs) and
-// rotates the result back into out[row].  Split s weighs exp(m_s - M); the
-// outputs are summed in split order, loads several splits ahead.
+// grid rows, block 256: one workgroup merges the S split partials of its row
+// ([row][S] maxima -- in log2 units for the prefill kernel, natural for the
+// decode kernel -- and sums, [row][S][kD] outputs) and rotates the result
+// back into out[row].  Split s weighs exp(m_s - M); wave w sums the splits
+// w, w + 4, .. (several loads in flight), the four partial sums are added in
+// wave order through LDS, and wave 0 normalises and rotates.
 template <bool LOG2>
 __global__ void __launch_bounds__(256) tq_split_combine_kernel(const float *__restrict__ part_o,
                                                                const float *__restrict__ part_m,
                                                                const float *__restrict__ part_l, int rows, int S,
                                                                const float *__restrict__ signs,
                                                                __half *__restrict__ out) {
-    __shared__ float fs[4][kMaxSplits];
+    __shared__ float osum[4][kD];
+    __shared__ float lsums[4];
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-    const int row = blockIdx.x * 4 + wave;
-    if (row >= rows) return;   // no workgroup barrier below
+    const int row = blockIdx.x;
     const float *pm = part_m + (size_t)row * S;
     const float *pl = part_l + (size_t)row * S;
     float mx = -INFINITY;
     for (int sp = lane; sp < S; sp += 64) mx = fmaxf(mx, pm[sp]);
 #pragma unroll
     for (int st = 32; st >= 1; st >>= 1) mx = fmaxf(mx, __shfl_xor(mx, st));
-    float lsum = 0.0f;
-    for (int sp = lane; sp < S; sp += 64) {
+    const float *po = part_o + (size_t)row * S * kD;
+    float o0 = 0.0f, o1 = 0.0f, ls = 0.0f;
+#pragma unroll 4
+    for (int sp = wave; sp < S; sp += 4) {
         const float m = pm[sp];
         const float f = (mx == -INFINITY || m == -INFINITY) ? 0.0f
                                                             : (LOG2 ? __builtin_amdgcn_exp2f(m - mx) : __expf(m - mx));
-        fs[wave][sp] = f;
-        lsum = __builtin_fmaf(f, pl[sp], lsum);
-    }
-    lsum = imh_qk::wave_sum64(lsum);
-    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-    __builtin_amdgcn_wave_barrier();
-    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-    const float *po = part_o + (size_t)row * S * kD;
-    float o0 = 0.0f, o1 = 0.0f;
-#pragma unroll 8
-    for (int sp = 0; sp < S; sp++) {
-        const float f = fs[wave][sp];
+        ls = __builtin_fmaf(f, pl[sp], ls);
         o0 = __builtin_fmaf(po[(size_t)sp * kD + lane], f, o0);
         o1 = __builtin_fmaf(po[(size_t)sp * kD + lane + 64], f, o1);
     }
+    osum[wave][lane] = o0;
+    osum[wave][lane + 64] = o1;
+    if (lane == 0) lsums[wave] = ls;
+    __syncthreads();
+    if (wave != 0) return;
+    o0 = ((osum[0][lane] + osum[1][lane]) + osum[2][lane]) + osum[3][lane];
+    o1 = ((osum[0][lane + 64] + osum[1][lane + 64]) + osum[2][lane + 64]) + osum[3][lane + 64];
+    const float lsum = ((lsums[0] + lsums[1]) + lsums[2]) + lsums[3];
     const float inv = 1.0f / fmaxf(lsum, 1e-10f);
     const float sg0 = signs[lane], sg1 = signs[lane + 64];
     float x0 = o0 * inv * sg0, x1 = o1 * inv * sg1;
@@ -1298,7 +1298,7 @@ static int run_prefill_attention(imh_stream *stream, const imh_tq_tables *t, con
 #undef IMH_TQ_PREFILL
     IMH_HIP(hipGetLastError());
     if (S > 1) {
-        hipLaunchKernelGGL(tq_split_combine_kernel<true>, dim3(qblocks), dim3(256), 0, stream->stream, po, pm, pls,
+        hipLaunchKernelGGL(tq_split_combine_kernel<true>, dim3((unsigned)rows), dim3(256), 0, stream->stream, po, pm, pls,
                            (int)rows, (int)S, t->signs, reinterpret_cast<__half *>(out));
         IMH_HIP(hipGetLastError());
     }
@@ -1434,7 +1434,7 @@ static int run_attention(imh_stream *stream, const imh_tq_tables *t, const imh_t
     IMH_HIP(hipGetLastError());
     if (S > 1) {   // the splits' merge, in stream order after every partial
         const int rows = (int)(B * num_heads);
-        hipLaunchKernelGGL(tq_split_combine_kernel<false>, dim3((rows + 3) / 4), dim3(256), 0, stream->stream, po, pm,
+        hipLaunchKernelGGL(tq_split_combine_kernel<false>, dim3((unsigned)rows), dim3(256), 0, stream->stream, po, pm,
                            pl, rows, (int)S, t->signs, reinterpret_cast<__half *>(out));
         IMH_HIP(hipGetLastError());
     }
