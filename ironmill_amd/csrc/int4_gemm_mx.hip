@@ -20,9 +20,10 @@
 //    sum a (128 + q) and the group's correction subtracts (128 + z) sum a,
 //    with sum a the row's group sum of the rounded operand (exact products,
 //    f32 sums).  fp8: q is looked up as its e4m3 encoding (exact for 0..15)
-//    and the correction subtracts z sum a.  The correction is the group's
-//    first matrix-core product (the row sum split into three exact bf16
-//    pieces against -c), so the fold of a group is one multiply-add.
+//    and the correction subtracts z sum a.  The correction is one more
+//    matrix-core product per tile and group (the row sum split into three
+//    exact bf16 pieces against -c; the last of the group's bf16 products),
+//    so the fold of a group is one multiply-add.
 //  * a prep kernel writes the operand rows (x / awq rounded, each 8-element
 //    chunk in the slot order the code unpack produces) and their group sums.
 //  * the 32 x 32 matrix-core shapes (v_mfma_f32_32x32x16_bf16,
@@ -31,9 +32,10 @@
 //  * workgroup tile 64 (M) x 256 columns, four waves each owning 64 x 64
 //    (2 x 2 MFMA tiles of 32 x 32); the next group's A (global -> registers
 //    -> other LDS buffer) and B (global -> registers) are loaded while the
-//    current group computes, unconditionally (the last group re-loads
-//    itself), so no wait for them sits inside the compute: one barrier per
-//    group.  K is split over workgroups when the tile grid is smaller than
+//    current group computes, their loads issued one or two per k step (a
+//    burst of twelve at the group's start held the wave's issue for ~400
+//    cycles), unconditionally (the last group re-loads itself), so no wait
+//    for them sits inside the compute: one barrier per group.  K is split over workgroups when the tile grid is smaller than
 //    twice the CU count; the f32 partials are summed in split order by a
 //    second kernel (deterministic).
 #include <hip/hip_runtime.h>
@@ -204,15 +206,19 @@ __global__ void __launch_bounds__(kThreads, 2) gemm_mx_kernel(
         szrow[j] = (size_t)n * G;
     }
     // A staging: chunk c = i * 256 + tid of the group's 64 x (128 * EB) bytes
+    auto load_a1 = [&](int g, int i, u32x4_t *ar) __attribute__((always_inline)) {
+        const int c = i * kThreads + tid;
+        const int r = c / (kGS * EB / 16), cc = c - r * (kGS * EB / 16);
+        const int m = min(m0 + r, M - 1);
+        ar[i] = *reinterpret_cast<const u32x4_t *>(aop + ((size_t)m * K + (size_t)g * kGS) * EB + cc * 16);
+    };
+    auto load_gs = [&](int g, float &gs) __attribute__((always_inline)) {
+        gs = tid < kBM ? gsum[(size_t)min(m0 + tid, M - 1) * G + g] : 0.0f;
+    };
     auto load_a = [&](int g, u32x4_t *ar, float &gs) __attribute__((always_inline)) {
 #pragma unroll
-        for (int i = 0; i < ACH; i++) {
-            const int c = i * kThreads + tid;
-            const int r = c / (kGS * EB / 16), cc = c - r * (kGS * EB / 16);
-            const int m = min(m0 + r, M - 1);
-            ar[i] = *reinterpret_cast<const u32x4_t *>(aop + ((size_t)m * K + (size_t)g * kGS) * EB + cc * 16);
-        }
-        gs = tid < kBM ? gsum[(size_t)min(m0 + tid, M - 1) * G + g] : 0.0f;
+        for (int i = 0; i < ACH; i++) load_a1(g, i, ar);
+        load_gs(g, gs);
     };
     auto store_a = [&](int buf, const u32x4_t *ar, float gs) __attribute__((always_inline)) {
 #pragma unroll
@@ -229,15 +235,18 @@ __global__ void __launch_bounds__(kThreads, 2) gemm_mx_kernel(
         u32x4_t w[2][2];
         uint16_t s[2], z[2];
     };
-    auto load_b = [&](int g, BRegs &b) __attribute__((always_inline)) {
-#pragma unroll
-        for (int j = 0; j < 2; j++) {
+    auto load_b1 = [&](int g, int j, BRegs &b) __attribute__((always_inline)) {
+        {
             const uint8_t *p = brow[j] + (size_t)g * 64;
             b.w[j][0] = *reinterpret_cast<const u32x4_t *>(p);
             b.w[j][1] = *reinterpret_cast<const u32x4_t *>(p + (P == PREC_BF16 ? 16 : 32));
             b.s[j] = reinterpret_cast<const uint16_t *>(scales)[szrow[j] + g];
             b.z[j] = reinterpret_cast<const uint16_t *>(zeros)[szrow[j] + g];
         }
+    };
+    auto load_b = [&](int g, BRegs &b) __attribute__((always_inline)) {
+        load_b1(g, 0, b);
+        load_b1(g, 1, b);
     };
 
     float16_t acc[2][2];
@@ -251,10 +260,11 @@ __global__ void __launch_bounds__(kThreads, 2) gemm_mx_kernel(
     // One group: the MFMAs of the four 32 x 32 tiles over the group's k
     // steps, then each tile's group partial folded into acc with the scale
     // and zero-point of the lane's column and the group sums of its rows.
-    auto compute = [&](int buf, const BRegs &b) __attribute__((always_inline)) {
+    // hook(st) runs at k step st: it issues the next group's loads.
+    auto compute = [&](int buf, const BRegs &b, auto &&hook) __attribute__((always_inline)) {
         // The group's zero-point correction -c * rowsum (c = 128 + z for the
-        // bf16 codes, which carry 128; z for fp8) starts each tile's
-        // accumulator, on the matrix core: A lane (m, 0) holds the row sum
+        // bf16 codes, which carry 128; z for fp8) is added to each tile's
+        // group accumulator on the matrix core: A lane (m, 0) holds the row sum
         // split into three bf16 pieces (hi + mid + lo == rowsum exactly), B
         // lane (n, 0) -c three times (exact in bf16), all other k slots zero
         // -- so the fold is one multiply-add per output.
@@ -280,12 +290,8 @@ __global__ void __launch_bounds__(kThreads, 2) gemm_mx_kernel(
         if (P == PREC_BF16) {
             float16_t gg[2][2];
 #pragma unroll
-            for (int mi = 0; mi < 2; mi++)
-#pragma unroll
-                for (int j = 0; j < 2; j++)
-                    gg[mi][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(ca[mi], cb[j], zero16, 0, 0, 0);
-#pragma unroll
             for (int st = 0; st < 8; st++) {
+                hook(st);
                 bf16x8_t af[2], bf[2];
 #pragma unroll
                 for (int mi = 0; mi < 2; mi++)
@@ -305,8 +311,16 @@ __global__ void __launch_bounds__(kThreads, 2) gemm_mx_kernel(
                 for (int mi = 0; mi < 2; mi++)
 #pragma unroll
                     for (int j = 0; j < 2; j++)
-                        gg[mi][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af[mi], bf[j], gg[mi][j], 0, 0, 0);
+                        gg[mi][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af[mi], bf[j], st == 0 ? zero16 : gg[mi][j],
+                                                                            0, 0, 0);
             }
+            // the zero-point correction last: its operands (an LDS read and a
+            // short VALU chain) are built while the k steps run, not ahead of them
+#pragma unroll
+            for (int mi = 0; mi < 2; mi++)
+#pragma unroll
+                for (int j = 0; j < 2; j++)
+                    gg[mi][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(ca[mi], cb[j], gg[mi][j], 0, 0, 0);
 #pragma unroll
             for (int mi = 0; mi < 2; mi++)
 #pragma unroll
@@ -316,6 +330,8 @@ __global__ void __launch_bounds__(kThreads, 2) gemm_mx_kernel(
                     for (int i = 0; i < 16; i++) acc[mi][j][i] = __builtin_fmaf(sj, gg[mi][j][i], acc[mi][j][i]);
                 }
         } else {
+#pragma unroll
+            for (int st = 0; st < 6; st++) hook(st);
             // both k steps' A fragments, then per column fragment its B
             // fragments and the two tiles' MFMAs: one tile's partial live at a time
             i32x8_t af[2][2];
@@ -374,9 +390,14 @@ __global__ void __launch_bounds__(kThreads, 2) gemm_mx_kernel(
     }
     auto step = [&](int g, int buf, const BRegs &cur, BRegs &nxt) __attribute__((always_inline)) {
         const int gn = min(g + 1, g_end - 1);
-        load_a(gn, ar, gsv);
-        load_b(gn, nxt);
-        compute(buf, cur);
+        // the next group's loads spread over the k steps: A chunks first (they
+        // are stored to LDS after the compute), then B
+        compute(buf, cur, [&](int st) __attribute__((always_inline)) {
+            if (st < ACH) load_a1(gn, st, ar);
+            if (st == ACH) load_gs(gn, gsv);
+            if (st == 4) load_b1(gn, 0, nxt);
+            if (st == 5) load_b1(gn, 1, nxt);
+        });
         store_a(buf ^ 1, ar, gsv);
         __syncthreads();
     };
