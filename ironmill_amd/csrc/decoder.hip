@@ -21,6 +21,7 @@
 //   residual + post-attention RMSNorm + gate/up + SiLU/GELU (one launch)
 //                                               -> residual, act
 //   down projection                             -> ffn_down
+//     (at 1-2 rows: reads the operand image the gate/up launch wrote)
 //   [l < L-1] residual + next input RMSNorm + next Q | K | V (one launch)
 //   [l = L-1] residual add                      -> hidden
 // final RMSNorm, LM head -> logits; positions += 1.
@@ -236,7 +237,8 @@ int run_schedule(imh_decoder *d, imh_stream *s, const uint32_t *token_ids, const
                                               r.attn_out, 0));
         }
         IMH_TRY(imh_encode_affine_projection_int4(s, r.attn_out, R, &w.o_proj, r.ffn_down));
-        {   // post-attention residual + norm, then gate + up + activation: one launch
+        {   // post-attention residual + norm, then gate + up + activation (one
+            // launch), then down (at 1-2 rows from the operand image gate/up wrote)
             imh_fused_residual_norm_params rp{};
             rp.a = r.hidden;
             rp.b = r.ffn_down;
@@ -245,9 +247,9 @@ int run_schedule(imh_decoder *d, imh_stream *s, const uint32_t *token_ids, const
             rp.normed_output = r.norm_out;
             rp.token_count = R;
             rp.eps = c.rms_eps;
-            IMH_TRY(imh::encode_resnorm_gate_up_act_int4(s, &rp, R, &w.gate_proj, &w.up_proj, r.act, c.use_gelu));
+            IMH_TRY(imh::encode_resnorm_ffn_block_int4(s, &rp, R, &w.gate_proj, &w.up_proj, &w.down_proj, r.act,
+                                                       r.ffn_down, c.use_gelu));
         }
-        IMH_TRY(imh_encode_affine_projection_int4(s, r.act, R, &w.down_proj, r.ffn_down));
         if (l + 1 < c.num_layers) {
             const imh_decoder_layer_weights &nw = d->layers[l + 1];
             imh_fused_residual_norm_params fp{};

@@ -126,6 +126,12 @@ int encode_segmented_matvec_int4(imh_stream *s, const uint16_t *x, const imh_fus
 int encode_resnorm_gate_up_act_int4(imh_stream *s, const imh_fused_residual_norm_params *rn, uint32_t B,
                                     const imh_affine_int4_weight *gate, const imh_affine_int4_weight *up,
                                     uint16_t *out, int use_gelu);
+// The residual + norm, gate/up + activation and down projection of a decoder
+// layer's FFN: at 1-2 rows on the row-band kernel the gate/up launch hands
+// down its operand image; otherwise the two ops.
+int encode_resnorm_ffn_block_int4(imh_stream *s, const imh_fused_residual_norm_params *rn, uint32_t B,
+                                  const imh_affine_int4_weight *gate, const imh_affine_int4_weight *up,
+                                  const imh_affine_int4_weight *down, uint16_t *act, uint16_t *y, int use_gelu);
 
 // The step's token written to the TurboQuant cache at row seq_lens[b] - 1
 // and attended over [0, seq_lens[b]) in one launch (the write runs in one

@@ -410,6 +410,70 @@ ActIn plain_in(const uint16_t *x, const imh_affine_int4_weight *w) {
     return in;
 }
 
+MatPtrs mat_ptrs(const imh_affine_int4_weight *w0, const imh_affine_int4_weight *w1, uint16_t *out0) {
+    MatPtrs mp = {};
+    const imh_affine_int4_weight *ws[2] = {w0, w1};
+    for (int i = 0; i < (w1 ? 2 : 1); i++) {
+        mp.data[i] = ws[i]->data;
+        mp.scales[i] = reinterpret_cast<const __half *>(ws[i]->scales);
+        mp.zeros[i] = reinterpret_cast<const __half *>(ws[i]->zeros);
+    }
+    mp.out[0] = reinterpret_cast<__half *>(out0);
+    return mp;
+}
+
+// An FFN block (gate/up + activation, then down) at 1-2 rows when both run on
+// the row-band kernel: the gate/up launch also writes the down projection's
+// operand image (act / down's AWQ scales, split into f16 hi + lo), and the
+// down launch stages that image instead of forming it from act -- a division
+// and split per element that each of its workgroups would otherwise repeat
+// over all of K.  gin: the gate/up source (plain or residual-norm); *done
+// false: nothing was launched (the caller runs the two ops).
+int ffn_band_pair(imh_stream *s, ActIn gin, uint32_t B, const imh_affine_int4_weight *gate,
+                  const imh_affine_int4_weight *up, const imh_affine_int4_weight *down, uint16_t *act_out,
+                  uint16_t *y, int epi, bool *done) {
+    *done = false;
+    if (B < 1 || B > 2 || !act_out || !y || misaligned16(act_out)) return IMH_OK;
+    if (misaligned16(gin.a) || misaligned16(gin.b) || misaligned16(gin.gamma) || misaligned16(gin.awq) ||
+        misaligned16(gin.residual_out) || misaligned16(gin.normed_out) || misaligned16(down->awq_scales))
+        return IMH_OK;
+    if (check_weight(gate, "") || check_weight(up, "") || check_weight(down, "")) {
+        imh::clear_error();
+        return IMH_OK;
+    }
+    if (up->n != gate->n || up->k != gate->k || down->k != gate->n) return IMH_OK;
+    int rc = imh::use_device(s->dev);
+    if (rc) return rc;
+    const int cus = s->dev->props.multiProcessorCount;
+    const int F = (int)gate->n, H = (int)gate->k, Hd = (int)down->n;
+    void *scr = nullptr;
+    rc = imh::stream_scratch(s, 0, (size_t)2 * B * F * sizeof(_Float16), &scr);
+    if (rc) return rc;
+    _Float16 *ihi = static_cast<_Float16 *>(scr), *ilo = ihi + (size_t)B * F;
+    MatPtrs gm = mat_ptrs(gate, up, act_out);
+    MatPtrs dm = mat_ptrs(down, nullptr, y);
+    gin.img_out_hi = ihi;
+    gin.img_out_lo = ilo;
+    gin.img_awq = reinterpret_cast<const __half *>(down->awq_scales);
+    ActIn din = {};
+    din.a = reinterpret_cast<const __half *>(act_out);
+    din.hi = ihi;
+    din.lo = ilo;
+    din.img_src = 1;
+    bool fg = false, fd = false;
+    rc = launch_band_matvec(s->stream, cus, (int)B, 2, epi, F, H, gm, gin, &fg, true);
+    if (!rc) rc = launch_band_matvec(s->stream, cus, (int)B, 1, EPI_STORE, Hd, F, dm, din, &fd, true);
+    if (rc || !fg || !fd) return rc;
+    rc = launch_band_matvec(s->stream, cus, (int)B, 2, epi, F, H, gm, gin, &fg);
+    if (rc) return rc;
+    if (!fg) return imh::fail(IMH_EDEVICE, "ffn_band_pair: the gate/up launch was refused after its probe");
+    rc = launch_band_matvec(s->stream, cus, (int)B, 1, EPI_STORE, Hd, F, dm, din, &fd);
+    if (rc) return rc;
+    if (!fd) return imh::fail(IMH_EDEVICE, "ffn_band_pair: the down launch was refused after its probe");
+    *done = true;
+    return IMH_OK;
+}
+
 }  // namespace
 
 namespace imh {
@@ -493,6 +557,27 @@ int encode_resnorm_gate_up_act_int4(imh_stream *s, const imh_fused_residual_norm
     return run_op(s, in, B, gate, up, use_gelu ? EPI_GELU : EPI_SILU, out, nullptr, who);
 }
 
+int encode_resnorm_ffn_block_int4(imh_stream *s, const imh_fused_residual_norm_params *rn, uint32_t B,
+                                  const imh_affine_int4_weight *gate, const imh_affine_int4_weight *up,
+                                  const imh_affine_int4_weight *down, uint16_t *act, uint16_t *y, int use_gelu) {
+    if (s && rn && rn->a && rn->b && rn->norm_weight && rn->residual_output && rn->normed_output && gate && up &&
+        down) {
+        ActIn in = plain_in(nullptr, gate);
+        in.a = reinterpret_cast<const __half *>(rn->a);
+        in.b = reinterpret_cast<const __half *>(rn->b);
+        in.gamma = reinterpret_cast<const __half *>(rn->norm_weight);
+        in.residual_out = reinterpret_cast<__half *>(rn->residual_output);
+        in.normed_out = reinterpret_cast<__half *>(rn->normed_output);
+        in.eps = rn->eps;
+        in.round_mode = 1;
+        bool done = false;
+        const int rc = ffn_band_pair(s, in, B, gate, up, down, act, y, use_gelu ? EPI_GELU : EPI_SILU, &done);
+        if (rc || done) return rc;
+    }
+    const int rc = encode_resnorm_gate_up_act_int4(s, rn, B, gate, up, act, use_gelu);
+    return rc ? rc : imh_encode_affine_projection_int4(s, act, B, down, y);
+}
+
 }  // namespace imh
 
 extern "C" {
@@ -531,6 +616,12 @@ int imh_encode_ffn_block_int4(imh_stream *stream, const uint16_t *x, uint32_t to
     if (rc) return rc;
     if (down->k != gate->n)
         return imh::fail(IMH_EINVAL, std::string(who) + ": down.k must equal the intermediate size (gate.n)");
+    {
+        bool done = false;
+        rc = ffn_band_pair(stream, plain_in(x, gate), token_count, gate, up, down, act_out, y,
+                           use_gelu ? EPI_GELU : EPI_SILU, &done);
+        if (rc || done) return rc;
+    }
     rc = run_op(stream, plain_in(x, gate), token_count, gate, up, use_gelu ? EPI_GELU : EPI_SILU, act_out, nullptr,
                 who);
     return rc ? rc : run_op(stream, plain_in(act_out, down), token_count, down, nullptr, EPI_STORE, y, nullptr, who);

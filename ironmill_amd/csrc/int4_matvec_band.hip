@@ -70,7 +70,7 @@ __host__ __device__ inline BandLds band_lds(int G, int BM, int NMAT, int TM, int
 }
 
 // grid NWG; block 64 * NMAT * W.
-template <int NMAT, int EPI, int TM, int NP, int BM, int XC, bool RN, int PD = 1>
+template <int NMAT, int EPI, int TM, int NP, int BM, int XC, bool RN, bool IMG = false, int PD = 1>
 __global__ void __launch_bounds__(512) int4_band_kernel(MatPtrs mp, const ActIn in, int N, int K, int B, int W) {
     const __half *__restrict__ x = in.a;
     const __half *__restrict__ awq = in.awq;
@@ -109,10 +109,20 @@ __global__ void __launch_bounds__(512) int4_band_kernel(MatPtrs mp, const ActIn 
         __builtin_amdgcn_make_buffer_rsrc((void *)awq, 0, awq ? K * 2 : 0, kRsrcWord3);
     u32x4_t xv[XC][BM], wv[XC];
     u32x4_t bv[RN ? XC : 1][BM], gv[RN ? XC : 1];   // RN: b rows and gamma
+    u32x4_t lv[IMG ? XC : 1][BM];                    // IMG: the lo halves (xv: hi)
 #pragma unroll
     for (int i = 0; i < XC; i++) {
         const int c = min(i * nthr + tid, nchunks - 1);
         const size_t e = (size_t)c * 8;
+        if constexpr (IMG) {
+#pragma unroll
+            for (int b = 0; b < BM; b++) {
+                const size_t o = (size_t)min(b, B - 1) * K + e;
+                xv[i][b] = *reinterpret_cast<const u32x4_t *>(in.hi + o);
+                lv[i][b] = *reinterpret_cast<const u32x4_t *>(in.lo + o);
+            }
+            continue;
+        }
 #pragma unroll
         for (int b = 0; b < BM; b++) xv[i][b] = *reinterpret_cast<const u32x4_t *>(x + (size_t)min(b, B - 1) * K + e);
         if (RN) {
@@ -229,6 +239,13 @@ __global__ void __launch_bounds__(512) int4_band_kernel(MatPtrs mp, const ActIn 
 #pragma unroll
         for (int b = 0; b < BM; b++) {
             const _Float16 *xh = reinterpret_cast<const _Float16 *>(&xv[i][b]);
+            half8_t hi, lo;
+            float sh, sl;
+            if constexpr (IMG) {
+                hi = __builtin_bit_cast(half8_t, xv[i][b]);
+                lo = __builtin_bit_cast(half8_t, lv[i][b]);
+                chunk_sums(hi, lo, sh, sl);
+            } else {
             float v[8];
             if (RN) {
                 const _Float16 *bh = reinterpret_cast<const _Float16 *>(&bv[i][b]);
@@ -254,9 +271,8 @@ __global__ void __launch_bounds__(512) int4_band_kernel(MatPtrs mp, const ActIn 
 #pragma unroll
                 for (int e = 0; e < 8; e++) v[e] = div_awq(v[e], (float)wh[e]);
             }
-            half8_t hi, lo;
-            float sh, sl;
             chunk_operands(v, hi, lo, sh, sl);
+            }
             _Float16 *dst = img + ((size_t)(g * 2) * BM + b) * kRS + (c & 15) * 8;
             if (live) {
                 *reinterpret_cast<half8_t *>(dst) = hi;
@@ -358,12 +374,9 @@ __global__ void __launch_bounds__(512) int4_band_kernel(MatPtrs mp, const ActIn 
         }
     }
     __syncthreads();
-    for (int o = tid; o < RT * BM; o += nthr) {
-        const int r = o % RT, b = o / RT;
-        const int row = rb + r;
-        if (r >= nrows || b >= B) continue;
+    // the row's sums over the waves' parts (in part order), per matrix
+    auto row_sums = [&](int r, int b, float *sum) __attribute__((always_inline)) {
         const int t = r >> 3, rl = r & 7;
-        float sum[NMAT];
 #pragma unroll
         for (int mt = 0; mt < NMAT; mt++) {
             float s = 0.0f;
@@ -372,20 +385,57 @@ __global__ void __launch_bounds__(512) int4_band_kernel(MatPtrs mp, const ActIn 
             if (RN && !rnd) s *= BM <= 2 ? (b == 0 ? ri[0] : ri[BM - 1]) : rinv[b];
             sum[mt] = s;
         }
-        if (EPI == EPI_SILU || EPI == EPI_GELU) {
-            const float g = sum[0], u = sum[NMAT - 1];
-            float act;
-            if (EPI == EPI_SILU) {
-                act = g / (1.0f + __expf(-g));
-            } else {
-                float inner = 0.7978845608f * (g + 0.044715f * g * g * g);
-                inner = fminf(fmaxf(inner, -10.0f), 10.0f);
-                act = 0.5f * g * (1.0f + tanhf(inner));
-            }
-            mp.out[0][(size_t)b * N + row] = __float2half(act * u);
-        } else {
+    };
+    if constexpr (EPI == EPI_SILU || EPI == EPI_GELU) {
+        // rows in pairs (r, r + 1): with img_out, the pair is also the element
+        // pair (v[2i], v[2i + 1]) of the next projection's operand image (the
+        // host guarantees even band starts and lengths then)
+        for (int o = tid; o < (RT / 2) * BM; o += nthr) {
+            const int r = 2 * (o % (RT / 2)), b = o / (RT / 2);
+            if (r >= nrows || b >= B) continue;
+            __half h[2];
 #pragma unroll
-            for (int mt = 0; mt < NMAT; mt++) mp.out[mt][(size_t)b * N + row] = __float2half(sum[mt]);
+            for (int e = 0; e < 2; e++) {
+                if (r + e >= nrows) continue;
+                float sum[NMAT];
+                row_sums(r + e, b, sum);
+                const float g = sum[0], u = sum[NMAT - 1];
+                float act;
+                if (EPI == EPI_SILU) {
+                    act = g / (1.0f + __expf(-g));
+                } else {
+                    float inner = 0.7978845608f * (g + 0.044715f * g * g * g);
+                    inner = fminf(fmaxf(inner, -10.0f), 10.0f);
+                    act = 0.5f * g * (1.0f + tanhf(inner));
+                }
+                h[e] = __float2half(act * u);
+                mp.out[0][(size_t)b * N + rb + r + e] = h[e];
+            }
+            if (in.img_out_hi) {
+                const int k = rb + r;   // even
+                float v0 = __half2float(h[0]), v1 = __half2float(h[1]);
+                if (in.img_awq) {
+                    v0 = div_awq(v0, __half2float(in.img_awq[k]));
+                    v1 = div_awq(v1, __half2float(in.img_awq[k + 1]));
+                }
+                _Float16 ah, al, ch, cl;
+                pair_operands(v0, v1, ah, al, ch, cl);
+                const size_t base = (size_t)b * N + (k & ~7);
+                const int i = (k & 7) >> 1;
+                in.img_out_hi[base + i] = ah;
+                in.img_out_hi[base + 4 + i] = ch;
+                in.img_out_lo[base + i] = al;
+                in.img_out_lo[base + 4 + i] = cl;
+            }
+        }
+    } else {
+        for (int o = tid; o < RT * BM; o += nthr) {
+            const int r = o % RT, b = o / RT;
+            if (r >= nrows || b >= B) continue;
+            float sum[NMAT];
+            row_sums(r, b, sum);
+#pragma unroll
+            for (int mt = 0; mt < NMAT; mt++) mp.out[mt][(size_t)b * N + rb + r] = __float2half(sum[mt]);
         }
     }
 }
@@ -406,40 +456,40 @@ bool allow_lds(F kernel, size_t lds) {
                                (int)lds) == hipSuccess;
 }
 
-template <int NMAT, int EPI, int TM, int NP, int BM, bool RN>
+template <int NMAT, int EPI, int TM, int NP, int BM, bool RN, bool IMG>
 bool launch_xc(int xc, const BandLaunch &L, const MatPtrs &mp, const ActIn &in) {
     if (xc == 1) {
-        if (!allow_lds(int4_band_kernel<NMAT, EPI, TM, NP, BM, 1, RN>, L.lds)) return false;
-        hipLaunchKernelGGL((int4_band_kernel<NMAT, EPI, TM, NP, BM, 1, RN>), L.grid, L.block, L.lds, L.st, mp, in, L.N,
-                           L.K, L.B, L.W);
+        if (!allow_lds(int4_band_kernel<NMAT, EPI, TM, NP, BM, 1, RN, IMG>, L.lds)) return false;
+        hipLaunchKernelGGL((int4_band_kernel<NMAT, EPI, TM, NP, BM, 1, RN, IMG>), L.grid, L.block, L.lds, L.st, mp, in,
+                           L.N, L.K, L.B, L.W);
     } else if (BM <= 2) {   // three activation chunks per thread: 1-2 batch rows only
-        if (!allow_lds(int4_band_kernel<NMAT, EPI, TM, NP, BM, BM <= 2 ? 3 : 1, RN>, L.lds)) return false;
-        hipLaunchKernelGGL((int4_band_kernel<NMAT, EPI, TM, NP, BM, BM <= 2 ? 3 : 1, RN>), L.grid, L.block, L.lds,
-                           L.st, mp, in, L.N, L.K, L.B, L.W);
+        if (!allow_lds(int4_band_kernel<NMAT, EPI, TM, NP, BM, BM <= 2 ? 3 : 1, RN, IMG>, L.lds)) return false;
+        hipLaunchKernelGGL((int4_band_kernel<NMAT, EPI, TM, NP, BM, BM <= 2 ? 3 : 1, RN, IMG>), L.grid, L.block,
+                           L.lds, L.st, mp, in, L.N, L.K, L.B, L.W);
     }
     return true;
 }
 
 // batch rows per instantiation: 1, 2, 4 (3-4 rows) and 8 (5-8 rows; plain
-// sources only)
-template <int NMAT, int EPI, int TM, int NP, bool RN>
+// sources only); an image source at 1-2 rows
+template <int NMAT, int EPI, int TM, int NP, bool RN, bool IMG>
 bool launch_bm(int bm, int xc, const BandLaunch &L, const MatPtrs &mp, const ActIn &in) {
-    if (bm == 1) return launch_xc<NMAT, EPI, TM, NP, 1, RN>(xc, L, mp, in);
-    if (bm == 2) return launch_xc<NMAT, EPI, TM, NP, 2, RN>(xc, L, mp, in);
-    if constexpr (!RN) {
-        if (bm == 4) return launch_xc<NMAT, EPI, TM, NP, 4, RN>(xc, L, mp, in);
-        return launch_xc<NMAT, EPI, TM, NP, 8, RN>(xc, L, mp, in);
+    if (bm == 1) return launch_xc<NMAT, EPI, TM, NP, 1, RN, IMG>(xc, L, mp, in);
+    if (bm == 2) return launch_xc<NMAT, EPI, TM, NP, 2, RN, IMG>(xc, L, mp, in);
+    if constexpr (!RN && !IMG) {
+        if (bm == 4) return launch_xc<NMAT, EPI, TM, NP, 4, RN, IMG>(xc, L, mp, in);
+        return launch_xc<NMAT, EPI, TM, NP, 8, RN, IMG>(xc, L, mp, in);
     }
     return false;
 }
 
 // (TM, NP) instantiated: (2, 5), (3, 5) and (5, 3); the host picks the
 // smallest TM that holds the band.
-template <int NMAT, int EPI, bool RN>
+template <int NMAT, int EPI, bool RN, bool IMG = false>
 bool launch_shape(int tm, int bm, int xc, const BandLaunch &L, const MatPtrs &mp, const ActIn &in) {
-    if (tm <= 2) return launch_bm<NMAT, EPI, 2, 5, RN>(bm, xc, L, mp, in);
-    if (tm <= 3) return launch_bm<NMAT, EPI, 3, 5, RN>(bm, xc, L, mp, in);
-    return launch_bm<NMAT, EPI, 5, 3, RN>(bm, xc, L, mp, in);
+    if (tm <= 2) return launch_bm<NMAT, EPI, 2, 5, RN, IMG>(bm, xc, L, mp, in);
+    if (tm <= 3) return launch_bm<NMAT, EPI, 3, 5, RN, IMG>(bm, xc, L, mp, in);
+    return launch_bm<NMAT, EPI, 5, 3, RN, IMG>(bm, xc, L, mp, in);
 }
 
 }  // namespace
@@ -447,7 +497,9 @@ bool launch_shape(int tm, int bm, int xc, const BandLaunch &L, const MatPtrs &mp
 // Launches the band kernel when it applies (B <= 8, no row segments, an even
 // number of groups, the shape within the instantiated tiles and the LDS
 // budget -- 64 KB for 1-2 batch rows, 160 KB with one activation chunk per
-// thread above; a residual-norm source only at 1-2 batch rows, with
+// thread above; an operand image source (in.img_src) or output
+// (in.img_out_hi, every band on even rows) at 1-2 batch rows only; a
+// residual-norm source only at 1-2 batch rows, with
 // round_mode 0 or 1, as nmat 1 with EPI_STORE or nmat 2 with an activation);
 // *used reports whether it did.  probe: only whether it would apply.
 int launch_band_matvec(hipStream_t st, int cus, int B, int nmat, int epi, int N, int K, const MatPtrs &mp,
@@ -457,6 +509,10 @@ int launch_band_matvec(hipStream_t st, int cus, int B, int nmat, int epi, int N,
     const int G = K / kGS;
     if (B < 1 || B > 8 || mp.seg[0] != 0 || G % 2 || G < 2) return IMH_OK;
     const int bm = B <= 2 ? B : B <= 4 ? 4 : 8;
+    // an image source: one matrix, no norm, 1-2 rows; an image output: a
+    // gate/up pair with an activation, 1-2 rows
+    if (in.img_src && (rn || nmat != 1 || epi != EPI_STORE || bm > 2 || !in.hi || !in.lo)) return IMH_OK;
+    if (in.img_out_hi && (nmat != 2 || epi == EPI_STORE || bm > 2 || !in.img_out_lo)) return IMH_OK;
     // above two rows every workgroup would redo the whole residual + norm of
     // every row (measured slower than the rows kernel + the plain band)
     if (bm > 2 && rn) return IMH_OK;
@@ -471,6 +527,12 @@ int launch_band_matvec(hipStream_t st, int cus, int B, int nmat, int epi, int N,
     const int rows = (N + nwg - 1) / nwg;
     const int tm = (rows + 7) / 8;
     if (tm > 5) return IMH_OK;
+    if (in.img_out_hi) {
+        // the epilogue writes element pairs: every band must start on an even row
+        // and hold an even number of rows
+        for (int b = 0; b <= nwg; b++)
+            if ((int)(((uint32_t)N * (uint32_t)b) / (uint32_t)nwg) % 2) return IMH_OK;
+    }
     const int TM = tm <= 2 ? 2 : tm <= 3 ? 3 : 5, NPmax = tm <= 3 ? 5 : 3;
     // waves per matrix: as few as keep each wave within NPmax pairs (1-2
     // rows); all eight above, so one activation chunk per thread covers K
@@ -488,7 +550,9 @@ int launch_band_matvec(hipStream_t st, int cus, int B, int nmat, int epi, int N,
     }
     BandLaunch L{dim3(nwg), dim3(nthr), lds, st, N, K, B, W};
     bool ok;
-    if (rn) {
+    if (in.img_src) {
+        ok = launch_shape<1, EPI_STORE, false, true>(tm, bm, xc, L, mp, in);
+    } else if (rn) {
         if (nmat == 1)
             ok = launch_shape<1, EPI_STORE, true>(tm, bm, xc, L, mp, in);
         else if (epi == EPI_SILU)

@@ -112,6 +112,15 @@ struct ActIn {
     const _Float16 *hi2;
     const _Float16 *lo2;
     const float *gsum2;
+    // Row-band kernel only.  img_out_hi / img_out_lo (gate/up pair with an
+    // activation): also write the activation, divided by img_awq (NULL: not
+    // divided), as the operand image [B][N] of the projection that reads it
+    // (the down projection of an FFN block).  img_src: hi / lo hold such an
+    // image and gsum is NULL -- the kernel sums the groups itself.
+    _Float16 *img_out_hi;
+    _Float16 *img_out_lo;
+    const __half *img_awq;
+    int img_src;
 };
 
 // Split v into f16 hi + lo with hi + lo == v to ~22 bits.
@@ -125,24 +134,39 @@ __device__ __forceinline__ void split_hilo(float v, _Float16 &hi, _Float16 &lo) 
 // hi/lo halves.  sh / sl get the chunk's share of the group sums: the codes
 // q == z everywhere give sum_i a_i (z + 16 z) + c_i (16 z), so the sum that the
 // zero point multiplies is sum_i 17 a_i + 16 c_i, per half.
-__device__ __forceinline__ void chunk_operands(const float v[8], half8_t &hi, half8_t &lo, float &sh,
-                                               float &sl) {
+// Elements (v0, v1) = (v[2i], v[2i + 1]) -> slots i (a) and 4 + i (c).
+__device__ __forceinline__ void pair_operands(float v0, float v1, _Float16 &ah, _Float16 &al, _Float16 &ch,
+                                              _Float16 &cl) {
+    const float c = v1 * 0.0625f - v0;
+    split_hilo(v0, ah, al);
+    split_hilo(c, ch, cl);
+}
+
+// The chunk's share of the group sums, from its operand halves (one order
+// for every kernel that forms them: the image writers and the kernels that
+// read an image without sums).
+__device__ __forceinline__ void chunk_sums(const half8_t &hi, const half8_t &lo, float &sh, float &sl) {
     sh = 0.0f;
     sl = 0.0f;
 #pragma unroll
     for (int i = 0; i < 4; i++) {
-        const float a = v[2 * i];
-        const float c = v[2 * i + 1] * 0.0625f - a;
+        sh = sh + __builtin_fmaf(17.0f, (float)hi[i], 16.0f * (float)hi[4 + i]);
+        sl = sl + __builtin_fmaf(17.0f, (float)lo[i], 16.0f * (float)lo[4 + i]);
+    }
+}
+
+__device__ __forceinline__ void chunk_operands(const float v[8], half8_t &hi, half8_t &lo, float &sh,
+                                               float &sl) {
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
         _Float16 ah, al, ch, cl;
-        split_hilo(a, ah, al);
-        split_hilo(c, ch, cl);
+        pair_operands(v[2 * i], v[2 * i + 1], ah, al, ch, cl);
         hi[i] = ah;
         lo[i] = al;
         hi[4 + i] = ch;
         lo[4 + i] = cl;
-        sh += 17.0f * (float)ah + 16.0f * (float)ch;
-        sl += 17.0f * (float)al + 16.0f * (float)cl;
     }
+    chunk_sums(hi, lo, sh, sl);
 }
 
 using imh_dpp::row16_sum;
