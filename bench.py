@@ -8,7 +8,9 @@ Workload of the headline number: the Qwen3-4B decode
 FFN block at batch 1 -- fused gate+up 2560 -> 2 x 9728 with SiLU, then down
 9728 -> 2560, INT4 group-128 weights from N(0, 0.02), AWQ scales U[0.5, 2],
 fp16 activations N(0,1) with 1 % of channels x20.  A step is one such FFN block
-through the public ops (one kernel launch each).  The weights are replicated over >= 512 MB of distinct buffers and the steps
+through the public FFN-block op imh_encode_ffn_block_int4 (encode_ffn_block):
+two kernel launches, the gate/up one also writing the down projection's
+operand image.  The weights are replicated over >= 512 MB of distinct buffers and the steps
 rotate through them, so the MI355X's 256 MB Infinity Cache cannot serve them.
 
 Bytes are counted as in the reference's kernel_bandwidth_bench
@@ -610,8 +612,7 @@ def main():
     # ---- the step: FFN block through the public ops ----
     def ffn_step(i):
         g, u, d = W[i % reps]
-        ops.encode_fused_ffn_gate_up_act_int4(stream, x, g, u, act, B)
-        ops.encode_projection(stream, act, d, y, B)
+        ops.encode_ffn_block_int4(stream, x, g, u, d, act, y, B)
 
     total_ms = time_loop(dev, stream, ffn_step, args.steps, args.warmup)
     ms = total_ms / args.steps
