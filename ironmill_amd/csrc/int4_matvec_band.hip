@@ -387,18 +387,18 @@ __global__ void __launch_bounds__(512) int4_band_kernel(MatPtrs mp, const ActIn 
         }
     };
     if constexpr (EPI == EPI_SILU || EPI == EPI_GELU) {
-        // rows in pairs (r, r + 1): with img_out, the pair is also the element
-        // pair (v[2i], v[2i + 1]) of the next projection's operand image (the
-        // host guarantees even band starts and lengths then)
-        for (int o = tid; o < (RT / 2) * BM; o += nthr) {
-            const int r = 2 * (o % (RT / 2)), b = o / (RT / 2);
-            if (r >= nrows || b >= B) continue;
-            __half h[2];
-#pragma unroll
-            for (int e = 0; e < 2; e++) {
-                if (r + e >= nrows) continue;
+        // with img_out the row pair (r, r + 1) is also the element pair
+        // (v[2i], v[2i + 1]) of the next projection's operand image: the two
+        // rows sit in adjacent lanes (the host guarantees even band starts and
+        // lengths), so the even lane takes its neighbour's value by a shuffle
+        for (int o0 = 0; o0 < RT * BM; o0 += nthr) {
+            const int o = o0 + tid;
+            const int r = o % RT, b = o / RT;
+            const bool live = o < RT * BM && r < nrows && b < B;
+            float v = 0.0f;
+            if (live) {
                 float sum[NMAT];
-                row_sums(r + e, b, sum);
+                row_sums(r, b, sum);
                 const float g = sum[0], u = sum[NMAT - 1];
                 float act;
                 if (EPI == EPI_SILU) {
@@ -408,24 +408,24 @@ __global__ void __launch_bounds__(512) int4_band_kernel(MatPtrs mp, const ActIn 
                     inner = fminf(fmaxf(inner, -10.0f), 10.0f);
                     act = 0.5f * g * (1.0f + tanhf(inner));
                 }
-                h[e] = __float2half(act * u);
-                mp.out[0][(size_t)b * N + rb + r + e] = h[e];
+                const __half h = __float2half(act * u);
+                mp.out[0][(size_t)b * N + rb + r] = h;
+                v = __half2float(h);
+                if (in.img_out_hi && in.img_awq) v = div_awq(v, __half2float(in.img_awq[rb + r]));
             }
-            if (in.img_out_hi) {
-                const int k = rb + r;   // even
-                float v0 = __half2float(h[0]), v1 = __half2float(h[1]);
-                if (in.img_awq) {
-                    v0 = div_awq(v0, __half2float(in.img_awq[k]));
-                    v1 = div_awq(v1, __half2float(in.img_awq[k + 1]));
+            if (in.img_out_hi) {   // uniform
+                const float v1 = __shfl_xor(v, 1);
+                if (live && (r & 1) == 0) {
+                    const int k = rb + r;
+                    _Float16 ah, al, ch, cl;
+                    pair_operands(v, v1, ah, al, ch, cl);
+                    const size_t base = (size_t)b * N + (k & ~7);
+                    const int i = (k & 7) >> 1;
+                    in.img_out_hi[base + i] = ah;
+                    in.img_out_hi[base + 4 + i] = ch;
+                    in.img_out_lo[base + i] = al;
+                    in.img_out_lo[base + 4 + i] = cl;
                 }
-                _Float16 ah, al, ch, cl;
-                pair_operands(v0, v1, ah, al, ch, cl);
-                const size_t base = (size_t)b * N + (k & ~7);
-                const int i = (k & 7) >> 1;
-                in.img_out_hi[base + i] = ah;
-                in.img_out_hi[base + 4 + i] = ch;
-                in.img_out_lo[base + i] = al;
-                in.img_out_lo[base + 4 + i] = cl;
             }
         }
     } else {
