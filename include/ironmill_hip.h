@@ -170,8 +170,10 @@ int imh_encode_fused_ffn_gate_up_act_int4(imh_stream *stream, const uint16_t *x,
 /* encode_ffn_block (metal/ffn.rs:13-144) for INT4 gate/up/down: act_out =
  * f16(act(x.Wg) * (x.Wu)) as imh_encode_fused_ffn_gate_up_act_int4 writes it
  * (act_out [token_count][gate->n]), then y = act_out . Wd^T with down's
- * awq_scales (y [token_count][down->n]), as the two ops (matvec below 32
- * tokens, GEMM from 32).  down->k must equal gate->n. */
+ * awq_scales (y [token_count][down->n]), with the two ops' results (matvec
+ * below 32 tokens, GEMM from 32; at 1-2 tokens the gate/up launch also hands
+ * the down launch its operand image through the stream's scratch).  down->k
+ * must equal gate->n. */
 int imh_encode_ffn_block_int4(imh_stream *stream, const uint16_t *x, uint32_t token_count,
                               const imh_affine_int4_weight *gate, const imh_affine_int4_weight *up,
                               const imh_affine_int4_weight *down, uint16_t *act_out, uint16_t *y,
