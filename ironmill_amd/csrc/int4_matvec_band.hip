@@ -70,7 +70,7 @@ __host__ __device__ inline BandLds band_lds(int G, int BM, int NMAT, int TM, int
 }
 
 // grid NWG; block 64 * NMAT * W.
-template <int NMAT, int EPI, int TM, int NP, int BM, int XC, bool RN, bool IMG = false, int PD = 1>
+template <int NMAT, int EPI, int TM, int NP, int BM, int XC, bool RN, bool IMG = false, int PD = 1, bool MB = false>
 __global__ void __launch_bounds__(512) int4_band_kernel(MatPtrs mp, const ActIn in, int N, int K, int B, int W) {
     const __half *__restrict__ x = in.a;
     const __half *__restrict__ awq = in.awq;
@@ -84,10 +84,14 @@ __global__ void __launch_bounds__(512) int4_band_kernel(MatPtrs mp, const ActIn 
     const int p0 = (part * P) / W;
     const int np = ((part + 1) * P) / W - p0;
     // (the host keeps N * NWG below 2^32)
-    const int rb = (int)(((uint32_t)N * blockIdx.x) / gridDim.x);
-    const int re = (int)(((uint32_t)N * (blockIdx.x + 1)) / gridDim.x);
-    const int nrows = re - rb;
+    const int RB = (int)(((uint32_t)N * blockIdx.x) / gridDim.x);
+    const int RE = (int)(((uint32_t)N * (blockIdx.x + 1)) / gridDim.x);
     const int RT = TM * 8;                     // band rows held in LDS (padded)
+    // MB: the band [RB, RE) in blocks of RT rows, one after the other over the
+    // operand image staged once (tall matrices at 3-8 rows); else one block
+    const int nblk = MB ? (RE - RB + RT - 1) / RT : 1;
+    int rb = RB;
+    int nrows = MB ? min(RT, RE - RB) : RE - RB;
 
     const BandLds L = band_lds(G, BM, NMAT, TM, waves, RN);
     _Float16 *img = reinterpret_cast<_Float16 *>(lds_b + L.img);
@@ -133,18 +137,21 @@ __global__ void __launch_bounds__(512) int4_band_kernel(MatPtrs mp, const ActIn 
         }
         wv[i] = __builtin_bit_cast(u32x4_t, __builtin_amdgcn_raw_buffer_load_b128(awq_r, (int)(e * 2), 0, 0));
     }
-    // (b) scale / zero words of the band: word w of matrix m covers groups
-    // 2p, 2p + 1 of band row w / P (the band's rows are contiguous)
-    const int szw = nrows * P;
+    // (b) scale / zero words of the block: word w of matrix m covers groups
+    // 2p, 2p + 1 of block row w / P (the block's rows are contiguous)
+    int szw = nrows * P;
     uint32_t sv[kSZC], zv[kSZC];
+    auto load_sz = [&](int rb_, int szw_) __attribute__((always_inline)) {
 #pragma unroll
-    for (int i = 0; i < kSZC; i++) {
-        const int w = min(i * nthr + tid, NMAT * szw - 1);
-        const int m = (NMAT == 2 && w >= szw) ? 1 : 0;
-        const size_t src = (size_t)rb * P + (w - m * szw);
-        sv[i] = reinterpret_cast<const uint32_t *>(m ? mp.scales[1] : mp.scales[0])[src];
-        zv[i] = reinterpret_cast<const uint32_t *>(m ? mp.zeros[1] : mp.zeros[0])[src];
-    }
+        for (int i = 0; i < kSZC; i++) {
+            const int w = min(i * nthr + tid, NMAT * szw_ - 1);
+            const int m = (NMAT == 2 && w >= szw_) ? 1 : 0;
+            const size_t src = (size_t)rb_ * P + (w - m * szw_);
+            sv[i] = reinterpret_cast<const uint32_t *>(m ? mp.scales[1] : mp.scales[0])[src];
+            zv[i] = reinterpret_cast<const uint32_t *>(m ? mp.zeros[1] : mp.zeros[0])[src];
+        }
+    };
+    load_sz(rb, szw);
     // issue order: every wave's small loads ahead of any weight load in the
     // CU's memory pipeline, which returns them in order (an execution barrier
     // only: nothing waits for the loads here)
@@ -160,15 +167,18 @@ __global__ void __launch_bounds__(512) int4_band_kernel(MatPtrs mp, const ActIn 
     // the MFMAs run while the rest streams in (a wave whose next load cannot
     // issue waits there, in order).
     const __amdgpu_buffer_rsrc_t w_r = __builtin_amdgcn_make_buffer_rsrc(
-        (void *)(wdata + (size_t)rb * (K / 2)), 0, nrows * (K / 2), kRsrcWord3);
+        (void *)(wdata + (size_t)RB * (K / 2)), 0, (RE - RB) * (K / 2), kRsrcWord3);
     const int woff = jr * (K / 2) + jh * 64 + kq * 16;
     u32x4_t wq[TM][NP];
-    auto load_pair = [&](int i) __attribute__((always_inline)) {
+    // pair i of the block at row offset bo (from RB) into slot i
+    auto load_pair_at = [&](int bo, int i) __attribute__((always_inline)) {
 #pragma unroll
         for (int t = 0; t < TM; t++)
-            wq[t][i] = __builtin_bit_cast(u32x4_t, __builtin_amdgcn_raw_buffer_load_b128(
-                                                       w_r, woff + t * 8 * (K / 2) + (p0 + min(i, np - 1)) * 128, 0, 0));
+            wq[t][i] = __builtin_bit_cast(
+                u32x4_t, __builtin_amdgcn_raw_buffer_load_b128(
+                             w_r, woff + (bo + t * 8) * (K / 2) + (p0 + min(i, np - 1)) * 128, 0, 0));
     };
+    auto load_pair = [&](int i) __attribute__((always_inline)) { load_pair_at(rb - RB, i); };
 #pragma unroll
     for (int i = 0; i < PD && i < NP; i++) load_pair(i);
 
@@ -299,6 +309,17 @@ __global__ void __launch_bounds__(512) int4_band_kernel(MatPtrs mp, const ActIn 
     const int ah = ai >> 3, aplane = (ai >> 2) & 1, ab = ai & 3;
     const bool a_live = ab < BMH;
     const int dplane = (lane >> 4) & 1;
+    for (int blk = 0; blk < nblk; blk++) {
+    if (MB && blk > 0) {
+        // the previous block's MFMAs are done with szs and its epilogue with
+        // red (the barrier before that epilogue, and this one): this block's
+        // scale / zero words in
+#pragma unroll
+        for (int i = 0; i < kSZC; i++) sz_store(min(i * nthr + tid, NMAT * szw - 1), sv[i], zv[i]);
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
+        __builtin_amdgcn_s_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+    }
     const int ntile = (nrows + 7) >> 3;
     float acc[TM][BM];
 #pragma unroll
@@ -354,6 +375,12 @@ __global__ void __launch_bounds__(512) int4_band_kernel(MatPtrs mp, const ActIn 
                     }
                 }
             }
+        }
+        if constexpr (MB) {
+            // the next block's first pairs into the slots this one is done
+            // with, and its scale / zero words into registers
+            if (blk + 1 < nblk && i + PD >= NP) load_pair_at(rb + RT - RB, i + PD - NP);
+            if (blk + 1 < nblk && i == 0) load_sz(rb + RT, min(RT, RE - rb - RT) * P);
         }
     }
     // (h) rows r = lane & 7 of each tile sit at lanes r (h 0, hi), r + 16
@@ -438,6 +465,12 @@ __global__ void __launch_bounds__(512) int4_band_kernel(MatPtrs mp, const ActIn 
             for (int mt = 0; mt < NMAT; mt++) mp.out[mt][(size_t)b * N + rb + r] = __float2half(sum[mt]);
         }
     }
+    if constexpr (MB) {
+        rb += RT;
+        nrows = min(RT, RE - rb);
+        szw = nrows * P;
+    }
+    }   // blocks
 }
 
 struct BandLaunch {
@@ -483,6 +516,16 @@ bool launch_bm(int bm, int xc, const BandLaunch &L, const MatPtrs &mp, const Act
     return false;
 }
 
+// Tall matrices at 3-8 rows: 5-tile blocks, two pairs per wave, both issued
+// ahead (and the next block's two while the last ones compute).
+template <int BM>
+bool launch_mb(const BandLaunch &L, const MatPtrs &mp, const ActIn &in) {
+    if (!allow_lds(int4_band_kernel<1, EPI_STORE, 5, 2, BM, 1, false, false, 2, true>, L.lds)) return false;
+    hipLaunchKernelGGL((int4_band_kernel<1, EPI_STORE, 5, 2, BM, 1, false, false, 2, true>), L.grid, L.block, L.lds,
+                       L.st, mp, in, L.N, L.K, L.B, L.W);
+    return true;
+}
+
 // (TM, NP) instantiated: (2, 5), (3, 5) and (5, 3); the host picks the
 // smallest TM that holds the band.
 template <int NMAT, int EPI, bool RN, bool IMG = false>
@@ -521,10 +564,14 @@ int launch_band_matvec(hipStream_t st, int cus, int B, int nmat, int epi, int N,
         if ((reinterpret_cast<uintptr_t>(mp.scales[i]) | reinterpret_cast<uintptr_t>(mp.zeros[i])) & 3) return IMH_OK;
     const int P = G / 2;
     const int ntiles = (N + 7) / 8;
-    // workgroups: one band per CU, more (bands of up to 5 tiles) for tall matrices
-    const int nwg = std::min(std::max(cus, (ntiles + 4) / 5), N);
+    // workgroups: one band per CU, more (bands of up to 5 tiles) for tall
+    // matrices -- except at 3-8 rows (one plain-source matrix), where every
+    // workgroup would stage the operand image of all of K for 40 rows: there
+    // one band per CU, walked in blocks of 5 tiles over one staging (mb)
+    const bool mb = bm > 2 && !rn && !in.img_src && nmat == 1 && epi == EPI_STORE && (ntiles + 4) / 5 > cus;
+    const int nwg = mb ? cus : std::min(std::max(cus, (ntiles + 4) / 5), N);
     if ((uint64_t)N * nwg >= (1ull << 32)) return IMH_OK;
-    const int rows = (N + nwg - 1) / nwg;
+    const int rows = mb ? 40 : (N + nwg - 1) / nwg;   // mb: rows per block
     const int tm = (rows + 7) / 8;
     if (tm > 5) return IMH_OK;
     if (in.img_out_hi) {
@@ -533,7 +580,7 @@ int launch_band_matvec(hipStream_t st, int cus, int B, int nmat, int epi, int N,
         for (int b = 0; b <= nwg; b++)
             if ((int)(((uint32_t)N * (uint32_t)b) / (uint32_t)nwg) % 2) return IMH_OK;
     }
-    const int TM = tm <= 2 ? 2 : tm <= 3 ? 3 : 5, NPmax = tm <= 3 ? 5 : 3;
+    const int TM = tm <= 2 ? 2 : tm <= 3 ? 3 : 5, NPmax = mb ? 2 : tm <= 3 ? 5 : 3;
     // waves per matrix: as few as keep each wave within NPmax pairs (1-2
     // rows); all eight above, so one activation chunk per thread covers K
     const int W = bm > 2 ? std::min(8 / nmat, P) : std::min((P + NPmax - 1) / NPmax, 8 / nmat);
@@ -550,7 +597,9 @@ int launch_band_matvec(hipStream_t st, int cus, int B, int nmat, int epi, int N,
     }
     BandLaunch L{dim3(nwg), dim3(nthr), lds, st, N, K, B, W};
     bool ok;
-    if (in.img_src) {
+    if (mb) {
+        ok = bm == 4 ? launch_mb<4>(L, mp, in) : launch_mb<8>(L, mp, in);
+    } else if (in.img_src) {
         ok = launch_shape<1, EPI_STORE, false, true>(tm, bm, xc, L, mp, in);
     } else if (rn) {
         if (nmat == 1)

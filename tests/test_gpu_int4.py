@@ -74,6 +74,11 @@ def gpu_layout_y(q, x16, awq16=None):
     (1024, 2560, 2, False),   # Qwen3-4B K / V projection, batch 2
     (5000, 1024, 1, True),    # bands of 17-24 rows
     (151936 // 8, 2560, 1, False),   # an LM-head-like tall matrix (bands of 5 tiles)
+    (151936 // 8, 2560, 4, True),    # 3-8 rows on a tall matrix: one band per CU in 5-tile blocks
+    (151936 // 8, 2560, 8, False),
+    (15003, 2560, 5, True),          # the same with a ragged last block
+    (12000, 1024, 8, True),          # one group pair per wave
+    (151936, 2560, 8, False),        # the Qwen3-4B LM head at 8 rows
 ])
 def test_projection_matches_oracle(dev, stream, n, k, batch, awq):
     w, s = make_weight(n, k, seed=n + k + batch, awq=awq)
