@@ -19,8 +19,9 @@
 //    value 128 + q exactly (one v_perm per two codes); the MFMA gives
 //    sum a (128 + q) and the group's correction subtracts (128 + z) sum a,
 //    with sum a the row's group sum of the rounded operand (exact products,
-//    f32 sums).  fp8: q is looked up as its e4m3 encoding (exact for 0..15)
-//    and the correction subtracts z sum a.  The correction is one more
+//    f32 sums).  fp8: the code byte itself, read as e4m3, is q * 2^-9 exactly
+//    (subnormals and the first binade), the matrix core's block scale 2^9
+//    restores q, and the correction subtracts z sum a.  The correction is one more
 //    matrix-core product per tile and group (the row sum split into three
 //    exact bf16 pieces against -c; the last of the group's bf16 products),
 //    so the fold of a group is one multiply-add.
@@ -65,18 +66,11 @@ constexpr float kE4M3Max = 448.0f;
 
 enum Prec : int { PREC_BF16 = 1, PREC_FP8 = 2 };
 
-// e4m3 encodings of 0..7 (OCP E4M3: bias 7, 1.0 = 0x38); 8..15 are 0x48 + q
-constexpr uint32_t kE4m3Lo = 0x44403800u;   // e(3) e(2) e(1) e(0)
-constexpr uint32_t kE4m3Hi = 0x4E4C4A48u;   // e(7) e(6) e(5) e(4)
-
-// four codes (0..15, one per byte) -> their e4m3 encodings
-__device__ __forceinline__ uint32_t e4m3_of_codes(uint32_t q) {
-    const uint32_t small = __builtin_amdgcn_perm(kE4m3Hi, kE4m3Lo, q & 0x07070707u);
-    const uint32_t big = q + 0x48484848u;
-    // per byte 0xFF where q >= 8: v_perm selector 12 gives 0x00, 13 gives 0xFF
-    const uint32_t mask = __builtin_amdgcn_perm(0u, 0u, ((q >> 3) & 0x01010101u) + 0x0C0C0C0Cu);
-    return (big & mask) | (small & ~mask);
-}
+// fp8 B operand: a code byte q (0..15) read as OCP E4M3 is q * 2^-9 exactly
+// (0..7 are the subnormals m * 2^-9, 8..15 the first binade 2^-6 (1 + m / 8));
+// the matrix core's E8M0 block scale 2^9 (exponent 127 + 9) restores q.
+constexpr uint32_t kScaleCodesE8m0 = 0x88888888u;
+constexpr uint32_t kScaleOneE8m0 = 0x7F7F7F7Fu;
 
 // grid (ceil(K / 8 / 256), M), block 256: chunk c (8 elements) of row m:
 // a = x / awq (no awq: x) rounded to the operand type, stored in slot order
@@ -350,12 +344,12 @@ __global__ void __launch_bounds__(kThreads, 2) gemm_mx_kernel(
                 i32x8_t bf[2];
 #pragma unroll
                 for (int t = 0; t < 2; t++)
-                    // code dword d = codes 8 d .. 8 d + 7 -> e4m3 of the even codes, then the odd
+                    // code dword d = codes 8 d .. 8 d + 7 -> the even codes' bytes, then the odd
 #pragma unroll
                     for (int d = 0; d < 4; d++) {
                         const uint32_t w = b.w[j][t][d];
-                        bf[t][2 * d] = (int)e4m3_of_codes(w & 0x0F0F0F0Fu);
-                        bf[t][2 * d + 1] = (int)e4m3_of_codes((w >> 4) & 0x0F0F0F0Fu);
+                        bf[t][2 * d] = (int)(w & 0x0F0F0F0Fu);
+                        bf[t][2 * d + 1] = (int)((w >> 4) & 0x0F0F0F0Fu);
                     }
                 const float sj = (float)__builtin_bit_cast(_Float16, b.s[j]);
 #pragma unroll
@@ -363,9 +357,9 @@ __global__ void __launch_bounds__(kThreads, 2) gemm_mx_kernel(
                     float16_t g = __builtin_amdgcn_mfma_f32_32x32x16_bf16(ca[mi], cb[j], zero16, 0, 0, 0);
 #pragma unroll
                     for (int t = 0; t < 2; t++)
-                        // formats 0 / 0: e4m3 x e4m3; scale exponents 127: x1
-                        g = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(af[mi][t], bf[t], g, 0, 0, 0, 0x7F7F7F7F, 0,
-                                                                            0x7F7F7F7F);
+                        // formats 0 / 0: e4m3 x e4m3; A scale x1, B scale x 2^9
+                        g = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(af[mi][t], bf[t], g, 0, 0, 0, kScaleOneE8m0,
+                                                                            0, kScaleCodesE8m0);
 #pragma unroll
                     for (int i = 0; i < 16; i++) acc[mi][j][i] = __builtin_fmaf(sj, g[i], acc[mi][j][i]);
                 }
