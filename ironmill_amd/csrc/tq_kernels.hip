@@ -26,6 +26,7 @@
 // (o, max, sum) and a second kernel merges the splits (log-sum-exp,
 // fused_sdpa_reduce, flash_decode.metal:163-215) and rotates back.
 #include <hip/hip_runtime.h>
+#include <type_traits>
 #include <hip/hip_fp16.h>
 
 #include <algorithm>
@@ -352,16 +353,58 @@ __device__ __forceinline__ void load_chunk(const ChunkRsrc &r, int p0, int n_l, 
 // (dims 32 g + 8 j .. + 7, k-slot order {0, 2, 1, 3} within each word): the
 // codebook entries' f16 hi and lo parts (one LDS lookup per byte) and the
 // +-1 QJL signs straight from bit 7.
-__device__ __forceinline__ void k_operands(const uint32_t *kw2, const uint32_t *ktab, half8_t &Bh, half8_t &Bl,
+// Codebook tables spread over the LDS banks (the lookups of 64 lanes with
+// random codes conflicted on ~55 % of the LDS's active cycles): row c of 256
+// bytes holds the K entry of code byte c in words 0..31 and the V entry in
+// words 32..63, and lane l reads copy l & 31, so the 32 lanes of a half-wave
+// hit 32 different banks whatever their codes.  The byte offset of code byte
+// k of w is one v_perm: (byte << 8) | lane offset (4 (l & 31), + 128 for V).
+constexpr int kTabRowBytes = 256;
+constexpr int kSpreadMinLen = 1024;   // positions per split from which the decode loop uses them
+constexpr int kTabBytes = 256 * kTabRowBytes;
+__device__ __forceinline__ uint32_t tab_read(const uint8_t *tabs, uint32_t w, int k, uint32_t lane_off) {
+    const uint32_t off = __builtin_amdgcn_perm(w, lane_off, 0x0C0C0000u | ((4u + (uint32_t)k) << 8));
+    return *reinterpret_cast<const uint32_t *>(tabs + off);
+}
+// tabs <- 32 copies of each entry of ktab / vtab (256 threads, wave w,
+// instruction i: rows 16 i + 4 w + (lane >> 4), 16 bytes per lane)
+__device__ __forceinline__ void spread_tables(uint8_t *tabs, const uint32_t *ktab, const uint32_t *vtab, int lane,
+                                              int wave) {
+    const int chunk = lane & 15;
+    const uint32_t *src = chunk < 8 ? ktab : vtab;
+#pragma unroll 4
+    for (int i = 0; i < 16; i++) {
+        const int r = 16 * i + 4 * wave + (lane >> 4);
+        const uint32_t v = src[r];
+        *reinterpret_cast<uint4 *>(tabs + r * kTabRowBytes + chunk * 16) = make_uint4(v, v, v, v);
+    }
+}
+
+// The loops' view of the tables: entries of code byte k of a word, K or V.
+// TabOne: the single 256-entry copies; TabSpread: the bank-spread copies.
+struct TabOne {
+    const uint32_t *kt, *vt;
+    __device__ __forceinline__ uint32_t k(uint32_t w, int b) const { return kt[(w >> (8 * b)) & 0xFF]; }
+    __device__ __forceinline__ uint32_t v(uint32_t w, int b) const { return vt[(w >> (8 * b)) & 0xFF]; }
+};
+struct TabSpread {
+    const uint8_t *t;
+    uint32_t lk, lv;
+    __device__ __forceinline__ uint32_t k(uint32_t w, int b) const { return tab_read(t, w, b, lk); }
+    __device__ __forceinline__ uint32_t v(uint32_t w, int b) const { return tab_read(t, w, b, lv); }
+};
+
+template <class Tab>
+__device__ __forceinline__ void k_operands(const uint32_t *kw2, const Tab &tab, half8_t &Bh, half8_t &Bl,
                                            half8_t &Bs) {
     uint32_t bh[4], bl[4], bs[4];
 #pragma unroll
     for (int hw = 0; hw < 2; hw++) {
         const uint32_t w = kw2[hw];
-        const uint32_t t0 = ktab[w & 0xFF];
-        const uint32_t t1 = ktab[(w >> 8) & 0xFF];
-        const uint32_t t2 = ktab[(w >> 16) & 0xFF];
-        const uint32_t t3 = ktab[w >> 24];
+        const uint32_t t0 = tab.k(w, 0);
+        const uint32_t t1 = tab.k(w, 1);
+        const uint32_t t2 = tab.k(w, 2);
+        const uint32_t t3 = tab.k(w, 3);
         bh[2 * hw] = __builtin_amdgcn_perm(t2, t0, 0x05040100u);
         bl[2 * hw] = __builtin_amdgcn_perm(t2, t0, 0x07060302u);
         bh[2 * hw + 1] = __builtin_amdgcn_perm(t3, t1, 0x05040100u);
@@ -377,19 +420,20 @@ __device__ __forceinline__ void k_operands(const uint32_t *kw2, const uint32_t *
 
 // P.V operand B of dim block j: codebook values (hi, lo) of byte j of the
 // lane's four V position rows
-__device__ __forceinline__ half8_t v_operand(const ChunkIn &c, int j, const uint32_t *vtab) {
+template <class Tab>
+__device__ __forceinline__ half8_t v_operand(const ChunkIn &c, int j, const Tab &tab) {
     uint32_t e[4];
 #pragma unroll
     for (int i = 0; i < 4; i++) {
         const uint32_t word = j < 4 ? c.v[i].x : c.v[i].y;
-        e[i] = vtab[(word >> (8 * (j & 3))) & 0xFF];
+        e[i] = tab.v(word, j & 3);
     }
     return __builtin_bit_cast(half8_t, make_uint4(e[0], e[1], e[2], e[3]));
 }
 
 // Occupancy: 3 waves per SIMD (168 VGPRs); the fused token writer's extra
 // live state needs more than that, so it runs at 2 rather than spill.
-template <int GQA, bool FUSED>
+template <int GQA, bool FUSED, bool SPREAD>
 __global__ void __launch_bounds__(64 * kWaves) __attribute__((amdgpu_waves_per_eu(FUSED ? 2 : 3))) tq_attention_kernel(
     const __half *__restrict__ q, int nh, int nkv, int max_seq, int seq_len, int T,
     const int32_t *__restrict__ seq_lens, float attn_scale, const float *__restrict__ signs,
@@ -405,7 +449,10 @@ __global__ void __launch_bounds__(64 * kWaves) __attribute__((amdgpu_waves_per_e
     __shared__ uint32_t ktab[256];   // entry c & 0x7F, indexed by the whole code byte
     __shared__ uint32_t vtab[256];   // V entry c, same packing as ktab
     __shared__ _Float16 wbuf[kWaves][4][16];
-    __shared__ float om[kWaves][GQA][kD];
+    // SPREAD: the spread tables of the KV loop; the waves' partial outputs om
+    // use the same bytes before the tables are built and after the loop
+    __shared__ __attribute__((aligned(16))) uint8_t tabs[SPREAD ? kTabBytes : kWaves * GQA * kD * 4];
+    float(*om)[GQA][kD] = reinterpret_cast<float(*)[GQA][kD]>(tabs);
     __shared__ float mm[kWaves][GQA];
     __shared__ float ll[kWaves][GQA];
     __shared__ float wres[2][kD];      // token writer: K residual, then its QJL projection
@@ -640,6 +687,20 @@ __global__ void __launch_bounds__(64 * kWaves) __attribute__((amdgpu_waves_per_e
             ll[wave][wl] = 0.0f;
         }
     } else {
+        // SPREAD: the spread codebook tables of the loop (their bytes held
+        // om's partial sums of the query projection, reduced above)
+        using Tab = typename std::conditional<SPREAD, TabSpread, TabOne>::type;
+        Tab tab;
+        if constexpr (SPREAD) {
+            spread_tables(tabs, ktab, vtab, lane, wave);
+            __syncthreads();
+            tab.t = tabs;
+            tab.lk = 4u * (uint32_t)(lane & 31);
+            tab.lv = tab.lk + 128u;
+        } else {
+            tab.kt = ktab;
+            tab.vt = vtab;
+        }
         // score operands A, k-slot order within each 4-byte word: bytes {0, 2, 1, 3}.
         // Rows 4h..4h+3 carry head h: aqk = {q_hi, q_lo, 0, 0} (against K hi),
         // aqh = {q_hi, 0, 0, 0} (against K lo), aqs = {0, 0, s_hi, s_lo} (against
@@ -681,7 +742,7 @@ __global__ void __launch_bounds__(64 * kWaves) __attribute__((amdgpu_waves_per_e
     #pragma unroll
             for (int j = 0; j < 4; j++) {
                 half8_t Bh, Bl, Bs;
-                k_operands(&kw[2 * j], ktab, Bh, Bl, Bs);
+                k_operands(&kw[2 * j], tab, Bh, Bl, Bs);
                 d1 = __builtin_amdgcn_mfma_f32_16x16x32_f16(aqk[j], Bh, d1, 0, 0, 0);
                 d1 = __builtin_amdgcn_mfma_f32_16x16x32_f16(aqh[j], Bl, d1, 0, 0, 0);
                 d1 = __builtin_amdgcn_mfma_f32_16x16x32_f16(aqs[j], Bs, d1, 0, 0, 0);
@@ -713,7 +774,7 @@ __global__ void __launch_bounds__(64 * kWaves) __attribute__((amdgpu_waves_per_e
             // byte j of the four position rows ----
     #pragma unroll
             for (int j = 0; j < 8; j++) {
-                const half8_t bv = v_operand(c, j, vtab);
+                const half8_t bv = v_operand(c, j, tab);
                 acc[j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(wa, bv, acc[j], 0, 0, 0);
             }
             __builtin_amdgcn_wave_barrier();   // wbuf is rewritten next chunk
@@ -723,6 +784,7 @@ __global__ void __launch_bounds__(64 * kWaves) __attribute__((amdgpu_waves_per_e
             load_chunk(crs, p0 + kChunk * kWaves, n_l, kg, cur);
             process(c, p0);
         }
+        if constexpr (SPREAD) __syncthreads();   // every wave is done with the tables: om takes their bytes
 
         // lane (c, g): acc[j][0] = o[head g][dim 8c + j]
         if (kg < GQA) {
@@ -891,7 +953,10 @@ __global__ void __launch_bounds__(64 * kWaves) __attribute__((amdgpu_waves_per_e
     __shared__ uint32_t ktab[256];
     __shared__ uint32_t vtab[256];
     __shared__ _Float16 wbuf[kWaves][16][16];
-    __shared__ float om[kWaves][16][kD];
+    // the spread codebook tables of the loop; the waves' partial outputs om
+    // take the same bytes after it
+    __shared__ __attribute__((aligned(16))) uint8_t tabs[kTabBytes];
+    float(*om)[16][kD] = reinterpret_cast<float(*)[16][kD]>(tabs);
     __shared__ float mm[kWaves][16];
     __shared__ float ll[kWaves][16];
 
@@ -943,6 +1008,12 @@ __global__ void __launch_bounds__(64 * kWaves) __attribute__((amdgpu_waves_per_e
 #pragma unroll
     for (int rr = 0; rr < 4; rr++) bnd[rr] = min(bound(4 * kg + rr), p_end);
     __syncthreads();
+    spread_tables(tabs, ktab, vtab, lane, wave);
+    __syncthreads();
+    TabSpread tab;
+    tab.t = tabs;
+    tab.lk = 4u * (uint32_t)(lane & 31);
+    tab.lv = tab.lk + 128u;
 
     // scores in log2 units (attn_scale * log2(e) folded into the per-position
     // scales): the softmax exponentials are single exp2s
@@ -968,7 +1039,7 @@ __global__ void __launch_bounds__(64 * kWaves) __attribute__((amdgpu_waves_per_e
 #pragma unroll
         for (int j = 0; j < 4; j++) {
             half8_t Bh, Bl, Bs;
-            k_operands(&kw[2 * j], ktab, Bh, Bl, Bs);
+            k_operands(&kw[2 * j], tab, Bh, Bl, Bs);
             dq = __builtin_amdgcn_mfma_f32_16x16x32_f16(aqh[j], Bh, dq, 0, 0, 0);
             ds = __builtin_amdgcn_mfma_f32_16x16x32_f16(ash[j], Bs, ds, 0, 0, 0);
             dq = __builtin_amdgcn_mfma_f32_16x16x32_f16(aqh[j], Bl, dq, 0, 0, 0);
@@ -1007,7 +1078,7 @@ __global__ void __launch_bounds__(64 * kWaves) __attribute__((amdgpu_waves_per_e
         const half8_t wa = {w4[0], w4[0], w4[1], w4[1], w4[2], w4[2], w4[3], w4[3]};
 #pragma unroll
         for (int j = 0; j < 8; j++)
-            acc[j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(wa, v_operand(c, j, vtab), acc[j], 0, 0, 0);
+            acc[j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(wa, v_operand(c, j, tab), acc[j], 0, 0, 0);
         __builtin_amdgcn_wave_barrier();   // wbuf is rewritten next chunk
     };
     // two chunk register sets in turn (no copies): the next chunk's loads are
@@ -1022,6 +1093,7 @@ __global__ void __launch_bounds__(64 * kWaves) __attribute__((amdgpu_waves_per_e
     }
 #pragma unroll
     for (int rr = 0; rr < 4; rr++) l_run[rr] = imh_dpp::row16_sum(l_run[rr]);
+    __syncthreads();   // every wave is done with the tables: om takes their bytes
 
     // lane (c, g): acc[j][rr] = o[row 4 g + rr][dim 8 c + j]
 #pragma unroll
@@ -1383,8 +1455,8 @@ static int run_attention(imh_stream *stream, const imh_tq_tables *t, const imh_t
     }
     const __half *qh = reinterpret_cast<const __half *>(q);
     dim3 grid(S, nkv, B);
-#define IMH_TQ_LAUNCH(G, F)                                                                                  \
-    hipLaunchKernelGGL((tq_attention_kernel<G, F>), grid, dim3(64 * kWaves), 0, stream->stream, qh, (int)num_heads, \
+#define IMH_TQ_LAUNCH(G, F, SP)                                                                                \
+    hipLaunchKernelGGL((tq_attention_kernel<G, F, SP>), grid, dim3(64 * kWaves), 0, stream->stream, qh, (int)num_heads, \
                        (int)nkv, (int)cache->max_seq_len, (int)L, (int)token_count, seq_lens, attn_scale,       \
                        t->signs, t->qjl_t,                                                                      \
                        t->k_codebook, t->v_codebook, cache->k_codes, cache->v_codes, cache->k_scales,           \
@@ -1421,14 +1493,23 @@ static int run_attention(imh_stream *stream, const imh_tq_tables *t, const imh_t
         fz.k_norm = qk ? reinterpret_cast<const __half *>(qk->k_norm) : nullptr;
         fz.qjl_t = t->qjl_t;
     }
+    // bank-spread tables from kSpreadMinLen positions per split (building
+    // them costs more than their lookups save on short splits); not with the
+    // token writers, whose workgroups would hold the tables' 64 KB of LDS too
+    // and no longer fit beside two streaming workgroups per CU
+    const bool spread = !fused && split_len >= kSpreadMinLen;
     if (fused) {   // the writer workgroups only in this instantiation
-        if (gqa == 4) IMH_TQ_LAUNCH(4, true);
-        else if (gqa == 2) IMH_TQ_LAUNCH(2, true);
-        else IMH_TQ_LAUNCH(1, true);
+        if (gqa == 4) IMH_TQ_LAUNCH(4, true, false);
+        else if (gqa == 2) IMH_TQ_LAUNCH(2, true, false);
+        else IMH_TQ_LAUNCH(1, true, false);
+    } else if (spread) {
+        if (gqa == 4) IMH_TQ_LAUNCH(4, false, true);
+        else if (gqa == 2) IMH_TQ_LAUNCH(2, false, true);
+        else IMH_TQ_LAUNCH(1, false, true);
     } else {
-        if (gqa == 4) IMH_TQ_LAUNCH(4, false);
-        else if (gqa == 2) IMH_TQ_LAUNCH(2, false);
-        else IMH_TQ_LAUNCH(1, false);
+        if (gqa == 4) IMH_TQ_LAUNCH(4, false, false);
+        else if (gqa == 2) IMH_TQ_LAUNCH(2, false, false);
+        else IMH_TQ_LAUNCH(1, false, false);
     }
 #undef IMH_TQ_LAUNCH
     IMH_HIP(hipGetLastError());
