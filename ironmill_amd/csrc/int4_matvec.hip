@@ -422,18 +422,21 @@ MatPtrs mat_ptrs(const imh_affine_int4_weight *w0, const imh_affine_int4_weight 
     return mp;
 }
 
-// An FFN block (gate/up + activation, then down) at 1-2 rows when both run on
-// the row-band kernel: the gate/up launch also writes the down projection's
+// An FFN block (gate/up + activation, then down) at 1-8 rows whose gate/up
+// runs on the row-band kernel: that launch also writes the down projection's
 // operand image (act / down's AWQ scales, split into f16 hi + lo), and the
-// down launch stages that image instead of forming it from act -- a division
-// and split per element that each of its workgroups would otherwise repeat
-// over all of K.  gin: the gate/up source (plain or residual-norm); *done
-// false: nothing was launched (the caller runs the two ops).
+// down launch stages that image instead of forming it from act -- at 1-2 rows
+// the band kernel (whose every workgroup would otherwise divide and split all
+// of K), at 3-8 the tile kernel, which then needs no prep launch; either sums
+// the groups itself.  gin: the gate/up source (plain, or residual-norm: at
+// 3-8 rows the rows kernel writes the residual and normed rows first and
+// gate/up read those).  *done false: nothing was launched (the caller runs
+// the two ops).
 int ffn_band_pair(imh_stream *s, ActIn gin, uint32_t B, const imh_affine_int4_weight *gate,
                   const imh_affine_int4_weight *up, const imh_affine_int4_weight *down, uint16_t *act_out,
                   uint16_t *y, int epi, bool *done) {
     *done = false;
-    if (B < 1 || B > 2 || !act_out || !y || misaligned16(act_out)) return IMH_OK;
+    if (B < 1 || B > 8 || !act_out || !y || misaligned16(act_out)) return IMH_OK;
     if (misaligned16(gin.a) || misaligned16(gin.b) || misaligned16(gin.gamma) || misaligned16(gin.awq) ||
         misaligned16(gin.residual_out) || misaligned16(gin.normed_out) || misaligned16(down->awq_scales))
         return IMH_OK;
@@ -442,6 +445,8 @@ int ffn_band_pair(imh_stream *s, ActIn gin, uint32_t B, const imh_affine_int4_we
         return IMH_OK;
     }
     if (up->n != gate->n || up->k != gate->k || down->k != gate->n) return IMH_OK;
+    const bool rn = gin.b != nullptr;
+    if (rn && B > 2 && gin.round_mode != 1) return IMH_OK;
     int rc = imh::use_device(s->dev);
     if (rc) return rc;
     const int cus = s->dev->props.multiProcessorCount;
@@ -452,24 +457,49 @@ int ffn_band_pair(imh_stream *s, ActIn gin, uint32_t B, const imh_affine_int4_we
     _Float16 *ihi = static_cast<_Float16 *>(scr), *ilo = ihi + (size_t)B * F;
     MatPtrs gm = mat_ptrs(gate, up, act_out);
     MatPtrs dm = mat_ptrs(down, nullptr, y);
-    gin.img_out_hi = ihi;
-    gin.img_out_lo = ilo;
-    gin.img_awq = reinterpret_cast<const __half *>(down->awq_scales);
+    ActIn pin = gin;   // the source the gate/up launch reads
+    if (rn && B > 2) {
+        pin = ActIn{};
+        pin.a = gin.normed_out;
+        pin.awq = gin.awq;
+    }
+    pin.img_out_hi = ihi;
+    pin.img_out_lo = ilo;
+    pin.img_awq = reinterpret_cast<const __half *>(down->awq_scales);
     ActIn din = {};
     din.a = reinterpret_cast<const __half *>(act_out);
     din.hi = ihi;
-    din.lo = ilo;
-    din.img_src = 1;
+    din.lo = ilo;   // gsum NULL: the down launch sums the groups
     bool fg = false, fd = false;
-    rc = launch_band_matvec(s->stream, cus, (int)B, 2, epi, F, H, gm, gin, &fg, true);
-    if (!rc) rc = launch_band_matvec(s->stream, cus, (int)B, 1, EPI_STORE, Hd, F, dm, din, &fd, true);
-    if (rc || !fg || !fd) return rc;
-    rc = launch_band_matvec(s->stream, cus, (int)B, 2, epi, F, H, gm, gin, &fg);
+    Plan p{};
+    rc = launch_band_matvec(s->stream, cus, (int)B, 2, epi, F, H, gm, pin, &fg, true);
+    if (rc || !fg) return rc;
+    if (B <= 2) {
+        din.img_src = 1;
+        rc = launch_band_matvec(s->stream, cus, (int)B, 1, EPI_STORE, Hd, F, dm, din, &fd, true);
+        if (rc || !fd) return rc;
+    } else {
+        if (plan_launch(s, 1, false, Hd, F, (int)B, "ffn_band_pair", p) || p.raw) {
+            imh::clear_error();
+            return IMH_OK;   // a RAW down (small K) builds its own operand
+        }
+    }
+    if (rn && B > 2) {
+        rc = encode_resnorm_rows(s, gin.a, gin.b, gin.gamma, gin.eps, gin.residual_out, gin.normed_out, (int)B, H);
+        if (rc) return rc;
+    }
+    rc = launch_band_matvec(s->stream, cus, (int)B, 2, epi, F, H, gm, pin, &fg);
     if (rc) return rc;
     if (!fg) return imh::fail(IMH_EDEVICE, "ffn_band_pair: the gate/up launch was refused after its probe");
-    rc = launch_band_matvec(s->stream, cus, (int)B, 1, EPI_STORE, Hd, F, dm, din, &fd);
-    if (rc) return rc;
-    if (!fd) return imh::fail(IMH_EDEVICE, "ffn_band_pair: the down launch was refused after its probe");
+    if (B <= 2) {
+        rc = launch_band_matvec(s->stream, cus, (int)B, 1, EPI_STORE, Hd, F, dm, din, &fd);
+        if (rc) return rc;
+        if (!fd) return imh::fail(IMH_EDEVICE, "ffn_band_pair: the down launch was refused after its probe");
+    } else {
+        rc = launch_image(1, EPI_STORE, p.L, dm, din);
+        if (rc) return rc;
+        IMH_HIP(hipGetLastError());
+    }
     *done = true;
     return IMH_OK;
 }

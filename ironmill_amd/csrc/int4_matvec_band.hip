@@ -540,8 +540,8 @@ bool launch_shape(int tm, int bm, int xc, const BandLaunch &L, const MatPtrs &mp
 // Launches the band kernel when it applies (B <= 8, no row segments, an even
 // number of groups, the shape within the instantiated tiles and the LDS
 // budget -- 64 KB for 1-2 batch rows, 160 KB with one activation chunk per
-// thread above; an operand image source (in.img_src) or output
-// (in.img_out_hi, every band on even rows) at 1-2 batch rows only; a
+// thread above; an operand image source (in.img_src, 1-2 batch rows) or
+// output (in.img_out_hi, every band on even rows); a
 // residual-norm source only at 1-2 batch rows, with
 // round_mode 0 or 1, as nmat 1 with EPI_STORE or nmat 2 with an activation);
 // *used reports whether it did.  probe: only whether it would apply.
@@ -553,9 +553,9 @@ int launch_band_matvec(hipStream_t st, int cus, int B, int nmat, int epi, int N,
     if (B < 1 || B > 8 || mp.seg[0] != 0 || G % 2 || G < 2) return IMH_OK;
     const int bm = B <= 2 ? B : B <= 4 ? 4 : 8;
     // an image source: one matrix, no norm, 1-2 rows; an image output: a
-    // gate/up pair with an activation, 1-2 rows
+    // gate/up pair with an activation
     if (in.img_src && (rn || nmat != 1 || epi != EPI_STORE || bm > 2 || !in.hi || !in.lo)) return IMH_OK;
-    if (in.img_out_hi && (nmat != 2 || epi == EPI_STORE || bm > 2 || !in.img_out_lo)) return IMH_OK;
+    if (in.img_out_hi && (nmat != 2 || epi == EPI_STORE || !in.img_out_lo)) return IMH_OK;
     // above two rows every workgroup would redo the whole residual + norm of
     // every row (measured slower than the rows kernel + the plain band)
     if (bm > 2 && rn) return IMH_OK;

@@ -307,10 +307,16 @@ int4_matvec_kernel(MatPtrs mp, ActIn in, int Nall, int K, int B, int parts, int 
         const int rc = r < bc ? r : 0;
         return (size_t)(m0 + rc) * 2 * G + (a >> 3) * G + g;
     };
+    // IMAGE without group sums (igs NULL: an image another launch wrote):
+    // each stage forms its groups' sums from the halves it stages; the
+    // loads below still go somewhere valid (the image itself, as floats), so
+    // no branch sits around them
+    const bool isum = !RAW && igs == nullptr;
+    const float *igs_ld = isum ? reinterpret_cast<const float *>(ihi) : igs;
     float xsum[RAW ? 1 : kSXChunks];
     if (!RAW) {
 #pragma unroll
-        for (int i = 0; i < kSXChunks; i++) xsum[i] = igs[sx_src(min(i * nthr + tid, sx_total - 1))];
+        for (int i = 0; i < kSXChunks; i++) xsum[i] = igs_ld[sx_src(min(i * nthr + tid, sx_total - 1))];
     }
 
     // A rows of this lane in each tile: plane n_l >> 3, batch row 8t + (n_l & 7)
@@ -354,6 +360,17 @@ int4_matvec_kernel(MatPtrs mp, ActIn in, int Nall, int K, int B, int parts, int 
         if (!RAW) {
             *reinterpret_cast<u32x4_t *>(xs + off) = ch.a;
             *reinterpret_cast<u32x4_t *>(xs + bc * RSX + off) = ch.b;
+            if (isum) {   // uniform
+                float sh, sl;
+                chunk_sums(__builtin_bit_cast(half8_t, ch.a), __builtin_bit_cast(half8_t, ch.b), sh, sl);
+                sh = row16_sum(sh);
+                sl = row16_sum(sl);
+                if (live && (tid & 15) == 0) {
+                    float *sx = sxs + ((gs0 + col / 16) * MT + (r >> 3)) * 16 + (r & 7);
+                    sx[0] = sh * kTwoM24;
+                    sx[8] = sl * kTwoM24;
+                }
+            }
             return;
         }
         const _Float16 *ah = reinterpret_cast<const _Float16 *>(&ch.a);
@@ -457,7 +474,7 @@ int4_matvec_kernel(MatPtrs mp, ActIn in, int Nall, int K, int B, int parts, int 
                 const size_t src = sz_elem(e, sp, zp, dst);
                 szs[dst] = (uint32_t)sp[src] | ((uint32_t)zp[src] << 16);
             }
-            if (!RAW) {
+            if (!RAW && !isum) {
 #pragma unroll
                 for (int i = 0; i < kSXChunks; i++) sxs[min(i * nthr + tid, sx_total - 1)] = xsum[i];
                 for (int e = kSXChunks * nthr + tid; e < sx_total; e += nthr) sxs[e] = igs[sx_src(e)];
