@@ -484,8 +484,9 @@ def main():
                     help="with --decode-only: time 5 eager steps only (no graph capture; for kernel traces)")
     ap.add_argument("--kernel-only", action="store_true",
                     help="only the prepared fused gate+up kernel loop (same as --kernel gate_up)")
-    ap.add_argument("--kernel", choices=["gate_up", "down", "gemm", "probe", "valu_ab"],
+    ap.add_argument("--kernel", choices=["gate_up", "down", "int8", "gemm", "probe", "valu_ab"],
                     help="one kernel alone, for rocprofv3 runs: the batch-B fused gate+up or down "
+                         "matvec, the INT8 down-shape "
                          "matvec, the prefill GEMM (--gemm-*), the streaming probe, or the MFMA / "
                          "VALU-dot matvec A/B; with --eager the launches are host launches (counter "
                          "runs see only those)")
@@ -564,6 +565,27 @@ def main():
         for k_, v in r.items():
             log(f"probe {k_}: {v['us']} us {v.get('GB/s', '-')} GB/s")
         print(json.dumps({"stream_probe": r}), flush=True)
+        return
+
+    if args.kernel == "int8":
+        # INT8 sensitive-layer weights at the down shape (K 9728 -> N 2560), weights rotating
+        # over replicas of 512 MB in total
+        from ironmill_amd import quant as Q
+        B = args.batch
+        q8w = Q.quantize_int8((np.random.default_rng(8).standard_normal((H, F)) * 0.02).astype(np.float32))
+        W8 = [ops.AffineInt8Weight(dev, q8w) for _ in range(max(2, math.ceil(512e6 / q8w.data.nbytes)))]
+        a8 = dev.upload(make_x(B, F, 97))
+        y8 = dev.empty((B, H), np.float16)
+        tot = (eager_loop if args.eager else time_loop)(
+            dev, stream, lambda i: ops.encode_projection_int8(stream, a8, W8[i % len(W8)], y8, B), args.steps,
+            args.warmup)
+        us = 1e3 * tot / args.steps
+        nb = q8w.data.nbytes + q8w.scales.nbytes * 2 + B * 2 * (F + H)
+        gbs = nb / (us * 1e-6) / 1e9
+        log(f"INT8 down kernel B={B}: {us:.2f} us  {gbs:.0f} GB/s ({100 * gbs / HBM_PEAK_GBS:.1f} %)")
+        print(json.dumps({"kernel": "int8w_band_kernel" if B <= 2 else "int8w_matvec_kernel", "batch": B,
+                          "us": round(us, 3), "GB/s": round(gbs, 1), "bytes": nb, "launches": args.steps,
+                          "eager": args.eager}))
         return
 
     B = args.batch

@@ -18,11 +18,12 @@
 //    (v_mfma_i32_16x16x64_i8): exact in int32, sum q8 q minus z sum q8, the
 //    two scales applied in f32.
 //
-// Both kernels: one workgroup per 16 weight rows, waves splitting the K
+// The tile kernels: one workgroup per 16 weight rows, waves splitting the K
 // groups of each stage, the activation staged in LDS per stage (all of K when
 // it fits), each wave's weights loaded into registers before the staging so
 // they are in flight meanwhile; wave partials reduced through LDS in a fixed
-// order (deterministic).
+// order (deterministic).  INT8 weights at 1-4 batch rows take the band kernel
+// (int8w_band_kernel) instead: a grid of one row band per compute unit.
 #include <hip/hip_runtime.h>
 #include <hip/hip_fp16.h>
 
@@ -165,6 +166,231 @@ __global__ void __launch_bounds__(64 * kMaxWaves) int8w_matvec_kernel(
         const int b = 4 * (lane >> 4) + r;
         if (b < B) y[(size_t)b * N + row] = __float2half(s[r]);
     }
+}
+
+// ---------------------------------------------------------------------------
+// INT8 weights, 1-4 batch rows, over a grid balanced on the compute units
+// ---------------------------------------------------------------------------
+// The tile kernel above gives each workgroup 16 rows, so the Qwen3-4B down
+// shape (2560 rows) fills 160 of 256 compute units.  Here workgroup b of NWG
+// owns the row band [N b / NWG, N (b+1) / NWG), cut into TM tiles of 8 rows
+// (the last one masked); W waves split the K groups of every tile, each wave
+// issuing all of its weight loads (TM x NPW x 16 bytes per lane) before the
+// activation is staged.  Same arithmetic per group as the tile kernel (codes
+// as f16 denormals, activation as f16 hi + lo, zero point on the group sums,
+// f32 accumulation); the group's two 64-code halves are summed separately.
+//  * B column j = r + 8h: row r of the tile, half h of the group; lane l loads
+//    16 codes of row r at 64 h + 16 kq (kq = l >> 4), so a wave reads 8 rows
+//    x 128 contiguous bytes.  MFMA u takes its bytes 8u .. 8u + 7.
+//  * A row i = 8h + 4 plane + b: batch row b (rows past B read row 0), f16 hi
+//    (plane 0) or lo (plane 1) of the activation at the same offsets.  Only
+//    result entries whose row and column share h are used: lane l holds D
+//    rows 4 (l >> 4) .. + 3 of column l & 15, used when (l >> 5) == ((l >> 3) & 1).
+//  * LDS: image [2 B][K + 8] f16 (plane-major), half-group sums [G][16] f32
+//    (entry 4 (2h + plane) + b, prescaled by 2^-24), the band's scales and zero
+//    points [rows][G] f16 (coalesced loads issued with the activation's, ahead
+//    of the weights); the wave partials overlay
+//    the image after the last MFMA and are summed in (wave, h, plane) order.
+__host__ __device__ inline size_t int8_band_img_bytes(int K, int B) { return (size_t)2 * B * (K + 8) * 2; }
+constexpr int PX = 2;   // activation chunks per thread loaded ahead of the weights
+
+template <int TM, int NPW>
+__global__ void __launch_bounds__(1024) int8w_band_kernel(const __half *__restrict__ x, const __half *__restrict__ awq,
+                                                          const uint8_t *__restrict__ w, const __half *__restrict__ scales,
+                                                          const __half *__restrict__ zeros, __half *__restrict__ y, int N,
+                                                          int K, int B) {
+    extern __shared__ __attribute__((aligned(16))) uint8_t lds8[];
+    const int tid = threadIdx.x, nthr = blockDim.x;
+    const int lane = tid & 63, waves = nthr >> 6;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int G = K / kGS;
+    const int rb = (int)((long long)N * blockIdx.x / gridDim.x);
+    const int re = (int)((long long)N * (blockIdx.x + 1) / gridDim.x);
+    const int j = lane & 15, kq = lane >> 4, r = j & 7, h = j >> 3;
+    const int g0 = (G * wave) / waves, ng = (G * (wave + 1)) / waves - g0;
+    const int RS = K + 8;
+    _Float16 *img = reinterpret_cast<_Float16 *>(lds8);
+    float *gsx = reinterpret_cast<float *>(lds8 + int8_band_img_bytes(K, B));
+    __half *szl = reinterpret_cast<__half *>(gsx + G * 16);   // [band row][G] scales, then zero points
+    const int nsz = (re - rb) * G;
+
+    // (a) the first PX chunks of the activation, then this wave's weights,
+    // scales and zero points, all issued before any of them is used (the
+    // loads complete in order, so the staging then waits for the activation
+    // alone)
+    const int cpr = K / 8, nch = B * cpr;
+    u32x4_t xr[PX], ar[PX];
+#pragma unroll
+    for (int p = 0; p < PX; p++) {
+        const int c = min(tid + p * nthr, nch - 1);
+        const int b = c / cpr, ci = c - b * cpr;
+        xr[p] = *reinterpret_cast<const u32x4_t *>(x + (size_t)b * K + (size_t)ci * 8);
+        if (awq) ar[p] = *reinterpret_cast<const u32x4_t *>(awq + (size_t)ci * 8);
+    }
+    // the band's scales and zero points (rows rb .. re - 1 are consecutive),
+    // stored to LDS after the activation is staged
+    __half sr[PX], zr[PX];
+#pragma unroll
+    for (int p = 0; p < PX; p++) {
+        const int e = min(tid + p * nthr, nsz - 1);
+        sr[p] = scales[(size_t)rb * G + e];
+        zr[p] = zeros[(size_t)rb * G + e];
+    }
+    // weights of the band's rows only: a buffer resource over rows rb .. re - 1,
+    // so the lanes of rows past the band read zeros without touching memory
+    constexpr uint32_t kRsrcWord3 = 0x00020000u;
+    const __amdgpu_buffer_rsrc_t w_r =
+        __builtin_amdgcn_make_buffer_rsrc((void *)(w + (size_t)rb * K), 0, (re - rb) * K, kRsrcWord3);
+    u32x4_t wq[TM][NPW];
+#pragma unroll
+    for (int t = 0; t < TM; t++) {
+#pragma unroll
+        for (int i = 0; i < NPW; i++) {
+            const int g = g0 + min(i, ng - 1);
+            wq[t][i] = __builtin_bit_cast(
+                u32x4_t, __builtin_amdgcn_raw_buffer_load_b128(w_r, (8 * t + r) * K + g * kGS + h * 64 + kq * 16, 0, 0));
+        }
+    }
+    // (b) the activation image of all of K: chunk c (8 elements) of batch row
+    // b; the 8 chunks of a half group are 8 consecutive lanes
+    auto stage = [&](int c, const u32x4_t &xv, const u32x4_t &av) {
+        const int b = c / cpr, ci = c - b * cpr;
+        const size_t k = (size_t)ci * 8;
+        const _Float16 *xh = reinterpret_cast<const _Float16 *>(&xv);
+        float v[8];
+#pragma unroll
+        for (int i = 0; i < 8; i++) v[i] = (float)xh[i];
+        if (awq) {
+            const _Float16 *ah = reinterpret_cast<const _Float16 *>(&av);
+#pragma unroll
+            for (int i = 0; i < 8; i++) v[i] = v[i] * __builtin_amdgcn_rcpf((float)ah[i]);
+        }
+        half8_t hi, lo;
+        float sh = 0.0f, sl = 0.0f;
+#pragma unroll
+        for (int i = 0; i < 8; i++) {
+            hi[i] = (_Float16)v[i];
+            lo[i] = (_Float16)(v[i] - (float)hi[i]);
+            sh += (float)hi[i];
+            sl += (float)lo[i];
+        }
+        *reinterpret_cast<half8_t *>(img + (size_t)b * RS + k) = hi;
+        *reinterpret_cast<half8_t *>(img + (size_t)(B + b) * RS + k) = lo;
+#pragma unroll
+        for (int o = 1; o < 8; o <<= 1) {
+            sh += __shfl_xor(sh, o);
+            sl += __shfl_xor(sl, o);
+        }
+        if ((ci & 7) == 0) {
+            const int g = ci >> 4, hh = (ci >> 3) & 1;
+            gsx[g * 16 + 4 * (2 * hh) + b] = sh * kTwoM24;
+            gsx[g * 16 + 4 * (2 * hh + 1) + b] = sl * kTwoM24;
+        }
+    };
+    // nch is a multiple of 16: the 8 lanes of a half group pass or fail each bound together
+#pragma unroll
+    for (int p = 0; p < PX; p++)
+        if (tid + p * nthr < nch) stage(tid + p * nthr, xr[p], ar[p]);
+    for (int c = tid + PX * nthr; c < nch; c += nthr) {
+        const int b = c / cpr, ci = c - b * cpr;
+        const u32x4_t xv = *reinterpret_cast<const u32x4_t *>(x + (size_t)b * K + (size_t)ci * 8);
+        u32x4_t av = xv;
+        if (awq) av = *reinterpret_cast<const u32x4_t *>(awq + (size_t)ci * 8);
+        stage(c, xv, av);
+    }
+    // then the scales and zero points (their wait may cover the weights)
+#pragma unroll
+    for (int p = 0; p < PX; p++)
+        if (tid + p * nthr < nsz) {
+            szl[tid + p * nthr] = sr[p];
+            szl[nsz + tid + p * nthr] = zr[p];
+        }
+    for (int e = tid + PX * nthr; e < nsz; e += nthr) {
+        szl[e] = scales[(size_t)rb * G + e];
+        szl[nsz + e] = zeros[(size_t)rb * G + e];
+    }
+    __syncthreads();
+    // (c) MFMAs: A row of this lane (i = j): half j >> 3, plane (j >> 2) & 1, batch row j & 3
+    const int ab = (j & 3) < B ? (j & 3) : 0;
+    const _Float16 *xa = img + (size_t)(((j >> 2) & 1) * B + ab) * RS + (j >> 3) * 64 + kq * 16;
+    float4_t acc[TM];
+#pragma unroll
+    for (int t = 0; t < TM; t++) acc[t] = float4_t{0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+    for (int i = 0; i < NPW; i++) {
+        if (i < ng) {
+            const int g = g0 + i;
+            const half8_t a0 = *reinterpret_cast<const half8_t *>(xa + (size_t)g * kGS);
+            const half8_t a1 = *reinterpret_cast<const half8_t *>(xa + (size_t)g * kGS + 8);
+            const float4_t sx = *reinterpret_cast<const float4_t *>(gsx + g * 16 + 4 * kq);
+#pragma unroll
+            for (int t = 0; t < TM; t++) {
+                float4_t d = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+                for (int u = 0; u < 2; u++) {
+                    const uint32_t w0 = wq[t][i][2 * u], w1 = wq[t][i][2 * u + 1];
+                    const u32x4_t bq = {__builtin_amdgcn_perm(0u, w0, 0x0C010C00u), __builtin_amdgcn_perm(0u, w0, 0x0C030C02u),
+                                        __builtin_amdgcn_perm(0u, w1, 0x0C010C00u), __builtin_amdgcn_perm(0u, w1, 0x0C030C02u)};
+                    d = __builtin_amdgcn_mfma_f32_16x16x32_f16(u ? a1 : a0, __builtin_bit_cast(half8_t, bq), d, 0, 0, 0);
+                }
+                const int lr = min(8 * t + r, re - rb - 1);
+                const float s24 = __half2float(szl[lr * G + g]) * kTwo24, z = __half2float(szl[nsz + lr * G + g]);
+#pragma unroll
+                for (int q = 0; q < 4; q++) acc[t][q] = __builtin_fmaf(s24, __builtin_fmaf(-z, sx[q], d[q]), acc[t][q]);
+            }
+        }
+    }
+    __syncthreads();
+    // (d) partials over the image; thread (t, r, b) sums waves, halves and planes in order
+    float4_t *red = reinterpret_cast<float4_t *>(lds8);
+#pragma unroll
+    for (int t = 0; t < TM; t++) red[(wave * TM + t) * 64 + lane] = acc[t];
+    __syncthreads();
+    if (tid >= TM * 8 * B) return;
+    const int t = tid / (8 * B), rr = (tid / B) & 7, b = tid % B;
+    const int row = rb + 8 * t + rr;
+    if (row >= re) return;
+    float s = 0.0f;
+    for (int wv = 0; wv < waves; wv++) {
+        const float4_t *p = red + (wv * TM + t) * 64;
+#pragma unroll
+        for (int hh = 0; hh < 2; hh++)
+#pragma unroll
+            for (int pl = 0; pl < 2; pl++) s += p[16 * (2 * hh + pl) + rr + 8 * hh][b];
+    }
+    y[(size_t)b * N + row] = __float2half(s);
+}
+
+template <int TM, int NPW>
+void launch_int8_band(hipStream_t st, int nwg, int waves, size_t lds, const __half *x, const __half *awq, const uint8_t *w,
+                      const __half *sc, const __half *zr, __half *y, int N, int K, int B) {
+    hipLaunchKernelGGL((int8w_band_kernel<TM, NPW>), dim3(nwg), dim3(64 * waves), lds, st, x, awq, w, sc, zr, y, N, K, B);
+}
+
+// Picks the band shape: bands of at most 5 tiles, waves holding at most
+// 10 / TM groups per tile, 1-4 batch rows whose image fits 96 KB of LDS.
+// Returns false (nothing launched) when the shape is outside those limits.
+bool int8_band_launch(hipStream_t st, int cus, const __half *x, const __half *awq, const uint8_t *w, const __half *sc,
+                      const __half *zr, __half *y, int N, int K, int B) {
+    const int G = K / kGS;
+    if (B < 1 || B > 4) return false;
+    int nwg = std::min(cus, (N + 7) / 8);
+    while ((N + nwg - 1) / nwg > 40) nwg += cus;
+    const int TM = ((N + nwg - 1) / nwg + 7) / 8;
+    const size_t img = int8_band_img_bytes(K, B) + (size_t)G * 16 * 4 + (size_t)TM * 8 * G * 4;
+    if (img > 96 * 1024) return false;
+    const int npw = std::min(8, 10 / TM);
+    const int waves = std::max(1, (G + npw - 1) / npw);
+    if (waves > 16) return false;
+    const size_t lds = std::max(img, (size_t)waves * TM * 64 * sizeof(float4_t));
+    switch (TM) {
+        case 1: launch_int8_band<1, 8>(st, nwg, waves, lds, x, awq, w, sc, zr, y, N, K, B); break;
+        case 2: launch_int8_band<2, 5>(st, nwg, waves, lds, x, awq, w, sc, zr, y, N, K, B); break;
+        case 3: launch_int8_band<3, 3>(st, nwg, waves, lds, x, awq, w, sc, zr, y, N, K, B); break;
+        case 4: launch_int8_band<4, 2>(st, nwg, waves, lds, x, awq, w, sc, zr, y, N, K, B); break;
+        default: launch_int8_band<5, 2>(st, nwg, waves, lds, x, awq, w, sc, zr, y, N, K, B); break;
+    }
+    return true;
 }
 
 // ---------------------------------------------------------------------------
@@ -325,6 +551,14 @@ int imh_encode_affine_projection_int8(imh_stream *stream, const uint16_t *x, uin
     rc = imh::use_device(stream->dev);
     if (rc) return rc;
     const int N = (int)w->n, K = (int)w->k, G = K / kGS;
+    if (token_count <= 4 &&
+        int8_band_launch(stream->stream, stream->dev->props.multiProcessorCount, reinterpret_cast<const __half *>(x),
+                         reinterpret_cast<const __half *>(w->awq_scales), w->data,
+                         reinterpret_cast<const __half *>(w->scales), reinterpret_cast<const __half *>(w->zeros),
+                         reinterpret_cast<__half *>(y), N, K, (int)token_count)) {
+        IMH_HIP(hipGetLastError());
+        return IMH_OK;
+    }
     const int waves = waves_for(G);
     // batch rows in launches of up to 8 (rows 0-7 of the MFMA tile hi, 8-15 lo)
     for (uint32_t b0 = 0; b0 < token_count; b0 += 8) {
