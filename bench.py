@@ -583,7 +583,7 @@ def main():
         nb = q8w.data.nbytes + q8w.scales.nbytes * 2 + B * 2 * (F + H)
         gbs = nb / (us * 1e-6) / 1e9
         log(f"INT8 down kernel B={B}: {us:.2f} us  {gbs:.0f} GB/s ({100 * gbs / HBM_PEAK_GBS:.1f} %)")
-        print(json.dumps({"kernel": "int8w_band_kernel" if B <= 2 else "int8w_matvec_kernel", "batch": B,
+        print(json.dumps({"kernel": "int8w_band_kernel" if B <= 3 else "int8w_matvec_kernel", "batch": B,
                           "us": round(us, 3), "GB/s": round(gbs, 1), "bytes": nb, "launches": args.steps,
                           "eager": args.eager}))
         return

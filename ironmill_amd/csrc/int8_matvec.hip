@@ -361,14 +361,21 @@ __global__ void __launch_bounds__(1024) int8w_band_kernel(const __half *__restri
     y[(size_t)b * N + row] = __float2half(s);
 }
 
+// false (nothing launched) if the runtime refuses LDS above 64 KB (gfx950 has 160 KB per CU)
 template <int TM, int NPW>
-void launch_int8_band(hipStream_t st, int nwg, int waves, size_t lds, const __half *x, const __half *awq, const uint8_t *w,
+bool launch_int8_band(hipStream_t st, int nwg, int waves, size_t lds, const __half *x, const __half *awq, const uint8_t *w,
                       const __half *sc, const __half *zr, __half *y, int N, int K, int B) {
+    if (lds > 64 * 1024 && hipFuncSetAttribute(reinterpret_cast<const void *>(int8w_band_kernel<TM, NPW>),
+                                               hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds) != hipSuccess) {
+        (void)hipGetLastError();
+        return false;
+    }
     hipLaunchKernelGGL((int8w_band_kernel<TM, NPW>), dim3(nwg), dim3(64 * waves), lds, st, x, awq, w, sc, zr, y, N, K, B);
+    return true;
 }
 
 // Picks the band shape: bands of at most 5 tiles, waves holding at most
-// 10 / TM groups per tile, 1-4 batch rows whose image fits 96 KB of LDS.
+// 10 / TM groups per tile, 1-4 batch rows whose image fits 156 KB of LDS.
 // Returns false (nothing launched) when the shape is outside those limits.
 bool int8_band_launch(hipStream_t st, int cus, const __half *x, const __half *awq, const uint8_t *w, const __half *sc,
                       const __half *zr, __half *y, int N, int K, int B) {
@@ -378,19 +385,18 @@ bool int8_band_launch(hipStream_t st, int cus, const __half *x, const __half *aw
     while ((N + nwg - 1) / nwg > 40) nwg += cus;
     const int TM = ((N + nwg - 1) / nwg + 7) / 8;
     const size_t img = int8_band_img_bytes(K, B) + (size_t)G * 16 * 4 + (size_t)TM * 8 * G * 4;
-    if (img > 96 * 1024) return false;
+    if (img > 156 * 1024) return false;
     const int npw = std::min(8, 10 / TM);
     const int waves = std::max(1, (G + npw - 1) / npw);
     if (waves > 16) return false;
     const size_t lds = std::max(img, (size_t)waves * TM * 64 * sizeof(float4_t));
     switch (TM) {
-        case 1: launch_int8_band<1, 8>(st, nwg, waves, lds, x, awq, w, sc, zr, y, N, K, B); break;
-        case 2: launch_int8_band<2, 5>(st, nwg, waves, lds, x, awq, w, sc, zr, y, N, K, B); break;
-        case 3: launch_int8_band<3, 3>(st, nwg, waves, lds, x, awq, w, sc, zr, y, N, K, B); break;
-        case 4: launch_int8_band<4, 2>(st, nwg, waves, lds, x, awq, w, sc, zr, y, N, K, B); break;
-        default: launch_int8_band<5, 2>(st, nwg, waves, lds, x, awq, w, sc, zr, y, N, K, B); break;
+        case 1: return launch_int8_band<1, 8>(st, nwg, waves, lds, x, awq, w, sc, zr, y, N, K, B);
+        case 2: return launch_int8_band<2, 5>(st, nwg, waves, lds, x, awq, w, sc, zr, y, N, K, B);
+        case 3: return launch_int8_band<3, 3>(st, nwg, waves, lds, x, awq, w, sc, zr, y, N, K, B);
+        case 4: return launch_int8_band<4, 2>(st, nwg, waves, lds, x, awq, w, sc, zr, y, N, K, B);
+        default: return launch_int8_band<5, 2>(st, nwg, waves, lds, x, awq, w, sc, zr, y, N, K, B);
     }
-    return true;
 }
 
 // ---------------------------------------------------------------------------

@@ -50,7 +50,8 @@ def int8_problem(n, k, b, seed, awq):
     (1000, 1024, 11, True),    # two launches of batch rows (8 + 3)
     (2560, 9728, 1, False),    # Qwen3-4B down shape (sensitive layer in INT8): band kernel, 2-tile bands
     (2560, 9728, 2, True),     # band kernel, two batch rows
-    (2560, 9728, 3, False),    # image too large for the band kernel: tile kernel
+    (2560, 9728, 3, False),    # band kernel, 127 KB of LDS
+    (2560, 9728, 4, False),    # image too large for the band kernel: tile kernel
     (9728, 2560, 4, True),     # band kernel, 5-tile bands, four batch rows
     (300, 5120, 1, False),     # band kernel, fewer bands than compute units
     (9728, 2560, 8, False),    # gate / up shape, batch 8
