@@ -23,7 +23,8 @@
 // it fits), each wave's weights loaded into registers before the staging so
 // they are in flight meanwhile; wave partials reduced through LDS in a fixed
 // order (deterministic).  INT8 weights at 1-4 batch rows take the band kernel
-// (int8w_band_kernel) instead: a grid of one row band per compute unit.
+// (int8w_band_kernel) instead, and INT4 x Q8 at 1-8 rows int4xq8_band_kernel:
+// a grid of one row band per compute unit.
 #include <hip/hip_runtime.h>
 #include <hip/hip_fp16.h>
 
@@ -525,6 +526,190 @@ __global__ void __launch_bounds__(64 * kMaxWaves) int4xq8_matvec_kernel(
     }
 }
 
+// ---------------------------------------------------------------------------
+// INT4 x Q8, 1-8 batch rows, over a grid balanced on the compute units
+// ---------------------------------------------------------------------------
+// Row bands as in int8w_band_kernel.  Lane (r, h, kq) loads 16 bytes (32
+// codes) of row r at byte 64 (2p + h) + 16 kq of the band's group pair p, so
+// a wave reads 8 rows x 128 contiguous bytes; B column j = r + 8h, A row i =
+// 8h + b (batch row b, rows past B read row 0); MFMA u takes codes 32 kq + 16u
+// .. + 15 of group 2p + h against the same q8 bytes.  Only result entries
+// whose row and column share h are used (lane l: (l >> 5) == ((l >> 3) & 1)).
+// Per group: ws * as * (sum q8 q - rint(z) sum q8) in f32 from the exact
+// int32 sums.  LDS: q8 image [B][K + 16], per-group q8 sums [G][8] int32 and
+// activation scales [G][8] f32, the band's scales and zero points [rows][G]
+// f16; the wave partials overlay them, summed in (wave, h) order.
+__host__ __device__ inline size_t q8_band_lds(int K, int B, int G, int TM) {
+    return (size_t)B * (K + 16) + (size_t)G * 8 * 8 + (size_t)TM * 8 * G * 4;
+}
+
+template <int TM, int NPW>
+__global__ void __launch_bounds__(1024) int4xq8_band_kernel(const int8_t *__restrict__ q8, const float *__restrict__ q8_scales,
+                                                            const uint8_t *__restrict__ w, const __half *__restrict__ scales,
+                                                            const __half *__restrict__ zeros, __half *__restrict__ y, int N,
+                                                            int K, int B) {
+    extern __shared__ __attribute__((aligned(16))) uint8_t lds8[];
+    const int tid = threadIdx.x, nthr = blockDim.x;
+    const int lane = tid & 63, waves = nthr >> 6;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int G = K / kGS, GP = (G + 1) / 2;
+    const int rb = (int)((long long)N * blockIdx.x / gridDim.x);
+    const int re = (int)((long long)N * (blockIdx.x + 1) / gridDim.x);
+    const int j = lane & 15, kq = lane >> 4, r = j & 7, h = j >> 3;
+    const int p0 = (GP * wave) / waves, np = (GP * (wave + 1)) / waves - p0;
+    const int RS = K + 16;
+    int8_t *img = reinterpret_cast<int8_t *>(lds8);
+    int *gsum = reinterpret_cast<int *>(lds8 + (size_t)B * RS);
+    float *gscl = reinterpret_cast<float *>(gsum + G * 8);
+    __half *szl = reinterpret_cast<__half *>(gscl + G * 8);
+    const int nsz = (re - rb) * G;
+
+    // (a) the first q8 chunk per thread, the band's scales / zero points,
+    // then this wave's weights (a buffer resource over the band's rows: lanes
+    // past it, or past the row's last group, read zeros or are discarded)
+    const int cpr = K / 16, nch = B * cpr;
+    const int c0 = min(tid, nch - 1);
+    const u32x4_t x0 = *reinterpret_cast<const u32x4_t *>(q8 + (size_t)(c0 / cpr) * K + (size_t)(c0 % cpr) * 16);
+    const int e0 = min(tid, nsz - 1);
+    const __half s0 = scales[(size_t)rb * G + e0], z0 = zeros[(size_t)rb * G + e0];
+    constexpr uint32_t kRsrcWord3 = 0x00020000u;
+    const __amdgpu_buffer_rsrc_t w_r =
+        __builtin_amdgcn_make_buffer_rsrc((void *)(w + (size_t)rb * (K / 2)), 0, (re - rb) * (K / 2), kRsrcWord3);
+    u32x4_t wq[TM][NPW];
+#pragma unroll
+    for (int t = 0; t < TM; t++)
+#pragma unroll
+        for (int i = 0; i < NPW; i++)
+            wq[t][i] = __builtin_bit_cast(
+                u32x4_t, __builtin_amdgcn_raw_buffer_load_b128(
+                             w_r, (8 * t + r) * (K / 2) + (2 * (p0 + min(i, np - 1)) + h) * 64 + kq * 16, 0, 0));
+    // (b) q8 rows into LDS with each group's sum (8 consecutive lanes per group)
+    auto stage = [&](int c, const u32x4_t &v) {
+        const int b = c / cpr, ci = c - b * cpr;
+        *reinterpret_cast<u32x4_t *>(img + (size_t)b * RS + ci * 16) = v;
+        int sum = 0;
+#pragma unroll
+        for (int d = 0; d < 4; d++) sum = __builtin_amdgcn_sdot4((int)v[d], 0x01010101, sum, false);
+        sum += __shfl_xor(sum, 1);
+        sum += __shfl_xor(sum, 2);
+        sum += __shfl_xor(sum, 4);
+        if ((ci & 7) == 0) {
+            gsum[(ci >> 3) * 8 + b] = sum;
+            gscl[(ci >> 3) * 8 + b] = q8_scales[(size_t)b * G + (ci >> 3)];
+        }
+    };
+    // nch is a multiple of 8: the 8 lanes of a group pass or fail each bound together
+    if (tid < nch) stage(tid, x0);
+    for (int c = tid + nthr; c < nch; c += nthr)
+        stage(c, *reinterpret_cast<const u32x4_t *>(q8 + (size_t)(c / cpr) * K + (size_t)(c % cpr) * 16));
+    if (tid < nsz) {
+        szl[tid] = s0;
+        szl[nsz + tid] = z0;
+    }
+    for (int e = tid + nthr; e < nsz; e += nthr) {
+        szl[e] = scales[(size_t)rb * G + e];
+        szl[nsz + e] = zeros[(size_t)rb * G + e];
+    }
+    __syncthreads();
+    // (c) integer MFMAs; A row of this lane: half j >> 3, batch row j & 7
+    const int ab = (j & 7) < B ? (j & 7) : 0;
+    const int8_t *xa = img + (size_t)ab * RS + (j >> 3) * kGS + kq * 32;
+    const int bq0 = 4 * ((lane >> 4) & 1);   // batch rows of this lane's D rows
+    float4_t acc[TM];
+#pragma unroll
+    for (int t = 0; t < TM; t++) acc[t] = float4_t{0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+    for (int i = 0; i < NPW; i++) {
+        if (i < np) {
+            const int pg = 2 * (p0 + i);   // first group of the pair
+            const u32x4_t a0 = *reinterpret_cast<const u32x4_t *>(xa + (size_t)pg * kGS);
+            const u32x4_t a1 = *reinterpret_cast<const u32x4_t *>(xa + (size_t)pg * kGS + 16);
+            const int g = pg + h;          // this lane's column group
+            const int gc = min(g, G - 1);
+            const i32x4_t gs4 = *reinterpret_cast<const i32x4_t *>(gsum + gc * 8 + bq0);
+            const float4_t as4 = *reinterpret_cast<const float4_t *>(gscl + gc * 8 + bq0);
+#pragma unroll
+            for (int t = 0; t < TM; t++) {
+                i32x4_t ai = {0, 0, 0, 0};
+#pragma unroll
+                for (int u = 0; u < 2; u++) {
+                    u32x4_t bq;
+#pragma unroll
+                    for (int hh = 0; hh < 2; hh++) {
+                        const uint32_t wd = wq[t][i][2 * u + hh];
+                        const uint32_t lo = wd & 0x0F0F0F0Fu, hi = (wd >> 4) & 0x0F0F0F0Fu;
+                        bq[2 * hh] = __builtin_amdgcn_perm(hi, lo, 0x05010400u);
+                        bq[2 * hh + 1] = __builtin_amdgcn_perm(hi, lo, 0x07030602u);
+                    }
+                    ai = __builtin_amdgcn_mfma_i32_16x16x64_i8(__builtin_bit_cast(i32x4_t, u ? a1 : a0),
+                                                               __builtin_bit_cast(i32x4_t, bq), ai, 0, 0, 0);
+                }
+                if (g < G) {
+                    const int lr = min(8 * t + r, re - rb - 1);
+                    const float ws = __half2float(szl[lr * G + g]);
+                    const int iz = (int)rintf(__half2float(szl[nsz + lr * G + g]));
+#pragma unroll
+                    for (int q = 0; q < 4; q++)
+                        acc[t][q] = __builtin_fmaf(ws * as4[q], (float)(ai[q] - iz * gs4[q]), acc[t][q]);
+                }
+            }
+        }
+    }
+    __syncthreads();
+    // (d) partials over the image; thread (t, r, b) sums waves and halves in order
+    float4_t *red = reinterpret_cast<float4_t *>(lds8);
+#pragma unroll
+    for (int t = 0; t < TM; t++) red[(wave * TM + t) * 64 + lane] = acc[t];
+    __syncthreads();
+    if (tid >= TM * 8 * B) return;
+    const int t = tid / (8 * B), rr = (tid / B) & 7, b = tid % B;
+    const int row = rb + 8 * t + rr;
+    if (row >= re) return;
+    float s = 0.0f;
+    for (int wv = 0; wv < waves; wv++) {
+        const float4_t *p = red + (wv * TM + t) * 64;
+#pragma unroll
+        for (int hh = 0; hh < 2; hh++) s += p[16 * (2 * hh + (b >> 2)) + rr + 8 * hh][b & 3];
+    }
+    y[(size_t)b * N + row] = __float2half(s);
+}
+
+template <int TM, int NPW>
+bool launch_q8_band(hipStream_t st, int nwg, int waves, size_t lds, const int8_t *q8, const float *q8s, const uint8_t *w,
+                    const __half *sc, const __half *zr, __half *y, int N, int K, int B) {
+    if (lds > 64 * 1024 && hipFuncSetAttribute(reinterpret_cast<const void *>(int4xq8_band_kernel<TM, NPW>),
+                                               hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds) != hipSuccess) {
+        (void)hipGetLastError();
+        return false;
+    }
+    hipLaunchKernelGGL((int4xq8_band_kernel<TM, NPW>), dim3(nwg), dim3(64 * waves), lds, st, q8, q8s, w, sc, zr, y, N, K,
+                       B);
+    return true;
+}
+
+// Band shape as for the INT8 band kernel, over group pairs; 1-8 batch rows.
+// Returns false (nothing launched) outside its limits.
+bool q8_band_launch(hipStream_t st, int cus, const int8_t *q8, const float *q8s, const uint8_t *w, const __half *sc,
+                    const __half *zr, __half *y, int N, int K, int B) {
+    const int G = K / kGS, GP = (G + 1) / 2;
+    if (B < 1 || B > 8) return false;
+    int nwg = std::min(cus, (N + 7) / 8);
+    while ((N + nwg - 1) / nwg > 40) nwg += cus;
+    const int TM = ((N + nwg - 1) / nwg + 7) / 8;
+    const int npw = std::min(8, 10 / TM);
+    const int waves = std::max(1, (GP + npw - 1) / npw);
+    if (waves > 16) return false;
+    const size_t lds = std::max(q8_band_lds(K, B, G, TM), (size_t)waves * TM * 64 * sizeof(float4_t));
+    if (lds > 156 * 1024) return false;
+    switch (TM) {
+        case 1: return launch_q8_band<1, 8>(st, nwg, waves, lds, q8, q8s, w, sc, zr, y, N, K, B);
+        case 2: return launch_q8_band<2, 5>(st, nwg, waves, lds, q8, q8s, w, sc, zr, y, N, K, B);
+        case 3: return launch_q8_band<3, 3>(st, nwg, waves, lds, q8, q8s, w, sc, zr, y, N, K, B);
+        case 4: return launch_q8_band<4, 2>(st, nwg, waves, lds, q8, q8s, w, sc, zr, y, N, K, B);
+        default: return launch_q8_band<5, 2>(st, nwg, waves, lds, q8, q8s, w, sc, zr, y, N, K, B);
+    }
+}
+
 int check_w(const imh_affine_int4_weight *w, const char *who) {
     if (!w || !w->data || !w->scales || !w->zeros)
         return imh::fail(IMH_EINVAL, std::string(who) + ": weight or one of its arrays is NULL");
@@ -612,6 +797,13 @@ int imh_encode_affine_matvec_int4xq8(imh_stream *stream, const int8_t *q8, const
     rc = imh::use_device(stream->dev);
     if (rc) return rc;
     const int N = (int)w->n, K = (int)w->k, G = K / kGS;
+    if (token_count <= 8 &&
+        q8_band_launch(stream->stream, stream->dev->props.multiProcessorCount, q8, q8_scales, w->data,
+                       reinterpret_cast<const __half *>(w->scales), reinterpret_cast<const __half *>(w->zeros),
+                       reinterpret_cast<__half *>(y), N, K, (int)token_count)) {
+        IMH_HIP(hipGetLastError());
+        return IMH_OK;
+    }
     const int waves = waves_for(G);
     int SG = std::max(1, std::min(G, kStageBytes / (16 * (kGS + 16))));
     SG = std::min(SG, waves * kNG);

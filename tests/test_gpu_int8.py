@@ -98,8 +98,10 @@ def test_quantize_input_q8_bit_exact(dev, stream, t, k):
 
 
 @pytest.mark.parametrize("n,k,t", [
-    (64, 128, 1),
+    (64, 128, 1),              # band kernel, one group (odd: the pair's second half is empty)
+    (300, 1152, 3),            # band kernel, 9 groups, fewer bands than compute units
     (1000, 1024, 5),           # ragged N
+    (9728, 2560, 8),           # band kernel, 5-tile bands, eight batch rows
     (4096, 2560, 16),          # q_proj, one full token tile
     (1000, 1024, 17),          # two token tiles, ragged
     (9728, 2560, 1),           # gate / up
