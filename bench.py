@@ -484,10 +484,10 @@ def main():
                     help="with --decode-only: time 5 eager steps only (no graph capture; for kernel traces)")
     ap.add_argument("--kernel-only", action="store_true",
                     help="only the prepared fused gate+up kernel loop (same as --kernel gate_up)")
-    ap.add_argument("--kernel", choices=["gate_up", "down", "int8", "gemm", "probe", "valu_ab"],
+    ap.add_argument("--kernel", choices=["gate_up", "down", "int8", "q8", "gemm", "probe", "valu_ab"],
                     help="one kernel alone, for rocprofv3 runs: the batch-B fused gate+up or down "
-                         "matvec, the INT8 down-shape "
-                         "matvec, the prefill GEMM (--gemm-*), the streaming probe, or the MFMA / "
+                         "matvec, the INT8 down-shape matvec, the INT4 x Q8 gate-shape "
+                         "quantize + matvec, the prefill GEMM (--gemm-*), the streaming probe, or the MFMA / "
                          "VALU-dot matvec A/B; with --eager the launches are host launches (counter "
                          "runs see only those)")
     ap.add_argument("--ab-case", type=int, nargs=3, metavar=("N", "K", "B"),
@@ -586,6 +586,29 @@ def main():
         print(json.dumps({"kernel": "int8w_band_kernel" if B <= 3 else "int8w_matvec_kernel", "batch": B,
                           "us": round(us, 3), "GB/s": round(gbs, 1), "bytes": nb, "launches": args.steps,
                           "eager": args.eager}))
+        return
+
+    if args.kernel == "q8":
+        # INT4 x Q8 at the gate shape (K 2560 -> N 9728): the quantize launch and the matvec
+        from ironmill_amd import quant as Q
+        B = args.batch
+        qg0 = Q.quantize_int4((np.random.default_rng(8).standard_normal((F, H)) * 0.02).astype(np.float32))
+        W4 = [ops.AffineQuantizedWeight(dev, qg0) for _ in range(max(2, math.ceil(512e6 / qg0.data.nbytes)))]
+        xq = dev.upload(make_x(B, H, 96))
+        q8d, q8s = dev.empty((B, H), np.int8), dev.empty((B, H // 128), np.float32)
+        gq = dev.empty((B, F), np.float16)
+
+        def q8_step(i):
+            ops.encode_quantize_input_q8(stream, xq, B, H, q8d, q8s)
+            ops.encode_affine_matvec_int4xq8(stream, q8d, q8s, B, W4[i % len(W4)], gq)
+
+        tot = (eager_loop if args.eager else time_loop)(dev, stream, q8_step, args.steps, args.warmup)
+        us = 1e3 * tot / args.steps
+        nb = int(F * H * INT4_BYTES_PER_ELEM + B * 2 * (H + F))
+        gbs = nb / (us * 1e-6) / 1e9
+        log(f"INT4xQ8 gate B={B}: {us:.2f} us (2 launches)  {gbs:.0f} GB/s")
+        print(json.dumps({"kernel": "q8_quantize_kernel + int4xq8_band_kernel", "batch": B, "us": round(us, 3),
+                          "GB/s": round(gbs, 1), "bytes": nb, "launches": 2 * args.steps, "eager": args.eager}))
         return
 
     B = args.batch
