@@ -478,27 +478,32 @@ struct BandLaunch {
     size_t lds;
     hipStream_t st;
     int N, K, B, W;
+    bool dry;   // only check that the instantiation accepts its LDS size
 };
 
 // Above 64 KB of LDS a kernel must be allowed the larger size first (gfx950
 // has 160 KB per CU); false if the runtime refuses.
 template <typename F>
 bool allow_lds(F kernel, size_t lds) {
-    return lds <= 64 * 1024 ||
-           hipFuncSetAttribute(reinterpret_cast<const void *>(kernel), hipFuncAttributeMaxDynamicSharedMemorySize,
-                               (int)lds) == hipSuccess;
+    if (lds <= 64 * 1024 || hipFuncSetAttribute(reinterpret_cast<const void *>(kernel),
+                                                hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds) == hipSuccess)
+        return true;
+    (void)hipGetLastError();   // the refusal is not an error of the op: a fallback runs it
+    return false;
 }
 
 template <int NMAT, int EPI, int TM, int NP, int BM, bool RN, bool IMG>
 bool launch_xc(int xc, const BandLaunch &L, const MatPtrs &mp, const ActIn &in) {
     if (xc == 1) {
         if (!allow_lds(int4_band_kernel<NMAT, EPI, TM, NP, BM, 1, RN, IMG>, L.lds)) return false;
-        hipLaunchKernelGGL((int4_band_kernel<NMAT, EPI, TM, NP, BM, 1, RN, IMG>), L.grid, L.block, L.lds, L.st, mp, in,
-                           L.N, L.K, L.B, L.W);
+        if (!L.dry)
+            hipLaunchKernelGGL((int4_band_kernel<NMAT, EPI, TM, NP, BM, 1, RN, IMG>), L.grid, L.block, L.lds, L.st, mp,
+                               in, L.N, L.K, L.B, L.W);
     } else if (BM <= 2) {   // three activation chunks per thread: 1-2 batch rows only
         if (!allow_lds(int4_band_kernel<NMAT, EPI, TM, NP, BM, BM <= 2 ? 3 : 1, RN, IMG>, L.lds)) return false;
-        hipLaunchKernelGGL((int4_band_kernel<NMAT, EPI, TM, NP, BM, BM <= 2 ? 3 : 1, RN, IMG>), L.grid, L.block,
-                           L.lds, L.st, mp, in, L.N, L.K, L.B, L.W);
+        if (!L.dry)
+            hipLaunchKernelGGL((int4_band_kernel<NMAT, EPI, TM, NP, BM, BM <= 2 ? 3 : 1, RN, IMG>), L.grid, L.block,
+                               L.lds, L.st, mp, in, L.N, L.K, L.B, L.W);
     }
     return true;
 }
@@ -521,8 +526,9 @@ bool launch_bm(int bm, int xc, const BandLaunch &L, const MatPtrs &mp, const Act
 template <int BM>
 bool launch_mb(const BandLaunch &L, const MatPtrs &mp, const ActIn &in) {
     if (!allow_lds(int4_band_kernel<1, EPI_STORE, 5, 2, BM, 1, false, false, 2, true>, L.lds)) return false;
-    hipLaunchKernelGGL((int4_band_kernel<1, EPI_STORE, 5, 2, BM, 1, false, false, 2, true>), L.grid, L.block, L.lds,
-                       L.st, mp, in, L.N, L.K, L.B, L.W);
+    if (!L.dry)
+        hipLaunchKernelGGL((int4_band_kernel<1, EPI_STORE, 5, 2, BM, 1, false, false, 2, true>), L.grid, L.block,
+                           L.lds, L.st, mp, in, L.N, L.K, L.B, L.W);
     return true;
 }
 
@@ -544,7 +550,8 @@ bool launch_shape(int tm, int bm, int xc, const BandLaunch &L, const MatPtrs &mp
 // output (in.img_out_hi, every band on even rows); a
 // residual-norm source only at 1-2 batch rows, with
 // round_mode 0 or 1, as nmat 1 with EPI_STORE or nmat 2 with an activation);
-// *used reports whether it did.  probe: only whether it would apply.
+// *used reports whether it did.  probe: only whether it would apply (nothing
+// is launched; the LDS size is checked with the runtime as for a launch).
 int launch_band_matvec(hipStream_t st, int cus, int B, int nmat, int epi, int N, int K, const MatPtrs &mp,
                        const ActIn &in, bool *used, bool probe) {
     *used = false;
@@ -591,11 +598,9 @@ int launch_band_matvec(hipStream_t st, int cus, int B, int nmat, int epi, int N,
     if (xc > 3 || (bm > 2 && xc > 1) || nmat * rows * P > kSZC * nthr) return IMH_OK;
     const size_t lds = band_lds(G, bm, nmat, TM, W * nmat, rn).total;
     if (lds > (bm <= 2 ? 64 : 160) * 1024) return IMH_OK;
-    if (probe) {
-        *used = true;
-        return IMH_OK;
-    }
-    BandLaunch L{dim3(nwg), dim3(nthr), lds, st, N, K, B, W};
+    // a probe takes the same dispatch with launches off: the instantiation
+    // must still accept its LDS size (hipFuncSetAttribute above 64 KB)
+    BandLaunch L{dim3(nwg), dim3(nthr), lds, st, N, K, B, W, probe};
     bool ok;
     if (mb) {
         ok = bm == 4 ? launch_mb<4>(L, mp, in) : launch_mb<8>(L, mp, in);
@@ -618,7 +623,7 @@ int launch_band_matvec(hipStream_t st, int cus, int B, int nmat, int epi, int N,
         ok = launch_shape<2, EPI_STORE, false>(tm, bm, xc, L, mp, in);
     }
     if (!ok) return IMH_OK;   // the LDS size was refused: the tile kernel runs the op
-    IMH_HIP(hipGetLastError());
+    if (!probe) IMH_HIP(hipGetLastError());
     *used = true;
     return IMH_OK;
 }

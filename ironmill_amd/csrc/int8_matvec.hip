@@ -347,19 +347,21 @@ __global__ void __launch_bounds__(1024) int8w_band_kernel(const __half *__restri
 #pragma unroll
     for (int t = 0; t < TM; t++) red[(wave * TM + t) * 64 + lane] = acc[t];
     __syncthreads();
-    if (tid >= TM * 8 * B) return;
-    const int t = tid / (8 * B), rr = (tid / B) & 7, b = tid % B;
-    const int row = rb + 8 * t + rr;
-    if (row >= re) return;
-    float s = 0.0f;
-    for (int wv = 0; wv < waves; wv++) {
-        const float4_t *p = red + (wv * TM + t) * 64;
+    // the block is sized from K, so it may hold fewer threads than outputs
+    for (int o = tid; o < TM * 8 * B; o += nthr) {
+        const int t = o / (8 * B), rr = (o / B) & 7, b = o % B;
+        const int row = rb + 8 * t + rr;
+        if (row >= re) continue;
+        float s = 0.0f;
+        for (int wv = 0; wv < waves; wv++) {
+            const float4_t *p = red + (wv * TM + t) * 64;
 #pragma unroll
-        for (int hh = 0; hh < 2; hh++)
+            for (int hh = 0; hh < 2; hh++)
 #pragma unroll
-            for (int pl = 0; pl < 2; pl++) s += p[16 * (2 * hh + pl) + rr + 8 * hh][b];
+                for (int pl = 0; pl < 2; pl++) s += p[16 * (2 * hh + pl) + rr + 8 * hh][b];
+        }
+        y[(size_t)b * N + row] = __float2half(s);
     }
-    y[(size_t)b * N + row] = __float2half(s);
 }
 
 // false (nothing launched) if the runtime refuses LDS above 64 KB (gfx950 has 160 KB per CU)
@@ -661,17 +663,19 @@ __global__ void __launch_bounds__(1024) int4xq8_band_kernel(const int8_t *__rest
 #pragma unroll
     for (int t = 0; t < TM; t++) red[(wave * TM + t) * 64 + lane] = acc[t];
     __syncthreads();
-    if (tid >= TM * 8 * B) return;
-    const int t = tid / (8 * B), rr = (tid / B) & 7, b = tid % B;
-    const int row = rb + 8 * t + rr;
-    if (row >= re) return;
-    float s = 0.0f;
-    for (int wv = 0; wv < waves; wv++) {
-        const float4_t *p = red + (wv * TM + t) * 64;
+    // the block is sized from K, so it may hold fewer threads than outputs
+    for (int o = tid; o < TM * 8 * B; o += nthr) {
+        const int t = o / (8 * B), rr = (o / B) & 7, b = o % B;
+        const int row = rb + 8 * t + rr;
+        if (row >= re) continue;
+        float s = 0.0f;
+        for (int wv = 0; wv < waves; wv++) {
+            const float4_t *p = red + (wv * TM + t) * 64;
 #pragma unroll
-        for (int hh = 0; hh < 2; hh++) s += p[16 * (2 * hh + (b >> 2)) + rr + 8 * hh][b & 3];
+            for (int hh = 0; hh < 2; hh++) s += p[16 * (2 * hh + (b >> 2)) + rr + 8 * hh][b & 3];
+        }
+        y[(size_t)b * N + row] = __float2half(s);
     }
-    y[(size_t)b * N + row] = __float2half(s);
 }
 
 template <int TM, int NPW>

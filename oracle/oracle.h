@@ -111,10 +111,16 @@ void orc_lloyd_max_gaussian(int dim, int bits, float *levels, float *bounds);
 double orc_normal_quantile(double p);
 double orc_erf(double x);
 
-/* rand 0.10 StdRng restated: ChaCha12 keyed by rand_core's PCG32
- * seed_from_u64 expansion.  The ChaCha block function is pinned by RFC 8439
- * vectors (rounds=20); the seed expansion and the word order are
- * "parity unpinned" (rand/chacha20 are not vendored in the reference). */
+/* rand 0.10 StdRng restated: ChaCha12 (64-bit block counter in words 12-13,
+ * stream words 14-15 zero) keyed by rand_core's PCG32 seed_from_u64
+ * expansion.  Pinned: the block function at 8, 12 and 20 rounds and the
+ * counter step (the all-zero-key vectors of draft-strombergson-chacha-test-
+ * vectors and RFC 8439's block), the keyed stream's word order (a zero key
+ * gives those blocks' words, low word first in each u64), and the PCG32
+ * advance and XSH-RR output (the pcg32 demo sequence).  Unpinned: how
+ * seed_from_u64 composes them (advance first, fixed increment; read from
+ * rand_core's published source -- rand/chacha20 are not vendored in the
+ * reference). */
 void orc_chacha_block(const uint32_t in[16], int rounds, uint32_t out[16]);
 typedef struct {
     uint32_t key[8];
@@ -122,8 +128,13 @@ typedef struct {
     uint32_t buf[64];
     int idx;
 } orc_stdrng;
+uint64_t orc_pcg32_advance(uint64_t state, uint64_t inc);
+uint32_t orc_pcg32_xsh_rr(uint64_t state);
+void orc_stdrng_from_key(orc_stdrng *r, const uint32_t key[8]);
 void orc_stdrng_seed_from_u64(orc_stdrng *r, uint64_t seed);
 uint64_t orc_stdrng_next_u64(orc_stdrng *r);
+/* n u64 draws of the stream keyed by key, or by seed_from_u64(seed) if key is NULL */
+void orc_stdrng_stream(const uint32_t *key, uint64_t seed, int n, uint64_t *out);
 /* turboquant/rotation.rs:13-25 (random_bool(0.5) per sign) and :31-49
  * (Box-Muller over random::<f64>()) -- parity unpinned, see above. */
 void orc_rotation_signs(int dim, uint64_t seed, float *signs);

@@ -65,6 +65,9 @@ def _declare(L):
         "orc_normal_quantile": (C.c_double, [C.c_double]),
         "orc_erf": (C.c_double, [C.c_double]),
         "orc_chacha_block": (None, [P, C.c_int, P]),
+        "orc_pcg32_advance": (C.c_uint64, [C.c_uint64, C.c_uint64]),
+        "orc_pcg32_xsh_rr": (C.c_uint32, [C.c_uint64]),
+        "orc_stdrng_stream": (None, [P, C.c_uint64, C.c_int, P]),
         "orc_rotation_signs": (None, [C.c_int, C.c_uint64, P]),
         "orc_qjl_matrix": (None, [C.c_int, C.c_uint64, P]),
         "orc_hadamard_rotate": (None, [P, P, C.c_int]),
@@ -307,6 +310,22 @@ def chacha_block(words16, rounds=20):
     return out
 
 
+def pcg32_advance(state, inc):
+    return int(lib().orc_pcg32_advance(state & (2 ** 64 - 1), inc & (2 ** 64 - 1)))
+
+
+def pcg32_xsh_rr(state):
+    return int(lib().orc_pcg32_xsh_rr(state & (2 ** 64 - 1)))
+
+
+def stdrng_stream(n, seed=0, key=None):
+    """n u64 draws of StdRng: keyed by the 8 words `key`, else seed_from_u64(seed)."""
+    out = np.zeros(n, np.uint64)
+    k = None if key is None else _c(key, np.uint32)
+    lib().orc_stdrng_stream(_p(k), seed, n, _p(out))
+    return out
+
+
 def rotation_signs(dim, seed):
     s = np.zeros(dim, np.float32)
     lib().orc_rotation_signs(dim, seed, _p(s))
@@ -524,10 +543,13 @@ class DecoderReference:
         self.emb = np.asarray(embedding16, np.float16)
         self.final_norm = final_norm16
         self.layers = []
+        memo = {}   # a weight object shared by several layers is dequantized once
         for L in layers:
             d = dict(L)
             for name in ("q_proj", "k_proj", "v_proj", "o_proj", "gate_proj", "up_proj", "down_proj"):
-                d[name] = self._dense(L[name])
+                if id(L[name]) not in memo:
+                    memo[id(L[name])] = self._dense(L[name])
+                d[name] = memo[id(L[name])]
             self.layers.append(d)
         self.lm = self._dense(lm_head)
         shp = (self.B, self.nkv, self.max_seq)

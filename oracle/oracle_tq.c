@@ -136,16 +136,39 @@ void orc_chacha_block(const uint32_t in[16], int rounds, uint32_t out[16]) {
     for (int i = 0; i < 16; i++) out[i] = x[i] + in[i];
 }
 
-void orc_stdrng_seed_from_u64(orc_stdrng *r, uint64_t state) {
-    /* rand_core SeedableRng::seed_from_u64: PCG32 output words fill the seed */
-    for (int i = 0; i < 8; i++) {
-        state = state * 6364136223846793005ULL + 11634580027462260723ULL;
-        uint32_t xorshifted = (uint32_t)(((state >> 18) ^ state) >> 27);
-        uint32_t rot = (uint32_t)(state >> 59);
-        r->key[i] = (xorshifted >> rot) | (xorshifted << ((32 - rot) & 31));
-    }
+/* PCG32 (O'Neill 2014): the LCG step and the XSH-RR output of a state */
+uint64_t orc_pcg32_advance(uint64_t state, uint64_t inc) { return state * 6364136223846793005ULL + inc; }
+
+uint32_t orc_pcg32_xsh_rr(uint64_t state) {
+    uint32_t xorshifted = (uint32_t)(((state >> 18) ^ state) >> 27);
+    uint32_t rot = (uint32_t)(state >> 59);
+    return (xorshifted >> rot) | (xorshifted << ((32 - rot) & 31));
+}
+
+void orc_stdrng_from_key(orc_stdrng *r, const uint32_t key[8]) {
+    for (int i = 0; i < 8; i++) r->key[i] = key[i];
     r->counter = 0;
     r->idx = 64;
+}
+
+void orc_stdrng_seed_from_u64(orc_stdrng *r, uint64_t state) {
+    /* rand_core SeedableRng::seed_from_u64: the state advances first (fixed
+     * increment), then its XSH-RR output is the next seed word */
+    uint32_t key[8];
+    for (int i = 0; i < 8; i++) {
+        state = orc_pcg32_advance(state, 11634580027462260723ULL);
+        key[i] = orc_pcg32_xsh_rr(state);
+    }
+    orc_stdrng_from_key(r, key);
+}
+
+void orc_stdrng_stream(const uint32_t *key, uint64_t seed, int n, uint64_t *out) {
+    orc_stdrng r;
+    if (key)
+        orc_stdrng_from_key(&r, key);
+    else
+        orc_stdrng_seed_from_u64(&r, seed);
+    for (int i = 0; i < n; i++) out[i] = orc_stdrng_next_u64(&r);
 }
 
 static void stdrng_refill(orc_stdrng *r) {

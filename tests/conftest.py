@@ -66,3 +66,31 @@ def assert_close(got, ref, rel=REL_L2_TOL, max_abs=MAX_ABS_TOL, what="", ulps=1)
         f"{what}: rel_l2={r:.3e} (tol {rel}) max_abs={m:.3e} (bound max({max_abs}, {ulps} ulp16)), "
         f"worst err/bound={worst:.2f}")
     return r, m
+
+
+# The decoder tests' bound on logits (tests/test_decode_sensitivity.py measures why):
+# every stored activation is f16, so sums in another order round some stored values one
+# step apart and the layers amplify those steps.  Two oracle variants show how far that
+# moves the logits on the test's own inputs: B32, the GPU upload's weight semantics summing
+# in f32 instead of f64 (B), and A, the reference's CPU path (weights rounded to f16).  The
+# GPU is held to 1e-3 against B, or to twice B32's distance from B, or to A's distance from
+# B -- no further from the exact computation than the reference's own CPU path -- and to
+# that bound plus A's distance from B against A (the triangle inequality).  Both measured
+# distances are held to SPREAD_CAP, so the bound cannot loosen with the data.
+SPREAD_CAP = 2e-3
+
+
+def assert_decoder_logits(got, want_a, want_b, want_b32, what=""):
+    """got: GPU logits; A: the reference's CPU path (f16 weights, f32 sums); B / B32: the
+    GPU upload's weight semantics summing in f64 / f32.  Returns (rel(GPU,B), rel(GPU,A),
+    spread, rel(A,B))."""
+    sens = rel_l2(want_b32, want_b)
+    ab = rel_l2(want_a, want_b)
+    gb, ga = rel_l2(got, want_b), rel_l2(got, want_a)
+    print(f"{what}: GPU-B {gb:.2e}  GPU-A {ga:.2e}  | oracle spread B32-B {sens:.2e}  A-B {ab:.2e}", flush=True)
+    assert np.all(np.isfinite(np.asarray(got, np.float64))), f"{what}: non-finite logits"
+    assert sens <= SPREAD_CAP and ab <= SPREAD_CAP, f"{what}: oracle spreads {sens:.3e} / {ab:.3e} exceed the cap"
+    bound = max(1e-3, 2 * sens, ab)
+    assert gb <= bound, f"{what}: rel(GPU, B) {gb:.3e} (bound {bound:.3e})"
+    assert ga <= bound + ab, f"{what}: rel(GPU, A) {ga:.3e} (bound {bound + ab:.3e})"
+    return gb, ga, sens, ab

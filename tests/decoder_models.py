@@ -59,3 +59,21 @@ def kv_rows(rng, batch, tokens, nkv, hd=128):
     for h in range(nkv):
         x[:, :, h, rng.choice(hd, 4, replace=False)] *= 10.0
     return x.astype(np.float16)
+
+
+QWEN3_4B = dict(hidden_size=2560, intermediate_size=9728, num_layers=36, num_heads=32, num_kv_heads=8, head_dim=128,
+                vocab_size=151936, rms_eps=1e-6, rope_theta=1e6)
+
+
+def shared_layer_model(seed: int, cfg: dict, std: float = 0.02):
+    """A model of cfg's full shape whose layers all hold one layer's weights (quantized from
+    N(0, std), AWQ as in host_model): every layer still runs every launch on its own cache and
+    activations, while the oracle dequantizes one layer instead of num_layers."""
+    one = dict(cfg, num_layers=1)
+    layers, emb, fnorm, lm = host_model(seed, one, std)
+    return [layers[0]] * cfg["num_layers"], emb, fnorm, lm
+
+
+def block_kv(rng, batch, block, nkv, hd=128):
+    """K and V rows [batch, block, nkv, hd] of one cache block (configs[2] distribution)."""
+    return kv_rows(rng, batch, block, nkv, hd), kv_rows(rng, batch, block, nkv, hd)

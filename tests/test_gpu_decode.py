@@ -9,22 +9,29 @@ Glue (against the numpy oracle, which stores f16 where the kernels do):
 
 Decode step (imh_decoder_step, the schedule of pipeline.rs:424-1172) against
 oracle.DecoderReference, the same schedule over the CPU dequantize-then-compute
-ops, for an FP16 and a TurboQuant KV cache, four tokens for two sequences at
-different positions.  Every stored activation is f16 on both sides, so each op
-adds at most the op-level differences the per-op tests bound; over two layers
-the logits stay within rel-L2 <= 1e-3 of the reference.
+ops, for an FP16 and a TurboQuant KV cache, four tokens for one or two
+sequences at different positions.  Every stored activation is f16 on both
+sides, so each op adds at most the op-level differences the per-op tests bound.
+The logits are held to the north-star rel-L2 1e-3 against the oracle on the GPU
+upload's weight semantics (weights="exact": (q - z16) * s16, f64 sums), or to
+the oracle's own spreads where they are larger (twice its f32-vs-f64
+distance, or the reference CPU path's distance from it; both capped:
+conftest.assert_decoder_logits), and to that bound plus the CPU path's
+distance from the exact oracle against the CPU path (f16 dequantized
+weights): the two weight semantics alone move these logits by ~1e-3, so 1e-3
+against the CPU path holds only by chance.
 With the TurboQuant cache a one-step difference in a K/V projection can move a
 vector across a codebook boundary (free-running, the logits drift to ~5e-3), so
 that test hands the oracle the code rows the GPU wrote at each step (the cache
-write itself is bit-exact on equal inputs in the op tests), bounds the share of
-code bytes that differed by the oracle's own sensitivity to one-step input
-changes, and holds the logits to the same 1e-3.
+write itself is bit-exact on equal inputs in the op tests) and bounds the share
+of code bytes that differed by the oracle's own sensitivity to one-step input
+changes.
 """
 import numpy as np
 import pytest
 
 import oracle as O
-from conftest import assert_close, rel_l2
+from conftest import assert_close, assert_decoder_logits
 from ironmill_amd import IronmillError, ops, quant
 
 pytestmark = pytest.mark.gpu
@@ -194,15 +201,19 @@ def build_decoder(dev, model, kv_cache, cfg=CFG):
     return d
 
 
-@pytest.mark.parametrize("kv_cache", ["fp16", "turboquant", "turboquant-host-tables"])
-def test_decoder_matches_reference(dev, stream, kv_cache):
+@pytest.mark.parametrize("kv_cache,batch", [("fp16", 2), ("turboquant", 2), ("turboquant-host-tables", 2),
+                                            ("fp16", 1), ("turboquant", 1)])
+def test_decoder_matches_reference(dev, stream, kv_cache, batch):
     """turboquant-host-tables: the decoder uses caller-built tables (imh_decoder_set_tq_tables,
     the path a binding takes to hand over the reference's own generator outputs), here the
-    oracle's tables for another seed, and the oracle runs on the same tables."""
+    oracle's tables for another seed, and the oracle runs on the same tables.  Batch 1 takes
+    the decoder's one-row launches (the residual-norm gate/up band writing down's operand
+    image, the segmented Q|K|V launch at one row, the attention that writes its token's row)."""
+    cfg = dict(CFG, batch=batch)
     model = make_model(dev, 77)
     host = kv_cache == "turboquant-host-tables"
     kv_cache = "turboquant" if host else kv_cache
-    d = build_decoder(dev, model, kv_cache)
+    d = build_decoder(dev, model, kv_cache, cfg)
     host_layers, _, emb, fnorm, lm = model
     tabs = None
     if host:
@@ -212,12 +223,17 @@ def test_decoder_matches_reference(dev, stream, kv_cache):
             v_bounds=tabs.v_bounds, qjl=tabs.qjl))
         d.set_tq_tables(t)
         assert np.array_equal(t.tables()["signs"], tabs.signs)
-    ref = O.DecoderReference(CFG, host_layers, emb, fnorm, lm, kv_cache=kv_cache, tables=tabs)
-    start = np.array([0, 9], np.int32)
+    ref = O.DecoderReference(cfg, host_layers, emb, fnorm, lm, kv_cache=kv_cache, tables=tabs)
+    exact = O.DecoderReference(cfg, host_layers, emb, fnorm, lm, kv_cache=kv_cache, tables=tabs, weights="exact",
+                               acc="f64")
+    exact32 = O.DecoderReference(cfg, host_layers, emb, fnorm, lm, kv_cache=kv_cache, tables=tabs, weights="exact",
+                                 acc="f32")
+    start = np.array([0, 9] if batch == 2 else [9], np.int32)
     d.reset(stream, start)
-    ref.positions = start.copy()
-    rng = np.random.default_rng(5)
-    logits = dev.empty((CFG["batch"], CFG["vocab_size"]), np.float16)
+    for r in (ref, exact, exact32):
+        r.positions = start.copy()
+    rng = np.random.default_rng(5 if batch == 2 else 6)
+    logits = dev.empty((batch, cfg["vocab_size"]), np.float16)
     flips = {}   # layer -> [K bytes differing, V bytes differing, bytes compared, far K/V differences]
 
     def force_rows(l, cache, pos):
@@ -226,7 +242,7 @@ def test_decoder_matches_reference(dev, stream, kv_cache):
         # a vector across a codebook boundary) and record how the bytes differed
         got = d.kv_cache(l)
         f = flips.setdefault(l, [0, 0, 0, 0])
-        for b in range(CFG["batch"]):
+        for b in range(batch):
             p = pos[b]
             rk, gk = cache["k_codes"][b, :, p].astype(int), got["k_codes"][b, :, p].astype(int)
             rv, gv = cache["v_codes"][b, :, p].astype(int), got["v_codes"][b, :, p].astype(int)
@@ -239,13 +255,21 @@ def test_decoder_matches_reference(dev, stream, kv_cache):
             for name in got:
                 cache[name][b, :, p] = got[name][b, :, p]
 
+    def copy_rows(l, cache, pos):
+        got = d.kv_cache(l)
+        for b in range(batch):
+            for name in got:
+                cache[name][b, :, pos[b]] = got[name][b, :, pos[b]]
+
+    tq = kv_cache == "turboquant"
     for step in range(4):
-        tok = rng.integers(0, CFG["vocab_size"], CFG["batch"]).astype(np.uint32)
+        tok = rng.integers(0, cfg["vocab_size"], batch).astype(np.uint32)
         d.step(stream, dev.upload(tok), logits)
         stream.sync()
-        want = ref.step(tok.astype(np.int64), cache_hook=force_rows if kv_cache == "turboquant" else None)
-        r = rel_l2(logits.read(), want)
-        assert r <= 1e-3, f"{kv_cache} step {step}: logits rel-L2 {r:.3e}"
+        want = ref.step(tok.astype(np.int64), cache_hook=force_rows if tq else None)
+        want_x = exact.step(tok.astype(np.int64), cache_hook=copy_rows if tq else None)
+        want_32 = exact32.step(tok.astype(np.int64), cache_hook=copy_rows if tq else None)
+        assert_decoder_logits(logits.read(), want, want_x, want_32, f"{kv_cache} B={batch} step {step}")
     assert np.array_equal(d.positions(), start + 4)
     if kv_cache == "turboquant":
         # one-f16-step input differences change ~4 % of K bytes (mostly QJL signs) and
@@ -262,7 +286,7 @@ def test_decoder_matches_reference(dev, stream, kv_cache):
     else:
         # the cache rows the steps wrote are the K/V projections: compare layer 1 with the oracle's
         got = d.kv_cache(1)
-        for b in range(CFG["batch"]):
+        for b in range(batch):
             rows = slice(start[b], start[b] + 4)
             assert_close(got["k"][b, :, rows], ref.caches[1]["k"][b, :, rows].astype(np.float32), rel=5e-3,
                          what="layer-1 K rows")

@@ -16,17 +16,21 @@ it across a codebook boundary or flip a QJL sign).  So the GPU is compared with
   B  -- the oracle with the GPU upload's weight semantics ((q - z16) * s16,
         exact) summing in float64, and
   A  -- the reference's CPU path (dequantized weights rounded to f16, f32 sums),
-and the bound is the oracle's own spread, measured in the same test:
-  rel(GPU, B) <= max(1e-3, 2 rel(B32, B)),
-  rel(GPU, A) <= max(1e-3, rel(A, B) + 2 rel(B32, B)),
+and the bound is the oracle's own spread, measured in the same test
+(conftest.assert_decoder_logits):
+  rel(GPU, B) <= max(1e-3, 2 rel(B32, B), rel(A, B)),
+  rel(GPU, A) <= that + rel(A, B),
 where B32 is B summing in float32.  A systematic error (a wrong index, scale
-or sign) moves the logits by far more than that spread.
+or sign) moves the logits by far more than that spread.  The spreads are held
+to conftest.SPREAD_CAP (2e-3), so the bound cannot loosen with the data: on
+these inputs (prefill 200, batch 1, 2 and 8, either cache) rel(B32, B)
+measures 0.90-1.38e-3 and rel(A, B) 1.31-1.76e-3 per step on the CPU.
 """
 import numpy as np
 import pytest
 
 import oracle as O
-from conftest import rel_l2
+from conftest import assert_decoder_logits
 from decoder_models import host_model, kv_rows
 from ironmill_amd import ops
 
@@ -63,7 +67,8 @@ def device_model(dev, model):
     return dev_layers, dev.upload(emb), dev.upload(fnorm), ops.AffineQuantizedWeight(dev, lm)
 
 
-@pytest.mark.parametrize("kv_cache,batch", [("fp16", 2), ("turboquant", 2), ("fp16", 8), ("turboquant", 8)])
+@pytest.mark.parametrize("kv_cache,batch", [("fp16", 1), ("turboquant", 1), ("fp16", 2), ("turboquant", 2),
+                                            ("fp16", 8), ("turboquant", 8)])
 def test_decoder_qwen_layout_free_running(dev, stream, model, kv_cache, batch):
     cfg = dict(CFG, batch=batch)
     print(f"decoder qwen layout kv={kv_cache} batch={batch}", flush=True)
@@ -107,14 +112,6 @@ def test_decoder_qwen_layout_free_running(dev, stream, model, kv_cache, batch):
         tok = rng.integers(0, cfg["vocab_size"], batch).astype(np.uint32)
         d.step(stream, dev.upload(tok), logits)
         stream.sync()
-        got = logits.read()
         want = {name: r.step(tok.astype(np.int64)) for name, r in refs.items()}
-        sens = rel_l2(want["B32"], want["B"])
-        ab = rel_l2(want["A"], want["B"])
-        gb, ga = rel_l2(got, want["B"]), rel_l2(got, want["A"])
-        print(f"  step {step}: GPU-B {gb:.2e}  GPU-A {ga:.2e}  | oracle spread B32-B {sens:.2e}  A-B {ab:.2e}",
-              flush=True)
-        assert np.all(np.isfinite(got))
-        assert gb <= max(1e-3, 2 * sens), f"step {step}: rel(GPU, B) {gb:.3e} vs oracle spread {sens:.3e}"
-        assert ga <= max(1e-3, ab + 2 * sens), f"step {step}: rel(GPU, A) {ga:.3e} vs A-B {ab:.3e}"
+        assert_decoder_logits(logits.read(), want["A"], want["B"], want["B32"], f"  step {step}")
     assert np.array_equal(d.sync_positions(stream), start + STEPS)

@@ -55,6 +55,8 @@ def int8_problem(n, k, b, seed, awq):
     (9728, 2560, 4, True),     # band kernel, 5-tile bands, four batch rows
     (300, 5120, 1, False),     # band kernel, fewer bands than compute units
     (9728, 2560, 8, False),    # gate / up shape, batch 8
+    (9728, 256, 2, False),     # band kernel with fewer threads (64) than outputs (80): looped epilogue
+    (9728, 256, 4, True),      # one wave against 160 outputs per band
 ])
 def test_int8_projection(dev, stream, n, k, b, awq):
     print(f"int8 projection n={n} k={k} b={b} awq={awq}", flush=True)
@@ -106,6 +108,8 @@ def test_quantize_input_q8_bit_exact(dev, stream, t, k):
     (1000, 1024, 17),          # two token tiles, ragged
     (9728, 2560, 1),           # gate / up
     (2560, 9728, 1),           # down
+    (3072, 1024, 8),           # Qwen3-0.6B gate / up: one wave against 128 outputs per band
+    (30000, 1024, 8),          # tall matrix, 5-tile bands: two waves against 320 outputs per band
 ])
 def test_int4xq8_matvec(dev, stream, n, k, t):
     print(f"int4xq8 n={n} k={k} t={t}", flush=True)

@@ -34,9 +34,9 @@ from test_gpu_decode import CFG, make_model
 pytestmark = pytest.mark.gpu
 
 
-def build(dev, model, kv_cache, windows=None):
+def build(dev, model, kv_cache, windows=None, cfg=CFG):
     host_layers, dev_layers, emb, fnorm, lm = model
-    d = ops.Decoder(dev, kv_cache=kv_cache, window_sizes=windows, **CFG)
+    d = ops.Decoder(dev, kv_cache=kv_cache, window_sizes=windows, **cfg)
     for l, dl in enumerate(dev_layers):
         d.set_layer(l, **{k: v for k, v in dl.items() if not k.startswith("_")})
     d._keep_lm = ops.AffineQuantizedWeight(dev, lm)
@@ -51,29 +51,34 @@ def check(got, ref_logits, exact_logits, what):
     assert r <= 1e-3 + spread, f"{what}: rel-L2 {r:.3e} against the CPU path"
 
 
-@pytest.mark.parametrize("kv_cache,T,windows", [
-    ("fp16", 7, None),
-    ("turboquant", 7, None),
-    ("fp16", 20, None),           # 40 rows: the GEMM ops
-    ("turboquant", 20, None),
+@pytest.mark.parametrize("kv_cache,T,windows,batch", [
+    ("fp16", 7, None, 2),
+    ("turboquant", 7, None, 2),
+    ("fp16", 20, None, 2),           # 40 rows: the GEMM ops
+    ("turboquant", 20, None, 2),
     # sliding-window layers: the chunk fills the rings up to 12 of 12 and 16 slots, the
     # decode steps after it wrap the smaller one
-    ("fp16", 7, [0, 16, 12]),
-    ("turboquant", 7, [0, 16, 12]),
+    ("fp16", 7, [0, 16, 12], 2),
+    ("turboquant", 7, [0, 16, 12], 2),
+    # one sequence: a 7-row chunk, then the decoder's one-row launches
+    ("fp16", 7, None, 1),
+    ("turboquant", 7, None, 1),
+    ("turboquant", 33, None, 1),     # 33 rows: the GEMM ops with one sequence
 ])
-def test_prefill_matches_stepwise_reference(dev, stream, kv_cache, T, windows):
+def test_prefill_matches_stepwise_reference(dev, stream, kv_cache, T, windows, batch):
+    cfg = dict(CFG, batch=batch)
     model = make_model(dev, 93)
-    d = build(dev, model, kv_cache, windows)
+    d = build(dev, model, kv_cache, windows, cfg)
     host_layers, _, emb, fnorm, lm = model
     kw = dict(kv_cache=kv_cache, window_sizes=windows)
-    ref = O.DecoderReference(CFG, host_layers, emb, fnorm, lm, **kw)
-    exact = O.DecoderReference(CFG, host_layers, emb, fnorm, lm, weights="exact", acc="f64", **kw)
-    start = np.array([0, 5], np.int32)
+    ref = O.DecoderReference(cfg, host_layers, emb, fnorm, lm, **kw)
+    exact = O.DecoderReference(cfg, host_layers, emb, fnorm, lm, weights="exact", acc="f64", **kw)
+    start = np.array([0, 5] if batch == 2 else [5], np.int32)
     d.reset(stream, start)
     ref.positions = start.copy()
     exact.positions = start.copy()
-    rng = np.random.default_rng(T)
-    B, V = CFG["batch"], CFG["vocab_size"]
+    rng = np.random.default_rng(T + 100 * batch)
+    B, V = batch, cfg["vocab_size"]
     logits = dev.empty((B, V), np.float16)
     chunk = rng.integers(0, V, (B, T)).astype(np.uint32)
     d.prefill(stream, dev.upload(chunk), T, logits)

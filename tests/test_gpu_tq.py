@@ -209,7 +209,7 @@ def fill_cache_blocks(dev, stream, tq, batch, nkv, ctx, block, seed):
     return cache
 
 
-@pytest.mark.parametrize("batch,ctx", [(8, 2048), (8, 8192), (16, 8192), (16, 32768)])
+@pytest.mark.parametrize("batch,ctx", [(1, 2048), (8, 2048), (8, 8192), (16, 8192), (8, 32768), (16, 32768)])
 def test_attention_benchmarked_shapes(dev, stream, tq, tables, batch, ctx):
     """Every (batch, context) of configs[2] that the benchmark reports beyond the cases
     above: all rows against the oracle, and the automatic split against one split (the

@@ -226,6 +226,43 @@ def test_chacha_block_rfc8439():
     assert bytes(ks.tolist()).hex() == "76b8e0ada0f13d90405d6ae55386bd28"
 
 
+def test_chacha_zero_key_vectors():
+    """The block function at 8, 12 and 20 rounds (draft-strombergson-chacha-test-vectors,
+    TC1: 256-bit all-zero key and IV, keystream blocks 1 and 2), and StdRng's stream layout:
+    keyed with zeros, its u64 draws are those blocks' words in order (64-bit counter from 0 in
+    words 12-13, stream words 0, low word first)."""
+    tc1 = {8: "3e00ef2f895f40d67f5bb8e81f09a5a12c840ec3ce9a7f3b181be188ef711a1e"
+              "984ce172b9216f419f445367456d5619314a42a3da86b001387bfdb80e0cfe42",
+           12: "9bf49a6a0755f953811fce125f2683d50429c3bb49e074147e0089a52eae155f"
+               "0564f879d27ae3c02ce82834acfa8c793a629f2ca0de6919610be82f411326be",
+           20: "76b8e0ada0f13d90405d6ae55386bd28bdd219b8a08ded1aa836efcc8b770dc7"
+               "da41597c5157488d7724e03fb8d84a376a43b8f41518a11cc387b669b2ee6586"}
+    block2_20 = ("9f07e7be5551387a98ba977c732d080dcb0f29a048e3656912c6533e32ee7aed"
+                 "29b721769ce64e43d57133b074d839d531ed1f28510afb45ace10a1f4b794d6f")
+    st = np.zeros(16, np.uint32)
+    st[:4] = [0x61707865, 0x3320646E, 0x79622D32, 0x6B206574]
+    for rounds, hexs in tc1.items():
+        assert O.chacha_block(st, rounds).astype("<u4").tobytes().hex() == hexs, rounds
+    st[12] = 1
+    assert O.chacha_block(st, 20).astype("<u4").tobytes().hex() == block2_20
+    draws = O.stdrng_stream(8, key=np.zeros(8, np.uint32))
+    assert draws.astype("<u8").tobytes().hex() == tc1[12]
+
+
+def test_pcg32_demo_sequence():
+    """PCG32's LCG step and XSH-RR output against the pcg32 reference demo (pcg32_srandom_r
+    with initstate 42, initseq 54: increment 2*54+1, state advanced, plus 42, advanced;
+    each output is XSH-RR of the state before the next step)."""
+    inc = (54 << 1) | 1
+    s = O.pcg32_advance(0, inc)
+    s = O.pcg32_advance(s + 42, inc)
+    got = []
+    for _ in range(6):
+        got.append(O.pcg32_xsh_rr(s))
+        s = O.pcg32_advance(s, inc)
+    assert got == [0xA15C02B7, 0x7B47F409, 0xBA1D3330, 0x83D2F293, 0xBFA4784B, 0xCBED606E]
+
+
 def test_lloyd_max_textbook_centroids():
     # Max (1960), unit-variance Gaussian: sigma = 1 at dim = 1
     cases = {1: [0.7979], 2: [0.4528, 1.5104], 3: [0.2451, 0.7560, 1.3440, 2.1520]}
@@ -412,7 +449,8 @@ def test_tq_attention_empty_sequence_is_zero(tabs):
 
 
 def test_tq_attention_matches_float_attention_on_dequantized_cache(tabs):
-    """The QJL term is a correction: with it, scores track the exact q.k closer than without."""
+    """The attention over a written cache stays near float attention on the unquantized rows
+    (the QJL term itself is pinned by test_tq_attention_qjl_term_statistics)."""
     rng = np.random.default_rng(11)
     ctx = 64
     k = rng.standard_normal((1, 1, ctx, 1, 128)).astype(np.float16)
@@ -425,6 +463,66 @@ def test_tq_attention_matches_float_attention_on_dequantized_cache(tabs):
     w = np.exp(s - s.max())
     exact = (w / w.sum()) @ vf
     assert np.linalg.norm(out[0, 0] - exact) / np.linalg.norm(exact) < 0.1
+
+
+def _tq_scores(tabs, k16, q16, r_scale, attn_scale):
+    """The oracle's attention score of each (K row, query) pair, read back through its softmax:
+    sequence i holds the K row at position 0 and, at position 1, a row of scale 0 (score 0
+    exactly); V is a constant code c at position 0 (scale 1) and scale 0 at position 1.  The
+    output is then R (sigmoid(s) vcb[c] 1), so sigmoid(s) = <out, R v0> / |R v0|^2.
+    r_scale multiplies the r-norms the QJL term reads (1: as written)."""
+    n = k16.shape[0]
+    kc, ks, kr = O.tq_cache_write(k16[:, None, None, :], tabs, True, 2)
+    c = int(np.argmax(np.abs(tabs.v_codebook)))
+    vc = np.zeros_like(kc)
+    vc[:, 0, 0, :] = c
+    vs = np.zeros_like(ks)
+    vs[:, 0, 0] = 1.0
+    out = O.tq_attention(q16[:, None, :], tabs, kc, vc, ks, vs, kr * np.float32(r_scale), 2, attn_scale,
+                         nthreads=8)[:, 0, :].astype(np.float64)
+    rv0 = O.hadamard_rotate(np.full(128, tabs.v_codebook[c], np.float32), tabs.signs).astype(np.float64)
+    p = out @ rv0 / (rv0 @ rv0)
+    assert n == p.size and np.all((p > 0) & (p < 1))
+    return np.log(p / (1 - p)) / attn_scale
+
+
+def _qjl_checks(qjl, resid):
+    """(slope of the QJL term on the exact residual product, mean squared score error with the
+    term over the error without it)."""
+    slope = float(qjl @ resid / (resid @ resid))
+    ratio = float(np.mean((resid - qjl) ** 2) / np.mean(resid ** 2))
+    return slope, ratio
+
+
+def _qjl_ok(slope, ratio):
+    return abs(slope - 2 / math.pi) <= 0.05 * (2 / math.pi) and 0.70 <= ratio <= 0.84
+
+
+def test_tq_attention_qjl_term_statistics(tabs):
+    """The QJL correction of the K scores (turboquant.metal:292-305, 344-351): score =
+    attn_scale (<q_rot, kcb[idx]> ks + sum_d s_q[d] sign_d r_norm ks sqrt(2/pi) / d), with
+    s_q = S q_rot and sign_d = sign((S r)_d), r = u - kcb[idx] the write's residual.  For a
+    Gaussian S, E[sign((S r)_d) (S q)_d] = sqrt(2/pi) <q, r> / |r|, so the term estimates
+    (2/pi) <q_rot, r> ks -- the biased estimator the shader's comment documents -- with
+    variance (2/pi) |q|^2 |r|^2 ks^2 / d.  Over 16000 random (K row, query) pairs:
+      * the term regressed on the exact residual product <q, x> - <q_rot, kcb[idx]> ks has
+        slope 2/pi within 5 % (measured 0.643 against 0.637; ~1.5 % standard error);
+      * it lowers the mean squared score error against the exact q.x to
+        1 - 4/pi + 4/pi^2 + 2/pi = 0.769 of its value without the term (measured 0.764).
+    A sign-flipped, removed or doubled term (planted below in the oracle's inputs: the
+    r-norms it reads times -1, 0, 2) fails."""
+    rng = np.random.default_rng(3)
+    n, att = 16000, 1 / math.sqrt(128)
+    k16 = rng.standard_normal((n, 128)).astype(np.float16)
+    q16 = rng.standard_normal((n, 128)).astype(np.float16)
+    exact = np.einsum("ij,ij->i", k16.astype(np.float64), q16.astype(np.float64))
+    s_cb = _tq_scores(tabs, k16, q16, 0.0, att)           # the codebook term alone
+    resid = exact - s_cb
+    slope, ratio = _qjl_checks(_tq_scores(tabs, k16, q16, 1.0, att) - s_cb, resid)
+    assert _qjl_ok(slope, ratio), f"slope {slope:.4f} (2/pi {2 / math.pi:.4f}), error ratio {ratio:.3f}"
+    for planted in (-1.0, 0.0, 2.0):
+        ps, pr = _qjl_checks(_tq_scores(tabs, k16, q16, planted, att) - s_cb, resid)
+        assert not _qjl_ok(ps, pr), f"r-norms x {planted}: slope {ps:.4f}, ratio {pr:.3f} passed"
 
 
 def test_tq_attention_long_context_exposes_f16_codebook_bias(tabs):
