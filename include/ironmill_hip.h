@@ -233,6 +233,20 @@ int imh_encode_quantize_input_q8(imh_stream *stream, const uint16_t *x, uint32_t
 int imh_encode_affine_matvec_int4xq8(imh_stream *stream, const int8_t *q8, const float *q8_scales,
                                      uint32_t token_count, const imh_affine_int4_weight *w, uint16_t *y);
 
+/* The decode projection on Q8 activations from the f16 row (pipeline.rs:639-664
+ * then projection.rs:123-143: encode_quantize_input_q8 followed by
+ * encode_affine_matvec_int4xq8) in one launch at 1-8 rows: each workgroup
+ * quantizes the row groups it stages with quantize_input_q8's arithmetic, so y
+ * equals imh_encode_quantize_input_q8 + imh_encode_affine_matvec_int4xq8 bit for
+ * bit.  q8_out [token_count][k] / q8_scales_out [token_count][k/128] (both or
+ * neither; 16-byte aligned) receive the codes and scales for reuse by the
+ * layer's other projections, as the reference reuses them.  Above 8 rows, or
+ * for shapes outside the one-launch kernel, the two launches run (codes in
+ * q8_out, or in the stream's scratch memory).  w->awq_scales must be NULL. */
+int imh_encode_affine_projection_int4_q8(imh_stream *stream, const uint16_t *x, uint32_t token_count,
+                                         const imh_affine_int4_weight *w, uint16_t *y, int8_t *q8_out,
+                                         float *q8_scales_out);
+
 /* FusedResidualNormAffineInt4Params (ops/fused.rs:45-66) with a token count. */
 typedef struct {
     const uint16_t *a;           /* [token_count][k] */

@@ -243,6 +243,7 @@ SIGNATURES = {
     "imh_diag_valu_matvec": (I, [P, P, U32, C.POINTER(AffineInt4Weight), P]),
     "imh_encode_quantize_input_q8": (I, [P, P, U32, U32, P, P]),
     "imh_encode_affine_matvec_int4xq8": (I, [P, P, P, U32, C.POINTER(AffineInt4Weight), P]),
+    "imh_encode_affine_projection_int4_q8": (I, [P, P, U32, C.POINTER(AffineInt4Weight), P, P, P]),
     "imh_encode_fused_residual_norm_affine_matvec_int4": (I, [P, C.POINTER(FusedResidualNormParams)]),
     "imh_tq_tables_create": (I, [P, U32, U32, C.c_uint64, C.POINTER(P)]),
     "imh_tq_tables_create_from_host": (I, [P, U32, U32, P, P, P, P, P, P, C.POINTER(P)]),

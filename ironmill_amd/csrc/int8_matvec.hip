@@ -541,12 +541,52 @@ __global__ void __launch_bounds__(64 * kMaxWaves) int4xq8_matvec_kernel(
 // int32 sums.  LDS: q8 image [B][K + 16], per-group q8 sums [G][8] int32 and
 // activation scales [G][8] f32, the band's scales and zero points [rows][G]
 // f16; the wave partials overlay them, summed in (wave, h) order.
+// FQ: the activation arrives as f16 and every workgroup quantizes it while it
+// stages it, with quantize_input_q8's arithmetic (q8_quantize_kernel: the
+// group's absmax over its 8 chunk lanes, scale = m / 127, q = clamp(rint(v *
+// (127 / m)), -127, 127)), so the codes and scales are those the separate
+// launch writes; workgroup 0 also stores them when q8_out is set.
 __host__ __device__ inline size_t q8_band_lds(int K, int B, int G, int TM) {
     return (size_t)B * (K + 16) + (size_t)G * 8 * 8 + (size_t)TM * 8 * G * 4;
 }
 
-template <int TM, int NPW>
+// 16 f16 activations (two 16-byte halves) -> 16 Q8 codes packed little-endian,
+// and the group's scale; the 8 chunks of a group are 8 consecutive lanes
+__device__ __forceinline__ u32x4_t q8_chunk(const u32x4_t &xa, const u32x4_t &xb, float &scale) {
+    const _Float16 *h0 = reinterpret_cast<const _Float16 *>(&xa);
+    const _Float16 *h1 = reinterpret_cast<const _Float16 *>(&xb);
+    float v[16];
+    float m = 0.0f;
+#pragma unroll
+    for (int i = 0; i < 8; i++) {
+        v[i] = (float)h0[i];
+        v[8 + i] = (float)h1[i];
+    }
+#pragma unroll
+    for (int i = 0; i < 16; i++) m = fmaxf(m, fabsf(v[i]));
+    m = fmaxf(m, __shfl_xor(m, 1));
+    m = fmaxf(m, __shfl_xor(m, 2));
+    m = fmaxf(m, __shfl_xor(m, 4));
+    scale = m / 127.0f;
+    const float inv = m > 0.0f ? 127.0f / m : 0.0f;
+    u32x4_t out;
+#pragma unroll
+    for (int d = 0; d < 4; d++) {
+        uint32_t word = 0;
+#pragma unroll
+        for (int e = 0; e < 4; e++) {
+            const int qv = (int)fminf(fmaxf(rintf(v[4 * d + e] * inv), -127.0f), 127.0f);
+            word |= ((uint32_t)qv & 0xFFu) << (8 * e);
+        }
+        out[d] = word;
+    }
+    return out;
+}
+
+template <int TM, int NPW, bool FQ>
 __global__ void __launch_bounds__(1024) int4xq8_band_kernel(const int8_t *__restrict__ q8, const float *__restrict__ q8_scales,
+                                                            const __half *__restrict__ x16, int8_t *__restrict__ q8_out,
+                                                            float *__restrict__ q8s_out,
                                                             const uint8_t *__restrict__ w, const __half *__restrict__ scales,
                                                             const __half *__restrict__ zeros, __half *__restrict__ y, int N,
                                                             int K, int B) {
@@ -565,13 +605,23 @@ __global__ void __launch_bounds__(1024) int4xq8_band_kernel(const int8_t *__rest
     float *gscl = reinterpret_cast<float *>(gsum + G * 8);
     __half *szl = reinterpret_cast<__half *>(gscl + G * 8);
     const int nsz = (re - rb) * G;
+    const bool store_q8 = FQ && q8_out && blockIdx.x == 0;
 
-    // (a) the first q8 chunk per thread, the band's scales / zero points,
-    // then this wave's weights (a buffer resource over the band's rows: lanes
-    // past it, or past the row's last group, read zeros or are discarded)
+    // (a) the first activation chunk per thread (16 q8 codes, or FQ: their 16
+    // f16 values), the band's scales / zero points, then this wave's weights
+    // (a buffer resource over the band's rows: lanes past it, or past the
+    // row's last group, read zeros or are discarded)
     const int cpr = K / 16, nch = B * cpr;
     const int c0 = min(tid, nch - 1);
-    const u32x4_t x0 = *reinterpret_cast<const u32x4_t *>(q8 + (size_t)(c0 / cpr) * K + (size_t)(c0 % cpr) * 16);
+    u32x4_t x0, x0b;
+    if constexpr (FQ) {
+        const __half *src = x16 + (size_t)(c0 / cpr) * K + (size_t)(c0 % cpr) * 16;
+        x0 = *reinterpret_cast<const u32x4_t *>(src);
+        x0b = *reinterpret_cast<const u32x4_t *>(src + 8);
+    } else {
+        x0 = *reinterpret_cast<const u32x4_t *>(q8 + (size_t)(c0 / cpr) * K + (size_t)(c0 % cpr) * 16);
+        x0b = x0;
+    }
     const int e0 = min(tid, nsz - 1);
     const __half s0 = scales[(size_t)rb * G + e0], z0 = zeros[(size_t)rb * G + e0];
     constexpr uint32_t kRsrcWord3 = 0x00020000u;
@@ -586,9 +636,13 @@ __global__ void __launch_bounds__(1024) int4xq8_band_kernel(const int8_t *__rest
                 u32x4_t, __builtin_amdgcn_raw_buffer_load_b128(
                              w_r, (8 * t + r) * (K / 2) + (2 * (p0 + min(i, np - 1)) + h) * 64 + kq * 16, 0, 0));
     // (b) q8 rows into LDS with each group's sum (8 consecutive lanes per group)
-    auto stage = [&](int c, const u32x4_t &v) {
+    auto stage = [&](int c, const u32x4_t &xa, const u32x4_t &xb) {
         const int b = c / cpr, ci = c - b * cpr;
+        float scl = 0.0f;
+        u32x4_t v = xa;
+        if constexpr (FQ) v = q8_chunk(xa, xb, scl);
         *reinterpret_cast<u32x4_t *>(img + (size_t)b * RS + ci * 16) = v;
+        if (store_q8) *reinterpret_cast<u32x4_t *>(q8_out + (size_t)b * K + ci * 16) = v;
         int sum = 0;
 #pragma unroll
         for (int d = 0; d < 4; d++) sum = __builtin_amdgcn_sdot4((int)v[d], 0x01010101, sum, false);
@@ -597,13 +651,25 @@ __global__ void __launch_bounds__(1024) int4xq8_band_kernel(const int8_t *__rest
         sum += __shfl_xor(sum, 4);
         if ((ci & 7) == 0) {
             gsum[(ci >> 3) * 8 + b] = sum;
-            gscl[(ci >> 3) * 8 + b] = q8_scales[(size_t)b * G + (ci >> 3)];
+            if constexpr (!FQ) scl = q8_scales[(size_t)b * G + (ci >> 3)];
+            gscl[(ci >> 3) * 8 + b] = scl;
+            if (store_q8) q8s_out[(size_t)b * G + (ci >> 3)] = scl;
         }
     };
     // nch is a multiple of 8: the 8 lanes of a group pass or fail each bound together
-    if (tid < nch) stage(tid, x0);
-    for (int c = tid + nthr; c < nch; c += nthr)
-        stage(c, *reinterpret_cast<const u32x4_t *>(q8 + (size_t)(c / cpr) * K + (size_t)(c % cpr) * 16));
+    if (tid < nch) stage(tid, x0, x0b);
+    for (int c = tid + nthr; c < nch; c += nthr) {
+        u32x4_t xa, xb;
+        if constexpr (FQ) {
+            const __half *src = x16 + (size_t)(c / cpr) * K + (size_t)(c % cpr) * 16;
+            xa = *reinterpret_cast<const u32x4_t *>(src);
+            xb = *reinterpret_cast<const u32x4_t *>(src + 8);
+        } else {
+            xa = *reinterpret_cast<const u32x4_t *>(q8 + (size_t)(c / cpr) * K + (size_t)(c % cpr) * 16);
+            xb = xa;
+        }
+        stage(c, xa, xb);
+    }
     if (tid < nsz) {
         szl[tid] = s0;
         szl[nsz + tid] = z0;
@@ -678,23 +744,40 @@ __global__ void __launch_bounds__(1024) int4xq8_band_kernel(const int8_t *__rest
     }
 }
 
-template <int TM, int NPW>
-bool launch_q8_band(hipStream_t st, int nwg, int waves, size_t lds, const int8_t *q8, const float *q8s, const uint8_t *w,
-                    const __half *sc, const __half *zr, __half *y, int N, int K, int B) {
-    if (lds > 64 * 1024 && hipFuncSetAttribute(reinterpret_cast<const void *>(int4xq8_band_kernel<TM, NPW>),
+// The activation of the band launch: Q8 codes and scales, or (FQ) f16 rows
+// quantized in the launch, optionally writing the codes and scales.
+struct Q8Src {
+    const int8_t *q8;
+    const float *q8s;
+    const __half *x16;
+    int8_t *q8_out;
+    float *q8s_out;
+};
+
+template <int TM, int NPW, bool FQ>
+bool launch_q8_band_t(hipStream_t st, int nwg, int waves, size_t lds, const Q8Src &src, const uint8_t *w,
+                      const __half *sc, const __half *zr, __half *y, int N, int K, int B) {
+    if (lds > 64 * 1024 && hipFuncSetAttribute(reinterpret_cast<const void *>(int4xq8_band_kernel<TM, NPW, FQ>),
                                                hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds) != hipSuccess) {
         (void)hipGetLastError();
         return false;
     }
-    hipLaunchKernelGGL((int4xq8_band_kernel<TM, NPW>), dim3(nwg), dim3(64 * waves), lds, st, q8, q8s, w, sc, zr, y, N, K,
-                       B);
+    hipLaunchKernelGGL((int4xq8_band_kernel<TM, NPW, FQ>), dim3(nwg), dim3(64 * waves), lds, st, src.q8, src.q8s,
+                       src.x16, src.q8_out, src.q8s_out, w, sc, zr, y, N, K, B);
     return true;
+}
+
+template <int TM, int NPW>
+bool launch_q8_band(hipStream_t st, int nwg, int waves, size_t lds, const Q8Src &src, const uint8_t *w,
+                    const __half *sc, const __half *zr, __half *y, int N, int K, int B) {
+    return src.x16 ? launch_q8_band_t<TM, NPW, true>(st, nwg, waves, lds, src, w, sc, zr, y, N, K, B)
+                   : launch_q8_band_t<TM, NPW, false>(st, nwg, waves, lds, src, w, sc, zr, y, N, K, B);
 }
 
 // Band shape as for the INT8 band kernel, over group pairs; 1-8 batch rows.
 // Returns false (nothing launched) outside its limits.
-bool q8_band_launch(hipStream_t st, int cus, const int8_t *q8, const float *q8s, const uint8_t *w, const __half *sc,
-                    const __half *zr, __half *y, int N, int K, int B) {
+bool q8_band_launch(hipStream_t st, int cus, const Q8Src &src, const uint8_t *w, const __half *sc, const __half *zr,
+                    __half *y, int N, int K, int B) {
     const int G = K / kGS, GP = (G + 1) / 2;
     if (B < 1 || B > 8) return false;
     int nwg = std::min(cus, (N + 7) / 8);
@@ -706,11 +789,11 @@ bool q8_band_launch(hipStream_t st, int cus, const int8_t *q8, const float *q8s,
     const size_t lds = std::max(q8_band_lds(K, B, G, TM), (size_t)waves * TM * 64 * sizeof(float4_t));
     if (lds > 156 * 1024) return false;
     switch (TM) {
-        case 1: return launch_q8_band<1, 8>(st, nwg, waves, lds, q8, q8s, w, sc, zr, y, N, K, B);
-        case 2: return launch_q8_band<2, 5>(st, nwg, waves, lds, q8, q8s, w, sc, zr, y, N, K, B);
-        case 3: return launch_q8_band<3, 3>(st, nwg, waves, lds, q8, q8s, w, sc, zr, y, N, K, B);
-        case 4: return launch_q8_band<4, 2>(st, nwg, waves, lds, q8, q8s, w, sc, zr, y, N, K, B);
-        default: return launch_q8_band<5, 2>(st, nwg, waves, lds, q8, q8s, w, sc, zr, y, N, K, B);
+        case 1: return launch_q8_band<1, 8>(st, nwg, waves, lds, src, w, sc, zr, y, N, K, B);
+        case 2: return launch_q8_band<2, 5>(st, nwg, waves, lds, src, w, sc, zr, y, N, K, B);
+        case 3: return launch_q8_band<3, 3>(st, nwg, waves, lds, src, w, sc, zr, y, N, K, B);
+        case 4: return launch_q8_band<4, 2>(st, nwg, waves, lds, src, w, sc, zr, y, N, K, B);
+        default: return launch_q8_band<5, 2>(st, nwg, waves, lds, src, w, sc, zr, y, N, K, B);
     }
 }
 
@@ -801,8 +884,9 @@ int imh_encode_affine_matvec_int4xq8(imh_stream *stream, const int8_t *q8, const
     rc = imh::use_device(stream->dev);
     if (rc) return rc;
     const int N = (int)w->n, K = (int)w->k, G = K / kGS;
+    const Q8Src src = {q8, q8_scales, nullptr, nullptr, nullptr};
     if (token_count <= 8 &&
-        q8_band_launch(stream->stream, stream->dev->props.multiProcessorCount, q8, q8_scales, w->data,
+        q8_band_launch(stream->stream, stream->dev->props.multiProcessorCount, src, w->data,
                        reinterpret_cast<const __half *>(w->scales), reinterpret_cast<const __half *>(w->zeros),
                        reinterpret_cast<__half *>(y), N, K, (int)token_count)) {
         IMH_HIP(hipGetLastError());
@@ -818,6 +902,48 @@ int imh_encode_affine_matvec_int4xq8(imh_stream *stream, const int8_t *q8, const
                        (int)token_count, SG);
     IMH_HIP(hipGetLastError());
     return IMH_OK;
+}
+
+int imh_encode_affine_projection_int4_q8(imh_stream *stream, const uint16_t *x, uint32_t token_count,
+                                         const imh_affine_int4_weight *w, uint16_t *y, int8_t *q8_out,
+                                         float *q8_scales_out) {
+    const char *who = "imh_encode_affine_projection_int4_q8";
+    if (!stream || !x || !y) return imh::fail(IMH_EINVAL, std::string(who) + ": NULL argument");
+    int rc = check_w(w, who);
+    if (rc) return rc;
+    if (w->awq_scales)
+        return imh::fail(IMH_EINVAL, std::string(who) + ": the Q8 path has no AWQ division (pipeline.rs:639-664)");
+    if ((q8_out == nullptr) != (q8_scales_out == nullptr))
+        return imh::fail(IMH_EINVAL, std::string(who) + ": q8_out and q8_scales_out are both given or both NULL");
+    if ((reinterpret_cast<uintptr_t>(x) | reinterpret_cast<uintptr_t>(q8_out)) & 15)
+        return imh::fail(IMH_EINVAL, std::string(who) + ": x and q8_out must be 16-byte aligned");
+    if (token_count == 0) return IMH_OK;
+    if (token_count > 65535) return imh::fail(IMH_EINVAL, std::string(who) + ": token_count above 65535");
+    rc = imh::use_device(stream->dev);
+    if (rc) return rc;
+    const int N = (int)w->n, K = (int)w->k, G = K / kGS;
+    const Q8Src src = {nullptr, nullptr, reinterpret_cast<const __half *>(x), q8_out, q8_scales_out};
+    if (token_count <= 8 &&
+        q8_band_launch(stream->stream, stream->dev->props.multiProcessorCount, src, w->data,
+                       reinterpret_cast<const __half *>(w->scales), reinterpret_cast<const __half *>(w->zeros),
+                       reinterpret_cast<__half *>(y), N, K, (int)token_count)) {
+        IMH_HIP(hipGetLastError());
+        return IMH_OK;
+    }
+    // outside the band kernel's shapes: the two launches, the codes in the
+    // caller's buffers or the stream's scratch memory
+    int8_t *q8 = q8_out;
+    float *q8s = q8_scales_out;
+    if (!q8) {
+        void *scr = nullptr;
+        const size_t code_bytes = ((size_t)token_count * K + 255) & ~(size_t)255;
+        rc = imh::stream_scratch(stream, 0, code_bytes + (size_t)token_count * G * sizeof(float), &scr);
+        if (rc) return rc;
+        q8 = static_cast<int8_t *>(scr);
+        q8s = reinterpret_cast<float *>(static_cast<uint8_t *>(scr) + code_bytes);
+    }
+    rc = imh_encode_quantize_input_q8(stream, x, token_count, (uint32_t)K, q8, q8s);
+    return rc ? rc : imh_encode_affine_matvec_int4xq8(stream, q8, q8s, token_count, w, y);
 }
 
 }  // extern "C"

@@ -95,6 +95,15 @@ def encode_affine_matvec_int4xq8(stream: Stream, q8, q8_scales, token_count: int
                                                C.byref(weight.c), _ptr(y)))
 
 
+def encode_projection_int4_q8(stream: Stream, x, weight: AffineQuantizedWeight, y, token_count: int,
+                              q8_out=None, q8_scales_out=None):
+    """The decode projection on Q8 activations quantized from the f16 rows x in the same launch
+    (quantize.metal:21-52 then affine_fused.metal:115-176; pipeline.rs:639-664); optionally
+    writes the codes / scales for the layer's other projections."""
+    check(lib.imh_encode_affine_projection_int4_q8(stream.handle, _ptr(x), token_count, C.byref(weight.c), _ptr(y),
+                                                   _ptr(q8_out), _ptr(q8_scales_out)))
+
+
 PROBE_TILE, PROBE_FLAT, PROBE_BAND = 0, 1, 2
 
 

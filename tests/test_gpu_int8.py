@@ -141,6 +141,43 @@ def test_int4xq8_matvec(dev, stream, n, k, t):
     assert r <= 2e-2
 
 
+@pytest.mark.parametrize("n,k,t,codes", [
+    (9728, 2560, 1, True),     # gate / up shape, codes written for reuse
+    (9728, 2560, 1, False),
+    (2560, 9728, 1, True),     # down shape
+    (4096, 2560, 8, True),     # eight rows
+    (3072, 1024, 8, False),    # fewer threads than outputs per band
+    (64, 128, 3, True),        # one group
+    (1000, 1024, 11, True),    # above 8 rows: the two launches, codes in the caller's buffers
+    (1000, 1024, 11, False),   # the two launches, codes in scratch memory
+])
+def test_projection_int4_q8_one_launch(dev, stream, n, k, t, codes):
+    """imh_encode_affine_projection_int4_q8 quantizes the f16 rows while it stages them: y
+    equals the quantize + matvec launches bit for bit, and the codes / scales it writes equal
+    imh_encode_quantize_input_q8's (bit-exact with the oracle)."""
+    print(f"int4 q8 one launch n={n} k={k} t={t} codes={codes}", flush=True)
+    rng = np.random.default_rng(3 * n + k + t)
+    q = quant.quantize_int4((rng.standard_normal((n, k)) * 0.02).astype(np.float32))
+    x = rng.standard_normal((t, k)).astype(np.float16)
+    x[0, :128] = 0.0                                        # an all-zero group
+    wt = ops.AffineQuantizedWeight(dev, q)
+    xd = dev.upload(x)
+    q8d, scd = dev.empty((t, k), np.int8), dev.empty((t, k // 128), np.float32)
+    y2 = dev.empty((t, n), np.float16)
+    ops.encode_quantize_input_q8(stream, xd, t, k, q8d, scd)
+    ops.encode_affine_matvec_int4xq8(stream, q8d, scd, t, wt, y2)
+    y1 = dev.empty((t, n), np.float16)
+    q8o = dev.empty((t, k), np.int8) if codes else None
+    sco = dev.empty((t, k // 128), np.float32) if codes else None
+    ops.encode_projection_int4_q8(stream, xd, wt, y1, t, q8o, sco)
+    stream.sync()
+    assert np.array_equal(y1.read().view(np.uint16), y2.read().view(np.uint16))
+    if codes:
+        q8, sc = O.quantize_input_q8(x)
+        assert np.array_equal(q8o.read(), q8)
+        assert np.array_equal(sco.read().view(np.uint32), sc.view(np.uint32))
+
+
 def test_int8_q8_errors(dev, stream):
     rng = np.random.default_rng(9)
     q = quant.quantize_int4((rng.standard_normal((64, 256)) * 0.02).astype(np.float32),
@@ -151,3 +188,9 @@ def test_int8_q8_errors(dev, stream):
         ops.encode_affine_matvec_int4xq8(stream, q8, sc, 1, wt, y)
     with pytest.raises(IronmillError, match="multiple of 128"):
         ops.encode_quantize_input_q8(stream, dev.empty((1, 200), np.float16), 1, 200, q8, sc)
+    with pytest.raises(IronmillError, match="no AWQ"):
+        ops.encode_projection_int4_q8(stream, dev.empty((1, 256), np.float16), wt, y, 1)
+    plain = ops.AffineQuantizedWeight(dev, quant.quantize_int4((rng.standard_normal((64, 256)) * 0.02)
+                                                               .astype(np.float32)))
+    with pytest.raises(IronmillError, match="both given or both NULL"):
+        ops.encode_projection_int4_q8(stream, dev.empty((1, 256), np.float16), plain, y, 1, q8_out=q8)
