@@ -16,7 +16,7 @@ LIBDIR = os.path.join(HERE, "lib")
 LIB = os.path.join(LIBDIR, "libironmill_hip.so")
 OBJDIR = os.path.join(HERE, "_build")
 
-SOURCES = ["runtime.hip", "int4_matvec.hip", "int4_matvec_raw.hip", "int4_matvec_mt2.hip", "int4_matvec_band.hip",
+SOURCES = ["runtime.hip", "int4_matvec.hip", "int4_matvec_raw.hip", "int4_matvec_mt2.hip", "int4_matvec_band.hip", "int4_matvec_da.hip",
            "int4_gemm.hip",
            "int4_gemm_mx.hip", "int8_matvec.hip",
            "tq_kernels.hip", "fp16_attention.hip", "glue_kernels.hip", "decoder.hip",

@@ -59,8 +59,9 @@ __global__ void __launch_bounds__(256) int4_prep_plain(const __half *__restrict_
     float sh, sl;
     chunk_operands(v, hi, lo, sh, sl);
     if (live) {
-        *reinterpret_cast<half8_t *>(xa_hi + base) = hi;
-        *reinterpret_cast<half8_t *>(xa_lo + base) = lo;
+        const size_t ib = (size_t)m * K + (size_t)img_chunk(c) * 8;
+        *reinterpret_cast<half8_t *>(xa_hi + ib) = hi;
+        *reinterpret_cast<half8_t *>(xa_lo + ib) = lo;
     }
     store_group_sums(sh, sl, live, gsum + (size_t)m * 2 * G, G, c / 16);
 }
@@ -133,18 +134,19 @@ __global__ void __launch_bounds__(256) int4_prep_resnorm(
         half8_t hi, lo;
         float sh, sl;
         chunk_operands(v, hi, lo, sh, sl);
+        const size_t ioff = row + (size_t)img_chunk(c) * 8;
         if (live) {
             *reinterpret_cast<half8_t *>(residual_out + off) = res;
             *reinterpret_cast<half8_t *>(normed_out + off) = nrm;
-            *reinterpret_cast<half8_t *>(xa_hi + off) = hi;
-            *reinterpret_cast<half8_t *>(xa_lo + off) = lo;
+            *reinterpret_cast<half8_t *>(xa_hi + ioff) = hi;
+            *reinterpret_cast<half8_t *>(xa_lo + ioff) = lo;
         }
         store_group_sums(sh, sl, live, gsum + (size_t)m * 2 * G, G, c / 16);
         if (rounded == 2) {   // uniform: the second (rounded) image
             chunk_operands(v2, hi, lo, sh, sl);
             if (live) {
-                *reinterpret_cast<half8_t *>(xa_hi2 + off) = hi;
-                *reinterpret_cast<half8_t *>(xa_lo2 + off) = lo;
+                *reinterpret_cast<half8_t *>(xa_hi2 + ioff) = hi;
+                *reinterpret_cast<half8_t *>(xa_lo2 + ioff) = lo;
             }
             store_group_sums(sh, sl, live, gsum2 + (size_t)m * 2 * G, G, c / 16);
         }
@@ -364,6 +366,7 @@ int run_matvec(imh_stream *s, ActIn in, uint32_t B, int nmat, int epi, int N, in
         hipLaunchKernelGGL(int4_prep_plain, grid, dim3(256), 0, s->stream, in.a, in.awq, hi, lo, gs, K);
     }
     IMH_HIP(hipGetLastError());
+    if (image_da_applies(nmat, (int)B, K)) return launch_image_da(s->stream, nmat, epi, N, K, (int)B, mp, in);
     return launch_image(nmat, epi, p.L, mp, in);
 }
 
@@ -495,6 +498,9 @@ int ffn_band_pair(imh_stream *s, ActIn gin, uint32_t B, const imh_affine_int4_we
         rc = launch_band_matvec(s->stream, cus, (int)B, 1, EPI_STORE, Hd, F, dm, din, &fd);
         if (rc) return rc;
         if (!fd) return imh::fail(IMH_EDEVICE, "ffn_band_pair: the down launch was refused after its probe");
+    } else if (image_da_applies(1, (int)B, F)) {
+        rc = launch_image_da(s->stream, 1, EPI_STORE, Hd, F, (int)B, dm, din);
+        if (rc) return rc;
     } else {
         rc = launch_image(1, EPI_STORE, p.L, dm, din);
         if (rc) return rc;

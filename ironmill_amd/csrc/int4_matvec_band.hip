@@ -121,7 +121,7 @@ __global__ void __launch_bounds__(512) int4_band_kernel(MatPtrs mp, const ActIn 
         if constexpr (IMG) {
 #pragma unroll
             for (int b = 0; b < BM; b++) {
-                const size_t o = (size_t)min(b, B - 1) * K + e;
+                const size_t o = (size_t)min(b, B - 1) * K + (size_t)img_chunk(c) * 8;
                 xv[i][b] = *reinterpret_cast<const u32x4_t *>(in.hi + o);
                 lv[i][b] = *reinterpret_cast<const u32x4_t *>(in.lo + o);
             }
@@ -446,7 +446,7 @@ __global__ void __launch_bounds__(512) int4_band_kernel(MatPtrs mp, const ActIn 
                     const int k = rb + r;
                     _Float16 ah, al, ch, cl;
                     pair_operands(v, v1, ah, al, ch, cl);
-                    const size_t base = (size_t)b * N + (k & ~7);
+                    const size_t base = (size_t)b * N + (size_t)img_chunk(k >> 3) * 8;
                     const int i = (k & 7) >> 1;
                     in.img_out_hi[base + i] = ah;
                     in.img_out_hi[base + 4 + i] = ch;

@@ -123,6 +123,15 @@ struct ActIn {
     int img_src;
 };
 
+// Operand images in memory (hi / lo planes [B][K]) hold each group's sixteen
+// 8-element chunks as a transposed 4 x 4 block: chunk 4a + b of a group sits
+// at position 4b + a (the map is its own inverse).  The direct-operand kernel's
+// 16-byte load j of lane quarter kq then reads chunk 4kq + j -- the chunk its
+// MFMA slot takes -- and the four quarters of a row read 64 contiguous bytes
+// per load; every other reader and writer maps chunk indices through this.
+// c: the chunk index along K (element k is in chunk k / 8).
+__host__ __device__ __forceinline__ int img_chunk(int c) { return (c & ~15) | ((c & 3) << 2) | ((c >> 2) & 3); }
+
 // Split v into f16 hi + lo with hi + lo == v to ~22 bits.
 __device__ __forceinline__ void split_hilo(float v, _Float16 &hi, _Float16 &lo) {
     hi = (_Float16)v;
@@ -340,8 +349,9 @@ int4_matvec_kernel(MatPtrs mp, ActIn in, int Nall, int K, int B, int parts, int 
         const size_t e = (size_t)gs0 * kGS + (size_t)col * 8;   // column within the row
         const size_t src = (size_t)(m0 + r) * K + e;
         if (!RAW) {
-            ch.a = *reinterpret_cast<const u32x4_t *>(ihi + src);
-            ch.b = *reinterpret_cast<const u32x4_t *>(ilo + src);
+            const size_t isrc = (size_t)(m0 + r) * K + (size_t)img_chunk(gs0 * 16 + col) * 8;
+            ch.a = *reinterpret_cast<const u32x4_t *>(ihi + isrc);
+            ch.b = *reinterpret_cast<const u32x4_t *>(ilo + isrc);
             return;
         }
         ch.a = *reinterpret_cast<const u32x4_t *>(in.a + src);
@@ -677,5 +687,11 @@ void launch_image_mt2(int nmat, int epi, const Launch &L, const MatPtrs &mp, con
 // *used is false where it does not apply.
 int launch_band_matvec(hipStream_t st, int cus, int B, int nmat, int epi, int N, int K, const MatPtrs &mp,
                        const ActIn &in, bool *used, bool probe = false);
+// The tile grid over an IMAGE source (in.hi / in.lo, in.hi2 / in.lo2 for the
+// later segments of round_mode 2, in.row_scale) with the operands read straight
+// from the image, 1-8 batch rows (int4_matvec_da.hip); the image's group sums
+// are not read (the kernel forms them on the matrix cores).
+bool image_da_applies(int nmat, int B, int K);
+int launch_image_da(hipStream_t st, int nmat, int epi, int N, int K, int B, const MatPtrs &mp, const ActIn &in);
 
 }  // namespace imh_int4
