@@ -74,6 +74,16 @@ template <int NMAT, int EPI, int TM, int NP, int BM, int XC, bool RN, bool IMG =
 __global__ void __launch_bounds__(512) int4_band_kernel(MatPtrs mp, const ActIn in, int N, int K, int B, int W) {
     const __half *__restrict__ x = in.a;
     const __half *__restrict__ awq = in.awq;
+    // every kernel argument this instantiation reads, into SGPRs here: left
+    // to itself the compiler issued some of their scalar loads ~120
+    // instructions in, a second serialized trip to the argument memory ahead
+    // of the first activation load
+    asm volatile("" ::"s"(mp.data[0]), "s"(mp.scales[0]), "s"(mp.zeros[0]), "s"(mp.out[0]), "s"(x), "s"(awq), "s"(N),
+                 "s"(K), "s"(B), "s"(W), "s"(gridDim.x), "s"(blockDim.x));
+    if constexpr (NMAT == 2) asm volatile("" ::"s"(mp.data[1]), "s"(mp.scales[1]), "s"(mp.zeros[1]), "s"(mp.out[1]));
+    if constexpr (RN) asm volatile("" ::"s"(in.b), "s"(in.gamma), "s"(in.residual_out), "s"(in.normed_out));
+    if constexpr (IMG) asm volatile("" ::"s"(in.hi), "s"(in.lo));
+    if constexpr (EPI != EPI_STORE) asm volatile("" ::"s"(in.img_out_hi), "s"(in.img_out_lo), "s"(in.img_awq));
     extern __shared__ __attribute__((aligned(16))) uint8_t lds_b[];
     const int tid = threadIdx.x, nthr = blockDim.x;
     // the wave index as a scalar, so the weight pointer it selects is uniform
