@@ -485,7 +485,9 @@ def main():
                     help="with --decode-only: time 5 eager steps only (no graph capture; for kernel traces)")
     ap.add_argument("--kernel-only", action="store_true",
                     help="only the prepared fused gate+up kernel loop (same as --kernel gate_up)")
-    ap.add_argument("--kernel", choices=["gate_up", "down", "int8", "q8", "gemm", "probe", "valu_ab"],
+    ap.add_argument("--proj", type=int, nargs=2, metavar=("N", "K"),
+                    help="with --kernel proj: the INT4 projection of an N x K weight (no AWQ; LM head: 151936 2560)")
+    ap.add_argument("--kernel", choices=["gate_up", "down", "int8", "q8", "gemm", "probe", "valu_ab", "proj"],
                     help="one kernel alone, for rocprofv3 runs: the batch-B fused gate+up or down "
                          "matvec, the INT8 down-shape matvec, the INT4 x Q8 gate-shape "
                          "quantize + matvec, the prefill GEMM (--gemm-*), the streaming probe, or the MFMA / "
@@ -566,6 +568,27 @@ def main():
         for k_, v in r.items():
             log(f"probe {k_}: {v['us']} us {v.get('GB/s', '-')} GB/s")
         print(json.dumps({"stream_probe": r}), flush=True)
+        return
+
+    if args.kernel == "proj":
+        # one INT4 projection (e.g. the LM head) at --batch, random codes and f16 scales / zero
+        # points in the upload layout, rotating over >= 512 MB of weights
+        B = args.batch
+        nn, kk = args.proj or (151936, 2560)
+        rng = np.random.default_rng(7)
+        per = nn * kk * INT4_BYTES_PER_ELEM
+        Wp = [random_int4(dev, ops, rng, nn, kk, awq=False) for _ in range(max(2, math.ceil(512e6 / per)))]
+        xp = dev.upload(make_x(B, kk, 95))
+        yp = dev.empty((B, nn), np.float16)
+        tot = (eager_loop if args.eager else time_loop)(
+            dev, stream, lambda i: ops.encode_projection(stream, xp, Wp[i % len(Wp)], yp, B), args.steps, args.warmup)
+        us = 1e3 * tot / args.steps
+        nb = per + 2 * B * (kk + nn)
+        gbs = nb / (us * 1e-6) / 1e9
+        log(f"INT4 projection {nn}x{kk} B={B}: {us:.2f} us  {gbs:.0f} GB/s ({100 * gbs / HBM_PEAK_GBS:.1f} %)")
+        print(json.dumps({"kernel": f"INT4 projection {nn}x{kk}", "batch": B, "us": round(us, 3),
+                          "GB/s": round(gbs, 1), "frac": round(gbs / HBM_PEAK_GBS, 4), "bytes": int(nb),
+                          "launches": args.steps, "eager": args.eager}))
         return
 
     if args.kernel == "int8":
@@ -751,6 +774,22 @@ def main():
                     details[f"gemm_{prec}_m{mm}_k{kk}_n{nn}"] = r
                     log(f"prefill GEMM {prec} M={mm} K={kk} N={nn}: {r['us']} us {r['TFLOP/s']} TFLOP/s "
                         f"({100 * r['frac']:.1f} % of dense {prec} MFMA)")
+        # the LM head (151936 x 2560, 206.6 MB) at one row: the INT4 decode matvec at its largest
+        # Qwen3-4B shape, where the launch floor is a small share of the launch
+        rng_lm = np.random.default_rng(7)
+        lm_per = 151936 * H * INT4_BYTES_PER_ELEM
+        WL = [random_int4(dev, ops, rng_lm, 151936, H, awq=False) for _ in range(3)]
+        xl = dev.upload(make_x(1, H, 95))
+        yl = dev.empty((1, 151936), np.float16)
+        t = time_loop(dev, stream, lambda i: ops.encode_projection(stream, xl, WL[i % 3], yl, 1),
+                      max(200, args.steps), max(200, args.warmup))
+        us = 1e3 * t / max(200, args.steps)
+        nb = lm_per + 2 * (H + 151936)
+        details["lm_head_b1"] = {"us": round(us, 2), "GB/s": round(nb / (us * 1e-6) / 1e9, 1),
+                                 "frac": round(nb / (us * 1e-6) / 1e9 / HBM_PEAK_GBS, 4), "bytes": int(nb),
+                                 "launches": max(200, args.steps)}
+        log(f"LM head B=1: {us:.2f} us ({details['lm_head_b1']['frac'] * 100:.1f} % of 8 TB/s)")
+        del WL
         details["stream_probe"] = bench_probe(dev, stream, ops, max(50, args.steps // 2), args.warmup, sweep=False)
         del W
         stream.sync()

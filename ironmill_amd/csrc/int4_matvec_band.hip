@@ -586,7 +586,11 @@ int launch_band_matvec(hipStream_t st, int cus, int B, int nmat, int epi, int N,
     // workgroup would stage the operand image of all of K for 40 rows: there
     // one band per CU, walked in blocks of 5 tiles over one staging (mb)
     const bool mb = bm > 2 && !rn && !in.img_src && nmat == 1 && epi == EPI_STORE && (ntiles + 4) / 5 > cus;
-    const int nwg = mb ? cus : std::min(std::max(cus, (ntiles + 4) / 5), N);
+    // tall matrices at 1-2 rows (the LM head): bands of 3 tiles, two waves of
+    // five pairs each -- 37.5 against 38.4 us with 5-tile bands of four waves
+    // (151936 x 2560 at one row, A/B on one box)
+    const bool tall12 = bm <= 2 && nmat == 1 && (ntiles + 4) / 5 > cus;
+    const int nwg = mb ? cus : std::min(std::max(cus, tall12 ? (ntiles + 2) / 3 : (ntiles + 4) / 5), N);
     if ((uint64_t)N * nwg >= (1ull << 32)) return IMH_OK;
     const int rows = mb ? 40 : (N + nwg - 1) / nwg;   // mb: rows per block
     const int tm = (rows + 7) / 8;

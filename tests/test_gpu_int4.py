@@ -73,7 +73,9 @@ def gpu_layout_y(q, x16, awq16=None):
     (2560, 4096, 1, True),    # Qwen3-4B O projection
     (1024, 2560, 2, False),   # Qwen3-4B K / V projection, batch 2
     (5000, 1024, 1, True),    # bands of 17-24 rows
-    (151936 // 8, 2560, 1, False),   # an LM-head-like tall matrix (bands of 5 tiles)
+    (151936 // 8, 2560, 1, False),   # an LM-head-like tall matrix (bands of 3 tiles at 1-2 rows)
+    (151936, 2560, 1, False),        # the Qwen3-4B LM head itself at one row
+    (15005, 2560, 2, True),          # tall, two rows, a ragged last band
     (151936 // 8, 2560, 4, True),    # 3-8 rows on a tall matrix: one band per CU in 5-tile blocks
     (151936 // 8, 2560, 8, False),
     (15003, 2560, 5, True),          # the same with a ragged last block
