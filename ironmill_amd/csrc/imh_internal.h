@@ -44,7 +44,7 @@ struct imh_buffer {
 // Per-stream scratch memory, grown on demand by the host code of an op.
 // Slot 0: INT4 activation operand images, the query operand planes of the
 // TurboQuant prefill attention; slot 1: attention split partials,
-// the gate output of a prefill gate/up op; slot 2: GEMM split-K partials.
+// the gate output of a prefill gate/up op; slot 2: GEMM and INT4 matvec split-K partials.
 // A graph captured on the stream records the slots' addresses, so a slot that
 // grows later keeps its old block alive (`retired`) until the stream is freed:
 // a replay never touches freed memory.

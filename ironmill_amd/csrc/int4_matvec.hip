@@ -300,6 +300,22 @@ int run_gemm(imh_stream *s, const ActIn &in, int M, const imh_affine_int4_weight
                        ws);
 }
 
+// Split-K over the image in in.hi / in.lo when it applies: one matrix, plain
+// store, no row segments or row scale (partials in stream scratch slot 2).
+int try_splitk(imh_stream *s, int nmat, int epi, int N, int K, uint32_t B, const MatPtrs &mp, const ActIn &in,
+               bool *used) {
+    *used = false;
+    const int cus = s->dev->props.multiProcessorCount;
+    if (epi != EPI_STORE || mp.seg[0] != 0 || in.row_scale || in.round_mode == 2 ||
+        !splitk_applies(nmat, (int)B, N, K, cus))
+        return IMH_OK;
+    void *ws = nullptr;
+    int rc = imh::stream_scratch(s, 2, splitk_workspace_bytes((int)B, N, K, cus), &ws);
+    if (rc) return rc;
+    *used = true;
+    return launch_splitk(s->stream, cus, N, K, (int)B, mp, in, ws);
+}
+
 // Plans and launches the matvec kernel for mp (N rows in total, segments
 // included): RAW when the workgroups can build the operand image themselves,
 // else the prep kernel writes it into stream scratch slot 0 first.
@@ -366,6 +382,11 @@ int run_matvec(imh_stream *s, ActIn in, uint32_t B, int nmat, int epi, int N, in
         hipLaunchKernelGGL(int4_prep_plain, grid, dim3(256), 0, s->stream, in.a, in.awq, hi, lo, gs, K);
     }
     IMH_HIP(hipGetLastError());
+    {
+        bool used = false;
+        rc = try_splitk(s, nmat, epi, N, K, B, mp, in, &used);
+        if (rc || used) return rc;
+    }
     if (image_da_applies(nmat, (int)B, K)) return launch_image_da(s->stream, nmat, epi, N, K, (int)B, mp, in);
     return launch_image(nmat, epi, p.L, mp, in);
 }
@@ -486,6 +507,11 @@ int ffn_band_pair(imh_stream *s, ActIn gin, uint32_t B, const imh_affine_int4_we
             imh::clear_error();
             return IMH_OK;   // a RAW down (small K) builds its own operand
         }
+        if (splitk_applies(1, (int)B, Hd, F, cus)) {   // reserve the partials before the first launch
+            void *ws = nullptr;
+            rc = imh::stream_scratch(s, 2, splitk_workspace_bytes((int)B, Hd, F, cus), &ws);
+            if (rc) return rc;
+        }
     }
     if (rn && B > 2) {
         rc = encode_resnorm_rows(s, gin.a, gin.b, gin.gamma, gin.eps, gin.residual_out, gin.normed_out, (int)B, H);
@@ -498,13 +524,20 @@ int ffn_band_pair(imh_stream *s, ActIn gin, uint32_t B, const imh_affine_int4_we
         rc = launch_band_matvec(s->stream, cus, (int)B, 1, EPI_STORE, Hd, F, dm, din, &fd);
         if (rc) return rc;
         if (!fd) return imh::fail(IMH_EDEVICE, "ffn_band_pair: the down launch was refused after its probe");
-    } else if (image_da_applies(1, (int)B, F)) {
-        rc = launch_image_da(s->stream, 1, EPI_STORE, Hd, F, (int)B, dm, din);
-        if (rc) return rc;
     } else {
-        rc = launch_image(1, EPI_STORE, p.L, dm, din);
+        bool used = false;
+        rc = try_splitk(s, 1, EPI_STORE, Hd, F, B, dm, din, &used);
         if (rc) return rc;
-        IMH_HIP(hipGetLastError());
+        if (!used && image_da_applies(1, (int)B, F)) {
+            rc = launch_image_da(s->stream, 1, EPI_STORE, Hd, F, (int)B, dm, din);
+            if (rc) return rc;
+            used = true;
+        }
+        if (!used) {
+            rc = launch_image(1, EPI_STORE, p.L, dm, din);
+            if (rc) return rc;
+            IMH_HIP(hipGetLastError());
+        }
     }
     *done = true;
     return IMH_OK;

@@ -185,7 +185,162 @@ void launch_ng_da(int ng, dim3 grid, dim3 block, size_t lds, hipStream_t st, con
         hipLaunchKernelGGL((int4_da_kernel<NMAT, EPI, 5>), grid, block, lds, st, mp, in, N, K, B, parts);
 }
 
+// Split-K over a prebuilt image, 1-8 rows: grid (bands of NT tiles, S
+// slices of K).  Workgroup (band, slice) reads the operand of its slice only
+// and the weights of its NT x 16 rows in that slice, so a CU moves ~1 / S of
+// the image the per-tile kernel reads; the band's f32 partial sums go to
+// part[slice][m][row] and int4_splitk_combine_kernel adds the slices in
+// slice order (deterministic).  Waves split the slice's groups (<= NG each);
+// each wave loads a group's A operand once (the direct-operand layout) and
+// uses it for the NT tiles' weights.
+template <int NT, int NG>
+__global__ void __launch_bounds__(1024) int4_splitk_kernel(MatPtrs mp, const ActIn in, int N, int K, int B, int S,
+                                                           float *__restrict__ part) {
+    extern __shared__ __attribute__((aligned(16))) float4_t red[];   // [NT][waves][64]
+    const int tid = threadIdx.x;
+    const int waves = blockDim.x >> 6;
+    const int lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int G = K / kGS;
+    const int slice = blockIdx.y;
+    const int gs0 = (slice * G) / S, gsn = ((slice + 1) * G) / S - gs0;
+    const int part_w = (wave + (int)blockIdx.x) % waves;   // rotated, as in the per-tile kernel
+    const int g0 = gs0 + (part_w * gsn) / waves;
+    const int ng = gs0 + ((part_w + 1) * gsn) / waves - g0;
+    const int row0 = blockIdx.x * 16 * NT;
+    const int n_l = lane & 15, kq = lane >> 4;
+
+    const uint16_t *sp0 = reinterpret_cast<const uint16_t *>(mp.scales[0]);
+    const uint16_t *zp0 = reinterpret_cast<const uint16_t *>(mp.zeros[0]);
+    int rowc[NT];
+#pragma unroll
+    for (int t = 0; t < NT; t++) rowc[t] = min(row0 + 16 * t + n_l, N - 1);
+    const int ar = (n_l & 7) < B ? (n_l & 7) : 0;
+    const _Float16 *arow = ((n_l >> 3) ? in.lo : in.hi) + (size_t)ar * K + kq * 8;
+
+    uint16_t sv[NG][NT], zv[NG][NT];
+#pragma unroll
+    for (int i = 0; i < NG; i++) {
+        const int g = g0 + min(i, max(ng - 1, 0));
+#pragma unroll
+        for (int t = 0; t < NT; t++) {
+            sv[i][t] = sp0[(size_t)rowc[t] * G + g];
+            zv[i][t] = zp0[(size_t)rowc[t] * G + g];
+        }
+    }
+    u32x4_t wq[NG][NT];
+    half8_t av[NG][4];
+#pragma unroll
+    for (int i = 0; i < NG; i++) {
+        const int g = g0 + min(i, max(ng - 1, 0));
+#pragma unroll
+        for (int j = 0; j < 4; j++) av[i][j] = *reinterpret_cast<const half8_t *>(arow + (size_t)g * kGS + j * 32);
+#pragma unroll
+        for (int t = 0; t < NT; t++)
+            wq[i][t] = *reinterpret_cast<const u32x4_t *>(mp.data[0] + (size_t)rowc[t] * (K / 2) + (size_t)g * 64 + kq * 16);
+    }
+    const half8_t ones = __builtin_bit_cast(half8_t, (u32x4_t){0x00110011u, 0x00110011u, 0x00100010u, 0x00100010u});
+    float4_t acc[NT];
+#pragma unroll
+    for (int t = 0; t < NT; t++) acc[t] = float4_t{0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+    for (int i = 0; i < NG; i++) {
+        if (i < ng) {
+            float4_t ds = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+            for (int j = 0; j < 4; j++) ds = __builtin_amdgcn_mfma_f32_16x16x32_f16(av[i][j], ones, ds, 0, 0, 0);
+#pragma unroll
+            for (int t = 0; t < NT; t++) {
+                float4_t d = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+                for (int j = 0; j < 4; j++) {
+                    const uint32_t w = wq[i][t][j];
+                    const uint32_t q0 = __builtin_amdgcn_perm(w, 0u, 0x0C050C04u);
+                    const uint32_t q1 = __builtin_amdgcn_perm(w, 0u, 0x0C070C06u);
+                    const u32x4_t bq = {q0, q1, q0 & 0x00F000F0u, q1 & 0x00F000F0u};
+                    d = __builtin_amdgcn_mfma_f32_16x16x32_f16(av[i][j], __builtin_bit_cast(half8_t, bq), d, 0, 0, 0);
+                }
+                const float s24 = (float)__builtin_bit_cast(_Float16, sv[i][t]) * kTwo24;
+                const float z = (float)__builtin_bit_cast(_Float16, zv[i][t]);
+#pragma unroll
+                for (int r = 0; r < 4; r++) acc[t][r] = __builtin_fmaf(s24, __builtin_fmaf(-z, ds[r], d[r]), acc[t][r]);
+            }
+        }
+    }
+#pragma unroll
+    for (int t = 0; t < NT; t++) red[(t * waves + part_w) * 64 + lane] = acc[t];
+    __syncthreads();
+    // thread (t, lane < 32): tile t, D rows 4 (lane >> 4) + r (hi) and + 8 (lo),
+    // parts in part order
+    for (int o = tid; o < NT * 32; o += blockDim.x) {
+        const int t = o >> 5, l = o & 31;
+        const float4_t *rp = red + t * waves * 64;
+        float4_t sum = rp[l] + rp[l + 32];
+        for (int p = 1; p < waves; p++) sum += rp[p * 64 + l] + rp[p * 64 + l + 32];
+        const int row = row0 + 16 * t + (l & 15);
+        if (row >= N) continue;
+#pragma unroll
+        for (int r = 0; r < 4; r++) {
+            const int m = 4 * (l >> 4) + r;
+            if (m < B) part[((size_t)slice * B + m) * N + row] = sum[r];
+        }
+    }
+}
+
+// y[m][n] = f16(sum over slices of part[s][m][n]), slices in order.
+__global__ void __launch_bounds__(256) int4_splitk_combine_kernel(const float *__restrict__ part, int S, int count,
+                                                                  __half *__restrict__ y) {
+    const int i = blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= count) return;
+    float s = part[i];
+    for (int k = 1; k < S; k++) s += part[(size_t)k * count + i];
+    y[i] = __float2half(s);
+}
+
 }  // namespace
+
+// Split-K applies where the per-tile grid leaves compute units idle (fewer
+// 16-row tiles than compute units) at 3-8 rows, one matrix, >= 32 groups.
+namespace {
+constexpr int kSplitNT = 5;   // 16-row tiles per band
+constexpr int kSplitNG = 2;   // groups per wave
+int splitk_slices(int N, int cus) {
+    const int bands = ((N + 15) / 16 + kSplitNT - 1) / kSplitNT;
+    return std::max(2, std::min(8, cus / std::max(1, bands)));
+}
+}  // namespace
+
+bool splitk_applies(int nmat, int B, int N, int K, int cus) {
+    const int G = K / kGS, tiles = (N + 15) / 16;
+    if (nmat != 1 || B < 3 || B > 8 || G < 32 || tiles >= cus) return false;
+    const int S = splitk_slices(N, cus);
+    return (G + S - 1) / S <= 16 * kSplitNG;   // 16 waves of kSplitNG groups
+}
+
+size_t splitk_workspace_bytes(int B, int N, int K, int cus) {
+    (void)K;
+    return (size_t)splitk_slices(N, cus) * B * N * sizeof(float);
+}
+
+int launch_splitk(hipStream_t st, int cus, int N, int K, int B, const MatPtrs &mp, const ActIn &in, void *ws) {
+    const int G = K / kGS;
+    constexpr int NT = kSplitNT;
+    const int bands = ((N + 15) / 16 + NT - 1) / NT;
+    const int S = splitk_slices(N, cus);
+    const int gper = (G + S - 1) / S;
+    const int waves = std::min(16, (gper + kSplitNG - 1) / kSplitNG);
+    if (waves * kSplitNG < gper) return imh::fail(IMH_EINVAL, "int4 split-K: too many groups per slice");
+    const size_t lds = (size_t)NT * waves * 64 * sizeof(float4_t);
+    float *part = static_cast<float *>(ws);
+    hipLaunchKernelGGL((int4_splitk_kernel<NT, kSplitNG>), dim3(bands, S), dim3(64 * waves), lds, st, mp, in, N, K, B, S,
+                       part);
+    IMH_HIP(hipGetLastError());
+    const int count = B * N;
+    hipLaunchKernelGGL(int4_splitk_combine_kernel, dim3((count + 255) / 256), dim3(256), 0, st, part, S, count,
+                       mp.out[0]);
+    IMH_HIP(hipGetLastError());
+    return IMH_OK;
+}
 
 bool image_da_applies(int nmat, int B, int K) {
     const int G = K / kGS;

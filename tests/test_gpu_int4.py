@@ -81,6 +81,12 @@ def gpu_layout_y(q, x16, awq16=None):
     (15003, 2560, 5, True),          # the same with a ragged last block
     (12000, 1024, 8, True),          # one group pair per wave
     (151936, 2560, 8, False),        # the Qwen3-4B LM head at 8 rows
+    # 3-8 rows with fewer 16-row tiles than compute units: split-K over K slices
+    (2560, 9728, 3, False),
+    (2560, 4096, 4, False),          # 32 groups, the fewest split
+    (1000, 9728, 6, True),           # ragged N, 13 bands
+    (2000, 5248, 5, True),           # 41 groups: slices of 5-6
+    (1024, 32768, 7, True),          # 256 groups: 16 waves of 2 groups per slice
 ])
 def test_projection_matches_oracle(dev, stream, n, k, batch, awq):
     w, s = make_weight(n, k, seed=n + k + batch, awq=awq)
