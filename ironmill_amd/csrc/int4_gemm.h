@@ -1,6 +1,7 @@
 // int4_gemm.h -- host entry points of the prefill INT4 GEMM (int4_gemm.hip).
 #pragma once
 
+#include <hip/hip_runtime.h>
 #include <hip/hip_fp16.h>
 
 #include "imh_internal.h"
@@ -21,6 +22,32 @@ size_t gemm_workspace_bytes(int M, int N, int K, int nmat, int cus);
 // from the f32 results
 int encode_gemm(imh_stream *s, const __half *x, int M, const imh_affine_int4_weight *w0,
                 const imh_affine_int4_weight *w1, int epi, __half *y0, __half *y1, void *workspace);
+
+// Sum of squares of a 256-thread workgroup's per-thread partials, in the
+// order of a halving tree over red[] (t + 128, then + 64, ... + 1): wave 0
+// forms the first two levels from red[], shuffles do the rest.  Two barriers
+// where an LDS tree takes nine; every thread gets rms_inv.
+__device__ __forceinline__ float block_rms_inv(float sq, float *red, float *bcast, int K, float eps) {
+    const int t = threadIdx.x;
+    red[t] = sq;
+    __syncthreads();
+    if (t < 64) {
+        float v = (red[t] + red[t + 128]) + (red[t + 64] + red[t + 192]);
+#pragma unroll
+        for (int st = 32; st >= 1; st >>= 1) v += __shfl_down(v, st);
+        if (t == 0) *bcast = 1.0f / __builtin_sqrtf(v / (float)K + eps);
+    }
+    __syncthreads();
+    return *bcast;
+}
+
+// Register chunks per thread of the residual-norm row kernels (256 threads
+// per row): 1, 2, 4 or 8.
+inline int resnorm_cpt(int K) {
+    const int c = (K / 8 + 255) / 256;
+    return c <= 1 ? 1 : c <= 2 ? 2 : c <= 4 ? 4 : 8;
+}
+
 // residual_out = f16(a + b), normed_out = f16((a + b) * rms_inv * gamma) per row
 int encode_resnorm_rows(imh_stream *s, const __half *a, const __half *b, const __half *gamma, float eps,
                         __half *residual_out, __half *normed_out, int B, int K);

@@ -382,42 +382,56 @@ __global__ void __launch_bounds__(256) int4_gemm_reduce_kernel(const float *__re
     }
 }
 
-// Residual + RMSNorm rows for the prefill path: grid (B), block 256.
-// residual_out = f16(a + b), normed_out = f16((a + b) * rms_inv * gamma).
+// Residual + RMSNorm rows (the prefill path and the 3-8-row decode FFN):
+// grid (B), block 256.  residual_out = f16(a + b), normed_out = f16((a + b) *
+// rms_inv * gamma).  Thread t takes chunks t, t + 256, ..: the first CPT of
+// them are loaded before the reduction and stay in registers (all of them for
+// K <= 2048 CPT); chunks past those are read again after it.
+template <int CPT>
 __global__ void __launch_bounds__(256) resnorm_rows_kernel(const __half *__restrict__ a,
                                                            const __half *__restrict__ b,
                                                            const __half *__restrict__ gamma, float eps,
                                                            __half *__restrict__ residual_out,
                                                            __half *__restrict__ normed_out, int K) {
     __shared__ float red[256];
+    __shared__ float rms_s;
     const size_t row = (size_t)blockIdx.x * K;
+    const int nchunk = K / 8;
+    const int iters = (nchunk + 255) / 256;
+    uint4 av[CPT], bv[CPT], gv[CPT];
+#pragma unroll
+    for (int it = 0; it < CPT; it++) {
+        const int c_raw = it * 256 + (int)threadIdx.x;
+        const int c = c_raw < nchunk ? c_raw : 0;
+        av[it] = *reinterpret_cast<const uint4 *>(a + row + (size_t)c * 8);
+        bv[it] = *reinterpret_cast<const uint4 *>(b + row + (size_t)c * 8);
+        gv[it] = *reinterpret_cast<const uint4 *>(gamma + (size_t)c * 8);
+    }
     float sq = 0.0f;
-    for (int c = threadIdx.x; c * 8 < K; c += blockDim.x) {
-        const uint4 av = *reinterpret_cast<const uint4 *>(a + row + (size_t)c * 8);
-        const uint4 bv = *reinterpret_cast<const uint4 *>(b + row + (size_t)c * 8);
-        const _Float16 *ah = reinterpret_cast<const _Float16 *>(&av);
-        const _Float16 *bh = reinterpret_cast<const _Float16 *>(&bv);
+    auto add_sq = [&](const uint4 &x, const uint4 &y) __attribute__((always_inline)) {
+        const _Float16 *ah = reinterpret_cast<const _Float16 *>(&x);
+        const _Float16 *bh = reinterpret_cast<const _Float16 *>(&y);
 #pragma unroll
         for (int i = 0; i < 8; i++) {
             const float r = (float)ah[i] + (float)bh[i];
             sq = __builtin_fmaf(r, r, sq);
         }
+    };
+#pragma unroll
+    for (int it = 0; it < CPT; it++)
+        if (it * 256 + (int)threadIdx.x < nchunk) add_sq(av[it], bv[it]);
+    for (int it = CPT; it < iters; it++) {
+        const int c = it * 256 + (int)threadIdx.x;
+        if (c < nchunk)
+            add_sq(*reinterpret_cast<const uint4 *>(a + row + (size_t)c * 8),
+                   *reinterpret_cast<const uint4 *>(b + row + (size_t)c * 8));
     }
-    red[threadIdx.x] = sq;
-    __syncthreads();
-    for (int s = 128; s > 0; s >>= 1) {
-        if ((int)threadIdx.x < s) red[threadIdx.x] += red[threadIdx.x + s];
-        __syncthreads();
-    }
-    const float rms_inv = 1.0f / __builtin_sqrtf(red[0] / (float)K + eps);
-    for (int c = threadIdx.x; c * 8 < K; c += blockDim.x) {
+    const float rms_inv = imh_int4::block_rms_inv(sq, red, &rms_s, K, eps);
+    auto emit = [&](int c, const uint4 &x, const uint4 &y, const uint4 &gw) __attribute__((always_inline)) {
         const size_t off = row + (size_t)c * 8;
-        const uint4 av = *reinterpret_cast<const uint4 *>(a + off);
-        const uint4 bv = *reinterpret_cast<const uint4 *>(b + off);
-        const uint4 gv = *reinterpret_cast<const uint4 *>(gamma + (size_t)c * 8);
-        const _Float16 *ah = reinterpret_cast<const _Float16 *>(&av);
-        const _Float16 *bh = reinterpret_cast<const _Float16 *>(&bv);
-        const _Float16 *gh = reinterpret_cast<const _Float16 *>(&gv);
+        const _Float16 *ah = reinterpret_cast<const _Float16 *>(&x);
+        const _Float16 *bh = reinterpret_cast<const _Float16 *>(&y);
+        const _Float16 *gh = reinterpret_cast<const _Float16 *>(&gw);
         half8_t res, nrm;
 #pragma unroll
         for (int i = 0; i < 8; i++) {
@@ -427,6 +441,18 @@ __global__ void __launch_bounds__(256) resnorm_rows_kernel(const __half *__restr
         }
         *reinterpret_cast<half8_t *>(residual_out + off) = res;
         *reinterpret_cast<half8_t *>(normed_out + off) = nrm;
+    };
+#pragma unroll
+    for (int it = 0; it < CPT; it++) {
+        const int c = it * 256 + (int)threadIdx.x;
+        if (c < nchunk) emit(c, av[it], bv[it], gv[it]);
+    }
+    for (int it = CPT; it < iters; it++) {
+        const int c = it * 256 + (int)threadIdx.x;
+        if (c < nchunk)
+            emit(c, *reinterpret_cast<const uint4 *>(a + row + (size_t)c * 8),
+                 *reinterpret_cast<const uint4 *>(b + row + (size_t)c * 8),
+                 *reinterpret_cast<const uint4 *>(gamma + (size_t)c * 8));
     }
 }
 
@@ -508,8 +534,12 @@ int encode_gemm(imh_stream *s, const __half *x, int M, const imh_affine_int4_wei
 
 int encode_resnorm_rows(imh_stream *s, const __half *a, const __half *b, const __half *gamma, float eps,
                         __half *residual_out, __half *normed_out, int B, int K) {
-    hipLaunchKernelGGL(resnorm_rows_kernel, dim3(B), dim3(256), 0, s->stream, a, b, gamma, eps, residual_out,
-                       normed_out, K);
+    const int cpt = resnorm_cpt(K);
+    auto kern = cpt == 1 ? resnorm_rows_kernel<1>
+                : cpt == 2 ? resnorm_rows_kernel<2>
+                : cpt == 4 ? resnorm_rows_kernel<4>
+                           : resnorm_rows_kernel<8>;
+    hipLaunchKernelGGL(kern, dim3(B), dim3(256), 0, s->stream, a, b, gamma, eps, residual_out, normed_out, K);
     IMH_HIP(hipGetLastError());
     return IMH_OK;
 }

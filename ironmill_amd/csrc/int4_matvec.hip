@@ -70,6 +70,11 @@ __global__ void __launch_bounds__(256) int4_prep_plain(const __half *__restrict_
 // residual_out / normed_out and the operand image of r * gamma / awq (the
 // matvec then scales by rms_inv); `rounded` 1: of normed_out / awq instead;
 // 2: both, the rounded one as the second image (hi2 / lo2 / gsum2).
+// Thread t takes chunks t, t + 256, ..: the first CPT of them (all of them
+// for K <= 2048 CPT) are loaded before the reduction and stay in registers,
+// so the row waits one memory latency; chunks past those (K > 16384 at CPT 8)
+// are read again after it.
+template <int CPT>
 __global__ void __launch_bounds__(256) int4_prep_resnorm(
     const __half *__restrict__ a, const __half *__restrict__ b, const __half *__restrict__ gamma,
     const __half *__restrict__ awq, float eps, __half *__restrict__ residual_out,
@@ -78,42 +83,53 @@ __global__ void __launch_bounds__(256) int4_prep_resnorm(
     _Float16 *__restrict__ xa_lo2, float *__restrict__ gsum2) {
     const int m = blockIdx.x;
     const int G = K / kGS;
+    const int nchunk = K / 8;
     const size_t row = (size_t)m * K;
     __shared__ float red[256];
+    __shared__ float rms_s;
+    uint4 av[CPT], bv[CPT], gv[CPT], wv[CPT];
+#pragma unroll
+    for (int it = 0; it < CPT; it++) {
+        const int c_raw = it * 256 + (int)threadIdx.x;
+        const int c = c_raw < nchunk ? c_raw : 0;
+        av[it] = *reinterpret_cast<const uint4 *>(a + row + (size_t)c * 8);
+        bv[it] = *reinterpret_cast<const uint4 *>(b + row + (size_t)c * 8);
+        gv[it] = *reinterpret_cast<const uint4 *>(gamma + (size_t)c * 8);
+        wv[it] = awq ? *reinterpret_cast<const uint4 *>(awq + (size_t)c * 8) : make_uint4(0, 0, 0, 0);
+    }
+    const int iters = (nchunk + 255) / 256;   // > CPT only at CPT 8, K > 16384
     float sq = 0.0f;
-    for (int c = threadIdx.x; c * 8 < K; c += blockDim.x) {
-        uint4 av = *reinterpret_cast<const uint4 *>(a + row + (size_t)c * 8);
-        uint4 bv = *reinterpret_cast<const uint4 *>(b + row + (size_t)c * 8);
-        const _Float16 *ah = reinterpret_cast<const _Float16 *>(&av);
-        const _Float16 *bh = reinterpret_cast<const _Float16 *>(&bv);
+    auto add_sq = [&](const uint4 &x, const uint4 &y) __attribute__((always_inline)) {
+        const _Float16 *ah = reinterpret_cast<const _Float16 *>(&x);
+        const _Float16 *bh = reinterpret_cast<const _Float16 *>(&y);
 #pragma unroll
         for (int i = 0; i < 8; i++) {
             float r = (float)ah[i] + (float)bh[i];
             sq = __builtin_fmaf(r, r, sq);
         }
+    };
+#pragma unroll
+    for (int it = 0; it < CPT; it++)
+        if (it * 256 + (int)threadIdx.x < nchunk) add_sq(av[it], bv[it]);
+    for (int it = CPT; it < iters; it++) {
+        const int c = it * 256 + (int)threadIdx.x;
+        if (c < nchunk)
+            add_sq(*reinterpret_cast<const uint4 *>(a + row + (size_t)c * 8),
+                   *reinterpret_cast<const uint4 *>(b + row + (size_t)c * 8));
     }
-    red[threadIdx.x] = sq;
-    __syncthreads();
-    for (int s = 128; s > 0; s >>= 1) {
-        if ((int)threadIdx.x < s) red[threadIdx.x] += red[threadIdx.x + s];
-        __syncthreads();
-    }
-    const float rms_inv = 1.0f / __builtin_sqrtf(red[0] / (float)K + eps);
+    const float rms_inv = block_rms_inv(sq, red, &rms_s, K, eps);
     if (threadIdx.x == 0) rms_out[m] = rms_inv;
-    // every thread runs the same number of iterations (K / 8 is a multiple of
-    // 16), so the 16 lanes of a group always meet in store_group_sums
-    const int iters = (K / 8 + blockDim.x - 1) / blockDim.x;
-    for (int it = 0; it < iters; it++) {
-        const int c_raw = it * blockDim.x + threadIdx.x;
-        const bool live = c_raw * 8 < K;
+    // every thread runs the same iterations (K / 8 is a multiple of 16), so
+    // the 16 lanes of a group always meet in store_group_sums
+    auto emit = [&](int it, const uint4 &x, const uint4 &y, const uint4 &gw, const uint4 &ww)
+                    __attribute__((always_inline)) {
+        const int c_raw = it * 256 + (int)threadIdx.x;
+        const bool live = c_raw < nchunk;
         const int c = live ? c_raw : 0;
         const size_t off = row + (size_t)c * 8;
-        uint4 av = *reinterpret_cast<const uint4 *>(a + off);
-        uint4 bv = *reinterpret_cast<const uint4 *>(b + off);
-        uint4 gv = *reinterpret_cast<const uint4 *>(gamma + (size_t)c * 8);
-        const _Float16 *ah = reinterpret_cast<const _Float16 *>(&av);
-        const _Float16 *bh = reinterpret_cast<const _Float16 *>(&bv);
-        const _Float16 *gh = reinterpret_cast<const _Float16 *>(&gv);
+        const _Float16 *ah = reinterpret_cast<const _Float16 *>(&x);
+        const _Float16 *bh = reinterpret_cast<const _Float16 *>(&y);
+        const _Float16 *gh = reinterpret_cast<const _Float16 *>(&gw);
         float v[8], v2[8];
         half8_t res, nrm;
         for (int i = 0; i < 8; i++) {
@@ -124,8 +140,7 @@ __global__ void __launch_bounds__(256) int4_prep_resnorm(
             v2[i] = (float)nrm[i];
         }
         if (awq) {
-            uint4 wv = *reinterpret_cast<const uint4 *>(awq + (size_t)c * 8);
-            const _Float16 *wh = reinterpret_cast<const _Float16 *>(&wv);
+            const _Float16 *wh = reinterpret_cast<const _Float16 *>(&ww);
             for (int i = 0; i < 8; i++) {
                 v[i] = div_awq(v[i], (float)wh[i]);
                 v2[i] = div_awq(v2[i], (float)wh[i]);
@@ -150,6 +165,15 @@ __global__ void __launch_bounds__(256) int4_prep_resnorm(
             }
             store_group_sums(sh, sl, live, gsum2 + (size_t)m * 2 * G, G, c / 16);
         }
+    };
+#pragma unroll
+    for (int it = 0; it < CPT; it++) emit(it, av[it], bv[it], gv[it], wv[it]);
+    for (int it = CPT; it < iters; it++) {
+        const int c = min(it * 256 + (int)threadIdx.x, nchunk - 1);
+        emit(it, *reinterpret_cast<const uint4 *>(a + row + (size_t)c * 8),
+             *reinterpret_cast<const uint4 *>(b + row + (size_t)c * 8),
+             *reinterpret_cast<const uint4 *>(gamma + (size_t)c * 8),
+             awq ? *reinterpret_cast<const uint4 *>(awq + (size_t)c * 8) : make_uint4(0, 0, 0, 0));
     }
 }
 
@@ -367,8 +391,13 @@ int run_matvec(imh_stream *s, ActIn in, uint32_t B, int nmat, int epi, int N, in
     float *gs = const_cast<float *>(in.gsum);
     if (rn) {
         const int rounded = in.round_mode;
-        hipLaunchKernelGGL(int4_prep_resnorm, dim3(B), dim3(256), 0, s->stream, in.a, in.b, in.gamma, in.awq,
-                           in.eps, in.residual_out, in.normed_out, hi, lo, gs, rms, K, rounded,
+        const int cpt = resnorm_cpt(K);
+        auto kern = cpt == 1 ? int4_prep_resnorm<1>
+                    : cpt == 2 ? int4_prep_resnorm<2>
+                    : cpt == 4 ? int4_prep_resnorm<4>
+                               : int4_prep_resnorm<8>;
+        hipLaunchKernelGGL(kern, dim3(B), dim3(256), 0, s->stream, in.a, in.b, in.gamma, in.awq, in.eps,
+                           in.residual_out, in.normed_out, hi, lo, gs, rms, K, rounded,
                            const_cast<_Float16 *>(in2.hi), const_cast<_Float16 *>(in2.lo),
                            const_cast<float *>(in2.gsum));
         in.row_scale = rounded == 1 ? nullptr : rms;

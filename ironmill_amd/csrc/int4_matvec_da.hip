@@ -287,13 +287,21 @@ __global__ void __launch_bounds__(1024) int4_splitk_kernel(MatPtrs mp, const Act
     }
 }
 
-// y[m][n] = f16(sum over slices of part[s][m][n]), slices in order.
+// y[m][n] = f16(sum over slices of part[s][m][n]), slices in order.  Every
+// slice's load is issued before the first add (S <= kMaxSlices), so the
+// thread waits one memory latency rather than S.
+constexpr int kMaxSlices = 8;
 __global__ void __launch_bounds__(256) int4_splitk_combine_kernel(const float *__restrict__ part, int S, int count,
                                                                   __half *__restrict__ y) {
     const int i = blockIdx.x * blockDim.x + threadIdx.x;
     if (i >= count) return;
-    float s = part[i];
-    for (int k = 1; k < S; k++) s += part[(size_t)k * count + i];
+    float v[kMaxSlices];
+#pragma unroll
+    for (int k = 0; k < kMaxSlices; k++) v[k] = k < S ? part[(size_t)k * count + i] : 0.0f;
+    float s = v[0];
+#pragma unroll
+    for (int k = 1; k < kMaxSlices; k++)
+        if (k < S) s += v[k];
     y[i] = __float2half(s);
 }
 
@@ -306,7 +314,7 @@ constexpr int kSplitNT = 5;   // 16-row tiles per band
 constexpr int kSplitNG = 2;   // groups per wave
 int splitk_slices(int N, int cus) {
     const int bands = ((N + 15) / 16 + kSplitNT - 1) / kSplitNT;
-    return std::max(2, std::min(8, cus / std::max(1, bands)));
+    return std::max(2, std::min(kMaxSlices, cus / std::max(1, bands)));
 }
 }  // namespace
 

@@ -129,8 +129,11 @@ def test_gemm_batched_gate_up(dev, stream):
     assert_close(uo.read(), O.matvec_f16w(wdq_u, x16, awq16, nthreads=8), what="gemm up", ulps=ulps_for(True))
 
 
-def test_gemm_fused_residual_norm(dev, stream):
-    m, n, k, eps = 40, 4096, 2560, 1e-6
+# the residual + norm rows kernel at 1, 2 and 8 register chunks per thread,
+# and past those (K > 16384: the chunks beyond are read again)
+@pytest.mark.parametrize("m,n,k", [(40, 4096, 2560), (33, 256, 1024), (32, 128, 16384), (34, 128, 16512)])
+def test_gemm_fused_residual_norm(dev, stream, m, n, k):
+    eps = 1e-6
     w, s = weight(n, k, 61, True)
     rng = np.random.default_rng(62)
     a = rng.standard_normal((m, k)).astype(np.float16)

@@ -230,9 +230,14 @@ def test_batched_gate_up(dev, stream, batch, awq):
     assert_close(uo.read(), O.matvec_f16w(wdq_u, x16, awq16, nthreads=8), what="up", ulps=2)
 
 
-@pytest.mark.parametrize("batch,awq", [(1, False), (1, True), (2, True), (3, True)])
-def test_fused_residual_norm_projection(dev, stream, batch, awq):
-    n, k, eps = 4096, 2560, 1e-6
+# 3-8 rows: the residual + norm prep kernel at 1, 2 and 8 register chunks per
+# thread, and past those (K > 16384: the chunks beyond are read again)
+@pytest.mark.parametrize("n,k,batch,awq", [
+    (4096, 2560, 1, False), (4096, 2560, 1, True), (4096, 2560, 2, True), (4096, 2560, 3, True),
+    (4096, 2560, 8, False), (512, 1024, 5, True), (128, 16384, 4, False), (128, 16512, 3, True),
+])
+def test_fused_residual_norm_projection(dev, stream, n, k, batch, awq):
+    eps = 1e-6
     w, s = make_weight(n, k, seed=31, awq=awq)
     rng = np.random.default_rng(32)
     a = rng.standard_normal((batch, k)).astype(np.float16)
