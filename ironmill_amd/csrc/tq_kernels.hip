@@ -460,7 +460,17 @@ __global__ void __launch_bounds__(64 * kWaves) __attribute__((amdgpu_waves_per_e
     const int tid = threadIdx.x;
     const int lane = tid & 63;
     const int wave = tid >> 6;
-    const int S = gridDim.x;
+    // S = gridDim.x through an asm that also takes every kernel argument the
+    // prologue reads: the compiler loads them all in one trip before it
+    // (otherwise in dependent batches).  Not volatile and no memory operand,
+    // so loads after it still count as unclobbered (scalar loads).
+    int S;
+    asm("" : "=s"(S) : "0"(gridDim.x), "s"(gridDim.y), "s"(gridDim.z), "s"(q), "s"(nh), "s"(nkv), "s"(max_seq),
+        "s"(seq_len), "s"(T), "s"(seq_lens), "s"(attn_scale), "s"(signs), "s"(qjl_t), "s"(kcb), "s"(vcb));
+    int S2;
+    asm("" : "=s"(S2) : "0"(S), "s"(kcodes), "s"(vcodes), "s"(kscales), "s"(vscales), "s"(krnorm), "s"(split_len),
+        "s"(qr.norm), "s"(qr.cos), "s"(qr.sin), "s"(qr.positions), "s"(qr.max_pos), "s"(qr.eps));
+    S = S2;
     // With the token writers (FUSED): the grid in dispatch order is every
     // group's S - 1 splits first, then the groups' writers, so the streaming
     // workgroups spread evenly over the CUs (two per CU at ~512) and the
@@ -475,10 +485,13 @@ __global__ void __launch_bounds__(64 * kWaves) __attribute__((amdgpu_waves_per_e
         kvh = g % (int)gridDim.y;
         z = g / (int)gridDim.y;
     }
-    const int b = z / T, tq = z - b * T;
+    // uniform (scalar loads of the per-sequence values below)
+    const int b = __builtin_amdgcn_readfirstlane(z / T), tq = z - b * T;
     const bool writer = FUSED && split == S - 1;   // the step's token (uniform per workgroup)
 
-    // with seq_lens, seq_len is the bound every length is clamped to
+    // with seq_lens, seq_len is the bound every length is clamped to; the
+    // sequence's RoPE position is read in the same trip
+    const int32_t pos_b = qr.positions[b];
     int L = seq_lens ? min(seq_lens[b], seq_len) : seq_len;
     L = L < 0 ? 0 : (L > max_seq ? max_seq : L);
     // causal (turboquant.metal:268): token t of T sees positions < L - T + t + 1
@@ -514,7 +527,7 @@ __global__ void __launch_bounds__(64 * kWaves) __attribute__((amdgpu_waves_per_e
     // QK-norm + RoPE operands, loaded unconditionally (a branch here would
     // make the compiler wait for them before the loads below issue)
     const __half *qnw = qr.norm ? qr.norm : qh;
-    const long rp = imh_qk::clamp_pos(qr.positions[b], qr.max_pos);
+    const long rp = imh_qk::clamp_pos(pos_b, qr.max_pos);
     const __half qw0 = qnw[lane], qw1 = qnw[lane + 64];
     const __half qc = qr.cos[rp * (kD / 2) + lane], qsn = qr.sin[rp * (kD / 2) + lane];
     const float kc = kcb[tid & 0x7F], vc = vcb[tid];
@@ -1155,8 +1168,9 @@ __global__ void __launch_bounds__(64 * kWaves) __attribute__((amdgpu_waves_per_e
 // ([row][S] maxima -- in log2 units for the prefill kernel, natural for the
 // decode kernel -- and sums, [row][S][kD] outputs) and rotates the result
 // back into out[row].  Split s weighs exp(m_s - M); wave w sums the splits
-// w, w + 4, .. (several loads in flight), the four partial sums are added in
-// wave order through LDS, and wave 0 normalises and rotates.
+// w, w + 4, .. (the first sixteen of them loaded together with the maxima), the
+// four partial sums are added in wave order through LDS, and wave 0
+// normalises and rotates.
 template <bool LOG2>
 __global__ void __launch_bounds__(256) tq_split_combine_kernel(const float *__restrict__ part_o,
                                                                const float *__restrict__ part_m,
@@ -1169,21 +1183,40 @@ __global__ void __launch_bounds__(256) tq_split_combine_kernel(const float *__re
     const int row = blockIdx.x;
     const float *pm = part_m + (size_t)row * S;
     const float *pl = part_l + (size_t)row * S;
-    float mx = -INFINITY;
-    for (int sp = lane; sp < S; sp += 64) mx = fmaxf(mx, pm[sp]);
+    const float *po = part_o + (size_t)row * S * kD;
+    // the maxima for the row maximum, then the wave's first kR splits (every
+    // load issued before the first wait: one memory latency for S <= 4 kR)
+    constexpr int kR = 16;
+    float mx = pm[lane < S ? lane : 0];
+    mx = lane < S ? mx : -INFINITY;
+    float mv[kR], lv[kR], ov0[kR], ov1[kR];
+#pragma unroll
+    for (int i = 0; i < kR; i++) {
+        const int sp = min(wave + 4 * i, S - 1);
+        mv[i] = pm[sp];
+        lv[i] = pl[sp];
+        ov0[i] = po[(size_t)sp * kD + lane];
+        ov1[i] = po[(size_t)sp * kD + lane + 64];
+    }
+    for (int sp = lane + 64; sp < S; sp += 64) mx = fmaxf(mx, pm[sp]);
 #pragma unroll
     for (int st = 32; st >= 1; st >>= 1) mx = fmaxf(mx, __shfl_xor(mx, st));
-    const float *po = part_o + (size_t)row * S * kD;
     float o0 = 0.0f, o1 = 0.0f, ls = 0.0f;
-#pragma unroll 4
-    for (int sp = wave; sp < S; sp += 4) {
-        const float m = pm[sp];
+    auto add = [&](float m, float l, float a0, float a1) __attribute__((always_inline)) {
         const float f = (mx == -INFINITY || m == -INFINITY) ? 0.0f
                                                             : (LOG2 ? __builtin_amdgcn_exp2f(m - mx) : __expf(m - mx));
-        ls = __builtin_fmaf(f, pl[sp], ls);
-        o0 = __builtin_fmaf(po[(size_t)sp * kD + lane], f, o0);
-        o1 = __builtin_fmaf(po[(size_t)sp * kD + lane + 64], f, o1);
-    }
+        ls = __builtin_fmaf(f, l, ls);
+        o0 = __builtin_fmaf(a0, f, o0);
+        o1 = __builtin_fmaf(a1, f, o1);
+    };
+    // splits in the order wave, wave + 4, .. (the sums' order does not depend
+    // on how the loads were batched)
+#pragma unroll
+    for (int i = 0; i < kR; i++)
+        if (wave + 4 * i < S) add(mv[i], lv[i], ov0[i], ov1[i]);
+#pragma unroll 4
+    for (int sp = wave + 4 * kR; sp < S; sp += 4)
+        add(pm[sp], pl[sp], po[(size_t)sp * kD + lane], po[(size_t)sp * kD + lane + 64]);
     osum[wave][lane] = o0;
     osum[wave][lane + 64] = o1;
     if (lane == 0) lsums[wave] = ls;
