@@ -175,8 +175,9 @@ __global__ void __launch_bounds__(kThreads, 2) gemm_mx_kernel(
     constexpr int EB = P == PREC_BF16 ? 2 : 1;     // operand bytes per element
     constexpr int RB = kGS * EB + 16;              // LDS row bytes of one group (16-byte pad)
     constexpr int ACH = kBM * kGS * EB / 16 / kThreads;   // 16-byte A chunks per thread per group
-    __shared__ __attribute__((aligned(16))) uint8_t As[2][kBM * RB];
-    __shared__ __attribute__((aligned(16))) float Gs[2][kBM];
+    // A stages: [stage buffer][group of the stage] -- two groups per barrier
+    __shared__ __attribute__((aligned(16))) uint8_t As[2][2][kBM * RB];
+    __shared__ __attribute__((aligned(16))) float Gs[2][2][kBM];
 
     const int tid = threadIdx.x;
     const int lane = tid & 63;
@@ -214,14 +215,14 @@ __global__ void __launch_bounds__(kThreads, 2) gemm_mx_kernel(
         for (int i = 0; i < ACH; i++) load_a1(g, i, ar);
         load_gs(g, gs);
     };
-    auto store_a = [&](int buf, const u32x4_t *ar, float gs) __attribute__((always_inline)) {
+    auto store_a = [&](int sb, int part, const u32x4_t *ar, float gs) __attribute__((always_inline)) {
 #pragma unroll
         for (int i = 0; i < ACH; i++) {
             const int c = i * kThreads + tid;
             const int r = c / (kGS * EB / 16), cc = c - r * (kGS * EB / 16);
-            *reinterpret_cast<u32x4_t *>(&As[buf][r * RB + cc * 16]) = ar[i];
+            *reinterpret_cast<u32x4_t *>(&As[sb][part][r * RB + cc * 16]) = ar[i];
         }
-        if (tid < kBM) Gs[buf][tid] = gs;
+        if (tid < kBM) Gs[sb][part][tid] = gs;
     };
     // B codes (32 bytes per fragment and lane), scales and zero-points of
     // group g; the scale and zero stay apart until used
@@ -255,7 +256,8 @@ __global__ void __launch_bounds__(kThreads, 2) gemm_mx_kernel(
     // steps, then each tile's group partial folded into acc with the scale
     // and zero-point of the lane's column and the group sums of its rows.
     // hook(st) runs at k step st: it issues the next group's loads.
-    auto compute = [&](int buf, const BRegs &b, auto &&hook) __attribute__((always_inline)) {
+    auto compute = [&](int sb, int part, const BRegs &b, auto &&hook) __attribute__((always_inline)) {
+        const uint8_t *Ab = As[sb][part];
         // The group's zero-point correction -c * rowsum (c = 128 + z for the
         // bf16 codes, which carry 128; z for fp8) is added to each tile's
         // group accumulator on the matrix core: A lane (m, 0) holds the row sum
@@ -267,7 +269,7 @@ __global__ void __launch_bounds__(kThreads, 2) gemm_mx_kernel(
             const __bf16 z0 = (__bf16)0.0f;
 #pragma unroll
             for (int mi = 0; mi < 2; mi++) {
-                const float rs = Gs[buf][32 * mi + nl];
+                const float rs = Gs[sb][part][32 * mi + nl];
                 const __bf16 r0 = (__bf16)rs;
                 const float e1 = rs - (float)r0;
                 const __bf16 r1 = (__bf16)e1;
@@ -289,7 +291,7 @@ __global__ void __launch_bounds__(kThreads, 2) gemm_mx_kernel(
                 bf16x8_t af[2], bf[2];
 #pragma unroll
                 for (int mi = 0; mi < 2; mi++)
-                    af[mi] = *reinterpret_cast<const bf16x8_t *>(&As[buf][(32 * mi + nl) * RB + (8 * h + st) * 16]);
+                    af[mi] = *reinterpret_cast<const bf16x8_t *>(&Ab[(32 * mi + nl) * RB + (8 * h + st) * 16]);
 #pragma unroll
                 for (int j = 0; j < 2; j++) {
                     // 8 codes -> bf16 128 + q in slot order {0, 2, 4, 6, 1, 3, 5, 7}
@@ -333,7 +335,7 @@ __global__ void __launch_bounds__(kThreads, 2) gemm_mx_kernel(
             for (int t = 0; t < 2; t++)
 #pragma unroll
                 for (int mi = 0; mi < 2; mi++) {
-                    const uint8_t *p = &As[buf][(32 * mi + nl) * RB + 64 * t + 32 * h];
+                    const uint8_t *p = &Ab[(32 * mi + nl) * RB + 64 * t + 32 * h];
                     const u32x4_t a0 = *reinterpret_cast<const u32x4_t *>(p);
                     const u32x4_t a1 = *reinterpret_cast<const u32x4_t *>(p + 16);
                     af[mi][t] = (i32x8_t){(int)a0[0], (int)a0[1], (int)a0[2], (int)a0[3],
@@ -367,37 +369,48 @@ __global__ void __launch_bounds__(kThreads, 2) gemm_mx_kernel(
         }
     };
 
-    // Ping-pong over two B register sets (no copies between iterations): a
-    // group computes from LDS buffer buf and set `cur` while the next group's
-    // A (registers, stored to the other buffer after the MFMAs) and B (the
-    // other set) are in flight.  The prefetch is unconditional -- the last
-    // group loads itself again -- so the compiler's wait for the current
-    // set never has to cover the prefetch.
+    // Ping-pong over two B register sets (no copies between iterations), A in
+    // stages of two groups with one barrier per stage: group g computes from
+    // stage buffer sb (part g & 1 of the stage) while group g + 2's A is
+    // loaded into registers and, after g's MFMAs, stored to the other stage
+    // buffer -- free since the barrier that closed the stage before (every
+    // wave was done reading it) -- and group g + 1's B into the other set.
+    // The prefetch is unconditional -- past the last group the last one is
+    // loaded again -- so the compiler's wait for the current set never has to
+    // cover the prefetch.
     u32x4_t ar[ACH];
     BRegs b0, b1;
     float gsv = 0.0f;
     if (g_begin < g_end) {
         load_a(g_begin, ar, gsv);
         load_b(g_begin, b0);
-        store_a(0, ar, gsv);
+        store_a(0, 0, ar, gsv);
+        load_a(min(g_begin + 1, g_end - 1), ar, gsv);
+        store_a(0, 1, ar, gsv);
         __syncthreads();
     }
-    auto step = [&](int g, int buf, const BRegs &cur, BRegs &nxt) __attribute__((always_inline)) {
-        const int gn = min(g + 1, g_end - 1);
-        // the next group's loads spread over the k steps: A chunks first (they
-        // are stored to LDS after the compute), then B
-        compute(buf, cur, [&](int st) __attribute__((always_inline)) {
-            if (st < ACH) load_a1(gn, st, ar);
-            if (st == ACH) load_gs(gn, gsv);
-            if (st == 4) load_b1(gn, 0, nxt);
-            if (st == 5) load_b1(gn, 1, nxt);
+    auto step = [&](int g, int sb, int part, const BRegs &cur, BRegs &nxt) __attribute__((always_inline)) {
+        const int ga = min(g + 2, g_end - 1), gb = min(g + 1, g_end - 1);
+        // the loads spread over the k steps: A chunks first (they are stored
+        // to LDS after the compute), then B
+        compute(sb, part, cur, [&](int st) __attribute__((always_inline)) {
+            if (st < ACH) load_a1(ga, st, ar);
+            if (st == ACH) load_gs(ga, gsv);
+            if (st == 4) load_b1(gb, 0, nxt);
+            if (st == 5) load_b1(gb, 1, nxt);
         });
-        store_a(buf ^ 1, ar, gsv);
-        __syncthreads();
+        store_a(sb ^ 1, part, ar, gsv);
     };
-    for (int g = g_begin; g < g_end; g += 2) {
-        step(g, 0, b0, b1);
-        if (g + 1 < g_end) step(g + 1, 1, b1, b0);
+    // two stages per iteration: the stage buffers' indices are constants
+    for (int g = g_begin; g < g_end; g += 4) {
+        step(g, 0, 0, b0, b1);
+        if (g + 1 < g_end) step(g + 1, 0, 1, b1, b0);
+        __syncthreads();
+        if (g + 2 < g_end) {
+            step(g + 2, 1, 0, b0, b1);
+            if (g + 3 < g_end) step(g + 3, 1, 1, b1, b0);
+            __syncthreads();
+        }
     }
 
     // D of tile (mi, j): lane holds rows 32 mi + 8 (i >> 2) + 4 h + (i & 3), column 32 j + nl
