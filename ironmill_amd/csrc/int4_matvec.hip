@@ -324,20 +324,20 @@ int run_gemm(imh_stream *s, const ActIn &in, int M, const imh_affine_int4_weight
                        ws);
 }
 
-// Split-K over the image in in.hi / in.lo when it applies: one matrix, plain
-// store, no row segments or row scale (partials in stream scratch slot 2).
+// Split-K over the image in in.hi / in.lo (and hi2 / lo2 for a mixed
+// rounding's later segments) when it applies: one matrix with its row
+// segments, plain store (partials in stream scratch slot 2).
 int try_splitk(imh_stream *s, int nmat, int epi, int N, int K, uint32_t B, const MatPtrs &mp, const ActIn &in,
                bool *used) {
     *used = false;
     const int cus = s->dev->props.multiProcessorCount;
-    if (epi != EPI_STORE || mp.seg[0] != 0 || in.row_scale || in.round_mode == 2 ||
-        !splitk_applies(nmat, (int)B, N, K, cus))
-        return IMH_OK;
+    const int split_rows = (in.round_mode == 2 && mp.seg[0] > 0) ? mp.seg[0] : N;
+    if (epi != EPI_STORE || !splitk_applies(nmat, (int)B, N, K, split_rows, cus)) return IMH_OK;
     void *ws = nullptr;
-    int rc = imh::stream_scratch(s, 2, splitk_workspace_bytes((int)B, N, K, cus), &ws);
+    int rc = imh::stream_scratch(s, 2, splitk_workspace_bytes((int)B, N, split_rows, cus), &ws);
     if (rc) return rc;
     *used = true;
-    return launch_splitk(s->stream, cus, N, K, (int)B, mp, in, ws);
+    return launch_splitk(s->stream, cus, N, K, (int)B, mp, in, split_rows, ws);
 }
 
 // Plans and launches the matvec kernel for mp (N rows in total, segments
@@ -536,9 +536,9 @@ int ffn_band_pair(imh_stream *s, ActIn gin, uint32_t B, const imh_affine_int4_we
             imh::clear_error();
             return IMH_OK;   // a RAW down (small K) builds its own operand
         }
-        if (splitk_applies(1, (int)B, Hd, F, cus)) {   // reserve the partials before the first launch
+        if (splitk_applies(1, (int)B, Hd, F, Hd, cus)) {   // reserve the partials before the first launch
             void *ws = nullptr;
-            rc = imh::stream_scratch(s, 2, splitk_workspace_bytes((int)B, Hd, F, cus), &ws);
+            rc = imh::stream_scratch(s, 2, splitk_workspace_bytes((int)B, Hd, Hd, cus), &ws);
             if (rc) return rc;
         }
     }

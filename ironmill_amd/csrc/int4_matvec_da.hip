@@ -185,17 +185,20 @@ void launch_ng_da(int ng, dim3 grid, dim3 block, size_t lds, hipStream_t st, con
         hipLaunchKernelGGL((int4_da_kernel<NMAT, EPI, 5>), grid, block, lds, st, mp, in, N, K, B, parts);
 }
 
-// Split-K over a prebuilt image, 1-8 rows: grid (bands of NT tiles, S
+// Split-K over a prebuilt image, 3-8 rows: grid (bands of NT tiles, S
 // slices of K).  Workgroup (band, slice) reads the operand of its slice only
 // and the weights of its NT x 16 rows in that slice, so a CU moves ~1 / S of
 // the image the per-tile kernel reads; the band's f32 partial sums go to
 // part[slice][m][row] and int4_splitk_combine_kernel adds the slices in
 // slice order (deterministic).  Waves split the slice's groups (<= NG each);
 // each wave loads a group's A operand once (the direct-operand layout) and
-// uses it for the NT tiles' weights.
+// uses it for the NT tiles' weights.  Row segments: each tile takes its own
+// segment's weights (segment starts are multiples of 16).  Tiles [0, gb) and
+// [gb, tiles) are banded apart -- bands0 bands, then the rest -- because with
+// a mixed rounding (round_mode 2) the rows from gb on read the second image.
 template <int NT, int NG>
 __global__ void __launch_bounds__(1024) int4_splitk_kernel(MatPtrs mp, const ActIn in, int N, int K, int B, int S,
-                                                           float *__restrict__ part) {
+                                                           int gb, int bands0, float *__restrict__ part) {
     extern __shared__ __attribute__((aligned(16))) float4_t red[];   // [NT][waves][64]
     const int tid = threadIdx.x;
     const int waves = blockDim.x >> 6;
@@ -207,16 +210,33 @@ __global__ void __launch_bounds__(1024) int4_splitk_kernel(MatPtrs mp, const Act
     const int part_w = (wave + (int)blockIdx.x) % waves;   // rotated, as in the per-tile kernel
     const int g0 = gs0 + (part_w * gsn) / waves;
     const int ng = gs0 + ((part_w + 1) * gsn) / waves - g0;
-    const int row0 = blockIdx.x * 16 * NT;
     const int n_l = lane & 15, kq = lane >> 4;
 
-    const uint16_t *sp0 = reinterpret_cast<const uint16_t *>(mp.scales[0]);
-    const uint16_t *zp0 = reinterpret_cast<const uint16_t *>(mp.zeros[0]);
+    const int band = blockIdx.x;
+    const bool grp1 = band >= bands0;
+    const int tiles = (N + 15) / 16;
+    const int tile0 = grp1 ? gb + (band - bands0) * NT : band * NT;
+    const int tile_end = grp1 ? tiles : gb;
+    const bool img2 = grp1 && in.round_mode == 2;
+    // tile t: its segment's weights, scales and zero points, and the lane's
+    // row within the segment (tiles past the band's end redo its last tile;
+    // they store nothing)
+    const uint8_t *wd[NT];
+    const uint16_t *sp[NT], *zp[NT];
     int rowc[NT];
 #pragma unroll
-    for (int t = 0; t < NT; t++) rowc[t] = min(row0 + 16 * t + n_l, N - 1);
+    for (int t = 0; t < NT; t++) {
+        const int r0 = min(tile0 + t, tile_end - 1) * 16;
+        const int sg = (mp.seg[0] > 0 && r0 >= mp.seg[0]) ? ((mp.seg[1] > 0 && r0 >= mp.seg[1]) ? 2 : 1) : 0;
+        const int base = sg == 0 ? 0 : (sg == 1 ? mp.seg[0] : mp.seg[1]);
+        const int end = sg == 0 ? (mp.seg[0] > 0 ? mp.seg[0] : N) : (sg == 1 && mp.seg[1] > 0 ? mp.seg[1] : N);
+        wd[t] = sg == 0 ? mp.data[0] : (sg == 1 ? mp.data[1] : mp.data[2]);
+        sp[t] = reinterpret_cast<const uint16_t *>(sg == 0 ? mp.scales[0] : (sg == 1 ? mp.scales[1] : mp.scales[2]));
+        zp[t] = reinterpret_cast<const uint16_t *>(sg == 0 ? mp.zeros[0] : (sg == 1 ? mp.zeros[1] : mp.zeros[2]));
+        rowc[t] = min(r0 + n_l, end - 1) - base;
+    }
     const int ar = (n_l & 7) < B ? (n_l & 7) : 0;
-    const _Float16 *arow = ((n_l >> 3) ? in.lo : in.hi) + (size_t)ar * K + kq * 8;
+    const _Float16 *arow = ((n_l >> 3) ? (img2 ? in.lo2 : in.lo) : (img2 ? in.hi2 : in.hi)) + (size_t)ar * K + kq * 8;
 
     uint16_t sv[NG][NT], zv[NG][NT];
 #pragma unroll
@@ -224,8 +244,8 @@ __global__ void __launch_bounds__(1024) int4_splitk_kernel(MatPtrs mp, const Act
         const int g = g0 + min(i, max(ng - 1, 0));
 #pragma unroll
         for (int t = 0; t < NT; t++) {
-            sv[i][t] = sp0[(size_t)rowc[t] * G + g];
-            zv[i][t] = zp0[(size_t)rowc[t] * G + g];
+            sv[i][t] = sp[t][(size_t)rowc[t] * G + g];
+            zv[i][t] = zp[t][(size_t)rowc[t] * G + g];
         }
     }
     u32x4_t wq[NG][NT];
@@ -237,7 +257,7 @@ __global__ void __launch_bounds__(1024) int4_splitk_kernel(MatPtrs mp, const Act
         for (int j = 0; j < 4; j++) av[i][j] = *reinterpret_cast<const half8_t *>(arow + (size_t)g * kGS + j * 32);
 #pragma unroll
         for (int t = 0; t < NT; t++)
-            wq[i][t] = *reinterpret_cast<const u32x4_t *>(mp.data[0] + (size_t)rowc[t] * (K / 2) + (size_t)g * 64 + kq * 16);
+            wq[i][t] = *reinterpret_cast<const u32x4_t *>(wd[t] + (size_t)rowc[t] * (K / 2) + (size_t)g * 64 + kq * 16);
     }
     const half8_t ones = __builtin_bit_cast(half8_t, (u32x4_t){0x00110011u, 0x00110011u, 0x00100010u, 0x00100010u});
     float4_t acc[NT];
@@ -274,10 +294,11 @@ __global__ void __launch_bounds__(1024) int4_splitk_kernel(MatPtrs mp, const Act
     // parts in part order
     for (int o = tid; o < NT * 32; o += blockDim.x) {
         const int t = o >> 5, l = o & 31;
+        if (tile0 + t >= tile_end) continue;
         const float4_t *rp = red + t * waves * 64;
         float4_t sum = rp[l] + rp[l + 32];
         for (int p = 1; p < waves; p++) sum += rp[p * 64 + l] + rp[p * 64 + l + 32];
-        const int row = row0 + 16 * t + (l & 15);
+        const int row = (tile0 + t) * 16 + (l & 15);
         if (row >= N) continue;
 #pragma unroll
         for (int r = 0; r < 4; r++) {
@@ -287,13 +308,16 @@ __global__ void __launch_bounds__(1024) int4_splitk_kernel(MatPtrs mp, const Act
     }
 }
 
-// y[m][n] = f16(sum over slices of part[s][m][n]), slices in order.  Every
+// y = f16(sum over slices of part[s][m][row], slices in order, times
+// row_scale[m] for rows below scale_rows) into the row's segment.  Every
 // slice's load is issued before the first add (S <= kMaxSlices), so the
 // thread waits one memory latency rather than S.
 constexpr int kMaxSlices = 8;
-__global__ void __launch_bounds__(256) int4_splitk_combine_kernel(const float *__restrict__ part, int S, int count,
-                                                                  __half *__restrict__ y) {
+__global__ void __launch_bounds__(256) int4_splitk_combine_kernel(const float *__restrict__ part, int S, int B, int N,
+                                                                  MatPtrs mp, const float *__restrict__ row_scale,
+                                                                  int scale_rows) {
     const int i = blockIdx.x * blockDim.x + threadIdx.x;
+    const int count = B * N;
     if (i >= count) return;
     float v[kMaxSlices];
 #pragma unroll
@@ -302,50 +326,64 @@ __global__ void __launch_bounds__(256) int4_splitk_combine_kernel(const float *_
 #pragma unroll
     for (int k = 1; k < kMaxSlices; k++)
         if (k < S) s += v[k];
-    y[i] = __float2half(s);
+    const int m = i / N, row = i - m * N;
+    if (row_scale && row < scale_rows) s *= row_scale[m];
+    const int sg = (mp.seg[0] > 0 && row >= mp.seg[0]) ? ((mp.seg[1] > 0 && row >= mp.seg[1]) ? 2 : 1) : 0;
+    const int base = sg == 0 ? 0 : (sg == 1 ? mp.seg[0] : mp.seg[1]);
+    const int end = sg == 0 ? (mp.seg[0] > 0 ? mp.seg[0] : N) : (sg == 1 && mp.seg[1] > 0 ? mp.seg[1] : N);
+    __half *o = sg == 0 ? mp.out[0] : (sg == 1 ? mp.out[1] : mp.out[2]);
+    o[(size_t)m * (end - base) + (row - base)] = __float2half(s);
 }
 
 }  // namespace
 
-// Split-K applies where the per-tile grid leaves compute units idle (fewer
-// 16-row tiles than compute units) at 3-8 rows, one matrix, >= 32 groups.
+// Split-K over an image: one matrix (row segments allowed), 3-8 rows, >= 16
+// groups, up to two tiles per CU -- where the per-tile kernels would read the
+// whole operand image once per 16 rows.  split_rows: the rows from there on
+// read the second image (mixed rounding), N otherwise.
 namespace {
 constexpr int kSplitNT = 5;   // 16-row tiles per band
 constexpr int kSplitNG = 2;   // groups per wave
-int splitk_slices(int N, int cus) {
-    const int bands = ((N + 15) / 16 + kSplitNT - 1) / kSplitNT;
-    return std::max(2, std::min(kMaxSlices, cus / std::max(1, bands)));
+struct SplitBands {
+    int gb, bands0, bands, S;
+};
+SplitBands splitk_bands(int N, int split_rows, int cus) {
+    const int tiles = (N + 15) / 16;
+    SplitBands b;
+    b.gb = split_rows >= N ? tiles : std::min(tiles, split_rows / 16);
+    b.bands0 = (b.gb + kSplitNT - 1) / kSplitNT;
+    b.bands = b.bands0 + (tiles - b.gb + kSplitNT - 1) / kSplitNT;
+    b.S = std::max(2, std::min(kMaxSlices, cus / std::max(1, b.bands)));
+    return b;
 }
 }  // namespace
 
-bool splitk_applies(int nmat, int B, int N, int K, int cus) {
+bool splitk_applies(int nmat, int B, int N, int K, int split_rows, int cus) {
     const int G = K / kGS, tiles = (N + 15) / 16;
-    if (nmat != 1 || B < 3 || B > 8 || G < 32 || tiles >= cus) return false;
-    const int S = splitk_slices(N, cus);
-    return (G + S - 1) / S <= 16 * kSplitNG;   // 16 waves of kSplitNG groups
+    if (nmat != 1 || B < 3 || B > 8 || G < 16 || tiles > 2 * cus) return false;
+    const SplitBands b = splitk_bands(N, split_rows, cus);
+    return (G + b.S - 1) / b.S <= 16 * kSplitNG;   // 16 waves of kSplitNG groups
 }
 
-size_t splitk_workspace_bytes(int B, int N, int K, int cus) {
-    (void)K;
-    return (size_t)splitk_slices(N, cus) * B * N * sizeof(float);
+size_t splitk_workspace_bytes(int B, int N, int split_rows, int cus) {
+    return (size_t)splitk_bands(N, split_rows, cus).S * B * N * sizeof(float);
 }
 
-int launch_splitk(hipStream_t st, int cus, int N, int K, int B, const MatPtrs &mp, const ActIn &in, void *ws) {
+int launch_splitk(hipStream_t st, int cus, int N, int K, int B, const MatPtrs &mp, const ActIn &in, int split_rows,
+                  void *ws) {
     const int G = K / kGS;
-    constexpr int NT = kSplitNT;
-    const int bands = ((N + 15) / 16 + NT - 1) / NT;
-    const int S = splitk_slices(N, cus);
-    const int gper = (G + S - 1) / S;
+    const SplitBands b = splitk_bands(N, split_rows, cus);
+    const int gper = (G + b.S - 1) / b.S;
     const int waves = std::min(16, (gper + kSplitNG - 1) / kSplitNG);
     if (waves * kSplitNG < gper) return imh::fail(IMH_EINVAL, "int4 split-K: too many groups per slice");
-    const size_t lds = (size_t)NT * waves * 64 * sizeof(float4_t);
+    const size_t lds = (size_t)kSplitNT * waves * 64 * sizeof(float4_t);
     float *part = static_cast<float *>(ws);
-    hipLaunchKernelGGL((int4_splitk_kernel<NT, kSplitNG>), dim3(bands, S), dim3(64 * waves), lds, st, mp, in, N, K, B, S,
-                       part);
+    hipLaunchKernelGGL((int4_splitk_kernel<kSplitNT, kSplitNG>), dim3(b.bands, b.S), dim3(64 * waves), lds, st, mp, in,
+                       N, K, B, b.S, b.gb, b.bands0, part);
     IMH_HIP(hipGetLastError());
     const int count = B * N;
-    hipLaunchKernelGGL(int4_splitk_combine_kernel, dim3((count + 255) / 256), dim3(256), 0, st, part, S, count,
-                       mp.out[0]);
+    hipLaunchKernelGGL(int4_splitk_combine_kernel, dim3((count + 255) / 256), dim3(256), 0, st, part, b.S, B, N, mp,
+                       in.row_scale, split_rows);
     IMH_HIP(hipGetLastError());
     return IMH_OK;
 }

@@ -693,11 +693,14 @@ int launch_band_matvec(hipStream_t st, int cus, int B, int nmat, int epi, int N,
 // are not read (the kernel forms them on the matrix cores).
 bool image_da_applies(int nmat, int B, int K);
 int launch_image_da(hipStream_t st, int nmat, int epi, int N, int K, int B, const MatPtrs &mp, const ActIn &in);
-// Split-K over an IMAGE source (one matrix, EPI_STORE, no row segments or
-// row scale, 3-8 rows) where the tile grid would leave compute units idle:
-// f32 partials in ws (splitk_workspace_bytes), then a combine launch.
-bool splitk_applies(int nmat, int B, int N, int K, int cus);
-size_t splitk_workspace_bytes(int B, int N, int K, int cus);
-int launch_splitk(hipStream_t st, int cus, int N, int K, int B, const MatPtrs &mp, const ActIn &in, void *ws);
+// Split-K over an IMAGE source (one matrix with its row segments, EPI_STORE,
+// 3-8 rows): f32 partials in ws (splitk_workspace_bytes), then a combine
+// launch that applies in.row_scale to the rows below split_rows and writes
+// each row's segment.  split_rows: the first row of the second image (mixed
+// rounding: mp.seg[0]), else N.
+bool splitk_applies(int nmat, int B, int N, int K, int split_rows, int cus);
+size_t splitk_workspace_bytes(int B, int N, int split_rows, int cus);
+int launch_splitk(hipStream_t st, int cus, int N, int K, int B, const MatPtrs &mp, const ActIn &in, int split_rows,
+                  void *ws);
 
 }  // namespace imh_int4
