@@ -35,6 +35,31 @@ __device__ __forceinline__ float row16_max(float v) {
     return v;
 }
 
+// The same reductions for code where all 16 lanes of the row are active: the
+// moves leave the lanes' old values undefined (every source lane of these
+// patterns lies inside the row), so the compiler can fold each move into the
+// add or max as a DPP operand instead of first zeroing the destination.
+template <int CTRL>
+__device__ __forceinline__ float dpp_mov_full(float v) {
+    return __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), CTRL, 0xF, 0xF, false));
+}
+
+__device__ __forceinline__ float row16_sum_full(float v) {
+    v += dpp_mov_full<kQuadXor1>(v);
+    v += dpp_mov_full<kQuadXor2>(v);
+    v += dpp_mov_full<kRowRor4>(v);
+    v += dpp_mov_full<kRowRor8>(v);
+    return v;
+}
+
+__device__ __forceinline__ float row16_max_full(float v) {
+    v = fmaxf(v, dpp_mov_full<kQuadXor1>(v));
+    v = fmaxf(v, dpp_mov_full<kQuadXor2>(v));
+    v = fmaxf(v, dpp_mov_full<kRowRor4>(v));
+    v = fmaxf(v, dpp_mov_full<kRowRor8>(v));
+    return v;
+}
+
 // the value in the wave's first active lane, as a wave-uniform scalar
 __device__ __forceinline__ float first_lane(float v) {
     return __builtin_bit_cast(float, __builtin_amdgcn_readfirstlane(__builtin_bit_cast(int, v)));

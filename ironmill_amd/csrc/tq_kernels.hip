@@ -256,7 +256,7 @@ __global__ void __launch_bounds__(64 * kWriteMaxWaves) tq_cache_write_kernel(
 // positions 4g..4g+3 at dims 8c..8c+7 (four 8-byte row loads, coalesced
 // across the 16 lanes of a row) and its B operand for block j is the
 // codebook values (f16 hi, lo) of byte j of the four rows -- a register
-// transpose, no LDS staging.  The weights w * v_scale go through a 128-byte
+// transpose, no LDS staging.  The weights w * v_scale go through a 256-byte
 // per-wave LDS buffer into row 4hh of operand A as f16, each weight twice.  Built with -amdgpu-mfma-vgpr-form so the accumulators
 // stay in VGPRs (no AGPR round trip around the softmax rescale).
 // Optional QK-norm + RoPE of the query ahead of the rotation (head_dim 128 =
@@ -361,6 +361,7 @@ __device__ __forceinline__ void load_chunk(const ChunkRsrc &r, int p0, int n_l, 
 // k of w is one v_perm: (byte << 8) | lane offset (4 (l & 31), + 128 for V).
 constexpr int kTabRowBytes = 256;
 constexpr int kSpreadMinLen = 1024;   // positions per split from which the decode loop uses them
+constexpr int kLazyMinLen = 1024;     // positions per split from which the rescale is lazy
 constexpr int kTabBytes = 256 * kTabRowBytes;
 __device__ __forceinline__ uint32_t tab_read(const uint8_t *tabs, uint32_t w, int k, uint32_t lane_off) {
     const uint32_t off = __builtin_amdgcn_perm(w, lane_off, 0x0C0C0000u | ((4u + (uint32_t)k) << 8));
@@ -418,6 +419,29 @@ __device__ __forceinline__ void k_operands(const uint32_t *kw2, const Tab &tab, 
     Bs = __builtin_bit_cast(half8_t, make_uint4(bs[0], bs[1], bs[2], bs[3]));
 }
 
+// Score operand B of code word w (dims 4t .. 4t + 3 of the lane's 32): the
+// four bytes' codebook entries as they sit in the table, (f16 hi, f16 lo)
+// pairs, so each k pair of the contraction is one dim's hi and lo part and no
+// repacking is needed (the operand A row that takes q_hi twice gives
+// q_hi (K_hi + K_lo), the row that takes q_lo and 0 gives q_lo K_hi).
+template <class Tab>
+__device__ __forceinline__ half8_t k_pair_operand(uint32_t w, const Tab &tab) {
+    return __builtin_bit_cast(half8_t, make_uint4(tab.k(w, 0), tab.k(w, 1), tab.k(w, 2), tab.k(w, 3)));
+}
+// The +-1 QJL signs of code words kw2[0], kw2[1] from bit 7, k-slot order
+// {0, 2, 1, 3} within each word.
+__device__ __forceinline__ half8_t k_sign_operand(const uint32_t *kw2) {
+    uint32_t bs[4];
+#pragma unroll
+    for (int hw = 0; hw < 2; hw++) {
+        const uint32_t w = kw2[hw];
+        // +1 (0x3C00) where bit 7 of the code is set, -1 (0xBC00) where not
+        bs[2 * hw] = ((w << 8) & 0x80008000u) ^ 0xBC00BC00u;
+        bs[2 * hw + 1] = (w & 0x80008000u) ^ 0xBC00BC00u;
+    }
+    return __builtin_bit_cast(half8_t, make_uint4(bs[0], bs[1], bs[2], bs[3]));
+}
+
 // P.V operand B of dim block j: codebook values (hi, lo) of byte j of the
 // lane's four V position rows
 template <class Tab>
@@ -433,7 +457,10 @@ __device__ __forceinline__ half8_t v_operand(const ChunkIn &c, int j, const Tab 
 
 // Occupancy: 3 waves per SIMD (168 VGPRs); the fused token writer's extra
 // live state needs more than that, so it runs at 2 rather than spill.
-template <int GQA, bool FUSED, bool SPREAD>
+// LAZY: the softmax rescale of the output accumulators is skipped for chunks
+// where no head's running maximum grew (chosen for splits of kLazyMinLen
+// positions or more).
+template <int GQA, bool FUSED, bool SPREAD, bool LAZY>
 __global__ void __launch_bounds__(64 * kWaves) __attribute__((amdgpu_waves_per_eu(FUSED ? 2 : 3))) tq_attention_kernel(
     const __half *__restrict__ q, int nh, int nkv, int max_seq, int seq_len, int T,
     const int32_t *__restrict__ seq_lens, float attn_scale, const float *__restrict__ signs,
@@ -448,7 +475,8 @@ __global__ void __launch_bounds__(64 * kWaves) __attribute__((amdgpu_waves_per_e
     __shared__ int32_t wpm[2][256];    // token writer: prefix maxima
     __shared__ uint32_t ktab[256];   // entry c & 0x7F, indexed by the whole code byte
     __shared__ uint32_t vtab[256];   // V entry c, same packing as ktab
-    __shared__ _Float16 wbuf[kWaves][4][16];
+    // P.V weights of a chunk, each f16 twice (hi and lo slots of operand A)
+    __shared__ __attribute__((aligned(16))) uint32_t wbuf[kWaves][4][16];
     // SPREAD: the spread tables of the KV loop; the waves' partial outputs om
     // use the same bytes before the tables are built and after the loop
     __shared__ __attribute__((aligned(16))) uint8_t tabs[SPREAD ? kTabBytes : kWaves * GQA * kD * 4];
@@ -714,31 +742,37 @@ __global__ void __launch_bounds__(64 * kWaves) __attribute__((amdgpu_waves_per_e
             tab.kt = ktab;
             tab.vt = vtab;
         }
-        // score operands A, k-slot order within each 4-byte word: bytes {0, 2, 1, 3}.
-        // Rows 4h..4h+3 carry head h: aqk = {q_hi, q_lo, 0, 0} (against K hi),
-        // aqh = {q_hi, 0, 0, 0} (against K lo), aqs = {0, 0, s_hi, s_lo} (against
-        // the QJL signs), so one accumulator holds, in lane group h's four
-        // registers, q_hi.K + q_hi.K_lo, q_lo.K_hi, s_hi.sgn, s_lo.sgn.
+        // score operands A.  Rows 4h..4h+3 carry head h.  Against the table
+        // pairs of word t (k pair i/2 = dim 32 g + 4 t + i/2, hi then lo):
+        // aq[t] = {q_hi, q_hi} in row 4h and {q_lo, 0} in row 4h + 1; against
+        // the QJL signs of words 2j, 2j + 1 (k-slot order {0, 2, 1, 3} within
+        // each word): aqs[j] = s_hi in row 4h + 2, s_lo in row 4h + 3.  Lane
+        // group h's four accumulator registers then hold q_hi.K + q_hi.K_lo,
+        // q_lo.K_hi (ds) and s_hi.sgn, s_lo.sgn (dg).
         const int am = lane & 15;
         const int ah = am >> 2, ar = am & 3;
         const bool arow = ah < GQA;
-        half8_t aqk[4], aqh[4], aqs[4];
+        half8_t aq[8], aqs[4];
+        const _Float16 z = (_Float16)0.0f;
+    #pragma unroll
+        for (int t = 0; t < 8; t++) {
+    #pragma unroll
+            for (int i = 0; i < 4; i++) {
+                const float vq = arow ? qs[ah][0][kg * 32 + 4 * t + i] : 0.0f;
+                const _Float16 qh = (_Float16)vq;
+                const _Float16 ql = (_Float16)(vq - (float)qh);
+                aq[t][2 * i] = ar == 0 ? qh : (ar == 1 ? ql : z);
+                aq[t][2 * i + 1] = ar == 0 ? qh : z;
+            }
+        }
         constexpr int slot_byte[8] = {0, 2, 1, 3, 4, 6, 5, 7};
     #pragma unroll
         for (int j = 0; j < 4; j++) {
     #pragma unroll
             for (int i = 0; i < 8; i++) {
-                float vq = 0.0f, vs = 0.0f;
-                if (arow) {
-                    const int d = kg * 32 + j * 8 + slot_byte[i];
-                    vq = qs[ah][0][d];
-                    vs = qs[ah][1][d];
-                }
-                const _Float16 qh = (_Float16)vq, sh = (_Float16)vs;
-                const _Float16 ql = (_Float16)(vq - (float)qh), sl = (_Float16)(vs - (float)sh);
-                const _Float16 z = (_Float16)0.0f;
-                aqk[j][i] = ar == 0 ? qh : (ar == 1 ? ql : z);
-                aqh[j][i] = ar == 0 ? qh : z;
+                const float vs = arow ? qs[ah][1][kg * 32 + j * 8 + slot_byte[i]] : 0.0f;
+                const _Float16 sh = (_Float16)vs;
+                const _Float16 sl = (_Float16)(vs - (float)sh);
                 aqs[j][i] = ar == 2 ? sh : (ar == 3 ? sl : z);
             }
         }
@@ -751,38 +785,41 @@ __global__ void __launch_bounds__(64 * kWaves) __attribute__((amdgpu_waves_per_e
         auto process = [&](const ChunkIn &c, const int p0) __attribute__((always_inline)) {
             // ---- scores S[h][n] for 16 positions via MFMA ----
             const uint32_t kw[8] = {c.k0.x, c.k0.y, c.k0.z, c.k0.w, c.k1.x, c.k1.y, c.k1.z, c.k1.w};
-            float4_t d1 = {0, 0, 0, 0};
+            float4_t ds = {0, 0, 0, 0}, dg = {0, 0, 0, 0};
     #pragma unroll
             for (int j = 0; j < 4; j++) {
-                half8_t Bh, Bl, Bs;
-                k_operands(&kw[2 * j], tab, Bh, Bl, Bs);
-                d1 = __builtin_amdgcn_mfma_f32_16x16x32_f16(aqk[j], Bh, d1, 0, 0, 0);
-                d1 = __builtin_amdgcn_mfma_f32_16x16x32_f16(aqh[j], Bl, d1, 0, 0, 0);
-                d1 = __builtin_amdgcn_mfma_f32_16x16x32_f16(aqs[j], Bs, d1, 0, 0, 0);
+                ds = __builtin_amdgcn_mfma_f32_16x16x32_f16(aq[2 * j], k_pair_operand(kw[2 * j], tab), ds, 0, 0, 0);
+                dg = __builtin_amdgcn_mfma_f32_16x16x32_f16(aqs[j], k_sign_operand(&kw[2 * j]), dg, 0, 0, 0);
+                ds = __builtin_amdgcn_mfma_f32_16x16x32_f16(aq[2 * j + 1], k_pair_operand(kw[2 * j + 1], tab), ds, 0,
+                                                           0, 0);
             }
-            // lane (n, g): d1[0..3] = the four partial products of head g at position p0 + n
+            // lane (n, g): ds[0..1], dg[2..3] = the four partial products of head g at position p0 + n
             const bool valid = (p0 + n_l) < p_end;
             const float qw = c.krn * qjl_factor * c.ksc;
-            const float sc = valid ? attn_scale * ((d1[0] + d1[1]) * c.ksc + (d1[2] + d1[3]) * qw) : -INFINITY;
-            const float cm = imh_dpp::row16_max(sc);
+            const float sc = valid ? attn_scale * ((ds[0] + ds[1]) * c.ksc + (dg[2] + dg[3]) * qw) : -INFINITY;
+            const float cm = imh_dpp::row16_max_full(sc);
             const float nm = fmaxf(m_run, cm);
             const bool live = nm != -INFINITY;   // a head with no position yet keeps weight 0
             const float corr = live ? __expf(m_run - nm) : 1.0f;
             const float w = live ? __expf(sc - nm) : 0.0f;
-            l_run = l_run * corr + imh_dpp::row16_sum(w);
+            l_run = l_run * corr + imh_dpp::row16_sum_full(w);
             m_run = nm;
-            if (__builtin_amdgcn_ballot_w64(corr != 1.0f)) {   // some head's max grew
+            // LAZY: only when some head's maximum grew, which on long splits
+            // is rare after the first chunks; on short splits the test and
+            // its branch cost more than the eight multiplies they skip
+            if (!LAZY || __builtin_amdgcn_ballot_w64(corr != 1.0f)) {
     #pragma unroll
                 for (int j = 0; j < 8; j++) acc[j][0] *= corr;
             }
-            // weights * v_scale as f16 hi + lo, transposed through LDS into operand A
-            wbuf[wave][kg][n_l] = (_Float16)(w * c.vsc);
+            // weights * v_scale as f16, each twice (against the V entries' hi
+            // and lo), transposed through LDS into operand A
+            const uint32_t wh = __builtin_bit_cast(uint16_t, (_Float16)(w * c.vsc));
+            wbuf[wave][kg][n_l] = wh | (wh << 16);
             __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
             __builtin_amdgcn_wave_barrier();
             __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-            half4_t w4 = {0, 0, 0, 0};
-            if (arow && ar == 0) w4 = *reinterpret_cast<const half4_t *>(&wbuf[wave][ah][4 * kg]);
-            const half8_t wa = {w4[0], w4[0], w4[1], w4[1], w4[2], w4[2], w4[3], w4[3]};
+            half8_t wa = {0, 0, 0, 0, 0, 0, 0, 0};
+            if (arow && ar == 0) wa = *reinterpret_cast<const half8_t *>(&wbuf[wave][ah][4 * kg]);
             // ---- o += W . V: operand B of block j = codebook values (hi, lo) of
             // byte j of the four position rows ----
     #pragma unroll
@@ -1488,8 +1525,8 @@ static int run_attention(imh_stream *stream, const imh_tq_tables *t, const imh_t
     }
     const __half *qh = reinterpret_cast<const __half *>(q);
     dim3 grid(S, nkv, B);
-#define IMH_TQ_LAUNCH(G, F, SP)                                                                                \
-    hipLaunchKernelGGL((tq_attention_kernel<G, F, SP>), grid, dim3(64 * kWaves), 0, stream->stream, qh, (int)num_heads, \
+#define IMH_TQ_LAUNCH(G, F, SP, LZ)                                                                            \
+    hipLaunchKernelGGL((tq_attention_kernel<G, F, SP, LZ>), grid, dim3(64 * kWaves), 0, stream->stream, qh, (int)num_heads, \
                        (int)nkv, (int)cache->max_seq_len, (int)L, (int)token_count, seq_lens, attn_scale,       \
                        t->signs, t->qjl_t,                                                                      \
                        t->k_codebook, t->v_codebook, cache->k_codes, cache->v_codes, cache->k_scales,           \
@@ -1531,18 +1568,28 @@ static int run_attention(imh_stream *stream, const imh_tq_tables *t, const imh_t
     // token writers, whose workgroups would hold the tables' 64 KB of LDS too
     // and no longer fit beside two streaming workgroups per CU
     const bool spread = !fused && split_len >= kSpreadMinLen;
-    if (fused) {   // the writer workgroups only in this instantiation
-        if (gqa == 4) IMH_TQ_LAUNCH(4, true, false);
-        else if (gqa == 2) IMH_TQ_LAUNCH(2, true, false);
-        else IMH_TQ_LAUNCH(1, true, false);
+    // lazy rescale from kLazyMinLen positions per split (decode at batch 8,
+    // ctx 8k: 3.51 -> 3.34 ms per step; at batch 1, ~5 chunks per wave, the
+    // eager rescale is faster: 1.74 -> 1.72 ms); the spread instantiation
+    // always has long splits
+    static_assert(kLazyMinLen == kSpreadMinLen, "non-fused: lazy exactly when spread");
+    const bool lazy = split_len >= kLazyMinLen;
+    if (fused && lazy) {   // the writer workgroups only in these instantiations
+        if (gqa == 4) IMH_TQ_LAUNCH(4, true, false, true);
+        else if (gqa == 2) IMH_TQ_LAUNCH(2, true, false, true);
+        else IMH_TQ_LAUNCH(1, true, false, true);
+    } else if (fused) {
+        if (gqa == 4) IMH_TQ_LAUNCH(4, true, false, false);
+        else if (gqa == 2) IMH_TQ_LAUNCH(2, true, false, false);
+        else IMH_TQ_LAUNCH(1, true, false, false);
     } else if (spread) {
-        if (gqa == 4) IMH_TQ_LAUNCH(4, false, true);
-        else if (gqa == 2) IMH_TQ_LAUNCH(2, false, true);
-        else IMH_TQ_LAUNCH(1, false, true);
+        if (gqa == 4) IMH_TQ_LAUNCH(4, false, true, true);
+        else if (gqa == 2) IMH_TQ_LAUNCH(2, false, true, true);
+        else IMH_TQ_LAUNCH(1, false, true, true);
     } else {
-        if (gqa == 4) IMH_TQ_LAUNCH(4, false, false);
-        else if (gqa == 2) IMH_TQ_LAUNCH(2, false, false);
-        else IMH_TQ_LAUNCH(1, false, false);
+        if (gqa == 4) IMH_TQ_LAUNCH(4, false, false, false);
+        else if (gqa == 2) IMH_TQ_LAUNCH(2, false, false, false);
+        else IMH_TQ_LAUNCH(1, false, false, false);
     }
 #undef IMH_TQ_LAUNCH
     IMH_HIP(hipGetLastError());
