@@ -36,9 +36,11 @@
 //    current group computes, their loads issued one or two per k step (a
 //    burst of twelve at the group's start held the wave's issue for ~400
 //    cycles), unconditionally (the last group re-loads itself), so no wait
-//    for them sits inside the compute: one barrier per group.  K is split over workgroups when the tile grid is smaller than
-//    twice the CU count; the f32 partials are summed in split order by a
-//    second kernel (deterministic).
+//    for them sits inside the compute: one barrier per group.  K is split over
+//    workgroups when the tile grid leaves workgroup slots (two per CU) idle
+//    and a model of the dispatch says the split pays for its partials; the
+//    f32 partials are summed in split order by a second kernel
+//    (deterministic).
 #include <hip/hip_runtime.h>
 #include <hip/hip_fp16.h>
 
@@ -453,6 +455,40 @@ int check_gemm_weight(const imh_affine_int4_weight *w, const char *who) {
     return IMH_OK;
 }
 
+// K splits for a grid of `tiles` output tiles (fewer than the slots, two
+// per CU).  Workgroups of a launch are dispatched as slots free up, and each
+// costs about the same per group: ~2.4 us bf16 / ~1.9 us fp8 with two per
+// CU, ~0.9 of that alone on its CU.  So a grid of W workgroups runs full
+// rounds of two per CU, then its remainder (one per CU where it fits); a
+// split adds the partials' round trip (written during the GEMM, read back by
+// the reduce launch at ~4.5 TB/s plus ~2 us).  Measured against the earlier
+// rule (as many splits as fill two per CU, rounded up): K 2560 -> N 9728 at
+// M = 512 (304 tiles) 1 split instead of 2, 65 -> 57 us (bf16); K 9728 ->
+// N 2560 at M = 512 (80 tiles) 6 instead of 7, 72 -> 60 us; at M = 2048
+// (320 tiles) 1 split took 200 us against 186 with 2 and 185-191 with 3.
+// At least 4 groups per split.
+double grid_us(long long W, int per, int cus, double g2) {
+    double us = 0.0;
+    for (; W > 2 * cus; W -= 2 * cus) us += per * g2;
+    return us + per * (W > cus ? g2 : 0.9 * g2);
+}
+int gemm_splits(int tiles, int G, int M, int N, int cus, int P) {
+    const double g2 = P == PREC_BF16 ? 2.4 : 1.9;
+    int best = 1;
+    double best_us = grid_us(tiles, G, cus, g2);
+    for (int s = 2; s <= G / 4; s++) {
+        const int per = (G + s - 1) / s;
+        if ((G + per - 1) / per != s) continue;
+        const double us = grid_us((long long)tiles * s, per, cus, g2) +
+                          ((double)s * M * N * 4 + (double)M * N * 2) / 4.5e6 + 2.0;
+        if (us < best_us * 0.98) {   // a split must win clearly
+            best_us = us;
+            best = s;
+        }
+    }
+    return best;
+}
+
 }  // namespace
 
 extern "C" {
@@ -479,12 +515,11 @@ int imh_affine_gemm_int4(imh_stream *stream, const void *x, uint32_t M, const im
     const int N = (int)w->n, K = (int)w->k, G = K / kGS;
     const int P = precision == IMH_GEMM_BF16 ? PREC_BF16 : PREC_FP8;
     const int eb = P == PREC_BF16 ? 2 : 1;
-    // K split: about two workgroups per CU, at least 4 groups per split
+    // K split (fewer tiles than workgroup slots, two per CU)
     const int cus = stream->dev->props.multiProcessorCount;
     const int wgc = P == PREC_BF16 ? wg_cols<PREC_BF16>() : wg_cols<PREC_FP8>();
     const int tiles = ((N + wgc - 1) / wgc) * (((int)M + kBM - 1) / kBM);
-    int splits = 1;
-    if (tiles < 2 * cus) splits = std::max(1, std::min((2 * cus + tiles - 1) / tiles, G / 4));
+    int splits = tiles < 2 * cus ? gemm_splits(tiles, G, (int)M, N, cus, P) : 1;
     const int per = (G + splits - 1) / splits;
     splits = (G + per - 1) / per;
     // scratch slot 0: operand rows + group sums; slot 2: split partials
