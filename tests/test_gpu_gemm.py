@@ -3,8 +3,9 @@ superblock_matmul_int4, affine_matmul.metal:10-152, reached through
 encode_projection at token_count > 1, projection.rs:227-312) against the CPU
 oracle's dequantize-then-compute chain.
 
-The GEMM multiplies the f16 dequantized weight with x (exact f16) or, with
-AWQ, with x / awq carried as f16 hi + lo (~22 bits; rounding it to f16 alone,
+The GEMM multiplies the exact weight (the code minus its zero point in f16,
+the f16 scale applied per group in f32) with x (exact f16) or, with AWQ,
+with x / awq carried as f16 hi + lo (~22 bits; rounding it to f16 alone,
 as the reference's prefill kernel does, moves outputs by several fp16 steps
 where terms cancel).  Tolerance as on the decode path: rel-L2 <= 1e-3
 and max-abs <= max(2e-2, 2 fp16 steps of the reference value)
@@ -38,6 +39,16 @@ def acts(m, k, seed):
     idx = rng.choice(k, max(1, k // 100), replace=False)
     x[:, idx] *= 20.0
     return x.astype(np.float16)
+
+
+def exact_weights(q):
+    """The uploaded weight exactly, in f64: f16 scale x (code - f16 zero point)."""
+    codes = np.empty((q.n, q.k), np.float64)
+    codes[:, 0::2] = q.data & 0xF
+    codes[:, 1::2] = q.data >> 4
+    sc = np.repeat(q.scales.astype(np.float64), q.group_size, axis=1)
+    zp = np.repeat(q.zeros.astype(np.float64), q.group_size, axis=1)
+    return sc * (codes - zp)
 
 
 def dense(w, s):
@@ -106,10 +117,37 @@ def test_gemm_fused_gate_up(dev, stream, act):
     xd, out = dev.upload(x16), dev.empty((m, n), np.float16)
     ops.encode_fused_ffn_gate_up_act_int4(stream, xd, gate, up, out, m, use_gelu=(act == "gelu"))
     stream.sync()
+    got = out.read().astype(np.float64)
     wdq_g, awq16 = dense(wg, s)
     wdq_u, _ = dense(wu, s)
     ref = O.gate_up_act(wdq_g, wdq_u, x16, awq16, act=act)
-    assert_close(out.read(), ref, what=f"gemm fused gate+up {act}", ulps=ulps_for(True))
+    assert_close(got, ref, what=f"gemm fused gate+up {act} vs the CPU path", max_abs=np.inf)
+    # Element-wise against the exact value of what the kernel computes: the
+    # uploaded codes with their f16 scales and zero points, x / awq unrounded,
+    # in f64.  The CPU path rounds each dequantized weight to f16; act(gate) *
+    # up amplifies that, and at this shape it alone moves an output ~5 f16
+    # steps (row 31, column 8523: exact -6.9241, CPU path -6.9079, 0.98 of
+    # max(2e-2, 2 steps)), so the bound there would pass or fail on the
+    # rounding direction of a correct result.  Bound: 2 f16 steps of the exact
+    # value, plus 2^-16 of the summed magnitudes the f32 accumulation and the
+    # hi / lo split of x / awq see, carried through act(gate) * up.
+    qg = quant.quantize_int4(wg, awq_scales=s)
+    qu = quant.quantize_int4(wu, awq_scales=s)
+    xa = x16.astype(np.float64) / s.astype(np.float16).astype(np.float64)[None, :]
+    Wg, Wu = exact_weights(qg), exact_weights(qu)
+    g, u = xa @ Wg.T, xa @ Wu.T
+    mg, mu = np.abs(xa) @ np.abs(Wg).T, np.abs(xa) @ np.abs(Wu).T
+    if act == "silu":
+        a = g / (1.0 + np.exp(-g))
+    else:
+        a = 0.5 * g * (1.0 + np.tanh(0.7978845608028654 * (g + 0.044715 * g ** 3)))
+    exact = a * u
+    slack = 2.0 ** -16 * 1.1 * (np.abs(u) * mg + np.abs(a) * mu)
+    bound = 2.0 * np.spacing(np.abs(exact).astype(np.float16)).astype(np.float64) + slack
+    err = np.abs(got - exact)
+    worst = np.unravel_index(np.argmax(err / bound), err.shape)
+    assert np.all(err <= bound), (f"gemm fused gate+up {act}: |got - exact| {err[worst]:.3e} > "
+                                  f"{bound[worst]:.3e} at {worst} (exact {exact[worst]:.5f}, got {got[worst]:.5f})")
 
 
 def test_gemm_batched_gate_up(dev, stream):
