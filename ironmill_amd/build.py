@@ -24,9 +24,15 @@ SOURCES = ["runtime.hip", "int4_matvec.hip", "int4_matvec_raw.hip", "int4_matvec
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 # -packed-fp32-ops: hipcc must not emit packed f32 VALU ops (they have given
 # silent wrong results on these machines); the host pass ignores the feature.
+# -amdgpu-kernarg-preload-count: the dispatcher places a kernel's leading
+# scalar arguments (up to 14 SGPRs) in registers before its first
+# instruction, so the loads that need them issue without waiting for the
+# argument memory (~0.25 us per latency-bound launch; the code object keeps
+# a 256-byte entry that loads them itself for dispatchers without preload).
 FLAGS = [
     "--offload-arch=gfx950", "-O3", "-std=c++17", "-fPIC", "-Wall",
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+    "-mllvm", "-amdgpu-kernarg-preload-count=16",
 ]
 
 
