@@ -190,7 +190,8 @@ def bench_attention(dev, stream, ops, batch, ctx, steps, warmup, layers, eager=F
     ms = total / steps
     gbs = tq_bytes(batch, ctx) / (ms * 1e-3) / 1e9
     return {"batch": batch, "ctx": ctx, "us": round(ms * 1e3, 2), "GB/s": round(gbs, 1),
-            "frac": round(gbs / HBM_PEAK_GBS, 4), "bytes": tq_bytes(batch, ctx)}
+            "frac": round(gbs / HBM_PEAK_GBS, 4), "bytes": tq_bytes(batch, ctx), "launches": steps,
+            "warmup_launches": warmup}
 
 
 def bench_tq_prefill(dev, stream, ops, batch, ctx, tokens, steps, warmup, eager=False):
@@ -245,7 +246,7 @@ def bench_fp16_attention(dev, stream, ops, batch, ctx, steps, warmup, layers, ea
     nbytes = fp16_kv_bytes(batch, ctx)
     gbs = nbytes / (ms * 1e-3) / 1e9
     return {"batch": batch, "ctx": ctx, "us": round(ms * 1e3, 2), "GB/s": round(gbs, 1),
-            "frac": round(gbs / HBM_PEAK_GBS, 4), "bytes": nbytes}
+            "frac": round(gbs / HBM_PEAK_GBS, 4), "bytes": nbytes, "launches": steps, "warmup_launches": warmup}
 
 
 GEMM_PEAK_TFS = {"f16": 2500.0, "bf16": 2500.0, "fp8": 5000.0}   # MI355X dense MFMA peaks
@@ -796,13 +797,16 @@ def main():
         # sustained rates: a warmup graph long enough for the clocks to settle
         # (measured: the first ~50 ms of back-to-back launches after the weight
         # benchmarks run up to 10 % slower than the steady state)
-        att_warm = max(200, args.warmup)
+        # (~25 us per call at batch 1: 2000 warmup launches are ~50 ms, and 500
+        # timed ones ~12 ms; ~200 us at batch 16)
+        att_runs = {1: (max(500, args.steps), max(2000, args.warmup)),
+                    16: (max(20, args.steps // 4), max(200, args.warmup))}
         for bb, layers in ((1, 8), (16, 1)):
-            r = bench_attention(dev, stream, ops, bb, 32768, max(20, args.steps // 4), att_warm, layers)
+            r = bench_attention(dev, stream, ops, bb, 32768, *att_runs[bb], layers)
             details[f"tq_attention_b{bb}_ctx32k"] = r
             log(f"TQ attention B={bb} ctx=32k: {r['us']} us {r['GB/s']} GB/s")
         for bb, layers in ((1, 8), (16, 1)):
-            r = bench_fp16_attention(dev, stream, ops, bb, 32768, max(20, args.steps // 4), att_warm, layers)
+            r = bench_fp16_attention(dev, stream, ops, bb, 32768, *att_runs[bb], layers)
             details[f"fp16_attention_b{bb}_ctx32k"] = r
             log(f"FP16-KV attention B={bb} ctx=32k: {r['us']} us {r['GB/s']} GB/s")
         for bb in (1, 8):

@@ -70,22 +70,41 @@ __host__ __device__ inline BandLds band_lds(int G, int BM, int NMAT, int TM, int
 }
 
 // grid NWG; block 64 * NMAT * W.
+// Leading arguments: what the loads ahead of the issue-order barrier need,
+// which the dispatcher preloads into SGPRs (14 at most) before the first
+// instruction -- so those loads do not wait for the argument memory:
+//   plain (and MB): x, awq, scales / zeros of matrix 0, then those of matrix
+//                   1 (two matrices) or matrix 0's weights (one);
+//   residual-norm:  a, b, gamma, awq, scales / zeros of matrix 0;
+//   image:          hi, lo, scales / zeros, weights;
+// and the dimensions in two words, nwb = N | W << 20 | B << 24 and kg = K |
+// NWG << 16 (the grid and block sizes would be argument loads of their own).
+// The rest comes from mp / in.  (Eight pointers of 48 bits with the
+// dimensions in their high halves, seven words, measured no faster: gate+up
+// B=1 7.96 -> 7.91 us, down 6.46 -> 6.57.)
+struct BandLead {
+    const void *p[6];
+    uint32_t nwb, kg;
+};
 template <int NMAT, int EPI, int TM, int NP, int BM, int XC, bool RN, bool IMG = false, int PD = 1, bool MB = false>
-__global__ void __launch_bounds__(512) int4_band_kernel(MatPtrs mp, const ActIn in, int N, int K, int B, int W) {
-    const __half *__restrict__ x = in.a;
-    const __half *__restrict__ awq = in.awq;
-    // every kernel argument this instantiation reads, into SGPRs here: left
-    // to itself the compiler issued some of their scalar loads ~120
-    // instructions in, a second serialized trip to the argument memory ahead
-    // of the first activation load
-    asm volatile("" ::"s"(mp.data[0]), "s"(mp.scales[0]), "s"(mp.zeros[0]), "s"(mp.out[0]), "s"(x), "s"(awq), "s"(N),
-                 "s"(K), "s"(B), "s"(W), "s"(gridDim.x), "s"(blockDim.x));
-    if constexpr (NMAT == 2) asm volatile("" ::"s"(mp.data[1]), "s"(mp.scales[1]), "s"(mp.zeros[1]), "s"(mp.out[1]));
-    if constexpr (RN) asm volatile("" ::"s"(in.b), "s"(in.gamma), "s"(in.residual_out), "s"(in.normed_out));
-    if constexpr (IMG) asm volatile("" ::"s"(in.hi), "s"(in.lo));
-    if constexpr (EPI != EPI_STORE) asm volatile("" ::"s"(in.img_out_hi), "s"(in.img_out_lo), "s"(in.img_awq));
+__global__ void __launch_bounds__(512) int4_band_kernel(const void *l0, const void *l1, const void *l2,
+                                                        const void *l3, const void *l4, const void *l5, uint32_t nwb,
+                                                        uint32_t kg, MatPtrs mp, const ActIn in) {
+    const int N = (int)(nwb & 0xFFFFFu), W = (int)((nwb >> 20) & 0xFu), B = (int)(nwb >> 24);
+    const int K = (int)(kg & 0xFFFFu), nwg = (int)(kg >> 16);
+    const __half *__restrict__ x = static_cast<const __half *>(l0);   // plain: x; RN: a
+    const __half *__restrict__ awq = static_cast<const __half *>(RN ? l3 : IMG ? nullptr : l1);
+    const __half *__restrict__ xb = static_cast<const __half *>(l1);  // RN: b
+    const __half *__restrict__ gam = static_cast<const __half *>(l2);  // RN: gamma
+    const _Float16 *__restrict__ ihi = static_cast<const _Float16 *>(l0), *__restrict__ ilo =
+        static_cast<const _Float16 *>(l1);   // IMG
+    const __half *sc0 = static_cast<const __half *>(RN ? l4 : l2), *zr0 = static_cast<const __half *>(RN ? l5 : l3);
+    const __half *sc1 = (NMAT == 2 && !RN) ? static_cast<const __half *>(l4) : mp.scales[1];
+    const __half *zr1 = (NMAT == 2 && !RN) ? static_cast<const __half *>(l5) : mp.zeros[1];
+    const uint8_t *wd0 = (NMAT == 1 && !RN) ? static_cast<const uint8_t *>(l4) : mp.data[0];
+    const uint8_t *wd1 = mp.data[1];
     extern __shared__ __attribute__((aligned(16))) uint8_t lds_b[];
-    const int tid = threadIdx.x, nthr = blockDim.x;
+    const int tid = threadIdx.x, nthr = 64 * NMAT * W;
     // the wave index as a scalar, so the weight pointer it selects is uniform
     // and the buffer resources stay in scalar registers
     const int lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6), waves = nthr >> 6;
@@ -94,8 +113,8 @@ __global__ void __launch_bounds__(512) int4_band_kernel(MatPtrs mp, const ActIn 
     const int p0 = (part * P) / W;
     const int np = ((part + 1) * P) / W - p0;
     // (the host keeps N * NWG below 2^32)
-    const int RB = (int)(((uint32_t)N * blockIdx.x) / gridDim.x);
-    const int RE = (int)(((uint32_t)N * (blockIdx.x + 1)) / gridDim.x);
+    const int RB = (int)(((uint32_t)N * blockIdx.x) / (uint32_t)nwg);
+    const int RE = (int)(((uint32_t)N * (blockIdx.x + 1)) / (uint32_t)nwg);
     const int RT = TM * 8;                     // band rows held in LDS (padded)
     // MB: the band [RB, RE) in blocks of RT rows, one after the other over the
     // operand image staged once (tall matrices at 3-8 rows); else one block
@@ -132,8 +151,8 @@ __global__ void __launch_bounds__(512) int4_band_kernel(MatPtrs mp, const ActIn 
 #pragma unroll
             for (int b = 0; b < BM; b++) {
                 const size_t o = (size_t)min(b, B - 1) * K + (size_t)img_chunk(c) * 8;
-                xv[i][b] = *reinterpret_cast<const u32x4_t *>(in.hi + o);
-                lv[i][b] = *reinterpret_cast<const u32x4_t *>(in.lo + o);
+                xv[i][b] = *reinterpret_cast<const u32x4_t *>(ihi + o);
+                lv[i][b] = *reinterpret_cast<const u32x4_t *>(ilo + o);
             }
             continue;
         }
@@ -142,8 +161,8 @@ __global__ void __launch_bounds__(512) int4_band_kernel(MatPtrs mp, const ActIn 
         if (RN) {
 #pragma unroll
             for (int b = 0; b < BM; b++)
-                bv[i][b] = *reinterpret_cast<const u32x4_t *>(in.b + (size_t)min(b, B - 1) * K + e);
-            gv[i] = *reinterpret_cast<const u32x4_t *>(in.gamma + e);
+                bv[i][b] = *reinterpret_cast<const u32x4_t *>(xb + (size_t)min(b, B - 1) * K + e);
+            gv[i] = *reinterpret_cast<const u32x4_t *>(gam + e);
         }
         wv[i] = __builtin_bit_cast(u32x4_t, __builtin_amdgcn_raw_buffer_load_b128(awq_r, (int)(e * 2), 0, 0));
     }
@@ -157,8 +176,8 @@ __global__ void __launch_bounds__(512) int4_band_kernel(MatPtrs mp, const ActIn 
             const int w = min(i * nthr + tid, NMAT * szw_ - 1);
             const int m = (NMAT == 2 && w >= szw_) ? 1 : 0;
             const size_t src = (size_t)rb_ * P + (w - m * szw_);
-            sv[i] = reinterpret_cast<const uint32_t *>(m ? mp.scales[1] : mp.scales[0])[src];
-            zv[i] = reinterpret_cast<const uint32_t *>(m ? mp.zeros[1] : mp.zeros[0])[src];
+            sv[i] = reinterpret_cast<const uint32_t *>(m ? sc1 : sc0)[src];
+            zv[i] = reinterpret_cast<const uint32_t *>(m ? zr1 : zr0)[src];
         }
     };
     load_sz(rb, szw);
@@ -171,7 +190,7 @@ __global__ void __launch_bounds__(512) int4_band_kernel(MatPtrs mp, const ActIn 
     // (c) weights: lane (j = lane & 15, kq = lane >> 4), row j & 7 of each
     // tile, group j >> 3 of each pair; rows past the band load nothing
     const int jr = lane & 7, jh = (lane >> 3) & 1, kq = lane >> 4;
-    const uint8_t *wdata = (NMAT == 2 && mat) ? mp.data[1] : mp.data[0];
+    const uint8_t *wdata = (NMAT == 2 && mat) ? wd1 : wd0;
     // Issued pair by pair, tiles inner (the order the MFMAs consume them):
     // the first PD pairs now, each later one PD pairs ahead of its MFMAs, so
     // the MFMAs run while the rest streams in (a wave whose next load cannot
@@ -487,9 +506,11 @@ struct BandLaunch {
     dim3 grid, block;
     size_t lds;
     hipStream_t st;
-    int N, K, B, W;
+    BandLead a;
     bool dry;   // only check that the instantiation accepts its LDS size
 };
+#define IMH_BAND_ARGS(L) \
+    L.a.p[0], L.a.p[1], L.a.p[2], L.a.p[3], L.a.p[4], L.a.p[5], L.a.nwb, L.a.kg
 
 // Above 64 KB of LDS a kernel must be allowed the larger size first (gfx950
 // has 160 KB per CU); false if the runtime refuses.
@@ -507,13 +528,13 @@ bool launch_xc(int xc, const BandLaunch &L, const MatPtrs &mp, const ActIn &in) 
     if (xc == 1) {
         if (!allow_lds(int4_band_kernel<NMAT, EPI, TM, NP, BM, 1, RN, IMG>, L.lds)) return false;
         if (!L.dry)
-            hipLaunchKernelGGL((int4_band_kernel<NMAT, EPI, TM, NP, BM, 1, RN, IMG>), L.grid, L.block, L.lds, L.st, mp,
-                               in, L.N, L.K, L.B, L.W);
+            hipLaunchKernelGGL((int4_band_kernel<NMAT, EPI, TM, NP, BM, 1, RN, IMG>), L.grid, L.block, L.lds, L.st,
+                               IMH_BAND_ARGS(L), mp, in);
     } else if (BM <= 2) {   // three activation chunks per thread: 1-2 batch rows only
         if (!allow_lds(int4_band_kernel<NMAT, EPI, TM, NP, BM, BM <= 2 ? 3 : 1, RN, IMG>, L.lds)) return false;
         if (!L.dry)
             hipLaunchKernelGGL((int4_band_kernel<NMAT, EPI, TM, NP, BM, BM <= 2 ? 3 : 1, RN, IMG>), L.grid, L.block,
-                               L.lds, L.st, mp, in, L.N, L.K, L.B, L.W);
+                               L.lds, L.st, IMH_BAND_ARGS(L), mp, in);
     }
     return true;
 }
@@ -538,7 +559,7 @@ bool launch_mb(const BandLaunch &L, const MatPtrs &mp, const ActIn &in) {
     if (!allow_lds(int4_band_kernel<1, EPI_STORE, 5, 2, BM, 1, false, false, 2, true>, L.lds)) return false;
     if (!L.dry)
         hipLaunchKernelGGL((int4_band_kernel<1, EPI_STORE, 5, 2, BM, 1, false, false, 2, true>), L.grid, L.block,
-                           L.lds, L.st, mp, in, L.N, L.K, L.B, L.W);
+                           L.lds, L.st, IMH_BAND_ARGS(L), mp, in);
     return true;
 }
 
@@ -614,7 +635,21 @@ int launch_band_matvec(hipStream_t st, int cus, int B, int nmat, int epi, int N,
     if (lds > (bm <= 2 ? 64 : 160) * 1024) return IMH_OK;
     // a probe takes the same dispatch with launches off: the instantiation
     // must still accept its LDS size (hipFuncSetAttribute above 64 KB)
-    BandLaunch L{dim3(nwg), dim3(nthr), lds, st, N, K, B, W, probe};
+    // the leading arguments (see int4_band_kernel) and the packed dimensions
+    if (N >= (1 << 20) || K >= (1 << 16) || nwg >= (1 << 16) || W >= 16 || B >= 16) return IMH_OK;
+    BandLead a{};
+    if (in.img_src) {
+        a = BandLead{{in.hi, in.lo, mp.scales[0], mp.zeros[0], mp.data[0], nullptr}, 0, 0};
+    } else if (rn) {
+        a = BandLead{{in.a, in.b, in.gamma, in.awq, mp.scales[0], mp.zeros[0]}, 0, 0};
+    } else {
+        a = BandLead{{in.a, in.awq, mp.scales[0], mp.zeros[0], nmat == 2 ? (const void *)mp.scales[1] : mp.data[0],
+                      nmat == 2 ? (const void *)mp.zeros[1] : nullptr},
+                     0, 0};
+    }
+    a.nwb = (uint32_t)N | ((uint32_t)W << 20) | ((uint32_t)B << 24);
+    a.kg = (uint32_t)K | ((uint32_t)nwg << 16);
+    BandLaunch L{dim3(nwg), dim3(nthr), lds, st, a, probe};
     bool ok;
     if (mb) {
         ok = bm == 4 ? launch_mb<4>(L, mp, in) : launch_mb<8>(L, mp, in);
