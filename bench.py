@@ -662,7 +662,8 @@ def main():
         us = 1e3 * tot / args.steps
         gbs = down_bytes(B) / (us * 1e-6) / 1e9
         log(f"down kernel B={B}: {us:.2f} us  {gbs:.0f} GB/s ({100 * gbs / HBM_PEAK_GBS:.1f} %)")
-        print(json.dumps({"kernel": ("int4_band_kernel" if B <= 2 else "int4_matvec_kernel") + " (down projection)",
+        print(json.dumps({"kernel": ("int4_band_kernel" if B <= 2 else "int4_prep_plain + int4_splitk_kernel + combine"
+                                     if B <= 8 else "int4_matvec_kernel") + " (down projection)",
                           "batch": B, "us": round(us, 3),
                           "GB/s": round(gbs, 1), "launches": args.steps, "eager": args.eager}))
         return
@@ -678,7 +679,7 @@ def main():
     k_gbs = k_bytes / (k_us * 1e-6) / 1e9
     log(f"gate+up kernel: {k_us:.2f} us  {k_gbs:.0f} GB/s ({100 * k_gbs / HBM_PEAK_GBS:.1f} %)")
     if args.kernel == "gate_up":
-        print(json.dumps({"kernel": ("int4_band_kernel" if B <= 2 else "int4_matvec_kernel") + "<2, SILU> (gate+up)",
+        print(json.dumps({"kernel": ("int4_band_kernel" if B <= 8 else "int4_matvec_kernel") + "<2, SILU> (gate+up)",
                           "batch": B, "us": round(k_us, 3),
                           "GB/s": round(k_gbs, 1), "launches": ksteps, "eager": args.eager}))
         return
@@ -839,7 +840,7 @@ def main():
                    "awq": True, "weight_replicas": reps},
         "roofline": {"bound": "hbm", "achieved": round(k_gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(k_gbs / HBM_PEAK_GBS, 4), "traffic": traffic,
-                     "kernel": ("int4_band_kernel" if B <= 2 else "int4_matvec_kernel") + " (fused gate+up, SiLU, AWQ)",
+                     "kernel": ("int4_band_kernel" if B <= 8 else "int4_matvec_kernel") + " (fused gate+up, SiLU, AWQ)",
                      "bytes_per_launch": k_bytes, "us_per_launch": round(k_us, 3), "launches": ksteps,
                      "warmup_launches": kwarm},
         "cpu_baseline": cpu,
