@@ -248,17 +248,20 @@ __global__ void __launch_bounds__(512) int4_band_kernel(const void *l0, const vo
         __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
         __builtin_amdgcn_s_barrier();
         __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+        // lane 8 b + j (j < 8) sums groups j, j + 8, .. of batch row b in
+        // order, xor shuffles add the eight partial sums pairwise, and every
+        // thread takes each row's sum from lane 8 b (one chain of G / 8 LDS
+        // reads per lane: eight serial chains per thread took ~1.3 us)
+        {
+            const int rr = lane >> 3, j = lane & 7;
+            float ss = 0.0f;
+            if (rr < BM)
+                for (int g = j; g < G; g += 8) ss += rsq[g * BM + rr];
+            ss += __shfl_xor(ss, 1);
+            ss += __shfl_xor(ss, 2);
+            ss += __shfl_xor(ss, 4);
 #pragma unroll
-        for (int b = 0; b < BM; b++) {
-            float t8[8];
-#pragma unroll
-            for (int j = 0; j < 8; j++) {
-                float ss = 0.0f;
-                for (int g = j; g < G; g += 8) ss += rsq[g * BM + b];
-                t8[j] = ss;
-            }
-            const float ss = ((t8[0] + t8[1]) + (t8[2] + t8[3])) + ((t8[4] + t8[5]) + (t8[6] + t8[7]));
-            ri[b] = 1.0f / __builtin_sqrtf(ss / (float)K + in.eps);
+            for (int b = 0; b < BM; b++) ri[b] = 1.0f / __builtin_sqrtf(__shfl(ss, 8 * b) / (float)K + in.eps);
         }
         if (BM > 2 && tid < BM) {
             float r = ri[0];
