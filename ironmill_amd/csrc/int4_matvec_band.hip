@@ -41,6 +41,7 @@
 #include <hip/hip_fp16.h>
 
 #include <algorithm>
+#include <type_traits>
 
 #include "imh_internal.h"
 #include "int4_matvec_kernel.h"
@@ -433,16 +434,44 @@ __global__ void __launch_bounds__(512) int4_band_kernel(const void *l0, const vo
         }
     }
     __syncthreads();
-    // the row's sums over the waves' parts (in part order), per matrix
+    // the row's sums over the waves' parts (in part order), per matrix: the
+    // W <= 8 / NMAT reads issued together, then added in order (a loop to
+    // the runtime W waited for each read in turn)
     auto row_sums = [&](int r, int b, float *sum) __attribute__((always_inline)) {
         const int t = r >> 3, rl = r & 7;
+        constexpr int WM = 8 / NMAT;
+        // part 0 of matrix 0 for this (row, batch row); parts TM * NH * 8
+        // float4s apart (a uniform offset per part)
+        const float *r0 = reinterpret_cast<const float *>(red + (t * NH + (b >> 2)) * 8 + rl) + (b & 3);
+        constexpr int pst = TM * NH * 8 * 4;
+        // W <= 4: the reads of 2 or 4 parts (clamped to the last) issued
+        // together, then added in order; W > 4 (down: 8) the loop, which the
+        // compiler unrolls by 8 with one wait (left as a loop to the runtime
+        // W, W <= 4 waited for each read in turn)
+        auto parts_sum = [&](int mt, auto n) __attribute__((always_inline)) {
+            constexpr int PN = decltype(n)::value;
+            const float *rm = r0 + mt * W * pst;
+            float pv[PN];
+#pragma unroll
+            for (int p = 0; p < PN; p++) pv[p] = rm[min(p, W - 1) * pst];
+            float s = 0.0f;
+#pragma unroll
+            for (int p = 0; p < PN; p++)
+                if (p < W) s += pv[p];
+            return s;
+        };
 #pragma unroll
         for (int mt = 0; mt < NMAT; mt++) {
             float s = 0.0f;
-            for (int p = 0; p < W; p++) s += red[(((mt * W + p) * TM + t) * NH + (b >> 2)) * 8 + rl][b & 3];
+            if (W <= 2) {
+                s = parts_sum(mt, std::integral_constant<int, 2>{});
+            } else if (WM <= 4 || W <= 4) {
+                s = parts_sum(mt, std::integral_constant<int, WM < 4 ? WM : 4>{});
+            } else {
+                for (int p = 0; p < W; p++) s += r0[(mt * W + p) * pst];
+            }
             // round_mode 0: the row's rms_inv scales both projections, ahead of the activation
-            if (RN && !rnd) s *= BM <= 2 ? (b == 0 ? ri[0] : ri[BM - 1]) : rinv[b];
-            sum[mt] = s;
+            sum[mt] = (RN && !rnd) ? s * (BM <= 2 ? (b == 0 ? ri[0] : ri[BM - 1]) : rinv[b]) : s;
         }
     };
     if constexpr (EPI == EPI_SILU || EPI == EPI_GELU) {

@@ -202,8 +202,9 @@ __device__ __forceinline__ float div_awq(float v, float w) { return v * __builti
 // right after them, before anything waits.  The first stage is peeled so no
 // loop-carried wait sits ahead of the first weight loads.
 // Occupancy target (waves per SIMD) the register allocator works to: 6 where
-// the live state fits 80 VGPRs without spilling, fewer for the heavier shapes
-// (every instantiation compiles without scratch).
+// the live state fits 80 VGPRs without spilling, fewer for the heavier shapes.
+// The decode step's instantiations (NG 2) compile without scratch; some raw
+// shapes with NG >= 4 spill 12-28 bytes per lane at these targets.
 constexpr int waves_per_simd(int NG, int MT, int XC, int SRC) {
     return ((SRC == SRC_RAW_RN && XC == 2) || (NG >= 8 && XC == 2)) ? 4
            : (NG <= 5 && (MT == 1 || XC == 1) && (SRC == SRC_IMAGE || (XC == 1 && SRC == SRC_RAW))) ? 6
@@ -607,12 +608,25 @@ int4_matvec_kernel(MatPtrs mp, ActIn in, int Nall, int K, int B, int parts, int 
     const int t = lane >> 5;
     if (t >= MT) return;
     const int l2 = lane & 31;
+    // parts 1, 2, .. added in order, their reads issued four parts at a time
+    // (clamped to the last part) so one wait covers four
     float4_t sum[NMAT];
 #pragma unroll
     for (int mt = 0; mt < NMAT; mt++) {
         const float4_t *rp = red + (t * waves + mt * parts) * 64;
         sum[mt] = rp[l2] + rp[l2 + 32];
-        for (int p = 1; p < parts; p++) sum[mt] += rp[p * 64 + l2] + rp[p * 64 + l2 + 32];
+        for (int p0 = 1; p0 < parts; p0 += 4) {
+            float4_t pv[4][2];
+#pragma unroll
+            for (int j = 0; j < 4; j++) {
+                const int p = min(p0 + j, parts - 1);
+                pv[j][0] = rp[p * 64 + l2];
+                pv[j][1] = rp[p * 64 + l2 + 32];
+            }
+#pragma unroll
+            for (int j = 0; j < 4; j++)
+                if (p0 + j < parts) sum[mt] += pv[j][0] + pv[j][1];
+        }
     }
     if (row >= N) return;
     const int mrow = 8 * t + 4 * (l2 >> 4);   // batch row within the tile
