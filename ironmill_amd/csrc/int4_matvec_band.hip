@@ -182,6 +182,19 @@ __global__ void __launch_bounds__(512) int4_band_kernel(const void *l0, const vo
         }
     };
     load_sz(rb, szw);
+    // image output: the AWQ scale of the next projection at this thread's
+    // first epilogue row, loaded with the small loads -- read in the
+    // epilogue it put a memory round trip after the join (rows past the band,
+    // and launches without an image output, read zeros)
+    float img_w0 = 0.0f;
+    if constexpr (EPI != EPI_STORE && !MB) {
+        const bool iw = in.img_out_hi && in.img_awq;
+        const __amdgpu_buffer_rsrc_t ia_r = __builtin_amdgcn_make_buffer_rsrc(
+            (void *)(reinterpret_cast<const char *>(in.img_awq) + (iw ? (size_t)RB * 2 : 0)), 0, iw ? nrows * 2 : 0,
+            kRsrcWord3);
+        img_w0 = __half2float(__builtin_bit_cast(
+            __half, (uint16_t)__builtin_amdgcn_raw_buffer_load_b16(ia_r, (tid % RT) * 2, 0, 0)));
+    }
     // issue order: every wave's small loads ahead of any weight load in the
     // CU's memory pipeline, which returns them in order (an execution barrier
     // only: nothing waits for the loads here)
@@ -499,7 +512,8 @@ __global__ void __launch_bounds__(512) int4_band_kernel(const void *l0, const vo
                 const __half h = __float2half(act * u);
                 mp.out[0][(size_t)b * N + rb + r] = h;
                 v = __half2float(h);
-                if (in.img_out_hi && in.img_awq) v = div_awq(v, __half2float(in.img_awq[rb + r]));
+                if (in.img_out_hi && in.img_awq)
+                    v = div_awq(v, o0 == 0 ? img_w0 : __half2float(in.img_awq[rb + r]));
             }
             if (in.img_out_hi) {   // uniform
                 const float v1 = __shfl_xor(v, 1);
