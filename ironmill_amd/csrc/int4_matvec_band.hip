@@ -452,7 +452,7 @@ __global__ void __launch_bounds__(512) int4_band_kernel(const void *l0, const vo
     // the runtime W waited for each read in turn)
     auto row_sums = [&](int r, int b, float *sum) __attribute__((always_inline)) {
         const int t = r >> 3, rl = r & 7;
-        constexpr int WM = 8 / NMAT;
+        constexpr int WM = 8 / NMAT;   // the host keeps W <= 8 / NMAT
         // part 0 of matrix 0 for this (row, batch row); parts TM * NH * 8
         // float4s apart (a uniform offset per part)
         const float *r0 = reinterpret_cast<const float *>(red + (t * NH + (b >> 2)) * 8 + rl) + (b & 3);
