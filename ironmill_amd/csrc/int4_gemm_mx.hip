@@ -177,9 +177,11 @@ __global__ void __launch_bounds__(kThreads, 2) gemm_mx_kernel(
     constexpr int EB = P == PREC_BF16 ? 2 : 1;     // operand bytes per element
     constexpr int RB = kGS * EB + 16;              // LDS row bytes of one group (16-byte pad)
     constexpr int ACH = kBM * kGS * EB / 16 / kThreads;   // 16-byte A chunks per thread per group
-    // A stages: [stage buffer][group of the stage] -- two groups per barrier
-    __shared__ __attribute__((aligned(16))) uint8_t As[2][2][kBM * RB];
-    __shared__ __attribute__((aligned(16))) float Gs[2][2][kBM];
+    // A stages: [stage buffer][group of the stage] -- GPB groups per barrier:
+    // two at bf16, four at fp8 (its operand is half the bytes: the same LDS)
+    constexpr int GPB = P == PREC_BF16 ? 2 : 4;
+    __shared__ __attribute__((aligned(16))) uint8_t As[2][GPB][kBM * RB];
+    __shared__ __attribute__((aligned(16))) float Gs[2][GPB][kBM];
 
     const int tid = threadIdx.x;
     const int lane = tid & 63;
@@ -387,12 +389,15 @@ __global__ void __launch_bounds__(kThreads, 2) gemm_mx_kernel(
         load_a(g_begin, ar, gsv);
         load_b(g_begin, b0);
         store_a(0, 0, ar, gsv);
-        load_a(min(g_begin + 1, g_end - 1), ar, gsv);
-        store_a(0, 1, ar, gsv);
+#pragma unroll
+        for (int q = 1; q < GPB; q++) {
+            load_a(min(g_begin + q, g_end - 1), ar, gsv);
+            store_a(0, q, ar, gsv);
+        }
         __syncthreads();
     }
     auto step = [&](int g, int sb, int part, const BRegs &cur, BRegs &nxt) __attribute__((always_inline)) {
-        const int ga = min(g + 2, g_end - 1), gb = min(g + 1, g_end - 1);
+        const int ga = min(g + GPB, g_end - 1), gb = min(g + 1, g_end - 1);
         // the loads spread over the k steps: A chunks first (they are stored
         // to LDS after the compute), then B
         compute(sb, part, cur, [&](int st) __attribute__((always_inline)) {
@@ -403,14 +408,23 @@ __global__ void __launch_bounds__(kThreads, 2) gemm_mx_kernel(
         });
         store_a(sb ^ 1, part, ar, gsv);
     };
-    // two stages per iteration: the stage buffers' indices are constants
-    for (int g = g_begin; g < g_end; g += 4) {
-        step(g, 0, 0, b0, b1);
-        if (g + 1 < g_end) step(g + 1, 0, 1, b1, b0);
+    // two stages per iteration: the stage buffers' indices are constants (GPB
+    // is even, so group parity and part parity pick the same B set)
+    for (int g = g_begin; g < g_end; g += 2 * GPB) {
+#pragma unroll
+        for (int q = 0; q < GPB; q++) {
+            if (g + q >= g_end) break;
+            if (q & 1) step(g + q, 0, q, b1, b0);
+            else step(g + q, 0, q, b0, b1);
+        }
         __syncthreads();
-        if (g + 2 < g_end) {
-            step(g + 2, 1, 0, b0, b1);
-            if (g + 3 < g_end) step(g + 3, 1, 1, b1, b0);
+        if (g + GPB < g_end) {
+#pragma unroll
+            for (int q = 0; q < GPB; q++) {
+                if (g + GPB + q >= g_end) break;
+                if (q & 1) step(g + GPB + q, 1, q, b1, b0);
+                else step(g + GPB + q, 1, q, b0, b1);
+            }
             __syncthreads();
         }
     }
