@@ -238,20 +238,24 @@ __global__ void __launch_bounds__(1024) int8w_band_kernel(const __half *__restri
         zr[p] = zeros[(size_t)rb * G + e];
     }
     // weights of the band's rows only: a buffer resource over rows rb .. re - 1,
-    // so the lanes of rows past the band read zeros without touching memory
+    // so the lanes of rows past the band read zeros without touching memory.
+    // Group i of every tile is issued one group ahead of its MFMAs (the first
+    // before the staging): a wave whose next load cannot issue waits there, so
+    // loads issued all at once held the MFMAs until the whole band was asked
+    // for.  (An execution barrier between every wave's small loads and the
+    // weights, which the INT4 band kernel takes, measured slower here.)
     constexpr uint32_t kRsrcWord3 = 0x00020000u;
     const __amdgpu_buffer_rsrc_t w_r =
         __builtin_amdgcn_make_buffer_rsrc((void *)(w + (size_t)rb * K), 0, (re - rb) * K, kRsrcWord3);
     u32x4_t wq[TM][NPW];
+    auto load_group = [&](int i) __attribute__((always_inline)) {
+        const int g = g0 + min(i, ng - 1);
 #pragma unroll
-    for (int t = 0; t < TM; t++) {
-#pragma unroll
-        for (int i = 0; i < NPW; i++) {
-            const int g = g0 + min(i, ng - 1);
+        for (int t = 0; t < TM; t++)
             wq[t][i] = __builtin_bit_cast(
                 u32x4_t, __builtin_amdgcn_raw_buffer_load_b128(w_r, (8 * t + r) * K + g * kGS + h * 64 + kq * 16, 0, 0));
-        }
-    }
+    };
+    load_group(0);
     // (b) the activation image of all of K: chunk c (8 elements) of batch row
     // b; the 8 chunks of a half group are 8 consecutive lanes
     auto stage = [&](int c, const u32x4_t &xv, const u32x4_t &av) {
@@ -319,6 +323,7 @@ __global__ void __launch_bounds__(1024) int8w_band_kernel(const __half *__restri
     for (int t = 0; t < TM; t++) acc[t] = float4_t{0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
     for (int i = 0; i < NPW; i++) {
+        if (i + 1 < NPW) load_group(i + 1);
         if (i < ng) {
             const int g = g0 + i;
             const half8_t a0 = *reinterpret_cast<const half8_t *>(xa + (size_t)g * kGS);
