@@ -632,14 +632,17 @@ __global__ void __launch_bounds__(1024) int4xq8_band_kernel(const int8_t *__rest
     constexpr uint32_t kRsrcWord3 = 0x00020000u;
     const __amdgpu_buffer_rsrc_t w_r =
         __builtin_amdgcn_make_buffer_rsrc((void *)(w + (size_t)rb * (K / 2)), 0, (re - rb) * (K / 2), kRsrcWord3);
+    // pair i of every tile issued one pair ahead of its MFMAs (the first now),
+    // as in the INT8 band kernel
     u32x4_t wq[TM][NPW];
+    auto load_pair = [&](int i) __attribute__((always_inline)) {
 #pragma unroll
-    for (int t = 0; t < TM; t++)
-#pragma unroll
-        for (int i = 0; i < NPW; i++)
+        for (int t = 0; t < TM; t++)
             wq[t][i] = __builtin_bit_cast(
                 u32x4_t, __builtin_amdgcn_raw_buffer_load_b128(
                              w_r, (8 * t + r) * (K / 2) + (2 * (p0 + min(i, np - 1)) + h) * 64 + kq * 16, 0, 0));
+    };
+    load_pair(0);
     // (b) q8 rows into LDS with each group's sum (8 consecutive lanes per group)
     auto stage = [&](int c, const u32x4_t &xa, const u32x4_t &xb) {
         const int b = c / cpr, ci = c - b * cpr;
@@ -693,6 +696,7 @@ __global__ void __launch_bounds__(1024) int4xq8_band_kernel(const int8_t *__rest
     for (int t = 0; t < TM; t++) acc[t] = float4_t{0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
     for (int i = 0; i < NPW; i++) {
+        if (i + 1 < NPW) load_pair(i + 1);
         if (i < np) {
             const int pg = 2 * (p0 + i);   // first group of the pair
             const u32x4_t a0 = *reinterpret_cast<const u32x4_t *>(xa + (size_t)pg * kGS);
