@@ -671,7 +671,12 @@ int launch_band_matvec(hipStream_t st, int cus, int B, int nmat, int epi, int N,
     const int TM = tm <= 2 ? 2 : tm <= 3 ? 3 : 5, NPmax = mb ? 2 : tm <= 3 ? 5 : 3;
     // waves per matrix: as few as keep each wave within NPmax pairs (1-2
     // rows); all eight above, so one activation chunk per thread covers K
-    const int W = bm > 2 ? std::min(8 / nmat, P) : std::min((P + NPmax - 1) / NPmax, 8 / nmat);
+    // at 1-2 rows, 2-tile bands one per CU (O, K/V-sized and the down
+    // projection): all eight waves, fewer pairs each -- O (2560 x 4096) B=1
+    // 5.19 -> 4.77 us with 8 waves of 2 pairs instead of 4 of 4; 3-tile
+    // bands (6144 x 2560) measured slower that way and keep the fewest waves
+    int W = bm > 2 ? std::min(8 / nmat, P) : std::min((P + NPmax - 1) / NPmax, 8 / nmat);
+    if (bm <= 2 && !tall12 && nwg <= cus && TM == 2) W = std::min(8 / nmat, P);
     const int np = (P + W - 1) / W;
     if (np > NPmax) return IMH_OK;
     const int nthr = 64 * W * nmat;
