@@ -609,10 +609,14 @@ bool launch_mb(const BandLaunch &L, const MatPtrs &mp, const ActIn &in) {
     return true;
 }
 
-// (TM, NP) instantiated: (2, 5), (3, 5) and (5, 3); the host picks the
-// smallest TM that holds the band.
+// (TM, NP) instantiated: (2, 2), (2, 5), (3, 5) and (5, 3); the host picks
+// the smallest TM that holds the band, and (2, 2) when its waves hold at most
+// two pairs (O and K/V-sized matrices on eight waves): a wave loads a slot for
+// every NP, re-reading its last pair for the slots past its own -- with (2, 5)
+// three of O's five loads per tile were such re-reads (O B=1 4.77 -> 4.18 us).
 template <int NMAT, int EPI, bool RN, bool IMG = false>
-bool launch_shape(int tm, int bm, int xc, const BandLaunch &L, const MatPtrs &mp, const ActIn &in) {
+bool launch_shape(int tm, int bm, int xc, const BandLaunch &L, const MatPtrs &mp, const ActIn &in, int np = 5) {
+    if (tm <= 2 && np <= 2) return launch_bm<NMAT, EPI, 2, 2, RN, IMG>(bm, xc, L, mp, in);
     if (tm <= 2) return launch_bm<NMAT, EPI, 2, 5, RN, IMG>(bm, xc, L, mp, in);
     if (tm <= 3) return launch_bm<NMAT, EPI, 3, 5, RN, IMG>(bm, xc, L, mp, in);
     return launch_bm<NMAT, EPI, 5, 3, RN, IMG>(bm, xc, L, mp, in);
@@ -705,16 +709,16 @@ int launch_band_matvec(hipStream_t st, int cus, int B, int nmat, int epi, int N,
     if (mb) {
         ok = bm == 4 ? launch_mb<4>(L, mp, in) : launch_mb<8>(L, mp, in);
     } else if (in.img_src) {
-        ok = launch_shape<1, EPI_STORE, false, true>(tm, bm, xc, L, mp, in);
+        ok = launch_shape<1, EPI_STORE, false, true>(tm, bm, xc, L, mp, in, np);
     } else if (rn) {
         if (nmat == 1)
-            ok = launch_shape<1, EPI_STORE, true>(tm, bm, xc, L, mp, in);
+            ok = launch_shape<1, EPI_STORE, true>(tm, bm, xc, L, mp, in, np);
         else if (epi == EPI_SILU)
             ok = launch_shape<2, EPI_SILU, true>(tm, bm, xc, L, mp, in);
         else
             ok = launch_shape<2, EPI_GELU, true>(tm, bm, xc, L, mp, in);
     } else if (nmat == 1) {
-        ok = launch_shape<1, EPI_STORE, false>(tm, bm, xc, L, mp, in);
+        ok = launch_shape<1, EPI_STORE, false>(tm, bm, xc, L, mp, in, np);
     } else if (epi == EPI_SILU) {
         ok = launch_shape<2, EPI_SILU, false>(tm, bm, xc, L, mp, in);
     } else if (epi == EPI_GELU) {
