@@ -214,12 +214,23 @@ __global__ void __launch_bounds__(512) int4_band_kernel(const void *l0, const vo
     const int woff = jr * (K / 2) + jh * 64 + kq * 16;
     u32x4_t wq[TM][NP];
     // pair i of the block at row offset bo (from RB) into slot i
+    // slots past the wave's own pairs: a plain one-matrix launch loads them
+    // past the resource's range (zeros, no memory access) rather than
+    // re-reading its last pair -- down B=1 6.56 -> 6.20 us.  With two
+    // matrices, an image or residual-norm source or the multi-block mode that
+    // measured no faster or slower (the decode step at B=1 / B=8 1.608 ->
+    // 1.617 ms / 3.275 -> 3.291 ms), so those re-read.  The MFMAs skip them
+    // either way.
+    constexpr int kPastRange = 0x40000000;
     auto load_pair_at = [&](int bo, int i) __attribute__((always_inline)) {
 #pragma unroll
         for (int t = 0; t < TM; t++)
             wq[t][i] = __builtin_bit_cast(
                 u32x4_t, __builtin_amdgcn_raw_buffer_load_b128(
-                             w_r, woff + (bo + t * 8) * (K / 2) + (p0 + min(i, np - 1)) * 128, 0, 0));
+                             w_r,
+                             (NMAT == 1 && !IMG && !RN && !MB) ? (i < np ? woff + (bo + t * 8) * (K / 2) + (p0 + i) * 128 : kPastRange)
+                                       : woff + (bo + t * 8) * (K / 2) + (p0 + min(i, np - 1)) * 128,
+                             0, 0));
     };
     auto load_pair = [&](int i) __attribute__((always_inline)) { load_pair_at(rb - RB, i); };
 #pragma unroll
