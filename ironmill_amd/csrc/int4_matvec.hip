@@ -243,7 +243,13 @@ int plan_launch(imh_stream *s, int nmat, bool rn, int N, int K, int B, const cha
     const int MT = rows > 8 ? 2 : 1;
     const int tiles = (N + 15) / 16;
     const int btiles = (B + 15) / 16;
-    const int parts = pick_parts(tiles * btiles, nmat, G, s->dev->props.multiProcessorCount);
+    // the residual-norm source at one row (the decoder's Q|K|V, 384 tiles):
+    // eight waves per tile, not the twelve the residency rule gives --
+    // decode step B=1 1.613 -> 1.565 ms (4 waves 1.564, 5 1.573, 6 1.585,
+    // 10 1.604, 16 1.725 ms; A/B on one box, two rounds)
+    const int parts = (rn && nmat == 1 && B == 1)
+                          ? std::max((G + kMaxGroups - 1) / kMaxGroups, std::min(8, G))
+                          : pick_parts(tiles * btiles, nmat, G, s->dev->props.multiProcessorCount);
     const int waves = nmat * parts;
     const int nthr = 64 * waves;
     const size_t red_bytes = (size_t)MT * waves * 64 * sizeof(float4_t);
