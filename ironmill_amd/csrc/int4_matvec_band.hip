@@ -214,13 +214,14 @@ __global__ void __launch_bounds__(512) int4_band_kernel(const void *l0, const vo
     const int woff = jr * (K / 2) + jh * 64 + kq * 16;
     u32x4_t wq[TM][NP];
     // pair i of the block at row offset bo (from RB) into slot i
-    // slots past the wave's own pairs: a plain one-matrix launch loads them
-    // past the resource's range (zeros, no memory access) rather than
-    // re-reading its last pair -- down B=1 6.56 -> 6.20 us.  With two
-    // matrices, an image or residual-norm source or the multi-block mode that
-    // measured no faster or slower (the decode step at B=1 / B=8 1.608 ->
-    // 1.617 ms / 3.275 -> 3.291 ms), so those re-read.  The MFMAs skip them
-    // either way.
+    // slots past the wave's own pairs: a plain one-matrix launch in 2-tile
+    // bands of 5 pair slots (down) loads them past the resource's range
+    // (zeros, no memory access) rather than re-reading its last pair -- down
+    // B=1 6.56 -> 6.20 us.  Elsewhere the select on every load's offset cost
+    // more than it saved (6144 x 2560 in 3-tile bands, no spare slot: 5.69 ->
+    // 6.36 us; with two matrices, an image or residual-norm source or the
+    // multi-block mode the decode step measured 1.608 -> 1.617 ms at B=1),
+    // so those re-read.  The MFMAs skip the spare slots either way.
     constexpr int kPastRange = 0x40000000;
     auto load_pair_at = [&](int bo, int i) __attribute__((always_inline)) {
 #pragma unroll
@@ -228,7 +229,7 @@ __global__ void __launch_bounds__(512) int4_band_kernel(const void *l0, const vo
             wq[t][i] = __builtin_bit_cast(
                 u32x4_t, __builtin_amdgcn_raw_buffer_load_b128(
                              w_r,
-                             (NMAT == 1 && !IMG && !RN && !MB) ? (i < np ? woff + (bo + t * 8) * (K / 2) + (p0 + i) * 128 : kPastRange)
+                             (NMAT == 1 && !IMG && !RN && !MB && TM == 2 && NP == 5) ? (i < np ? woff + (bo + t * 8) * (K / 2) + (p0 + i) * 128 : kPastRange)
                                        : woff + (bo + t * 8) * (K / 2) + (p0 + min(i, np - 1)) * 128,
                              0, 0));
     };
