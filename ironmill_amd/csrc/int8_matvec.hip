@@ -798,7 +798,10 @@ bool q8_band_launch(hipStream_t st, int cus, const Q8Src &src, const uint8_t *w,
     int nwg = std::min(cus, (N + 7) / 8);
     while ((N + nwg - 1) / nwg > 40) nwg += cus;
     const int TM = ((N + nwg - 1) / nwg + 7) / 8;
-    const int npw = std::min(8, 10 / TM);
+    // 5-tile bands (the gate shape): one group pair per wave, as many waves
+    // as pairs -- B=1 / 2 / 4 7.96 / 8.01 / 8.94 -> 6.97 / 7.25 / 7.64 us
+    // against five waves of two (four of three: 8.02 / 8.78 / 9.82 us)
+    const int npw = TM == 5 ? 1 : std::min(8, 10 / TM);
     const int waves = std::max(1, (GP + npw - 1) / npw);
     if (waves > 16) return false;
     const size_t lds = std::max(q8_band_lds(K, B, G, TM), (size_t)waves * TM * 64 * sizeof(float4_t));
@@ -808,7 +811,7 @@ bool q8_band_launch(hipStream_t st, int cus, const Q8Src &src, const uint8_t *w,
         case 2: return launch_q8_band<2, 5>(st, nwg, waves, lds, src, w, sc, zr, y, N, K, B);
         case 3: return launch_q8_band<3, 3>(st, nwg, waves, lds, src, w, sc, zr, y, N, K, B);
         case 4: return launch_q8_band<4, 2>(st, nwg, waves, lds, src, w, sc, zr, y, N, K, B);
-        default: return launch_q8_band<5, 2>(st, nwg, waves, lds, src, w, sc, zr, y, N, K, B);
+        default: return launch_q8_band<5, 1>(st, nwg, waves, lds, src, w, sc, zr, y, N, K, B);
     }
 }
 
