@@ -343,7 +343,7 @@ __global__ void __launch_bounds__(256) int4_splitk_combine_kernel(const float *_
 // read the second image (mixed rounding), N otherwise.
 namespace {
 constexpr int kSplitNT = 5;   // 16-row tiles per band
-constexpr int kSplitNG = 2;   // groups per wave
+constexpr int kSplitNG = 2;   // groups per wave at most (one up to 16 groups per slice)
 struct SplitBands {
     int gb, bands0, bands, S;
 };
@@ -374,12 +374,20 @@ int launch_splitk(hipStream_t st, int cus, int N, int K, int B, const MatPtrs &m
     const int G = K / kGS;
     const SplitBands b = splitk_bands(N, split_rows, cus);
     const int gper = (G + b.S - 1) / b.S;
-    const int waves = std::min(16, (gper + kSplitNG - 1) / kSplitNG);
-    if (waves * kSplitNG < gper) return imh::fail(IMH_EINVAL, "int4 split-K: too many groups per slice");
+    // one group per wave while a slice holds at most 16 (down at 3-8 rows:
+    // 10 waves of 1 -- B=4 / 8 12.19 / 12.76 -> 11.46 / 12.03 us, decode step
+    // B=8 3.26 -> 3.21 ms, against 5 waves of 2), else two
+    const int ng = gper <= 16 ? 1 : kSplitNG;
+    const int waves = std::min(16, (gper + ng - 1) / ng);
+    if (waves * ng < gper) return imh::fail(IMH_EINVAL, "int4 split-K: too many groups per slice");
     const size_t lds = (size_t)kSplitNT * waves * 64 * sizeof(float4_t);
     float *part = static_cast<float *>(ws);
-    hipLaunchKernelGGL((int4_splitk_kernel<kSplitNT, kSplitNG>), dim3(b.bands, b.S), dim3(64 * waves), lds, st, mp, in,
-                       N, K, B, b.S, b.gb, b.bands0, part);
+    if (ng == 1)
+        hipLaunchKernelGGL((int4_splitk_kernel<kSplitNT, 1>), dim3(b.bands, b.S), dim3(64 * waves), lds, st, mp, in, N,
+                           K, B, b.S, b.gb, b.bands0, part);
+    else
+        hipLaunchKernelGGL((int4_splitk_kernel<kSplitNT, kSplitNG>), dim3(b.bands, b.S), dim3(64 * waves), lds, st, mp,
+                           in, N, K, B, b.S, b.gb, b.bands0, part);
     IMH_HIP(hipGetLastError());
     const int count = B * N;
     hipLaunchKernelGGL(int4_splitk_combine_kernel, dim3((count + 255) / 256), dim3(256), 0, st, part, b.S, B, N, mp,
