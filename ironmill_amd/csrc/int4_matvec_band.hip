@@ -693,6 +693,14 @@ int launch_band_matvec(hipStream_t st, int cus, int B, int nmat, int epi, int N,
     // bands (6144 x 2560) measured slower that way and keep the fewest waves
     int W = bm > 2 ? std::min(8 / nmat, P) : std::min((P + NPmax - 1) / NPmax, 8 / nmat);
     if (bm <= 2 && !tall12 && nwg <= cus && TM == 2) W = std::min(8 / nmat, P);
+    // multi-block (3-8 rows, tall): the fewest waves that keep eight waves'
+    // pair count, so every wave holds the same -- the LM head's 10 pairs on
+    // five waves of two, not eight of one or two (B=4 / 8 68.8 / 94.2 ->
+    // 63.2 / 84.7 us)
+    if (mb) {
+        const int npw = (P + 7) / 8;
+        W = (P + npw - 1) / npw;
+    }
     const int np = (P + W - 1) / W;
     if (np > NPmax) return IMH_OK;
     const int nthr = 64 * W * nmat;
